@@ -1,0 +1,326 @@
+/* q35_hip.h -- C ABI of the MI355X (gfx950) batched-decode backend for the
+ * qwen35-cpu engine.
+ *
+ * The reference engine runs its decode step in CpuEngine::Impl::forward_batch
+ * (src/runtime/cpu_engine.inl:201-325) through free functions on raw
+ * caller-owned buffers (the headers in include/qwen35x/cpu/). This header is the seam a
+ * HIP backend plugs into: plain C, POD arguments, integer status codes, no
+ * exceptions, no torch or HIP types in any signature. Every kernel-level entry
+ * point takes DEVICE pointers and enqueues on the context's stream; the
+ * *_sync helpers and q35_context_synchronize() wait for completion.
+ *
+ * Each declaration names the reference interface it replaces (file:line,
+ * paths relative to the reference checkout).
+ *
+ * Threading: one owner thread per context, like the reference engine contract
+ * (docs/cpu-engine-api.md:3-6). Calls on one context must not overlap.
+ */
+#ifndef Q35_HIP_H
+#define Q35_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- status */
+enum {
+  Q35_OK = 0,
+  Q35_ERR_INVALID = 1,     /* bad argument or geometry (state untouched)      */
+  Q35_ERR_HIP = 2,         /* a HIP runtime call failed                       */
+  Q35_ERR_OOM = 3,         /* device or host allocation failed                */
+  Q35_ERR_STATE = 4,       /* wrong object state (unknown slot/request, ...)  */
+  Q35_ERR_UNSUPPORTED = 5, /* shape outside what the kernels implement        */
+  Q35_ERR_IO = 6           /* artifact read/write failure                     */
+};
+
+/* ------------------------------------------------------------ block types
+ * Byte-compatible mirrors of the reference block layouts, include/qwen35x/cpu/q4_0.h:36-70.
+ * Q4_0BlockX8 DOT4 encoding (q4_dot4.h:5-6): qs[32t+4r+j] = u[r][8t+j] | u[r][8t+4+j] << 4,
+ * value = (u - 8) * half(d[r]); matrices are ordered [row/8][block]. */
+typedef struct { uint16_t d[8]; uint8_t qs[128]; } q35_q4_0_block_x8;                  /* 144 B */
+typedef struct { float scales[4]; int16_t sums[4]; int8_t qs[128]; } q35_q8_0_block_x4; /* 152 B */
+typedef struct { float scales[1]; int16_t sums[1]; int8_t qs[32]; int16_t pad; } q35_q8_0_block_x1; /* 40 B */
+
+typedef struct q35_context q35_context;
+
+/* ------------------------------------------------------------- context
+ * Replaces the executor (include/qwen35x/cpu/executor.h:45-123): the GPU grid
+ * and one HIP stream take its role. stream == NULL creates a private stream;
+ * otherwise the given hipStream_t is used and not destroyed. */
+int q35_context_create(int device, void *stream, q35_context **out);
+void q35_context_destroy(q35_context *ctx);
+int q35_context_synchronize(q35_context *ctx);
+void *q35_context_stream(q35_context *ctx);
+const char *q35_context_last_error(const q35_context *ctx);
+const char *q35_status_string(int status);
+/* Device properties as read at create time: CU count, gcnArch name. */
+int q35_context_device_info(const q35_context *ctx, int *cu_count, char *arch, size_t arch_size);
+
+/* Plain device memory plumbing for callers without their own allocator. */
+int q35_device_alloc(q35_context *ctx, size_t bytes, void **out);
+int q35_device_free(q35_context *ctx, void *ptr);
+int q35_memcpy_h2d(q35_context *ctx, void *dst, const void *src, size_t bytes); /* synchronous */
+int q35_memcpy_d2h(q35_context *ctx, void *dst, const void *src, size_t bytes); /* synchronous */
+int q35_memcpy_d2d(q35_context *ctx, void *dst, const void *src, size_t bytes); /* async */
+int q35_memset_device(q35_context *ctx, void *dst, int value, size_t bytes);    /* async */
+/* HIP-event timing on the context stream: begin() records, end() records,
+ * waits, and returns the elapsed milliseconds. */
+int q35_timer_begin(q35_context *ctx);
+int q35_timer_end(q35_context *ctx, double *elapsed_ms);
+
+/* -------------------------------------------------- activation preparation */
+/* q8_0_quantize_vector_1, include/qwen35x/cpu/q4_0.h:109-114 (identity basis) */
+int q35_q8_0_quantize_vector_1(q35_context *ctx, const float *input, q35_q8_0_block_x1 *output,
+                               size_t blocks_per_vector);
+/* q8_0_quantize_vectors_4, q4_0.h:101-106; vector_count % 4 == 0 */
+int q35_q8_0_quantize_vectors_4(q35_context *ctx, const float *input, q35_q8_0_block_x4 *output,
+                                size_t vector_count, size_t blocks_per_vector);
+/* q4_h128_prepare_activation_1, include/qwen35x/cpu/q4_h128.h:94-99 */
+int q35_q4_h128_prepare_activation_1(q35_context *ctx, const float *input,
+                                     q35_q8_0_block_x1 *output, size_t column_count,
+                                     uint64_t sign_seed);
+/* q4_h128_prepare_activations_4, q4_h128.h:105-111; vector_count % 4 == 0 */
+int q35_q4_h128_prepare_activations_4(q35_context *ctx, const float *input,
+                                      q35_q8_0_block_x4 *output, size_t vector_count,
+                                      size_t column_count, uint64_t sign_seed);
+
+/* ------------------------------------------------------- Q4-G32-DOT4 GEMV/GEMM */
+/* q4_dot4_matvec, include/qwen35x/cpu/q4_dot4.h:10-11; rows % 8 == 0 */
+int q35_q4_dot4_matvec(q35_context *ctx, const q35_q4_0_block_x8 *matrix,
+                       const q35_q8_0_block_x1 *vector, float *output, size_t rows,
+                       size_t blocks);
+/* q4_dot4_matmul, q4_dot4.h:12-13; rows % 8 == 0, vectors % 4 == 0, output
+ * token-major with row stride `stride` (>= rows). */
+int q35_q4_dot4_matmul(q35_context *ctx, const q35_q4_0_block_x8 *matrix,
+                       const q35_q8_0_block_x4 *vectors, float *output, size_t rows,
+                       size_t vectors_count, size_t blocks, size_t stride);
+/* Same contraction with one wavefront per 64-row group running the whole block
+ * range, so every output is the reference's single fma chain over blocks
+ * (q4_dot4.cpp:43-56): bit-exact FP32. No reference counterpart; slower. */
+int q35_q4_dot4_matmul_exact(q35_context *ctx, const q35_q4_0_block_x8 *matrix,
+                             const q35_q8_0_block_x4 *vectors, float *output, size_t rows,
+                             size_t vectors_count, size_t blocks, size_t stride);
+/* Integer parity hook (no reference counterpart): the exact int32 per-block dot
+ * sum_k (u-8)*a that the matmul kernel forms before its FP32 scaling, written
+ * as [vectors][rows][blocks]. Runs the same device code as q35_q4_dot4_matmul. */
+int q35_q4_dot4_block_dots(q35_context *ctx, const q35_q4_0_block_x8 *matrix,
+                           const q35_q8_0_block_x4 *vectors, int32_t *output, size_t rows,
+                           size_t vectors_count, size_t blocks);
+/* Batched greedy head: q4_dot4_argmax (q4_dot4.h:19-21) for `vectors_count`
+ * rows sharing each weight tile, as greedy_batch_rows does
+ * (src/runtime/cpu_engine_greedy.inl:12-63): per-row repetition penalty
+ * (v > 0 ? v/p : v*p when counts[row][token] > 0 and p > 1), lowest index on
+ * ties. counts is [vectors][rows] int32 or NULL; penalties is [vectors] or NULL.
+ * Writes out_index[vectors] and out_value[vectors] (device pointers). */
+int q35_q4_dot4_argmax_batch(q35_context *ctx, const q35_q4_0_block_x8 *matrix,
+                             const q35_q8_0_block_x4 *vectors, const int32_t *counts,
+                             const float *penalties, size_t rows, size_t vectors_count,
+                             size_t blocks, int32_t *out_index, float *out_value);
+
+/* --------------------------------------------------------------- DeltaNet */
+/* gated_delta_net_update_rows, include/qwen35x/cpu/delta_net.h:18-31.
+ * state [head][value_dim][key_dim]; q,k [head][key_dim]; v,out [head][value_dim]. */
+int q35_gated_delta_net_update_rows(q35_context *ctx, float *state, const float *q,
+                                    const float *k, const float *v, const float *alpha,
+                                    const float *beta, float *output, size_t head_count,
+                                    size_t key_dim, size_t value_dim, size_t row_begin,
+                                    size_t row_end);
+/* Batched form used by the step: `batch` requests, each with its own state at
+ * states[r] (device array of device pointers). q,k [batch][head][key_dim],
+ * v,output [batch][head][value_dim], alpha,beta [batch][head]. key_dim must be 128. */
+int q35_gated_delta_net_update_batch(q35_context *ctx, float *const *states, const float *q,
+                                     const float *k, const float *v, const float *alpha,
+                                     const float *beta, float *output, size_t batch,
+                                     size_t head_count, size_t key_dim, size_t value_dim);
+
+/* ------------------------------------------------------ paged attention */
+/* causal_attention_decode_gqa_pairs with AttentionKvRows
+ * (include/qwen35x/cpu/full_attention.h:10-20,92-112), batched over requests
+ * and walking page tables instead of per-token row pointers.
+ * K/V pools are FP16 [page][page_tokens][kv_heads][head_dim]; page_table is
+ * [batch][max_pages] int32 page ids; seq_lens[batch] (>= 1) tokens to attend.
+ * q, gates, output are [batch][heads][head_dim]. head_dim must be 256 or 128. */
+int q35_attention_decode_paged(q35_context *ctx, const float *q, const float *gates,
+                               const uint16_t *k_pool, const uint16_t *v_pool,
+                               const int32_t *page_table, size_t max_pages,
+                               const int32_t *seq_lens, size_t page_tokens, float *output,
+                               size_t batch, int heads, int kv_heads, int head_dim, float scale);
+/* attention_cache_store_f16, full_attention.h:22-26 (RNE, quiet NaN) */
+int q35_attention_cache_store_f16(q35_context *ctx, const float *input, uint16_t *output,
+                                  size_t count);
+
+/* ------------------------------------------------------ activation ops */
+/* rms_norm_f32, include/qwen35x/cpu/activation.h:45-55 */
+int q35_rms_norm_f32(q35_context *ctx, const float *input, const float *weight, float *output,
+                     size_t rows, size_t width, float eps, float weight_offset);
+/* l2_normalize_f32, activation.h:57-63 (in place) */
+int q35_l2_normalize_f32(q35_context *ctx, float *values, size_t rows, size_t width, float eps,
+                         float output_scale);
+/* causal_conv1d_silu_f32 with batch_size 1, activation.h:29-43 (kernel-major weights) */
+int q35_causal_conv1d_silu_f32(q35_context *ctx, float *state, size_t ring_index,
+                               const float *input, const float *kernel_major_weights,
+                               float *output, size_t channel_count, size_t kernel_size);
+/* silu_mul_f32, activation.h:71-77 */
+int q35_silu_mul_f32(q35_context *ctx, const float *gate, const float *up, float *output,
+                     size_t count);
+/* rope_f32, activation.h:16-27 */
+int q35_rope_f32(q35_context *ctx, float *values, size_t head_count, size_t head_dim,
+                 size_t rope_dim, const float *cosine, const float *sine);
+
+/* =================================================================== model
+ * Shapes of a Qwen3.5 hybrid text model (RuntimeDims, src/runtime/weights.inl:336-357). */
+typedef struct {
+  int32_t n_layers, hidden, intermediate, vocab;
+  int32_t n_heads, n_kv_heads, head_dim, rope_dim;
+  float rope_theta, rms_eps;
+  int32_t lin_kernel, lin_k_heads, lin_v_heads, lin_k_dim, lin_v_dim;
+  uint64_t sign_seed;
+} q35_model_dims;
+
+/* Tensor encodings of the Q35H128 artifact (include/qwen35x/weights/q4_h128_artifact.h:13-29). */
+enum { Q35_ENC_F32 = 0, Q35_ENC_Q4_0_DOT4 = 5, Q35_ENC_Q4_H128_DOT4 = 6 };
+
+typedef struct q35_model q35_model;
+
+/* Model upload. CpuModel::load + load_model_weights_from_q4_h128
+ * (src/runtime/cpu_engine.inl:32-69, weights.inl:1624-1816): tensors are
+ * addressed by their HF names and given as the artifact bytes as-is (DOT4
+ * tiles, FP32 vectors). layer_is_linear[n_layers] is the attention schedule. */
+int q35_model_create(q35_context *ctx, const q35_model_dims *dims,
+                     const uint8_t *layer_is_linear, q35_model **out);
+int q35_model_upload_tensor(q35_model *model, const char *name, int encoding,
+                            const uint64_t *shape, size_t rank, const void *host_bytes,
+                            size_t byte_count);
+int q35_model_finalize(q35_model *model); /* checks every required tensor is present */
+void q35_model_destroy(q35_model *model);
+/* Reads a Q35H128 v1 artifact (src/weights/q4_h128_artifact.cpp) and uploads it. */
+int q35_model_load_artifact(q35_context *ctx, const char *artifact_path,
+                            const q35_model_dims *dims, const uint8_t *layer_is_linear,
+                            q35_model **out);
+/* Dims of the named reference shapes: 0 = 0.8B, 1 = 2B, 2 = 4B
+ * (text_architecture, src/compiler/profile_loader.cpp:439-462). */
+int q35_model_dims_preset(int which, q35_model_dims *dims, uint8_t *layer_is_linear,
+                          size_t layer_capacity);
+/* Random-init artifact in the Q35H128 v1 format: linear weights ~N(0, std)
+ * pushed through the reference's H128 + Q4 packing math (q4_h128.cpp:195-252,
+ * q4_dot4.cpp:5-18), identity-basis tied head, norms 0 (Qwen 1+w form), linear
+ * attention norm 1, seeded A_log/dt_bias/conv weights. Host-only. */
+int q35_write_random_artifact(const char *path, const q35_model_dims *dims,
+                              const uint8_t *layer_is_linear, uint64_t seed, float weight_std);
+/* The FP32 rows [row0, row0+rows) x cols that the generator draws for tensor
+ * `name` before packing (no reference counterpart; lets tests run the same
+ * rows through the reference packer). */
+int q35_random_weight_rows(const char *name, uint64_t seed, uint64_t row0, uint64_t rows,
+                           uint64_t cols, float weight_std, float *out);
+
+/* ================================================================= runtime
+ * Device state for decode: request slots (DeltaNet state, conv ring, token
+ * counts), a paged FP16 KV pool, work buffers and captured step graphs. */
+typedef struct {
+  int32_t max_slots;      /* resident requests (CpuEngineConfig::max_resident_requests) */
+  int32_t max_batch;      /* rows per step (<= 64)                                      */
+  int32_t max_context;    /* tokens per request (CpuEngineConfig::max_context)          */
+  int32_t page_tokens;    /* tokens per KV page (power of two, 16..256)                 */
+  int32_t total_pages;    /* KV pool capacity in pages; 0 = max_slots*ceil(ctx/page)    */
+  int32_t use_graphs;     /* capture each step shape as a hipGraph and replay it        */
+} q35_runtime_config;
+
+typedef struct q35_runtime q35_runtime;
+
+int q35_runtime_create(q35_model *model, const q35_runtime_config *config, q35_runtime **out);
+void q35_runtime_destroy(q35_runtime *rt);
+
+/* Slot lifecycle: CpuEngine::Impl::initialize / retire (cpu_engine.inl:327-383,
+ * 432-440). Allocation zeroes the slot's DeltaNet and conv state and sets its
+ * token counts from the prompt (cpu_engine.inl:376-378). */
+int q35_slot_alloc(q35_runtime *rt, const int32_t *prompt_tokens, size_t prompt_count,
+                   int32_t *out_slot);
+int q35_slot_free(q35_runtime *rt, int32_t slot);
+
+/* KV page pool honouring KvPagesF16 (include/qwen35x/cpu/kv_pages.h:12-100):
+ * pages are reference counted; q35_page_copy is the copy-on-write step used
+ * when appending to a shared tail page. One page id covers every full
+ * attention layer. */
+int q35_page_alloc(q35_runtime *rt, int32_t *out_page);
+int q35_page_retain(q35_runtime *rt, int32_t page);
+int q35_page_release(q35_runtime *rt, int32_t page);
+int q35_page_copy(q35_runtime *rt, int32_t src_page, int32_t dst_page, int32_t tokens);
+int q35_page_refcount(q35_runtime *rt, int32_t page);
+int q35_runtime_free_pages(q35_runtime *rt);
+
+/* One decode step for `batch` rows -- the body of forward_batch
+ * (cpu_engine.inl:201-325) followed by greedy_batch (cpu_engine_greedy.inl:65-128).
+ * All arrays are HOST memory and are packed into device metadata once per step.
+ *   slots[b]      request slot of row b (distinct)
+ *   positions[b]  tokens already committed for the row (the input token is
+ *                 written to KV position positions[b])
+ *   tokens[b]     input token
+ *   count_input[b] 1 when the input token must be added to the row's penalty
+ *                 counts before the head (a generated token), 0 for prompt
+ *                 tokens (already counted at slot allocation)
+ *   penalties[b]  repetition penalty (1 = none)
+ *   page_table    [batch][max_pages] page ids covering positions 0..positions[b]
+ * out_tokens[b] receives the greedy token; out_logits, when non-NULL, receives
+ * the raw logits [batch][vocab] (the full-logits path, cpu_engine.inl:321). */
+typedef struct {
+  int32_t batch;
+  const int32_t *slots;
+  const int32_t *positions;
+  const int32_t *tokens;
+  const uint8_t *count_input;
+  const float *penalties;
+  const int32_t *page_table;
+  int32_t max_pages;
+} q35_step_desc;
+int q35_runtime_step(q35_runtime *rt, const q35_step_desc *desc, int32_t *out_tokens,
+                     float *out_logits);
+/* Copies the final normalized hidden rows of the last step ([batch][hidden]). */
+int q35_runtime_last_hidden(q35_runtime *rt, float *out, size_t count);
+
+/* ================================================================= engine
+ * C mirror of qwen35x::CpuEngine (include/qwen35x/runtime/cpu_engine.h:173-215)
+ * for greedy requests, built on the runtime above. IDs are monotonic and never
+ * reused; one owner calls serially; a failed batch marks every row failed
+ * (cpu_engine.inl:970-977). */
+typedef struct q35_engine q35_engine;
+enum { Q35_REQ_PREFILL = 0, Q35_REQ_DECODE = 1, Q35_REQ_COMPLETE = 2, Q35_REQ_CANCELLED = 3,
+       Q35_REQ_FAILED = 4, Q35_REQ_QUEUED = 5 };
+typedef struct {
+  int32_t max_resident_requests;
+  int32_t max_context;
+  int32_t max_decode_batch_size;
+  int32_t prefill_chunk_size;  /* prompt tokens per advance() of a prefilling request */
+  int32_t page_tokens;
+  int32_t use_graphs;
+} q35_engine_config;
+typedef struct {
+  int32_t status;
+  uint64_t generated_tokens, committed_tokens, prefill_tokens, decode_forwards;
+  double prefill_ms, decode_ms;
+} q35_request_result;
+
+int q35_engine_create(q35_model *model, const q35_engine_config *config, q35_engine **out);
+void q35_engine_destroy(q35_engine *engine);
+int q35_engine_submit(q35_engine *engine, const int32_t *prompt_tokens, size_t prompt_count,
+                      size_t max_new_tokens, float repetition_penalty,
+                      const int32_t *stop_token_ids, size_t stop_count, uint64_t *out_id);
+int q35_engine_advance(q35_engine *engine, uint64_t id);
+int q35_engine_advance_batch(q35_engine *engine, const uint64_t *ids, size_t count);
+int q35_engine_step(q35_engine *engine, int32_t *progressed);
+/* No reference counterpart: prefill several requests together, one prompt
+ * token per request per device step, until every prompt is consumed (the
+ * reference prefills one request per advance(), cpu_engine.inl:668-790). */
+int q35_engine_prefill_batch(q35_engine *engine, const uint64_t *ids, size_t count);
+int q35_engine_result(q35_engine *engine, uint64_t id, q35_request_result *out,
+                      int32_t *tokens, size_t token_capacity, size_t *token_count);
+int q35_engine_cancel(q35_engine *engine, uint64_t id);
+int q35_engine_release(q35_engine *engine, uint64_t id);
+const char *q35_engine_last_error(const q35_engine *engine);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* Q35_HIP_H */

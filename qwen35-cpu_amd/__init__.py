@@ -1,0 +1,501 @@
+"""Python binding of the MI355X (gfx950) decode backend, libq35hip.so.
+
+Mirrors the reference's operator surface -- the free functions of
+include/qwen35x/cpu/*.h and the CpuEngine API of
+include/qwen35x/runtime/cpu_engine.h -- over the C ABI declared in
+include/q35_hip.h. There is no CPU fallback: importing this module without a
+built libq35hip.so raises, and every call runs the HIP kernels.
+
+The directory name is not a Python identifier; load it as
+``importlib`` module ``qwen35_cpu_amd`` (see ``load()`` in __graft_entry__.py).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int32, c_size_t, c_uint8, c_uint64, c_void_p
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libq35hip.so")
+
+Q35_OK = 0
+STATUS = {0: "ok", 1: "invalid argument", 2: "HIP runtime error", 3: "out of memory",
+          4: "invalid state", 5: "unsupported shape", 6: "I/O error"}
+REQ_STATUS = {0: "prefill", 1: "decode", 2: "complete", 3: "cancelled", 4: "failed", 5: "queued"}
+ENC_F32, ENC_Q4_0_DOT4, ENC_Q4_H128_DOT4 = 0, 5, 6
+DEFAULT_SIGN_SEED = 0x5148333548313238  # q4_h128.h:25-26
+
+Q4X8_BYTES, Q8X4_BYTES, Q8X1_BYTES = 144, 152, 40
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(
+        f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+        "(there is no CPU fallback for the MI355X backend)")
+lib = ctypes.CDLL(LIB_PATH)
+
+
+class Q35Error(RuntimeError):
+    pass
+
+
+class ModelDims(ctypes.Structure):
+    """RuntimeDims (src/runtime/weights.inl:336-357)."""
+    _fields_ = [("n_layers", c_int32), ("hidden", c_int32), ("intermediate", c_int32), ("vocab", c_int32),
+                ("n_heads", c_int32), ("n_kv_heads", c_int32), ("head_dim", c_int32), ("rope_dim", c_int32),
+                ("rope_theta", c_float), ("rms_eps", c_float),
+                ("lin_kernel", c_int32), ("lin_k_heads", c_int32), ("lin_v_heads", c_int32),
+                ("lin_k_dim", c_int32), ("lin_v_dim", c_int32), ("sign_seed", c_uint64)]
+
+    def as_dict(self):
+        return {f: getattr(self, f) for f, _ in self._fields_}
+
+
+class RuntimeConfig(ctypes.Structure):
+    _fields_ = [("max_slots", c_int32), ("max_batch", c_int32), ("max_context", c_int32),
+                ("page_tokens", c_int32), ("total_pages", c_int32), ("use_graphs", c_int32)]
+
+
+class StepDesc(ctypes.Structure):
+    _fields_ = [("batch", c_int32), ("slots", POINTER(c_int32)), ("positions", POINTER(c_int32)),
+                ("tokens", POINTER(c_int32)), ("count_input", POINTER(c_uint8)),
+                ("penalties", POINTER(c_float)), ("page_table", POINTER(c_int32)), ("max_pages", c_int32)]
+
+
+class EngineConfig(ctypes.Structure):
+    _fields_ = [("max_resident_requests", c_int32), ("max_context", c_int32),
+                ("max_decode_batch_size", c_int32), ("prefill_chunk_size", c_int32),
+                ("page_tokens", c_int32), ("use_graphs", c_int32)]
+
+
+class RequestResult(ctypes.Structure):
+    _fields_ = [("status", c_int32), ("generated_tokens", c_uint64), ("committed_tokens", c_uint64),
+                ("prefill_tokens", c_uint64), ("decode_forwards", c_uint64),
+                ("prefill_ms", c_double), ("decode_ms", c_double)]
+
+
+P = c_void_p
+_SIGS = {
+    "q35_context_create": (c_int, [c_int, P, POINTER(P)]),
+    "q35_context_destroy": (None, [P]),
+    "q35_context_synchronize": (c_int, [P]),
+    "q35_context_stream": (P, [P]),
+    "q35_context_last_error": (c_char_p, [P]),
+    "q35_status_string": (c_char_p, [c_int]),
+    "q35_context_device_info": (c_int, [P, POINTER(c_int), c_char_p, c_size_t]),
+    "q35_device_alloc": (c_int, [P, c_size_t, POINTER(P)]),
+    "q35_device_free": (c_int, [P, P]),
+    "q35_memcpy_h2d": (c_int, [P, P, P, c_size_t]),
+    "q35_memcpy_d2h": (c_int, [P, P, P, c_size_t]),
+    "q35_memcpy_d2d": (c_int, [P, P, P, c_size_t]),
+    "q35_memset_device": (c_int, [P, P, c_int, c_size_t]),
+    "q35_timer_begin": (c_int, [P]),
+    "q35_timer_end": (c_int, [P, POINTER(c_double)]),
+    "q35_q8_0_quantize_vector_1": (c_int, [P, P, P, c_size_t]),
+    "q35_q8_0_quantize_vectors_4": (c_int, [P, P, P, c_size_t, c_size_t]),
+    "q35_q4_h128_prepare_activation_1": (c_int, [P, P, P, c_size_t, c_uint64]),
+    "q35_q4_h128_prepare_activations_4": (c_int, [P, P, P, c_size_t, c_size_t, c_uint64]),
+    "q35_q4_dot4_matvec": (c_int, [P, P, P, P, c_size_t, c_size_t]),
+    "q35_q4_dot4_matmul": (c_int, [P, P, P, P, c_size_t, c_size_t, c_size_t, c_size_t]),
+    "q35_q4_dot4_matmul_exact": (c_int, [P, P, P, P, c_size_t, c_size_t, c_size_t, c_size_t]),
+    "q35_q4_dot4_block_dots": (c_int, [P, P, P, P, c_size_t, c_size_t, c_size_t]),
+    "q35_q4_dot4_argmax_batch": (c_int, [P, P, P, P, P, c_size_t, c_size_t, c_size_t, P, P]),
+    "q35_gated_delta_net_update_rows": (c_int, [P, P, P, P, P, P, P, P, c_size_t, c_size_t, c_size_t,
+                                                c_size_t, c_size_t]),
+    "q35_gated_delta_net_update_batch": (c_int, [P, P, P, P, P, P, P, P, c_size_t, c_size_t, c_size_t,
+                                                 c_size_t]),
+    "q35_attention_decode_paged": (c_int, [P, P, P, P, P, P, c_size_t, P, c_size_t, P, c_size_t, c_int,
+                                           c_int, c_int, c_float]),
+    "q35_attention_cache_store_f16": (c_int, [P, P, P, c_size_t]),
+    "q35_rms_norm_f32": (c_int, [P, P, P, P, c_size_t, c_size_t, c_float, c_float]),
+    "q35_l2_normalize_f32": (c_int, [P, P, c_size_t, c_size_t, c_float, c_float]),
+    "q35_causal_conv1d_silu_f32": (c_int, [P, P, c_size_t, P, P, P, c_size_t, c_size_t]),
+    "q35_silu_mul_f32": (c_int, [P, P, P, P, c_size_t]),
+    "q35_rope_f32": (c_int, [P, P, c_size_t, c_size_t, c_size_t, P, P]),
+    "q35_model_create": (c_int, [P, POINTER(ModelDims), P, POINTER(P)]),
+    "q35_model_upload_tensor": (c_int, [P, c_char_p, c_int, POINTER(c_uint64), c_size_t, P, c_size_t]),
+    "q35_model_finalize": (c_int, [P]),
+    "q35_model_destroy": (None, [P]),
+    "q35_model_load_artifact": (c_int, [P, c_char_p, POINTER(ModelDims), P, POINTER(P)]),
+    "q35_model_dims_preset": (c_int, [c_int, POINTER(ModelDims), P, c_size_t]),
+    "q35_write_random_artifact": (c_int, [c_char_p, POINTER(ModelDims), P, c_uint64, c_float]),
+    "q35_random_weight_rows": (c_int, [c_char_p, c_uint64, c_uint64, c_uint64, c_uint64, c_float, P]),
+    "q35_runtime_create": (c_int, [P, POINTER(RuntimeConfig), POINTER(P)]),
+    "q35_runtime_destroy": (None, [P]),
+    "q35_slot_alloc": (c_int, [P, P, c_size_t, POINTER(c_int32)]),
+    "q35_slot_free": (c_int, [P, c_int32]),
+    "q35_page_alloc": (c_int, [P, POINTER(c_int32)]),
+    "q35_page_retain": (c_int, [P, c_int32]),
+    "q35_page_release": (c_int, [P, c_int32]),
+    "q35_page_copy": (c_int, [P, c_int32, c_int32, c_int32]),
+    "q35_page_refcount": (c_int, [P, c_int32]),
+    "q35_runtime_free_pages": (c_int, [P]),
+    "q35_runtime_step": (c_int, [P, POINTER(StepDesc), P, P]),
+    "q35_runtime_last_hidden": (c_int, [P, P, c_size_t]),
+    "q35_engine_create": (c_int, [P, POINTER(EngineConfig), POINTER(P)]),
+    "q35_engine_destroy": (None, [P]),
+    "q35_engine_submit": (c_int, [P, P, c_size_t, c_size_t, c_float, P, c_size_t, POINTER(c_uint64)]),
+    "q35_engine_advance": (c_int, [P, c_uint64]),
+    "q35_engine_advance_batch": (c_int, [P, P, c_size_t]),
+    "q35_engine_step": (c_int, [P, POINTER(c_int32)]),
+    "q35_engine_prefill_batch": (c_int, [P, P, c_size_t]),
+    "q35_engine_result": (c_int, [P, c_uint64, POINTER(RequestResult), P, c_size_t, POINTER(c_size_t)]),
+    "q35_engine_cancel": (c_int, [P, c_uint64]),
+    "q35_engine_release": (c_int, [P, c_uint64]),
+    "q35_engine_last_error": (c_char_p, [P]),
+}
+for _name, (_res, _args) in _SIGS.items():
+    _f = getattr(lib, _name)
+    _f.restype = _res
+    _f.argtypes = _args
+
+
+def _ptr(a):
+    """Host numpy array -> void*."""
+    return ctypes.c_void_p(a.ctypes.data) if a is not None else None
+
+
+def model_dims(preset: int = 0):
+    """Dims + attention schedule of the reference shapes: 0 = 0.8B, 1 = 2B, 2 = 4B."""
+    d = ModelDims()
+    sched = np.zeros(64, np.uint8)
+    _check(lib.q35_model_dims_preset(preset, ctypes.byref(d), _ptr(sched), 64), "dims preset")
+    return d, sched[: d.n_layers].copy()
+
+
+def _check(status, what, ctx=None):
+    if status != Q35_OK:
+        detail = ""
+        if ctx is not None:
+            detail = lib.q35_context_last_error(ctx).decode(errors="replace")
+        raise Q35Error(f"{what}: {STATUS.get(status, status)} {detail}".strip())
+
+
+class DeviceArray:
+    """A device allocation with its host-side shape/dtype."""
+
+    def __init__(self, ctx: "Context", shape, dtype):
+        self.ctx, self.shape, self.dtype = ctx, tuple(shape), np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape)) * self.dtype.itemsize if self.shape else self.dtype.itemsize
+        p = c_void_p()
+        _check(lib.q35_device_alloc(ctx.handle, max(self.nbytes, 1), ctypes.byref(p)), "device alloc", ctx.handle)
+        self.ptr = p
+
+    @property
+    def address(self):
+        return self.ptr.value
+
+    def upload(self, host):
+        host = np.ascontiguousarray(host, dtype=self.dtype)
+        assert host.nbytes == self.nbytes, (host.nbytes, self.nbytes)
+        _check(lib.q35_memcpy_h2d(self.ctx.handle, self.ptr, _ptr(host), host.nbytes), "h2d", self.ctx.handle)
+        return self
+
+    def download(self):
+        out = np.empty(self.shape, self.dtype)
+        _check(lib.q35_memcpy_d2h(self.ctx.handle, _ptr(out), self.ptr, self.nbytes), "d2h", self.ctx.handle)
+        return out
+
+    def free(self):
+        if self.ptr is not None and self.ptr.value:
+            lib.q35_device_free(self.ctx.handle, self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Context:
+    """One device, one stream (replaces the reference CpuExecutor)."""
+
+    def __init__(self, device: int = 0):
+        h = c_void_p()
+        _check(lib.q35_context_create(device, None, ctypes.byref(h)), "context create")
+        self.handle = h
+
+    def device_info(self):
+        cu = c_int()
+        arch = ctypes.create_string_buffer(64)
+        _check(lib.q35_context_device_info(self.handle, ctypes.byref(cu), arch, 64), "device info")
+        return cu.value, arch.value.decode()
+
+    def array(self, host=None, shape=None, dtype=None):
+        if host is not None:
+            host = np.ascontiguousarray(host)
+            return DeviceArray(self, host.shape, host.dtype).upload(host)
+        return DeviceArray(self, shape, dtype)
+
+    def synchronize(self):
+        _check(lib.q35_context_synchronize(self.handle), "synchronize", self.handle)
+
+    def check(self, status, what):
+        _check(status, what, self.handle)
+
+    def timer_begin(self):
+        self.check(lib.q35_timer_begin(self.handle), "timer")
+
+    def timer_end(self):
+        ms = c_double()
+        self.check(lib.q35_timer_end(self.handle, ctypes.byref(ms)), "timer")
+        return ms.value
+
+    def close(self):
+        if self.handle is not None:
+            lib.q35_context_destroy(self.handle)
+            self.handle = None
+
+
+# ------------------------------------------------------------------ operators
+# Same names and argument meaning as the reference free functions; buffers are
+# DeviceArray objects (device memory), shapes follow the reference layouts.
+
+def q8_0_quantize_vector_1(ctx, x, out, blocks):
+    ctx.check(lib.q35_q8_0_quantize_vector_1(ctx.handle, x.ptr, out.ptr, blocks), "q8_0_quantize_vector_1")
+
+
+def q8_0_quantize_vectors_4(ctx, x, out, vectors, blocks):
+    ctx.check(lib.q35_q8_0_quantize_vectors_4(ctx.handle, x.ptr, out.ptr, vectors, blocks), "q8_0_quantize_vectors_4")
+
+
+def q4_h128_prepare_activation_1(ctx, x, out, columns, seed=DEFAULT_SIGN_SEED):
+    ctx.check(lib.q35_q4_h128_prepare_activation_1(ctx.handle, x.ptr, out.ptr, columns, seed),
+              "q4_h128_prepare_activation_1")
+
+
+def q4_h128_prepare_activations_4(ctx, x, out, vectors, columns, seed=DEFAULT_SIGN_SEED):
+    ctx.check(lib.q35_q4_h128_prepare_activations_4(ctx.handle, x.ptr, out.ptr, vectors, columns, seed),
+              "q4_h128_prepare_activations_4")
+
+
+def q4_dot4_matvec(ctx, m, v, out, rows, blocks):
+    ctx.check(lib.q35_q4_dot4_matvec(ctx.handle, m.ptr, v.ptr, out.ptr, rows, blocks), "q4_dot4_matvec")
+
+
+def q4_dot4_matmul(ctx, m, v, out, rows, count, blocks, stride, exact=False):
+    f = lib.q35_q4_dot4_matmul_exact if exact else lib.q35_q4_dot4_matmul
+    ctx.check(f(ctx.handle, m.ptr, v.ptr, out.ptr, rows, count, blocks, stride), "q4_dot4_matmul")
+
+
+def q4_dot4_block_dots(ctx, m, v, out, rows, count, blocks):
+    ctx.check(lib.q35_q4_dot4_block_dots(ctx.handle, m.ptr, v.ptr, out.ptr, rows, count, blocks),
+              "q4_dot4_block_dots")
+
+
+def q4_dot4_argmax_batch(ctx, m, v, counts, penalties, rows, count, blocks, out_index, out_value):
+    ctx.check(lib.q35_q4_dot4_argmax_batch(ctx.handle, m.ptr, v.ptr, counts.ptr if counts else None,
+                                           penalties.ptr if penalties else None, rows, count, blocks,
+                                           out_index.ptr, out_value.ptr if out_value else None),
+              "q4_dot4_argmax_batch")
+
+
+def gated_delta_net_update_rows(ctx, state, q, k, v, alpha, beta, out, heads, kdim, vdim, begin, end):
+    ctx.check(lib.q35_gated_delta_net_update_rows(ctx.handle, state.ptr, q.ptr, k.ptr, v.ptr, alpha.ptr, beta.ptr,
+                                                  out.ptr, heads, kdim, vdim, begin, end),
+              "gated_delta_net_update_rows")
+
+
+def gated_delta_net_update_batch(ctx, state_ptrs, q, k, v, alpha, beta, out, batch, heads, kdim, vdim):
+    ctx.check(lib.q35_gated_delta_net_update_batch(ctx.handle, state_ptrs.ptr, q.ptr, k.ptr, v.ptr, alpha.ptr,
+                                                   beta.ptr, out.ptr, batch, heads, kdim, vdim),
+              "gated_delta_net_update_batch")
+
+
+def attention_decode_paged(ctx, q, gates, k_pool, v_pool, page_table, max_pages, seq_lens, page_tokens, out,
+                           batch, heads, kv_heads, head_dim, scale):
+    ctx.check(lib.q35_attention_decode_paged(ctx.handle, q.ptr, gates.ptr, k_pool.ptr, v_pool.ptr, page_table.ptr,
+                                             max_pages, seq_lens.ptr, page_tokens, out.ptr, batch, heads, kv_heads,
+                                             head_dim, scale), "attention_decode_paged")
+
+
+def attention_cache_store_f16(ctx, x, out, count):
+    ctx.check(lib.q35_attention_cache_store_f16(ctx.handle, x.ptr, out.ptr, count), "attention_cache_store_f16")
+
+
+def rms_norm_f32(ctx, x, w, out, rows, width, eps, offset):
+    ctx.check(lib.q35_rms_norm_f32(ctx.handle, x.ptr, w.ptr, out.ptr, rows, width, eps, offset), "rms_norm_f32")
+
+
+def l2_normalize_f32(ctx, x, rows, width, eps, scale=1.0):
+    ctx.check(lib.q35_l2_normalize_f32(ctx.handle, x.ptr, rows, width, eps, scale), "l2_normalize_f32")
+
+
+def causal_conv1d_silu_f32(ctx, state, ring, x, w, out, channels, kernel):
+    ctx.check(lib.q35_causal_conv1d_silu_f32(ctx.handle, state.ptr, ring, x.ptr, w.ptr, out.ptr, channels, kernel),
+              "causal_conv1d_silu_f32")
+
+
+def silu_mul_f32(ctx, g, u, out, count):
+    ctx.check(lib.q35_silu_mul_f32(ctx.handle, g.ptr, u.ptr, out.ptr, count), "silu_mul_f32")
+
+
+def rope_f32(ctx, x, heads, head_dim, rope_dim, cos, sin):
+    ctx.check(lib.q35_rope_f32(ctx.handle, x.ptr, heads, head_dim, rope_dim, cos.ptr, sin.ptr), "rope_f32")
+
+
+# --------------------------------------------------------------- model level
+
+def write_random_artifact(path, dims, schedule, seed=1, weight_std=0.02):
+    """Random-init Q35H128 artifact (weights ~N(0, weight_std) through the H128/Q4 packer)."""
+    sched = np.ascontiguousarray(schedule, np.uint8)
+    _check(lib.q35_write_random_artifact(os.fsencode(path), ctypes.byref(dims), _ptr(sched), seed, weight_std),
+           "write_random_artifact")
+
+
+def random_weight_rows(name, seed, row0, rows, cols, weight_std=0.02):
+    out = np.empty((rows, cols), np.float32)
+    _check(lib.q35_random_weight_rows(name.encode(), seed, row0, rows, cols, weight_std, _ptr(out)),
+           "random_weight_rows")
+    return out
+
+
+class Model:
+    """CpuModel::load equivalent: weights resident in HBM."""
+
+    def __init__(self, ctx, dims, schedule, artifact=None):
+        self.ctx, self.dims = ctx, dims
+        self.schedule = np.ascontiguousarray(schedule, np.uint8)
+        h = c_void_p()
+        if artifact is not None:
+            ctx.check(lib.q35_model_load_artifact(ctx.handle, os.fsencode(artifact), ctypes.byref(dims),
+                                                  _ptr(self.schedule), ctypes.byref(h)), "model load")
+        else:
+            ctx.check(lib.q35_model_create(ctx.handle, ctypes.byref(dims), _ptr(self.schedule), ctypes.byref(h)),
+                      "model create")
+        self.handle = h
+
+    def upload(self, name, encoding, shape, payload):
+        payload = np.ascontiguousarray(payload)
+        shp = (c_uint64 * len(shape))(*shape)
+        self.ctx.check(lib.q35_model_upload_tensor(self.handle, name.encode(), encoding, shp, len(shape),
+                                                   _ptr(payload), payload.nbytes), "upload " + name)
+
+    def finalize(self):
+        self.ctx.check(lib.q35_model_finalize(self.handle), "model finalize")
+
+    def close(self):
+        if self.handle is not None:
+            lib.q35_model_destroy(self.handle)
+            self.handle = None
+
+
+class Runtime:
+    """Device slots, KV page pool and the captured decode step."""
+
+    def __init__(self, model, max_slots=16, max_batch=16, max_context=1024, page_tokens=16, total_pages=0,
+                 use_graphs=True):
+        self.model, self.ctx = model, model.ctx
+        self.cfg = RuntimeConfig(max_slots, max_batch, max_context, page_tokens, total_pages, int(use_graphs))
+        h = c_void_p()
+        self.ctx.check(lib.q35_runtime_create(model.handle, ctypes.byref(self.cfg), ctypes.byref(h)), "runtime create")
+        self.handle = h
+        self.max_pages = (max_context + page_tokens - 1) // page_tokens
+
+    def slot_alloc(self, prompt):
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        s = c_int32()
+        self.ctx.check(lib.q35_slot_alloc(self.handle, _ptr(prompt), prompt.size, ctypes.byref(s)), "slot alloc")
+        return s.value
+
+    def slot_free(self, slot):
+        self.ctx.check(lib.q35_slot_free(self.handle, slot), "slot free")
+
+    def page_alloc(self):
+        p = c_int32()
+        self.ctx.check(lib.q35_page_alloc(self.handle, ctypes.byref(p)), "page alloc")
+        return p.value
+
+    def page_release(self, page):
+        self.ctx.check(lib.q35_page_release(self.handle, page), "page release")
+
+    def step(self, slots, positions, tokens, page_table, count_input=None, penalties=None, logits=False):
+        slots = np.ascontiguousarray(slots, np.int32)
+        positions = np.ascontiguousarray(positions, np.int32)
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        b = slots.size
+        table = np.ascontiguousarray(page_table, np.int32).reshape(b, -1)
+        ci = np.ascontiguousarray(count_input if count_input is not None else np.zeros(b), np.uint8)
+        pen = np.ascontiguousarray(penalties if penalties is not None else np.ones(b), np.float32)
+        d = StepDesc(b, slots.ctypes.data_as(POINTER(c_int32)), positions.ctypes.data_as(POINTER(c_int32)),
+                     tokens.ctypes.data_as(POINTER(c_int32)), ci.ctypes.data_as(POINTER(c_uint8)),
+                     pen.ctypes.data_as(POINTER(c_float)), table.ctypes.data_as(POINTER(c_int32)), table.shape[1])
+        out = np.empty(b, np.int32)
+        lg = np.empty((b, self.model.dims.vocab), np.float32) if logits else None
+        self.ctx.check(lib.q35_runtime_step(self.handle, ctypes.byref(d), _ptr(out), _ptr(lg)), "runtime step")
+        return (out, lg) if logits else out
+
+    def last_hidden(self, batch):
+        out = np.empty((batch, self.model.dims.hidden), np.float32)
+        self.ctx.check(lib.q35_runtime_last_hidden(self.handle, _ptr(out), out.size), "last hidden")
+        return out
+
+    def close(self):
+        if self.handle is not None:
+            lib.q35_runtime_destroy(self.handle)
+            self.handle = None
+
+
+class Engine:
+    """CpuEngine mirror (include/qwen35x/runtime/cpu_engine.h:173-215), greedy requests."""
+
+    def __init__(self, model, max_resident_requests=32, max_context=8192, max_decode_batch_size=32,
+                 prefill_chunk_size=128, page_tokens=16, use_graphs=True):
+        self.model, self.ctx = model, model.ctx
+        cfg = EngineConfig(max_resident_requests, max_context, max_decode_batch_size, prefill_chunk_size,
+                           page_tokens, int(use_graphs))
+        h = c_void_p()
+        self.ctx.check(lib.q35_engine_create(model.handle, ctypes.byref(cfg), ctypes.byref(h)), "engine create")
+        self.handle = h
+
+    def _check(self, status, what):
+        if status != Q35_OK:
+            raise Q35Error(f"{what}: {STATUS.get(status, status)} "
+                           f"{lib.q35_engine_last_error(self.handle).decode(errors='replace')}")
+
+    def submit(self, prompt, max_new_tokens=128, repetition_penalty=1.0, stop_token_ids=()):
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        stops = np.ascontiguousarray(stop_token_ids, np.int32)
+        rid = c_uint64()
+        self._check(lib.q35_engine_submit(self.handle, _ptr(prompt), prompt.size, max_new_tokens,
+                                          repetition_penalty, _ptr(stops) if stops.size else None, stops.size,
+                                          ctypes.byref(rid)), "submit")
+        return rid.value
+
+    def advance(self, rid):
+        self._check(lib.q35_engine_advance(self.handle, rid), "advance")
+
+    def advance_batch(self, ids):
+        a = np.ascontiguousarray(ids, np.uint64)
+        self._check(lib.q35_engine_advance_batch(self.handle, _ptr(a), a.size), "advance_batch")
+
+    def prefill_batch(self, ids):
+        a = np.ascontiguousarray(ids, np.uint64)
+        self._check(lib.q35_engine_prefill_batch(self.handle, _ptr(a), a.size), "prefill_batch")
+
+    def step(self):
+        p = c_int32()
+        self._check(lib.q35_engine_step(self.handle, ctypes.byref(p)), "step")
+        return bool(p.value)
+
+    def result(self, rid):
+        r = RequestResult()
+        n = c_size_t()
+        self._check(lib.q35_engine_result(self.handle, rid, ctypes.byref(r), None, 0, ctypes.byref(n)), "result")
+        toks = np.empty(n.value, np.int32)
+        if n.value:
+            self._check(lib.q35_engine_result(self.handle, rid, None, _ptr(toks), n.value, None), "result")
+        return r, toks
+
+    def cancel(self, rid):
+        self._check(lib.q35_engine_cancel(self.handle, rid), "cancel")
+
+    def release(self, rid):
+        self._check(lib.q35_engine_release(self.handle, rid), "release")
+
+    def close(self):
+        if self.handle is not None:
+            lib.q35_engine_destroy(self.handle)
+            self.handle = None

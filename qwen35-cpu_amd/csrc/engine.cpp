@@ -1,0 +1,417 @@
+// q35_engine: the request-level mirror of qwen35x::CpuEngine
+// (include/qwen35x/runtime/cpu_engine.h:173-215) for greedy requests, driving
+// the device runtime one step at a time.
+//   submit          cpu_engine.inl:832-930 (validation, admission)
+//   advance         one prefill chunk or one decode row (cpu_engine.inl:668-790)
+//   advance_batch   one decode row per distinct active request; validation
+//                   leaves requests untouched; a failed forward fails every
+//                   row and is never retried (cpu_engine.inl:939-1017)
+//   step            serving scheduler: retire, admit, alternate decode batches
+//                   with prefill chunks, rotate for fairness
+//                   (cpu_engine_scheduler.inl:2-105)
+// Request state lives on the device: a slot (DeltaNet state, conv ring,
+// penalty counts) and a list of KV pages that grows as positions advance.
+#include <algorithm>
+#include <chrono>
+#include <cstring>
+#include <map>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "runtime.h"
+
+namespace {
+
+struct Request {
+  uint64_t id = 0;
+  std::vector<int32_t> prompt;
+  size_t max_new = 0;
+  float penalty = 1.0F;
+  std::vector<int32_t> stops;
+  int status = Q35_REQ_QUEUED;
+  int slot = -1;
+  std::vector<int32_t> pages;
+  size_t committed = 0;  // tokens whose state is in the slot / KV
+  int32_t pending = -1;  // next decode input (last generated token)
+  std::vector<int32_t> output;
+  q35_request_result result{};
+  bool resident = false;
+};
+
+double ms_since(std::chrono::steady_clock::time_point t) {
+  return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t).count();
+}
+
+}  // namespace
+
+struct q35_engine {
+  q35_model *model = nullptr;
+  q35_runtime *rt = nullptr;
+  q35_engine_config cfg{};
+  int32_t max_queued = 0;
+  std::map<uint64_t, Request> reqs;
+  uint64_t next_id = 1;
+  std::string error;
+  bool prefer_decode = true, scheduling = false;
+  uint64_t last_prefill = 0, last_decode = 0;
+};
+
+namespace {
+
+int fail(q35_engine *e, int status, const std::string &msg) {
+  e->error = msg;
+  return status;
+}
+
+bool terminal(const Request &r) {
+  return r.status == Q35_REQ_COMPLETE || r.status == Q35_REQ_CANCELLED || r.status == Q35_REQ_FAILED;
+}
+
+void retire(q35_engine *e, Request &r) {
+  if (!r.resident || !terminal(r)) return;
+  for (int32_t p : r.pages) (void)q35_page_release(e->rt, p);
+  r.pages.clear();
+  if (r.slot >= 0) (void)q35_slot_free(e->rt, r.slot);
+  r.slot = -1;
+  r.resident = false;
+}
+
+int activate(q35_engine *e, Request &r) {
+  int32_t slot = -1;
+  const int st = q35_slot_alloc(e->rt, r.prompt.data(), r.prompt.size(), &slot);
+  if (st != Q35_OK) return fail(e, st, e->model->ctx->error.c_str());
+  r.slot = slot;
+  r.resident = true;
+  r.status = Q35_REQ_PREFILL;
+  return Q35_OK;
+}
+
+// Make sure a page covers `position` (KvPagesF16::append allocates the next page).
+int ensure_page(q35_engine *e, Request &r, size_t position) {
+  const size_t need = position / static_cast<size_t>(e->cfg.page_tokens) + 1;
+  while (r.pages.size() < need) {
+    int32_t p = -1;
+    const int st = q35_page_alloc(e->rt, &p);
+    if (st != Q35_OK) return fail(e, st, "KV page pool exhausted");
+    r.pages.push_back(p);
+  }
+  return Q35_OK;
+}
+
+// select() (cpu_engine.inl:441-487): append, stop ids, completion.
+void select_token(Request &r, int32_t token) {
+  ++r.result.generated_tokens;
+  r.output.push_back(token);
+  r.pending = token;
+  if (std::find(r.stops.begin(), r.stops.end(), token) != r.stops.end()) {
+    r.output.pop_back();
+    r.status = Q35_REQ_COMPLETE;
+  } else {
+    r.status = r.output.size() == r.max_new ? Q35_REQ_COMPLETE : Q35_REQ_DECODE;
+  }
+}
+
+// One device step over `rows`: each row feeds `inputs[i]` at position
+// rows[i]->committed. count_input marks generated tokens.
+int run_step(q35_engine *e, const std::vector<Request *> &rows, const std::vector<int32_t> &inputs,
+             const std::vector<uint8_t> &count_input, std::vector<int32_t> &out) {
+  const int B = static_cast<int>(rows.size());
+  const int max_pages = (e->cfg.max_context + e->cfg.page_tokens - 1) / e->cfg.page_tokens;
+  std::vector<int32_t> slots(B), positions(B), table(static_cast<size_t>(B) * max_pages, 0);
+  std::vector<float> pen(B);
+  for (int b = 0; b < B; ++b) {
+    Request &r = *rows[b];
+    int st = ensure_page(e, r, r.committed);
+    if (st != Q35_OK) return st;
+    slots[b] = r.slot;
+    positions[b] = static_cast<int32_t>(r.committed);
+    pen[b] = r.penalty;
+    std::copy(r.pages.begin(), r.pages.end(), table.begin() + static_cast<size_t>(b) * max_pages);
+  }
+  q35_step_desc d{};
+  d.batch = B;
+  d.slots = slots.data();
+  d.positions = positions.data();
+  d.tokens = inputs.data();
+  d.count_input = count_input.data();
+  d.penalties = pen.data();
+  d.page_table = table.data();
+  d.max_pages = max_pages;
+  out.assign(B, -1);
+  const int st = q35_runtime_step(e->rt, &d, out.data(), nullptr);
+  if (st != Q35_OK) return fail(e, st, e->model->ctx->error.c_str());
+  for (auto *r : rows) ++r->committed;
+  return Q35_OK;
+}
+
+void fail_rows(const std::vector<Request *> &rows) {
+  for (auto *r : rows) r->status = Q35_REQ_FAILED;
+}
+
+}  // namespace
+
+extern "C" int q35_engine_create(q35_model *m, const q35_engine_config *cfg, q35_engine **out) {
+  if (m == nullptr || cfg == nullptr || out == nullptr) return Q35_ERR_INVALID;
+  *out = nullptr;
+  if (cfg->max_resident_requests <= 0 || cfg->max_context <= 0 || cfg->max_decode_batch_size <= 0 ||
+      cfg->max_decode_batch_size > q35::kMaxTokens || cfg->page_tokens <= 0)
+    return Q35_ERR_INVALID;
+  auto *e = new (std::nothrow) q35_engine();
+  if (e == nullptr) return Q35_ERR_OOM;
+  e->model = m;
+  e->cfg = *cfg;
+  if (e->cfg.prefill_chunk_size <= 0) e->cfg.prefill_chunk_size = 128;
+  q35_runtime_config rc{};
+  rc.max_slots = cfg->max_resident_requests;
+  rc.max_batch = std::max(cfg->max_decode_batch_size, 1);
+  rc.max_context = cfg->max_context;
+  rc.page_tokens = cfg->page_tokens;
+  rc.use_graphs = cfg->use_graphs;
+  const int st = q35_runtime_create(m, &rc, &e->rt);
+  if (st != Q35_OK) {
+    delete e;
+    return st;
+  }
+  *out = e;
+  return Q35_OK;
+}
+
+extern "C" void q35_engine_destroy(q35_engine *e) {
+  if (e == nullptr) return;
+  q35_runtime_destroy(e->rt);
+  delete e;
+}
+
+extern "C" const char *q35_engine_last_error(const q35_engine *e) {
+  return e ? e->error.c_str() : "null engine";
+}
+
+extern "C" int q35_engine_submit(q35_engine *e, const int32_t *prompt, size_t n, size_t max_new,
+                                 float penalty, const int32_t *stops, size_t n_stops, uint64_t *out_id) {
+  if (e == nullptr || out_id == nullptr) return Q35_ERR_INVALID;
+  *out_id = 0;
+  e->error.clear();
+  const int vocab = e->model->d.vocab;
+  const size_t ctx = static_cast<size_t>(e->cfg.max_context);
+  size_t resident = 0;
+  for (auto &kv : e->reqs) resident += kv.second.resident;
+  if (prompt == nullptr || n == 0 || max_new == 0 || n > ctx || max_new - 1 > ctx - n ||
+      !(penalty >= 1.0F) || e->reqs.size() >= static_cast<size_t>(e->cfg.max_resident_requests) + 64)
+    return fail(e, Q35_ERR_INVALID, "Invalid request or resident/context limit reached.");
+  for (size_t i = 0; i < n; ++i)
+    if (prompt[i] < 0 || prompt[i] >= vocab) return fail(e, Q35_ERR_INVALID, "Invalid request token.");
+  Request r;
+  r.id = e->next_id++;
+  r.prompt.assign(prompt, prompt + n);
+  r.max_new = max_new;
+  r.penalty = penalty;
+  if (stops && n_stops) r.stops.assign(stops, stops + n_stops);
+  r.status = Q35_REQ_QUEUED;
+  if (resident < static_cast<size_t>(e->cfg.max_resident_requests)) {
+    const int st = activate(e, r);
+    if (st != Q35_OK) return st;
+  }
+  *out_id = r.id;
+  e->reqs.emplace(r.id, std::move(r));
+  return Q35_OK;
+}
+
+// Prefill `rows` jointly, one prompt token per row per device step, until each
+// row has consumed `limit` more tokens or its prompt. The step that consumes
+// the last prompt token yields the first generated token.
+static int prefill_rows(q35_engine *e, std::vector<Request *> rows, size_t limit) {
+  const auto t0 = std::chrono::steady_clock::now();
+  std::vector<Request *> all = rows;
+  while (!rows.empty()) {
+    std::vector<int32_t> in, out;
+    std::vector<uint8_t> cnt;
+    for (auto *r : rows) {
+      in.push_back(r->prompt[r->committed]);
+      cnt.push_back(0);
+    }
+    const int st = run_step(e, rows, in, cnt, out);
+    if (st != Q35_OK) {
+      fail_rows(all);
+      return st;
+    }
+    std::vector<Request *> next;
+    for (size_t i = 0; i < rows.size(); ++i) {
+      Request *r = rows[i];
+      ++r->result.prefill_tokens;
+      if (r->committed == r->prompt.size()) {
+        select_token(*r, out[i]);
+      } else if (r->result.prefill_tokens % limit != 0) {
+        next.push_back(r);
+      }
+    }
+    rows.swap(next);
+  }
+  const double ms = ms_since(t0);
+  for (auto *r : all) {
+    r->result.prefill_ms += ms / all.size();
+    r->result.committed_tokens = r->committed;
+  }
+  return Q35_OK;
+}
+
+extern "C" int q35_engine_advance(q35_engine *e, uint64_t id) {
+  if (e == nullptr) return Q35_ERR_INVALID;
+  e->error.clear();
+  auto it = e->reqs.find(id);
+  if (it == e->reqs.end()) return fail(e, Q35_ERR_STATE, "Unknown request ID.");
+  Request &r = it->second;
+  if (r.status == Q35_REQ_PREFILL) return prefill_rows(e, {&r}, static_cast<size_t>(e->cfg.prefill_chunk_size));
+  if (r.status != Q35_REQ_DECODE) return fail(e, Q35_ERR_STATE, "Request is not active.");
+  return q35_engine_advance_batch(e, &id, 1);
+}
+
+extern "C" int q35_engine_advance_batch(q35_engine *e, const uint64_t *ids, size_t count) {
+  if (e == nullptr) return Q35_ERR_INVALID;
+  e->error.clear();
+  if (count == 0) return Q35_OK;
+  if (ids == nullptr || count > static_cast<size_t>(e->cfg.max_decode_batch_size))
+    return fail(e, Q35_ERR_INVALID, "Decode batch exceeds max_decode_batch_size.");
+  std::vector<Request *> rows;
+  for (size_t i = 0; i < count; ++i) {
+    auto it = e->reqs.find(ids[i]);
+    if (it == e->reqs.end() || it->second.status != Q35_REQ_DECODE ||
+        std::find(rows.begin(), rows.end(), &it->second) != rows.end())
+      return fail(e, Q35_ERR_INVALID, "Decode batch requires distinct active decode requests.");
+    rows.push_back(&it->second);
+  }
+  const auto t0 = std::chrono::steady_clock::now();
+  std::vector<int32_t> in, out;
+  std::vector<uint8_t> cnt;
+  for (auto *r : rows) {
+    in.push_back(r->pending);
+    cnt.push_back(1);
+  }
+  const int st = run_step(e, rows, in, cnt, out);
+  if (st != Q35_OK) {
+    // A failed forward may have updated state: never retry it.
+    fail_rows(rows);
+    return st;
+  }
+  const double ms = ms_since(t0);
+  for (size_t i = 0; i < rows.size(); ++i) {
+    Request *r = rows[i];
+    ++r->result.decode_forwards;
+    r->result.decode_ms += ms / rows.size();
+    r->result.committed_tokens = r->committed;
+    select_token(*r, out[i]);
+  }
+  return Q35_OK;
+}
+
+// Extension without a reference counterpart: prefill several requests in the
+// same device steps (the reference prefills one request per advance()).
+extern "C" int q35_engine_prefill_batch(q35_engine *e, const uint64_t *ids, size_t count) {
+  if (e == nullptr || (count && ids == nullptr)) return Q35_ERR_INVALID;
+  e->error.clear();
+  if (count > static_cast<size_t>(e->cfg.max_decode_batch_size))
+    return fail(e, Q35_ERR_INVALID, "Prefill batch exceeds max_decode_batch_size.");
+  std::vector<Request *> rows;
+  for (size_t i = 0; i < count; ++i) {
+    auto it = e->reqs.find(ids[i]);
+    if (it == e->reqs.end() || it->second.status != Q35_REQ_PREFILL ||
+        std::find(rows.begin(), rows.end(), &it->second) != rows.end())
+      return fail(e, Q35_ERR_INVALID, "Prefill batch requires distinct prefilling requests.");
+    rows.push_back(&it->second);
+  }
+  return prefill_rows(e, rows, static_cast<size_t>(e->cfg.max_context));
+}
+
+extern "C" int q35_engine_step(q35_engine *e, int32_t *progressed) {
+  if (e == nullptr || progressed == nullptr) return Q35_ERR_INVALID;
+  *progressed = 0;
+  e->error.clear();
+  if (e->scheduling) return fail(e, Q35_ERR_STATE, "step is not reentrant.");
+  e->scheduling = true;
+  struct Guard {
+    bool &v;
+    ~Guard() { v = false; }
+  } guard{e->scheduling};
+  size_t resident = 0;
+  std::vector<uint64_t> queued;
+  for (auto &kv : e->reqs) {
+    retire(e, kv.second);
+    resident += kv.second.resident;
+    if (kv.second.status == Q35_REQ_QUEUED) queued.push_back(kv.first);
+  }
+  // admit at most one queued request per step (max_prefill_requests = 1)
+  if (!queued.empty() && resident < static_cast<size_t>(e->cfg.max_resident_requests)) {
+    Request &r = e->reqs.at(queued.front());
+    *progressed = 1;
+    const int st = activate(e, r);
+    if (st != Q35_OK) {
+      r.status = Q35_REQ_FAILED;
+      return st;
+    }
+  }
+  std::vector<uint64_t> prefill, decode;
+  for (auto &kv : e->reqs) {
+    if (kv.second.status == Q35_REQ_PREFILL) prefill.push_back(kv.first);
+    if (kv.second.status == Q35_REQ_DECODE) decode.push_back(kv.first);
+  }
+  auto rotate = [](std::vector<uint64_t> &ids, uint64_t last) {
+    std::rotate(ids.begin(), std::upper_bound(ids.begin(), ids.end(), last), ids.end());
+  };
+  rotate(prefill, e->last_prefill);
+  rotate(decode, e->last_decode);
+  if (prefill.empty() && decode.empty()) return Q35_OK;
+  const bool do_decode = !decode.empty() && (prefill.empty() || e->prefer_decode);
+  e->prefer_decode = !do_decode;
+  *progressed = 1;
+  int st;
+  std::vector<uint64_t> work;
+  if (do_decode) {
+    decode.resize(std::min(decode.size(), static_cast<size_t>(e->cfg.max_decode_batch_size)));
+    work = decode;
+    e->last_decode = work.back();
+    st = q35_engine_advance_batch(e, work.data(), work.size());
+  } else {
+    work.push_back(prefill.front());
+    e->last_prefill = work.back();
+    st = q35_engine_advance(e, work.front());
+  }
+  for (auto id : work) retire(e, e->reqs.at(id));
+  return st;
+}
+
+extern "C" int q35_engine_result(q35_engine *e, uint64_t id, q35_request_result *out, int32_t *tokens,
+                                 size_t capacity, size_t *count) {
+  if (e == nullptr) return Q35_ERR_INVALID;
+  auto it = e->reqs.find(id);
+  if (it == e->reqs.end()) return fail(e, Q35_ERR_STATE, "Unknown request ID.");
+  const Request &r = it->second;
+  if (out != nullptr) {
+    *out = r.result;
+    out->status = r.status;
+    out->committed_tokens = r.committed;
+  }
+  if (count != nullptr) *count = r.output.size();
+  if (tokens != nullptr) std::memcpy(tokens, r.output.data(), std::min(capacity, r.output.size()) * 4);
+  return Q35_OK;
+}
+
+extern "C" int q35_engine_cancel(q35_engine *e, uint64_t id) {
+  if (e == nullptr) return Q35_ERR_INVALID;
+  auto it = e->reqs.find(id);
+  if (it == e->reqs.end()) return Q35_ERR_STATE;
+  Request &r = it->second;
+  if (!terminal(r)) r.status = Q35_REQ_CANCELLED;
+  retire(e, r);
+  return Q35_OK;
+}
+
+extern "C" int q35_engine_release(q35_engine *e, uint64_t id) {
+  if (e == nullptr) return Q35_ERR_INVALID;
+  auto it = e->reqs.find(id);
+  if (it == e->reqs.end()) return Q35_ERR_STATE;
+  Request &r = it->second;
+  if (!terminal(r)) r.status = Q35_REQ_CANCELLED;
+  retire(e, r);
+  e->reqs.erase(it);
+  return Q35_OK;
+}

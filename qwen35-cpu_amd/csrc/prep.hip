@@ -1,0 +1,212 @@
+// Activation preparation for the Q4-G32-DOT4 projections: optional producer
+// (RMSNorm, SiLU*mul, split-K attention merge), then the randomized-sign
+// Hadamard-128 rotation and per-32 int8 quantization.
+//
+// Reference semantics (bit-exact given the same FP32 input):
+//   signs + FWHT stage order 1,2,...,64     src/cpu/q4_h128.cpp:35-61
+//   absmax/127, unrounded 1/scale, round half away from zero, clamp +-127,
+//   stored scale = binary16(scale) * 1/sqrt(128)   q4_0.cpp:212-235, q4_h128.cpp:319-321
+// One workgroup (4 wavefronts) per token row; each wavefront owns whole
+// 128-column blocks, two values per lane, so the first six FWHT stages are
+// lane shuffles and the last one is in-lane.
+#include "q35_device.h"
+#include "q35_internal.h"
+
+namespace q35 {
+namespace {
+
+constexpr int kPrepThreads = 256;
+
+// Merge of split-K attention partials for one (token, head, dim), pairwise in
+// split order with the zero-sum identity (merge_attention_partial,
+// src/cpu/full_attention_tiled.cpp:66-78), then normalised and gated
+// (full_attention.cpp:104-127).
+__device__ float attention_merge_value(const PrepArgs &a, int t, int c) {
+  const int h = c / a.head_dim, d = c - h * a.head_dim;
+  const int seq = a.seq_lens[t];
+  const int splits = (seq + a.split_tokens - 1) / a.split_tokens;
+  const size_t hs = (static_cast<size_t>(t) * a.heads + h) * a.max_splits;
+  float m = 0.0F, l = 0.0F, v = 0.0F;
+  for (int s = 0; s < splits; ++s) {
+    const float om = a.part_ml[(hs + s) * 2], ol = a.part_ml[(hs + s) * 2 + 1];
+    const float ov = a.part_o[(hs + s) * a.head_dim + d];
+    if (ol == 0.0F) continue;
+    if (l == 0.0F) {
+      m = om; l = ol; v = ov;
+      continue;
+    }
+    const float mm = fmaxf(m, om);
+    const float x = expf(m - mm), y = expf(om - mm);
+    v = x * v + y * ov;
+    l = x * l + y * ol;
+    m = mm;
+  }
+  const float inv = 1.0F / (l > 0.0F ? l : 1.0F);
+  const float g = a.gates[(static_cast<size_t>(t) * a.heads + h) * a.head_dim + d];
+  return (v * inv) * sigmoid_stable(g);
+}
+
+template <int SRC>
+__device__ __forceinline__ float load_source(const PrepArgs &a, int t, int c, float rms_inv) {
+  const float *row = a.x + static_cast<size_t>(t) * a.x_stride;
+  if constexpr (SRC == kPrepPlain) {
+    return row[c];
+  } else if constexpr (SRC == kPrepRmsNorm) {
+    return row[c] * rms_inv * (a.weight[c] + a.weight_offset);
+  } else if constexpr (SRC == kPrepSiluMul) {
+    return silu_times(row[c], row[c + a.K]);
+  } else {
+    return attention_merge_value(a, t, c);
+  }
+}
+
+template <int SRC>
+__global__ __launch_bounds__(kPrepThreads) void prep_kernel(PrepArgs a) {
+  __shared__ float scratch[8];
+  const int t = blockIdx.x;
+  const int K = a.K, nb = K >> 5;
+  if (a.argmax_reset != nullptr && t == 0)
+    for (int i = threadIdx.x; i < a.argmax_reset_count; i += kPrepThreads) a.argmax_reset[i] = 0ull;
+
+  float rms_inv = 1.0F;
+  if constexpr (SRC == kPrepRmsNorm) {
+    const float *row = a.x + static_cast<size_t>(t) * a.x_stride;
+    float ss = 0.0F;
+    for (int i = threadIdx.x; i < K; i += kPrepThreads) ss += row[i] * row[i];
+    ss = block_sum<kPrepThreads / 64>(ss, scratch);
+    rms_inv = 1.0F / sqrtf(ss / static_cast<float>(K) + a.eps);
+  }
+
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int tile = t >> 4, tok = t & 15;
+  for (int blk = wave; blk < (K >> 7); blk += kPrepThreads / 64) {
+    const int c0 = blk * 128 + lane, c1 = c0 + 64;
+    float v0 = load_source<SRC>(a, t, c0, rms_inv);
+    float v1 = load_source<SRC>(a, t, c1, rms_inv);
+    if (a.normed_out != nullptr) {
+      a.normed_out[static_cast<size_t>(t) * K + c0] = v0;
+      a.normed_out[static_cast<size_t>(t) * K + c1] = v1;
+    }
+    if (a.h128) {
+      const uint64_t w0 = h128_sign_word(blk, 0, a.seed), w1 = h128_sign_word(blk, 1, a.seed);
+      if ((w0 >> lane) & 1ull) v0 = -v0;
+      if ((w1 >> lane) & 1ull) v1 = -v1;
+#pragma unroll
+      for (int s = 1; s < 64; s <<= 1) {
+        const float p0 = __shfl_xor(v0, s, 64), p1 = __shfl_xor(v1, s, 64);
+        if (lane & s) {
+          v0 = p0 - v0;
+          v1 = p1 - v1;
+        } else {
+          v0 = v0 + p0;
+          v1 = v1 + p1;
+        }
+      }
+      const float lhs = v0;
+      v0 = lhs + v1;
+      v1 = lhs - v1;
+    }
+    // Two 32-value groups per value slot: group(v0) = lane/32, group(v1) = 2 + lane/32.
+    float vals[2] = {v0, v1};
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const float v = vals[half];
+      const float amax = group_max<32>(fabsf(v));
+      const float scale = amax / 127.0F;
+      const float inv = scale == 0.0F ? 0.0F : 1.0F / scale;
+      float r = roundf(v * inv);
+      r = fminf(fmaxf(r, -127.0F), 127.0F);
+      const int code = static_cast<int>(r);
+      const int sum = group_sum_int<32>(code);
+      float stored = half_bits_to_float(float_to_half_bits(scale));
+      if (a.h128) stored *= kH128InvSqrt;
+      const int b = blk * 4 + half * 2 + (lane >> 5);
+      const int k = lane & 31;
+      if (a.codes != nullptr) {
+        uint8_t *dst = reinterpret_cast<uint8_t *>(a.codes);
+        const size_t word = (static_cast<size_t>(tile) * nb + b) * 64 + tok + 16 * (k >> 3);
+        dst[word * 8 + (k & 7)] = static_cast<uint8_t>(static_cast<int8_t>(code));
+        if (k == 0)
+          a.params[(static_cast<size_t>(tile) * nb + b) * 16 + tok] = ActParam{stored, -8 * sum};
+      }
+      if (a.x4 != nullptr) {
+        q35_q8_0_block_x4 &blkx = a.x4[static_cast<size_t>(t >> 2) * nb + b];
+        blkx.qs[(t & 3) * 32 + k] = static_cast<int8_t>(code);
+        if (k == 0) {
+          blkx.scales[t & 3] = stored;
+          blkx.sums[t & 3] = static_cast<int16_t>(sum);
+        }
+      }
+      if (a.x1 != nullptr) {
+        q35_q8_0_block_x1 &blk1 = a.x1[static_cast<size_t>(t) * nb + b];
+        blk1.qs[k] = static_cast<int8_t>(code);
+        if (k == 0) {
+          blk1.scales[0] = stored;
+          blk1.sums[0] = static_cast<int16_t>(sum);
+          blk1.pad = 0;
+        }
+      }
+    }
+  }
+}
+
+// X4 (reference prefill layout) -> A16.
+__global__ void x4_to_a16_kernel(const q35_q8_0_block_x4 *x4, int tokens, int nb, uint64_t *codes,
+                                 ActParam *params) {
+  const int b = blockIdx.x, tile = blockIdx.y, lane = threadIdx.x;
+  const int tok = tile * 16 + (lane & 15), g = lane >> 4;
+  uint64_t word = 0;
+  ActParam p{0.0F, 0};
+  if (tok < tokens) {
+    const q35_q8_0_block_x4 &src = x4[static_cast<size_t>(tok >> 2) * nb + b];
+    const uint8_t *q = reinterpret_cast<const uint8_t *>(src.qs) + (tok & 3) * 32 + g * 8;
+    for (int i = 0; i < 8; ++i) word |= static_cast<uint64_t>(q[i]) << (8 * i);
+    p = ActParam{src.scales[tok & 3], -8 * static_cast<int32_t>(src.sums[tok & 3])};
+  }
+  codes[(static_cast<size_t>(tile) * nb + b) * 64 + lane] = word;
+  if (g == 0) params[(static_cast<size_t>(tile) * nb + b) * 16 + (lane & 15)] = p;
+}
+
+__global__ void x1_to_a16_kernel(const q35_q8_0_block_x1 *x1, int nb, uint64_t *codes,
+                                 ActParam *params) {
+  const int b = blockIdx.x, lane = threadIdx.x;
+  const int tok = lane & 15, g = lane >> 4;
+  uint64_t word = 0;
+  ActParam p{0.0F, 0};
+  if (tok == 0) {
+    const uint8_t *q = reinterpret_cast<const uint8_t *>(x1[b].qs) + g * 8;
+    for (int i = 0; i < 8; ++i) word |= static_cast<uint64_t>(q[i]) << (8 * i);
+    p = ActParam{x1[b].scales[0], -8 * static_cast<int32_t>(x1[b].sums[0])};
+  }
+  codes[static_cast<size_t>(b) * 64 + lane] = word;
+  if (g == 0) params[static_cast<size_t>(b) * 16 + tok] = p;
+}
+
+}  // namespace
+
+hipError_t launch_prep(const PrepArgs &a, hipStream_t stream) {
+  if (a.tokens <= 0) return hipSuccess;
+  const dim3 grid(a.tokens), block(kPrepThreads);
+  switch (a.source) {
+    case kPrepPlain: Q35_LAUNCH((prep_kernel<kPrepPlain>), grid, block, 0, stream, a); break;
+    case kPrepRmsNorm: Q35_LAUNCH((prep_kernel<kPrepRmsNorm>), grid, block, 0, stream, a); break;
+    case kPrepSiluMul: Q35_LAUNCH((prep_kernel<kPrepSiluMul>), grid, block, 0, stream, a); break;
+    default: Q35_LAUNCH((prep_kernel<kPrepAttnMerge>), grid, block, 0, stream, a); break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_x4_to_a16(const q35_q8_0_block_x4 *x4, int tokens, int nb, uint64_t *codes,
+                            ActParam *params, hipStream_t stream) {
+  const dim3 grid(nb, (tokens + 15) / 16);
+  Q35_LAUNCH((x4_to_a16_kernel), grid, 64, 0, stream, x4, tokens, nb, codes, params);
+  return hipGetLastError();
+}
+
+hipError_t launch_x1_to_a16(const q35_q8_0_block_x1 *x1, int nb, uint64_t *codes,
+                            ActParam *params, hipStream_t stream) {
+  Q35_LAUNCH((x1_to_a16_kernel), nb, 64, 0, stream, x1, nb, codes, params);
+  return hipGetLastError();
+}
+
+}  // namespace q35

@@ -1,0 +1,97 @@
+// Device-side helpers shared by the gfx950 kernels (64-lane wavefronts).
+#pragma once
+
+#include "q35_hip_api.h"
+
+#include <cstdint>
+
+namespace q35 {
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t h) {
+  return __half2float(__ushort_as_half(h));
+}
+// Round to nearest even, as float_to_half (src/cpu/q8_0.cpp:18-55) for finite values.
+__device__ __forceinline__ uint16_t float_to_half_bits(float f) {
+  return __half_as_ushort(__float2half_rn(f));
+}
+
+// XOR-butterfly reductions over groups of `Width` lanes (Width <= 64, power of 2).
+template <int Width>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int m = Width / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+template <int Width>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int m = Width / 2; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+template <int Width>
+__device__ __forceinline__ int group_sum_int(int v) {
+#pragma unroll
+  for (int m = Width / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+// Sum over a whole workgroup of `Waves` wavefronts; every thread gets the result.
+template <int Waves>
+__device__ __forceinline__ float block_sum(float v, float *scratch) {
+  v = group_sum<64>(v);
+  const int wave = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) scratch[wave] = v;
+  __syncthreads();
+  float total = 0.0F;
+#pragma unroll
+  for (int w = 0; w < Waves; ++w) total += scratch[w];
+  return total;
+}
+
+// splitmix64 sign words of the randomized-sign H128 basis (src/cpu/q4_h128.cpp:16-33).
+__device__ __forceinline__ uint64_t splitmix64(uint64_t v) {
+  v += 0x9e3779b97f4a7c15ull;
+  v = (v ^ (v >> 30)) * 0xbf58476d1ce4e5b9ull;
+  v = (v ^ (v >> 27)) * 0x94d049bb133111ebull;
+  return v ^ (v >> 31);
+}
+__device__ __forceinline__ uint64_t h128_sign_word(uint64_t block, uint64_t word, uint64_t seed) {
+  return splitmix64(seed + block * 0x9e3779b97f4a7c15ull + word * 0xd1b54a32d192ed03ull);
+}
+
+// Logistic functions with the reference's branch structure
+// (src/runtime/weights.inl:656-678, src/cpu/activation.cpp:329-357).
+__device__ __forceinline__ float sigmoid_stable(float x) {
+  if (x >= 0.0F) return 1.0F / (1.0F + expf(-x));
+  const float z = expf(x);
+  return z / (1.0F + z);
+}
+__device__ __forceinline__ float silu_times(float g, float u) {
+  const float e = expf(-fabsf(g));
+  const float s = g >= 0.0F ? 1.0F / (1.0F + e) : e / (1.0F + e);
+  return g * s * u;
+}
+__device__ __forceinline__ float softplus_stable(float x) {
+  if (x > 20.0F) return x;
+  if (x < -20.0F) return expf(x);
+  return log1pf(expf(x));
+}
+
+// Monotone 64-bit key: larger value first, then lower index (ties go to the
+// lowest token, src/runtime/cpu_engine_greedy.inl:53-56).
+__device__ __forceinline__ unsigned long long argmax_key(float value, uint32_t index) {
+  uint32_t u = __float_as_uint(value);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return (static_cast<unsigned long long>(u) << 32) | static_cast<uint32_t>(0xffffffffu - index);
+}
+__device__ __forceinline__ float argmax_key_value(unsigned long long key) {
+  uint32_t u = static_cast<uint32_t>(key >> 32);
+  u = (u & 0x80000000u) ? (u & 0x7fffffffu) : ~u;
+  return __uint_as_float(u);
+}
+__device__ __forceinline__ uint32_t argmax_key_index(unsigned long long key) {
+  return 0xffffffffu - static_cast<uint32_t>(key & 0xffffffffu);
+}
+
+}  // namespace q35

@@ -1,0 +1,19 @@
+// The HIP API surface used by the backend. The product is always built by
+// hipcc for gfx950; Q35_HOST_EMULATION selects the test-only CPU build in
+// tests/emu/ (the same kernel sources run on host threads under
+// AddressSanitizer to bounds-check every kernel before it runs on a GPU).
+#pragma once
+
+#ifdef Q35_HOST_EMULATION
+#include "q35_host_emulation.h"
+#else
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#define Q35_LAUNCH(kernel, grid, block, smem, stream, ...) \
+  hipLaunchKernelGGL(kernel, grid, block, smem, stream, __VA_ARGS__)
+#define Q35_V4I int __attribute__((ext_vector_type(4)))
+#define Q35_MFMA_I32_16X16X32_I8(a, b, c, cbsz, abid, blgp) \
+  __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, cbsz, abid, blgp)
+#define Q35_DYNAMIC_SHARED(type, name) extern __shared__ type name[]
+#endif

@@ -1,0 +1,206 @@
+// Internal declarations shared by the HIP kernels and the host runtime of the
+// MI355X decode backend. Not part of the public ABI (include/q35_hip.h).
+#pragma once
+
+#include "q35_hip_api.h"
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "q35_hip.h"
+
+namespace q35 {
+
+// ---------------------------------------------------------------- context
+struct Context {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  bool own_stream = false;
+  int cu_count = 0;
+  std::string arch;
+  std::string error;
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+};
+
+int set_error(Context *ctx, int status, const std::string &message);
+int hip_error(Context *ctx, hipError_t e, const char *what);
+
+#define Q35_HIP_TRY(ctx, expr)                                   \
+  do {                                                           \
+    hipError_t q35_e_ = (expr);                                  \
+    if (q35_e_ != hipSuccess) return ::q35::hip_error((ctx), q35_e_, #expr); \
+  } while (0)
+
+// ------------------------------------------------------------- block types
+static_assert(sizeof(q35_q4_0_block_x8) == 144, "Q4_0BlockX8 is 144 bytes");
+static_assert(sizeof(q35_q8_0_block_x4) == 152, "Q8_0BlockX4 is 152 bytes");
+static_assert(sizeof(q35_q8_0_block_x1) == 40, "Q8_0BlockX1 is 40 bytes");
+static_assert(offsetof(q35_q8_0_block_x4, qs) == 24, "Q8_0BlockX4 layout");
+static_assert(offsetof(q35_q8_0_block_x1, qs) == 6, "Q8_0BlockX1 layout");
+
+// Prepared activations in the layout the MFMA GEMM consumes ("A16"): for each
+// 16-token tile and 32-column block, 64 lanes x 8 bytes where lane l carries
+// token (l % 16) and columns 8*(l/16) .. 8*(l/16)+7 of the block; plus one
+// ActParam per token: the FP32 activation scale (binary16-rounded, with the
+// H128 1/sqrt(128) folded in exactly as the reference does) and -8 * sum of
+// the int8 codes (the offset-binary correction of q4_dot4_simd.inl:89).
+struct ActParam {
+  float scale;
+  int32_t corr;
+};
+
+constexpr float kH128InvSqrt = 0.08838834764831844055F;  // q4_h128.h:24
+constexpr int kMaxTokens = 64;                            // rows per GEMM launch
+
+// ------------------------------------------------------------ launchers
+// All launchers enqueue on `stream` and return hipSuccess or the launch error.
+
+// Activation preparation source modes.
+enum PrepSource : int {
+  kPrepPlain = 0,      // y = x
+  kPrepRmsNorm = 1,    // y = rms_norm(x, w, eps, offset 1)   (prefill.inl:3-14)
+  kPrepSiluMul = 2,    // y = silu(gate) * up, gate/up = halves of a 2K row
+  kPrepAttnMerge = 3,  // y = merged split-K attention partials * sigmoid(gate)
+};
+
+struct PrepArgs {
+  int source = kPrepPlain;
+  const float *x = nullptr;      // [tokens][x_stride]
+  int x_stride = 0;
+  const float *weight = nullptr; // RMSNorm weight [K]
+  float eps = 1e-6F;
+  float weight_offset = 1.0F;
+  // attention merge inputs
+  const float *part_o = nullptr;   // [tokens][heads][splits][head_dim]
+  const float *part_ml = nullptr;  // [tokens][heads][splits][2] (max, sum)
+  const int32_t *seq_lens = nullptr;
+  const float *gates = nullptr;    // [tokens][heads][head_dim]
+  int heads = 0, head_dim = 0, max_splits = 0, split_tokens = 0;
+  // output
+  int tokens = 0, K = 0;
+  bool h128 = true;
+  uint64_t seed = 0;
+  uint64_t *codes = nullptr;       // A16 layout
+  ActParam *params = nullptr;
+  q35_q8_0_block_x4 *x4 = nullptr; // reference X4 layout (optional)
+  q35_q8_0_block_x1 *x1 = nullptr; // reference X1 layout (optional)
+  float *normed_out = nullptr;     // optional copy of y [tokens][K]
+  // optional: reset 64-bit argmax keys [count] (used before the head GEMM)
+  unsigned long long *argmax_reset = nullptr;
+  int argmax_reset_count = 0;
+};
+hipError_t launch_prep(const PrepArgs &a, hipStream_t stream);
+
+// Converts reference X4 blocks into the A16 layout (kernel-level matmul entry).
+hipError_t launch_x4_to_a16(const q35_q8_0_block_x4 *x4, int tokens, int nb, uint64_t *codes,
+                            ActParam *params, hipStream_t stream);
+hipError_t launch_x1_to_a16(const q35_q8_0_block_x1 *x1, int nb, uint64_t *codes,
+                            ActParam *params, hipStream_t stream);
+
+struct GemmArgs {
+  const q35_q4_0_block_x8 *w = nullptr;
+  int rows = 0, nb = 0;            // rows % 8 == 0
+  const uint64_t *codes = nullptr; // A16
+  const ActParam *params = nullptr;
+  int tokens = 0;                  // valid tokens (<= kMaxTokens)
+  float *out = nullptr;            // [tokens][stride]
+  int stride = 0;
+  const float *residual = nullptr; // optional, added in the epilogue, [tokens][stride]
+  int32_t *block_dots = nullptr;   // parity hook: [tokens][rows][nb]
+  bool exact = false;              // one wave per row group runs all blocks (ksplit must be 1)
+  // greedy head mode: fused penalty + argmax into 64-bit keys per token
+  unsigned long long *argmax_keys = nullptr;
+  const int32_t *counts = nullptr;  // [tokens][counts_stride]
+  const int32_t *count_rows = nullptr; // optional per-token row index into counts
+  long long counts_stride = 0;
+  const float *penalties = nullptr;
+  // split-K scratch (owned by the caller)
+  int ksplit = 1;
+  float *partials = nullptr;       // [ksplit][tokens][rows]
+  unsigned *counters = nullptr;    // [row_groups * token_groups], zero-initialised
+};
+int gemm_choose_ksplit(int rows, int nb, int cu_count);
+size_t gemm_partial_floats(int rows, int tokens, int ksplit);
+size_t gemm_counter_count(int rows, int tokens);
+hipError_t launch_gemm(const GemmArgs &a, hipStream_t stream);
+hipError_t launch_argmax_unpack(const unsigned long long *keys, int count, int32_t *index,
+                                float *value, hipStream_t stream);
+
+// DeltaNet
+struct DeltaArgs {
+  bool fused = true;          // fused linear-attention step (conv, norms, gates, gated norm)
+  float *const *states = nullptr;  // [batch] -> [v_heads][vd][kd]
+  float *state_base = nullptr;     // alternative: slot-strided base
+  const int32_t *slots = nullptr;  // [batch] slot of each row (with state_base)
+  long long state_slot_stride = 0; // floats between slots
+  int batch = 0, k_heads = 0, v_heads = 0, kd = 0, vd = 0;
+  // raw mode inputs
+  const float *q = nullptr, *k = nullptr, *v = nullptr, *alpha = nullptr, *beta = nullptr;
+  float *out = nullptr;            // raw: [batch][v_heads][vd]; fused: core [batch][v_heads*vd]
+  // fused mode inputs
+  const float *proj = nullptr;     // [batch][proj_stride] = [qkv | z | b | a]
+  int proj_stride = 0;
+  float *conv_base = nullptr;      // slot-strided conv state [(kernel-1)][channels]
+  long long conv_slot_stride = 0;
+  const int32_t *positions = nullptr;
+  const float *conv_w = nullptr;   // kernel-major [kernel][channels]
+  int kernel = 4;
+  const float *dt_bias = nullptr, *ssm_a = nullptr, *norm_w = nullptr;
+  float eps = 1e-6F;
+};
+hipError_t launch_delta(const DeltaArgs &a, hipStream_t stream);
+
+// Full attention
+struct AttnPrepArgs {
+  const float *proj = nullptr;  // [batch][proj_stride] = [q|gate interleaved per head | k | v]
+  int proj_stride = 0;
+  int batch = 0, heads = 0, kv_heads = 0, head_dim = 0, rope_dim = 0;
+  const float *q_norm = nullptr, *k_norm = nullptr;
+  float eps = 1e-6F;
+  const float *rope_cos = nullptr, *rope_sin = nullptr;  // [max_context][rope_dim/2]
+  const int32_t *positions = nullptr;
+  const int32_t *page_table = nullptr;  // [batch][max_pages]
+  int max_pages = 0, page_tokens = 0;
+  uint16_t *k_pool = nullptr, *v_pool = nullptr;  // this layer's pool base
+  float *q_out = nullptr, *gate_out = nullptr;    // [batch][heads][head_dim]
+};
+hipError_t launch_attn_prep(const AttnPrepArgs &a, hipStream_t stream);
+
+struct AttnArgs {
+  const float *q = nullptr;       // [batch][heads][head_dim]
+  const uint16_t *k_pool = nullptr, *v_pool = nullptr;
+  const int32_t *page_table = nullptr;
+  int max_pages = 0, page_tokens = 0;
+  const int32_t *seq_lens = nullptr;     // either seq_lens or positions(+1)
+  const int32_t *positions = nullptr;
+  int batch = 0, heads = 0, kv_heads = 0, head_dim = 0;
+  float scale = 0.0625F;
+  int split_tokens = 256, max_splits = 1;
+  float *part_o = nullptr;        // [batch][heads][max_splits][head_dim]
+  float *part_ml = nullptr;       // [batch][heads][max_splits][2]
+};
+hipError_t launch_attention(const AttnArgs &a, hipStream_t stream);
+// Stand-alone merge (+ gate) used by the kernel-level entry point.
+hipError_t launch_attention_merge(const AttnArgs &a, const float *gates, float *out,
+                                  hipStream_t stream);
+
+// Elementwise / small ops (kernel-level entries and the step)
+hipError_t launch_rms_norm(const float *x, const float *w, float *y, int rows, int width,
+                           float eps, float offset, hipStream_t stream);
+hipError_t launch_l2_normalize(float *x, int rows, int width, float eps, float scale,
+                               hipStream_t stream);
+hipError_t launch_conv1d_silu(float *state, int ring, const float *input, const float *w,
+                              float *out, int channels, int kernel, hipStream_t stream);
+hipError_t launch_silu_mul(const float *g, const float *u, float *out, long long n,
+                           hipStream_t stream);
+hipError_t launch_rope(float *x, int heads, int head_dim, int rope_dim, const float *c,
+                       const float *s, hipStream_t stream);
+hipError_t launch_store_f16(const float *x, uint16_t *y, long long n, hipStream_t stream);
+// Embedding gather of the tied identity-basis head (gguf_matrix.inl:21-26) plus
+// the penalty-count increment of the step's input tokens.
+hipError_t launch_embed(const q35_q4_0_block_x8 *embed, int nb, const int32_t *tokens,
+                        int batch, float *x, int hidden, int32_t *counts, long long counts_stride,
+                        const int32_t *slots, const uint8_t *count_input, hipStream_t stream);
+
+}  // namespace q35

@@ -1,0 +1,517 @@
+// Host runtime and C ABI (include/q35_hip.h): context, kernel-level entry
+// points, model upload, request slots, KV page pool and the decode step.
+#include "runtime.h"
+
+#include "q35_hip_api.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+namespace q35 {
+
+int set_error(Context *ctx, int status, const std::string &message) {
+  if (ctx != nullptr) ctx->error = message;
+  return status;
+}
+
+int hip_error(Context *ctx, hipError_t e, const char *what) {
+  return set_error(ctx, e == hipErrorOutOfMemory ? Q35_ERR_OOM : Q35_ERR_HIP,
+                   std::string(what) + ": " + hipGetErrorString(e));
+}
+
+namespace {
+
+// Grow-only scratch owned by a context for the kernel-level entry points.
+struct Scratch {
+  void *ptr = nullptr;
+  size_t bytes = 0;
+};
+std::map<const Context *, Scratch> g_scratch;
+
+int scratch_get(Context *ctx, size_t bytes, void **out) {
+  Scratch &s = g_scratch[ctx];
+  if (s.bytes < bytes) {
+    Q35_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    if (s.ptr != nullptr) Q35_HIP_TRY(ctx, hipFree(s.ptr));
+    s.ptr = nullptr;
+    s.bytes = 0;
+    Q35_HIP_TRY(ctx, hipMalloc(&s.ptr, bytes));
+    s.bytes = bytes;
+  }
+  *out = s.ptr;
+  return Q35_OK;
+}
+
+size_t align256(size_t n) { return (n + 255) & ~static_cast<size_t>(255); }
+
+int launch_status(Context *ctx, hipError_t e, const char *what) {
+  return e == hipSuccess ? Q35_OK : hip_error(ctx, e, what);
+}
+
+}  // namespace
+}  // namespace q35
+
+using namespace q35;
+
+// ====================================================================== context
+extern "C" int q35_context_create(int device, void *stream, q35_context **out) {
+  if (out == nullptr) return Q35_ERR_INVALID;
+  *out = nullptr;
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count <= device || device < 0)
+    return Q35_ERR_HIP;
+  auto *ctx = new (std::nothrow) q35_context();
+  if (ctx == nullptr) return Q35_ERR_OOM;
+  ctx->device = device;
+  if (hipSetDevice(device) != hipSuccess) {
+    delete ctx;
+    return Q35_ERR_HIP;
+  }
+  hipDeviceProp_t prop{};
+  if (hipGetDeviceProperties(&prop, device) == hipSuccess) {
+    ctx->cu_count = prop.multiProcessorCount;
+    ctx->arch = prop.gcnArchName;
+  }
+  if (stream != nullptr) {
+    ctx->stream = static_cast<hipStream_t>(stream);
+  } else {
+    if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
+      delete ctx;
+      return Q35_ERR_HIP;
+    }
+    ctx->own_stream = true;
+  }
+  if (hipEventCreate(&ctx->t0) != hipSuccess || hipEventCreate(&ctx->t1) != hipSuccess) {
+    if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return Q35_ERR_HIP;
+  }
+  *out = ctx;
+  return Q35_OK;
+}
+
+extern "C" void q35_context_destroy(q35_context *ctx) {
+  if (ctx == nullptr) return;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  auto it = g_scratch.find(ctx);
+  if (it != g_scratch.end()) {
+    if (it->second.ptr != nullptr) (void)hipFree(it->second.ptr);
+    g_scratch.erase(it);
+  }
+  (void)hipEventDestroy(ctx->t0);
+  (void)hipEventDestroy(ctx->t1);
+  if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+}
+
+extern "C" int q35_context_synchronize(q35_context *ctx) {
+  if (ctx == nullptr) return Q35_ERR_INVALID;
+  Q35_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  return Q35_OK;
+}
+
+extern "C" void *q35_context_stream(q35_context *ctx) { return ctx ? ctx->stream : nullptr; }
+
+extern "C" const char *q35_context_last_error(const q35_context *ctx) {
+  return ctx ? ctx->error.c_str() : "null context";
+}
+
+extern "C" const char *q35_status_string(int status) {
+  switch (status) {
+    case Q35_OK: return "ok";
+    case Q35_ERR_INVALID: return "invalid argument";
+    case Q35_ERR_HIP: return "HIP runtime error";
+    case Q35_ERR_OOM: return "out of memory";
+    case Q35_ERR_STATE: return "invalid state";
+    case Q35_ERR_UNSUPPORTED: return "unsupported shape";
+    case Q35_ERR_IO: return "I/O error";
+    default: return "unknown status";
+  }
+}
+
+extern "C" int q35_context_device_info(const q35_context *ctx, int *cu_count, char *arch,
+                                       size_t arch_size) {
+  if (ctx == nullptr) return Q35_ERR_INVALID;
+  if (cu_count) *cu_count = ctx->cu_count;
+  if (arch && arch_size) {
+    std::strncpy(arch, ctx->arch.c_str(), arch_size - 1);
+    arch[arch_size - 1] = 0;
+  }
+  return Q35_OK;
+}
+
+extern "C" int q35_device_alloc(q35_context *ctx, size_t bytes, void **out) {
+  if (ctx == nullptr || out == nullptr) return Q35_ERR_INVALID;
+  Q35_HIP_TRY(ctx, hipMalloc(out, bytes ? bytes : 1));
+  return Q35_OK;
+}
+extern "C" int q35_device_free(q35_context *ctx, void *ptr) {
+  if (ctx == nullptr) return Q35_ERR_INVALID;
+  Q35_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  Q35_HIP_TRY(ctx, hipFree(ptr));
+  return Q35_OK;
+}
+extern "C" int q35_memcpy_h2d(q35_context *ctx, void *dst, const void *src, size_t bytes) {
+  if (ctx == nullptr) return Q35_ERR_INVALID;
+  Q35_HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+  Q35_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  return Q35_OK;
+}
+extern "C" int q35_memcpy_d2h(q35_context *ctx, void *dst, const void *src, size_t bytes) {
+  if (ctx == nullptr) return Q35_ERR_INVALID;
+  Q35_HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+  Q35_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  return Q35_OK;
+}
+extern "C" int q35_memcpy_d2d(q35_context *ctx, void *dst, const void *src, size_t bytes) {
+  if (ctx == nullptr) return Q35_ERR_INVALID;
+  Q35_HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+  return Q35_OK;
+}
+extern "C" int q35_memset_device(q35_context *ctx, void *dst, int value, size_t bytes) {
+  if (ctx == nullptr) return Q35_ERR_INVALID;
+  Q35_HIP_TRY(ctx, hipMemsetAsync(dst, value, bytes, ctx->stream));
+  return Q35_OK;
+}
+extern "C" int q35_timer_begin(q35_context *ctx) {
+  if (ctx == nullptr) return Q35_ERR_INVALID;
+  Q35_HIP_TRY(ctx, hipEventRecord(ctx->t0, ctx->stream));
+  return Q35_OK;
+}
+extern "C" int q35_timer_end(q35_context *ctx, double *elapsed_ms) {
+  if (ctx == nullptr || elapsed_ms == nullptr) return Q35_ERR_INVALID;
+  Q35_HIP_TRY(ctx, hipEventRecord(ctx->t1, ctx->stream));
+  Q35_HIP_TRY(ctx, hipEventSynchronize(ctx->t1));
+  float ms = 0.0F;
+  Q35_HIP_TRY(ctx, hipEventElapsedTime(&ms, ctx->t0, ctx->t1));
+  *elapsed_ms = ms;
+  return Q35_OK;
+}
+
+// ======================================================= activation preparation
+static int prep_entry(q35_context *ctx, const float *input, q35_q8_0_block_x1 *x1,
+                      q35_q8_0_block_x4 *x4, size_t vectors, size_t columns, bool h128,
+                      uint64_t seed) {
+  if (ctx == nullptr || input == nullptr || (x1 == nullptr && x4 == nullptr))
+    return Q35_ERR_INVALID;
+  if (columns == 0 || columns % (h128 ? 128 : 32) != 0 || vectors == 0 || vectors > (1u << 20))
+    return set_error(ctx, Q35_ERR_INVALID, "invalid activation geometry");
+  if (!h128 && columns % 128 != 0)
+    return set_error(ctx, Q35_ERR_UNSUPPORTED, "identity preparation needs columns % 128 == 0");
+  PrepArgs a;
+  a.source = kPrepPlain;
+  a.x = input;
+  a.x_stride = static_cast<int>(columns);
+  a.tokens = static_cast<int>(vectors);
+  a.K = static_cast<int>(columns);
+  a.h128 = h128;
+  a.seed = seed;
+  a.x1 = x1;
+  a.x4 = x4;
+  return launch_status(ctx, launch_prep(a, ctx->stream), "prep kernel");
+}
+
+extern "C" int q35_q8_0_quantize_vector_1(q35_context *ctx, const float *input,
+                                          q35_q8_0_block_x1 *output, size_t blocks) {
+  return prep_entry(ctx, input, output, nullptr, 1, blocks * 32, false, 0);
+}
+extern "C" int q35_q8_0_quantize_vectors_4(q35_context *ctx, const float *input,
+                                           q35_q8_0_block_x4 *output, size_t vectors,
+                                           size_t blocks) {
+  if (vectors % 4 != 0) return set_error(ctx, Q35_ERR_INVALID, "vector_count % 4 != 0");
+  return prep_entry(ctx, input, nullptr, output, vectors, blocks * 32, false, 0);
+}
+extern "C" int q35_q4_h128_prepare_activation_1(q35_context *ctx, const float *input,
+                                                q35_q8_0_block_x1 *output, size_t columns,
+                                                uint64_t seed) {
+  return prep_entry(ctx, input, output, nullptr, 1, columns, true, seed);
+}
+extern "C" int q35_q4_h128_prepare_activations_4(q35_context *ctx, const float *input,
+                                                 q35_q8_0_block_x4 *output, size_t vectors,
+                                                 size_t columns, uint64_t seed) {
+  if (vectors % 4 != 0) return set_error(ctx, Q35_ERR_INVALID, "vector_count % 4 != 0");
+  return prep_entry(ctx, input, nullptr, output, vectors, columns, true, seed);
+}
+
+// ================================================================ DOT4 GEMM
+namespace {
+// Runs the GEMM over `vectors` tokens (chunks of kMaxTokens) from X4 or X1
+// activations. `exact` forces the single-wave fma chain per row.
+int matmul_entry(q35_context *ctx, const q35_q4_0_block_x8 *m, const q35_q8_0_block_x4 *x4,
+                 const q35_q8_0_block_x1 *x1, float *out, int32_t *dots, size_t rows,
+                 size_t vectors, size_t blocks, size_t stride, bool exact,
+                 unsigned long long *keys, const int32_t *counts, const float *penalties) {
+  if (ctx == nullptr || m == nullptr || (x4 == nullptr && x1 == nullptr) ||
+      (out == nullptr && dots == nullptr && keys == nullptr))
+    return Q35_ERR_INVALID;
+  // split-K partial sums need an FP32 destination
+  if (out == nullptr && !exact && keys == nullptr && dots == nullptr) return Q35_ERR_INVALID;
+  if (rows == 0 || rows % 8 != 0 || blocks == 0 || vectors == 0 || rows > (1u << 28) ||
+      blocks > (1u << 16) || (out != nullptr && stride < rows))
+    return set_error(ctx, Q35_ERR_INVALID, "invalid DOT4 geometry");
+  const int nb = static_cast<int>(blocks);
+  const size_t chunk = kMaxTokens;
+  const size_t code_bytes = align256(4 * 64 * static_cast<size_t>(nb) * sizeof(uint64_t));
+  const size_t param_bytes = align256(4 * 16 * static_cast<size_t>(nb) * sizeof(ActParam));
+  const int ksplit = (exact || dots != nullptr || keys != nullptr)
+                         ? 1
+                         : gemm_choose_ksplit(static_cast<int>(rows), nb, ctx->cu_count);
+  const size_t part_bytes = align256(gemm_partial_floats(static_cast<int>(rows), kMaxTokens, ksplit) * 4);
+  const size_t cnt_bytes = align256(gemm_counter_count(static_cast<int>(rows), kMaxTokens) * 4);
+  void *scratch = nullptr;
+  int st = scratch_get(ctx, code_bytes + param_bytes + part_bytes + cnt_bytes, &scratch);
+  if (st != Q35_OK) return st;
+  auto *codes = reinterpret_cast<uint64_t *>(scratch);
+  auto *params = reinterpret_cast<ActParam *>(static_cast<char *>(scratch) + code_bytes);
+  auto *partials = reinterpret_cast<float *>(static_cast<char *>(scratch) + code_bytes + param_bytes);
+  auto *counters =
+      reinterpret_cast<unsigned *>(static_cast<char *>(scratch) + code_bytes + param_bytes + part_bytes);
+  if (ksplit > 1) Q35_HIP_TRY(ctx, hipMemsetAsync(counters, 0, cnt_bytes, ctx->stream));
+  for (size_t t0 = 0; t0 < vectors; t0 += chunk) {
+    const size_t n = std::min(chunk, vectors - t0);
+    hipError_t e;
+    if (x4 != nullptr)
+      e = launch_x4_to_a16(x4 + (t0 / 4) * blocks, static_cast<int>(n), nb, codes, params, ctx->stream);
+    else
+      e = launch_x1_to_a16(x1 + t0 * blocks, nb, codes, params, ctx->stream);
+    if (e != hipSuccess) return hip_error(ctx, e, "activation layout kernel");
+    GemmArgs g;
+    g.w = m;
+    g.rows = static_cast<int>(rows);
+    g.nb = nb;
+    g.codes = codes;
+    g.params = params;
+    g.tokens = static_cast<int>(n);
+    g.out = out ? out + t0 * stride : nullptr;
+    g.stride = static_cast<int>(stride);
+    g.block_dots = dots ? dots + t0 * rows * blocks : nullptr;
+    g.exact = exact;
+    g.argmax_keys = keys ? keys + t0 : nullptr;
+    g.counts = counts ? counts + t0 * rows : nullptr;
+    g.counts_stride = static_cast<long long>(rows);
+    g.penalties = penalties ? penalties + t0 : nullptr;
+    g.ksplit = ksplit;
+    g.partials = partials;
+    g.counters = counters;
+    e = launch_gemm(g, ctx->stream);
+    if (e != hipSuccess) return hip_error(ctx, e, "DOT4 GEMM kernel");
+  }
+  return Q35_OK;
+}
+}  // namespace
+
+extern "C" int q35_q4_dot4_matvec(q35_context *ctx, const q35_q4_0_block_x8 *matrix,
+                                  const q35_q8_0_block_x1 *vector, float *output, size_t rows,
+                                  size_t blocks) {
+  return matmul_entry(ctx, matrix, nullptr, vector, output, nullptr, rows, 1, blocks, rows, false,
+                      nullptr, nullptr, nullptr);
+}
+extern "C" int q35_q4_dot4_matmul(q35_context *ctx, const q35_q4_0_block_x8 *matrix,
+                                  const q35_q8_0_block_x4 *vectors, float *output, size_t rows,
+                                  size_t count, size_t blocks, size_t stride) {
+  if (count % 4 != 0) return set_error(ctx, Q35_ERR_INVALID, "vector_count % 4 != 0");
+  return matmul_entry(ctx, matrix, vectors, nullptr, output, nullptr, rows, count, blocks, stride,
+                      false, nullptr, nullptr, nullptr);
+}
+// Bit-exact FP32 variant (no public declaration in the reference; used by the parity tests).
+extern "C" int q35_q4_dot4_matmul_exact(q35_context *ctx, const q35_q4_0_block_x8 *matrix,
+                                        const q35_q8_0_block_x4 *vectors, float *output,
+                                        size_t rows, size_t count, size_t blocks, size_t stride) {
+  if (count % 4 != 0) return set_error(ctx, Q35_ERR_INVALID, "vector_count % 4 != 0");
+  return matmul_entry(ctx, matrix, vectors, nullptr, output, nullptr, rows, count, blocks, stride,
+                      true, nullptr, nullptr, nullptr);
+}
+extern "C" int q35_q4_dot4_block_dots(q35_context *ctx, const q35_q4_0_block_x8 *matrix,
+                                      const q35_q8_0_block_x4 *vectors, int32_t *output,
+                                      size_t rows, size_t count, size_t blocks) {
+  if (count % 4 != 0) return set_error(ctx, Q35_ERR_INVALID, "vector_count % 4 != 0");
+  return matmul_entry(ctx, matrix, vectors, nullptr, nullptr, output, rows, count, blocks, rows,
+                      true, nullptr, nullptr, nullptr);
+}
+extern "C" int q35_q4_dot4_argmax_batch(q35_context *ctx, const q35_q4_0_block_x8 *matrix,
+                                        const q35_q8_0_block_x4 *vectors, const int32_t *counts,
+                                        const float *penalties, size_t rows, size_t count,
+                                        size_t blocks, int32_t *out_index, float *out_value) {
+  if (ctx == nullptr || out_index == nullptr) return Q35_ERR_INVALID;
+  if (count % 4 != 0 || count == 0) return set_error(ctx, Q35_ERR_INVALID, "vector_count % 4 != 0");
+  unsigned long long *keys = nullptr;
+  Q35_HIP_TRY(ctx, hipMallocAsync(reinterpret_cast<void **>(&keys), count * 8, ctx->stream));
+  Q35_HIP_TRY(ctx, hipMemsetAsync(keys, 0, count * 8, ctx->stream));
+  int st = matmul_entry(ctx, matrix, vectors, nullptr, nullptr, nullptr, rows, count, blocks, rows,
+                        false, keys, counts, penalties);
+  if (st == Q35_OK) {
+    hipError_t e = launch_argmax_unpack(keys, static_cast<int>(count), out_index, out_value, ctx->stream);
+    if (e != hipSuccess) st = hip_error(ctx, e, "argmax unpack");
+  }
+  (void)hipFreeAsync(keys, ctx->stream);
+  return st;
+}
+
+// ================================================================= DeltaNet
+namespace q35 {
+namespace {
+__global__ void delta_rows_kernel(float *state, const float *q, const float *k, const float *v,
+                                  const float *alpha, const float *beta, float *out, int kd, int vd,
+                                  long long row_begin) {
+  const long long row = row_begin + blockIdx.x;
+  const int head = static_cast<int>(row / vd), vrow = static_cast<int>(row % vd);
+  const int lane = threadIdx.x;
+  float *s = state + row * kd;
+  const float *kh = k + static_cast<size_t>(head) * kd, *qh = q + static_cast<size_t>(head) * kd;
+  const float al = alpha[head];
+  float sk = 0.0F;
+  for (int c = lane; c < kd; c += 64) {
+    const float dec = s[c] * al;
+    s[c] = dec;
+    sk += dec * kh[c];
+  }
+  for (int m = 32; m >= 1; m >>= 1) sk += __shfl_xor(sk, m, 64);
+  const float delta = (v[static_cast<size_t>(head) * vd + vrow] - sk) * beta[head];
+  float sq = 0.0F;
+  for (int c = lane; c < kd; c += 64) {
+    const float up = s[c] + delta * kh[c];
+    s[c] = up;
+    sq += up * qh[c];
+  }
+  for (int m = 32; m >= 1; m >>= 1) sq += __shfl_xor(sq, m, 64);
+  if (lane == 0) out[static_cast<size_t>(head) * vd + vrow] = sq;
+}
+}  // namespace
+}  // namespace q35
+
+extern "C" int q35_gated_delta_net_update_rows(q35_context *ctx, float *state, const float *q,
+                                               const float *k, const float *v, const float *alpha,
+                                               const float *beta, float *output, size_t heads,
+                                               size_t kd, size_t vd, size_t row_begin,
+                                               size_t row_end) {
+  if (ctx == nullptr) return Q35_ERR_INVALID;
+  const size_t total = heads * vd;
+  // delta_net.cpp:193-200: empty or out-of-range row spans are a no-op
+  if (row_begin >= row_end || row_begin >= total) return Q35_OK;
+  const size_t end = std::min(row_end, total);
+  Q35_LAUNCH((q35::delta_rows_kernel), static_cast<unsigned>(end - row_begin), 64, 0, ctx->stream, 
+      state, q, k, v, alpha, beta, output, static_cast<int>(kd), static_cast<int>(vd),
+      static_cast<long long>(row_begin));
+  return launch_status(ctx, hipGetLastError(), "delta rows kernel");
+}
+
+extern "C" int q35_gated_delta_net_update_batch(q35_context *ctx, float *const *states,
+                                                const float *q, const float *k, const float *v,
+                                                const float *alpha, const float *beta,
+                                                float *output, size_t batch, size_t heads,
+                                                size_t kd, size_t vd) {
+  if (ctx == nullptr || states == nullptr) return Q35_ERR_INVALID;
+  if (kd != 128 || vd != 128) return set_error(ctx, Q35_ERR_UNSUPPORTED, "DeltaNet tile needs d_k = d_v = 128");
+  DeltaArgs a;
+  a.fused = false;
+  a.states = states;
+  a.batch = static_cast<int>(batch);
+  a.k_heads = static_cast<int>(heads);
+  a.v_heads = static_cast<int>(heads);
+  a.kd = 128;
+  a.vd = 128;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.alpha = alpha;
+  a.beta = beta;
+  a.out = output;
+  return launch_status(ctx, launch_delta(a, ctx->stream), "DeltaNet kernel");
+}
+
+// ================================================================ attention
+extern "C" int q35_attention_decode_paged(q35_context *ctx, const float *q, const float *gates,
+                                          const uint16_t *k_pool, const uint16_t *v_pool,
+                                          const int32_t *page_table, size_t max_pages,
+                                          const int32_t *seq_lens, size_t page_tokens,
+                                          float *output, size_t batch, int heads, int kv_heads,
+                                          int head_dim, float scale) {
+  if (ctx == nullptr || q == nullptr || gates == nullptr || output == nullptr) return Q35_ERR_INVALID;
+  if (head_dim != 256 || kv_heads <= 0 || heads % kv_heads != 0 || batch == 0 || page_tokens == 0)
+    return set_error(ctx, Q35_ERR_UNSUPPORTED, "attention needs head_dim 256 and heads % kv_heads == 0");
+  std::vector<int32_t> lens(batch);
+  Q35_HIP_TRY(ctx, hipMemcpyAsync(lens.data(), seq_lens, batch * 4, hipMemcpyDeviceToHost, ctx->stream));
+  Q35_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  int max_len = 1;
+  for (auto l : lens) {
+    if (l <= 0 || static_cast<size_t>(l) > max_pages * page_tokens)
+      return set_error(ctx, Q35_ERR_INVALID, "sequence length outside the page table");
+    max_len = std::max(max_len, l);
+  }
+  AttnArgs a;
+  a.q = q;
+  a.k_pool = k_pool;
+  a.v_pool = v_pool;
+  a.page_table = page_table;
+  a.max_pages = static_cast<int>(max_pages);
+  a.page_tokens = static_cast<int>(page_tokens);
+  a.seq_lens = seq_lens;
+  a.batch = static_cast<int>(batch);
+  a.heads = heads;
+  a.kv_heads = kv_heads;
+  a.head_dim = head_dim;
+  a.scale = scale;
+  a.split_tokens = 256;
+  a.max_splits = (max_len + 255) / 256;
+  const size_t parts = batch * static_cast<size_t>(heads) * a.max_splits;
+  void *scratch = nullptr;
+  int st = scratch_get(ctx, align256(parts * 256 * 4) + align256(parts * 2 * 4), &scratch);
+  if (st != Q35_OK) return st;
+  a.part_o = static_cast<float *>(scratch);
+  a.part_ml = reinterpret_cast<float *>(static_cast<char *>(scratch) + align256(parts * 256 * 4));
+  hipError_t e = launch_attention(a, ctx->stream);
+  if (e != hipSuccess) return hip_error(ctx, e, "attention kernel");
+  return launch_status(ctx, launch_attention_merge(a, gates, output, ctx->stream), "attention merge");
+}
+
+extern "C" int q35_attention_cache_store_f16(q35_context *ctx, const float *input, uint16_t *output,
+                                             size_t count) {
+  if (ctx == nullptr) return Q35_ERR_INVALID;
+  return launch_status(ctx, launch_store_f16(input, output, static_cast<long long>(count), ctx->stream),
+                       "store f16");
+}
+
+// ============================================================ activation ops
+extern "C" int q35_rms_norm_f32(q35_context *ctx, const float *input, const float *weight,
+                                float *output, size_t rows, size_t width, float eps, float offset) {
+  if (ctx == nullptr) return Q35_ERR_INVALID;
+  return launch_status(ctx, launch_rms_norm(input, weight, output, static_cast<int>(rows),
+                                            static_cast<int>(width), eps, offset, ctx->stream),
+                       "rms norm");
+}
+extern "C" int q35_l2_normalize_f32(q35_context *ctx, float *values, size_t rows, size_t width,
+                                    float eps, float scale) {
+  if (ctx == nullptr) return Q35_ERR_INVALID;
+  return launch_status(ctx, launch_l2_normalize(values, static_cast<int>(rows), static_cast<int>(width),
+                                                eps, scale, ctx->stream),
+                       "l2 normalize");
+}
+extern "C" int q35_causal_conv1d_silu_f32(q35_context *ctx, float *state, size_t ring,
+                                          const float *input, const float *w, float *output,
+                                          size_t channels, size_t kernel) {
+  if (ctx == nullptr || kernel < 2) return Q35_ERR_INVALID;
+  return launch_status(ctx, launch_conv1d_silu(state, static_cast<int>(ring), input, w, output,
+                                               static_cast<int>(channels), static_cast<int>(kernel),
+                                               ctx->stream),
+                       "conv1d");
+}
+extern "C" int q35_silu_mul_f32(q35_context *ctx, const float *gate, const float *up, float *output,
+                                size_t count) {
+  if (ctx == nullptr) return Q35_ERR_INVALID;
+  return launch_status(ctx, launch_silu_mul(gate, up, output, static_cast<long long>(count), ctx->stream),
+                       "silu mul");
+}
+extern "C" int q35_rope_f32(q35_context *ctx, float *values, size_t heads, size_t head_dim,
+                            size_t rope_dim, const float *cosine, const float *sine) {
+  if (ctx == nullptr) return Q35_ERR_INVALID;
+  // activation.cpp:131-133: invalid rotary width is a no-op
+  if (rope_dim == 0 || rope_dim > head_dim || (rope_dim & 1u) != 0 || rope_dim > 512) return Q35_OK;
+  return launch_status(ctx, launch_rope(values, static_cast<int>(heads), static_cast<int>(head_dim),
+                                        static_cast<int>(rope_dim), cosine, sine, ctx->stream),
+                       "rope");
+}

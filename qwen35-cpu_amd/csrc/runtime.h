@@ -1,0 +1,84 @@
+// Host-side objects behind the C ABI: model weights in HBM, per-request
+// device state, the paged KV pool and the captured decode step.
+#pragma once
+
+#include <map>
+#include <set>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "q35_internal.h"
+
+struct q35_context : q35::Context {};
+
+namespace q35 {
+
+struct LayerDev {
+  bool linear = false;
+  const q35_q4_0_block_x8 *in_proj = nullptr, *out_proj = nullptr, *gate_up = nullptr,
+                          *down = nullptr;
+  int in_rows = 0, out_cols = 0;
+  const float *input_norm = nullptr, *post_norm = nullptr;
+  const float *conv_w = nullptr, *lin_norm = nullptr, *dt_bias = nullptr, *ssm_a = nullptr;
+  const float *q_norm = nullptr, *k_norm = nullptr;
+};
+
+}  // namespace q35
+
+struct q35_model {
+  q35::Context *ctx = nullptr;
+  q35_model_dims d{};
+  std::vector<uint8_t> is_linear;
+  const q35_q4_0_block_x8 *embed = nullptr;
+  const float *final_norm = nullptr;
+  std::vector<q35::LayerDev> layers;
+  std::vector<void *> allocations;
+  std::set<std::string> uploaded;
+  std::set<std::string> required;
+  bool finalized = false;
+  size_t weight_bytes = 0;  // packed projection + head bytes in HBM
+  int n_linear = 0, n_full = 0;
+  std::vector<int> linear_index, full_index;  // per layer
+};
+
+struct q35_runtime {
+  q35_model *model = nullptr;
+  q35::Context *ctx = nullptr;
+  q35_runtime_config cfg{};
+  int max_pages_per_row = 0;
+  int split_tokens = 256, max_splits = 1;
+  // slot state
+  float *recurrent = nullptr;  // [slots][n_lin][vh][vd][kd]
+  float *conv = nullptr;       // [slots][n_lin][kernel-1][channels]
+  int32_t *counts = nullptr;   // [slots][vocab]
+  long long rec_slot_stride = 0, conv_slot_stride = 0;
+  std::vector<uint8_t> slot_used;
+  // KV pool [n_full][pages][page_tokens][kvh][hd]
+  uint16_t *k_pool = nullptr, *v_pool = nullptr;
+  size_t layer_pool_elems = 0;
+  std::vector<int> page_ref;
+  std::vector<int> free_pages;
+  float *rope_cos = nullptr, *rope_sin = nullptr;
+  // work buffers
+  float *x = nullptr, *proj = nullptr, *core = nullptr, *q_rot = nullptr, *gates = nullptr;
+  float *part_o = nullptr, *part_ml = nullptr, *partials = nullptr, *logits = nullptr;
+  float *hidden_out = nullptr;
+  uint64_t *codes = nullptr;
+  q35::ActParam *params = nullptr;
+  unsigned *counters = nullptr;
+  unsigned long long *argmax_keys = nullptr;
+  int32_t *tokens_out_dev = nullptr;
+  // step metadata (pinned host + device copy)
+  size_t meta_bytes = 0;
+  unsigned char *meta_host = nullptr, *meta_dev = nullptr;
+  int32_t *tokens_out_host = nullptr;
+  size_t proj_width = 0, core_width = 0;
+  std::map<std::pair<int, int>, hipGraphExec_t> graphs;
+  int last_batch = 0;
+  std::vector<void *> allocations;
+};
+
+namespace q35 {
+int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits);
+}

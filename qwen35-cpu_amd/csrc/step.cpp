@@ -1,0 +1,786 @@
+// Model upload, request slots, KV page pool and the batched decode step
+// (the MI355X body of CpuEngine::Impl::forward_batch, cpu_engine.inl:201-325).
+#include "runtime.h"
+
+#include "q35_hip_api.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+using namespace q35;
+
+namespace {
+
+size_t align256(size_t n) { return (n + 255) & ~static_cast<size_t>(255); }
+
+std::string layer_prefix(int i) {
+  return "model.language_model.layers." + std::to_string(i) + ".";
+}
+
+int model_alloc(q35_model *m, size_t bytes, void **out) {
+  Q35_HIP_TRY(m->ctx, hipMalloc(out, bytes ? bytes : 1));
+  m->allocations.push_back(*out);
+  return Q35_OK;
+}
+
+int rt_alloc(q35_runtime *rt, size_t bytes, void **out) {
+  Q35_HIP_TRY(rt->ctx, hipMalloc(out, bytes ? bytes : 1));
+  rt->allocations.push_back(*out);
+  return Q35_OK;
+}
+
+}  // namespace
+
+// ===================================================================== model
+extern "C" int q35_model_dims_preset(int which, q35_model_dims *d, uint8_t *is_linear,
+                                     size_t capacity) {
+  if (d == nullptr) return Q35_ERR_INVALID;
+  // text_architecture, src/compiler/profile_loader.cpp:439-462; RuntimeDims
+  // defaults (weights.inl:336-357, profile_loader.cpp:366-378)
+  q35_model_dims x{};
+  x.vocab = 248320;
+  x.head_dim = 256;
+  x.rope_theta = 10000000.0F;
+  x.rms_eps = 1.0e-6F;
+  x.lin_kernel = 4;
+  x.lin_k_heads = 16;
+  x.lin_k_dim = 128;
+  x.lin_v_dim = 128;
+  x.sign_seed = 0x5148333548313238ull;  // q4_h128.h:25-26
+  if (which == 0) {
+    x.n_layers = 24; x.hidden = 1024; x.intermediate = 3584;
+    x.n_heads = 8; x.n_kv_heads = 2; x.lin_v_heads = 16;
+  } else if (which == 1) {
+    x.n_layers = 24; x.hidden = 2048; x.intermediate = 6144;
+    x.n_heads = 8; x.n_kv_heads = 2; x.lin_v_heads = 16;
+  } else if (which == 2) {
+    x.n_layers = 32; x.hidden = 2560; x.intermediate = 9216;
+    x.n_heads = 16; x.n_kv_heads = 4; x.lin_v_heads = 32;
+  } else {
+    return Q35_ERR_INVALID;
+  }
+  // partial_rotary_factor 0.25 (weights.inl:1580-1583)
+  x.rope_dim = static_cast<int32_t>(static_cast<float>(x.head_dim) * 0.25F);
+  if (x.rope_dim % 2) x.rope_dim -= 1;
+  *d = x;
+  if (is_linear != nullptr) {
+    if (capacity < static_cast<size_t>(x.n_layers)) return Q35_ERR_INVALID;
+    for (int i = 0; i < x.n_layers; ++i) is_linear[i] = ((i + 1) % 4 != 0) ? 1 : 0;
+  }
+  return Q35_OK;
+}
+
+extern "C" int q35_model_create(q35_context *ctx, const q35_model_dims *dims,
+                                const uint8_t *layer_is_linear, q35_model **out) {
+  if (ctx == nullptr || dims == nullptr || layer_is_linear == nullptr || out == nullptr)
+    return Q35_ERR_INVALID;
+  *out = nullptr;
+  const q35_model_dims &d = *dims;
+  if (d.n_layers <= 0 || d.hidden <= 0 || d.hidden % 128 || d.intermediate % 128 ||
+      d.vocab <= 0 || d.vocab % 8 || d.n_heads <= 0 || d.n_kv_heads <= 0 ||
+      d.n_heads % d.n_kv_heads || d.head_dim != 256 || d.lin_k_dim != 128 || d.lin_v_dim != 128 ||
+      d.lin_v_heads % d.lin_k_heads || d.lin_kernel < 2 || d.rope_dim <= 0 || d.rope_dim > d.head_dim ||
+      (d.lin_v_heads * d.lin_v_dim) % 128 || (d.n_heads * d.head_dim) % 128)
+    return set_error(ctx, Q35_ERR_UNSUPPORTED, "model shape outside the kernels' support");
+  auto *m = new (std::nothrow) q35_model();
+  if (m == nullptr) return Q35_ERR_OOM;
+  m->ctx = ctx;
+  m->d = d;
+  m->is_linear.assign(layer_is_linear, layer_is_linear + d.n_layers);
+  m->layers.resize(d.n_layers);
+  m->linear_index.assign(d.n_layers, -1);
+  m->full_index.assign(d.n_layers, -1);
+  m->required = {"model.language_model.embed_tokens.weight", "model.language_model.norm.weight"};
+  for (int i = 0; i < d.n_layers; ++i) {
+    const std::string p = layer_prefix(i);
+    m->layers[i].linear = m->is_linear[i] != 0;
+    for (const char *n : {"input_layernorm.weight", "post_attention_layernorm.weight",
+                          "mlp.gate_up_proj.weight", "mlp.down_proj.weight"})
+      m->required.insert(p + n);
+    if (m->layers[i].linear) {
+      m->linear_index[i] = m->n_linear++;
+      for (const char *n : {"linear_attn.in_proj_all.weight", "linear_attn.conv1d.weight",
+                            "linear_attn.out_proj.weight", "linear_attn.norm.weight",
+                            "linear_attn.A_log", "linear_attn.dt_bias"})
+        m->required.insert(p + n);
+    } else {
+      m->full_index[i] = m->n_full++;
+      for (const char *n : {"self_attn.qkv_proj.weight", "self_attn.o_proj.weight",
+                            "self_attn.q_norm.weight", "self_attn.k_norm.weight"})
+        m->required.insert(p + n);
+    }
+  }
+  *out = m;
+  return Q35_OK;
+}
+
+extern "C" void q35_model_destroy(q35_model *m) {
+  if (m == nullptr) return;
+  (void)hipSetDevice(m->ctx->device);
+  (void)hipStreamSynchronize(m->ctx->stream);
+  for (void *p : m->allocations) (void)hipFree(p);
+  delete m;
+}
+
+namespace {
+
+int expect_shape(q35_model *m, const std::string &name, const uint64_t *shape, size_t rank,
+                 std::initializer_list<uint64_t> want) {
+  bool ok = rank == want.size();
+  size_t i = 0;
+  for (uint64_t w : want) {
+    if (!ok) break;
+    ok = shape[i++] == w;
+  }
+  return ok ? Q35_OK : set_error(m->ctx, Q35_ERR_INVALID, "wrong shape for " + name);
+}
+
+// Uploads `bytes` to a fresh device buffer; returns its address in *dst.
+int upload(q35_model *m, const void *host, size_t bytes, const void **dst) {
+  void *p = nullptr;
+  int st = model_alloc(m, bytes, &p);
+  if (st != Q35_OK) return st;
+  Q35_HIP_TRY(m->ctx, hipMemcpy(p, host, bytes, hipMemcpyHostToDevice));
+  *dst = p;
+  return Q35_OK;
+}
+
+}  // namespace
+
+extern "C" int q35_model_upload_tensor(q35_model *m, const char *name_c, int encoding,
+                                       const uint64_t *shape, size_t rank, const void *bytes,
+                                       size_t count) {
+  if (m == nullptr || name_c == nullptr || shape == nullptr || bytes == nullptr) return Q35_ERR_INVALID;
+  const std::string name(name_c);
+  const q35_model_dims &d = m->d;
+  const uint64_t H = d.hidden, I = d.intermediate;
+  const uint64_t q_dim = static_cast<uint64_t>(d.lin_k_heads) * d.lin_k_dim;
+  const uint64_t v_dim = static_cast<uint64_t>(d.lin_v_heads) * d.lin_v_dim;
+  const uint64_t ch = 2 * q_dim + v_dim;
+  const uint64_t hd = d.head_dim;
+  auto q4 = [&](std::initializer_list<uint64_t> want, int enc, const q35_q4_0_block_x8 **dst,
+                size_t *weight_bytes) -> int {
+    int st = expect_shape(m, name, shape, rank, want);
+    if (st != Q35_OK) return st;
+    if (encoding != enc) return set_error(m->ctx, Q35_ERR_INVALID, "wrong encoding for " + name);
+    const uint64_t rows = shape[0], cols = shape[1];
+    if (rows % 8 || cols % 32 || count != rows / 8 * (cols / 32) * 144)
+      return set_error(m->ctx, Q35_ERR_INVALID, "wrong DOT4 payload size for " + name);
+    *weight_bytes += count;
+    return upload(m, bytes, count, reinterpret_cast<const void **>(dst));
+  };
+  auto f32 = [&](std::initializer_list<uint64_t> want, const float **dst) -> int {
+    int st = expect_shape(m, name, shape, rank, want);
+    if (st != Q35_OK) return st;
+    uint64_t n = 1;
+    for (uint64_t w : want) n *= w;
+    if (encoding != Q35_ENC_F32 || count != n * 4)
+      return set_error(m->ctx, Q35_ERR_INVALID, "wrong F32 payload for " + name);
+    return upload(m, bytes, count, reinterpret_cast<const void **>(dst));
+  };
+  int st = Q35_ERR_INVALID;
+  if (name == "model.language_model.embed_tokens.weight") {
+    st = q4({static_cast<uint64_t>(d.vocab), H}, Q35_ENC_Q4_0_DOT4, &m->embed, &m->weight_bytes);
+  } else if (name == "model.language_model.norm.weight") {
+    st = f32({H}, &m->final_norm);
+  } else if (name.rfind("model.language_model.layers.", 0) == 0) {
+    const size_t p0 = std::strlen("model.language_model.layers.");
+    const size_t dot = name.find('.', p0);
+    if (dot == std::string::npos) return set_error(m->ctx, Q35_ERR_INVALID, "bad tensor name " + name);
+    const int li = std::atoi(name.substr(p0, dot - p0).c_str());
+    if (li < 0 || li >= d.n_layers) return set_error(m->ctx, Q35_ERR_INVALID, "bad layer in " + name);
+    const std::string leaf = name.substr(dot + 1);
+    LayerDev &L = m->layers[li];
+    if (leaf == "input_layernorm.weight") st = f32({H}, &L.input_norm);
+    else if (leaf == "post_attention_layernorm.weight") st = f32({H}, &L.post_norm);
+    else if (leaf == "mlp.gate_up_proj.weight") st = q4({2 * I, H}, Q35_ENC_Q4_H128_DOT4, &L.gate_up, &m->weight_bytes);
+    else if (leaf == "mlp.down_proj.weight") st = q4({H, I}, Q35_ENC_Q4_H128_DOT4, &L.down, &m->weight_bytes);
+    else if (L.linear && leaf == "linear_attn.in_proj_all.weight") {
+      st = q4({ch + v_dim + 2 * static_cast<uint64_t>(d.lin_v_heads), H}, Q35_ENC_Q4_H128_DOT4,
+              &L.in_proj, &m->weight_bytes);
+      L.in_rows = static_cast<int>(shape[0]);
+    } else if (L.linear && leaf == "linear_attn.out_proj.weight") {
+      st = q4({H, v_dim}, Q35_ENC_Q4_H128_DOT4, &L.out_proj, &m->weight_bytes);
+      L.out_cols = static_cast<int>(v_dim);
+    } else if (L.linear && leaf == "linear_attn.conv1d.weight") {
+      st = expect_shape(m, name, shape, rank, {ch, 1, static_cast<uint64_t>(d.lin_kernel)});
+      if (st == Q35_OK && (encoding != Q35_ENC_F32 || count != ch * d.lin_kernel * 4))
+        st = set_error(m->ctx, Q35_ERR_INVALID, "wrong F32 payload for " + name);
+      if (st == Q35_OK) {
+        // pack_conv1d_kernel_major (weights.inl:532-544): [channel][kernel] -> [kernel][channel]
+        const float *src = static_cast<const float *>(bytes);
+        std::vector<float> km(ch * d.lin_kernel);
+        for (int k = 0; k < d.lin_kernel; ++k)
+          for (uint64_t c = 0; c < ch; ++c) km[k * ch + c] = src[c * d.lin_kernel + k];
+        st = upload(m, km.data(), km.size() * 4, reinterpret_cast<const void **>(&L.conv_w));
+      }
+    } else if (L.linear && leaf == "linear_attn.norm.weight") st = f32({static_cast<uint64_t>(d.lin_v_dim)}, &L.lin_norm);
+    else if (L.linear && leaf == "linear_attn.dt_bias") st = f32({static_cast<uint64_t>(d.lin_v_heads)}, &L.dt_bias);
+    else if (L.linear && leaf == "linear_attn.A_log") {
+      st = expect_shape(m, name, shape, rank, {static_cast<uint64_t>(d.lin_v_heads)});
+      if (st == Q35_OK && (encoding != Q35_ENC_F32 || count != static_cast<size_t>(d.lin_v_heads) * 4))
+        st = set_error(m->ctx, Q35_ERR_INVALID, "wrong F32 payload for " + name);
+      if (st == Q35_OK) {
+        // ssm_a = -exp(A_log) in FP32 (weights.inl:1750-1754)
+        const float *src = static_cast<const float *>(bytes);
+        std::vector<float> a(d.lin_v_heads);
+        for (int h = 0; h < d.lin_v_heads; ++h) a[h] = -std::exp(src[h]);
+        st = upload(m, a.data(), a.size() * 4, reinterpret_cast<const void **>(&L.ssm_a));
+      }
+    } else if (!L.linear && leaf == "self_attn.qkv_proj.weight") {
+      st = q4({2 * d.n_heads * hd + 2 * d.n_kv_heads * hd, H}, Q35_ENC_Q4_H128_DOT4, &L.in_proj,
+              &m->weight_bytes);
+      L.in_rows = static_cast<int>(shape[0]);
+    } else if (!L.linear && leaf == "self_attn.o_proj.weight") {
+      st = q4({H, d.n_heads * hd}, Q35_ENC_Q4_H128_DOT4, &L.out_proj, &m->weight_bytes);
+      L.out_cols = static_cast<int>(d.n_heads * hd);
+    } else if (!L.linear && leaf == "self_attn.q_norm.weight") st = f32({hd}, &L.q_norm);
+    else if (!L.linear && leaf == "self_attn.k_norm.weight") st = f32({hd}, &L.k_norm);
+    else return set_error(m->ctx, Q35_ERR_INVALID, "unexpected tensor " + name);
+  } else {
+    return set_error(m->ctx, Q35_ERR_INVALID, "unexpected tensor " + name);
+  }
+  if (st == Q35_OK) m->uploaded.insert(name);
+  return st;
+}
+
+extern "C" int q35_model_finalize(q35_model *m) {
+  if (m == nullptr) return Q35_ERR_INVALID;
+  for (const auto &n : m->required)
+    if (!m->uploaded.count(n)) return set_error(m->ctx, Q35_ERR_STATE, "missing tensor " + n);
+  m->finalized = true;
+  return Q35_OK;
+}
+
+// =================================================================== runtime
+namespace {
+
+struct MetaLayout {
+  size_t slots, positions, tokens, seq_lens, penalties, count_input, page_table, total;
+};
+
+MetaLayout meta_layout(int max_batch, int max_pages) {
+  MetaLayout L{};
+  size_t o = 0;
+  auto take = [&](size_t bytes) { const size_t at = o; o = align256(o + bytes); return at; };
+  L.slots = take(max_batch * 4);
+  L.positions = take(max_batch * 4);
+  L.tokens = take(max_batch * 4);
+  L.seq_lens = take(max_batch * 4);
+  L.penalties = take(max_batch * 4);
+  L.count_input = take(max_batch);
+  L.page_table = take(static_cast<size_t>(max_batch) * max_pages * 4);
+  L.total = o;
+  return L;
+}
+
+}  // namespace
+
+extern "C" int q35_runtime_create(q35_model *m, const q35_runtime_config *cfg, q35_runtime **out) {
+  if (m == nullptr || cfg == nullptr || out == nullptr) return Q35_ERR_INVALID;
+  *out = nullptr;
+  if (!m->finalized) return set_error(m->ctx, Q35_ERR_STATE, "model not finalized");
+  const q35_model_dims &d = m->d;
+  if (cfg->max_slots <= 0 || cfg->max_batch <= 0 || cfg->max_batch > kMaxTokens ||
+      cfg->max_context <= 0 || cfg->page_tokens < 1 || (cfg->page_tokens & (cfg->page_tokens - 1)))
+    return set_error(m->ctx, Q35_ERR_INVALID, "invalid runtime config");
+  auto *rt = new (std::nothrow) q35_runtime();
+  if (rt == nullptr) return Q35_ERR_OOM;
+  rt->model = m;
+  rt->ctx = m->ctx;
+  rt->cfg = *cfg;
+  rt->max_pages_per_row = (cfg->max_context + cfg->page_tokens - 1) / cfg->page_tokens;
+  rt->max_splits = (cfg->max_context + rt->split_tokens - 1) / rt->split_tokens;
+  if (rt->cfg.total_pages <= 0) rt->cfg.total_pages = cfg->max_slots * rt->max_pages_per_row;
+  Context *ctx = m->ctx;
+  const int B = cfg->max_batch;
+  const size_t H = d.hidden, I = d.intermediate;
+  const size_t v_dim = static_cast<size_t>(d.lin_v_heads) * d.lin_v_dim;
+  const size_t q_dim = static_cast<size_t>(d.lin_k_heads) * d.lin_k_dim;
+  const size_t ch = 2 * q_dim + v_dim;
+  const size_t kvw = static_cast<size_t>(d.n_kv_heads) * d.head_dim;
+  size_t in_max = 0;
+  for (const auto &L : m->layers) in_max = std::max(in_max, static_cast<size_t>(L.in_rows));
+  rt->proj_width = std::max(in_max, 2 * I);
+  rt->core_width = std::max({v_dim, static_cast<size_t>(d.n_heads) * d.head_dim, I, H});
+  int st = Q35_OK;
+  auto alloc = [&](size_t bytes, void **p) {
+    if (st == Q35_OK) st = rt_alloc(rt, bytes, p);
+  };
+  // slot state
+  rt->rec_slot_stride = static_cast<long long>(m->n_linear) * d.lin_v_heads * d.lin_v_dim * d.lin_k_dim;
+  rt->conv_slot_stride = static_cast<long long>(m->n_linear) * (d.lin_kernel - 1) * ch;
+  alloc(static_cast<size_t>(cfg->max_slots) * rt->rec_slot_stride * 4, reinterpret_cast<void **>(&rt->recurrent));
+  alloc(static_cast<size_t>(cfg->max_slots) * rt->conv_slot_stride * 4, reinterpret_cast<void **>(&rt->conv));
+  alloc(static_cast<size_t>(cfg->max_slots) * d.vocab * 4, reinterpret_cast<void **>(&rt->counts));
+  // KV pool
+  rt->layer_pool_elems = static_cast<size_t>(rt->cfg.total_pages) * cfg->page_tokens * kvw;
+  alloc(std::max<size_t>(1, m->n_full) * rt->layer_pool_elems * 2, reinterpret_cast<void **>(&rt->k_pool));
+  alloc(std::max<size_t>(1, m->n_full) * rt->layer_pool_elems * 2, reinterpret_cast<void **>(&rt->v_pool));
+  // RoPE tables, computed like CpuEngine::Impl::initialize (cpu_engine.inl:343-355)
+  const size_t half = d.rope_dim / 2;
+  alloc(static_cast<size_t>(cfg->max_context) * half * 4, reinterpret_cast<void **>(&rt->rope_cos));
+  alloc(static_cast<size_t>(cfg->max_context) * half * 4, reinterpret_cast<void **>(&rt->rope_sin));
+  // work buffers
+  alloc(B * H * 4, reinterpret_cast<void **>(&rt->x));
+  alloc(B * rt->proj_width * 4, reinterpret_cast<void **>(&rt->proj));
+  alloc(B * rt->core_width * 4, reinterpret_cast<void **>(&rt->core));
+  alloc(B * static_cast<size_t>(d.n_heads) * d.head_dim * 4, reinterpret_cast<void **>(&rt->q_rot));
+  alloc(B * static_cast<size_t>(d.n_heads) * d.head_dim * 4, reinterpret_cast<void **>(&rt->gates));
+  const size_t parts = static_cast<size_t>(B) * d.n_heads * rt->max_splits;
+  alloc(parts * d.head_dim * 4, reinterpret_cast<void **>(&rt->part_o));
+  alloc(parts * 2 * 4, reinterpret_cast<void **>(&rt->part_ml));
+  alloc(B * H * 4, reinterpret_cast<void **>(&rt->hidden_out));
+  const size_t kmax = std::max({H, I, rt->core_width});
+  alloc(4 * 64 * (kmax / 32) * 8, reinterpret_cast<void **>(&rt->codes));
+  alloc(4 * 16 * (kmax / 32) * sizeof(ActParam), reinterpret_cast<void **>(&rt->params));
+  size_t part_floats = 0, counter_n = 0;
+  auto consider = [&](int rows, int nb) {
+    const int s = gemm_choose_ksplit(rows, nb, ctx->cu_count);
+    part_floats = std::max(part_floats, gemm_partial_floats(rows, kMaxTokens, s));
+    counter_n = std::max(counter_n, gemm_counter_count(rows, kMaxTokens));
+  };
+  for (const auto &L : m->layers) {
+    consider(L.in_rows, d.hidden / 32);
+    consider(d.hidden, L.out_cols / 32);
+    consider(2 * d.intermediate, d.hidden / 32);
+    consider(d.hidden, d.intermediate / 32);
+  }
+  consider(d.vocab, d.hidden / 32);
+  alloc(std::max<size_t>(part_floats, 1) * 4, reinterpret_cast<void **>(&rt->partials));
+  alloc(counter_n * 4, reinterpret_cast<void **>(&rt->counters));
+  alloc(kMaxTokens * 8, reinterpret_cast<void **>(&rt->argmax_keys));
+  alloc(kMaxTokens * 4, reinterpret_cast<void **>(&rt->tokens_out_dev));
+  const MetaLayout ml = meta_layout(B, rt->max_pages_per_row);
+  rt->meta_bytes = ml.total;
+  alloc(ml.total, reinterpret_cast<void **>(&rt->meta_dev));
+  if (st == Q35_OK && hipHostMalloc(reinterpret_cast<void **>(&rt->meta_host), ml.total) != hipSuccess)
+    st = set_error(ctx, Q35_ERR_OOM, "pinned metadata");
+  if (st == Q35_OK && hipHostMalloc(reinterpret_cast<void **>(&rt->tokens_out_host), kMaxTokens * 4) != hipSuccess)
+    st = set_error(ctx, Q35_ERR_OOM, "pinned output");
+  if (st == Q35_OK) {
+    std::vector<float> inv(half), cs(static_cast<size_t>(cfg->max_context) * half), sn(cs.size());
+    for (size_t i = 0; i < half; ++i)
+      inv[i] = std::pow(d.rope_theta, -static_cast<float>(2 * i) / static_cast<float>(d.rope_dim));
+    for (size_t p = 0; p < static_cast<size_t>(cfg->max_context); ++p)
+      for (size_t i = 0; i < half; ++i) {
+        const float angle = static_cast<float>(p) * inv[i];
+        cs[p * half + i] = std::cos(angle);
+        sn[p * half + i] = std::sin(angle);
+      }
+    if (hipMemcpy(rt->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(rt->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemset(rt->counters, 0, counter_n * 4) != hipSuccess ||
+        hipMemset(rt->k_pool, 0, std::max<size_t>(1, m->n_full) * rt->layer_pool_elems * 2) != hipSuccess ||
+        hipMemset(rt->v_pool, 0, std::max<size_t>(1, m->n_full) * rt->layer_pool_elems * 2) != hipSuccess)
+      st = set_error(ctx, Q35_ERR_HIP, "runtime initialisation copies");
+  }
+  if (st != Q35_OK) {
+    q35_runtime_destroy(rt);
+    return st;
+  }
+  rt->slot_used.assign(cfg->max_slots, 0);
+  rt->page_ref.assign(rt->cfg.total_pages, 0);
+  rt->free_pages.reserve(rt->cfg.total_pages);
+  for (int p = rt->cfg.total_pages - 1; p >= 0; --p) rt->free_pages.push_back(p);
+  *out = rt;
+  return Q35_OK;
+}
+
+extern "C" void q35_runtime_destroy(q35_runtime *rt) {
+  if (rt == nullptr) return;
+  (void)hipSetDevice(rt->ctx->device);
+  (void)hipStreamSynchronize(rt->ctx->stream);
+  for (auto &kv : rt->graphs) (void)hipGraphExecDestroy(kv.second);
+  for (void *p : rt->allocations) (void)hipFree(p);
+  if (rt->meta_host) (void)hipHostFree(rt->meta_host);
+  if (rt->tokens_out_host) (void)hipHostFree(rt->tokens_out_host);
+  delete rt;
+}
+
+extern "C" int q35_slot_alloc(q35_runtime *rt, const int32_t *prompt, size_t n, int32_t *out_slot) {
+  if (rt == nullptr || out_slot == nullptr || (n && prompt == nullptr)) return Q35_ERR_INVALID;
+  const q35_model_dims &d = rt->model->d;
+  int slot = -1;
+  for (int s = 0; s < rt->cfg.max_slots; ++s)
+    if (!rt->slot_used[s]) { slot = s; break; }
+  if (slot < 0) return set_error(rt->ctx, Q35_ERR_STATE, "no free request slot");
+  for (size_t i = 0; i < n; ++i)
+    if (prompt[i] < 0 || prompt[i] >= d.vocab) return set_error(rt->ctx, Q35_ERR_INVALID, "prompt token out of range");
+  Context *ctx = rt->ctx;
+  Q35_HIP_TRY(ctx, hipMemsetAsync(rt->recurrent + slot * rt->rec_slot_stride, 0, rt->rec_slot_stride * 4, ctx->stream));
+  Q35_HIP_TRY(ctx, hipMemsetAsync(rt->conv + slot * rt->conv_slot_stride, 0, rt->conv_slot_stride * 4, ctx->stream));
+  // prompt token counts (cpu_engine.inl:376-378)
+  std::vector<int32_t> counts(d.vocab, 0);
+  for (size_t i = 0; i < n; ++i) ++counts[prompt[i]];
+  Q35_HIP_TRY(ctx, hipMemcpyAsync(rt->counts + static_cast<size_t>(slot) * d.vocab, counts.data(),
+                                  counts.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+  Q35_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  rt->slot_used[slot] = 1;
+  *out_slot = slot;
+  return Q35_OK;
+}
+
+extern "C" int q35_slot_free(q35_runtime *rt, int32_t slot) {
+  if (rt == nullptr || slot < 0 || slot >= rt->cfg.max_slots || !rt->slot_used[slot]) return Q35_ERR_STATE;
+  rt->slot_used[slot] = 0;
+  return Q35_OK;
+}
+
+extern "C" int q35_page_alloc(q35_runtime *rt, int32_t *out) {
+  if (rt == nullptr || out == nullptr) return Q35_ERR_INVALID;
+  if (rt->free_pages.empty()) return set_error(rt->ctx, Q35_ERR_OOM, "KV page pool exhausted");
+  const int p = rt->free_pages.back();
+  rt->free_pages.pop_back();
+  rt->page_ref[p] = 1;
+  *out = p;
+  return Q35_OK;
+}
+extern "C" int q35_page_retain(q35_runtime *rt, int32_t p) {
+  if (rt == nullptr || p < 0 || p >= rt->cfg.total_pages || rt->page_ref[p] <= 0) return Q35_ERR_STATE;
+  ++rt->page_ref[p];
+  return Q35_OK;
+}
+extern "C" int q35_page_release(q35_runtime *rt, int32_t p) {
+  if (rt == nullptr || p < 0 || p >= rt->cfg.total_pages || rt->page_ref[p] <= 0) return Q35_ERR_STATE;
+  if (--rt->page_ref[p] == 0) rt->free_pages.push_back(p);
+  return Q35_OK;
+}
+extern "C" int q35_page_refcount(q35_runtime *rt, int32_t p) {
+  if (rt == nullptr || p < 0 || p >= rt->cfg.total_pages) return -1;
+  return rt->page_ref[p];
+}
+extern "C" int q35_runtime_free_pages(q35_runtime *rt) {
+  return rt ? static_cast<int>(rt->free_pages.size()) : -1;
+}
+// Copy-on-write: the first `tokens` rows of src into dst, every full layer
+// (KvPagesF16::append on a shared tail page, kv_pages.h:52-60).
+extern "C" int q35_page_copy(q35_runtime *rt, int32_t src, int32_t dst, int32_t tokens) {
+  if (rt == nullptr || src < 0 || dst < 0 || src >= rt->cfg.total_pages || dst >= rt->cfg.total_pages ||
+      tokens < 0 || tokens > rt->cfg.page_tokens)
+    return Q35_ERR_INVALID;
+  const size_t kvw = static_cast<size_t>(rt->model->d.n_kv_heads) * rt->model->d.head_dim;
+  const size_t page_elems = static_cast<size_t>(rt->cfg.page_tokens) * kvw;
+  const size_t bytes = static_cast<size_t>(tokens) * kvw * 2;
+  for (int l = 0; l < rt->model->n_full; ++l) {
+    const size_t base = l * rt->layer_pool_elems;
+    Q35_HIP_TRY(rt->ctx, hipMemcpyAsync(rt->k_pool + base + dst * page_elems, rt->k_pool + base + src * page_elems,
+                                        bytes, hipMemcpyDeviceToDevice, rt->ctx->stream));
+    Q35_HIP_TRY(rt->ctx, hipMemcpyAsync(rt->v_pool + base + dst * page_elems, rt->v_pool + base + src * page_elems,
+                                        bytes, hipMemcpyDeviceToDevice, rt->ctx->stream));
+  }
+  return Q35_OK;
+}
+
+namespace q35 {
+
+// Enqueues one decode step for `batch` rows whose metadata is already in
+// rt->meta_host; the host copy is part of the enqueued work so the whole
+// sequence can be captured as a graph.
+int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
+  q35_model *m = rt->model;
+  Context *ctx = rt->ctx;
+  const q35_model_dims &d = m->d;
+  hipStream_t s = ctx->stream;
+  const MetaLayout ml = meta_layout(rt->cfg.max_batch, rt->max_pages_per_row);
+  auto *mdev = rt->meta_dev;
+  const auto *slots = reinterpret_cast<const int32_t *>(mdev + ml.slots);
+  const auto *positions = reinterpret_cast<const int32_t *>(mdev + ml.positions);
+  const auto *tokens = reinterpret_cast<const int32_t *>(mdev + ml.tokens);
+  const auto *seq_lens = reinterpret_cast<const int32_t *>(mdev + ml.seq_lens);
+  const auto *penalties = reinterpret_cast<const float *>(mdev + ml.penalties);
+  const auto *count_input = reinterpret_cast<const uint8_t *>(mdev + ml.count_input);
+  const auto *page_table = reinterpret_cast<const int32_t *>(mdev + ml.page_table);
+  const int H = d.hidden, I = d.intermediate;
+  const int v_dim = d.lin_v_heads * d.lin_v_dim;
+  const int q_dim = d.lin_k_heads * d.lin_k_dim;
+  const int ch = 2 * q_dim + v_dim;
+  const size_t kvw = static_cast<size_t>(d.n_kv_heads) * d.head_dim;
+  const size_t page_elems = static_cast<size_t>(rt->cfg.page_tokens) * kvw;
+  (void)page_elems;
+  hipError_t e;
+#define Q35_STEP(expr, what)                               \
+  do {                                                     \
+    e = (expr);                                            \
+    if (e != hipSuccess) return hip_error(ctx, e, what);   \
+  } while (0)
+
+  Q35_STEP(hipMemcpyAsync(rt->meta_dev, rt->meta_host, rt->meta_bytes, hipMemcpyHostToDevice, s), "metadata copy");
+  Q35_STEP(launch_embed(m->embed, H / 32, tokens, batch, rt->x, H, rt->counts, d.vocab, slots, count_input, s),
+           "embedding");
+
+  auto prep = [&](int source, const float *x, int x_stride, const float *w, int K, bool h128) {
+    PrepArgs a;
+    a.source = source;
+    a.x = x;
+    a.x_stride = x_stride;
+    a.weight = w;
+    a.eps = d.rms_eps;
+    a.weight_offset = 1.0F;
+    a.tokens = batch;
+    a.K = K;
+    a.h128 = h128;
+    a.seed = d.sign_seed;
+    a.codes = rt->codes;
+    a.params = rt->params;
+    return a;
+  };
+  auto gemm = [&](const q35_q4_0_block_x8 *w, int rows, int K, float *out, int stride,
+                  const float *residual) {
+    GemmArgs g;
+    g.w = w;
+    g.rows = rows;
+    g.nb = K / 32;
+    g.codes = rt->codes;
+    g.params = rt->params;
+    g.tokens = batch;
+    g.out = out;
+    g.stride = stride;
+    g.residual = residual;
+    g.ksplit = gemm_choose_ksplit(rows, K / 32, ctx->cu_count);
+    g.partials = rt->partials;
+    g.counters = rt->counters;
+    return launch_gemm(g, s);
+  };
+
+  for (int l = 0; l < d.n_layers; ++l) {
+    const LayerDev &L = m->layers[l];
+    Q35_STEP(launch_prep(prep(kPrepRmsNorm, rt->x, H, L.input_norm, H, true), s), "input norm prep");
+    Q35_STEP(gemm(L.in_proj, L.in_rows, H, rt->proj, L.in_rows, nullptr), "in projection");
+    if (L.linear) {
+      const int li = m->linear_index[l];
+      DeltaArgs a;
+      a.fused = true;
+      a.state_base = rt->recurrent + static_cast<size_t>(li) * d.lin_v_heads * d.lin_v_dim * d.lin_k_dim;
+      a.slots = slots;
+      a.state_slot_stride = rt->rec_slot_stride;
+      a.batch = batch;
+      a.k_heads = d.lin_k_heads;
+      a.v_heads = d.lin_v_heads;
+      a.kd = d.lin_k_dim;
+      a.vd = d.lin_v_dim;
+      a.out = rt->core;
+      a.proj = rt->proj;
+      a.proj_stride = L.in_rows;
+      a.conv_base = rt->conv + static_cast<size_t>(li) * (d.lin_kernel - 1) * ch;
+      a.conv_slot_stride = rt->conv_slot_stride;
+      a.positions = positions;
+      a.conv_w = L.conv_w;
+      a.kernel = d.lin_kernel;
+      a.dt_bias = L.dt_bias;
+      a.ssm_a = L.ssm_a;
+      a.norm_w = L.lin_norm;
+      a.eps = d.rms_eps;
+      Q35_STEP(launch_delta(a, s), "DeltaNet");
+      Q35_STEP(launch_prep(prep(kPrepPlain, rt->core, v_dim, nullptr, v_dim, true), s), "core prep");
+    } else {
+      const int fi = m->full_index[l];
+      AttnPrepArgs p;
+      p.proj = rt->proj;
+      p.proj_stride = L.in_rows;
+      p.batch = batch;
+      p.heads = d.n_heads;
+      p.kv_heads = d.n_kv_heads;
+      p.head_dim = d.head_dim;
+      p.rope_dim = d.rope_dim;
+      p.q_norm = L.q_norm;
+      p.k_norm = L.k_norm;
+      p.eps = d.rms_eps;
+      p.rope_cos = rt->rope_cos;
+      p.rope_sin = rt->rope_sin;
+      p.positions = positions;
+      p.page_table = page_table;
+      p.max_pages = rt->max_pages_per_row;
+      p.page_tokens = rt->cfg.page_tokens;
+      p.k_pool = rt->k_pool + static_cast<size_t>(fi) * rt->layer_pool_elems;
+      p.v_pool = rt->v_pool + static_cast<size_t>(fi) * rt->layer_pool_elems;
+      p.q_out = rt->q_rot;
+      p.gate_out = rt->gates;
+      Q35_STEP(launch_attn_prep(p, s), "attention prep");
+      AttnArgs a;
+      a.q = rt->q_rot;
+      a.k_pool = p.k_pool;
+      a.v_pool = p.v_pool;
+      a.page_table = page_table;
+      a.max_pages = rt->max_pages_per_row;
+      a.page_tokens = rt->cfg.page_tokens;
+      a.seq_lens = seq_lens;
+      a.batch = batch;
+      a.heads = d.n_heads;
+      a.kv_heads = d.n_kv_heads;
+      a.head_dim = d.head_dim;
+      a.scale = 1.0F / std::sqrt(static_cast<float>(d.head_dim));
+      a.split_tokens = rt->split_tokens;
+      a.max_splits = rt->max_splits;
+      a.part_o = rt->part_o;
+      a.part_ml = rt->part_ml;
+      Q35_STEP(launch_attention(a, s), "attention");
+      PrepArgs pa = prep(kPrepAttnMerge, nullptr, 0, nullptr, d.n_heads * d.head_dim, true);
+      pa.part_o = rt->part_o;
+      pa.part_ml = rt->part_ml;
+      pa.seq_lens = seq_lens;
+      pa.gates = rt->gates;
+      pa.heads = d.n_heads;
+      pa.head_dim = d.head_dim;
+      pa.max_splits = rt->max_splits;
+      pa.split_tokens = rt->split_tokens;
+      Q35_STEP(launch_prep(pa, s), "attention merge prep");
+    }
+    Q35_STEP(gemm(L.out_proj, H, L.out_cols, rt->x, H, rt->x), "out projection");
+    Q35_STEP(launch_prep(prep(kPrepRmsNorm, rt->x, H, L.post_norm, H, true), s), "post norm prep");
+    Q35_STEP(gemm(L.gate_up, 2 * I, H, rt->proj, 2 * I, nullptr), "gate_up projection");
+    Q35_STEP(launch_prep(prep(kPrepSiluMul, rt->proj, 2 * I, nullptr, I, true), s), "silu prep");
+    Q35_STEP(gemm(L.down, H, I, rt->x, H, rt->x), "down projection");
+  }
+  PrepArgs fin = prep(kPrepRmsNorm, rt->x, H, m->final_norm, H, false);
+  fin.normed_out = rt->hidden_out;
+  fin.argmax_reset = rt->argmax_keys;
+  fin.argmax_reset_count = batch;
+  Q35_STEP(launch_prep(fin, s), "final norm prep");
+  if (want_logits) {
+    Q35_STEP(gemm(m->embed, d.vocab, H, rt->logits, d.vocab, nullptr), "logits head");
+  } else {
+    GemmArgs g;
+    g.w = m->embed;
+    g.rows = d.vocab;
+    g.nb = H / 32;
+    g.codes = rt->codes;
+    g.params = rt->params;
+    g.tokens = batch;
+    g.argmax_keys = rt->argmax_keys;
+    g.counts = rt->counts;
+    g.count_rows = slots;
+    g.counts_stride = d.vocab;
+    g.penalties = penalties;
+    g.ksplit = 1;
+    Q35_STEP(launch_gemm(g, s), "greedy head");
+    Q35_STEP(launch_argmax_unpack(rt->argmax_keys, batch, rt->tokens_out_dev, nullptr, s), "argmax unpack");
+    Q35_STEP(hipMemcpyAsync(rt->tokens_out_host, rt->tokens_out_dev, batch * 4, hipMemcpyDeviceToHost, s),
+             "token copy");
+  }
+#undef Q35_STEP
+  return Q35_OK;
+}
+
+}  // namespace q35
+
+extern "C" int q35_runtime_step(q35_runtime *rt, const q35_step_desc *desc, int32_t *out_tokens,
+                                float *out_logits) {
+  if (rt == nullptr || desc == nullptr) return Q35_ERR_INVALID;
+  Context *ctx = rt->ctx;
+  const q35_model_dims &d = rt->model->d;
+  const int B = desc->batch;
+  if (B <= 0 || B > rt->cfg.max_batch || desc->slots == nullptr || desc->positions == nullptr ||
+      desc->tokens == nullptr || desc->page_table == nullptr || desc->max_pages <= 0)
+    return set_error(ctx, Q35_ERR_INVALID, "invalid step descriptor");
+  // validate on the host so no kernel ever sees an out-of-range index
+  std::vector<uint8_t> seen(rt->cfg.max_slots, 0);
+  for (int b = 0; b < B; ++b) {
+    const int slot = desc->slots[b], pos = desc->positions[b], tok = desc->tokens[b];
+    if (slot < 0 || slot >= rt->cfg.max_slots || !rt->slot_used[slot] || seen[slot])
+      return set_error(ctx, Q35_ERR_INVALID, "step rows need distinct allocated slots");
+    seen[slot] = 1;
+    if (pos < 0 || pos >= rt->cfg.max_context) return set_error(ctx, Q35_ERR_INVALID, "position outside max_context");
+    if (tok < 0 || tok >= d.vocab) return set_error(ctx, Q35_ERR_INVALID, "token out of range");
+    if (pos / rt->cfg.page_tokens >= desc->max_pages)
+      return set_error(ctx, Q35_ERR_INVALID, "page table does not cover the position");
+    for (int p = 0; p <= pos / rt->cfg.page_tokens; ++p) {
+      const int page = desc->page_table[static_cast<size_t>(b) * desc->max_pages + p];
+      if (page < 0 || page >= rt->cfg.total_pages || rt->page_ref[page] <= 0)
+        return set_error(ctx, Q35_ERR_INVALID, "page table names a free or invalid page");
+    }
+  }
+  const MetaLayout ml = meta_layout(rt->cfg.max_batch, rt->max_pages_per_row);
+  unsigned char *h = rt->meta_host;
+  std::memset(h, 0, rt->meta_bytes);
+  auto *slots = reinterpret_cast<int32_t *>(h + ml.slots);
+  auto *positions = reinterpret_cast<int32_t *>(h + ml.positions);
+  auto *tokens = reinterpret_cast<int32_t *>(h + ml.tokens);
+  auto *seq_lens = reinterpret_cast<int32_t *>(h + ml.seq_lens);
+  auto *penalties = reinterpret_cast<float *>(h + ml.penalties);
+  auto *count_input = reinterpret_cast<uint8_t *>(h + ml.count_input);
+  auto *pt = reinterpret_cast<int32_t *>(h + ml.page_table);
+  for (int b = 0; b < B; ++b) {
+    slots[b] = desc->slots[b];
+    positions[b] = desc->positions[b];
+    tokens[b] = desc->tokens[b];
+    seq_lens[b] = desc->positions[b] + 1;
+    penalties[b] = desc->penalties ? desc->penalties[b] : 1.0F;
+    count_input[b] = desc->count_input ? desc->count_input[b] : 0;
+    const int used = std::min(desc->max_pages, rt->max_pages_per_row);
+    for (int p = 0; p < used; ++p)
+      pt[static_cast<size_t>(b) * rt->max_pages_per_row + p] = desc->page_table[static_cast<size_t>(b) * desc->max_pages + p];
+  }
+  const bool want_logits = out_logits != nullptr;
+  if (want_logits && rt->logits == nullptr) {
+    int st = rt_alloc(rt, static_cast<size_t>(rt->cfg.max_batch) * d.vocab * 4, reinterpret_cast<void **>(&rt->logits));
+    if (st != Q35_OK) return st;
+  }
+  int st = Q35_OK;
+  if (rt->cfg.use_graphs) {
+    const auto key = std::make_pair(B, want_logits ? 1 : 0);
+    auto it = rt->graphs.find(key);
+    if (it == rt->graphs.end()) {
+      Q35_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+      Q35_HIP_TRY(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+      st = runtime_enqueue_step(rt, B, want_logits);
+      hipGraph_t graph = nullptr;
+      const hipError_t ce = hipStreamEndCapture(ctx->stream, &graph);
+      if (st != Q35_OK) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return st;
+      }
+      if (ce != hipSuccess) return hip_error(ctx, ce, "end capture");
+      hipGraphExec_t exec = nullptr;
+      const hipError_t ie = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(graph);
+      if (ie != hipSuccess) return hip_error(ctx, ie, "graph instantiate");
+      it = rt->graphs.emplace(key, exec).first;
+    }
+    Q35_HIP_TRY(ctx, hipGraphLaunch(it->second, ctx->stream));
+  } else {
+    st = runtime_enqueue_step(rt, B, want_logits);
+    if (st != Q35_OK) return st;
+  }
+  if (want_logits)
+    Q35_HIP_TRY(ctx, hipMemcpyAsync(out_logits, rt->logits, static_cast<size_t>(B) * d.vocab * 4,
+                                    hipMemcpyDeviceToHost, ctx->stream));
+  Q35_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  rt->last_batch = B;
+  if (out_tokens != nullptr) {
+    if (want_logits) {
+      // greedy token from the raw logits with the penalty rule
+      // (cpu_engine_greedy.inl:45-57 / sample_token_from_logits, layers.inl:519-545)
+      std::vector<int32_t> cnt(d.vocab);
+      for (int b = 0; b < B; ++b) {
+        const float *lg = out_logits + static_cast<size_t>(b) * d.vocab;
+        const float pen = desc->penalties ? desc->penalties[b] : 1.0F;
+        if (pen > 1.0F)
+          Q35_HIP_TRY(ctx, hipMemcpy(cnt.data(), rt->counts + static_cast<size_t>(desc->slots[b]) * d.vocab,
+                                     d.vocab * 4, hipMemcpyDeviceToHost));
+        float best = -INFINITY;
+        int at = 0;
+        for (int t = 0; t < d.vocab; ++t) {
+          float v = lg[t];
+          if (pen > 1.0F && cnt[t] > 0) v = v > 0 ? v / pen : v * pen;
+          if (v > best) { best = v; at = t; }
+        }
+        out_tokens[b] = at;
+      }
+    } else {
+      std::memcpy(out_tokens, rt->tokens_out_host, B * 4);
+    }
+  }
+  return Q35_OK;
+}
+
+extern "C" int q35_runtime_last_hidden(q35_runtime *rt, float *out, size_t count) {
+  if (rt == nullptr || out == nullptr) return Q35_ERR_INVALID;
+  const size_t n = std::min(count, static_cast<size_t>(rt->last_batch) * rt->model->d.hidden);
+  Q35_HIP_TRY(rt->ctx, hipMemcpy(out, rt->hidden_out, n * 4, hipMemcpyDeviceToHost));
+  return Q35_OK;
+}

@@ -1,0 +1,130 @@
+"""Q4-G32-DOT4 GEMV/GEMM parity on the GPU (config 1 and edge shapes).
+
+Bar: int32 block dots bit-exact; the exact-mode FP32 outputs bit-exact (same
+fma chain as q4_dot4.cpp:43-56); production split-K outputs within 1e-5
+relative (north-star bar 1e-3); argmax indices exact."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _problem(orc, rng, rows, cols, vectors):
+    canon = orc.random_q4_blocks(rng, rows, cols)
+    packed = orc.dot4_pack(canon, rows, cols // 32)
+    x = rng.standard_normal((vectors, cols)).astype(np.float32)
+    return packed, x
+
+
+@pytest.mark.parametrize("vectors", [4, 16])
+def test_config1_matmul_h128(q, ctx, orc, vectors):
+    rng = np.random.default_rng(3701 + vectors)
+    rows, cols = 3584, 1024
+    packed, x = _problem(orc, rng, rows, cols, vectors)
+    act = orc.h128_prepare_4(x)
+    want = orc.dot4_matmul(packed, act, rows, vectors, cols // 32)
+    dm, da = ctx.array(packed), ctx.array(act)
+    out = ctx.array(shape=(vectors, rows), dtype=np.float32)
+    print(f"config1 matmul B={vectors}", flush=True)
+    q.q4_dot4_matmul(ctx, dm, da, out, rows, vectors, cols // 32, rows, exact=True)
+    got = out.download()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    q.q4_dot4_matmul(ctx, dm, da, out, rows, vectors, cols // 32, rows)
+    fast = out.download()
+    scale = np.abs(want).max()
+    assert np.max(np.abs(fast - want)) <= 1e-5 * scale
+    # int32 block dots, bit-exact against the brute-force oracle
+    dots = ctx.array(shape=(vectors, rows, cols // 32), dtype=np.int32)
+    q.q4_dot4_block_dots(ctx, dm, da, dots, rows, vectors, cols // 32)
+    got_dots = dots.download()
+    for t in (0, vectors - 1):
+        codes, _, _ = orc.x4_vector(act, t)
+        assert np.array_equal(got_dots[t], orc.dot4_block_dots(packed, codes, rows, cols // 32))
+
+
+def test_config1_matvec_b1(q, ctx, orc):
+    rng = np.random.default_rng(1701)
+    rows, cols = 3584, 1024
+    packed, x = _problem(orc, rng, rows, cols, 1)
+    act = orc.q8_quantize_1(x[0])
+    want = orc.dot4_matvec(packed, act, rows, cols // 32)
+    dm, da = ctx.array(packed), ctx.array(act)
+    out = ctx.array(shape=(rows,), dtype=np.float32)
+    print("config1 matvec B=1", flush=True)
+    q.q4_dot4_matvec(ctx, dm, da, out, rows, cols // 32)
+    got = out.download()
+    assert np.max(np.abs(got - want)) <= 1e-5 * np.abs(want).max()
+
+
+@pytest.mark.parametrize("rows,blocks,vectors,stride", [(8, 1, 4, 8), (24, 3, 8, 31), (200, 112, 12, 207),
+                                                        (1032, 32, 64, 1032), (64, 4, 20, 64)])
+def test_edge_shapes(q, ctx, orc, rows, blocks, vectors, stride):
+    rng = np.random.default_rng(rows * 7 + blocks)
+    packed, x = _problem(orc, rng, rows, blocks * 32, vectors)
+    act = orc.q8_quantize_4(x)
+    want = orc.dot4_matmul(packed, act, rows, vectors, blocks, stride)
+    dm, da = ctx.array(packed), ctx.array(act)
+    init = np.full((vectors, stride), -123.0, np.float32)
+    out = ctx.array(init)
+    print(f"edge rows={rows} blocks={blocks} vectors={vectors}", flush=True)
+    q.q4_dot4_matmul(ctx, dm, da, out, rows, vectors, blocks, stride, exact=True)
+    got = out.download()
+    assert np.array_equal(got[:, :rows].view(np.uint32), want[:, :rows].view(np.uint32))
+    assert np.all(got[:, rows:] == -123.0), "wrote past `rows` into the stride padding"
+
+
+def test_extreme_codes(q, ctx, orc):
+    """All-15 / all-0 codes with +-127 activations (the reference test's patterns 0 and 1)."""
+    rows, blocks, vectors = 64, 64, 4
+    for pattern in (0, 1):
+        canon = np.zeros((rows, blocks), orc.Q4_0)
+        canon["qs"] = 255 if pattern == 0 else 0
+        canon["d"] = np.float16(1.0).view(np.uint16)
+        packed = orc.dot4_pack(canon, rows, blocks)
+        act = np.zeros((vectors // 4, blocks), orc.Q8X4)
+        act["qs"] = -128 if pattern == 0 else 127
+        act["sums"] = act["qs"].reshape(vectors // 4, blocks, 4, 32).astype(np.int32).sum(-1)
+        act["scales"] = 0.001
+        want = orc.dot4_matmul(packed, act, rows, vectors, blocks)
+        dm, da = ctx.array(packed), ctx.array(act)
+        out = ctx.array(shape=(vectors, rows), dtype=np.float32)
+        q.q4_dot4_matmul(ctx, dm, da, out, rows, vectors, blocks, rows, exact=True)
+        assert np.array_equal(out.download(), want)
+
+
+def test_argmax_batch_penalty(q, ctx, orc):
+    """Fused greedy head: per-row penalty and lowest-index ties (cpu_engine_greedy.inl:45-57)."""
+    rng = np.random.default_rng(11)
+    rows, cols, vectors = 4096, 1024, 8
+    packed, x = _problem(orc, rng, rows, cols, vectors)
+    act = orc.q8_quantize_4(x)
+    logits = orc.dot4_matmul(packed, act, rows, vectors, cols // 32)
+    counts = (rng.random((vectors, rows)) < 0.05).astype(np.int32) * 2
+    pen = np.array([1.0, 1.05, 1.3, 1.0, 2.0, 1.0, 1.1, 1.0], np.float32)
+    adj = logits.copy()
+    for v in range(vectors):
+        m = (counts[v] > 0) & (pen[v] > 1)
+        adj[v, m] = np.where(adj[v, m] > 0, adj[v, m] / pen[v], adj[v, m] * pen[v])
+    want = adj.argmax(1)
+    dm, da, dc, dp = ctx.array(packed), ctx.array(act), ctx.array(counts), ctx.array(pen)
+    idx = ctx.array(shape=(vectors,), dtype=np.int32)
+    val = ctx.array(shape=(vectors,), dtype=np.float32)
+    q.q4_dot4_argmax_batch(ctx, dm, da, dc, dp, rows, vectors, cols // 32, idx, val)
+    got = idx.download()
+    for v in range(vectors):
+        top2 = np.sort(adj[v])[-2:]
+        if top2[1] - top2[0] > 1e-4 * abs(top2[1]):
+            assert got[v] == want[v]
+        else:
+            assert adj[v, got[v]] >= top2[1] - 1e-4 * abs(top2[1])
+    # exact ties go to the lowest index
+    canon = np.zeros((16, 1), orc.Q4_0)
+    canon["qs"] = 0x99
+    canon["d"] = np.float16(1.0).view(np.uint16)
+    tpk = orc.dot4_pack(canon, 16, 1)
+    tact = np.zeros((1, 1), orc.Q8X4)
+    tact["qs"] = 1
+    tact["sums"] = 32
+    tact["scales"] = 1.0
+    q.q4_dot4_argmax_batch(ctx, ctx.array(tpk), ctx.array(tact), None, None, 16, 4, 1, idx, val)
+    assert np.all(idx.download()[:4] == 0)
