@@ -1,0 +1,226 @@
+#!/usr/bin/env python3
+"""Batched-decode throughput of the MI355X backend on the reference's headline
+workload: a random-init Qwen3.5-0.8B-shaped hybrid model (24 layers, 3
+GatedDeltaNet : 1 gated attention, Q4-G32-DOT4 H128 weights), 16 requests with
+512-token random prompts, greedy decode.
+
+One step = one decode forward of the 16-row batch through CpuEngine's
+advance_batch equivalent (q35_engine_advance_batch): host scheduling, one
+metadata upload, the captured step graph, the fused greedy head and the token
+read-back. Throughput counts decode forwards x rows / seconds, the reference's
+definition (src/cpu_engine_bench_main.cpp:301).
+
+After the timed region, a profiled region of the same decode (eager launches,
+HIP events on the runtime's stream around every kernel) gives per-kernel-class
+durations and the roofline of the dominant kernel. The reference CPU engine,
+built from the reference sources into oracle/_ref, is timed on a bounded sample
+of the same workload as the baseline.
+
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+METRIC = "decode tokens/s at B=16 (0.8B random-init, 1 GPU); Q4 GEMV % peak HBM BW"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+# the 0.8B text config the reference's ProfileLoader reads (profile_loader.cpp:320-420)
+CONFIG_08B = {
+    "_name_or_path": "Qwen/Qwen3.5-0.8B", "model_type": "qwen3_5",
+    "text_config": {
+        "model_type": "qwen3_5_text", "num_hidden_layers": 24, "hidden_size": 1024,
+        "intermediate_size": 3584, "num_attention_heads": 8, "num_key_value_heads": 2, "head_dim": 256,
+        "vocab_size": 248320, "max_position_embeddings": 32768, "rms_norm_eps": 1e-06,
+        "tie_word_embeddings": True, "full_attention_interval": 4, "linear_conv_kernel_dim": 4,
+        "linear_num_key_heads": 16, "linear_num_value_heads": 16, "linear_key_head_dim": 128,
+        "linear_value_head_dim": 128,
+        "rope_parameters": {"rope_theta": 10000000.0, "partial_rotary_factor": 0.25}}}
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def prepare_model_dir(q, seed, weight_std):
+    """Writes the random-init artifact (and the reference's config.json) once per host."""
+    d, sched = q.model_dims(0)
+    path = os.path.join(tempfile.gettempdir(), f"q35_bench_0p8b_s{seed}")
+    os.makedirs(path, exist_ok=True)
+    art = os.path.join(path, "model.q35h128")
+    if not os.path.exists(art):
+        t = time.time()
+        q.write_random_artifact(art + ".part", d, sched, seed=seed, weight_std=weight_std)
+        os.replace(art + ".part", art)
+        log(f"wrote random-init artifact {art} ({os.path.getsize(art) / 1e6:.1f} MB) in {time.time() - t:.1f}s")
+    with open(os.path.join(path, "config.json"), "w") as f:
+        json.dump(CONFIG_08B, f)
+    return d, sched, path, art
+
+
+def cpu_baseline(model_dir, artifact, batch, prompt_len, new_tokens, threads):
+    """The reference CpuEngine (oracle/_ref, built from the reference sources)
+    on a bounded sample: `batch` requests, `prompt_len`-token prompts,
+    `new_tokens` greedy outputs; decode forwards x rows / decode seconds."""
+    from oracle import q35_oracle as orc  # the checker build, timed as the baseline only
+
+    if not orc.ref_available():
+        log("oracle/_ref not built: no CPU baseline")
+        return None
+    r = orc.ref()
+    rng = np.random.default_rng(4242)
+    prompts = rng.integers(0, CONFIG_08B["text_config"]["vocab_size"], size=(batch, prompt_len)).astype(np.int32)
+    out = np.zeros((batch, new_tokens), np.int32)
+    ms = ctypes.c_double()
+    err = ctypes.create_string_buffer(512)
+    t = time.time()
+    rc = r.ref_engine_greedy(os.fsencode(model_dir), os.fsencode(artifact), threads, prompts.ctypes.data,
+                             prompt_len, batch, new_tokens, 1.0, out.ctypes.data, None, None, ctypes.byref(ms),
+                             err, 512)
+    if rc != 0:
+        log(f"reference engine failed: {err.value.decode(errors='replace')}")
+        return None
+    forwards = new_tokens - 1  # the first output token comes out of prefill
+    value = batch * forwards * 1000.0 / ms.value
+    log(f"reference CPU engine: {value:.1f} tok/s decode on {threads} threads ({time.time() - t:.1f}s wall)")
+    return {"value": round(value, 2), "unit": "tokens/s", "cores": threads, "kind": "reference",
+            "sample": f"{batch} requests x {prompt_len}-token random prompts, {new_tokens} greedy tokens each; "
+                      f"{forwards} decode forwards per request timed through CpuEngine::advance_batch on the "
+                      f"same random-init 0.8B artifact"}
+
+
+def roofline(name, stats, traffic):
+    ms, launches, nbytes = stats
+    if launches == 0 or ms <= 0:
+        return None
+    per_launch_bytes = nbytes / launches
+    per_launch_s = ms / launches / 1000.0
+    achieved = per_launch_bytes / per_launch_s / 1e9
+    t = traffic.get(name) if traffic else None
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": t.get("bytes_per_launch") if isinstance(t, dict) else None,
+            "kernel_class": name, "launches": launches, "avg_us": round(ms / launches * 1000.0, 2),
+            "algorithmic_bytes_per_launch": round(per_launch_bytes)}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=119, help="timed decode forwards")
+    ap.add_argument("--warmup", type=int, default=8, help="untimed decode forwards")
+    ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--profile-steps", type=int, default=16, help="decode forwards in the profiled region")
+    ap.add_argument("--cpu-baseline", choices=("on", "off"), default="on")
+    ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, cpus)")
+    ap.add_argument("--cpu-tokens", type=int, default=32, help="greedy tokens per request in the CPU sample")
+    ap.add_argument("--seed", type=int, default=1)
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              f"(asked for --gpus {args.gpus}, WORLD_SIZE {world})", file=sys.stderr)
+        sys.exit(2)
+    if args.steps <= 0 or args.warmup < 0 or args.batch <= 0 or args.profile_steps < 0:
+        ap.error("steps must be positive and warmup/profile-steps non-negative")
+
+    import __graft_entry__ as entry
+
+    q = entry.load()
+    ctx = q.Context(0)
+    cu, arch = ctx.device_info()
+    log(f"device {arch}, {cu} CUs")
+    d, sched, model_dir, artifact = prepare_model_dir(q, args.seed, 0.02)
+
+    t = time.time()
+    model = q.Model(ctx, d, sched, artifact=artifact)
+    log(f"model resident in HBM in {time.time() - t:.1f}s")
+    total_new = 1 + args.warmup + args.steps + args.profile_steps
+    engine = q.Engine(model, max_resident_requests=args.batch, max_context=args.prompt + total_new + 16,
+                      max_decode_batch_size=args.batch, prefill_chunk_size=128, page_tokens=16, use_graphs=True)
+    rng = np.random.default_rng(20261201)
+    prompts = rng.integers(0, d.vocab, size=(args.batch, args.prompt)).astype(np.int32)
+    ids = [engine.submit(p, max_new_tokens=total_new) for p in prompts]
+    t = time.time()
+    engine.prefill_batch(ids)
+    log(f"prefilled {args.batch} x {args.prompt} tokens in {time.time() - t:.2f}s")
+
+    for _ in range(args.warmup):
+        engine.advance_batch(ids)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        engine.advance_batch(ids)
+    ctx.synchronize()
+    elapsed = time.perf_counter() - t0
+    tok_s = args.batch * args.steps / elapsed
+    log(f"timed {args.steps} decode forwards: {elapsed * 1000 / args.steps:.3f} ms/step, {tok_s:.0f} tok/s")
+
+    prof = {}
+    if args.profile_steps:
+        engine.profile_reset()
+        engine.set_profiling(True)
+        for _ in range(args.profile_steps):
+            engine.advance_batch(ids)
+        ctx.synchronize()
+        engine.set_profiling(False)
+        prof = engine.profile()
+        step_ms = sum(v[0] for v in prof.values()) / args.profile_steps
+        for name, (ms, n, by) in sorted(prof.items(), key=lambda kv: -kv[1][0]):
+            if n:
+                log(f"  {name:10s} {ms / args.profile_steps * 1000:9.1f} us/step  {n // args.profile_steps:4d} "
+                    f"launches/step  {by / ms / 1e6 if ms else 0:8.1f} GB/s")
+        log(f"  kernel time per step {step_ms * 1000:.1f} us (eager, events)")
+
+    for rid in ids:
+        res, toks = engine.result(rid)
+        if toks.size != 1 + args.warmup + args.steps + args.profile_steps:
+            raise SystemExit(f"request {rid} produced {toks.size} tokens")
+    engine.close()
+    model.close()
+    ctx.close()
+
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f)
+    dominant = max(prof, key=lambda k: prof[k][0]) if prof else None
+    roof = roofline(dominant, prof[dominant], traffic) if dominant else None
+    gemm_roof = roofline("gemm", prof["gemm"], traffic) if prof else None
+
+    base = None
+    if args.cpu_baseline == "on":
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        base = cpu_baseline(model_dir, artifact, args.batch, args.prompt, args.cpu_tokens, threads)
+
+    line = {
+        "metric": METRIC, "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(elapsed * 1000 / args.steps, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "q4xi8->i32 (projections), f32 (DeltaNet, attention)",
+        "data": "synthetic: random-init weights N(0,0.02) packed to Q4-G32-DOT4 H128, random-token prompts",
+        "config": {"workload": "random-init Qwen3.5-0.8B-shaped hybrid, batched greedy decode",
+                   "batch": args.batch, "prompt_tokens": args.prompt,
+                   "decode_forwards_timed": args.steps, "graphs": True},
+        "roofline": roof, "q4_gemm_roofline": gemm_roof, "cpu_baseline": base,
+    }
+    if base:
+        line["speedup_vs_cpu_baseline"] = round(tok_s / base["value"], 1)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

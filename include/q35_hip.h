@@ -280,6 +280,20 @@ int q35_runtime_step(q35_runtime *rt, const q35_step_desc *desc, int32_t *out_to
 /* Copies the final normalized hidden rows of the last step ([batch][hidden]). */
 int q35_runtime_last_hidden(q35_runtime *rt, float *out, size_t count);
 
+/* Kernel-level timing, no reference counterpart (the reference reports only
+ * request-level prefill_ms/decode_ms, cpu_engine.h:147). While enabled,
+ * steps launch eagerly (no graph replay) and every kernel launch is bracketed
+ * by a pair of HIP events on the runtime's stream; elapsed times, launch
+ * counts and the launches' algorithmic HBM bytes accumulate per kernel class
+ * until q35_runtime_profile_reset. */
+enum { Q35_KERNEL_EMBED = 0, Q35_KERNEL_PREP = 1, Q35_KERNEL_GEMM = 2, Q35_KERNEL_DELTA = 3,
+       Q35_KERNEL_ATTN_PREP = 4, Q35_KERNEL_ATTENTION = 5, Q35_KERNEL_ARGMAX = 6,
+       Q35_KERNEL_CLASSES = 7 };
+int q35_runtime_set_profiling(q35_runtime *rt, int enable);
+int q35_runtime_profile_reset(q35_runtime *rt);
+int q35_runtime_profile_read(q35_runtime *rt, int kernel_class, double *total_ms,
+                             uint64_t *launches, double *algorithmic_bytes);
+
 /* ================================================================= engine
  * C mirror of qwen35x::CpuEngine (include/qwen35x/runtime/cpu_engine.h:173-215)
  * for greedy requests, built on the runtime above. IDs are monotonic and never
@@ -317,6 +331,8 @@ int q35_engine_prefill_batch(q35_engine *engine, const uint64_t *ids, size_t cou
 int q35_engine_result(q35_engine *engine, uint64_t id, q35_request_result *out,
                       int32_t *tokens, size_t token_capacity, size_t *token_count);
 int q35_engine_cancel(q35_engine *engine, uint64_t id);
+/* The runtime the engine steps (for q35_runtime_set_profiling and friends). */
+q35_runtime *q35_engine_runtime(q35_engine *engine);
 int q35_engine_release(q35_engine *engine, uint64_t id);
 const char *q35_engine_last_error(const q35_engine *engine);
 

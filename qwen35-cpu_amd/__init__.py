@@ -24,7 +24,10 @@ Q35_OK = 0
 STATUS = {0: "ok", 1: "invalid argument", 2: "HIP runtime error", 3: "out of memory",
           4: "invalid state", 5: "unsupported shape", 6: "I/O error"}
 REQ_STATUS = {0: "prefill", 1: "decode", 2: "complete", 3: "cancelled", 4: "failed", 5: "queued"}
+REQ_STATUS_INV = {v: k for k, v in REQ_STATUS.items()}
 ENC_F32, ENC_Q4_0_DOT4, ENC_Q4_H128_DOT4 = 0, 5, 6
+# kernel classes of the step profiler (q35_runtime_profile_read)
+KERNEL_CLASSES = ("embed", "prep", "gemm", "delta", "attn_prep", "attention", "argmax")
 DEFAULT_SIGN_SEED = 0x5148333548313238  # q4_h128.h:25-26
 
 Q4X8_BYTES, Q8X4_BYTES, Q8X1_BYTES = 144, 152, 40
@@ -133,6 +136,9 @@ _SIGS = {
     "q35_runtime_free_pages": (c_int, [P]),
     "q35_runtime_step": (c_int, [P, POINTER(StepDesc), P, P]),
     "q35_runtime_last_hidden": (c_int, [P, P, c_size_t]),
+    "q35_runtime_set_profiling": (c_int, [P, c_int]),
+    "q35_runtime_profile_reset": (c_int, [P]),
+    "q35_runtime_profile_read": (c_int, [P, c_int, POINTER(c_double), POINTER(c_uint64), POINTER(c_double)]),
     "q35_engine_create": (c_int, [P, POINTER(EngineConfig), POINTER(P)]),
     "q35_engine_destroy": (None, [P]),
     "q35_engine_submit": (c_int, [P, P, c_size_t, c_size_t, c_float, P, c_size_t, POINTER(c_uint64)]),
@@ -144,6 +150,7 @@ _SIGS = {
     "q35_engine_cancel": (c_int, [P, c_uint64]),
     "q35_engine_release": (c_int, [P, c_uint64]),
     "q35_engine_last_error": (c_char_p, [P]),
+    "q35_engine_runtime": (P, [P]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _f = getattr(lib, _name)
@@ -382,7 +389,31 @@ class Model:
             self.handle = None
 
 
-class Runtime:
+class _Profiled:
+    """Kernel-level timing of the decode step (q35_runtime_set_profiling):
+    eager launches, each bracketed by HIP events on the runtime's stream."""
+
+    def _rt(self):
+        raise NotImplementedError
+
+    def set_profiling(self, enable=True):
+        self.ctx.check(lib.q35_runtime_set_profiling(self._rt(), int(enable)), "set profiling")
+
+    def profile_reset(self):
+        self.ctx.check(lib.q35_runtime_profile_reset(self._rt()), "profile reset")
+
+    def profile(self):
+        """{class: (total_ms, launches, algorithmic_bytes)}."""
+        out = {}
+        for i, name in enumerate(KERNEL_CLASSES):
+            ms, n, by = c_double(), c_uint64(), c_double()
+            self.ctx.check(lib.q35_runtime_profile_read(self._rt(), i, ctypes.byref(ms), ctypes.byref(n),
+                                                        ctypes.byref(by)), "profile read")
+            out[name] = (ms.value, n.value, by.value)
+        return out
+
+
+class Runtime(_Profiled):
     """Device slots, KV page pool and the captured decode step."""
 
     def __init__(self, model, max_slots=16, max_batch=16, max_context=1024, page_tokens=16, total_pages=0,
@@ -427,6 +458,9 @@ class Runtime:
         self.ctx.check(lib.q35_runtime_step(self.handle, ctypes.byref(d), _ptr(out), _ptr(lg)), "runtime step")
         return (out, lg) if logits else out
 
+    def _rt(self):
+        return self.handle
+
     def last_hidden(self, batch):
         out = np.empty((batch, self.model.dims.hidden), np.float32)
         self.ctx.check(lib.q35_runtime_last_hidden(self.handle, _ptr(out), out.size), "last hidden")
@@ -438,7 +472,7 @@ class Runtime:
             self.handle = None
 
 
-class Engine:
+class Engine(_Profiled):
     """CpuEngine mirror (include/qwen35x/runtime/cpu_engine.h:173-215), greedy requests."""
 
     def __init__(self, model, max_resident_requests=32, max_context=8192, max_decode_batch_size=32,
@@ -449,6 +483,9 @@ class Engine:
         h = c_void_p()
         self.ctx.check(lib.q35_engine_create(model.handle, ctypes.byref(cfg), ctypes.byref(h)), "engine create")
         self.handle = h
+
+    def _rt(self):
+        return lib.q35_engine_runtime(self.handle)
 
     def _check(self, status, what):
         if status != Q35_OK:

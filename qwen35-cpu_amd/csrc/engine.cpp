@@ -395,6 +395,8 @@ extern "C" int q35_engine_result(q35_engine *e, uint64_t id, q35_request_result 
   return Q35_OK;
 }
 
+extern "C" q35_runtime *q35_engine_runtime(q35_engine *e) { return e ? e->rt : nullptr; }
+
 extern "C" int q35_engine_cancel(q35_engine *e, uint64_t id) {
   if (e == nullptr) return Q35_ERR_INVALID;
   auto it = e->reqs.find(id);

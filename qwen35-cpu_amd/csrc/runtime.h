@@ -77,8 +77,19 @@ struct q35_runtime {
   std::map<std::pair<int, int>, hipGraphExec_t> graphs;
   int last_batch = 0;
   std::vector<void *> allocations;
+  // kernel-level timing: event pairs reused across steps, the (class, bytes)
+  // of each bracketed launch of the step in flight, and per-class totals
+  bool profiling = false;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> prof_events;
+  std::vector<std::pair<int, double>> prof_pending;
+  double prof_ms[Q35_KERNEL_CLASSES] = {};
+  double prof_bytes[Q35_KERNEL_CLASSES] = {};
+  uint64_t prof_launches[Q35_KERNEL_CLASSES] = {};
 };
 
 namespace q35 {
 int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits);
+// Algorithmic HBM bytes of one GEMM launch: packed weights, A16 codes and
+// scales of every token, FP32 outputs (and the residual read when fused).
+double gemm_algorithmic_bytes(int rows, int nb, int tokens, bool stores, bool residual);
 }

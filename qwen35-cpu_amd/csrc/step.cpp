@@ -396,6 +396,7 @@ extern "C" void q35_runtime_destroy(q35_runtime *rt) {
   (void)hipSetDevice(rt->ctx->device);
   (void)hipStreamSynchronize(rt->ctx->stream);
   for (auto &kv : rt->graphs) (void)hipGraphExecDestroy(kv.second);
+  for (auto &ev : rt->prof_events) (void)hipEventDestroy(ev.first), (void)hipEventDestroy(ev.second);
   for (void *p : rt->allocations) (void)hipFree(p);
   if (rt->meta_host) (void)hipHostFree(rt->meta_host);
   if (rt->tokens_out_host) (void)hipHostFree(rt->tokens_out_host);
@@ -478,6 +479,53 @@ extern "C" int q35_page_copy(q35_runtime *rt, int32_t src, int32_t dst, int32_t 
 
 namespace q35 {
 
+double gemm_algorithmic_bytes(int rows, int nb, int tokens, bool stores, bool residual) {
+  const double weights = static_cast<double>(rows / 8) * nb * sizeof(q35_q4_0_block_x8);
+  const double acts = static_cast<double>(tokens) * (nb * 32.0 + sizeof(ActParam));
+  const double outs = static_cast<double>(tokens) * rows * 4.0 * ((stores ? 1 : 0) + (residual ? 1 : 0));
+  return weights + acts + outs;
+}
+
+namespace {
+
+// Starts a bracketed launch: records the start event of the next free pair on
+// `s` and remembers the launch's class and algorithmic bytes; *stop receives
+// the event to record after the launch.
+hipError_t profile_begin(q35_runtime *rt, hipStream_t s, int cls, double bytes, hipEvent_t *stop) {
+  const size_t i = rt->prof_pending.size();
+  if (i == rt->prof_events.size()) {
+    hipEvent_t a = nullptr, b = nullptr;
+    hipError_t e = hipEventCreate(&a);
+    if (e != hipSuccess) return e;
+    e = hipEventCreate(&b);
+    if (e != hipSuccess) {
+      (void)hipEventDestroy(a);
+      return e;
+    }
+    rt->prof_events.emplace_back(a, b);
+  }
+  rt->prof_pending.emplace_back(cls, bytes);
+  *stop = rt->prof_events[i].second;
+  return hipEventRecord(rt->prof_events[i].first, s);
+}
+
+// After the step's stream synchronisation: fold the bracketed launches into
+// the per-class totals.
+int profile_collect(q35_runtime *rt) {
+  for (size_t i = 0; i < rt->prof_pending.size(); ++i) {
+    float ms = 0;
+    Q35_HIP_TRY(rt->ctx, hipEventElapsedTime(&ms, rt->prof_events[i].first, rt->prof_events[i].second));
+    const int cls = rt->prof_pending[i].first;
+    rt->prof_ms[cls] += ms;
+    rt->prof_bytes[cls] += rt->prof_pending[i].second;
+    rt->prof_launches[cls] += 1;
+  }
+  rt->prof_pending.clear();
+  return Q35_OK;
+}
+
+}  // namespace
+
 // Enqueues one decode step for `batch` rows whose metadata is already in
 // rt->meta_host; the host copy is part of the enqueued work so the whole
 // sequence can be captured as a graph.
@@ -508,10 +556,26 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
     e = (expr);                                            \
     if (e != hipSuccess) return hip_error(ctx, e, what);   \
   } while (0)
+  // A kernel launch; with profiling on it is bracketed by an event pair and
+  // counted under `cls` with `bytes` algorithmic HBM bytes.
+#define Q35_KERNEL(cls, bytes, expr, what)                                     \
+  do {                                                                         \
+    hipEvent_t q35_stop_ = nullptr;                                            \
+    if (rt->profiling) Q35_STEP(profile_begin(rt, s, (cls), (bytes), &q35_stop_), "profile event"); \
+    Q35_STEP(expr, what);                                                      \
+    if (q35_stop_ != nullptr) Q35_STEP(hipEventRecord(q35_stop_, s), "profile event"); \
+  } while (0)
+  const double B = batch;
+  const auto *host_seq = reinterpret_cast<const int32_t *>(rt->meta_host + ml.seq_lens);
+  double kv_tokens = 0;
+  for (int b = 0; b < batch; ++b) kv_tokens += host_seq[b];
+  // activation prep: FP32 rows in (x_cols wide), A16 codes + scales out
+  auto prep_bytes = [&](double x_cols, int K) { return B * (x_cols * 4.0 + K + sizeof(ActParam)); };
 
   Q35_STEP(hipMemcpyAsync(rt->meta_dev, rt->meta_host, rt->meta_bytes, hipMemcpyHostToDevice, s), "metadata copy");
-  Q35_STEP(launch_embed(m->embed, H / 32, tokens, batch, rt->x, H, rt->counts, d.vocab, slots, count_input, s),
-           "embedding");
+  Q35_KERNEL(Q35_KERNEL_EMBED, B * (H / 32 * 18.0 + H * 4.0 + 8.0),
+             launch_embed(m->embed, H / 32, tokens, batch, rt->x, H, rt->counts, d.vocab, slots, count_input, s),
+             "embedding");
 
   auto prep = [&](int source, const float *x, int x_stride, const float *w, int K, bool h128) {
     PrepArgs a;
@@ -549,8 +613,10 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
 
   for (int l = 0; l < d.n_layers; ++l) {
     const LayerDev &L = m->layers[l];
-    Q35_STEP(launch_prep(prep(kPrepRmsNorm, rt->x, H, L.input_norm, H, true), s), "input norm prep");
-    Q35_STEP(gemm(L.in_proj, L.in_rows, H, rt->proj, L.in_rows, nullptr), "in projection");
+    Q35_KERNEL(Q35_KERNEL_PREP, prep_bytes(H, H) + H * 4.0,
+               launch_prep(prep(kPrepRmsNorm, rt->x, H, L.input_norm, H, true), s), "input norm prep");
+    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_algorithmic_bytes(L.in_rows, H / 32, batch, true, false),
+               gemm(L.in_proj, L.in_rows, H, rt->proj, L.in_rows, nullptr), "in projection");
     if (L.linear) {
       const int li = m->linear_index[l];
       DeltaArgs a;
@@ -575,8 +641,14 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
       a.ssm_a = L.ssm_a;
       a.norm_w = L.lin_norm;
       a.eps = d.rms_eps;
-      Q35_STEP(launch_delta(a, s), "DeltaNet");
-      Q35_STEP(launch_prep(prep(kPrepPlain, rt->core, v_dim, nullptr, v_dim, true), s), "core prep");
+      // recurrent state read + written, projection row in, conv ring (K-1 rows
+      // read, one written), core output
+      const double delta_bytes =
+          B * (2.0 * d.lin_v_heads * d.lin_v_dim * d.lin_k_dim * 4.0 + L.in_rows * 4.0 +
+               static_cast<double>(d.lin_kernel) * ch * 4.0 + v_dim * 4.0);
+      Q35_KERNEL(Q35_KERNEL_DELTA, delta_bytes, launch_delta(a, s), "DeltaNet");
+      Q35_KERNEL(Q35_KERNEL_PREP, prep_bytes(v_dim, v_dim),
+                 launch_prep(prep(kPrepPlain, rt->core, v_dim, nullptr, v_dim, true), s), "core prep");
     } else {
       const int fi = m->full_index[l];
       AttnPrepArgs p;
@@ -600,7 +672,10 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
       p.v_pool = rt->v_pool + static_cast<size_t>(fi) * rt->layer_pool_elems;
       p.q_out = rt->q_rot;
       p.gate_out = rt->gates;
-      Q35_STEP(launch_attn_prep(p, s), "attention prep");
+      // projection row in; rotated q, gate, and the new K/V rows (FP16) out
+      Q35_KERNEL(Q35_KERNEL_ATTN_PREP,
+                 B * (L.in_rows * 4.0 + 2.0 * d.n_heads * d.head_dim * 4.0 + 2.0 * kvw * 2.0),
+                 launch_attn_prep(p, s), "attention prep");
       AttnArgs a;
       a.q = rt->q_rot;
       a.k_pool = p.k_pool;
@@ -618,7 +693,12 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
       a.max_splits = rt->max_splits;
       a.part_o = rt->part_o;
       a.part_ml = rt->part_ml;
-      Q35_STEP(launch_attention(a, s), "attention");
+      // every cached K and V row of each request once, q in, split partials out
+      const double splits_used = std::ceil(kv_tokens / rt->split_tokens);
+      Q35_KERNEL(Q35_KERNEL_ATTENTION,
+                 kv_tokens * kvw * 2.0 * 2.0 + B * d.n_heads * d.head_dim * 4.0 +
+                     splits_used * d.n_heads * (d.head_dim + 2) * 4.0,
+                 launch_attention(a, s), "attention");
       PrepArgs pa = prep(kPrepAttnMerge, nullptr, 0, nullptr, d.n_heads * d.head_dim, true);
       pa.part_o = rt->part_o;
       pa.part_ml = rt->part_ml;
@@ -628,21 +708,29 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
       pa.head_dim = d.head_dim;
       pa.max_splits = rt->max_splits;
       pa.split_tokens = rt->split_tokens;
-      Q35_STEP(launch_prep(pa, s), "attention merge prep");
+      Q35_KERNEL(Q35_KERNEL_PREP,
+                 splits_used * d.n_heads * (d.head_dim + 2) * 4.0 + prep_bytes(d.n_heads * d.head_dim, d.n_heads * d.head_dim),
+                 launch_prep(pa, s), "attention merge prep");
     }
-    Q35_STEP(gemm(L.out_proj, H, L.out_cols, rt->x, H, rt->x), "out projection");
-    Q35_STEP(launch_prep(prep(kPrepRmsNorm, rt->x, H, L.post_norm, H, true), s), "post norm prep");
-    Q35_STEP(gemm(L.gate_up, 2 * I, H, rt->proj, 2 * I, nullptr), "gate_up projection");
-    Q35_STEP(launch_prep(prep(kPrepSiluMul, rt->proj, 2 * I, nullptr, I, true), s), "silu prep");
-    Q35_STEP(gemm(L.down, H, I, rt->x, H, rt->x), "down projection");
+    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_algorithmic_bytes(H, L.out_cols / 32, batch, true, true),
+               gemm(L.out_proj, H, L.out_cols, rt->x, H, rt->x), "out projection");
+    Q35_KERNEL(Q35_KERNEL_PREP, prep_bytes(H, H) + H * 4.0,
+               launch_prep(prep(kPrepRmsNorm, rt->x, H, L.post_norm, H, true), s), "post norm prep");
+    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_algorithmic_bytes(2 * I, H / 32, batch, true, false),
+               gemm(L.gate_up, 2 * I, H, rt->proj, 2 * I, nullptr), "gate_up projection");
+    Q35_KERNEL(Q35_KERNEL_PREP, prep_bytes(2.0 * I, I),
+               launch_prep(prep(kPrepSiluMul, rt->proj, 2 * I, nullptr, I, true), s), "silu prep");
+    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_algorithmic_bytes(H, I / 32, batch, true, true),
+               gemm(L.down, H, I, rt->x, H, rt->x), "down projection");
   }
   PrepArgs fin = prep(kPrepRmsNorm, rt->x, H, m->final_norm, H, false);
   fin.normed_out = rt->hidden_out;
   fin.argmax_reset = rt->argmax_keys;
   fin.argmax_reset_count = batch;
-  Q35_STEP(launch_prep(fin, s), "final norm prep");
+  Q35_KERNEL(Q35_KERNEL_PREP, prep_bytes(H, H) + H * 4.0 + B * H * 4.0, launch_prep(fin, s), "final norm prep");
   if (want_logits) {
-    Q35_STEP(gemm(m->embed, d.vocab, H, rt->logits, d.vocab, nullptr), "logits head");
+    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_algorithmic_bytes(d.vocab, H / 32, batch, true, false),
+               gemm(m->embed, d.vocab, H, rt->logits, d.vocab, nullptr), "logits head");
   } else {
     GemmArgs g;
     g.w = m->embed;
@@ -657,11 +745,14 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
     g.counts_stride = d.vocab;
     g.penalties = penalties;
     g.ksplit = 1;
-    Q35_STEP(launch_gemm(g, s), "greedy head");
-    Q35_STEP(launch_argmax_unpack(rt->argmax_keys, batch, rt->tokens_out_dev, nullptr, s), "argmax unpack");
+    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_algorithmic_bytes(d.vocab, H / 32, batch, false, false), launch_gemm(g, s),
+               "greedy head");
+    Q35_KERNEL(Q35_KERNEL_ARGMAX, B * 12.0,
+               launch_argmax_unpack(rt->argmax_keys, batch, rt->tokens_out_dev, nullptr, s), "argmax unpack");
     Q35_STEP(hipMemcpyAsync(rt->tokens_out_host, rt->tokens_out_dev, batch * 4, hipMemcpyDeviceToHost, s),
              "token copy");
   }
+#undef Q35_KERNEL
 #undef Q35_STEP
   return Q35_OK;
 }
@@ -721,7 +812,7 @@ extern "C" int q35_runtime_step(q35_runtime *rt, const q35_step_desc *desc, int3
     if (st != Q35_OK) return st;
   }
   int st = Q35_OK;
-  if (rt->cfg.use_graphs) {
+  if (rt->cfg.use_graphs && !rt->profiling) {
     const auto key = std::make_pair(B, want_logits ? 1 : 0);
     auto it = rt->graphs.find(key);
     if (it == rt->graphs.end()) {
@@ -750,6 +841,10 @@ extern "C" int q35_runtime_step(q35_runtime *rt, const q35_step_desc *desc, int3
     Q35_HIP_TRY(ctx, hipMemcpyAsync(out_logits, rt->logits, static_cast<size_t>(B) * d.vocab * 4,
                                     hipMemcpyDeviceToHost, ctx->stream));
   Q35_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  if (rt->profiling) {
+    st = profile_collect(rt);
+    if (st != Q35_OK) return st;
+  }
   rt->last_batch = B;
   if (out_tokens != nullptr) {
     if (want_logits) {
@@ -775,6 +870,28 @@ extern "C" int q35_runtime_step(q35_runtime *rt, const q35_step_desc *desc, int3
       std::memcpy(out_tokens, rt->tokens_out_host, B * 4);
     }
   }
+  return Q35_OK;
+}
+
+extern "C" int q35_runtime_set_profiling(q35_runtime *rt, int enable) {
+  if (rt == nullptr) return Q35_ERR_INVALID;
+  rt->profiling = enable != 0;
+  rt->prof_pending.clear();
+  return Q35_OK;
+}
+
+extern "C" int q35_runtime_profile_reset(q35_runtime *rt) {
+  if (rt == nullptr) return Q35_ERR_INVALID;
+  for (int c = 0; c < Q35_KERNEL_CLASSES; ++c) rt->prof_ms[c] = rt->prof_bytes[c] = 0, rt->prof_launches[c] = 0;
+  return Q35_OK;
+}
+
+extern "C" int q35_runtime_profile_read(q35_runtime *rt, int cls, double *total_ms, uint64_t *launches,
+                                        double *bytes) {
+  if (rt == nullptr || cls < 0 || cls >= Q35_KERNEL_CLASSES) return Q35_ERR_INVALID;
+  if (total_ms) *total_ms = rt->prof_ms[cls];
+  if (launches) *launches = rt->prof_launches[cls];
+  if (bytes) *bytes = rt->prof_bytes[cls];
   return Q35_OK;
 }
 
