@@ -86,8 +86,8 @@ def cpu_baseline(model_dir, artifact, batch, prompt_len, new_tokens, threads):
     ms = ctypes.c_double()
     err = ctypes.create_string_buffer(512)
     t = time.time()
-    rc = r.ref_engine_greedy(os.fsencode(model_dir), os.fsencode(artifact), threads, prompts.ctypes.data,
-                             prompt_len, batch, new_tokens, 1.0, out.ctypes.data, None, None, ctypes.byref(ms),
+    rc = r.ref_engine_greedy(os.fsencode(model_dir), os.fsencode(artifact), threads, 0, prompts.ctypes.data,
+                             prompt_len, batch, new_tokens, 1.0, None, out.ctypes.data, None, None, ctypes.byref(ms),
                              err, 512)
     if rc != 0:
         log(f"reference engine failed: {err.value.decode(errors='replace')}")

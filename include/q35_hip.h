@@ -223,7 +223,7 @@ typedef struct {
   int32_t max_slots;      /* resident requests (CpuEngineConfig::max_resident_requests) */
   int32_t max_batch;      /* rows per step (<= 64)                                      */
   int32_t max_context;    /* tokens per request (CpuEngineConfig::max_context)          */
-  int32_t page_tokens;    /* tokens per KV page (power of two, 16..256)                 */
+  int32_t page_tokens;    /* tokens per KV page (a power of two)                        */
   int32_t total_pages;    /* KV pool capacity in pages; 0 = max_slots*ceil(ctx/page)    */
   int32_t use_graphs;     /* capture each step shape as a hipGraph and replay it        */
 } q35_runtime_config;

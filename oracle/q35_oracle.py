@@ -373,8 +373,9 @@ def ref():
             "ref_rms_norm_f32": (None, [P, P, P, c_size_t, c_size_t, c_float, c_float, c_int]),
             "ref_l2_normalize_f32": (None, [P, c_size_t, c_size_t, c_float, c_float, c_int]),
             "ref_silu_mul_f32": (None, [P, P, P, c_size_t, c_int]),
-            "ref_engine_greedy": (c_int, [ctypes.c_char_p, ctypes.c_char_p, c_int, P, c_size_t, c_size_t, c_size_t,
-                                          c_float, P, P, P, P, ctypes.c_char_p, c_size_t]),
+            "ref_engine_set_probe": (None, [P, c_size_t, P]),
+            "ref_engine_greedy": (c_int, [ctypes.c_char_p, ctypes.c_char_p, c_int, c_int, P, c_size_t, c_size_t, c_size_t,
+                                          c_float, P, P, P, P, P, ctypes.c_char_p, c_size_t]),
         }
         for name, (res, args) in sigs.items():
             f = getattr(r, name)

@@ -159,6 +159,18 @@ void ref_silu_mul_f32(const float *g, const float *u, float *out, std::size_t n,
   silu_mul_f32(g, u, out, n, be(b));
 }
 
+// Optional logit probes for the next ref_engine_greedy call with logits
+// capture: the raw logits at `count` fixed vocabulary indices of every (row,
+// step) go to values[row][step][count]. Cleared by passing count 0.
+static const std::int32_t *g_probe_index = nullptr;
+static std::size_t g_probe_count = 0;
+static float *g_probe_values = nullptr;
+void ref_engine_set_probe(const std::int32_t *index, std::size_t count, float *values) {
+  g_probe_index = index;
+  g_probe_count = count;
+  g_probe_values = values;
+}
+
 // Greedy decode through the reference engine (cpu_engine.h:173-215), the way
 // src/cpu_engine_bench_main.cpp:241-301 drives it: every request is prefilled
 // with advance(), then advance_batch() runs until all requests complete.
@@ -166,10 +178,15 @@ void ref_silu_mul_f32(const float *g, const float *u, float *out, std::size_t n,
 // top_values/top_index are non-null, a logits callback records the 8 largest
 // raw logits of every (row, step) into [batch][new_tokens][8] (the callback
 // makes the engine take its full-logits path, cpu_engine.inl:307-321).
+// backend is the Q8_0Backend of every kernel (q8_0.h:23-31; 0 = auto_select).
+// forced, when non-null, is [batch][new_tokens]: the rows' forced_output_tokens
+// (cpu_engine.h:108; every output is forced and logits are still reported),
+// which teacher-forces a fixed token sequence through the decode path.
 // Returns 0 on success; the error text is copied into error[error_size].
-int ref_engine_greedy(const char *model_dir, const char *artifact, int threads,
+int ref_engine_greedy(const char *model_dir, const char *artifact, int threads, int backend,
                       const std::int32_t *prompts, std::size_t prompt_len, std::size_t batch,
-                      std::size_t new_tokens, float penalty, std::int32_t *out_tokens,
+                      std::size_t new_tokens, float penalty, const std::int32_t *forced,
+                      std::int32_t *out_tokens,
                       float *top_values, std::int32_t *top_index, double *decode_ms,
                       char *error, std::size_t error_size) {
   std::string err;
@@ -185,6 +202,7 @@ int ref_engine_greedy(const char *model_dir, const char *artifact, int threads,
   CpuLoadOptions options;
   options.model_dir = model_dir;
   options.cpu_q4_h128_path = artifact;
+  options.cpu_q8_backend = be(backend);  // options.h:17; 0 = auto_select
   auto model = CpuModel::load(*profile, options, err);
   if (!model) return fail(err);
   CpuEngineConfig config;
@@ -217,6 +235,10 @@ int ref_engine_greedy(const char *model_dir, const char *artifact, int threads,
       at[p] = static_cast<std::int32_t>(t);
     }
     std::memcpy(c.values + (c.row * c.new_tokens + step) * 8, best, sizeof(best));
+    if (g_probe_count != 0) {
+      float *dst = g_probe_values + (c.row * c.new_tokens + step) * g_probe_count;
+      for (std::size_t i = 0; i < g_probe_count; ++i) dst[i] = logits[g_probe_index[i]];
+    }
     std::memcpy(c.index + (c.row * c.new_tokens + step) * 8, at, sizeof(at));
     return true;
   };
@@ -227,6 +249,8 @@ int ref_engine_greedy(const char *model_dir, const char *artifact, int threads,
     spec.max_new_tokens = new_tokens;
     spec.sampling.temperature = 0.0F;
     spec.sampling.repetition_penalty = penalty;
+    if (forced != nullptr)
+      spec.forced_output_tokens.assign(forced + r * new_tokens, forced + (r + 1) * new_tokens);
     if (top_values && top_index) {
       captures[r] = Capture{top_values, top_index, new_tokens, r};
       spec.logits_callback = callback;

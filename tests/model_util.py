@@ -2,6 +2,9 @@
 restatement of the reference packer, run by the oracle and by the HIP runtime."""
 from __future__ import annotations
 
+import os
+import struct
+
 import numpy as np
 
 from oracle import q35_oracle as orc
@@ -143,3 +146,112 @@ def hip_greedy(q, ctx, d, sched, tensors, prompts, new_tokens, penalty=1.0, want
             out[:, n] = res
     rt.close()
     return (out, np.stack(logits, 1)) if want_logits else out
+
+
+def fnv1a(b):
+    h = 0xcbf29ce484222325
+    for x in np.frombuffer(b, np.uint8):
+        h = ((h ^ int(x)) * 0x100000001b3) & ((1 << 64) - 1)
+    return h
+
+
+def read_artifact(path):
+    """Q35H128 v1 reader (src/weights/q4_h128_artifact.cpp layout), independent of the library."""
+    raw = open(path, "rb").read()
+    assert raw[:8] == b"Q35H128\0"
+    version, endian, header, align = struct.unpack_from("<4I", raw, 8)
+    assert (version, endian, header, align) == (1, 0x01020304, 96, 64)
+    count, dir_off, dir_bytes, data_off, seed = struct.unpack_from("<5Q", raw, 24)
+    layers, hidden, inter, vocab = struct.unpack_from("<4I", raw, 64)
+    tensors, pos = {}, dir_off
+    for _ in range(count):
+        name_size, rank, enc, transform, group, zero = struct.unpack_from("<6I", raw, pos)
+        tseed, elems, off, size, checksum = struct.unpack_from("<5Q", raw, pos + 24)
+        name = raw[pos + 64:pos + 64 + name_size].decode()
+        shape = struct.unpack_from(f"<{rank}Q", raw, pos + 64 + name_size)
+        pos += 64 + name_size + 8 * rank
+        assert off % 64 == 0 and off >= data_off and off + size <= len(raw) and zero == 0
+        tensors[name] = dict(enc=enc, transform=transform, group=group, seed=tseed, elems=elems, shape=shape,
+                             data=raw[off:off + size], checksum=checksum)
+    assert pos == dir_off + dir_bytes
+    return dict(seed=seed, dims=(layers, hidden, inter, vocab)), tensors
+
+
+def artifact_tensors(path):
+    """{hf_name: (encoding, shape, payload bytes as uint8)} of a Q35H128 file."""
+    _, t = read_artifact(path)
+    return {k: (v["enc"], list(v["shape"]), np.frombuffer(v["data"], np.uint8)) for k, v in t.items()}
+
+
+GOLDEN_0P8B = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "engine_0p8b.npz")
+
+
+def golden_0p8b():
+    """Reference-engine greedy tokens and top-8 logits (tests/golden/make_engine_golden.py)."""
+    with np.load(GOLDEN_0P8B) as f:
+        return {k: np.ascontiguousarray(f[k]) for k in f.files}
+
+
+def write_0p8b_artifact(q, directory, seed, weight_std):
+    d, sched = q.model_dims(0)
+    path = os.path.join(directory, "model.q35h128")
+    q.write_random_artifact(path, d, sched, seed=seed, weight_std=weight_std)
+    return d, sched, path
+
+
+def check_against_golden(tokens, logits_at, g, tol):
+    """tokens [B, N] must equal the reference's up to each row's first
+    near-tie (top-2 gap below 2*tol); logits_at(row, step, index[8]) gives our
+    raw logits at the reference's top-8 indices, which must agree within tol
+    for every position compared."""
+    ref_tok, top_v, top_i = g["tokens"], g["top_values"], g["top_index"]
+    compared = 0
+    for r in range(ref_tok.shape[0]):
+        for n in range(ref_tok.shape[1]):
+            got = logits_at(r, n, top_i[r, n])
+            assert np.max(np.abs(got - top_v[r, n])) < tol, (r, n, got, top_v[r, n])
+            compared += 1
+            if tokens[r, n] != ref_tok[r, n]:
+                assert top_v[r, n, 0] - top_v[r, n, 1] < 2 * tol, (r, n)
+                break
+    return compared
+
+
+def oracle_envelope(d, sched, tensors, prompts, new_tokens, penalty=1.0, want=None):
+    """The model's own quantization noise: the oracle against itself with the
+    RMSNorm epsilon moved by 10%, a last-ulp change of every norm. Activation
+    quantization rounds each 32-value block's scale to binary16, so such a
+    change flips whole blocks wherever a scale sits on a rounding boundary,
+    and the flips compound through the recurrent state. Returns
+    (logits, tokens, max_abs, mean_abs) of the unperturbed run and the
+    perturbed run's distance from it."""
+    if want is None:
+        want = oracle_greedy(d, sched, tensors, prompts, new_tokens, penalty, want_logits=True)
+    tok, lg = want
+    d2 = dict(d)
+    d2["rms_eps"] = d["rms_eps"] * 1.1
+    _, lg2 = oracle_greedy(d2, sched, tensors, prompts, new_tokens, penalty, want_logits=True)
+    diff = np.abs(lg2[:, 0] - lg[:, 0])
+    return lg, tok, float(diff.max()), float(diff.mean())
+
+
+def reference_envelope(g):
+    """The reference's own cross-ISA spread in the 0.8B golden: its scalar
+    Q8_0 backend against the host's auto-selected one, over the probe logits
+    of every teacher-forced position. Returns (max_abs, mean_abs)."""
+    diff = np.abs(g["forced_b1_probe"] - g["forced_b0_probe"])
+    return float(diff.max()), float(diff.mean())
+
+
+def teacher_forced_probe_logits(step_fn, seq, probe_index):
+    """Feeds seq[:, i] at position i for i < len-1 through step_fn(i, tokens)
+    -> logits [rows][vocab]; returns logits at probe_index [rows][len-1][P]
+    and the argmax tokens [rows][len-1]."""
+    rows, n = seq.shape
+    out = np.zeros((rows, n - 1, probe_index.size), np.float32)
+    top = np.zeros((rows, n - 1), np.int32)
+    for i in range(n - 1):
+        lg = step_fn(i, seq[:, i])
+        out[:, i] = lg[:, probe_index]
+        top[:, i] = np.argmax(lg, axis=1)
+    return out, top

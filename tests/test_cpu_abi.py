@@ -7,11 +7,12 @@ present) packs the same FP32 rows; the dims presets match the reference's
 text_architecture shapes."""
 import os
 import re
-import struct
 import subprocess
 
 import numpy as np
 import pytest
+
+from tests.model_util import fnv1a, read_artifact
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "q35_hip.h")
@@ -59,35 +60,6 @@ def test_dims_presets(q):
             (layers, hidden, inter, heads, kvh, vh)
         assert d.vocab == 248320 and d.head_dim == 256 and d.rope_dim == 64 and d.lin_k_heads == 16
         assert sched.tolist() == [0 if (i + 1) % 4 == 0 else 1 for i in range(layers)]
-
-
-def fnv1a(b):
-    h = 0xcbf29ce484222325
-    for x in np.frombuffer(b, np.uint8):
-        h = ((h ^ int(x)) * 0x100000001b3) & ((1 << 64) - 1)
-    return h
-
-
-def read_artifact(path):
-    """Q35H128 v1 reader (src/weights/q4_h128_artifact.cpp layout), independent of the library."""
-    raw = open(path, "rb").read()
-    assert raw[:8] == b"Q35H128\0"
-    version, endian, header, align = struct.unpack_from("<4I", raw, 8)
-    assert (version, endian, header, align) == (1, 0x01020304, 96, 64)
-    count, dir_off, dir_bytes, data_off, seed = struct.unpack_from("<5Q", raw, 24)
-    layers, hidden, inter, vocab = struct.unpack_from("<4I", raw, 64)
-    tensors, pos = {}, dir_off
-    for _ in range(count):
-        name_size, rank, enc, transform, group, zero = struct.unpack_from("<6I", raw, pos)
-        tseed, elems, off, size, checksum = struct.unpack_from("<5Q", raw, pos + 24)
-        name = raw[pos + 64:pos + 64 + name_size].decode()
-        shape = struct.unpack_from(f"<{rank}Q", raw, pos + 64 + name_size)
-        pos += 64 + name_size + 8 * rank
-        assert off % 64 == 0 and off >= data_off and off + size <= len(raw) and zero == 0
-        tensors[name] = dict(enc=enc, transform=transform, group=group, seed=tseed, elems=elems, shape=shape,
-                             data=raw[off:off + size], checksum=checksum)
-    assert pos == dir_off + dir_bytes
-    return dict(seed=seed, dims=(layers, hidden, inter, vocab)), tensors
 
 
 @pytest.fixture(scope="module")

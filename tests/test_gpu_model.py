@@ -1,11 +1,22 @@
 """Whole decode step on the GPU against the oracle's restatement of
-forward_batch (cpu_engine.inl:201-325) on a small hybrid model: greedy tokens
-identical (margin-aware), raw logits within 1e-2 max-abs; graph replay
-identical to eager launches."""
+forward_batch (cpu_engine.inl:201-325) on a small hybrid model.
+
+Activation quantization rounds every 32-value block's scale to binary16, so
+two correct implementations whose reductions differ in the last ulp (a tree
+sum on the GPU, a sequential sum in the oracle, SIMD lanes in the reference)
+flip whole blocks now and then, and the flips compound through the recurrent
+state: the reference's own scalar and AVX-512 builds disagree by up to 0.23 in
+the 0.8B model's logits. The bar here is therefore the model's own noise
+envelope (tests.model_util.oracle_envelope): the GPU may be no further from
+the oracle than the oracle is from itself under a last-ulp perturbation of
+its norms (x1.5), and greedy tokens must agree until the first position whose
+top-2 margin is inside that envelope. Graph replay must be bit-identical to
+eager launches, and the fused greedy head identical to argmax of the logits."""
 import numpy as np
 import pytest
 
-from tests.model_util import build_small_model, hip_greedy, oracle_greedy, small_dims, upload_model
+from tests.model_util import (build_small_model, hip_greedy, oracle_envelope, oracle_greedy, small_dims,
+                              upload_model)
 
 pytestmark = pytest.mark.gpu
 
@@ -19,23 +30,26 @@ def small(q, ctx):
     model.close()
 
 
+def tokens_agree(got, want, want_lg, margin):
+    for r in range(want.shape[0]):
+        for n in range(want.shape[1]):
+            if got[r, n] != want[r, n]:
+                top2 = np.sort(want_lg[r, n])[-2:]
+                assert top2[1] - top2[0] < margin, (r, n, top2)
+                break
+
+
 def test_greedy_tokens_and_logits(q, ctx, orc, small):
     d, sched, tensors, model = small
     prompts = np.random.default_rng(1).integers(0, d["vocab"], size=(5, 24)).astype(np.int32)
     print("small model: oracle", flush=True)
-    want, want_lg = oracle_greedy(d, sched, tensors, prompts, 8, want_logits=True)
-    print("small model: HIP", flush=True)
+    want_lg, want, env_max, env_mean = oracle_envelope(d, sched, tensors, prompts, 8)
+    print(f"small model: envelope max {env_max:.4f} mean {env_mean:.5f}; HIP", flush=True)
     got, got_lg = hip_greedy(q, ctx, d, sched, tensors, prompts, 8, want_logits=True, model=model)
-    assert np.max(np.abs(got_lg[:, 0] - want_lg[:, 0])) < 1e-2
-    # teacher-forced comparison is not available here, so compare while the
-    # sequences agree, requiring agreement wherever the oracle's margin is clear
-    for r in range(prompts.shape[0]):
-        for n in range(8):
-            top2 = np.sort(want_lg[r, n])[-2:]
-            if got[r, n] != want[r, n]:
-                assert top2[1] - top2[0] < 1e-2, (r, n)
-                break
-            assert np.max(np.abs(got_lg[r, n] - want_lg[r, n])) < 1e-2, (r, n)
+    diff = np.abs(got_lg[:, 0] - want_lg[:, 0])
+    print(f"small model: HIP vs oracle max {diff.max():.4f} mean {diff.mean():.5f}", flush=True)
+    assert diff.max() <= 1.5 * env_max + 1e-3 and diff.mean() <= 1.5 * env_mean + 1e-4
+    tokens_agree(got, want, want_lg, env_max)
 
 
 def test_greedy_path_matches_logits_path(q, ctx, small):
@@ -57,12 +71,11 @@ def test_graph_replay_equals_eager(q, ctx, small):
 def test_penalty_and_page_sizes(q, ctx, orc, small):
     d, sched, tensors, model = small
     prompts = np.random.default_rng(4).integers(0, 64, size=(2, 20)).astype(np.int32)
-    want, want_lg = oracle_greedy(d, sched, tensors, prompts, 6, penalty=1.3, want_logits=True)
+    want_lg, want, env_max, _ = oracle_envelope(d, sched, tensors, prompts, 6, penalty=1.3)
+    results = []
     for pt in (1, 16, 64):
         got = hip_greedy(q, ctx, d, sched, tensors, prompts, 6, penalty=1.3, page_tokens=pt, model=model)
-        for r in range(2):
-            for n in range(6):
-                if got[r, n] != want[r, n]:
-                    top2 = np.sort(want_lg[r, n])[-2:]
-                    assert top2[1] - top2[0] < 5e-2
-                    break
+        tokens_agree(got, want, want_lg, env_max)
+        results.append(got)
+    # the page size only changes where KV rows live, never the arithmetic
+    assert np.array_equal(results[0], results[1]) and np.array_equal(results[1], results[2])

@@ -1,0 +1,52 @@
+"""The CPU oracle's whole decode step (q35o_forward_batch, the restatement of
+forward_batch, cpu_engine.inl:201-325) on the random-init 0.8B artifact
+against the reference CpuEngine's teacher-forced logits
+(tests/golden/engine_0p8b.npz). Activation quantization makes any two
+implementations with different reduction orders drift apart through binary16
+scale flips; the reference's scalar and auto-selected backends themselves
+differ by the envelope stored in the golden. The oracle must stay within 1.5x
+that envelope of the reference's production (auto) backend."""
+import os
+
+import numpy as np
+import pytest
+
+from tests.model_util import (artifact_tensors, golden_0p8b, reference_envelope, teacher_forced_probe_logits,
+                              write_0p8b_artifact)
+
+ROWS = 2
+
+
+@pytest.fixture(scope="module")
+def artifact(q, tmp_path_factory):
+    g = golden_0p8b()
+    d, sched, path = write_0p8b_artifact(q, str(tmp_path_factory.mktemp("m08")), int(g["seed"][0]),
+                                         float(g["weight_std"][0]))
+    yield d, sched, path, g
+    os.remove(path)
+
+
+def test_oracle_within_reference_envelope(orc, artifact):
+    d, sched, path, g = artifact
+    m = orc.OracleModel(d.as_dict(), sched, artifact_tensors(path))
+    seq = g["forced_sequence"][:ROWS]
+    states = [m.new_state(seq.shape[1] + 1, seq[r, :1]) for r in range(ROWS)]
+
+    def step(i, tokens):
+        _, lg, _ = m.step(states, tokens, 1.0, True)
+        for r in range(ROWS):
+            states[r]["counts"][seq[r, i + 1]] += 1
+        return lg
+
+    got, top = teacher_forced_probe_logits(step, seq, g["probe_index"])
+    env_max, env_mean = reference_envelope(g)
+    diff = np.abs(got - g["forced_b0_probe"][:ROWS])
+    print(f"oracle vs reference: max {diff.max():.4f} mean {diff.mean():.5f}; "
+          f"reference scalar vs auto: max {env_max:.4f} mean {env_mean:.5f}")
+    assert diff.max() <= 1.5 * env_max and diff.mean() <= 1.5 * env_mean
+    # the first position runs one token from an empty state: flips are rare there
+    assert np.abs(got[:, 0] - g["forced_b0_probe"][:ROWS, 0]).max() < 0.1
+    ref_top = g["forced_b0_top_index"][:ROWS, :, 0]
+    margin = g["forced_b0_top_values"][:ROWS, :, 0] - g["forced_b0_top_values"][:ROWS, :, 1]
+    clear = margin > 2 * env_max
+    assert np.array_equal(top[clear], ref_top[clear])
