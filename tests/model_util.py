@@ -238,8 +238,24 @@ def oracle_envelope(d, sched, tensors, prompts, new_tokens, penalty=1.0, want=No
 def reference_envelope(g):
     """The reference's own cross-ISA spread in the 0.8B golden: its scalar
     Q8_0 backend against the host's auto-selected one, over the probe logits
-    of every teacher-forced position. Returns (max_abs, mean_abs)."""
+    of every teacher-forced position. Returns (max_abs, mean_abs,
+    mean_abs of the first four positions)."""
     diff = np.abs(g["forced_b1_probe"] - g["forced_b0_probe"])
+    return float(diff.max()), float(diff.mean()), float(diff[:, :4].mean())
+
+
+def check_within_envelope(got, g, rows):
+    """Probe logits [rows][steps][P] against the reference's auto backend:
+    no further than 1.5x the reference's own scalar-vs-auto spread, overall
+    and over the first four positions (where flips have not compounded yet).
+    Returns (max_abs, mean_abs)."""
+    env_max, env_mean, env_early = reference_envelope(g)
+    diff = np.abs(got - g["forced_b0_probe"][:rows])
+    print(f"vs reference: max {diff.max():.4f} mean {diff.mean():.5f} early {diff[:, :4].mean():.5f} "
+          f"(reference scalar vs auto: max {env_max:.4f} mean {env_mean:.5f} early {env_early:.5f})", flush=True)
+    assert diff.max() <= 1.5 * env_max
+    assert diff.mean() <= 1.5 * env_mean
+    assert diff[:, :4].mean() <= 1.5 * env_early
     return float(diff.max()), float(diff.mean())
 
 
