@@ -128,6 +128,8 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, cpus)")
     ap.add_argument("--cpu-tokens", type=int, default=32, help="greedy tokens per request in the CPU sample")
     ap.add_argument("--seed", type=int, default=1)
+    ap.add_argument("--graphs", choices=("on", "off"), default="on",
+                    help="replay captured step graphs (off: eager launches, e.g. under rocprofv3)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -151,7 +153,7 @@ def main():
     log(f"model resident in HBM in {time.time() - t:.1f}s")
     total_new = 1 + args.warmup + args.steps + args.profile_steps
     engine = q.Engine(model, max_resident_requests=args.batch, max_context=args.prompt + total_new + 16,
-                      max_decode_batch_size=args.batch, prefill_chunk_size=128, page_tokens=16, use_graphs=True)
+                      max_decode_batch_size=args.batch, prefill_chunk_size=128, page_tokens=16, use_graphs=args.graphs == "on")
     rng = np.random.default_rng(20261201)
     prompts = rng.integers(0, d.vocab, size=(args.batch, args.prompt)).astype(np.int32)
     ids = [engine.submit(p, max_new_tokens=total_new) for p in prompts]
@@ -214,7 +216,7 @@ def main():
         "data": "synthetic: random-init weights N(0,0.02) packed to Q4-G32-DOT4 H128, random-token prompts",
         "config": {"workload": "random-init Qwen3.5-0.8B-shaped hybrid, batched greedy decode",
                    "batch": args.batch, "prompt_tokens": args.prompt,
-                   "decode_forwards_timed": args.steps, "graphs": True},
+                   "decode_forwards_timed": args.steps, "graphs": args.graphs == "on"},
         "roofline": roof, "q4_gemm_roofline": gemm_roof, "cpu_baseline": base,
     }
     if base:

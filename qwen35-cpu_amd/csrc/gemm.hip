@@ -2,22 +2,34 @@
 //
 // Reads the reference's 144-byte Q4_0BlockX8 DOT4 tiles in place (no repack):
 //   qs[32t+4r+j] = u[r][8t+j] | u[r][8t+4+j] << 4          (q4_dot4.h:5-6)
-// A wavefront owns 64 output rows (eight 8-row tiles) and one 16-token tile.
-// Lane l loads the 16-byte segment m = 2*(l/16) + (l%16)%2 of tile (l%16)/2:
-// four 32-bit words = rows 4h..4h+3 of chunk t = l/16, i.e. eight consecutive
-// columns each. Word i, unpacked to two int8x4 (low nibbles = columns 8t..8t+3,
-// high nibbles = 8t+4..8t+7), is exactly the A operand of
-// v_mfma_i32_16x16x32_i8 #i for virtual row l%16 and k-group l/16, so each
-// 128-byte tile body is consumed by one coalesced 16-byte load per lane and
-// the per-block int32 dot comes out of four MFMAs:
-//   D_i[4G+v][tok] = sum_k u*a - 8*sum_a         (C operand = -8*sum_a)
-// which is the reference's integer dot (q4_dot4_simd.inl:66-89). Output lane
-// (G, tok) holds rows 16G + 4v + i, so the FP32 epilogue
+// so the 32-bit word 8t+r of a tile body holds row r's columns 8t..8t+3 (low
+// nibbles) and 8t+4..8t+7 (high nibbles).
+//
+// Work decomposition. A workgroup owns a 64-row group (eight 8-row tiles) and
+// W <= 16 wavefronts that split the K blocks of that group; every wavefront
+// issues the loads of all of its blocks (at most 8 per chunk) before the
+// first MFMA, so one launch keeps W x 8 x 1.1 KB of weights in flight per
+// workgroup and the weight stream never waits on the activation chain.
+//
+// Lane l = (G = l/16, c = l%16) loads, per 32-column block, the 16-byte body
+// segment 2G + (c%2) of tile c/2 -- four words = rows 4(c%2)..4(c%2)+3 of
+// tile c/2, columns 8G..8G+7 -- plus the four FP16 scales of those rows (8
+// bytes at tile offset 8(c%2)). Word i, unpacked to int8, is the B operand of
+// v_mfma_i32_16x16x32_i8 #i for B column c (= output row 4c+i) and k-group G;
+// the A operand is the prepared activation word of token c, k-group G (the
+// "A16" layout). One extra MFMA against a constant -8 B operand yields
+// -8 * sum(a) per token, which seeds the C operand of the four real MFMAs, so
+//   D_i[4G+j][c] = sum_k (u - 8) * a      (q4_dot4_simd.inl:66-89)
+// is the reference's exact int32 block dot for row 4c+i and token 4G+j. The
+// FP32 epilogue per block is the reference's
 //   acc = fma(float(dot), half(d_row) * s_tok, acc)   (q4_dot4.cpp:53)
-// runs per row and token in block order. Waves of a workgroup split the block
-// range; the workgroup sums its waves in fixed order, and split-K workgroups
-// are summed in split order by the last one to finish, so results are
-// deterministic run to run.
+// in block order within each wavefront; the wavefronts are summed in fixed
+// order through LDS, so results are deterministic. With one wavefront per
+// group (exact mode) every output is the reference's single fma chain.
+//
+// The greedy head (argmax epilogue) runs a grid-stride loop over row groups
+// and leaves one 64-bit (value, lowest index) key per workgroup and token;
+// argmax_finalize_kernel reduces those keys per token. No atomics anywhere.
 #include "q35_device.h"
 #include "q35_internal.h"
 
@@ -26,9 +38,10 @@ namespace {
 
 typedef Q35_V4I v4i;
 
-constexpr int kGemmThreads = 256;
 constexpr int kRowsPerGroup = 64;
-constexpr int kRedStride = 68;  // 64 rows + pad (LDS bank spread)
+constexpr int kChunk = 8;          // blocks per wavefront held in flight
+constexpr int kMaxWaves = 16;
+constexpr long kMinus8 = static_cast<long>(0xF8F8F8F8F8F8F8F8ull);  // int8 -8 x 8
 
 __device__ __forceinline__ long unpack_word(uint32_t w) {
   const uint32_t lo = w & 0x0f0f0f0fu;
@@ -36,237 +49,237 @@ __device__ __forceinline__ long unpack_word(uint32_t w) {
   return static_cast<long>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-template <int TT>
-__global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs a) {
-  __shared__ float red[4][16][kRedStride];
-  __shared__ unsigned long long best[4][16];
-  __shared__ int last_flag;
-
-  const int rg = blockIdx.x, split = blockIdx.y, tg = blockIdx.z;
+template <bool ARGMAX, bool DOTS>
+__global__ __launch_bounds__(1024) void gemm_kernel(GemmArgs a) {
+  Q35_DYNAMIC_SHARED(float, smem);
+  const int W = static_cast<int>(blockDim.x) >> 6;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int c = lane & 15, G = lane >> 4, T = c >> 1, h = c & 1;
-  const int ntiles = a.rows >> 3, nb = a.nb;
-  const int rt = rg * 8 + T;
-  const bool row_ok = rt < ntiles;
-  const int ht0 = rg * 8 + 2 * G;
-  const bool h0_ok = ht0 < ntiles, h1_ok = ht0 + 1 < ntiles;
+  const int G = lane >> 4, c = lane & 15, h = c & 1, T = c >> 1;
+  const int nb = a.nb, ntiles = a.rows >> 3;
+  const int groups = (ntiles + 7) >> 3;
+  float *act_scale = smem;                  // [nb][16] scales of the token tile
+  float *red = smem + nb * 16;              // [W][a.red_tokens][64] wave partials
+  unsigned long long *best = reinterpret_cast<unsigned long long *>(red + W * a.red_tokens * 64);  // [16]
 
-  const int S = a.ksplit;
-  const int kb0 = (split * nb) / S, kb1 = ((split + 1) * nb) / S;
-  // exact mode: one wave runs the whole block range, so each output is the
-  // reference's single fma chain over blocks (bit-exact FP32)
-  const int per_wave = a.exact ? (kb1 - kb0) : ((kb1 - kb0 + 3) >> 2);
-  const int wb0 = a.exact ? (wave == 0 ? kb0 : kb1) : kb0 + wave * per_wave;
-  const int wb1 = a.exact ? (wave == 0 ? kb1 : kb1) : min(kb1, wb0 + per_wave);
+  const int per = a.exact ? nb : (nb + W - 1) / W;
+  const int b0 = min(nb, wave * per), b1 = min(nb, b0 + per);
+  const int token_tiles = (a.tokens + 15) >> 4;
+  const uint8_t *wbase = reinterpret_cast<const uint8_t *>(a.w);
 
-  const uint8_t *W = reinterpret_cast<const uint8_t *>(a.w);
-  const uint8_t *wrow = W + (static_cast<size_t>(rt) * nb) * 144 + 16 + 16 * (2 * G + h);
-  const uint8_t *hrow0 = W + (static_cast<size_t>(ht0) * nb) * 144;
-  const uint8_t *hrow1 = hrow0 + static_cast<size_t>(nb) * 144;
+  for (int tt = 0; tt < token_tiles; ++tt) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < nb * 16; i += blockDim.x)
+      act_scale[i] = a.params[static_cast<size_t>(tt) * nb * 16 + i].scale;
+    if (ARGMAX && threadIdx.x < 16) best[threadIdx.x] = 0ull;
+    __syncthreads();
+    const uint64_t *acodes = a.codes + static_cast<size_t>(tt) * nb * 64 + lane;
 
-  float acc[TT][16];
-#pragma unroll
-  for (int tt = 0; tt < TT; ++tt)
-#pragma unroll
-    for (int j = 0; j < 16; ++j) acc[tt][j] = 0.0F;
-
-  for (int b = wb0; b < wb1; ++b) {
-    uint4 q = make_uint4(0, 0, 0, 0), d0 = make_uint4(0, 0, 0, 0), d1 = make_uint4(0, 0, 0, 0);
-    if (row_ok) q = *reinterpret_cast<const uint4 *>(wrow + static_cast<size_t>(b) * 144);
-    if (h0_ok) d0 = *reinterpret_cast<const uint4 *>(hrow0 + static_cast<size_t>(b) * 144);
-    if (h1_ok) d1 = *reinterpret_cast<const uint4 *>(hrow1 + static_cast<size_t>(b) * 144);
-    const long A0 = unpack_word(q.x), A1 = unpack_word(q.y), A2 = unpack_word(q.z),
-               A3 = unpack_word(q.w);
-    float ds[16];
-    {
-      const uint32_t hw[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-#pragma unroll
-      for (int j = 0; j < 16; ++j)
-        ds[j] = half_bits_to_float(static_cast<uint16_t>(hw[j >> 1] >> (16 * (j & 1))));
-    }
-#pragma unroll
-    for (int tt = 0; tt < TT; ++tt) {
-      const size_t ablk = (static_cast<size_t>(tg * TT + tt) * nb + b);
-      const long B = static_cast<long>(a.codes[ablk * 64 + lane]);
-      const ActParam p = a.params[ablk * 16 + c];
-      const v4i C = {p.corr, p.corr, p.corr, p.corr};
-      const v4i D0 = Q35_MFMA_I32_16X16X32_I8(A0, B, C, 0, 0, 0);
-      const v4i D1 = Q35_MFMA_I32_16X16X32_I8(A1, B, C, 0, 0, 0);
-      const v4i D2 = Q35_MFMA_I32_16X16X32_I8(A2, B, C, 0, 0, 0);
-      const v4i D3 = Q35_MFMA_I32_16X16X32_I8(A3, B, C, 0, 0, 0);
-      const v4i D[4] = {D0, D1, D2, D3};
+    for (int g = blockIdx.x; g < groups; g += gridDim.x) {
+      float acc[4][4];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int j = 4 * v + i;
-          acc[tt][j] = fmaf(static_cast<float>(D[i][v]), ds[j] * p.scale, acc[tt][j]);
+        for (int j = 0; j < 4; ++j) acc[i][j] = 0.0F;
+      // rows past the matrix read a valid tile (the last); their outputs are
+      // never stored
+      const int rt = min(g * 8 + T, ntiles - 1);
+      const uint8_t *qrow = wbase + static_cast<size_t>(rt) * nb * 144 + 16 + 16 * (2 * G + h);
+      const uint8_t *drow = wbase + static_cast<size_t>(rt) * nb * 144 + 8 * h;
+
+      for (int cb = b0; cb < b1; cb += kChunk) {
+        // all loads of the chunk first (indices clamped into the wave's
+        // range, so no load is predicated), then the MFMAs
+        q35_u32x4 q[kChunk];
+        q35_u32x2 d[kChunk];
+        long act[kChunk];
+#pragma unroll
+        for (int i = 0; i < kChunk; ++i) {
+          const size_t b = static_cast<size_t>(min(cb + i, b1 - 1));
+          q[i] = Q35_LOAD_NT(reinterpret_cast<const q35_u32x4 *>(qrow + b * 144));
+          d[i] = Q35_LOAD_NT(reinterpret_cast<const q35_u32x2 *>(drow + b * 144));
+          act[i] = static_cast<long>(acodes[b * 64]);
         }
-      if (a.block_dots != nullptr) {
-        const int tok = (tg * TT + tt) * 16 + c;
-        if (tok < a.tokens) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < kChunk; ++i) {
+          // a padded slot past the wave's range re-reads its last block; a
+          // zero row scale makes its contribution exactly +0 (acc is never -0)
+          const bool valid = cb + i < b1;
+          const int b = valid ? cb + i : b1 - 1;
+          if (!valid) d[i] = q35_u32x2{0u, 0u};
+          const v4i zero = {0, 0, 0, 0};
+          const v4i corr = Q35_MFMA_I32_16X16X32_I8(act[i], kMinus8, zero, 0, 0, 0);
+          v4i D[4];
+          D[0] = Q35_MFMA_I32_16X16X32_I8(act[i], unpack_word(q[i][0]), corr, 0, 0, 0);
+          D[1] = Q35_MFMA_I32_16X16X32_I8(act[i], unpack_word(q[i][1]), corr, 0, 0, 0);
+          D[2] = Q35_MFMA_I32_16X16X32_I8(act[i], unpack_word(q[i][2]), corr, 0, 0, 0);
+          D[3] = Q35_MFMA_I32_16X16X32_I8(act[i], unpack_word(q[i][3]), corr, 0, 0, 0);
+          const float *sp = act_scale + b * 16 + 4 * G;
+          const float sa[4] = {sp[0], sp[1], sp[2], sp[3]};
+          const float dw[4] = {half_bits_to_float(static_cast<uint16_t>(d[i][0] & 0xffffu)),
+                               half_bits_to_float(static_cast<uint16_t>(d[i][0] >> 16)),
+                               half_bits_to_float(static_cast<uint16_t>(d[i][1] & 0xffffu)),
+                               half_bits_to_float(static_cast<uint16_t>(d[i][1] >> 16))};
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-              const int row = rg * kRowsPerGroup + 16 * G + 4 * v + i;
-              if (row < a.rows)
-                a.block_dots[(static_cast<size_t>(tok) * a.rows + row) * nb + b] = D[i][v];
+          for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              acc[r][j] = fmaf(static_cast<float>(D[r][j]), dw[r] * sa[j], acc[r][j]);
+          if constexpr (DOTS) {
+            if (!valid) continue;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int tok = tt * 16 + 4 * G + j;
+              if (tok >= a.tokens) continue;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int row = g * kRowsPerGroup + 4 * c + r;
+                if (row < a.rows)
+                  a.block_dots[(static_cast<size_t>(tok) * a.rows + row) * nb + b] = D[r][j];
+              }
             }
-        }
-      }
-    }
-  }
-
-  // Workgroup reduction (waves in fixed order), then store / split-K / argmax.
-#pragma unroll
-  for (int tt = 0; tt < TT; ++tt) {
-#pragma unroll
-    for (int j = 0; j < 16; ++j) red[wave][c][16 * G + j] = acc[tt][j];
-    __syncthreads();
-    const int tok0 = (tg * TT + tt) * 16;
-    float sums[4];
-    int rows_[4], toks_[4];
-#pragma unroll
-    for (int e4 = 0; e4 < 4; ++e4) {
-      const int e = threadIdx.x + e4 * kGemmThreads;
-      const int tk = e >> 6, row = e & 63;
-      sums[e4] = ((red[0][tk][row] + red[1][tk][row]) + red[2][tk][row]) + red[3][tk][row];
-      rows_[e4] = rg * kRowsPerGroup + row;
-      toks_[e4] = tok0 + tk;
-    }
-    __syncthreads();
-    if (a.argmax_keys != nullptr) {
-      // Greedy head: penalty then per-token max key over this group's rows.
-#pragma unroll
-      for (int e4 = 0; e4 < 4; ++e4) {
-        const int tk = toks_[e4], row = rows_[e4];
-        unsigned long long key = 0ull;
-        if (tk < a.tokens && row < a.rows) {
-          float val = sums[e4];
-          const float pen = a.penalties != nullptr ? a.penalties[tk] : 1.0F;
-          if (pen > 1.0F && a.counts != nullptr) {
-            const long long crow = a.count_rows != nullptr ? a.count_rows[tk] : tk;
-            if (a.counts[crow * a.counts_stride + row] > 0) val = val > 0.0F ? val / pen : val * pen;
           }
-          key = argmax_key(val, static_cast<uint32_t>(row));
-        }
-        // threads of one wave share the token (e>>6 is wave-uniform per e4)
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) {
-          const unsigned long long o = __shfl_xor(key, m, 64);
-          key = o > key ? o : key;
-        }
-        if (lane == 0 && key != 0ull && tk < a.tokens) atomicMax(&a.argmax_keys[tk], key);
-      }
-      continue;
-    }
-    if (S == 1) {
-      // the block-dots parity entry runs without an FP32 output buffer
-      if (a.out == nullptr) continue;
-#pragma unroll
-      for (int e4 = 0; e4 < 4; ++e4) {
-        const int tk = toks_[e4], row = rows_[e4];
-        if (tk < a.tokens && row < a.rows) {
-          const size_t o = static_cast<size_t>(tk) * a.stride + row;
-          float val = sums[e4];
-          if (a.residual != nullptr) val = a.residual[o] + val;
-          a.out[o] = val;
         }
       }
-    } else {
-#pragma unroll
-      for (int e4 = 0; e4 < 4; ++e4) {
-        const int tk = toks_[e4], row = rows_[e4];
-        if (tk < a.tokens && row < a.rows)
-          a.partials[(static_cast<size_t>(split) * a.tokens + tk) * a.rows + row] = sums[e4];
-      }
-    }
-  }
-  (void)best;
-  if (a.argmax_keys != nullptr || S == 1) return;
 
-  // Split-K: the last workgroup of this (row group, token group) sums all
-  // splits in split order.
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned idx = static_cast<unsigned>(tg) * gridDim.x + rg;
-    const unsigned prev = atomicAdd(&a.counters[idx], 1u);
-    last_flag = (prev == static_cast<unsigned>(S - 1));
-    if (last_flag) a.counters[idx] = 0u;
-  }
-  __syncthreads();
-  if (!last_flag) return;
-  __threadfence();
-  const int tok_begin = tg * TT * 16;
-  const int tok_end = min(a.tokens, tok_begin + TT * 16);
-  const int row_begin = rg * kRowsPerGroup;
-  const int row_end = min(a.rows, row_begin + kRowsPerGroup);
-  const int nrow = row_end - row_begin;
-  for (int e = threadIdx.x; e < (tok_end - tok_begin) * kRowsPerGroup; e += kGemmThreads) {
-    const int tk = tok_begin + e / kRowsPerGroup, row = row_begin + e % kRowsPerGroup;
-    if (e % kRowsPerGroup >= nrow) continue;
-    float val = 0.0F;
-    for (int s = 0; s < S; ++s) {
-      val += a.partials[(static_cast<size_t>(s) * a.tokens + tk) * a.rows + row];
+      // Fixed-order sum of the wavefronts' partials, then the epilogue. The
+      // token range is reduced in passes of red_tokens tokens (16 or 8) to
+      // bound LDS.
+      for (int t0 = 0; t0 < 16; t0 += a.red_tokens) {
+        if (4 * G >= t0 && 4 * G < t0 + a.red_tokens) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            float *dst = red + (static_cast<size_t>(wave) * a.red_tokens + (4 * G + j - t0)) * 64 + 4 * c;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dst[r] = acc[r][j];
+          }
+        }
+        __syncthreads();
+        for (int e = threadIdx.x; e < a.red_tokens * 64; e += blockDim.x) {
+          const int t = e >> 6, r = e & 63;
+          float s = red[static_cast<size_t>(t) * 64 + r];
+          for (int w = 1; w < W; ++w) s += red[(static_cast<size_t>(w) * a.red_tokens + t) * 64 + r];
+          const int tok = tt * 16 + t0 + t, row = g * kRowsPerGroup + r;
+          if constexpr (!ARGMAX) {
+            if (tok < a.tokens && row < a.rows && a.out != nullptr) {
+              const size_t o = static_cast<size_t>(tok) * a.stride + row;
+              a.out[o] = a.residual != nullptr ? a.residual[o] + s : s;
+            }
+          } else {
+            // greedy head: repetition penalty, then the per-token best key of
+            // this group (all 64 lanes of a wave share t)
+            unsigned long long key = 0ull;
+            if (tok < a.tokens && row < a.rows) {
+              float val = s;
+              const float pen = a.penalties != nullptr ? a.penalties[tok] : 1.0F;
+              if (pen > 1.0F && a.counts != nullptr) {
+                const long long crow = a.count_rows != nullptr ? a.count_rows[tok] : tok;
+                if (a.counts[crow * a.counts_stride + row] > 0) val = val > 0.0F ? val / pen : val * pen;
+              }
+              key = argmax_key(val, static_cast<uint32_t>(row));
+            }
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) {
+              const unsigned long long o = __shfl_xor(key, m, 64);
+              key = o > key ? o : key;
+            }
+            if (lane == 0 && key > best[t0 + t]) best[t0 + t] = key;
+          }
+        }
+        __syncthreads();
+      }
     }
-    const size_t o = static_cast<size_t>(tk) * a.stride + row;
-    if (a.residual != nullptr) val = a.residual[o] + val;
-    a.out[o] = val;
+    if (ARGMAX) {
+      __syncthreads();
+      if (threadIdx.x < 16) {
+        const int tok = tt * 16 + threadIdx.x;
+        if (tok < a.tokens) a.cand[static_cast<size_t>(blockIdx.x) * a.cand_stride + tok] = best[threadIdx.x];
+      }
+    }
   }
 }
 
-__global__ void argmax_unpack_kernel(const unsigned long long *keys, int count, int32_t *index,
-                                     float *value) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= count) return;
-  const unsigned long long k = keys[i];
-  if (index != nullptr) index[i] = static_cast<int32_t>(argmax_key_index(k));
-  if (value != nullptr) value[i] = argmax_key_value(k);
+// One wavefront per token: the best key over all workgroups' candidates.
+__global__ __launch_bounds__(64) void argmax_finalize_kernel(const unsigned long long *cand, int ncand,
+                                                             int cand_stride, int tokens, int32_t *index,
+                                                             float *value) {
+  const int tok = blockIdx.x, lane = threadIdx.x;
+  if (tok >= tokens) return;
+  unsigned long long key = 0ull;
+  for (int i = lane; i < ncand; i += 64) {
+    const unsigned long long k = cand[static_cast<size_t>(i) * cand_stride + tok];
+    key = k > key ? k : key;
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const unsigned long long o = __shfl_xor(key, m, 64);
+    key = o > key ? o : key;
+  }
+  if (lane == 0) {
+    if (index != nullptr) index[tok] = static_cast<int32_t>(argmax_key_index(key));
+    if (value != nullptr) value[tok] = argmax_key_value(key);
+  }
+}
+
+struct GemmShape {
+  int waves, grid, red_tokens;
+  size_t smem;
+};
+
+GemmShape gemm_shape(const GemmArgs &a, int cu_count) {
+  GemmShape s{};
+  const int groups = (a.rows / 8 + 7) / 8;
+  s.waves = a.exact ? 1 : std::min(kMaxWaves, std::max(1, (a.nb + kChunk - 1) / kChunk));
+  const bool argmax = a.cand != nullptr;
+  const int cus = cu_count > 0 ? cu_count : 256;
+  s.grid = argmax ? std::min(groups, a.cand_capacity > 0 ? a.cand_capacity : 4 * cus) : groups;
+  s.red_tokens = 16;
+  auto bytes = [&](int red_tokens) {
+    return (static_cast<size_t>(a.nb) * 16 + static_cast<size_t>(s.waves) * red_tokens * 64) * 4 + 16 * 8;
+  };
+  s.smem = bytes(16);
+  if (s.smem > 65536) {
+    s.red_tokens = 8;
+    s.smem = bytes(8);
+  }
+  return s;
 }
 
 }  // namespace
 
-int gemm_choose_ksplit(int rows, int nb, int cu_count) {
-  const int groups = (rows + kRowsPerGroup - 1) / kRowsPerGroup;
-  const int target = cu_count > 0 ? cu_count : 256;
-  int s = 1;
-  // grow the split while the grid underfills the chip and every wave keeps
-  // at least two blocks
-  while (groups * s < target && nb / (s * 2) >= 8) s *= 2;
-  return s;
+int gemm_argmax_grid(int rows, int cu_count) {
+  const int groups = (rows / 8 + 7) / 8;
+  return std::min(groups, 4 * (cu_count > 0 ? cu_count : 256));
 }
 
-size_t gemm_partial_floats(int rows, int tokens, int ksplit) {
-  return ksplit > 1 ? static_cast<size_t>(ksplit) * tokens * rows : 0;
-}
-
-size_t gemm_counter_count(int rows, int tokens) {
-  const int groups = (rows + kRowsPerGroup - 1) / kRowsPerGroup;
-  const int tgroups = (tokens + 63) / 64 * 4;
-  return static_cast<size_t>(groups) * tgroups;
+bool gemm_shape_supported(int rows, int nb, bool exact) {
+  if (rows <= 0 || rows % 8 != 0 || nb <= 0) return false;
+  GemmArgs a;
+  a.rows = rows;
+  a.nb = nb;
+  a.exact = exact;
+  return gemm_shape(a, 256).smem <= 65536;
 }
 
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t stream) {
   if (a.tokens <= 0 || a.rows <= 0) return hipSuccess;
-  const int tiles = (a.tokens + 15) / 16;
-  const int groups = (a.rows + kRowsPerGroup - 1) / kRowsPerGroup;
-  int TT = tiles >= 4 ? 4 : (tiles >= 2 ? 2 : 1);
-  if (TT == 2 && tiles == 3) TT = 4;
-  const dim3 block(kGemmThreads);
-  const dim3 grid(groups, a.ksplit, (tiles + TT - 1) / TT);
-  switch (TT) {
-    case 1: Q35_LAUNCH((gemm_kernel<1>), grid, block, 0, stream, a); break;
-    case 2: Q35_LAUNCH((gemm_kernel<2>), grid, block, 0, stream, a); break;
-    default: Q35_LAUNCH((gemm_kernel<4>), grid, block, 0, stream, a); break;
+  const GemmShape s = gemm_shape(a, a.cu_count);
+  if (s.smem > 65536) return hipErrorInvalidValue;
+  GemmArgs b = a;
+  b.red_tokens = s.red_tokens;
+  if (a.cand != nullptr) {
+    Q35_LAUNCH((gemm_kernel<true, false>), dim3(s.grid), dim3(64 * s.waves), s.smem, stream, b);
+  } else if (a.block_dots != nullptr) {
+    Q35_LAUNCH((gemm_kernel<false, true>), dim3(s.grid), dim3(64 * s.waves), s.smem, stream, b);
+  } else {
+    Q35_LAUNCH((gemm_kernel<false, false>), dim3(s.grid), dim3(64 * s.waves), s.smem, stream, b);
   }
   return hipGetLastError();
 }
 
-hipError_t launch_argmax_unpack(const unsigned long long *keys, int count, int32_t *index,
-                                float *value, hipStream_t stream) {
-  Q35_LAUNCH((argmax_unpack_kernel), (count + 255) / 256, 256, 0, stream, keys, count, index, value);
+hipError_t launch_argmax_finalize(const unsigned long long *cand, int ncand, int cand_stride, int tokens,
+                                  int32_t *index, float *value, hipStream_t stream) {
+  Q35_LAUNCH((argmax_finalize_kernel), dim3(tokens), dim3(64), 0, stream, cand, ncand, cand_stride, tokens,
+             index, value);
   return hipGetLastError();
 }
 

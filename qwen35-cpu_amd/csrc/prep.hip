@@ -6,9 +6,10 @@
 //   signs + FWHT stage order 1,2,...,64     src/cpu/q4_h128.cpp:35-61
 //   absmax/127, unrounded 1/scale, round half away from zero, clamp +-127,
 //   stored scale = binary16(scale) * 1/sqrt(128)   q4_0.cpp:212-235, q4_h128.cpp:319-321
-// One workgroup (4 wavefronts) per token row; each wavefront owns whole
-// 128-column blocks, two values per lane, so the first six FWHT stages are
-// lane shuffles and the last one is in-lane.
+// One wavefront per (token, 128-column block), four per workgroup, so a
+// 16-token step spreads over 16 x K/128 wavefronts; two values per lane, the
+// first six FWHT stages are lane shuffles and the last one is in-lane. An
+// RMSNorm source recomputes its row's sum of squares in each wavefront.
 #include "q35_device.h"
 #include "q35_internal.h"
 
@@ -62,24 +63,23 @@ __device__ __forceinline__ float load_source(const PrepArgs &a, int t, int c, fl
 
 template <int SRC>
 __global__ __launch_bounds__(kPrepThreads) void prep_kernel(PrepArgs a) {
-  __shared__ float scratch[8];
-  const int t = blockIdx.x;
-  const int K = a.K, nb = K >> 5;
-  if (a.argmax_reset != nullptr && t == 0)
-    for (int i = threadIdx.x; i < a.argmax_reset_count; i += kPrepThreads) a.argmax_reset[i] = 0ull;
+  const int K = a.K, nb = K >> 5, nblk = K >> 7;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int item = blockIdx.x * (kPrepThreads / 64) + wave;
+  if (item >= a.tokens * nblk) return;  // whole wavefronts only; no workgroup barrier below
+  const int t = item / nblk, blk = item - t * nblk;
 
   float rms_inv = 1.0F;
   if constexpr (SRC == kPrepRmsNorm) {
     const float *row = a.x + static_cast<size_t>(t) * a.x_stride;
     float ss = 0.0F;
-    for (int i = threadIdx.x; i < K; i += kPrepThreads) ss += row[i] * row[i];
-    ss = block_sum<kPrepThreads / 64>(ss, scratch);
+    for (int i = lane; i < K; i += 64) ss += row[i] * row[i];
+    ss = group_sum<64>(ss);
     rms_inv = 1.0F / sqrtf(ss / static_cast<float>(K) + a.eps);
   }
 
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int tile = t >> 4, tok = t & 15;
-  for (int blk = wave; blk < (K >> 7); blk += kPrepThreads / 64) {
+  {
     const int c0 = blk * 128 + lane, c1 = c0 + 64;
     float v0 = load_source<SRC>(a, t, c0, rms_inv);
     float v1 = load_source<SRC>(a, t, c1, rms_inv);
@@ -186,7 +186,8 @@ __global__ void x1_to_a16_kernel(const q35_q8_0_block_x1 *x1, int nb, uint64_t *
 
 hipError_t launch_prep(const PrepArgs &a, hipStream_t stream) {
   if (a.tokens <= 0) return hipSuccess;
-  const dim3 grid(a.tokens), block(kPrepThreads);
+  const int items = a.tokens * (a.K >> 7);
+  const dim3 grid((items + kPrepThreads / 64 - 1) / (kPrepThreads / 64)), block(kPrepThreads);
   switch (a.source) {
     case kPrepPlain: Q35_LAUNCH((prep_kernel<kPrepPlain>), grid, block, 0, stream, a); break;
     case kPrepRmsNorm: Q35_LAUNCH((prep_kernel<kPrepRmsNorm>), grid, block, 0, stream, a); break;

@@ -16,4 +16,11 @@
 #define Q35_MFMA_I32_16X16X32_I8(a, b, c, cbsz, abid, blgp) \
   __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, cbsz, abid, blgp)
 #define Q35_DYNAMIC_SHARED(type, name) extern __shared__ type name[]
+// Streaming loads of data read once per step (weights, recurrent state, KV):
+// marked non-temporal so they do not displace reused lines in L1/L2.
+typedef unsigned int q35_u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int q35_u32x2 __attribute__((ext_vector_type(2)));
+typedef float q35_f32x4 __attribute__((ext_vector_type(4)));
+#define Q35_LOAD_NT(ptr) __builtin_nontemporal_load(ptr)
+#define Q35_STORE_NT(value, ptr) __builtin_nontemporal_store(value, ptr)
 #endif

@@ -86,9 +86,6 @@ struct PrepArgs {
   q35_q8_0_block_x4 *x4 = nullptr; // reference X4 layout (optional)
   q35_q8_0_block_x1 *x1 = nullptr; // reference X1 layout (optional)
   float *normed_out = nullptr;     // optional copy of y [tokens][K]
-  // optional: reset 64-bit argmax keys [count] (used before the head GEMM)
-  unsigned long long *argmax_reset = nullptr;
-  int argmax_reset_count = 0;
 };
 hipError_t launch_prep(const PrepArgs &a, hipStream_t stream);
 
@@ -101,31 +98,32 @@ hipError_t launch_x1_to_a16(const q35_q8_0_block_x1 *x1, int nb, uint64_t *codes
 struct GemmArgs {
   const q35_q4_0_block_x8 *w = nullptr;
   int rows = 0, nb = 0;            // rows % 8 == 0
-  const uint64_t *codes = nullptr; // A16
-  const ActParam *params = nullptr;
-  int tokens = 0;                  // valid tokens (<= kMaxTokens)
+  const uint64_t *codes = nullptr; // A16 [token_tile][nb][64]
+  const ActParam *params = nullptr;// [token_tile][nb][16]
+  int tokens = 0;                  // valid tokens
   float *out = nullptr;            // [tokens][stride]
   int stride = 0;
   const float *residual = nullptr; // optional, added in the epilogue, [tokens][stride]
   int32_t *block_dots = nullptr;   // parity hook: [tokens][rows][nb]
-  bool exact = false;              // one wave per row group runs all blocks (ksplit must be 1)
-  // greedy head mode: fused penalty + argmax into 64-bit keys per token
-  unsigned long long *argmax_keys = nullptr;
-  const int32_t *counts = nullptr;  // [tokens][counts_stride]
+  bool exact = false;              // one wavefront per row group runs all blocks
+  // greedy head mode: per-workgroup best (penalised value, lowest index) keys
+  unsigned long long *cand = nullptr;  // [grid][cand_stride]
+  int cand_stride = 0;
+  int cand_capacity = 0;           // workgroups the cand buffer holds (0 = default grid)
+  const int32_t *counts = nullptr;  // [rows of counts][counts_stride]
   const int32_t *count_rows = nullptr; // optional per-token row index into counts
   long long counts_stride = 0;
   const float *penalties = nullptr;
-  // split-K scratch (owned by the caller)
-  int ksplit = 1;
-  float *partials = nullptr;       // [ksplit][tokens][rows]
-  unsigned *counters = nullptr;    // [row_groups * token_groups], zero-initialised
+  int cu_count = 0;
+  int red_tokens = 16;             // set by the launcher
 };
-int gemm_choose_ksplit(int rows, int nb, int cu_count);
-size_t gemm_partial_floats(int rows, int tokens, int ksplit);
-size_t gemm_counter_count(int rows, int tokens);
+// Workgroups of the greedy head launch (= candidate rows per token).
+int gemm_argmax_grid(int rows, int cu_count);
+// Whether launch_gemm handles this matrix shape (LDS bound).
+bool gemm_shape_supported(int rows, int nb, bool exact);
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t stream);
-hipError_t launch_argmax_unpack(const unsigned long long *keys, int count, int32_t *index,
-                                float *value, hipStream_t stream);
+hipError_t launch_argmax_finalize(const unsigned long long *cand, int ncand, int cand_stride, int tokens,
+                                  int32_t *index, float *value, hipStream_t stream);
 
 // DeltaNet
 struct DeltaArgs {

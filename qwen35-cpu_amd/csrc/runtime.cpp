@@ -241,37 +241,32 @@ extern "C" int q35_q4_h128_prepare_activations_4(q35_context *ctx, const float *
 // ================================================================ DOT4 GEMM
 namespace {
 // Runs the GEMM over `vectors` tokens (chunks of kMaxTokens) from X4 or X1
-// activations. `exact` forces the single-wave fma chain per row.
+// activations. `exact` forces the single-wave fma chain per row. With `index`
+// set it runs the greedy head instead (penalty + argmax per vector).
 int matmul_entry(q35_context *ctx, const q35_q4_0_block_x8 *m, const q35_q8_0_block_x4 *x4,
                  const q35_q8_0_block_x1 *x1, float *out, int32_t *dots, size_t rows,
-                 size_t vectors, size_t blocks, size_t stride, bool exact,
-                 unsigned long long *keys, const int32_t *counts, const float *penalties) {
+                 size_t vectors, size_t blocks, size_t stride, bool exact, int32_t *index,
+                 float *value, const int32_t *counts, const float *penalties) {
   if (ctx == nullptr || m == nullptr || (x4 == nullptr && x1 == nullptr) ||
-      (out == nullptr && dots == nullptr && keys == nullptr))
+      (out == nullptr && dots == nullptr && index == nullptr))
     return Q35_ERR_INVALID;
-  // split-K partial sums need an FP32 destination
-  if (out == nullptr && !exact && keys == nullptr && dots == nullptr) return Q35_ERR_INVALID;
   if (rows == 0 || rows % 8 != 0 || blocks == 0 || vectors == 0 || rows > (1u << 28) ||
       blocks > (1u << 16) || (out != nullptr && stride < rows))
     return set_error(ctx, Q35_ERR_INVALID, "invalid DOT4 geometry");
   const int nb = static_cast<int>(blocks);
+  if (!gemm_shape_supported(static_cast<int>(rows), nb, exact))
+    return set_error(ctx, Q35_ERR_UNSUPPORTED, "DOT4 block count beyond the kernel's LDS budget");
   const size_t chunk = kMaxTokens;
   const size_t code_bytes = align256(4 * 64 * static_cast<size_t>(nb) * sizeof(uint64_t));
   const size_t param_bytes = align256(4 * 16 * static_cast<size_t>(nb) * sizeof(ActParam));
-  const int ksplit = (exact || dots != nullptr || keys != nullptr)
-                         ? 1
-                         : gemm_choose_ksplit(static_cast<int>(rows), nb, ctx->cu_count);
-  const size_t part_bytes = align256(gemm_partial_floats(static_cast<int>(rows), kMaxTokens, ksplit) * 4);
-  const size_t cnt_bytes = align256(gemm_counter_count(static_cast<int>(rows), kMaxTokens) * 4);
+  const int grid = gemm_argmax_grid(static_cast<int>(rows), ctx->cu_count);
+  const size_t cand_bytes = index != nullptr ? align256(static_cast<size_t>(grid) * kMaxTokens * 8) : 0;
   void *scratch = nullptr;
-  int st = scratch_get(ctx, code_bytes + param_bytes + part_bytes + cnt_bytes, &scratch);
+  int st = scratch_get(ctx, code_bytes + param_bytes + cand_bytes, &scratch);
   if (st != Q35_OK) return st;
   auto *codes = reinterpret_cast<uint64_t *>(scratch);
   auto *params = reinterpret_cast<ActParam *>(static_cast<char *>(scratch) + code_bytes);
-  auto *partials = reinterpret_cast<float *>(static_cast<char *>(scratch) + code_bytes + param_bytes);
-  auto *counters =
-      reinterpret_cast<unsigned *>(static_cast<char *>(scratch) + code_bytes + param_bytes + part_bytes);
-  if (ksplit > 1) Q35_HIP_TRY(ctx, hipMemsetAsync(counters, 0, cnt_bytes, ctx->stream));
+  auto *cand = reinterpret_cast<unsigned long long *>(static_cast<char *>(scratch) + code_bytes + param_bytes);
   for (size_t t0 = 0; t0 < vectors; t0 += chunk) {
     const size_t n = std::min(chunk, vectors - t0);
     hipError_t e;
@@ -291,15 +286,22 @@ int matmul_entry(q35_context *ctx, const q35_q4_0_block_x8 *m, const q35_q8_0_bl
     g.stride = static_cast<int>(stride);
     g.block_dots = dots ? dots + t0 * rows * blocks : nullptr;
     g.exact = exact;
-    g.argmax_keys = keys ? keys + t0 : nullptr;
-    g.counts = counts ? counts + t0 * rows : nullptr;
-    g.counts_stride = static_cast<long long>(rows);
-    g.penalties = penalties ? penalties + t0 : nullptr;
-    g.ksplit = ksplit;
-    g.partials = partials;
-    g.counters = counters;
+    g.cu_count = ctx->cu_count;
+    if (index != nullptr) {
+      g.cand = cand;
+      g.cand_stride = kMaxTokens;
+      g.cand_capacity = grid;
+      g.counts = counts ? counts + t0 * rows : nullptr;
+      g.counts_stride = static_cast<long long>(rows);
+      g.penalties = penalties ? penalties + t0 : nullptr;
+    }
     e = launch_gemm(g, ctx->stream);
     if (e != hipSuccess) return hip_error(ctx, e, "DOT4 GEMM kernel");
+    if (index != nullptr) {
+      e = launch_argmax_finalize(cand, grid, kMaxTokens, static_cast<int>(n), index + t0,
+                                 value ? value + t0 : nullptr, ctx->stream);
+      if (e != hipSuccess) return hip_error(ctx, e, "argmax finalize");
+    }
   }
   return Q35_OK;
 }
@@ -309,14 +311,14 @@ extern "C" int q35_q4_dot4_matvec(q35_context *ctx, const q35_q4_0_block_x8 *mat
                                   const q35_q8_0_block_x1 *vector, float *output, size_t rows,
                                   size_t blocks) {
   return matmul_entry(ctx, matrix, nullptr, vector, output, nullptr, rows, 1, blocks, rows, false,
-                      nullptr, nullptr, nullptr);
+                      nullptr, nullptr, nullptr, nullptr);
 }
 extern "C" int q35_q4_dot4_matmul(q35_context *ctx, const q35_q4_0_block_x8 *matrix,
                                   const q35_q8_0_block_x4 *vectors, float *output, size_t rows,
                                   size_t count, size_t blocks, size_t stride) {
   if (count % 4 != 0) return set_error(ctx, Q35_ERR_INVALID, "vector_count % 4 != 0");
   return matmul_entry(ctx, matrix, vectors, nullptr, output, nullptr, rows, count, blocks, stride,
-                      false, nullptr, nullptr, nullptr);
+                      false, nullptr, nullptr, nullptr, nullptr);
 }
 // Bit-exact FP32 variant (no public declaration in the reference; used by the parity tests).
 extern "C" int q35_q4_dot4_matmul_exact(q35_context *ctx, const q35_q4_0_block_x8 *matrix,
@@ -324,14 +326,14 @@ extern "C" int q35_q4_dot4_matmul_exact(q35_context *ctx, const q35_q4_0_block_x
                                         size_t rows, size_t count, size_t blocks, size_t stride) {
   if (count % 4 != 0) return set_error(ctx, Q35_ERR_INVALID, "vector_count % 4 != 0");
   return matmul_entry(ctx, matrix, vectors, nullptr, output, nullptr, rows, count, blocks, stride,
-                      true, nullptr, nullptr, nullptr);
+                      true, nullptr, nullptr, nullptr, nullptr);
 }
 extern "C" int q35_q4_dot4_block_dots(q35_context *ctx, const q35_q4_0_block_x8 *matrix,
                                       const q35_q8_0_block_x4 *vectors, int32_t *output,
                                       size_t rows, size_t count, size_t blocks) {
   if (count % 4 != 0) return set_error(ctx, Q35_ERR_INVALID, "vector_count % 4 != 0");
   return matmul_entry(ctx, matrix, vectors, nullptr, nullptr, output, rows, count, blocks, rows,
-                      true, nullptr, nullptr, nullptr);
+                      true, nullptr, nullptr, nullptr, nullptr);
 }
 extern "C" int q35_q4_dot4_argmax_batch(q35_context *ctx, const q35_q4_0_block_x8 *matrix,
                                         const q35_q8_0_block_x4 *vectors, const int32_t *counts,
@@ -339,17 +341,8 @@ extern "C" int q35_q4_dot4_argmax_batch(q35_context *ctx, const q35_q4_0_block_x
                                         size_t blocks, int32_t *out_index, float *out_value) {
   if (ctx == nullptr || out_index == nullptr) return Q35_ERR_INVALID;
   if (count % 4 != 0 || count == 0) return set_error(ctx, Q35_ERR_INVALID, "vector_count % 4 != 0");
-  unsigned long long *keys = nullptr;
-  Q35_HIP_TRY(ctx, hipMallocAsync(reinterpret_cast<void **>(&keys), count * 8, ctx->stream));
-  Q35_HIP_TRY(ctx, hipMemsetAsync(keys, 0, count * 8, ctx->stream));
-  int st = matmul_entry(ctx, matrix, vectors, nullptr, nullptr, nullptr, rows, count, blocks, rows,
-                        false, keys, counts, penalties);
-  if (st == Q35_OK) {
-    hipError_t e = launch_argmax_unpack(keys, static_cast<int>(count), out_index, out_value, ctx->stream);
-    if (e != hipSuccess) st = hip_error(ctx, e, "argmax unpack");
-  }
-  (void)hipFreeAsync(keys, ctx->stream);
-  return st;
+  return matmul_entry(ctx, matrix, vectors, nullptr, nullptr, nullptr, rows, count, blocks, rows, false,
+                      out_index, out_value, counts, penalties);
 }
 
 // ================================================================= DeltaNet

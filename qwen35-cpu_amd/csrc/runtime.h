@@ -62,12 +62,13 @@ struct q35_runtime {
   float *rope_cos = nullptr, *rope_sin = nullptr;
   // work buffers
   float *x = nullptr, *proj = nullptr, *core = nullptr, *q_rot = nullptr, *gates = nullptr;
-  float *part_o = nullptr, *part_ml = nullptr, *partials = nullptr, *logits = nullptr;
+  float *part_o = nullptr, *part_ml = nullptr, *logits = nullptr;
   float *hidden_out = nullptr;
   uint64_t *codes = nullptr;
   q35::ActParam *params = nullptr;
-  unsigned *counters = nullptr;
-  unsigned long long *argmax_keys = nullptr;
+  // greedy head: per-workgroup best keys [cand_rows][kMaxTokens]
+  unsigned long long *cand = nullptr;
+  int cand_rows = 0;
   int32_t *tokens_out_dev = nullptr;
   // step metadata (pinned host + device copy)
   size_t meta_bytes = 0;

@@ -338,22 +338,8 @@ extern "C" int q35_runtime_create(q35_model *m, const q35_runtime_config *cfg, q
   const size_t kmax = std::max({H, I, rt->core_width});
   alloc(4 * 64 * (kmax / 32) * 8, reinterpret_cast<void **>(&rt->codes));
   alloc(4 * 16 * (kmax / 32) * sizeof(ActParam), reinterpret_cast<void **>(&rt->params));
-  size_t part_floats = 0, counter_n = 0;
-  auto consider = [&](int rows, int nb) {
-    const int s = gemm_choose_ksplit(rows, nb, ctx->cu_count);
-    part_floats = std::max(part_floats, gemm_partial_floats(rows, kMaxTokens, s));
-    counter_n = std::max(counter_n, gemm_counter_count(rows, kMaxTokens));
-  };
-  for (const auto &L : m->layers) {
-    consider(L.in_rows, d.hidden / 32);
-    consider(d.hidden, L.out_cols / 32);
-    consider(2 * d.intermediate, d.hidden / 32);
-    consider(d.hidden, d.intermediate / 32);
-  }
-  consider(d.vocab, d.hidden / 32);
-  alloc(std::max<size_t>(part_floats, 1) * 4, reinterpret_cast<void **>(&rt->partials));
-  alloc(counter_n * 4, reinterpret_cast<void **>(&rt->counters));
-  alloc(kMaxTokens * 8, reinterpret_cast<void **>(&rt->argmax_keys));
+  rt->cand_rows = gemm_argmax_grid(d.vocab, ctx->cu_count);
+  alloc(static_cast<size_t>(rt->cand_rows) * kMaxTokens * 8, reinterpret_cast<void **>(&rt->cand));
   alloc(kMaxTokens * 4, reinterpret_cast<void **>(&rt->tokens_out_dev));
   const MetaLayout ml = meta_layout(B, rt->max_pages_per_row);
   rt->meta_bytes = ml.total;
@@ -374,7 +360,6 @@ extern "C" int q35_runtime_create(q35_model *m, const q35_runtime_config *cfg, q
       }
     if (hipMemcpy(rt->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(rt->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemset(rt->counters, 0, counter_n * 4) != hipSuccess ||
         hipMemset(rt->k_pool, 0, std::max<size_t>(1, m->n_full) * rt->layer_pool_elems * 2) != hipSuccess ||
         hipMemset(rt->v_pool, 0, std::max<size_t>(1, m->n_full) * rt->layer_pool_elems * 2) != hipSuccess)
       st = set_error(ctx, Q35_ERR_HIP, "runtime initialisation copies");
@@ -605,9 +590,7 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
     g.out = out;
     g.stride = stride;
     g.residual = residual;
-    g.ksplit = gemm_choose_ksplit(rows, K / 32, ctx->cu_count);
-    g.partials = rt->partials;
-    g.counters = rt->counters;
+    g.cu_count = ctx->cu_count;
     return launch_gemm(g, s);
   };
 
@@ -725,8 +708,6 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
   }
   PrepArgs fin = prep(kPrepRmsNorm, rt->x, H, m->final_norm, H, false);
   fin.normed_out = rt->hidden_out;
-  fin.argmax_reset = rt->argmax_keys;
-  fin.argmax_reset_count = batch;
   Q35_KERNEL(Q35_KERNEL_PREP, prep_bytes(H, H) + H * 4.0 + B * H * 4.0, launch_prep(fin, s), "final norm prep");
   if (want_logits) {
     Q35_KERNEL(Q35_KERNEL_GEMM, gemm_algorithmic_bytes(d.vocab, H / 32, batch, true, false),
@@ -739,16 +720,19 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
     g.codes = rt->codes;
     g.params = rt->params;
     g.tokens = batch;
-    g.argmax_keys = rt->argmax_keys;
+    g.cand = rt->cand;
+    g.cand_stride = kMaxTokens;
+    g.cand_capacity = rt->cand_rows;
     g.counts = rt->counts;
     g.count_rows = slots;
     g.counts_stride = d.vocab;
     g.penalties = penalties;
-    g.ksplit = 1;
+    g.cu_count = ctx->cu_count;
     Q35_KERNEL(Q35_KERNEL_GEMM, gemm_algorithmic_bytes(d.vocab, H / 32, batch, false, false), launch_gemm(g, s),
                "greedy head");
-    Q35_KERNEL(Q35_KERNEL_ARGMAX, B * 12.0,
-               launch_argmax_unpack(rt->argmax_keys, batch, rt->tokens_out_dev, nullptr, s), "argmax unpack");
+    Q35_KERNEL(Q35_KERNEL_ARGMAX, rt->cand_rows * B * 8.0 + B * 4.0,
+               launch_argmax_finalize(rt->cand, rt->cand_rows, kMaxTokens, batch, rt->tokens_out_dev, nullptr, s),
+               "argmax finalize");
     Q35_STEP(hipMemcpyAsync(rt->tokens_out_host, rt->tokens_out_dev, batch * 4, hipMemcpyDeviceToHost, s),
              "token copy");
   }

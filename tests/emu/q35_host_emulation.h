@@ -220,6 +220,11 @@ inline q35emu_v4i q35emu_mfma_i8(long a, long b, q35emu_v4i c) {
   return d;
 }
 #define Q35_MFMA_I32_16X16X32_I8(a, b, c, cbsz, abid, blgp) q35emu_mfma_i8(a, b, c)
+typedef unsigned int q35_u32x4 __attribute__((vector_size(16)));
+typedef unsigned int q35_u32x2 __attribute__((vector_size(8)));
+typedef float q35_f32x4 __attribute__((vector_size(16)));
+#define Q35_LOAD_NT(ptr) (*(ptr))
+#define Q35_STORE_NT(value, ptr) (*(ptr) = (value))
 #define Q35_DYNAMIC_SHARED(type, name) \
   type *name = reinterpret_cast<type *>(::q35emu::t_ctx.launch->dynamic_smem.data())
 #define Q35_LAUNCH(kernel, grid, block, smem, stream, ...) \
