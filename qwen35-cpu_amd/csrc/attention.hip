@@ -4,15 +4,12 @@
 //   per-head RMSNorm with (1 + w) (weights.inl:1517-1527), split-half RoPE on the
 //   first rope_dim dims (activation.cpp:124-162), and the FP16 round-to-nearest
 //   KV append of normalised K and raw V (full_attention.cpp:18-46, kv_pages.h:40-69).
-// attention: split-K flash-decoding. One workgroup per (split of 256 context
-//   tokens, KV head, request) serves all query heads of the GQA group, so each
-//   K/V byte is read once. It walks the request's page table, scores with FP32
-//   math over FP16 keys (full_attention.cpp:82-93), keeps the split's ungated
-//   partial (max, sum, sum p*V); the splits are merged in order with the
-//   reference rule merge_attention_partial (full_attention_tiled.cpp:66-78),
-//   then normalised and multiplied by sigmoid(gate).
-#include "q35_device.h"
-#include "q35_internal.h"
+// attention: split-K flash-decoding over chunks of 64 context tokens (one
+//   workgroup per chunk, KV head and request; see attention_kernel), then
+//   attention_merge_kernel: log-sum-exp merge of the chunks, normalisation and
+//   sigmoid(gate), written as FP32 or prepared as the o projection's A16
+//   activations.
+#include "q35_quant.h"
 
 namespace q35 {
 namespace {
@@ -71,150 +68,202 @@ __global__ __launch_bounds__(kAttnThreads) void attn_prep_kernel(AttnPrepArgs a)
   }
 }
 
-__device__ __forceinline__ void load_half16(const uint16_t *p, float out[16]) {
-  const uint4 u0 = reinterpret_cast<const uint4 *>(p)[0];
-  const uint4 u1 = reinterpret_cast<const uint4 *>(p)[1];
-  const uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    out[2 * i] = half_bits_to_float(static_cast<uint16_t>(w[i] & 0xffffu));
-    out[2 * i + 1] = half_bits_to_float(static_cast<uint16_t>(w[i] >> 16));
-  }
-}
+// ---------------------------------------------------------------- attention
+// One workgroup per (chunk of kChunkTokens context tokens, KV head, request)
+// serves the QPK query heads of the GQA group, so every K/V byte is read
+// once. Thread t scores token t/4 over dims 64*(t%4)..+63 (eight 16-byte K
+// loads) and accumulates P*V for dims 4*(t%64)..+3 over tokens t/64 + 4j
+// (sixteen 8-byte V loads); all 24 loads are issued right after the page
+// table lookup. Scores are FP32 dot products over FP16 keys
+// (full_attention.cpp:82-93); the chunk leaves its partial (max, sum,
+// sum p*V) for the merge.
+constexpr int kChunkTokens = 64;
+constexpr int kQStride = 68;  // 64 dims + 4: the four dim-quarters land on distinct LDS banks
 
-// GQA group size QPK (query heads per KV head) is a template parameter.
 template <int QPK>
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
-  Q35_DYNAMIC_SHARED(float, smem);  // scores [QPK][split_tokens], then reduction
+  __shared__ float qs[QPK * 4 * kQStride];
+  __shared__ float probs[QPK][kChunkTokens];
+  __shared__ float s_m[QPK], s_l[QPK];
+  __shared__ float red[4][QPK][kHeadDim];
   const int sp = blockIdx.x, g = blockIdx.y, r = blockIdx.z;
   const int seq = a.seq_lens != nullptr ? a.seq_lens[r] : a.positions[r] + 1;
-  const int t0 = sp * a.split_tokens;
-  if (t0 >= seq) return;
-  const int t1 = min(seq, t0 + a.split_tokens);
-  const int n = t1 - t0;
+  const int t0 = sp * kChunkTokens;
+  if (t0 >= seq) return;  // whole workgroup
+  const int n = min(seq - t0, kChunkTokens);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int kvw = a.kv_heads * kHeadDim;
   const int32_t *pt = a.page_table + static_cast<size_t>(r) * a.max_pages;
-  float *scores = smem;  // [QPK][split_tokens]
 
-  // ---- QK: 16 lanes per token, 16 dims per lane, four tokens per wave step
-  const int sub = lane & 15, tslot = lane >> 4;
-  float qv[QPK][16];
+  // K: token ti = tid/4 (clamped into the chunk), dims 64*qq .. +63
+  const int qq = tid & 3, ti = min(tid >> 2, n - 1);
+  const int ktok = t0 + ti;
+  const int kpage = pt[ktok / a.page_tokens];
+  const q35_u32x4 *krow = reinterpret_cast<const q35_u32x4 *>(
+      a.k_pool + (static_cast<size_t>(kpage) * a.page_tokens + ktok % a.page_tokens) * kvw +
+      static_cast<size_t>(g) * kHeadDim + 64 * qq);
+  // V: tokens wave + 4j (clamped), dims 4*lane .. +3
+  q35_u32x2 vraw[16];
+  q35_u32x4 kraw[8];
 #pragma unroll
-  for (int u = 0; u < QPK; ++u) {
-    const float *qh = a.q + (static_cast<size_t>(r) * a.heads + g * QPK + u) * kHeadDim + 16 * sub;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) qv[u][i] = qh[i];
+  for (int j = 0; j < 16; ++j) {
+    const int vt = t0 + min(wave + 4 * j, n - 1);
+    const int vpage = pt[vt / a.page_tokens];
+    vraw[j] = Q35_LOAD_NT(reinterpret_cast<const q35_u32x2 *>(
+        a.v_pool + (static_cast<size_t>(vpage) * a.page_tokens + vt % a.page_tokens) * kvw +
+        static_cast<size_t>(g) * kHeadDim + 4 * lane));
   }
-  for (int base = wave * 4; base < n; base += 16) {
-    const int i = base + tslot;
-    float part[QPK];
 #pragma unroll
-    for (int u = 0; u < QPK; ++u) part[u] = 0.0F;
-    if (i < n) {
-      const int tok = t0 + i;
-      const int page = pt[tok / a.page_tokens];
-      const uint16_t *krow =
-          a.k_pool + (static_cast<size_t>(page) * a.page_tokens + tok % a.page_tokens) * kvw +
-          static_cast<size_t>(g) * kHeadDim + 16 * sub;
-      float kf[16];
-      load_half16(krow, kf);
+  for (int i = 0; i < 8; ++i) kraw[i] = Q35_LOAD_NT(krow + i);
+
+  // the group's query heads into LDS, quarter-padded
+  for (int e = tid; e < QPK * kHeadDim; e += kAttnThreads) {
+    const int u = e / kHeadDim, d = e % kHeadDim;
+    qs[(u * 4 + d / 64) * kQStride + d % 64] =
+        a.q[(static_cast<size_t>(r) * a.heads + g * QPK + u) * kHeadDim + d];
+  }
+  __syncthreads();
+
+  // ---- scores
+  float part[QPK];
 #pragma unroll
-      for (int u = 0; u < QPK; ++u)
+  for (int u = 0; u < QPK; ++u) part[u] = 0.0F;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) part[u] += qv[u][e] * kf[e];
+  for (int i = 0; i < 8; ++i) {
+    float kf[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      kf[2 * e] = half_bits_to_float(static_cast<uint16_t>(kraw[i][e] & 0xffffu));
+      kf[2 * e + 1] = half_bits_to_float(static_cast<uint16_t>(kraw[i][e] >> 16));
     }
 #pragma unroll
     for (int u = 0; u < QPK; ++u) {
-      const float s = group_sum<16>(part[u]);
-      if (sub == 0 && i < n) scores[u * a.split_tokens + i] = s * a.scale;
+      const float *qp = qs + (u * 4 + qq) * kQStride + 8 * i;
+      const q35_f32x4 qa = *reinterpret_cast<const q35_f32x4 *>(qp);
+      const q35_f32x4 qb = *reinterpret_cast<const q35_f32x4 *>(qp + 4);
+      part[u] += qa[0] * kf[0] + qa[1] * kf[1] + qa[2] * kf[2] + qa[3] * kf[3] + qb[0] * kf[4] +
+                 qb[1] * kf[5] + qb[2] * kf[6] + qb[3] * kf[7];
     }
+  }
+#pragma unroll
+  for (int u = 0; u < QPK; ++u) {
+    part[u] += q35_quad_xor1(part[u]);
+    part[u] += q35_quad_xor2(part[u]);
+    if (qq == 0) probs[u][tid >> 2] = (tid >> 2) < n ? part[u] * a.scale : -INFINITY;
   }
   __syncthreads();
 
-  // ---- softmax statistics per query head (wave u owns head u, u += 4)
-  __shared__ float s_max[kMaxGroup], s_sum[kMaxGroup];
+  // ---- chunk softmax statistics (wave u handles head u, u += 4)
   for (int u = wave; u < QPK; u += kAttnThreads / 64) {
-    float m = -INFINITY;
-    for (int i = lane; i < n; i += 64) m = fmaxf(m, scores[u * a.split_tokens + i]);
-    m = group_max<64>(m);
-    float l = 0.0F;
-    for (int i = lane; i < n; i += 64) {
-      const float p = expf(scores[u * a.split_tokens + i] - m);
-      scores[u * a.split_tokens + i] = p;
-      l += p;
-    }
-    l = group_sum<64>(l);
+    const float s = probs[u][lane];
+    const float m = group_max<64>(s);
+    const float p = lane < n ? expf(s - m) : 0.0F;
+    const float l = group_sum<64>(p);
+    probs[u][lane] = p;
     if (lane == 0) {
-      s_max[u] = m;
-      s_sum[u] = l;
+      s_m[u] = m;
+      s_l[u] = l;
     }
   }
   __syncthreads();
 
-  // ---- PV: lane owns 4 dims, waves split the tokens
+  // ---- P*V over this wave's tokens, then the fixed-order wave sum
   float acc[QPK][4];
 #pragma unroll
   for (int u = 0; u < QPK; ++u) acc[u][0] = acc[u][1] = acc[u][2] = acc[u][3] = 0.0F;
-  for (int i = wave; i < n; i += kAttnThreads / 64) {
-    const int tok = t0 + i;
-    const int page = pt[tok / a.page_tokens];
-    const uint16_t *vrow =
-        a.v_pool + (static_cast<size_t>(page) * a.page_tokens + tok % a.page_tokens) * kvw +
-        static_cast<size_t>(g) * kHeadDim + 4 * lane;
-    const uint2 raw = *reinterpret_cast<const uint2 *>(vrow);
-    const float v0 = half_bits_to_float(raw.x & 0xffffu), v1 = half_bits_to_float(raw.x >> 16);
-    const float v2 = half_bits_to_float(raw.y & 0xffffu), v3 = half_bits_to_float(raw.y >> 16);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int i = wave + 4 * j;
+    const float v0 = half_bits_to_float(static_cast<uint16_t>(vraw[j][0] & 0xffffu));
+    const float v1 = half_bits_to_float(static_cast<uint16_t>(vraw[j][0] >> 16));
+    const float v2 = half_bits_to_float(static_cast<uint16_t>(vraw[j][1] & 0xffffu));
+    const float v3 = half_bits_to_float(static_cast<uint16_t>(vraw[j][1] >> 16));
 #pragma unroll
     for (int u = 0; u < QPK; ++u) {
-      const float p = scores[u * a.split_tokens + i];
-      acc[u][0] += p * v0; acc[u][1] += p * v1; acc[u][2] += p * v2; acc[u][3] += p * v3;
+      const float p = probs[u][i];  // 0 past the chunk's tokens
+      acc[u][0] += p * v0;
+      acc[u][1] += p * v1;
+      acc[u][2] += p * v2;
+      acc[u][3] += p * v3;
     }
   }
-  __syncthreads();  // scores no longer needed: reuse smem for the wave reduction
-  float *red = smem;  // [4 waves][QPK][256]
 #pragma unroll
   for (int u = 0; u < QPK; ++u)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) red[(wave * QPK + u) * kHeadDim + 4 * lane + e] = acc[u][e];
+    *reinterpret_cast<q35_f32x4 *>(&red[wave][u][4 * lane]) = q35_f32x4{acc[u][0], acc[u][1], acc[u][2], acc[u][3]};
   __syncthreads();
-  for (int idx = tid; idx < QPK * kHeadDim; idx += kAttnThreads) {
-    const int u = idx / kHeadDim, dd = idx % kHeadDim;
-    float v = 0.0F;
-#pragma unroll
-    for (int w = 0; w < kAttnThreads / 64; ++w) v += red[(w * QPK + u) * kHeadDim + dd];
+  for (int e = tid; e < QPK * kHeadDim; e += kAttnThreads) {
+    const int u = e / kHeadDim, d = e % kHeadDim;
+    const float v = ((red[0][u][d] + red[1][u][d]) + red[2][u][d]) + red[3][u][d];
     const size_t hs = (static_cast<size_t>(r) * a.heads + g * QPK + u) * a.max_splits + sp;
-    a.part_o[hs * kHeadDim + dd] = v;
-    if (dd == 0) {
-      a.part_ml[hs * 2] = s_max[u];
-      a.part_ml[hs * 2 + 1] = s_sum[u];
+    a.part_o[hs * kHeadDim + d] = v;
+    if (d == 0) {
+      a.part_ml[hs * 2] = s_m[u];
+      a.part_ml[hs * 2 + 1] = s_l[u];
     }
   }
 }
 
-__global__ void attention_merge_kernel(AttnArgs a, const float *gates, float *out) {
-  const int h = blockIdx.x, r = blockIdx.y, d = threadIdx.x;
+// Merge of the chunk partials of one (request, head): log-sum-exp weights
+// exp(m_s - M) over all chunks (the same result as merging them pairwise with
+// merge_attention_partial, full_attention_tiled.cpp:66-78, up to rounding),
+// normalisation, and the sigmoid output gate (full_attention.cpp:104-127).
+// Wavefront b handles dims 128b + lane and 128b + 64 + lane -- one H128
+// block of the o projection's input -- and either stores the FP32 result or
+// prepares it as A16 activations.
+__global__ __launch_bounds__(128) void attention_merge_kernel(AttnArgs a, const float *gates, float *out,
+                                                             QuantOut qo, uint64_t seed) {
+  __shared__ float w_s[2][64];
+  const int h = blockIdx.x, r = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int seq = a.seq_lens != nullptr ? a.seq_lens[r] : a.positions[r] + 1;
-  const int splits = (seq + a.split_tokens - 1) / a.split_tokens;
+  const int splits = (seq + kChunkTokens - 1) / kChunkTokens;
   const size_t hs = (static_cast<size_t>(r) * a.heads + h) * a.max_splits;
-  float m = 0.0F, l = 0.0F, v = 0.0F;
-  for (int s = 0; s < splits; ++s) {
-    const float om = a.part_ml[(hs + s) * 2], ol = a.part_ml[(hs + s) * 2 + 1];
-    const float ov = a.part_o[(hs + s) * kHeadDim + d];
-    if (ol == 0.0F) continue;
-    if (l == 0.0F) {
-      m = om; l = ol; v = ov;
-      continue;
+  const int d0 = 128 * wave + lane, d1 = d0 + 64;
+  float acc0 = 0.0F, acc1 = 0.0F, L = 0.0F;
+  // global max over the chunks, then their weights in batches of 64
+  float M = -INFINITY;
+  for (int s = lane; s < splits; s += 64) M = fmaxf(M, a.part_ml[(hs + s) * 2]);
+  M = group_max<64>(M);
+  for (int s0 = 0; s0 < splits; s0 += 64) {
+    const int cnt = min(64, splits - s0);
+    float w = 0.0F, lw = 0.0F;
+    if (lane < cnt) {
+      w = expf(a.part_ml[(hs + s0 + lane) * 2] - M);
+      lw = w * a.part_ml[(hs + s0 + lane) * 2 + 1];
     }
-    const float mm = fmaxf(m, om);
-    const float x = expf(m - mm), y = expf(om - mm);
-    v = x * v + y * ov;
-    l = x * l + y * ol;
-    m = mm;
+    L += group_sum<64>(lw);
+    w_s[wave][lane] = w;
+    __syncthreads();
+    int s = 0;
+    for (; s + 4 <= cnt; s += 4) {
+      float o0[4], o1[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        o0[u] = a.part_o[(hs + s0 + s + u) * kHeadDim + d0];
+        o1[u] = a.part_o[(hs + s0 + s + u) * kHeadDim + d1];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        acc0 += w_s[wave][s + u] * o0[u];
+        acc1 += w_s[wave][s + u] * o1[u];
+      }
+    }
+    for (; s < cnt; ++s) {
+      acc0 += w_s[wave][s] * a.part_o[(hs + s0 + s) * kHeadDim + d0];
+      acc1 += w_s[wave][s] * a.part_o[(hs + s0 + s) * kHeadDim + d1];
+    }
+    __syncthreads();
   }
-  const float inv = 1.0F / (l > 0.0F ? l : 1.0F);
-  const size_t o = (static_cast<size_t>(r) * a.heads + h) * kHeadDim + d;
-  out[o] = (v * inv) * sigmoid_stable(gates[o]);
+  const float inv = 1.0F / (L > 0.0F ? L : 1.0F);
+  const size_t o = (static_cast<size_t>(r) * a.heads + h) * kHeadDim;
+  const float y0 = (acc0 * inv) * sigmoid_stable(gates[o + d0]);
+  const float y1 = (acc1 * inv) * sigmoid_stable(gates[o + d1]);
+  if (out != nullptr) {
+    out[o + d0] = y0;
+    out[o + d1] = y1;
+  }
+  if (qo.codes != nullptr)
+    h128_quantize_block(y0, y1, lane, r, 2 * h + wave, a.heads * kHeadDim / 32, true, seed, qo);
 }
 
 }  // namespace
@@ -228,25 +277,28 @@ hipError_t launch_attn_prep(const AttnPrepArgs &a, hipStream_t stream) {
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
   if (a.batch <= 0) return hipSuccess;
-  if (a.head_dim != kHeadDim || a.heads % a.kv_heads != 0) return hipErrorInvalidValue;
+  if (a.head_dim != kHeadDim || a.heads % a.kv_heads != 0 || a.split_tokens != kChunkTokens)
+    return hipErrorInvalidValue;
   const int qpk = a.heads / a.kv_heads;
-  const size_t score_bytes = static_cast<size_t>(qpk) * a.split_tokens * sizeof(float);
-  const size_t red_bytes = static_cast<size_t>(4) * qpk * kHeadDim * sizeof(float);
-  const size_t smem = score_bytes > red_bytes ? score_bytes : red_bytes;
   const dim3 grid(a.max_splits, a.kv_heads, a.batch), block(kAttnThreads);
   switch (qpk) {
-    case 1: Q35_LAUNCH((attention_kernel<1>), grid, block, smem, stream, a); break;
-    case 2: Q35_LAUNCH((attention_kernel<2>), grid, block, smem, stream, a); break;
-    case 4: Q35_LAUNCH((attention_kernel<4>), grid, block, smem, stream, a); break;
-    case 8: Q35_LAUNCH((attention_kernel<8>), grid, block, smem, stream, a); break;
+    case 1: Q35_LAUNCH((attention_kernel<1>), grid, block, 0, stream, a); break;
+    case 2: Q35_LAUNCH((attention_kernel<2>), grid, block, 0, stream, a); break;
+    case 4: Q35_LAUNCH((attention_kernel<4>), grid, block, 0, stream, a); break;
+    case 8: Q35_LAUNCH((attention_kernel<8>), grid, block, 0, stream, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
-hipError_t launch_attention_merge(const AttnArgs &a, const float *gates, float *out,
-                                  hipStream_t stream) {
-  Q35_LAUNCH((attention_merge_kernel), dim3(a.heads, a.batch), kHeadDim, 0, stream, a, gates, out);
+hipError_t launch_attention_merge(const AttnArgs &a, const float *gates, float *out, uint64_t *codes,
+                                  ActParam *params, uint64_t seed, hipStream_t stream) {
+  if (a.batch <= 0) return hipSuccess;
+  if (a.head_dim != kHeadDim || a.split_tokens != kChunkTokens) return hipErrorInvalidValue;
+  QuantOut qo;
+  qo.codes = codes;
+  qo.params = params;
+  Q35_LAUNCH((attention_merge_kernel), dim3(a.heads, a.batch), 128, 0, stream, a, gates, out, qo, seed);
   return hipGetLastError();
 }
 

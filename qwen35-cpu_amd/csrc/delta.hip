@@ -1,148 +1,194 @@
 // GatedDeltaNet decode update on CDNA4.
 //
-// One workgroup (256 threads) per (request, key head). The head's fp32 state
-// tile [value_row][key_col] = 128 x 128 (64 KiB) makes exactly one HBM round
-// trip: thread t holds the 16 float4 at flat offsets j*1024 + 4t (rows
-// j*8 + t/32, columns 4*(t%32)..+3), so every load/store instruction of the
-// workgroup covers 4 KiB contiguously, and each row's dot products reduce over
-// the 32 lanes of a half wavefront.
+// One workgroup (256 threads) per (value head, request). The head's fp32
+// state tile [value_row][key_col] = 128 x 128 (64 KiB) makes exactly one HBM
+// round trip, and its loads are the first instructions of the kernel, so the
+// 64 KiB are in flight while the rest of the step's inputs are prepared.
+// Thread t owns rows t/4 and 64 + t/4 and, within each, the eight float4 at
+// columns 16m + 4(t%4) (m = 0..7): four lanes share a row, so every row dot
+// product finishes with two DPP quad exchanges instead of a shuffle chain,
+// and one load instruction covers 16 rows x 64 contiguous bytes.
 //
-// Per value row (src/cpu/delta_net.cpp:63-98):
+// Per value row (src/cpu/delta_net.cpp:63-98), in the reference's order:
 //   S *= alpha;  sk = S.k;  delta = (v - sk) * beta;  S += delta * k;  o = S.q
 // The fused variant also runs the rest of run_linear_attention_step
 // (src/runtime/layers.inl:96-207) for its head: causal conv1d + SiLU over the
-// q/k/v channels with the (kernel-1)-slot ring (activation.cpp:164-222), L2
-// normalisation of q (x 1/sqrt(d_k)) and k, beta = sigmoid(b),
-// alpha = exp(softplus(a + dt_bias) * -exp(A_log)), and the gated RMSNorm
-// (offset 0) times SiLU(z). GQA heads (v_heads > k_heads) loop over the value
-// heads sharing this key head, as the reference repeats q/k (layers.inl:130-144).
-#include "q35_device.h"
-#include "q35_internal.h"
+// q/k/v channels (activation.cpp:164-222), L2 normalisation of q
+// (x 1/sqrt(d_k)) and k, beta = sigmoid(b), alpha = exp(softplus(a + dt_bias)
+// * -exp(A_log)), and the gated RMSNorm (offset 0) times SiLU(z) -- and then
+// prepares the head's 128 outputs, which are exactly H128 block `head` of the
+// out projection's input, as int8 A16 activations for the DOT4 GEMM. GQA
+// (v_heads > k_heads) maps value head vh to key head vh / (v_heads / k_heads),
+// as the reference repeats q/k (layers.inl:130-144).
+//
+// The conv history is a ring of `kernel` slots indexed by position % kernel
+// (slot p % kernel receives the input of position p; positions p-kernel+1 ..
+// p-1 are read), so no workgroup ever reads a slot another one writes in the
+// same step.
+#include "q35_quant.h"
 
 namespace q35 {
 namespace {
 
 constexpr int kDeltaThreads = 256;
+constexpr int kDim = 128;
 
 template <bool FUSED>
 __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
-  __shared__ float sq[128], sk[128], sv[128], so[128];
-  __shared__ float scratch[8];
+  __shared__ float sq[kDim], sk[kDim], sv[kDim], so[kDim];
+  __shared__ float red[8];
   __shared__ float s_alpha, s_beta;
-  const int kh = blockIdx.x, r = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int vh = blockIdx.x, r = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int per = a.v_heads / a.k_heads;
-  const int kd = a.kd, vd = a.vd;  // both 128 (checked by the launcher)
+  const int kh = vh / per;
+  const int quad = tid & 3, rowp = tid >> 2;
+
+  // ---- 1. the state tile: all 16 float4 per thread in flight first
   float *state_r = a.state_base != nullptr
                        ? a.state_base + static_cast<long long>(a.slots[r]) * a.state_slot_stride
                        : a.states[r];
+  q35_f32x4 *S = reinterpret_cast<q35_f32x4 *>(state_r + static_cast<size_t>(vh) * kDim * kDim);
+  q35_f32x4 *S0 = S + rowp * (kDim / 4) + quad;         // row rowp
+  q35_f32x4 *S1 = S + (rowp + 64) * (kDim / 4) + quad;  // row rowp + 64
+  q35_f32x4 st0[8], st1[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    st0[m] = Q35_LOAD_NT(S0 + 4 * m);
+    st1[m] = Q35_LOAD_NT(S1 + 4 * m);
+  }
 
-  const int q_dim = a.k_heads * kd, v_dim = a.v_heads * vd;
+  // ---- 2. q, k, v, gates of this head
+  const int q_dim = a.k_heads * kDim, v_dim = a.v_heads * kDim;
   const int channels = 2 * q_dim + v_dim;
   const float *prow = FUSED ? a.proj + static_cast<size_t>(r) * a.proj_stride : nullptr;
-  float *conv = nullptr;
-  int ring = 0, hist = a.kernel - 1;
+  float z0 = 0.0F, z1 = 0.0F;  // output gate of columns lane, 64 + lane (wave 0)
   if constexpr (FUSED) {
-    conv = a.conv_base + static_cast<long long>(a.slots[r]) * a.conv_slot_stride;
-    ring = a.positions[r] % hist;
-  }
-
-  // causal conv1d + SiLU of one channel (batch 1), updating the ring slot
-  auto conv_channel = [&](int ch) -> float {
-    const float x = prow[ch];
-    float sum = x * a.conv_w[static_cast<size_t>(hist) * channels + ch];
-    for (int k = 0; k < hist; ++k) {
-      const int slot = (ring + k) % hist;
-      sum += conv[static_cast<size_t>(slot) * channels + ch] *
-             a.conv_w[static_cast<size_t>(k) * channels + ch];
+    float *conv = a.conv_base + static_cast<long long>(a.slots[r]) * a.conv_slot_stride;
+    const int K = a.kernel, pos = a.positions[r];
+    // causal conv1d + SiLU of one channel (batch 1), writing the input into
+    // the ring slot of this position
+    auto conv_channel = [&](int ch) -> float {
+      const float x = prow[ch];
+      float sum = x * a.conv_w[static_cast<size_t>(K - 1) * channels + ch];
+      for (int k = 0; k < K - 1; ++k) {
+        const int p = pos - (K - 1) + k;
+        const int slot = ((p % K) + K) % K;
+        sum += conv[static_cast<size_t>(slot) * channels + ch] * a.conv_w[static_cast<size_t>(k) * channels + ch];
+      }
+      conv[static_cast<size_t>(pos % K) * channels + ch] = x;
+      return silu_times(sum, 1.0F);
+    };
+    // threads 0..127: q channel, 128..255: k channel of key head kh
+    const int i = tid & (kDim - 1);
+    const bool is_k = tid >= kDim;
+    const float y = conv_channel((is_k ? q_dim : 0) + kh * kDim + i);
+    const float vv = tid < kDim ? conv_channel(2 * q_dim + vh * kDim + tid) : 0.0F;
+    if (wave == 0) {
+      z0 = prow[channels + vh * kDim + lane];
+      z1 = prow[channels + vh * kDim + 64 + lane];
     }
-    conv[static_cast<size_t>(ring) * channels + ch] = x;
-    return silu_times(sum, 1.0F);
-  };
-
-  if constexpr (FUSED) {
-    // threads 0..127: q channel, 128..255: k channel of this key head
-    const int i = tid & 127;
-    const bool is_k = tid >= 128;
-    const int ch = (is_k ? q_dim : 0) + kh * kd + i;
-    const float y = conv_channel(ch);
-    // L2 norm per head over 128 values: each half of the block is two waves
-    float ss = group_sum<64>(y * y);
+    if (tid == 0) {
+      const float bval = prow[channels + v_dim + vh];
+      const float aval = prow[channels + v_dim + a.v_heads + vh];
+      s_beta = sigmoid_stable(bval);
+      const float pre = softplus_stable(aval + a.dt_bias[vh]);
+      s_alpha = expf(pre * a.ssm_a[vh]);
+    }
+    // L2 norms of q (waves 0-1) and k (waves 2-3) over 128 values
+    const float ss = group_sum<64>(y * y);
+    if (lane == 0) red[wave] = ss;
+    if (tid < kDim) sv[tid] = vv;
     __syncthreads();
-    if (lane == 0) scratch[tid >> 6] = ss;
-    __syncthreads();
-    ss = is_k ? scratch[2] + scratch[3] : scratch[0] + scratch[1];
-    const float scale = is_k ? 1.0F : 1.0F / sqrtf(static_cast<float>(kd));
-    const float m = scale / sqrtf(ss + 1.0e-6F);
+    const float tot = is_k ? red[2] + red[3] : red[0] + red[1];
+    const float scale = is_k ? 1.0F : 1.0F / sqrtf(static_cast<float>(kDim));
+    const float mul = scale / sqrtf(tot + 1.0e-6F);
     if (is_k)
-      sk[i] = y * m;
+      sk[i] = y * mul;
     else
-      sq[i] = y * m;
+      sq[i] = y * mul;
+  } else {
+    const size_t qk = (static_cast<size_t>(r) * a.v_heads + vh) * kDim;
+    if (tid < kDim) {
+      sq[tid] = a.q[qk + tid];
+      sk[tid] = a.k[qk + tid];
+      sv[tid] = a.v[qk + tid];
+    }
+    if (tid == 0) {
+      s_alpha = a.alpha[static_cast<size_t>(r) * a.v_heads + vh];
+      s_beta = a.beta[static_cast<size_t>(r) * a.v_heads + vh];
+    }
   }
+  __syncthreads();
 
-  for (int vi = 0; vi < per; ++vi) {
-    const int vh = kh * per + vi;
-    if constexpr (FUSED) {
-      if (tid < 128) sv[tid] = conv_channel(2 * q_dim + vh * vd + tid);
-      if (tid == 0) {
-        const float bval = prow[channels + v_dim + vh];
-        const float aval = prow[channels + v_dim + a.v_heads + vh];
-        s_beta = sigmoid_stable(bval);
-        const float pre = softplus_stable(aval + a.dt_bias[vh]);
-        s_alpha = expf(pre * a.ssm_a[vh]);
-      }
-    } else {
-      const size_t qk = (static_cast<size_t>(r) * a.v_heads + vh) * kd;
-      if (tid < 128) {
-        sq[tid] = a.q[qk + tid];
-        sk[tid] = a.k[qk + tid];
-        sv[tid] = a.v[(static_cast<size_t>(r) * a.v_heads + vh) * vd + tid];
-      }
-      if (tid == 0) {
-        s_alpha = a.alpha[static_cast<size_t>(r) * a.v_heads + vh];
-        s_beta = a.beta[static_cast<size_t>(r) * a.v_heads + vh];
-      }
-    }
-    float4 *S = reinterpret_cast<float4 *>(state_r + static_cast<size_t>(vh) * vd * kd);
-    float4 st[16];
+  // ---- 3. delta rule on the two rows of this thread
+  const float alpha = s_alpha, beta = s_beta;
+  q35_f32x4 kc[8];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) st[j] = S[j * 256 + tid];
-    __syncthreads();
-    const float alpha = s_alpha, beta = s_beta;
-    const int col = 4 * (tid & 31);
-    const float4 kc = make_float4(sk[col], sk[col + 1], sk[col + 2], sk[col + 3]);
-    const float4 qc = make_float4(sq[col], sq[col + 1], sq[col + 2], sq[col + 3]);
+  for (int m = 0; m < 8; ++m) kc[m] = *reinterpret_cast<const q35_f32x4 *>(sk + 16 * m + 4 * quad);
+  float d0 = 0.0F, d1 = 0.0F;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      float4 s = st[j];
-      s.x *= alpha; s.y *= alpha; s.z *= alpha; s.w *= alpha;
-      float d = s.x * kc.x + s.y * kc.y + s.z * kc.z + s.w * kc.w;
-      d = group_sum<32>(d);
-      const int row = j * 8 + (tid >> 5);
-      const float delta = (sv[row] - d) * beta;
-      s.x += delta * kc.x; s.y += delta * kc.y; s.z += delta * kc.z; s.w += delta * kc.w;
-      float e = s.x * qc.x + s.y * qc.y + s.z * qc.z + s.w * qc.w;
-      e = group_sum<32>(e);
-      st[j] = s;
-      if ((tid & 31) == 0) so[row] = e;
-    }
+  for (int m = 0; m < 8; ++m) {
+    st0[m] *= alpha;
+    st1[m] *= alpha;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) S[j * 256 + tid] = st[j];
-    __syncthreads();
-    if constexpr (FUSED) {
-      // gated RMSNorm (offset 0) over the head, then * SiLU(z)  (layers.inl:198-207)
-      const float o = tid < 128 ? so[tid] : 0.0F;
-      const float ss = block_sum<kDeltaThreads / 64>(o * o, scratch);
-      if (tid < 128) {
-        const float inv = 1.0F / sqrtf(ss / static_cast<float>(vd) + a.eps);
-        const float y = o * inv * (a.norm_w[tid] + 0.0F);
-        const float z = prow[channels + vh * vd + tid];
-        a.out[static_cast<size_t>(r) * v_dim + vh * vd + tid] = silu_times(z, y);
-      }
-    } else {
-      if (tid < 128) a.out[(static_cast<size_t>(r) * a.v_heads + vh) * vd + tid] = so[tid];
+    for (int e = 0; e < 4; ++e) {
+      d0 += st0[m][e] * kc[m][e];
+      d1 += st1[m][e] * kc[m][e];
     }
-    __syncthreads();
+  }
+  d0 += q35_quad_xor1(d0);
+  d1 += q35_quad_xor1(d1);
+  d0 += q35_quad_xor2(d0);
+  d1 += q35_quad_xor2(d1);
+  const float delta0 = (sv[rowp] - d0) * beta, delta1 = (sv[rowp + 64] - d1) * beta;
+  float o0 = 0.0F, o1 = 0.0F;
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const q35_f32x4 qc = *reinterpret_cast<const q35_f32x4 *>(sq + 16 * m + 4 * quad);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      st0[m][e] += delta0 * kc[m][e];
+      st1[m][e] += delta1 * kc[m][e];
+      o0 += st0[m][e] * qc[e];
+      o1 += st1[m][e] * qc[e];
+    }
+    Q35_STORE_NT(st0[m], S0 + 4 * m);
+    Q35_STORE_NT(st1[m], S1 + 4 * m);
+  }
+  o0 += q35_quad_xor1(o0);
+  o1 += q35_quad_xor1(o1);
+  o0 += q35_quad_xor2(o0);
+  o1 += q35_quad_xor2(o1);
+  if (quad == 0) {
+    so[rowp] = o0;
+    so[rowp + 64] = o1;
+  }
+  __syncthreads();
+
+  // ---- 4. outputs (wave 0: columns lane and 64 + lane)
+  if (wave != 0) return;
+  float y0 = so[lane], y1 = so[64 + lane];
+  if constexpr (FUSED) {
+    // gated RMSNorm (offset 0) over the head, then * SiLU(z)  (layers.inl:198-207)
+    const float ss = group_sum<64>(y0 * y0 + y1 * y1);
+    const float inv = 1.0F / sqrtf(ss / static_cast<float>(kDim) + a.eps);
+    y0 = silu_times(z0, y0 * inv * (a.norm_w[lane] + 0.0F));
+    y1 = silu_times(z1, y1 * inv * (a.norm_w[64 + lane] + 0.0F));
+    if (a.out != nullptr) {
+      a.out[static_cast<size_t>(r) * v_dim + vh * kDim + lane] = y0;
+      a.out[static_cast<size_t>(r) * v_dim + vh * kDim + 64 + lane] = y1;
+    }
+    if (a.codes != nullptr) {
+      QuantOut qo;
+      qo.codes = a.codes;
+      qo.params = a.params;
+      h128_quantize_block(y0, y1, lane, r, vh, v_dim / 32, true, a.seed, qo);
+    }
+  } else {
+    const size_t o = (static_cast<size_t>(r) * a.v_heads + vh) * kDim;
+    a.out[o + lane] = y0;
+    a.out[o + 64 + lane] = y1;
   }
 }
 
@@ -150,8 +196,8 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
 
 hipError_t launch_delta(const DeltaArgs &a, hipStream_t stream) {
   if (a.batch <= 0) return hipSuccess;
-  if (a.kd != 128 || a.vd != 128 || a.v_heads % a.k_heads != 0) return hipErrorInvalidValue;
-  const dim3 grid(a.k_heads, a.batch), block(kDeltaThreads);
+  if (a.kd != kDim || a.vd != kDim || a.v_heads % a.k_heads != 0) return hipErrorInvalidValue;
+  const dim3 grid(a.v_heads, a.batch), block(kDeltaThreads);
   if (a.fused)
     Q35_LAUNCH((delta_kernel<true>), grid, block, 0, stream, a);
   else

@@ -66,14 +66,14 @@ __global__ __launch_bounds__(1024) void gemm_kernel(GemmArgs a) {
   const int token_tiles = (a.tokens + 15) >> 4;
   const uint8_t *wbase = reinterpret_cast<const uint8_t *>(a.w);
 
-  for (int tt = 0; tt < token_tiles; ++tt) {
-    __syncthreads();
-    for (int i = threadIdx.x; i < nb * 16; i += blockDim.x)
-      act_scale[i] = a.params[static_cast<size_t>(tt) * nb * 16 + i].scale;
-    if (ARGMAX && threadIdx.x < 16) best[threadIdx.x] = 0ull;
-    __syncthreads();
-    const uint64_t *acodes = a.codes + static_cast<size_t>(tt) * nb * 64 + lane;
+  // a wavefront with an empty block range (never produced by gemm_shape, kept
+  // safe) reads block 0 and contributes nothing
+  const bool has_blocks = b0 < b1;
+  const int bl = has_blocks ? b1 - 1 : 0;
 
+  for (int tt = 0; tt < token_tiles; ++tt) {
+    const uint64_t *acodes = a.codes + static_cast<size_t>(tt) * nb * 64 + lane;
+    bool staged = false;
     for (int g = blockIdx.x; g < groups; g += gridDim.x) {
       float acc[4][4];
 #pragma unroll
@@ -86,7 +86,7 @@ __global__ __launch_bounds__(1024) void gemm_kernel(GemmArgs a) {
       const uint8_t *qrow = wbase + static_cast<size_t>(rt) * nb * 144 + 16 + 16 * (2 * G + h);
       const uint8_t *drow = wbase + static_cast<size_t>(rt) * nb * 144 + 8 * h;
 
-      for (int cb = b0; cb < b1; cb += kChunk) {
+      for (int cb = has_blocks ? b0 : 0; cb < (has_blocks ? b1 : 1); cb += kChunk) {
         // all loads of the chunk first (indices clamped into the wave's
         // range, so no load is predicated), then the MFMAs
         q35_u32x4 q[kChunk];
@@ -94,17 +94,28 @@ __global__ __launch_bounds__(1024) void gemm_kernel(GemmArgs a) {
         long act[kChunk];
 #pragma unroll
         for (int i = 0; i < kChunk; ++i) {
-          const size_t b = static_cast<size_t>(min(cb + i, b1 - 1));
+          const size_t b = static_cast<size_t>(min(cb + i, bl));
           q[i] = Q35_LOAD_NT(reinterpret_cast<const q35_u32x4 *>(qrow + b * 144));
           d[i] = Q35_LOAD_NT(reinterpret_cast<const q35_u32x2 *>(drow + b * 144));
           act[i] = static_cast<long>(acodes[b * 64]);
+        }
+        if (!staged) {
+          // the activation scales of this token tile, staged while the first
+          // chunk's weights are in flight (every wavefront reaches this point
+          // once per token tile: its first chunk of its first group)
+          staged = true;
+          __syncthreads();
+          for (int i = threadIdx.x; i < nb * 16; i += blockDim.x)
+            act_scale[i] = a.params[static_cast<size_t>(tt) * nb * 16 + i].scale;
+          if (ARGMAX && threadIdx.x < 16) best[threadIdx.x] = 0ull;
+          __syncthreads();
         }
 #pragma unroll
         for (int i = 0; i < kChunk; ++i) {
           // a padded slot past the wave's range re-reads its last block; a
           // zero row scale makes its contribution exactly +0 (acc is never -0)
-          const bool valid = cb + i < b1;
-          const int b = valid ? cb + i : b1 - 1;
+          const bool valid = has_blocks && cb + i < b1;
+          const int b = valid ? cb + i : bl;
           if (!valid) d[i] = q35_u32x2{0u, 0u};
           const v4i zero = {0, 0, 0, 0};
           const v4i corr = Q35_MFMA_I32_16X16X32_I8(act[i], kMinus8, zero, 0, 0, 0);

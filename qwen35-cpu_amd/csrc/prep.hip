@@ -10,8 +10,7 @@
 // 16-token step spreads over 16 x K/128 wavefronts; two values per lane, the
 // first six FWHT stages are lane shuffles and the last one is in-lane. An
 // RMSNorm source recomputes its row's sum of squares in each wavefront.
-#include "q35_device.h"
-#include "q35_internal.h"
+#include "q35_quant.h"
 
 namespace q35 {
 namespace {
@@ -71,14 +70,25 @@ __global__ __launch_bounds__(kPrepThreads) void prep_kernel(PrepArgs a) {
 
   float rms_inv = 1.0F;
   if constexpr (SRC == kPrepRmsNorm) {
-    const float *row = a.x + static_cast<size_t>(t) * a.x_stride;
+    // the row's sum of squares, four 16-byte loads per lane in flight
+    // (x_stride and K are multiples of 128)
+    const q35_f32x4 *row4 = reinterpret_cast<const q35_f32x4 *>(a.x + static_cast<size_t>(t) * a.x_stride);
+    const int n4 = K >> 2;
     float ss = 0.0F;
-    for (int i = lane; i < K; i += 64) ss += row[i] * row[i];
+    for (int i0 = lane; i0 < n4; i0 += 256) {
+      q35_f32x4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + 64 * u;
+        v[u] = i < n4 ? row4[i] : q35_f32x4{0.0F, 0.0F, 0.0F, 0.0F};
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) ss += v[u][0] * v[u][0] + v[u][1] * v[u][1] + v[u][2] * v[u][2] + v[u][3] * v[u][3];
+    }
     ss = group_sum<64>(ss);
     rms_inv = 1.0F / sqrtf(ss / static_cast<float>(K) + a.eps);
   }
 
-  const int tile = t >> 4, tok = t & 15;
   {
     const int c0 = blk * 128 + lane, c1 = c0 + 64;
     float v0 = load_source<SRC>(a, t, c0, rms_inv);
@@ -87,66 +97,12 @@ __global__ __launch_bounds__(kPrepThreads) void prep_kernel(PrepArgs a) {
       a.normed_out[static_cast<size_t>(t) * K + c0] = v0;
       a.normed_out[static_cast<size_t>(t) * K + c1] = v1;
     }
-    if (a.h128) {
-      const uint64_t w0 = h128_sign_word(blk, 0, a.seed), w1 = h128_sign_word(blk, 1, a.seed);
-      if ((w0 >> lane) & 1ull) v0 = -v0;
-      if ((w1 >> lane) & 1ull) v1 = -v1;
-#pragma unroll
-      for (int s = 1; s < 64; s <<= 1) {
-        const float p0 = __shfl_xor(v0, s, 64), p1 = __shfl_xor(v1, s, 64);
-        if (lane & s) {
-          v0 = p0 - v0;
-          v1 = p1 - v1;
-        } else {
-          v0 = v0 + p0;
-          v1 = v1 + p1;
-        }
-      }
-      const float lhs = v0;
-      v0 = lhs + v1;
-      v1 = lhs - v1;
-    }
-    // Two 32-value groups per value slot: group(v0) = lane/32, group(v1) = 2 + lane/32.
-    float vals[2] = {v0, v1};
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      const float v = vals[half];
-      const float amax = group_max<32>(fabsf(v));
-      const float scale = amax / 127.0F;
-      const float inv = scale == 0.0F ? 0.0F : 1.0F / scale;
-      float r = roundf(v * inv);
-      r = fminf(fmaxf(r, -127.0F), 127.0F);
-      const int code = static_cast<int>(r);
-      const int sum = group_sum_int<32>(code);
-      float stored = half_bits_to_float(float_to_half_bits(scale));
-      if (a.h128) stored *= kH128InvSqrt;
-      const int b = blk * 4 + half * 2 + (lane >> 5);
-      const int k = lane & 31;
-      if (a.codes != nullptr) {
-        uint8_t *dst = reinterpret_cast<uint8_t *>(a.codes);
-        const size_t word = (static_cast<size_t>(tile) * nb + b) * 64 + tok + 16 * (k >> 3);
-        dst[word * 8 + (k & 7)] = static_cast<uint8_t>(static_cast<int8_t>(code));
-        if (k == 0)
-          a.params[(static_cast<size_t>(tile) * nb + b) * 16 + tok] = ActParam{stored, -8 * sum};
-      }
-      if (a.x4 != nullptr) {
-        q35_q8_0_block_x4 &blkx = a.x4[static_cast<size_t>(t >> 2) * nb + b];
-        blkx.qs[(t & 3) * 32 + k] = static_cast<int8_t>(code);
-        if (k == 0) {
-          blkx.scales[t & 3] = stored;
-          blkx.sums[t & 3] = static_cast<int16_t>(sum);
-        }
-      }
-      if (a.x1 != nullptr) {
-        q35_q8_0_block_x1 &blk1 = a.x1[static_cast<size_t>(t) * nb + b];
-        blk1.qs[k] = static_cast<int8_t>(code);
-        if (k == 0) {
-          blk1.scales[0] = stored;
-          blk1.sums[0] = static_cast<int16_t>(sum);
-          blk1.pad = 0;
-        }
-      }
-    }
+    QuantOut o;
+    o.codes = a.codes;
+    o.params = a.params;
+    o.x4 = a.x4;
+    o.x1 = a.x1;
+    h128_quantize_block(v0, v1, lane, t, blk, nb, a.h128, a.seed, o);
   }
 }
 

@@ -24,3 +24,14 @@ typedef float q35_f32x4 __attribute__((ext_vector_type(4)));
 #define Q35_LOAD_NT(ptr) __builtin_nontemporal_load(ptr)
 #define Q35_STORE_NT(value, ptr) __builtin_nontemporal_store(value, ptr)
 #endif
+
+#ifndef Q35_HOST_EMULATION
+// Exchange with lane l^1 / l^2 inside each group of four lanes (DPP quad_perm
+// [1,0,3,2] and [2,3,0,1]): a register-to-register move, no LDS crossbar.
+__device__ __forceinline__ float q35_quad_xor1(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float q35_quad_xor2(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, true));
+}
+#endif

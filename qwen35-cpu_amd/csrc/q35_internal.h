@@ -139,13 +139,18 @@ struct DeltaArgs {
   // fused mode inputs
   const float *proj = nullptr;     // [batch][proj_stride] = [qkv | z | b | a]
   int proj_stride = 0;
-  float *conv_base = nullptr;      // slot-strided conv state [(kernel-1)][channels]
+  float *conv_base = nullptr;      // slot-strided conv ring [kernel][channels], slot = position % kernel
   long long conv_slot_stride = 0;
   const int32_t *positions = nullptr;
   const float *conv_w = nullptr;   // kernel-major [kernel][channels]
   int kernel = 4;
   const float *dt_bias = nullptr, *ssm_a = nullptr, *norm_w = nullptr;
   float eps = 1e-6F;
+  // fused mode: the gated outputs prepared as A16 activations of the out
+  // projection (H128 block = value head); `out` (FP32) is optional then
+  uint64_t *codes = nullptr;
+  ActParam *params = nullptr;
+  uint64_t seed = 0;
 };
 hipError_t launch_delta(const DeltaArgs &a, hipStream_t stream);
 
@@ -174,14 +179,17 @@ struct AttnArgs {
   const int32_t *positions = nullptr;
   int batch = 0, heads = 0, kv_heads = 0, head_dim = 0;
   float scale = 0.0625F;
-  int split_tokens = 256, max_splits = 1;
+  int split_tokens = 64, max_splits = 1;  // split_tokens must be kAttnChunkTokens
   float *part_o = nullptr;        // [batch][heads][max_splits][head_dim]
   float *part_ml = nullptr;       // [batch][heads][max_splits][2]
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t stream);
-// Stand-alone merge (+ gate) used by the kernel-level entry point.
-hipError_t launch_attention_merge(const AttnArgs &a, const float *gates, float *out,
-                                  hipStream_t stream);
+// Merge of the chunk partials + sigmoid gate: FP32 rows into `out` and/or the
+// o projection's A16 activations into codes/params (either may be null).
+// split_tokens must be kAttnChunkTokens.
+constexpr int kAttnChunkTokens = 64;
+hipError_t launch_attention_merge(const AttnArgs &a, const float *gates, float *out, uint64_t *codes,
+                                  ActParam *params, uint64_t seed, hipStream_t stream);
 
 // Elementwise / small ops (kernel-level entries and the step)
 hipError_t launch_rms_norm(const float *x, const float *w, float *y, int rows, int width,

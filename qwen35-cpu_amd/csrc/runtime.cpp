@@ -449,8 +449,8 @@ extern "C" int q35_attention_decode_paged(q35_context *ctx, const float *q, cons
   a.kv_heads = kv_heads;
   a.head_dim = head_dim;
   a.scale = scale;
-  a.split_tokens = 256;
-  a.max_splits = (max_len + 255) / 256;
+  a.split_tokens = kAttnChunkTokens;
+  a.max_splits = (max_len + kAttnChunkTokens - 1) / kAttnChunkTokens;
   const size_t parts = batch * static_cast<size_t>(heads) * a.max_splits;
   void *scratch = nullptr;
   int st = scratch_get(ctx, align256(parts * 256 * 4) + align256(parts * 2 * 4), &scratch);
@@ -459,7 +459,8 @@ extern "C" int q35_attention_decode_paged(q35_context *ctx, const float *q, cons
   a.part_ml = reinterpret_cast<float *>(static_cast<char *>(scratch) + align256(parts * 256 * 4));
   hipError_t e = launch_attention(a, ctx->stream);
   if (e != hipSuccess) return hip_error(ctx, e, "attention kernel");
-  return launch_status(ctx, launch_attention_merge(a, gates, output, ctx->stream), "attention merge");
+  return launch_status(ctx, launch_attention_merge(a, gates, output, nullptr, nullptr, 0, ctx->stream),
+                       "attention merge");
 }
 
 extern "C" int q35_attention_cache_store_f16(q35_context *ctx, const float *input, uint16_t *output,

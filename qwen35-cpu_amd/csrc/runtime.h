@@ -47,7 +47,7 @@ struct q35_runtime {
   q35::Context *ctx = nullptr;
   q35_runtime_config cfg{};
   int max_pages_per_row = 0;
-  int split_tokens = 256, max_splits = 1;
+  int split_tokens = q35::kAttnChunkTokens, max_splits = 1;
   // slot state
   float *recurrent = nullptr;  // [slots][n_lin][vh][vd][kd]
   float *conv = nullptr;       // [slots][n_lin][kernel-1][channels]

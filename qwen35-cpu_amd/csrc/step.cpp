@@ -313,7 +313,8 @@ extern "C" int q35_runtime_create(q35_model *m, const q35_runtime_config *cfg, q
   };
   // slot state
   rt->rec_slot_stride = static_cast<long long>(m->n_linear) * d.lin_v_heads * d.lin_v_dim * d.lin_k_dim;
-  rt->conv_slot_stride = static_cast<long long>(m->n_linear) * (d.lin_kernel - 1) * ch;
+  // conv ring of lin_kernel slots per layer, slot = position % lin_kernel
+  rt->conv_slot_stride = static_cast<long long>(m->n_linear) * d.lin_kernel * ch;
   alloc(static_cast<size_t>(cfg->max_slots) * rt->rec_slot_stride * 4, reinterpret_cast<void **>(&rt->recurrent));
   alloc(static_cast<size_t>(cfg->max_slots) * rt->conv_slot_stride * 4, reinterpret_cast<void **>(&rt->conv));
   alloc(static_cast<size_t>(cfg->max_slots) * d.vocab * 4, reinterpret_cast<void **>(&rt->counts));
@@ -615,7 +616,7 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
       a.out = rt->core;
       a.proj = rt->proj;
       a.proj_stride = L.in_rows;
-      a.conv_base = rt->conv + static_cast<size_t>(li) * (d.lin_kernel - 1) * ch;
+      a.conv_base = rt->conv + static_cast<size_t>(li) * d.lin_kernel * ch;
       a.conv_slot_stride = rt->conv_slot_stride;
       a.positions = positions;
       a.conv_w = L.conv_w;
@@ -624,14 +625,16 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
       a.ssm_a = L.ssm_a;
       a.norm_w = L.lin_norm;
       a.eps = d.rms_eps;
+      a.out = nullptr;
+      a.codes = rt->codes;
+      a.params = rt->params;
+      a.seed = d.sign_seed;
       // recurrent state read + written, projection row in, conv ring (K-1 rows
-      // read, one written), core output
+      // read, one written), prepared out-projection activations
       const double delta_bytes =
           B * (2.0 * d.lin_v_heads * d.lin_v_dim * d.lin_k_dim * 4.0 + L.in_rows * 4.0 +
-               static_cast<double>(d.lin_kernel) * ch * 4.0 + v_dim * 4.0);
+               static_cast<double>(d.lin_kernel) * ch * 4.0 + v_dim + v_dim / 32.0 * sizeof(ActParam));
       Q35_KERNEL(Q35_KERNEL_DELTA, delta_bytes, launch_delta(a, s), "DeltaNet");
-      Q35_KERNEL(Q35_KERNEL_PREP, prep_bytes(v_dim, v_dim),
-                 launch_prep(prep(kPrepPlain, rt->core, v_dim, nullptr, v_dim, true), s), "core prep");
     } else {
       const int fi = m->full_index[l];
       AttnPrepArgs p;
@@ -682,18 +685,12 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
                  kv_tokens * kvw * 2.0 * 2.0 + B * d.n_heads * d.head_dim * 4.0 +
                      splits_used * d.n_heads * (d.head_dim + 2) * 4.0,
                  launch_attention(a, s), "attention");
-      PrepArgs pa = prep(kPrepAttnMerge, nullptr, 0, nullptr, d.n_heads * d.head_dim, true);
-      pa.part_o = rt->part_o;
-      pa.part_ml = rt->part_ml;
-      pa.seq_lens = seq_lens;
-      pa.gates = rt->gates;
-      pa.heads = d.n_heads;
-      pa.head_dim = d.head_dim;
-      pa.max_splits = rt->max_splits;
-      pa.split_tokens = rt->split_tokens;
+      // chunk partials and gates in, o projection A16 activations out
       Q35_KERNEL(Q35_KERNEL_PREP,
-                 splits_used * d.n_heads * (d.head_dim + 2) * 4.0 + prep_bytes(d.n_heads * d.head_dim, d.n_heads * d.head_dim),
-                 launch_prep(pa, s), "attention merge prep");
+                 splits_used * d.n_heads * (d.head_dim + 2) * 4.0 +
+                     B * d.n_heads * d.head_dim * (4.0 + 1.0) + B * d.n_heads * d.head_dim / 32.0 * sizeof(ActParam),
+                 launch_attention_merge(a, rt->gates, nullptr, rt->codes, rt->params, d.sign_seed, s),
+                 "attention merge");
     }
     Q35_KERNEL(Q35_KERNEL_GEMM, gemm_algorithmic_bytes(H, L.out_cols / 32, batch, true, true),
                gemm(L.out_proj, H, L.out_cols, rt->x, H, rt->x), "out projection");
