@@ -24,15 +24,13 @@ __global__ __launch_bounds__(kAttnThreads) void attn_prep_kernel(AttnPrepArgs a)
   const int r = blockIdx.x, slot = blockIdx.y, d = threadIdx.x;
   const int hd = a.head_dim;
   const bool is_q = slot < a.heads;
-  const float *prow = a.proj + static_cast<size_t>(r) * a.proj_stride;
   float x = 0.0F;
   if (d < hd) {
     if (is_q) {
-      x = prow[static_cast<size_t>(slot) * 2 * hd + d];
-      a.gate_out[(static_cast<size_t>(r) * a.heads + slot) * hd + d] =
-          prow[static_cast<size_t>(slot) * 2 * hd + hd + d];
+      x = a.proj.at(r, slot * 2 * hd + d);
+      a.gate_out[(static_cast<size_t>(r) * a.heads + slot) * hd + d] = a.proj.at(r, slot * 2 * hd + hd + d);
     } else {
-      x = prow[static_cast<size_t>(a.heads) * 2 * hd + static_cast<size_t>(slot - a.heads) * hd + d];
+      x = a.proj.at(r, a.heads * 2 * hd + (slot - a.heads) * hd + d);
     }
   }
   const float ss = block_sum<kAttnThreads / 64>(x * x, scratch);
@@ -62,8 +60,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_prep_kernel(AttnPrepArgs a)
     const int page = a.page_table[static_cast<size_t>(r) * a.max_pages + pos / a.page_tokens];
     const size_t row = (static_cast<size_t>(page) * a.page_tokens + pos % a.page_tokens) * a.kv_heads + g;
     a.k_pool[row * hd + d] = float_to_half_bits(y);
-    const float v = prow[static_cast<size_t>(a.heads) * 2 * hd + static_cast<size_t>(a.kv_heads) * hd +
-                         static_cast<size_t>(g) * hd + d];
+    const float v = a.proj.at(r, a.heads * 2 * hd + a.kv_heads * hd + g * hd + d);
     a.v_pool[row * hd + d] = float_to_half_bits(v);
   }
 }
@@ -292,12 +289,12 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
 }
 
 hipError_t launch_attention_merge(const AttnArgs &a, const float *gates, float *out, uint64_t *codes,
-                                  ActParam *params, uint64_t seed, hipStream_t stream) {
+                                  float *scales, uint64_t seed, hipStream_t stream) {
   if (a.batch <= 0) return hipSuccess;
   if (a.head_dim != kHeadDim || a.split_tokens != kChunkTokens) return hipErrorInvalidValue;
   QuantOut qo;
   qo.codes = codes;
-  qo.params = params;
+  qo.scales = scales;
   Q35_LAUNCH((attention_merge_kernel), dim3(a.heads, a.batch), 128, 0, stream, a, gates, out, qo, seed);
   return hipGetLastError();
 }

@@ -61,7 +61,6 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
   // ---- 2. q, k, v, gates of this head
   const int q_dim = a.k_heads * kDim, v_dim = a.v_heads * kDim;
   const int channels = 2 * q_dim + v_dim;
-  const float *prow = FUSED ? a.proj + static_cast<size_t>(r) * a.proj_stride : nullptr;
   float z0 = 0.0F, z1 = 0.0F;  // output gate of columns lane, 64 + lane (wave 0)
   if constexpr (FUSED) {
     float *conv = a.conv_base + static_cast<long long>(a.slots[r]) * a.conv_slot_stride;
@@ -69,7 +68,7 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
     // causal conv1d + SiLU of one channel (batch 1), writing the input into
     // the ring slot of this position
     auto conv_channel = [&](int ch) -> float {
-      const float x = prow[ch];
+      const float x = a.proj.at(r, ch);
       float sum = x * a.conv_w[static_cast<size_t>(K - 1) * channels + ch];
       for (int k = 0; k < K - 1; ++k) {
         const int p = pos - (K - 1) + k;
@@ -85,12 +84,12 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
     const float y = conv_channel((is_k ? q_dim : 0) + kh * kDim + i);
     const float vv = tid < kDim ? conv_channel(2 * q_dim + vh * kDim + tid) : 0.0F;
     if (wave == 0) {
-      z0 = prow[channels + vh * kDim + lane];
-      z1 = prow[channels + vh * kDim + 64 + lane];
+      z0 = a.proj.at(r, channels + vh * kDim + lane);
+      z1 = a.proj.at(r, channels + vh * kDim + 64 + lane);
     }
     if (tid == 0) {
-      const float bval = prow[channels + v_dim + vh];
-      const float aval = prow[channels + v_dim + a.v_heads + vh];
+      const float bval = a.proj.at(r, channels + v_dim + vh);
+      const float aval = a.proj.at(r, channels + v_dim + a.v_heads + vh);
       s_beta = sigmoid_stable(bval);
       const float pre = softplus_stable(aval + a.dt_bias[vh]);
       s_alpha = expf(pre * a.ssm_a[vh]);
@@ -182,7 +181,7 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
     if (a.codes != nullptr) {
       QuantOut qo;
       qo.codes = a.codes;
-      qo.params = a.params;
+      qo.scales = a.scales;
       h128_quantize_block(y0, y1, lane, r, vh, v_dim / 32, true, a.seed, qo);
     }
   } else {

@@ -5,11 +5,16 @@
 // so the 32-bit word 8t+r of a tile body holds row r's columns 8t..8t+3 (low
 // nibbles) and 8t+4..8t+7 (high nibbles).
 //
-// Work decomposition. A workgroup owns a 64-row group (eight 8-row tiles) and
-// W <= 16 wavefronts that split the K blocks of that group; every wavefront
-// issues the loads of all of its blocks (at most 8 per chunk) before the
-// first MFMA, so one launch keeps W x 8 x 1.1 KB of weights in flight per
-// workgroup and the weight stream never waits on the activation chain.
+// Work decomposition. The rows form 64-row groups (eight 8-row tiles). A
+// workgroup owns one group and one of S contiguous K ranges (split-K across
+// workgroups, grid.y); its W wavefronts split that range, and every wavefront
+// issues the loads of all blocks of a chunk (KS blocks: weights, row scales,
+// activation codes and activation scales) before its first MFMA, so a launch
+// keeps groups x S x W x KS x 1.2 KB in flight and no wavefront waits on a
+// second round trip. The wavefronts of a workgroup are summed in fixed order
+// through LDS; with S > 1 each workgroup writes its partial sums to
+// partials[s][token][row] and the consumer kernel adds the S partials in split
+// order, so every result is deterministic.
 //
 // Lane l = (G = l/16, c = l%16) loads, per 32-column block, the 16-byte body
 // segment 2G + (c%2) of tile c/2 -- four words = rows 4(c%2)..4(c%2)+3 of
@@ -23,8 +28,7 @@
 // is the reference's exact int32 block dot for row 4c+i and token 4G+j. The
 // FP32 epilogue per block is the reference's
 //   acc = fma(float(dot), half(d_row) * s_tok, acc)   (q4_dot4.cpp:53)
-// in block order within each wavefront; the wavefronts are summed in fixed
-// order through LDS, so results are deterministic. With one wavefront per
+// in block order within each wavefront. With one wavefront and one split per
 // group (exact mode) every output is the reference's single fma chain.
 //
 // The greedy head (argmax epilogue) runs a grid-stride loop over row groups
@@ -39,8 +43,7 @@ namespace {
 typedef Q35_V4I v4i;
 
 constexpr int kRowsPerGroup = 64;
-constexpr int kChunk = 8;          // blocks per wavefront held in flight
-constexpr int kMaxWaves = 16;
+constexpr int kMaxWaves = 4;
 constexpr long kMinus8 = static_cast<long>(0xF8F8F8F8F8F8F8F8ull);  // int8 -8 x 8
 
 __device__ __forceinline__ long unpack_word(uint32_t w) {
@@ -49,31 +52,49 @@ __device__ __forceinline__ long unpack_word(uint32_t w) {
   return static_cast<long>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-template <bool ARGMAX, bool DOTS>
-__global__ __launch_bounds__(1024) void gemm_kernel(GemmArgs a) {
-  Q35_DYNAMIC_SHARED(float, smem);
+// Stores four consecutive rows of one token.
+__device__ __forceinline__ void store_row4(float *dst, bool vec, float v0, float v1, float v2, float v3) {
+  if (vec) {
+    *reinterpret_cast<q35_f32x4 *>(dst) = q35_f32x4{v0, v1, v2, v3};
+  } else {
+    dst[0] = v0;
+    dst[1] = v1;
+    dst[2] = v2;
+    dst[3] = v3;
+  }
+}
+
+template <int KS, bool ARGMAX, bool DOTS>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
+  Q35_DYNAMIC_SHARED(float, red);  // [W][16][64] wave partials, then [16] argmax keys
   const int W = static_cast<int>(blockDim.x) >> 6;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int G = lane >> 4, c = lane & 15, h = c & 1, T = c >> 1;
   const int nb = a.nb, ntiles = a.rows >> 3;
   const int groups = (ntiles + 7) >> 3;
-  float *act_scale = smem;                  // [nb][16] scales of the token tile
-  float *red = smem + nb * 16;              // [W][a.red_tokens][64] wave partials
-  unsigned long long *best = reinterpret_cast<unsigned long long *>(red + W * a.red_tokens * 64);  // [16]
+  const int S = gridDim.y, split = blockIdx.y;
+  unsigned long long *best = reinterpret_cast<unsigned long long *>(red + W * 16 * 64);
 
-  const int per = a.exact ? nb : (nb + W - 1) / W;
-  const int b0 = min(nb, wave * per), b1 = min(nb, b0 + per);
-  const int token_tiles = (a.tokens + 15) >> 4;
-  const uint8_t *wbase = reinterpret_cast<const uint8_t *>(a.w);
-
-  // a wavefront with an empty block range (never produced by gemm_shape, kept
-  // safe) reads block 0 and contributes nothing
+  // this wavefront's block range: split of the K range, then 1/W of it
+  const int sb0 = (split * nb) / S, sb1 = ((split + 1) * nb) / S;
+  const int per = (sb1 - sb0 + W - 1) / W;
+  const int b0 = min(sb1, sb0 + wave * per), b1 = min(sb1, b0 + per);
+  // a wavefront with an empty range (never planned, kept safe) reads block 0
+  // and contributes nothing
   const bool has_blocks = b0 < b1;
   const int bl = has_blocks ? b1 - 1 : 0;
+  const int token_tiles = (a.tokens + 15) >> 4;
+  const uint8_t *wbase = reinterpret_cast<const uint8_t *>(a.w);
+  const bool vec_out = (a.stride & 3) == 0;
 
   for (int tt = 0; tt < token_tiles; ++tt) {
     const uint64_t *acodes = a.codes + static_cast<size_t>(tt) * nb * 64 + lane;
-    bool staged = false;
+    const float *ascale = a.scales + static_cast<size_t>(tt) * nb * 16 + 4 * G;
+    unsigned long long run_best[4] = {0ull, 0ull, 0ull, 0ull};  // single-wave argmax
+    if (ARGMAX && W > 1) {
+      __syncthreads();
+      if (threadIdx.x < 16) best[threadIdx.x] = 0ull;
+    }
     for (int g = blockIdx.x; g < groups; g += gridDim.x) {
       float acc[4][4];
 #pragma unroll
@@ -86,36 +107,26 @@ __global__ __launch_bounds__(1024) void gemm_kernel(GemmArgs a) {
       const uint8_t *qrow = wbase + static_cast<size_t>(rt) * nb * 144 + 16 + 16 * (2 * G + h);
       const uint8_t *drow = wbase + static_cast<size_t>(rt) * nb * 144 + 8 * h;
 
-      for (int cb = has_blocks ? b0 : 0; cb < (has_blocks ? b1 : 1); cb += kChunk) {
+      for (int cb = has_blocks ? b0 : 0; cb < (has_blocks ? b1 : 1); cb += KS) {
         // all loads of the chunk first (indices clamped into the wave's
         // range, so no load is predicated), then the MFMAs
-        q35_u32x4 q[kChunk];
-        q35_u32x2 d[kChunk];
-        long act[kChunk];
+        q35_u32x4 q[KS];
+        q35_u32x2 d[KS];
+        long act[KS];
+        q35_f32x4 sa[KS];
 #pragma unroll
-        for (int i = 0; i < kChunk; ++i) {
+        for (int i = 0; i < KS; ++i) {
           const size_t b = static_cast<size_t>(min(cb + i, bl));
-          q[i] = Q35_LOAD_NT(reinterpret_cast<const q35_u32x4 *>(qrow + b * 144));
-          d[i] = Q35_LOAD_NT(reinterpret_cast<const q35_u32x2 *>(drow + b * 144));
+          q[i] = *reinterpret_cast<const q35_u32x4 *>(qrow + b * 144);
+          d[i] = *reinterpret_cast<const q35_u32x2 *>(drow + b * 144);
           act[i] = static_cast<long>(acodes[b * 64]);
-        }
-        if (!staged) {
-          // the activation scales of this token tile, staged while the first
-          // chunk's weights are in flight (every wavefront reaches this point
-          // once per token tile: its first chunk of its first group)
-          staged = true;
-          __syncthreads();
-          for (int i = threadIdx.x; i < nb * 16; i += blockDim.x)
-            act_scale[i] = a.params[static_cast<size_t>(tt) * nb * 16 + i].scale;
-          if (ARGMAX && threadIdx.x < 16) best[threadIdx.x] = 0ull;
-          __syncthreads();
+          sa[i] = *reinterpret_cast<const q35_f32x4 *>(ascale + b * 16);
         }
 #pragma unroll
-        for (int i = 0; i < kChunk; ++i) {
+        for (int i = 0; i < KS; ++i) {
           // a padded slot past the wave's range re-reads its last block; a
           // zero row scale makes its contribution exactly +0 (acc is never -0)
           const bool valid = has_blocks && cb + i < b1;
-          const int b = valid ? cb + i : bl;
           if (!valid) d[i] = q35_u32x2{0u, 0u};
           const v4i zero = {0, 0, 0, 0};
           const v4i corr = Q35_MFMA_I32_16X16X32_I8(act[i], kMinus8, zero, 0, 0, 0);
@@ -124,8 +135,6 @@ __global__ __launch_bounds__(1024) void gemm_kernel(GemmArgs a) {
           D[1] = Q35_MFMA_I32_16X16X32_I8(act[i], unpack_word(q[i][1]), corr, 0, 0, 0);
           D[2] = Q35_MFMA_I32_16X16X32_I8(act[i], unpack_word(q[i][2]), corr, 0, 0, 0);
           D[3] = Q35_MFMA_I32_16X16X32_I8(act[i], unpack_word(q[i][3]), corr, 0, 0, 0);
-          const float *sp = act_scale + b * 16 + 4 * G;
-          const float sa[4] = {sp[0], sp[1], sp[2], sp[3]};
           const float dw[4] = {half_bits_to_float(static_cast<uint16_t>(d[i][0] & 0xffffu)),
                                half_bits_to_float(static_cast<uint16_t>(d[i][0] >> 16)),
                                half_bits_to_float(static_cast<uint16_t>(d[i][1] & 0xffffu)),
@@ -134,9 +143,10 @@ __global__ __launch_bounds__(1024) void gemm_kernel(GemmArgs a) {
           for (int r = 0; r < 4; ++r)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-              acc[r][j] = fmaf(static_cast<float>(D[r][j]), dw[r] * sa[j], acc[r][j]);
+              acc[r][j] = fmaf(static_cast<float>(D[r][j]), dw[r] * sa[i][j], acc[r][j]);
           if constexpr (DOTS) {
             if (!valid) continue;
+            const int b = cb + i;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               const int tok = tt * 16 + 4 * G + j;
@@ -152,54 +162,113 @@ __global__ __launch_bounds__(1024) void gemm_kernel(GemmArgs a) {
         }
       }
 
-      // Fixed-order sum of the wavefronts' partials, then the epilogue. The
-      // token range is reduced in passes of red_tokens tokens (16 or 8) to
-      // bound LDS.
-      for (int t0 = 0; t0 < 16; t0 += a.red_tokens) {
-        if (4 * G >= t0 && 4 * G < t0 + a.red_tokens) {
+      if (ARGMAX && W == 1) {
+        // one wavefront: penalty, then the best key of tokens 4G..4G+3 over
+        // this lane's four rows and the 16 lanes sharing G
+        const int row0 = g * kRowsPerGroup + 4 * c;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            float *dst = red + (static_cast<size_t>(wave) * a.red_tokens + (4 * G + j - t0)) * 64 + 4 * c;
+        for (int j = 0; j < 4; ++j) {
+          const int tok = tt * 16 + 4 * G + j;
+          unsigned long long key = 0ull;
+          if (tok < a.tokens) {
+            const float pen = a.penalties != nullptr ? a.penalties[tok] : 1.0F;
+            const long long crow = a.count_rows != nullptr ? a.count_rows[tok] : tok;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) dst[r] = acc[r][j];
+            for (int r = 0; r < 4; ++r) {
+              const int row = row0 + r;
+              if (row >= a.rows) continue;
+              float val = acc[r][j];
+              if (pen > 1.0F && a.counts != nullptr && a.counts[crow * a.counts_stride + row] > 0)
+                val = val > 0.0F ? val / pen : val * pen;
+              const unsigned long long k = argmax_key(val, static_cast<uint32_t>(row));
+              key = k > key ? k : key;
+            }
+          }
+#pragma unroll
+          for (int m = 1; m < 16; m <<= 1) {
+            const unsigned long long o = __shfl_xor(key, m, 64);
+            key = o > key ? o : key;
+          }
+          run_best[j] = key > run_best[j] ? key : run_best[j];
+        }
+        continue;
+      }
+      if (!ARGMAX && W == 1) {
+        // one wavefront: store straight from registers (rows 4c..4c+3 of
+        // tokens 4G..4G+3)
+        const int row = g * kRowsPerGroup + 4 * c;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int tok = tt * 16 + 4 * G + j;
+          if (tok >= a.tokens || row >= a.rows) continue;
+          if (S > 1) {
+            float *dst = a.partials + (static_cast<size_t>(split) * a.tokens + tok) * a.rows + row;
+            store_row4(dst, true, acc[0][j], acc[1][j], acc[2][j], acc[3][j]);
+          } else if (a.out != nullptr) {
+            const size_t o = static_cast<size_t>(tok) * a.stride + row;
+            float v[4] = {acc[0][j], acc[1][j], acc[2][j], acc[3][j]};
+            if (a.residual != nullptr)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) v[r] = a.residual[o + r] + v[r];
+            store_row4(a.out + o, vec_out, v[0], v[1], v[2], v[3]);
           }
         }
-        __syncthreads();
-        for (int e = threadIdx.x; e < a.red_tokens * 64; e += blockDim.x) {
-          const int t = e >> 6, r = e & 63;
-          float s = red[static_cast<size_t>(t) * 64 + r];
-          for (int w = 1; w < W; ++w) s += red[(static_cast<size_t>(w) * a.red_tokens + t) * 64 + r];
-          const int tok = tt * 16 + t0 + t, row = g * kRowsPerGroup + r;
-          if constexpr (!ARGMAX) {
-            if (tok < a.tokens && row < a.rows && a.out != nullptr) {
+        continue;
+      }
+
+      // Fixed-order sum of the wavefronts' partials, then the epilogue.
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float *dst = red + (static_cast<size_t>(wave) * 16 + (4 * G + j)) * 64 + 4 * c;
+        *reinterpret_cast<q35_f32x4 *>(dst) = q35_f32x4{acc[0][j], acc[1][j], acc[2][j], acc[3][j]};
+      }
+      __syncthreads();
+      for (int e = threadIdx.x; e < 16 * 64; e += blockDim.x) {
+        const int t = e >> 6, r = e & 63;
+        float s = red[static_cast<size_t>(t) * 64 + r];
+        for (int w = 1; w < W; ++w) s += red[(static_cast<size_t>(w) * 16 + t) * 64 + r];
+        const int tok = tt * 16 + t, row = g * kRowsPerGroup + r;
+        if constexpr (!ARGMAX) {
+          if (tok < a.tokens && row < a.rows) {
+            if (S > 1) {
+              a.partials[(static_cast<size_t>(split) * a.tokens + tok) * a.rows + row] = s;
+            } else if (a.out != nullptr) {
               const size_t o = static_cast<size_t>(tok) * a.stride + row;
               a.out[o] = a.residual != nullptr ? a.residual[o] + s : s;
             }
-          } else {
-            // greedy head: repetition penalty, then the per-token best key of
-            // this group (all 64 lanes of a wave share t)
-            unsigned long long key = 0ull;
-            if (tok < a.tokens && row < a.rows) {
-              float val = s;
-              const float pen = a.penalties != nullptr ? a.penalties[tok] : 1.0F;
-              if (pen > 1.0F && a.counts != nullptr) {
-                const long long crow = a.count_rows != nullptr ? a.count_rows[tok] : tok;
-                if (a.counts[crow * a.counts_stride + row] > 0) val = val > 0.0F ? val / pen : val * pen;
-              }
-              key = argmax_key(val, static_cast<uint32_t>(row));
-            }
-#pragma unroll
-            for (int m = 32; m >= 1; m >>= 1) {
-              const unsigned long long o = __shfl_xor(key, m, 64);
-              key = o > key ? o : key;
-            }
-            if (lane == 0 && key > best[t0 + t]) best[t0 + t] = key;
           }
+        } else {
+          // greedy head: repetition penalty, then the per-token best key of
+          // this group (all 64 lanes of a wave share t)
+          unsigned long long key = 0ull;
+          if (tok < a.tokens && row < a.rows) {
+            float val = s;
+            const float pen = a.penalties != nullptr ? a.penalties[tok] : 1.0F;
+            if (pen > 1.0F && a.counts != nullptr) {
+              const long long crow = a.count_rows != nullptr ? a.count_rows[tok] : tok;
+              if (a.counts[crow * a.counts_stride + row] > 0) val = val > 0.0F ? val / pen : val * pen;
+            }
+            key = argmax_key(val, static_cast<uint32_t>(row));
+          }
+#pragma unroll
+          for (int m = 32; m >= 1; m >>= 1) {
+            const unsigned long long o = __shfl_xor(key, m, 64);
+            key = o > key ? o : key;
+          }
+          if (lane == 0 && key > best[t]) best[t] = key;
         }
-        __syncthreads();
       }
+      __syncthreads();
     }
-    if (ARGMAX) {
+    if (ARGMAX && W == 1) {
+      if (c == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int tok = tt * 16 + 4 * G + j;
+          if (tok < a.tokens) a.cand[static_cast<size_t>(blockIdx.x) * a.cand_stride + tok] = run_best[j];
+        }
+      }
+    } else if (ARGMAX) {
       __syncthreads();
       if (threadIdx.x < 16) {
         const int tok = tt * 16 + threadIdx.x;
@@ -231,58 +300,83 @@ __global__ __launch_bounds__(64) void argmax_finalize_kernel(const unsigned long
   }
 }
 
-struct GemmShape {
-  int waves, grid, red_tokens;
-  size_t smem;
-};
-
-GemmShape gemm_shape(const GemmArgs &a, int cu_count) {
-  GemmShape s{};
-  const int groups = (a.rows / 8 + 7) / 8;
-  s.waves = a.exact ? 1 : std::min(kMaxWaves, std::max(1, (a.nb + kChunk - 1) / kChunk));
-  const bool argmax = a.cand != nullptr;
-  const int cus = cu_count > 0 ? cu_count : 256;
-  s.grid = argmax ? std::min(groups, a.cand_capacity > 0 ? a.cand_capacity : 4 * cus) : groups;
-  s.red_tokens = 16;
-  auto bytes = [&](int red_tokens) {
-    return (static_cast<size_t>(a.nb) * 16 + static_cast<size_t>(s.waves) * red_tokens * 64) * 4 + 16 * 8;
-  };
-  s.smem = bytes(16);
-  if (s.smem > 65536) {
-    s.red_tokens = 8;
-    s.smem = bytes(8);
-  }
-  return s;
+// out[t][row] = (residual +) the split partial rows summed in split order;
+// used where no consumer kernel folds the reduction in (kernel-level entries).
+__global__ void split_reduce_kernel(SplitRows src, int tokens, float *out, int stride, const float *residual) {
+  const int row = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
+  if (row >= src.width || t >= tokens) return;
+  const size_t o = static_cast<size_t>(t) * stride + row;
+  const float v = src.at(t, row);
+  out[o] = residual != nullptr ? residual[o] + v : v;
 }
 
 }  // namespace
 
-int gemm_argmax_grid(int rows, int cu_count) {
-  const int groups = (rows / 8 + 7) / 8;
-  return std::min(groups, 4 * (cu_count > 0 ? cu_count : 256));
+hipError_t launch_split_reduce(const SplitRows &src, int tokens, float *out, int stride, const float *residual,
+                               hipStream_t stream) {
+  if (tokens <= 0 || src.width <= 0) return hipSuccess;
+  Q35_LAUNCH((split_reduce_kernel), dim3((src.width + 255) / 256, tokens), dim3(256), 0, stream, src, tokens, out,
+             stride, residual);
+  return hipGetLastError();
 }
 
-bool gemm_shape_supported(int rows, int nb, bool exact) {
-  if (rows <= 0 || rows % 8 != 0 || nb <= 0) return false;
-  GemmArgs a;
-  a.rows = rows;
-  a.nb = nb;
-  a.exact = exact;
-  return gemm_shape(a, 256).smem <= 65536;
+GemmPlan gemm_plan(int rows, int nb, bool exact, bool argmax, int cu_count, int force_ks, int force_split) {
+  GemmPlan p{};
+  const int groups = (rows / 8 + 7) / 8;
+  const int cus = cu_count > 0 ? cu_count : 256;
+  if (exact) {
+    p.ks = 8;
+    p.waves = 1;
+    p.split = 1;
+    p.grid = groups;
+  } else if (argmax) {
+    // one wavefront per workgroup walking whole row groups (all K chunks),
+    // several workgroups per CU to hide the chunk latency
+    p.ks = 8;
+    p.waves = 1;
+    p.split = 1;
+    p.grid = std::min(groups, 8 * cus);
+  } else {
+    // one wavefront per workgroup; K split across workgroups in chunks of 8
+    // blocks when the row groups alone give >= 64 workgroups, else of 4
+    // blocks (narrow outputs: more, shallower splits)
+    p.ks = force_ks > 0 ? force_ks : (groups >= 64 ? 8 : 4);
+    const int chunks = (nb + p.ks - 1) / p.ks;
+    p.split = force_split > 0 ? std::min(force_split, chunks) : std::min(chunks, 32);
+    const int per_split = (chunks + p.split - 1) / p.split;
+    p.waves = force_split > 0 ? std::min(kMaxWaves, per_split) : 1;
+    p.grid = groups;
+  }
+  p.smem = (static_cast<size_t>(p.waves) * 16 * 64) * 4 + 16 * 8;
+  return p;
+}
+
+int gemm_argmax_grid(int rows, int cu_count) {
+  return gemm_plan(rows, 32, false, true, cu_count, 0, 0).grid;
+}
+
+size_t gemm_partial_floats(int rows, int nb, int tokens, int cu_count) {
+  const GemmPlan p = gemm_plan(rows, nb, false, false, cu_count, 0, 0);
+  return p.split > 1 ? static_cast<size_t>(p.split) * tokens * rows : 0;
 }
 
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t stream) {
   if (a.tokens <= 0 || a.rows <= 0) return hipSuccess;
-  const GemmShape s = gemm_shape(a, a.cu_count);
-  if (s.smem > 65536) return hipErrorInvalidValue;
-  GemmArgs b = a;
-  b.red_tokens = s.red_tokens;
-  if (a.cand != nullptr) {
-    Q35_LAUNCH((gemm_kernel<true, false>), dim3(s.grid), dim3(64 * s.waves), s.smem, stream, b);
+  const bool argmax = a.cand != nullptr;
+  const bool exact = a.exact || a.block_dots != nullptr;
+  const GemmPlan p = gemm_plan(a.rows, a.nb, exact, argmax, a.cu_count, a.force_ks, a.force_split);
+  // a split plan writes [split][tokens][rows] partials; a single split writes `out`
+  if ((p.split > 1 && a.partials == nullptr) || (p.split == 1 && a.out == nullptr && !argmax && a.block_dots == nullptr))
+    return hipErrorInvalidValue;
+  const dim3 grid(p.grid, p.split), block(64 * p.waves);
+  if (argmax) {
+    Q35_LAUNCH((gemm_kernel<8, true, false>), grid, block, p.smem, stream, a);
   } else if (a.block_dots != nullptr) {
-    Q35_LAUNCH((gemm_kernel<false, true>), dim3(s.grid), dim3(64 * s.waves), s.smem, stream, b);
+    Q35_LAUNCH((gemm_kernel<8, false, true>), grid, block, p.smem, stream, a);
+  } else if (p.ks == 4) {
+    Q35_LAUNCH((gemm_kernel<4, false, false>), grid, block, p.smem, stream, a);
   } else {
-    Q35_LAUNCH((gemm_kernel<false, false>), dim3(s.grid), dim3(64 * s.waves), s.smem, stream, b);
+    Q35_LAUNCH((gemm_kernel<8, false, false>), grid, block, p.smem, stream, a);
   }
   return hipGetLastError();
 }

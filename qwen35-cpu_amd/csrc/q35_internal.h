@@ -42,86 +42,115 @@ static_assert(offsetof(q35_q8_0_block_x1, qs) == 6, "Q8_0BlockX1 layout");
 // Prepared activations in the layout the MFMA GEMM consumes ("A16"): for each
 // 16-token tile and 32-column block, 64 lanes x 8 bytes where lane l carries
 // token (l % 16) and columns 8*(l/16) .. 8*(l/16)+7 of the block; plus one
-// ActParam per token: the FP32 activation scale (binary16-rounded, with the
-// H128 1/sqrt(128) folded in exactly as the reference does) and -8 * sum of
-// the int8 codes (the offset-binary correction of q4_dot4_simd.inl:89).
-struct ActParam {
-  float scale;
-  int32_t corr;
-};
-
+// FP32 scale per (tile, block, token): the binary16-rounded activation scale
+// with the H128 1/sqrt(128) folded in exactly as the reference does. The int8
+// code sums the reference keeps beside each block (the offset-binary
+// correction of q4_dot4_simd.inl:89) are re-derived by the GEMM with an MFMA.
 constexpr float kH128InvSqrt = 0.08838834764831844055F;  // q4_h128.h:24
 constexpr int kMaxTokens = 64;                            // rows per GEMM launch
 
 // ------------------------------------------------------------ launchers
 // All launchers enqueue on `stream` and return hipSuccess or the launch error.
 
-// Activation preparation source modes.
+// Rows of a GEMM output that may still be split along K: the consumer adds
+// the `splits` partial rows in split order (deterministic).
+struct SplitRows {
+  const float *p = nullptr;   // [splits][tokens][width]
+  int splits = 1;
+  long long split_stride = 0; // tokens * width
+  int width = 0;              // floats per token row
+  __device__ __forceinline__ float at(int t, int col) const {
+    const float *q = p + static_cast<long long>(t) * width + col;
+    float v = q[0];
+    for (int s = 1; s < splits; ++s) v += q[s * split_stride];
+    return v;
+  }
+};
+
+// Activation preparation source modes (one wavefront per token and 128-column block).
 enum PrepSource : int {
   kPrepPlain = 0,      // y = x
-  kPrepRmsNorm = 1,    // y = rms_norm(x, w, eps, offset 1)   (prefill.inl:3-14)
-  kPrepSiluMul = 2,    // y = silu(gate) * up, gate/up = halves of a 2K row
-  kPrepAttnMerge = 3,  // y = merged split-K attention partials * sigmoid(gate)
+  kPrepSiluMul = 2,    // y = silu(gate) * up, gate/up = halves of a split 2K-wide row
 };
 
 struct PrepArgs {
   int source = kPrepPlain;
-  const float *x = nullptr;      // [tokens][x_stride]
+  const float *x = nullptr;      // plain: [tokens][x_stride]
   int x_stride = 0;
-  const float *weight = nullptr; // RMSNorm weight [K]
-  float eps = 1e-6F;
-  float weight_offset = 1.0F;
-  // attention merge inputs
-  const float *part_o = nullptr;   // [tokens][heads][splits][head_dim]
-  const float *part_ml = nullptr;  // [tokens][heads][splits][2] (max, sum)
-  const int32_t *seq_lens = nullptr;
-  const float *gates = nullptr;    // [tokens][heads][head_dim]
-  int heads = 0, head_dim = 0, max_splits = 0, split_tokens = 0;
+  SplitRows gate_up;             // silu: [splits][tokens][2K]
   // output
   int tokens = 0, K = 0;
   bool h128 = true;
   uint64_t seed = 0;
   uint64_t *codes = nullptr;       // A16 layout
-  ActParam *params = nullptr;
+  float *scales = nullptr;
   q35_q8_0_block_x4 *x4 = nullptr; // reference X4 layout (optional)
   q35_q8_0_block_x1 *x1 = nullptr; // reference X1 layout (optional)
-  float *normed_out = nullptr;     // optional copy of y [tokens][K]
 };
 hipError_t launch_prep(const PrepArgs &a, hipStream_t stream);
 
+// Residual update + RMSNorm(1 + w) + activation preparation, one workgroup per
+// token: x_out = x_in + sum of the split partial rows (when given),
+// y = rms_norm(x_out) (prefill.inl:3-14), then H128 (or identity) int8
+// quantization into A16; normed_out optionally keeps y.
+struct RmsPrepArgs {
+  const float *x_in = nullptr;   // [tokens][K]
+  SplitRows add;                 // optional split partial rows to add (add.p == nullptr: none)
+  float *x_out = nullptr;        // new residual rows (required when add.p != nullptr)
+  const float *weight = nullptr; // RMSNorm weight [K]
+  float eps = 1e-6F;
+  int tokens = 0, K = 0;
+  bool h128 = true;
+  uint64_t seed = 0;
+  uint64_t *codes = nullptr;
+  float *scales = nullptr;
+  float *normed_out = nullptr;   // optional [tokens][K]
+};
+hipError_t launch_rms_prep(const RmsPrepArgs &a, hipStream_t stream);
+
+
 // Converts reference X4 blocks into the A16 layout (kernel-level matmul entry).
 hipError_t launch_x4_to_a16(const q35_q8_0_block_x4 *x4, int tokens, int nb, uint64_t *codes,
-                            ActParam *params, hipStream_t stream);
+                            float *scales, hipStream_t stream);
 hipError_t launch_x1_to_a16(const q35_q8_0_block_x1 *x1, int nb, uint64_t *codes,
-                            ActParam *params, hipStream_t stream);
+                            float *scales, hipStream_t stream);
 
 struct GemmArgs {
   const q35_q4_0_block_x8 *w = nullptr;
   int rows = 0, nb = 0;            // rows % 8 == 0
   const uint64_t *codes = nullptr; // A16 [token_tile][nb][64]
-  const ActParam *params = nullptr;// [token_tile][nb][16]
+  const float *scales = nullptr;   // [token_tile][nb][16]
   int tokens = 0;                  // valid tokens
-  float *out = nullptr;            // [tokens][stride]
+  float *out = nullptr;            // [tokens][stride] (single split)
   int stride = 0;
   const float *residual = nullptr; // optional, added in the epilogue, [tokens][stride]
+  float *partials = nullptr;       // [split][tokens][rows] when the plan splits K
   int32_t *block_dots = nullptr;   // parity hook: [tokens][rows][nb]
   bool exact = false;              // one wavefront per row group runs all blocks
   // greedy head mode: per-workgroup best (penalised value, lowest index) keys
   unsigned long long *cand = nullptr;  // [grid][cand_stride]
   int cand_stride = 0;
-  int cand_capacity = 0;           // workgroups the cand buffer holds (0 = default grid)
   const int32_t *counts = nullptr;  // [rows of counts][counts_stride]
   const int32_t *count_rows = nullptr; // optional per-token row index into counts
   long long counts_stride = 0;
   const float *penalties = nullptr;
   int cu_count = 0;
-  int red_tokens = 16;             // set by the launcher
+  int force_ks = 0, force_split = 0;  // plan overrides (0 = automatic)
 };
+// Launch plan of one GEMM: blocks per wavefront chunk, wavefronts per
+// workgroup, K splits across workgroups, workgroups along the rows, LDS bytes.
+struct GemmPlan {
+  int ks, waves, split, grid;
+  size_t smem;
+};
+GemmPlan gemm_plan(int rows, int nb, bool exact, bool argmax, int cu_count, int force_ks, int force_split);
 // Workgroups of the greedy head launch (= candidate rows per token).
 int gemm_argmax_grid(int rows, int cu_count);
-// Whether launch_gemm handles this matrix shape (LDS bound).
-bool gemm_shape_supported(int rows, int nb, bool exact);
+// Floats of partial sums a split launch writes (0 when it does not split).
+size_t gemm_partial_floats(int rows, int nb, int tokens, int cu_count);
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t stream);
+hipError_t launch_split_reduce(const SplitRows &src, int tokens, float *out, int stride, const float *residual,
+                               hipStream_t stream);
 hipError_t launch_argmax_finalize(const unsigned long long *cand, int ncand, int cand_stride, int tokens,
                                   int32_t *index, float *value, hipStream_t stream);
 
@@ -137,8 +166,7 @@ struct DeltaArgs {
   const float *q = nullptr, *k = nullptr, *v = nullptr, *alpha = nullptr, *beta = nullptr;
   float *out = nullptr;            // raw: [batch][v_heads][vd]; fused: core [batch][v_heads*vd]
   // fused mode inputs
-  const float *proj = nullptr;     // [batch][proj_stride] = [qkv | z | b | a]
-  int proj_stride = 0;
+  SplitRows proj;                  // [splits][batch][in_rows] = [qkv | z | b | a]
   float *conv_base = nullptr;      // slot-strided conv ring [kernel][channels], slot = position % kernel
   long long conv_slot_stride = 0;
   const int32_t *positions = nullptr;
@@ -149,15 +177,14 @@ struct DeltaArgs {
   // fused mode: the gated outputs prepared as A16 activations of the out
   // projection (H128 block = value head); `out` (FP32) is optional then
   uint64_t *codes = nullptr;
-  ActParam *params = nullptr;
+  float *scales = nullptr;
   uint64_t seed = 0;
 };
 hipError_t launch_delta(const DeltaArgs &a, hipStream_t stream);
 
 // Full attention
 struct AttnPrepArgs {
-  const float *proj = nullptr;  // [batch][proj_stride] = [q|gate interleaved per head | k | v]
-  int proj_stride = 0;
+  SplitRows proj;               // [splits][batch][in_rows] = [q|gate interleaved per head | k | v]
   int batch = 0, heads = 0, kv_heads = 0, head_dim = 0, rope_dim = 0;
   const float *q_norm = nullptr, *k_norm = nullptr;
   float eps = 1e-6F;
@@ -185,11 +212,11 @@ struct AttnArgs {
 };
 hipError_t launch_attention(const AttnArgs &a, hipStream_t stream);
 // Merge of the chunk partials + sigmoid gate: FP32 rows into `out` and/or the
-// o projection's A16 activations into codes/params (either may be null).
+// o projection's A16 activations into codes/scales (either may be null).
 // split_tokens must be kAttnChunkTokens.
 constexpr int kAttnChunkTokens = 64;
 hipError_t launch_attention_merge(const AttnArgs &a, const float *gates, float *out, uint64_t *codes,
-                                  ActParam *params, uint64_t seed, hipStream_t stream);
+                                  float *scales, uint64_t seed, hipStream_t stream);
 
 // Elementwise / small ops (kernel-level entries and the step)
 hipError_t launch_rms_norm(const float *x, const float *w, float *y, int rows, int width,

@@ -18,7 +18,7 @@ namespace q35 {
 
 struct QuantOut {
   uint64_t *codes = nullptr;        // A16 [token_tile][nb][64]
-  ActParam *params = nullptr;       // [token_tile][nb][16]
+  float *scales = nullptr;       // [token_tile][nb][16]
   q35_q8_0_block_x4 *x4 = nullptr;  // reference X4 layout (optional)
   q35_q8_0_block_x1 *x1 = nullptr;  // reference X1 layout (optional)
 };
@@ -67,7 +67,7 @@ __device__ __forceinline__ void h128_quantize_block(float v0, float v1, int lane
       uint8_t *dst = reinterpret_cast<uint8_t *>(o.codes);
       const size_t word = (static_cast<size_t>(tile) * nb + b) * 64 + tok + 16 * (k >> 3);
       dst[word * 8 + (k & 7)] = static_cast<uint8_t>(static_cast<int8_t>(code));
-      if (k == 0) o.params[(static_cast<size_t>(tile) * nb + b) * 16 + tok] = ActParam{stored, -8 * sum};
+      if (k == 0) o.scales[(static_cast<size_t>(tile) * nb + b) * 16 + tok] = stored;
     }
     if (o.x4 != nullptr) {
       q35_q8_0_block_x4 &blkx = o.x4[static_cast<size_t>(t >> 2) * nb + b];

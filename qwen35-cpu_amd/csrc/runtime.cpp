@@ -254,49 +254,62 @@ int matmul_entry(q35_context *ctx, const q35_q4_0_block_x8 *m, const q35_q8_0_bl
       blocks > (1u << 16) || (out != nullptr && stride < rows))
     return set_error(ctx, Q35_ERR_INVALID, "invalid DOT4 geometry");
   const int nb = static_cast<int>(blocks);
-  if (!gemm_shape_supported(static_cast<int>(rows), nb, exact))
-    return set_error(ctx, Q35_ERR_UNSUPPORTED, "DOT4 block count beyond the kernel's LDS budget");
   const size_t chunk = kMaxTokens;
   const size_t code_bytes = align256(4 * 64 * static_cast<size_t>(nb) * sizeof(uint64_t));
-  const size_t param_bytes = align256(4 * 16 * static_cast<size_t>(nb) * sizeof(ActParam));
+  const size_t scale_bytes = align256(4 * 16 * static_cast<size_t>(nb) * sizeof(float));
   const int grid = gemm_argmax_grid(static_cast<int>(rows), ctx->cu_count);
   const size_t cand_bytes = index != nullptr ? align256(static_cast<size_t>(grid) * kMaxTokens * 8) : 0;
+  const size_t part_bytes =
+      align256(gemm_partial_floats(static_cast<int>(rows), nb, static_cast<int>(chunk), ctx->cu_count) * 4);
   void *scratch = nullptr;
-  int st = scratch_get(ctx, code_bytes + param_bytes + cand_bytes, &scratch);
+  int st = scratch_get(ctx, code_bytes + scale_bytes + cand_bytes + part_bytes, &scratch);
   if (st != Q35_OK) return st;
-  auto *codes = reinterpret_cast<uint64_t *>(scratch);
-  auto *params = reinterpret_cast<ActParam *>(static_cast<char *>(scratch) + code_bytes);
-  auto *cand = reinterpret_cast<unsigned long long *>(static_cast<char *>(scratch) + code_bytes + param_bytes);
+  char *base = static_cast<char *>(scratch);
+  auto *codes = reinterpret_cast<uint64_t *>(base);
+  auto *scales = reinterpret_cast<float *>(base + code_bytes);
+  auto *cand = reinterpret_cast<unsigned long long *>(base + code_bytes + scale_bytes);
+  auto *partials = reinterpret_cast<float *>(base + code_bytes + scale_bytes + cand_bytes);
   for (size_t t0 = 0; t0 < vectors; t0 += chunk) {
     const size_t n = std::min(chunk, vectors - t0);
     hipError_t e;
     if (x4 != nullptr)
-      e = launch_x4_to_a16(x4 + (t0 / 4) * blocks, static_cast<int>(n), nb, codes, params, ctx->stream);
+      e = launch_x4_to_a16(x4 + (t0 / 4) * blocks, static_cast<int>(n), nb, codes, scales, ctx->stream);
     else
-      e = launch_x1_to_a16(x1 + t0 * blocks, nb, codes, params, ctx->stream);
+      e = launch_x1_to_a16(x1 + t0 * blocks, nb, codes, scales, ctx->stream);
     if (e != hipSuccess) return hip_error(ctx, e, "activation layout kernel");
     GemmArgs g;
     g.w = m;
     g.rows = static_cast<int>(rows);
     g.nb = nb;
     g.codes = codes;
-    g.params = params;
+    g.scales = scales;
     g.tokens = static_cast<int>(n);
     g.out = out ? out + t0 * stride : nullptr;
     g.stride = static_cast<int>(stride);
+    g.partials = partials;
     g.block_dots = dots ? dots + t0 * rows * blocks : nullptr;
     g.exact = exact;
     g.cu_count = ctx->cu_count;
     if (index != nullptr) {
       g.cand = cand;
       g.cand_stride = kMaxTokens;
-      g.cand_capacity = grid;
       g.counts = counts ? counts + t0 * rows : nullptr;
       g.counts_stride = static_cast<long long>(rows);
       g.penalties = penalties ? penalties + t0 : nullptr;
     }
     e = launch_gemm(g, ctx->stream);
     if (e != hipSuccess) return hip_error(ctx, e, "DOT4 GEMM kernel");
+    const GemmPlan plan = gemm_plan(g.rows, nb, exact || dots != nullptr, index != nullptr, ctx->cu_count, 0, 0);
+    if (out != nullptr && plan.split > 1) {
+      SplitRows src;
+      src.p = partials;
+      src.splits = plan.split;
+      src.split_stride = static_cast<long long>(n) * rows;
+      src.width = static_cast<int>(rows);
+      e = launch_split_reduce(src, static_cast<int>(n), out + t0 * stride, static_cast<int>(stride), nullptr,
+                              ctx->stream);
+      if (e != hipSuccess) return hip_error(ctx, e, "split reduce");
+    }
     if (index != nullptr) {
       e = launch_argmax_finalize(cand, grid, kMaxTokens, static_cast<int>(n), index + t0,
                                  value ? value + t0 : nullptr, ctx->stream);

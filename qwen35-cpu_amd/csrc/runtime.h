@@ -61,11 +61,12 @@ struct q35_runtime {
   std::vector<int> free_pages;
   float *rope_cos = nullptr, *rope_sin = nullptr;
   // work buffers
-  float *x = nullptr, *proj = nullptr, *core = nullptr, *q_rot = nullptr, *gates = nullptr;
+  float *x[2] = {nullptr, nullptr};  // residual stream, ping-pong
+  float *proj = nullptr, *core = nullptr, *q_rot = nullptr, *gates = nullptr;
   float *part_o = nullptr, *part_ml = nullptr, *logits = nullptr;
   float *hidden_out = nullptr;
   uint64_t *codes = nullptr;
-  q35::ActParam *params = nullptr;
+  float *scales = nullptr;
   // greedy head: per-workgroup best keys [cand_rows][kMaxTokens]
   unsigned long long *cand = nullptr;
   int cand_rows = 0;

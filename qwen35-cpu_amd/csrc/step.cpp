@@ -327,8 +327,17 @@ extern "C" int q35_runtime_create(q35_model *m, const q35_runtime_config *cfg, q
   alloc(static_cast<size_t>(cfg->max_context) * half * 4, reinterpret_cast<void **>(&rt->rope_cos));
   alloc(static_cast<size_t>(cfg->max_context) * half * 4, reinterpret_cast<void **>(&rt->rope_sin));
   // work buffers
-  alloc(B * H * 4, reinterpret_cast<void **>(&rt->x));
-  alloc(B * rt->proj_width * 4, reinterpret_cast<void **>(&rt->proj));
+  alloc(B * H * 4, reinterpret_cast<void **>(&rt->x[0]));
+  alloc(B * H * 4, reinterpret_cast<void **>(&rt->x[1]));
+  // GEMM outputs: [split][batch][rows] for the largest split plan of any projection
+  size_t proj_floats = static_cast<size_t>(B) * rt->proj_width;
+  for (const auto &L : m->layers) {
+    proj_floats = std::max(proj_floats, gemm_partial_floats(L.in_rows, d.hidden / 32, B, ctx->cu_count));
+    proj_floats = std::max(proj_floats, gemm_partial_floats(d.hidden, L.out_cols / 32, B, ctx->cu_count));
+    proj_floats = std::max(proj_floats, gemm_partial_floats(2 * d.intermediate, d.hidden / 32, B, ctx->cu_count));
+    proj_floats = std::max(proj_floats, gemm_partial_floats(d.hidden, d.intermediate / 32, B, ctx->cu_count));
+  }
+  alloc(proj_floats * 4, reinterpret_cast<void **>(&rt->proj));
   alloc(B * rt->core_width * 4, reinterpret_cast<void **>(&rt->core));
   alloc(B * static_cast<size_t>(d.n_heads) * d.head_dim * 4, reinterpret_cast<void **>(&rt->q_rot));
   alloc(B * static_cast<size_t>(d.n_heads) * d.head_dim * 4, reinterpret_cast<void **>(&rt->gates));
@@ -338,7 +347,7 @@ extern "C" int q35_runtime_create(q35_model *m, const q35_runtime_config *cfg, q
   alloc(B * H * 4, reinterpret_cast<void **>(&rt->hidden_out));
   const size_t kmax = std::max({H, I, rt->core_width});
   alloc(4 * 64 * (kmax / 32) * 8, reinterpret_cast<void **>(&rt->codes));
-  alloc(4 * 16 * (kmax / 32) * sizeof(ActParam), reinterpret_cast<void **>(&rt->params));
+  alloc(4 * 16 * (kmax / 32) * sizeof(float), reinterpret_cast<void **>(&rt->scales));
   rt->cand_rows = gemm_argmax_grid(d.vocab, ctx->cu_count);
   alloc(static_cast<size_t>(rt->cand_rows) * kMaxTokens * 8, reinterpret_cast<void **>(&rt->cand));
   alloc(kMaxTokens * 4, reinterpret_cast<void **>(&rt->tokens_out_dev));
@@ -467,7 +476,7 @@ namespace q35 {
 
 double gemm_algorithmic_bytes(int rows, int nb, int tokens, bool stores, bool residual) {
   const double weights = static_cast<double>(rows / 8) * nb * sizeof(q35_q4_0_block_x8);
-  const double acts = static_cast<double>(tokens) * (nb * 32.0 + sizeof(ActParam));
+  const double acts = static_cast<double>(tokens) * (nb * 32.0 + sizeof(float));
   const double outs = static_cast<double>(tokens) * rows * 4.0 * ((stores ? 1 : 0) + (residual ? 1 : 0));
   return weights + acts + outs;
 }
@@ -556,51 +565,74 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
   double kv_tokens = 0;
   for (int b = 0; b < batch; ++b) kv_tokens += host_seq[b];
   // activation prep: FP32 rows in (x_cols wide), A16 codes + scales out
-  auto prep_bytes = [&](double x_cols, int K) { return B * (x_cols * 4.0 + K + sizeof(ActParam)); };
 
   Q35_STEP(hipMemcpyAsync(rt->meta_dev, rt->meta_host, rt->meta_bytes, hipMemcpyHostToDevice, s), "metadata copy");
   Q35_KERNEL(Q35_KERNEL_EMBED, B * (H / 32 * 18.0 + H * 4.0 + 8.0),
-             launch_embed(m->embed, H / 32, tokens, batch, rt->x, H, rt->counts, d.vocab, slots, count_input, s),
+             launch_embed(m->embed, H / 32, tokens, batch, rt->x[0], H, rt->counts, d.vocab, slots, count_input, s),
              "embedding");
 
-  auto prep = [&](int source, const float *x, int x_stride, const float *w, int K, bool h128) {
-    PrepArgs a;
-    a.source = source;
-    a.x = x;
-    a.x_stride = x_stride;
-    a.weight = w;
-    a.eps = d.rms_eps;
-    a.weight_offset = 1.0F;
-    a.tokens = batch;
-    a.K = K;
-    a.h128 = h128;
-    a.seed = d.sign_seed;
-    a.codes = rt->codes;
-    a.params = rt->params;
-    return a;
-  };
-  auto gemm = [&](const q35_q4_0_block_x8 *w, int rows, int K, float *out, int stride,
-                  const float *residual) {
+  // Residual stream: x[cur] holds it; a residual update writes x[cur ^ 1]
+  // (the prep kernels read whole rows, so the update cannot run in place).
+  int cur = 0;
+  // GEMM outputs land in rt->proj as [split][batch][rows]; `pending` describes
+  // the last one for its consumer.
+  SplitRows pending;
+  auto gemm = [&](const q35_q4_0_block_x8 *w, int rows, int K) -> hipError_t {
+    const GemmPlan p = gemm_plan(rows, K / 32, false, false, ctx->cu_count, 0, 0);
     GemmArgs g;
     g.w = w;
     g.rows = rows;
     g.nb = K / 32;
     g.codes = rt->codes;
-    g.params = rt->params;
+    g.scales = rt->scales;
     g.tokens = batch;
-    g.out = out;
-    g.stride = stride;
-    g.residual = residual;
+    g.out = rt->proj;
+    g.stride = rows;
+    g.partials = rt->proj;
     g.cu_count = ctx->cu_count;
+    pending.p = rt->proj;
+    pending.splits = p.split;
+    pending.split_stride = static_cast<long long>(batch) * rows;
+    pending.width = rows;
     return launch_gemm(g, s);
   };
+  // Residual update with the pending split rows (if `add`) + RMSNorm + prep.
+  auto rms_prep = [&](const float *w, bool add, bool h128, float *normed) -> hipError_t {
+    RmsPrepArgs a;
+    a.x_in = rt->x[cur];
+    if (add) {
+      a.add = pending;
+      a.x_out = rt->x[cur ^ 1];
+    }
+    a.weight = w;
+    a.eps = d.rms_eps;
+    a.tokens = batch;
+    a.K = H;
+    a.h128 = h128;
+    a.seed = d.sign_seed;
+    a.codes = rt->codes;
+    a.scales = rt->scales;
+    a.normed_out = normed;
+    const hipError_t e = launch_rms_prep(a, s);
+    if (add) cur ^= 1;
+    return e;
+  };
+  // bytes: residual row in (+ split partial rows and the new residual out),
+  // codes and scales out
+  auto rms_bytes = [&](bool add) {
+    return B * (H * 4.0 + (add ? pending.splits * H * 4.0 + H * 4.0 : 0.0) + H + H / 32.0 * 4.0) + H * 4.0;
+  };
+  auto gemm_bytes = [&](int rows, int K) {
+    const GemmPlan p = gemm_plan(rows, K / 32, false, false, ctx->cu_count, 0, 0);
+    return gemm_algorithmic_bytes(rows, K / 32, batch, true, false) + (p.split - 1) * B * rows * 4.0;
+  };
 
+  bool add_pending = false;  // the previous layer's down projection is still split
   for (int l = 0; l < d.n_layers; ++l) {
     const LayerDev &L = m->layers[l];
-    Q35_KERNEL(Q35_KERNEL_PREP, prep_bytes(H, H) + H * 4.0,
-               launch_prep(prep(kPrepRmsNorm, rt->x, H, L.input_norm, H, true), s), "input norm prep");
-    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_algorithmic_bytes(L.in_rows, H / 32, batch, true, false),
-               gemm(L.in_proj, L.in_rows, H, rt->proj, L.in_rows, nullptr), "in projection");
+    Q35_KERNEL(Q35_KERNEL_PREP, rms_bytes(add_pending), rms_prep(L.input_norm, add_pending, true, nullptr),
+               "input norm prep");
+    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(L.in_rows, H), gemm(L.in_proj, L.in_rows, H), "in projection");
     if (L.linear) {
       const int li = m->linear_index[l];
       DeltaArgs a;
@@ -613,9 +645,8 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
       a.v_heads = d.lin_v_heads;
       a.kd = d.lin_k_dim;
       a.vd = d.lin_v_dim;
-      a.out = rt->core;
-      a.proj = rt->proj;
-      a.proj_stride = L.in_rows;
+      a.out = nullptr;
+      a.proj = pending;
       a.conv_base = rt->conv + static_cast<size_t>(li) * d.lin_kernel * ch;
       a.conv_slot_stride = rt->conv_slot_stride;
       a.positions = positions;
@@ -625,21 +656,19 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
       a.ssm_a = L.ssm_a;
       a.norm_w = L.lin_norm;
       a.eps = d.rms_eps;
-      a.out = nullptr;
       a.codes = rt->codes;
-      a.params = rt->params;
+      a.scales = rt->scales;
       a.seed = d.sign_seed;
-      // recurrent state read + written, projection row in, conv ring (K-1 rows
-      // read, one written), prepared out-projection activations
+      // recurrent state read + written, projection row in (per split), conv
+      // ring (K-1 rows read, one written), prepared out-projection activations
       const double delta_bytes =
-          B * (2.0 * d.lin_v_heads * d.lin_v_dim * d.lin_k_dim * 4.0 + L.in_rows * 4.0 +
-               static_cast<double>(d.lin_kernel) * ch * 4.0 + v_dim + v_dim / 32.0 * sizeof(ActParam));
+          B * (2.0 * d.lin_v_heads * d.lin_v_dim * d.lin_k_dim * 4.0 + pending.splits * L.in_rows * 4.0 +
+               static_cast<double>(d.lin_kernel) * ch * 4.0 + v_dim + v_dim / 32.0 * 4.0);
       Q35_KERNEL(Q35_KERNEL_DELTA, delta_bytes, launch_delta(a, s), "DeltaNet");
     } else {
       const int fi = m->full_index[l];
       AttnPrepArgs p;
-      p.proj = rt->proj;
-      p.proj_stride = L.in_rows;
+      p.proj = pending;
       p.batch = batch;
       p.heads = d.n_heads;
       p.kv_heads = d.n_kv_heads;
@@ -658,9 +687,9 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
       p.v_pool = rt->v_pool + static_cast<size_t>(fi) * rt->layer_pool_elems;
       p.q_out = rt->q_rot;
       p.gate_out = rt->gates;
-      // projection row in; rotated q, gate, and the new K/V rows (FP16) out
+      // projection row in (per split); rotated q, gate, and the new K/V rows (FP16) out
       Q35_KERNEL(Q35_KERNEL_ATTN_PREP,
-                 B * (L.in_rows * 4.0 + 2.0 * d.n_heads * d.head_dim * 4.0 + 2.0 * kvw * 2.0),
+                 B * (pending.splits * L.in_rows * 4.0 + 2.0 * d.n_heads * d.head_dim * 4.0 + 2.0 * kvw * 2.0),
                  launch_attn_prep(p, s), "attention prep");
       AttnArgs a;
       a.q = rt->q_rot;
@@ -687,39 +716,54 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
                  launch_attention(a, s), "attention");
       // chunk partials and gates in, o projection A16 activations out
       Q35_KERNEL(Q35_KERNEL_PREP,
-                 splits_used * d.n_heads * (d.head_dim + 2) * 4.0 +
-                     B * d.n_heads * d.head_dim * (4.0 + 1.0) + B * d.n_heads * d.head_dim / 32.0 * sizeof(ActParam),
-                 launch_attention_merge(a, rt->gates, nullptr, rt->codes, rt->params, d.sign_seed, s),
+                 splits_used * d.n_heads * (d.head_dim + 2) * 4.0 + B * d.n_heads * d.head_dim * (4.0 + 1.0) +
+                     B * d.n_heads * d.head_dim / 32.0 * 4.0,
+                 launch_attention_merge(a, rt->gates, nullptr, rt->codes, rt->scales, d.sign_seed, s),
                  "attention merge");
     }
-    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_algorithmic_bytes(H, L.out_cols / 32, batch, true, true),
-               gemm(L.out_proj, H, L.out_cols, rt->x, H, rt->x), "out projection");
-    Q35_KERNEL(Q35_KERNEL_PREP, prep_bytes(H, H) + H * 4.0,
-               launch_prep(prep(kPrepRmsNorm, rt->x, H, L.post_norm, H, true), s), "post norm prep");
-    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_algorithmic_bytes(2 * I, H / 32, batch, true, false),
-               gemm(L.gate_up, 2 * I, H, rt->proj, 2 * I, nullptr), "gate_up projection");
-    Q35_KERNEL(Q35_KERNEL_PREP, prep_bytes(2.0 * I, I),
-               launch_prep(prep(kPrepSiluMul, rt->proj, 2 * I, nullptr, I, true), s), "silu prep");
-    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_algorithmic_bytes(H, I / 32, batch, true, true),
-               gemm(L.down, H, I, rt->x, H, rt->x), "down projection");
+    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(H, L.out_cols), gemm(L.out_proj, H, L.out_cols), "out projection");
+    Q35_KERNEL(Q35_KERNEL_PREP, rms_bytes(true), rms_prep(L.post_norm, true, true, nullptr), "post norm prep");
+    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(2 * I, H), gemm(L.gate_up, 2 * I, H), "gate_up projection");
+    PrepArgs sp;
+    sp.source = kPrepSiluMul;
+    sp.gate_up = pending;
+    sp.tokens = batch;
+    sp.K = I;
+    sp.h128 = true;
+    sp.seed = d.sign_seed;
+    sp.codes = rt->codes;
+    sp.scales = rt->scales;
+    Q35_KERNEL(Q35_KERNEL_PREP, B * (pending.splits * 2.0 * I * 4.0 + I + I / 32.0 * 4.0), launch_prep(sp, s),
+               "silu prep");
+    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(H, I), gemm(L.down, H, I), "down projection");
+    add_pending = true;
   }
-  PrepArgs fin = prep(kPrepRmsNorm, rt->x, H, m->final_norm, H, false);
-  fin.normed_out = rt->hidden_out;
-  Q35_KERNEL(Q35_KERNEL_PREP, prep_bytes(H, H) + H * 4.0 + B * H * 4.0, launch_prep(fin, s), "final norm prep");
+  Q35_KERNEL(Q35_KERNEL_PREP, rms_bytes(true) + B * H * 4.0, rms_prep(m->final_norm, true, false, rt->hidden_out),
+             "final norm prep");
   if (want_logits) {
-    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_algorithmic_bytes(d.vocab, H / 32, batch, true, false),
-               gemm(m->embed, d.vocab, H, rt->logits, d.vocab, nullptr), "logits head");
+    GemmArgs g;
+    g.w = m->embed;
+    g.rows = d.vocab;
+    g.nb = H / 32;
+    g.codes = rt->codes;
+    g.scales = rt->scales;
+    g.tokens = batch;
+    g.out = rt->logits;
+    g.stride = d.vocab;
+    g.force_split = 1;  // rt->logits holds one [batch][vocab] copy: never split K here
+    g.cu_count = ctx->cu_count;
+    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_algorithmic_bytes(d.vocab, H / 32, batch, true, false), launch_gemm(g, s),
+               "logits head");
   } else {
     GemmArgs g;
     g.w = m->embed;
     g.rows = d.vocab;
     g.nb = H / 32;
     g.codes = rt->codes;
-    g.params = rt->params;
+    g.scales = rt->scales;
     g.tokens = batch;
     g.cand = rt->cand;
     g.cand_stride = kMaxTokens;
-    g.cand_capacity = rt->cand_rows;
     g.counts = rt->counts;
     g.count_rows = slots;
     g.counts_stride = d.vocab;
