@@ -204,23 +204,25 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
 // exp(m_s - M) over all chunks (the same result as merging them pairwise with
 // merge_attention_partial, full_attention_tiled.cpp:66-78, up to rounding),
 // normalisation, and the sigmoid output gate (full_attention.cpp:104-127).
-// Wavefront b handles dims 128b + lane and 128b + 64 + lane -- one H128
-// block of the o projection's input -- and either stores the FP32 result or
-// prepares it as A16 activations.
-__global__ __launch_bounds__(128) void attention_merge_kernel(AttnArgs a, const float *gates, float *out,
-                                                             QuantOut qo, uint64_t seed) {
-  __shared__ float w_s[2][64];
-  const int h = blockIdx.x, r = blockIdx.y;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+// One wavefront per (128-dim block b, head h, request): lane j = lane % 16
+// holds dims 128b + 8j .. +7 -- one H128 block of the o projection's input --
+// and the result is stored as FP32 and/or prepared as A16 activations (the
+// four 16-lane rows compute the same values; row 0 stores).
+__global__ __launch_bounds__(64) void attention_merge_kernel(AttnArgs a, const float *gates, float *out,
+                                                            QuantOut qo, uint64_t seed) {
+  __shared__ float w_s[64];
+  const int b = blockIdx.x & 1, h = blockIdx.x >> 1, r = blockIdx.y;
+  const int lane = threadIdx.x, j = lane & 15;
   const int seq = a.seq_lens != nullptr ? a.seq_lens[r] : a.positions[r] + 1;
   const int splits = (seq + kChunkTokens - 1) / kChunkTokens;
   const size_t hs = (static_cast<size_t>(r) * a.heads + h) * a.max_splits;
-  const int d0 = 128 * wave + lane, d1 = d0 + 64;
-  float acc0 = 0.0F, acc1 = 0.0F, L = 0.0F;
+  const int d0 = 128 * b + 8 * j;
   // global max over the chunks, then their weights in batches of 64
   float M = -INFINITY;
   for (int s = lane; s < splits; s += 64) M = fmaxf(M, a.part_ml[(hs + s) * 2]);
   M = group_max<64>(M);
+  float acc[8] = {0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F};
+  float L = 0.0F;
   for (int s0 = 0; s0 < splits; s0 += 64) {
     const int cnt = min(64, splits - s0);
     float w = 0.0F, lw = 0.0F;
@@ -229,38 +231,39 @@ __global__ __launch_bounds__(128) void attention_merge_kernel(AttnArgs a, const 
       lw = w * a.part_ml[(hs + s0 + lane) * 2 + 1];
     }
     L += group_sum<64>(lw);
-    w_s[wave][lane] = w;
+    w_s[lane] = w;
     __syncthreads();
-    int s = 0;
-    for (; s + 4 <= cnt; s += 4) {
-      float o0[4], o1[4];
+    for (int s = 0; s < cnt; s += 4) {
+      q35_f32x4 o[4][2];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        o0[u] = a.part_o[(hs + s0 + s + u) * kHeadDim + d0];
-        o1[u] = a.part_o[(hs + s0 + s + u) * kHeadDim + d1];
+        const q35_f32x4 *src = reinterpret_cast<const q35_f32x4 *>(
+            a.part_o + (hs + s0 + min(s + u, cnt - 1)) * kHeadDim + d0);
+        o[u][0] = src[0];
+        o[u][1] = src[1];
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        acc0 += w_s[wave][s + u] * o0[u];
-        acc1 += w_s[wave][s + u] * o1[u];
+        if (s + u >= cnt) break;
+        const float ws = w_s[s + u];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc[e] += ws * o[u][0][e];
+          acc[4 + e] += ws * o[u][1][e];
+        }
       }
-    }
-    for (; s < cnt; ++s) {
-      acc0 += w_s[wave][s] * a.part_o[(hs + s0 + s) * kHeadDim + d0];
-      acc1 += w_s[wave][s] * a.part_o[(hs + s0 + s) * kHeadDim + d1];
     }
     __syncthreads();
   }
   const float inv = 1.0F / (L > 0.0F ? L : 1.0F);
-  const size_t o = (static_cast<size_t>(r) * a.heads + h) * kHeadDim;
-  const float y0 = (acc0 * inv) * sigmoid_stable(gates[o + d0]);
-  const float y1 = (acc1 * inv) * sigmoid_stable(gates[o + d1]);
-  if (out != nullptr) {
-    out[o + d0] = y0;
-    out[o + d1] = y1;
-  }
-  if (qo.codes != nullptr)
-    h128_quantize_block(y0, y1, lane, r, 2 * h + wave, a.heads * kHeadDim / 32, true, seed, qo);
+  const size_t o = (static_cast<size_t>(r) * a.heads + h) * kHeadDim + d0;
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = (acc[e] * inv) * sigmoid_stable(gates[o + e]);
+  if (out != nullptr && lane < 16)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[o + e] = y[e];
+  if (qo.codes != nullptr) h128_quantize_row16(y, r, 2 * h + b, a.heads * kHeadDim / 32, true, seed, qo, lane < 16);
 }
 
 }  // namespace
@@ -295,7 +298,7 @@ hipError_t launch_attention_merge(const AttnArgs &a, const float *gates, float *
   QuantOut qo;
   qo.codes = codes;
   qo.scales = scales;
-  Q35_LAUNCH((attention_merge_kernel), dim3(a.heads, a.batch), 128, 0, stream, a, gates, out, qo, seed);
+  Q35_LAUNCH((attention_merge_kernel), dim3(2 * a.heads, a.batch), 64, 0, stream, a, gates, out, qo, seed);
   return hipGetLastError();
 }
 

@@ -61,7 +61,7 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
   // ---- 2. q, k, v, gates of this head
   const int q_dim = a.k_heads * kDim, v_dim = a.v_heads * kDim;
   const int channels = 2 * q_dim + v_dim;
-  float z0 = 0.0F, z1 = 0.0F;  // output gate of columns lane, 64 + lane (wave 0)
+  float z[8] = {0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F};  // output gate, columns 8(lane%16)..+7 (wave 0)
   if constexpr (FUSED) {
     float *conv = a.conv_base + static_cast<long long>(a.slots[r]) * a.conv_slot_stride;
     const int K = a.kernel, pos = a.positions[r];
@@ -83,10 +83,7 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
     const bool is_k = tid >= kDim;
     const float y = conv_channel((is_k ? q_dim : 0) + kh * kDim + i);
     const float vv = tid < kDim ? conv_channel(2 * q_dim + vh * kDim + tid) : 0.0F;
-    if (wave == 0) {
-      z0 = a.proj.at(r, channels + vh * kDim + lane);
-      z1 = a.proj.at(r, channels + vh * kDim + 64 + lane);
-    }
+    if (wave == 0) a.proj.at8(r, channels + vh * kDim + 8 * (lane & 15), z);
     if (tid == 0) {
       const float bval = a.proj.at(r, channels + v_dim + vh);
       const float aval = a.proj.at(r, channels + v_dim + a.v_heads + vh);
@@ -165,29 +162,39 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
   }
   __syncthreads();
 
-  // ---- 4. outputs (wave 0: columns lane and 64 + lane)
+  // ---- 4. outputs: wave 0, lane j = lane % 16 holds columns 8j .. 8j+7
+  // (the four 16-lane rows compute the same values; row 0 stores)
   if (wave != 0) return;
-  float y0 = so[lane], y1 = so[64 + lane];
+  const int j = lane & 15;
+  const bool writer = lane < 16;
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = so[8 * j + e];
   if constexpr (FUSED) {
     // gated RMSNorm (offset 0) over the head, then * SiLU(z)  (layers.inl:198-207)
-    const float ss = group_sum<64>(y0 * y0 + y1 * y1);
+    float ss = 0.0F;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += y[e] * y[e];
+    ss += q35_row_xor(ss, 1);
+    ss += q35_row_xor(ss, 2);
+    ss += q35_row_xor(ss, 4);
+    ss += q35_row_xor(ss, 8);
     const float inv = 1.0F / sqrtf(ss / static_cast<float>(kDim) + a.eps);
-    y0 = silu_times(z0, y0 * inv * (a.norm_w[lane] + 0.0F));
-    y1 = silu_times(z1, y1 * inv * (a.norm_w[64 + lane] + 0.0F));
-    if (a.out != nullptr) {
-      a.out[static_cast<size_t>(r) * v_dim + vh * kDim + lane] = y0;
-      a.out[static_cast<size_t>(r) * v_dim + vh * kDim + 64 + lane] = y1;
-    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = silu_times(z[e], y[e] * inv * (a.norm_w[8 * j + e] + 0.0F));
+    if (a.out != nullptr && writer)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) a.out[static_cast<size_t>(r) * v_dim + vh * kDim + 8 * j + e] = y[e];
     if (a.codes != nullptr) {
       QuantOut qo;
       qo.codes = a.codes;
       qo.scales = a.scales;
-      h128_quantize_block(y0, y1, lane, r, vh, v_dim / 32, true, a.seed, qo);
+      h128_quantize_row16(y, r, vh, v_dim / 32, true, a.seed, qo, writer);
     }
-  } else {
-    const size_t o = (static_cast<size_t>(r) * a.v_heads + vh) * kDim;
-    a.out[o + lane] = y0;
-    a.out[o + 64 + lane] = y1;
+  } else if (writer) {
+    const size_t o = (static_cast<size_t>(r) * a.v_heads + vh) * kDim + 8 * j;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a.out[o + e] = y[e];
   }
 }
 

@@ -1,16 +1,14 @@
 // Activation preparation for the Q4-G32-DOT4 projections: the producer
 // (plain rows, SiLU(gate) * up over split GEMM partials, or residual update +
 // RMSNorm) followed by the randomized-sign Hadamard-128 rotation and per-32
-// int8 quantization (h128_quantize_block).
+// int8 quantization (h128_quantize_row16).
 //
 // Reference semantics (bit-exact given the same FP32 input):
 //   signs + FWHT stage order 1,2,...,64     src/cpu/q4_h128.cpp:35-61
 //   absmax/127, unrounded 1/scale, round half away from zero, clamp +-127,
 //   stored scale = binary16(scale) * 1/sqrt(128)   q4_0.cpp:212-235, q4_h128.cpp:319-321
-// prep_kernel: one wavefront per (token, 128-column block), four per
-// workgroup, so a 16-token step spreads over 16 x K/128 wavefronts; two
-// values per lane, the first six FWHT stages are lane shuffles and the last
-// one is in-lane. rms_prep_kernel: one workgroup per token (the row's sum of
+// prep_kernel: 16 lanes per (token, 128-column block), sixteen blocks per
+// workgroup. rms_prep_kernel: one workgroup per token (the row's sum of
 // squares is shared through LDS).
 #include "q35_quant.h"
 
@@ -19,36 +17,48 @@ namespace {
 
 constexpr int kPrepThreads = 256;
 
+// Eight consecutive source values of token t from column c0 (c0 % 8 == 0).
 template <int SRC>
-__device__ __forceinline__ float load_source(const PrepArgs &a, int t, int c) {
+__device__ __forceinline__ void load_source8(const PrepArgs &a, int t, int c0, float v[8]) {
   if constexpr (SRC == kPrepPlain) {
-    return a.x[static_cast<size_t>(t) * a.x_stride + c];
+    const q35_f32x4 *x = reinterpret_cast<const q35_f32x4 *>(a.x + static_cast<size_t>(t) * a.x_stride + c0);
+    const q35_f32x4 lo = x[0], hi = x[1];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = lo[e];
+      v[4 + e] = hi[e];
+    }
   } else {
-    return silu_times(a.gate_up.at(t, c), a.gate_up.at(t, c + a.K));
+    float g[8], u[8];
+    a.gate_up.at8(t, c0, g);
+    a.gate_up.at8(t, c0 + a.K, u);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = silu_times(g[e], u[e]);
   }
 }
 
+// 16 lanes per (token, 128-column block) item, 16 items per workgroup.
 template <int SRC>
 __global__ __launch_bounds__(kPrepThreads) void prep_kernel(PrepArgs a) {
   const int K = a.K, nb = K >> 5, nblk = K >> 7;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int item = blockIdx.x * (kPrepThreads / 64) + wave;
-  if (item >= a.tokens * nblk) return;  // whole wavefronts only; no workgroup barrier below
+  const int items = a.tokens * nblk;
+  const int item0 = static_cast<int>((blockIdx.x * blockDim.x + threadIdx.x) >> 4);
+  const bool active = item0 < items;
+  const int item = active ? item0 : items - 1;  // idle rows redo a valid item and store nothing
   const int t = item / nblk, blk = item - t * nblk;
-  const int c0 = blk * 128 + lane, c1 = c0 + 64;
-  const float v0 = load_source<SRC>(a, t, c0);
-  const float v1 = load_source<SRC>(a, t, c1);
+  float v[8];
+  load_source8<SRC>(a, t, blk * 128 + 8 * (threadIdx.x & 15), v);
   QuantOut o;
   o.codes = a.codes;
   o.scales = a.scales;
   o.x4 = a.x4;
   o.x1 = a.x1;
-  h128_quantize_block(v0, v1, lane, t, blk, nb, a.h128, a.seed, o);
+  h128_quantize_row16(v, t, blk, nb, a.h128, a.seed, o, active);
 }
 
 // Residual update + RMSNorm + preparation, one workgroup (256 threads) per
-// token. Thread t owns columns 4t + 1024j (float4); all its residual and
-// partial loads are issued before the first add.
+// token. Thread i owns the float4 columns 4i + 1024k; the residual and the
+// split partial rows of a column batch are loaded before the ordered sum.
 constexpr int kRmsThreads = 256;
 constexpr int kRmsMaxK = 4096;
 
@@ -62,10 +72,19 @@ __global__ __launch_bounds__(kRmsThreads) void rms_prep_kernel(RmsPrepArgs a) {
   for (int i = tid; i < n4; i += kRmsThreads) {
     q35_f32x4 v = xin[i];
     if (a.add.p != nullptr) {
-      const q35_f32x4 *pp = reinterpret_cast<const q35_f32x4 *>(a.add.p + static_cast<size_t>(t) * a.add.width) + i;
-      const long long st4 = a.add.split_stride >> 2;
-      q35_f32x4 sum = pp[0];
-      for (int s = 1; s < a.add.splits; ++s) sum += pp[s * st4];
+      // columns 4i..4i+3 of every split, eight splits per batch
+      const float *pp = a.add.p + static_cast<size_t>(t) * a.add.width + 4 * i;
+      q35_f32x4 sum = q35_f32x4{0.0F, 0.0F, 0.0F, 0.0F};
+      for (int s0 = 0; s0 < a.add.splits; s0 += 8) {
+        q35_f32x4 x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          x[u] = *reinterpret_cast<const q35_f32x4 *>(pp + static_cast<long long>(min(s0 + u, a.add.splits - 1)) *
+                                                                  a.add.split_stride);
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (s0 + u < a.add.splits) sum = (s0 + u == 0) ? x[u] : sum + x[u];
+      }
       v += sum;
       reinterpret_cast<q35_f32x4 *>(a.x_out + static_cast<size_t>(t) * K)[i] = v;
     }
@@ -80,15 +99,20 @@ __global__ __launch_bounds__(kRmsThreads) void rms_prep_kernel(RmsPrepArgs a) {
   QuantOut o;
   o.codes = a.codes;
   o.scales = a.scales;
-  for (int blk = wave; blk < (K >> 7); blk += kRmsThreads / 64) {
-    const int c0 = blk * 128 + lane, c1 = c0 + 64;
-    const float v0 = y[c0] * rms_inv * (a.weight[c0] + 1.0F);
-    const float v1 = y[c1] * rms_inv * (a.weight[c1] + 1.0F);
-    if (a.normed_out != nullptr) {
-      a.normed_out[static_cast<size_t>(t) * K + c0] = v0;
-      a.normed_out[static_cast<size_t>(t) * K + c1] = v1;
-    }
-    h128_quantize_block(v0, v1, lane, t, blk, K >> 5, a.h128, a.seed, o);
+  const int nblk = K >> 7, j = tid & 15;
+  for (int blk0 = 0; blk0 < nblk; blk0 += kRmsThreads / 16) {
+    if (blk0 + wave * 4 >= nblk) break;  // wave-uniform: all four rows idle
+    const int want = blk0 + (tid >> 4);
+    const bool active = want < nblk;
+    const int blk = active ? want : nblk - 1;
+    const int c0 = blk * 128 + 8 * j;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = y[c0 + e] * rms_inv * (a.weight[c0 + e] + 1.0F);
+    if (a.normed_out != nullptr && active)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) a.normed_out[static_cast<size_t>(t) * K + c0 + e] = v[e];
+    h128_quantize_row16(v, t, blk, K >> 5, a.h128, a.seed, o, active);
   }
 }
 
@@ -129,7 +153,7 @@ __global__ void x1_to_a16_kernel(const q35_q8_0_block_x1 *x1, int nb, uint64_t *
 hipError_t launch_prep(const PrepArgs &a, hipStream_t stream) {
   if (a.tokens <= 0) return hipSuccess;
   const int items = a.tokens * (a.K >> 7);
-  const dim3 grid((items + kPrepThreads / 64 - 1) / (kPrepThreads / 64)), block(kPrepThreads);
+  const dim3 grid((items + kPrepThreads / 16 - 1) / (kPrepThreads / 16)), block(kPrepThreads);
   if (a.source == kPrepSiluMul)
     Q35_LAUNCH((prep_kernel<kPrepSiluMul>), grid, block, 0, stream, a);
   else

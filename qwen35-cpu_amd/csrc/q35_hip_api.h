@@ -26,12 +26,28 @@ typedef float q35_f32x4 __attribute__((ext_vector_type(4)));
 #endif
 
 #ifndef Q35_HOST_EMULATION
-// Exchange with lane l^1 / l^2 inside each group of four lanes (DPP quad_perm
-// [1,0,3,2] and [2,3,0,1]): a register-to-register move, no LDS crossbar.
-__device__ __forceinline__ float q35_quad_xor1(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, true));
+// Exchange with lane l^m inside each 16-lane row, as register-to-register DPP
+// moves (no LDS crossbar): m = 1, 2 are quad_perm [1,0,3,2] / [2,3,0,1];
+// m = 4, 8 combine row_shl:m (lanes with bit m clear) and row_shr:m (set).
+__device__ __forceinline__ int q35_row_xor_i(int v, int m) {
+  switch (m) {
+    case 1: return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, true);
+    case 2: return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, true);
+    case 4: {
+      const int up = __builtin_amdgcn_update_dpp(0, v, 0x104, 0xF, 0xF, true);
+      const int dn = __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);
+      return (__lane_id() & 4) ? dn : up;
+    }
+    default: {
+      const int up = __builtin_amdgcn_update_dpp(0, v, 0x108, 0xF, 0xF, true);
+      const int dn = __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);
+      return (__lane_id() & 8) ? dn : up;
+    }
+  }
 }
-__device__ __forceinline__ float q35_quad_xor2(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, true));
+__device__ __forceinline__ float q35_row_xor(float v, int m) {
+  return __int_as_float(q35_row_xor_i(__float_as_int(v), m));
 }
+__device__ __forceinline__ float q35_quad_xor1(float v) { return q35_row_xor(v, 1); }
+__device__ __forceinline__ float q35_quad_xor2(float v) { return q35_row_xor(v, 2); }
 #endif

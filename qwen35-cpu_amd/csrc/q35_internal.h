@@ -59,11 +59,37 @@ struct SplitRows {
   int splits = 1;
   long long split_stride = 0; // tokens * width
   int width = 0;              // floats per token row
+  // one value; the loads of each batch of 8 splits are issued together
   __device__ __forceinline__ float at(int t, int col) const {
     const float *q = p + static_cast<long long>(t) * width + col;
-    float v = q[0];
-    for (int s = 1; s < splits; ++s) v += q[s * split_stride];
+    float v = 0.0F;
+    for (int s0 = 0; s0 < splits; s0 += 8) {
+      float x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = q[static_cast<long long>(min(s0 + u, splits - 1)) * split_stride];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (s0 + u < splits) v = (s0 + u == 0) ? x[u] : v + x[u];
+    }
     return v;
+  }
+  // eight consecutive values (col % 4 == 0, width % 4 == 0), batches of 4 splits
+  __device__ __forceinline__ void at8(int t, int col, float out[8]) const {
+    const float *q = p + static_cast<long long>(t) * width + col;
+    for (int s0 = 0; s0 < splits; s0 += 4) {
+      float x[4][8];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float *r = q + static_cast<long long>(min(s0 + u, splits - 1)) * split_stride;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[u][e] = r[e];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (s0 + u < splits)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) out[e] = (s0 + u == 0) ? x[u][e] : out[e] + x[u][e];
+    }
   }
 };
 

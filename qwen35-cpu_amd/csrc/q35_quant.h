@@ -9,6 +9,14 @@
 //   stored scale = binary16(scale) * 1/sqrt(128)   q4_0.cpp:212-235, q4_h128.cpp:319-321
 // With h128 == false it is the identity-basis quantizer q8_0_quantize_vector_1
 // (q4_0.cpp:212-235).
+//
+// Layout: a 16-lane row of the wavefront holds the block, lane j = lane % 16
+// holding columns 8j .. 8j+7. FWHT strides 1, 2, 4 run in registers and
+// strides 8, 16, 32, 64 exchange with lane j^1, j^2, j^4, j^8 through DPP row
+// moves, in the reference's stage order with the reference's (a+b, a-b)
+// butterflies; a 32-column group is four lanes, so its absmax and code sum
+// finish with two quad exchanges, and each lane's eight codes are exactly
+// one A16 word (token t, k-group j % 4 of block 4*blk + j/4).
 #pragma once
 
 #include "q35_device.h"
@@ -18,73 +26,86 @@ namespace q35 {
 
 struct QuantOut {
   uint64_t *codes = nullptr;        // A16 [token_tile][nb][64]
-  float *scales = nullptr;       // [token_tile][nb][16]
+  float *scales = nullptr;          // [token_tile][nb][16]
   q35_q8_0_block_x4 *x4 = nullptr;  // reference X4 layout (optional)
   q35_q8_0_block_x1 *x1 = nullptr;  // reference X1 layout (optional)
 };
 
-// One wavefront holds the block as v0 = column lane, v1 = column 64 + lane of
-// 128-column block `blk` of token t (nb = 32-column blocks per row).
-__device__ __forceinline__ void h128_quantize_block(float v0, float v1, int lane, int t, int blk, int nb,
-                                                    bool h128, uint64_t seed, const QuantOut &o) {
+// All 64 lanes of the wavefront call this (the DPP moves need every lane of
+// each row); rows whose `active` is false store nothing.
+__device__ __forceinline__ void h128_quantize_row16(float v[8], int t, int blk, int nb, bool h128,
+                                                    uint64_t seed, const QuantOut &o, bool active) {
+  const int j = __lane_id() & 15;
   if (h128) {
-    const uint64_t w0 = h128_sign_word(blk, 0, seed), w1 = h128_sign_word(blk, 1, seed);
-    if ((w0 >> lane) & 1ull) v0 = -v0;
-    if ((w1 >> lane) & 1ull) v1 = -v1;
+    const uint64_t w = h128_sign_word(blk, j >> 3, seed);
+    const int sh = (j & 7) * 8;
 #pragma unroll
-    for (int s = 1; s < 64; s <<= 1) {
-      const float p0 = __shfl_xor(v0, s, 64), p1 = __shfl_xor(v1, s, 64);
-      if (lane & s) {
-        v0 = p0 - v0;
-        v1 = p1 - v1;
-      } else {
-        v0 = v0 + p0;
-        v1 = v1 + p1;
+    for (int e = 0; e < 8; ++e)
+      if ((w >> (sh + e)) & 1ull) v[e] = -v[e];
+#pragma unroll
+    for (int s = 1; s < 8; s <<= 1)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (!(e & s)) {
+          const float a = v[e], b = v[e + s];
+          v[e] = a + b;
+          v[e + s] = a - b;
+        }
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) {
+      const bool upper = (j & m) != 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float p = q35_row_xor(v[e], m);
+        v[e] = upper ? p - v[e] : v[e] + p;
       }
     }
-    const float lhs = v0;
-    v0 = lhs + v1;
-    v1 = lhs - v1;
   }
-  const int tile = t >> 4, tok = t & 15;
-  // Two 32-value groups per value slot: group(v0) = lane/32, group(v1) = 2 + lane/32.
-  const float vals[2] = {v0, v1};
+  float amax = 0.0F;
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    const float v = vals[half];
-    const float amax = group_max<32>(fabsf(v));
-    const float scale = amax / 127.0F;
-    const float inv = scale == 0.0F ? 0.0F : 1.0F / scale;
-    float r = roundf(v * inv);
+  for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+  amax = fmaxf(amax, q35_row_xor(amax, 1));
+  amax = fmaxf(amax, q35_row_xor(amax, 2));
+  const float scale = amax / 127.0F;
+  const float inv = scale == 0.0F ? 0.0F : 1.0F / scale;
+  uint64_t word = 0;
+  int sum = 0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float r = roundf(v[e] * inv);
     r = fminf(fmaxf(r, -127.0F), 127.0F);
     const int code = static_cast<int>(r);
-    const int sum = group_sum_int<32>(code);
-    float stored = half_bits_to_float(float_to_half_bits(scale));
-    if (h128) stored *= kH128InvSqrt;
-    const int b = blk * 4 + half * 2 + (lane >> 5);
-    const int k = lane & 31;
-    if (o.codes != nullptr) {
-      uint8_t *dst = reinterpret_cast<uint8_t *>(o.codes);
-      const size_t word = (static_cast<size_t>(tile) * nb + b) * 64 + tok + 16 * (k >> 3);
-      dst[word * 8 + (k & 7)] = static_cast<uint8_t>(static_cast<int8_t>(code));
-      if (k == 0) o.scales[(static_cast<size_t>(tile) * nb + b) * 16 + tok] = stored;
+    sum += code;
+    word |= static_cast<uint64_t>(static_cast<uint8_t>(static_cast<int8_t>(code))) << (8 * e);
+  }
+  sum += q35_row_xor_i(sum, 1);
+  sum += q35_row_xor_i(sum, 2);
+  if (!active) return;
+  float stored = half_bits_to_float(float_to_half_bits(scale));
+  if (h128) stored *= kH128InvSqrt;
+  const int b = blk * 4 + (j >> 2), kg = j & 3;
+  const int tile = t >> 4, tok = t & 15;
+  if (o.codes != nullptr) {
+    o.codes[(static_cast<size_t>(tile) * nb + b) * 64 + tok + 16 * kg] = word;
+    if (kg == 0) o.scales[(static_cast<size_t>(tile) * nb + b) * 16 + tok] = stored;
+  }
+  if (o.x4 != nullptr) {
+    q35_q8_0_block_x4 &bx = o.x4[static_cast<size_t>(t >> 2) * nb + b];
+    *reinterpret_cast<uint64_t *>(&bx.qs[(t & 3) * 32 + 8 * kg]) = word;
+    if (kg == 0) {
+      bx.scales[t & 3] = stored;
+      bx.sums[t & 3] = static_cast<int16_t>(sum);
     }
-    if (o.x4 != nullptr) {
-      q35_q8_0_block_x4 &blkx = o.x4[static_cast<size_t>(t >> 2) * nb + b];
-      blkx.qs[(t & 3) * 32 + k] = static_cast<int8_t>(code);
-      if (k == 0) {
-        blkx.scales[t & 3] = stored;
-        blkx.sums[t & 3] = static_cast<int16_t>(sum);
-      }
-    }
-    if (o.x1 != nullptr) {
-      q35_q8_0_block_x1 &blk1 = o.x1[static_cast<size_t>(t) * nb + b];
-      blk1.qs[k] = static_cast<int8_t>(code);
-      if (k == 0) {
-        blk1.scales[0] = stored;
-        blk1.sums[0] = static_cast<int16_t>(sum);
-        blk1.pad = 0;
-      }
+  }
+  if (o.x1 != nullptr) {
+    q35_q8_0_block_x1 &b1 = o.x1[static_cast<size_t>(t) * nb + b];
+    uint8_t *q = reinterpret_cast<uint8_t *>(b1.qs) + 8 * kg;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q[e] = static_cast<uint8_t>(word >> (8 * e));
+    if (kg == 0) {
+      b1.scales[0] = stored;
+      b1.sums[0] = static_cast<int16_t>(sum);
+      b1.pad = 0;
     }
   }
 }

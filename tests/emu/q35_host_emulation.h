@@ -224,8 +224,11 @@ typedef unsigned int q35_u32x4 __attribute__((vector_size(16)));
 typedef unsigned int q35_u32x2 __attribute__((vector_size(8)));
 typedef float q35_f32x4 __attribute__((vector_size(16)));
 #define Q35_LOAD_NT(ptr) (*(ptr))
+inline int __lane_id() { return ::q35emu::t_ctx.lane; }
 inline float q35_quad_xor1(float v) { return ::q35emu::shfl_xor(v, 1); }
 inline float q35_quad_xor2(float v) { return ::q35emu::shfl_xor(v, 2); }
+inline float q35_row_xor(float v, int m) { return ::q35emu::shfl_xor(v, m); }
+inline int q35_row_xor_i(int v, int m) { return ::q35emu::shfl_xor(v, m); }
 #define Q35_STORE_NT(value, ptr) (*(ptr) = (value))
 #define Q35_DYNAMIC_SHARED(type, name) \
   type *name = reinterpret_cast<type *>(::q35emu::t_ctx.launch->dynamic_smem.data())
