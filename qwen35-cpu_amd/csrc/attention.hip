@@ -18,6 +18,7 @@ constexpr int kHeadDim = 256;
 constexpr int kAttnThreads = 256;
 constexpr int kMaxGroup = 8;  // query heads per KV head
 
+template <int MS>  // bound on the qkv projection's K splits
 __global__ __launch_bounds__(kAttnThreads) void attn_prep_kernel(AttnPrepArgs a) {
   __shared__ float scratch[8];
   __shared__ float ybuf[kHeadDim];
@@ -27,10 +28,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_prep_kernel(AttnPrepArgs a)
   float x = 0.0F;
   if (d < hd) {
     if (is_q) {
-      x = a.proj.at(r, slot * 2 * hd + d);
-      a.gate_out[(static_cast<size_t>(r) * a.heads + slot) * hd + d] = a.proj.at(r, slot * 2 * hd + hd + d);
+      x = a.proj.template sum<MS>(r, slot * 2 * hd + d);
+      a.gate_out[(static_cast<size_t>(r) * a.heads + slot) * hd + d] = a.proj.template sum<MS>(r, slot * 2 * hd + hd + d);
     } else {
-      x = a.proj.at(r, a.heads * 2 * hd + (slot - a.heads) * hd + d);
+      x = a.proj.template sum<MS>(r, a.heads * 2 * hd + (slot - a.heads) * hd + d);
     }
   }
   const float ss = block_sum<kAttnThreads / 64>(x * x, scratch);
@@ -60,7 +61,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_prep_kernel(AttnPrepArgs a)
     const int page = a.page_table[static_cast<size_t>(r) * a.max_pages + pos / a.page_tokens];
     const size_t row = (static_cast<size_t>(page) * a.page_tokens + pos % a.page_tokens) * a.kv_heads + g;
     a.k_pool[row * hd + d] = float_to_half_bits(y);
-    const float v = a.proj.at(r, a.heads * 2 * hd + a.kv_heads * hd + g * hd + d);
+    const float v = a.proj.template sum<MS>(r, a.heads * 2 * hd + a.kv_heads * hd + g * hd + d);
     a.v_pool[row * hd + d] = float_to_half_bits(v);
   }
 }
@@ -271,7 +272,13 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(AttnArgs a, const f
 hipError_t launch_attn_prep(const AttnPrepArgs &a, hipStream_t stream) {
   if (a.batch <= 0) return hipSuccess;
   if (a.head_dim > kHeadDim || a.rope_dim > a.head_dim) return hipErrorInvalidValue;
-  Q35_LAUNCH((attn_prep_kernel), dim3(a.batch, a.heads + a.kv_heads), kAttnThreads, 0, stream, a);
+  const dim3 grid(a.batch, a.heads + a.kv_heads);
+  switch (split_bound(a.proj.splits)) {
+    case 1: Q35_LAUNCH((attn_prep_kernel<1>), grid, kAttnThreads, 0, stream, a); break;
+    case 4: Q35_LAUNCH((attn_prep_kernel<4>), grid, kAttnThreads, 0, stream, a); break;
+    case 8: Q35_LAUNCH((attn_prep_kernel<8>), grid, kAttnThreads, 0, stream, a); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

@@ -2,8 +2,9 @@
 //
 // One workgroup (256 threads) per (value head, request). The head's fp32
 // state tile [value_row][key_col] = 128 x 128 (64 KiB) makes exactly one HBM
-// round trip, and its loads are the first instructions of the kernel, so the
-// 64 KiB are in flight while the rest of the step's inputs are prepared.
+// round trip; its loads are issued right after the head's few small inputs
+// (conv ring, projections, weights), so the 64 KiB are in flight while those
+// are combined.
 // Thread t owns rows t/4 and 64 + t/4 and, within each, the eight float4 at
 // columns 16m + 4(t%4) (m = 0..7): four lanes share a row, so every row dot
 // product finishes with two DPP quad exchanges instead of a shuffle chain,
@@ -21,10 +22,10 @@
 // (v_heads > k_heads) maps value head vh to key head vh / (v_heads / k_heads),
 // as the reference repeats q/k (layers.inl:130-144).
 //
-// The conv history is a ring of `kernel` slots indexed by position % kernel
-// (slot p % kernel receives the input of position p; positions p-kernel+1 ..
-// p-1 are read), so no workgroup ever reads a slot another one writes in the
-// same step.
+// The conv history is a ring of 4 (= conv kernel) slots indexed by
+// position % 4 (slot p % 4 receives the input of position p; positions
+// p-3 .. p-1 are read), so no workgroup ever reads a slot another one writes
+// in the same step.
 #include "q35_quant.h"
 
 namespace q35 {
@@ -32,8 +33,11 @@ namespace {
 
 constexpr int kDeltaThreads = 256;
 constexpr int kDim = 128;
+constexpr int kConvKernel = 4;  // linear_conv_kernel_dim of every Qwen3.5 size
 
-template <bool FUSED>
+// FUSED: the linear-attention step around the update; MS: compile-time bound
+// on the in-projection's K splits (so every input load is straight-line).
+template <bool FUSED, int MS>
 __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
   __shared__ float sq[kDim], sk[kDim], sv[kDim], so[kDim];
   __shared__ float red[8];
@@ -44,7 +48,8 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
   const int kh = vh / per;
   const int quad = tid & 3, rowp = tid >> 2;
 
-  // ---- 1. the state tile: all 16 float4 per thread in flight first
+  // state tile pointers (the loads are issued after this head's small inputs,
+  // so those arrive first: on gfx9 loads retire in issue order)
   float *state_r = a.state_base != nullptr
                        ? a.state_base + static_cast<long long>(a.slots[r]) * a.state_slot_stride
                        : a.states[r];
@@ -52,58 +57,90 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
   q35_f32x4 *S0 = S + rowp * (kDim / 4) + quad;         // row rowp
   q35_f32x4 *S1 = S + (rowp + 64) * (kDim / 4) + quad;  // row rowp + 64
   q35_f32x4 st0[8], st1[8];
+  auto load_state = [&]() {
 #pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    st0[m] = Q35_LOAD_NT(S0 + 4 * m);
-    st1[m] = Q35_LOAD_NT(S1 + 4 * m);
-  }
+    for (int m = 0; m < 8; ++m) {
+      st0[m] = Q35_LOAD_NT(S0 + 4 * m);
+      st1[m] = Q35_LOAD_NT(S1 + 4 * m);
+    }
+  };
 
-  // ---- 2. q, k, v, gates of this head
+  // ---- 2. q, k, v, gates of this head: every load first (the conv ring is
+  // written only after all reads), then the math
   const int q_dim = a.k_heads * kDim, v_dim = a.v_heads * kDim;
   const int channels = 2 * q_dim + v_dim;
-  float z[8] = {0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F};  // output gate, columns 8(lane%16)..+7 (wave 0)
+  // output gate and gated-norm weights of columns 8(lane%16)..+7 (wave 0)
+  float z[8] = {0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F};
+  float nw[8] = {0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F};
   if constexpr (FUSED) {
     float *conv = a.conv_base + static_cast<long long>(a.slots[r]) * a.conv_slot_stride;
-    const int K = a.kernel, pos = a.positions[r];
-    // causal conv1d + SiLU of one channel (batch 1), writing the input into
-    // the ring slot of this position
-    auto conv_channel = [&](int ch) -> float {
-      const float x = a.proj.at(r, ch);
-      float sum = x * a.conv_w[static_cast<size_t>(K - 1) * channels + ch];
-      for (int k = 0; k < K - 1; ++k) {
-        const int p = pos - (K - 1) + k;
-        const int slot = ((p % K) + K) % K;
-        sum += conv[static_cast<size_t>(slot) * channels + ch] * a.conv_w[static_cast<size_t>(k) * channels + ch];
-      }
-      conv[static_cast<size_t>(pos % K) * channels + ch] = x;
-      return silu_times(sum, 1.0F);
-    };
-    // threads 0..127: q channel, 128..255: k channel of key head kh
+    constexpr int K = kConvKernel;
+    const int pos = a.positions[r];
+    // threads 0..127: q channel, 128..255: k channel of key head kh; threads
+    // 0..127 also own the v channel of value head vh
     const int i = tid & (kDim - 1);
-    const bool is_k = tid >= kDim;
-    const float y = conv_channel((is_k ? q_dim : 0) + kh * kDim + i);
-    const float vv = tid < kDim ? conv_channel(2 * q_dim + vh * kDim + tid) : 0.0F;
-    if (wave == 0) a.proj.at8(r, channels + vh * kDim + 8 * (lane & 15), z);
+    const bool is_k = tid >= kDim, has_v = tid < kDim;
+    const int chq = (is_k ? q_dim : 0) + kh * kDim + i;
+    const int chv = has_v ? 2 * q_dim + vh * kDim + tid : chq;
+    const float xq = a.proj.template sum<MS>(r, chq);
+    const float xv = a.proj.template sum<MS>(r, chv);
+    float hq[K - 1], hv[K - 1], wq[K], wv[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      wq[k] = a.conv_w[static_cast<size_t>(k) * channels + chq];
+      wv[k] = a.conv_w[static_cast<size_t>(k) * channels + chv];
+    }
+#pragma unroll
+    for (int k = 0; k < K - 1; ++k) {
+      const int slot = (pos + 1 + k) & (K - 1);  // position pos - (K-1) + k
+      hq[k] = conv[static_cast<size_t>(slot) * channels + chq];
+      hv[k] = conv[static_cast<size_t>(slot) * channels + chv];
+    }
+    if (wave == 0) {
+      a.proj.template sum8<MS>(r, channels + vh * kDim + 8 * (lane & 15), z);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) nw[e] = a.norm_w[8 * (lane & 15) + e];
+    }
+    float bval = 0.0F, aval = 0.0F, dtb = 0.0F, sa_ = 0.0F;
     if (tid == 0) {
-      const float bval = a.proj.at(r, channels + v_dim + vh);
-      const float aval = a.proj.at(r, channels + v_dim + a.v_heads + vh);
+      bval = a.proj.template sum<MS>(r, channels + v_dim + vh);
+      aval = a.proj.template sum<MS>(r, channels + v_dim + a.v_heads + vh);
+      dtb = a.dt_bias[vh];
+      sa_ = a.ssm_a[vh];
+    }
+    load_state();
+    // causal conv1d + SiLU (activation.cpp:164-222: x * w[K-1] first, then
+    // the history oldest first)
+    float yq = xq * wq[K - 1], yv = xv * wv[K - 1];
+#pragma unroll
+    for (int k = 0; k < K - 1; ++k) {
+      yq += hq[k] * wq[k];
+      yv += hv[k] * wv[k];
+    }
+    yq = silu_times(yq, 1.0F);
+    yv = silu_times(yv, 1.0F);
+    // this position's inputs into the ring
+    conv[static_cast<size_t>(pos & (K - 1)) * channels + chq] = xq;
+    if (has_v) conv[static_cast<size_t>(pos & (K - 1)) * channels + chv] = xv;
+    if (tid == 0) {
       s_beta = sigmoid_stable(bval);
-      const float pre = softplus_stable(aval + a.dt_bias[vh]);
-      s_alpha = expf(pre * a.ssm_a[vh]);
+      const float pre = softplus_stable(aval + dtb);
+      s_alpha = expf(pre * sa_);
     }
     // L2 norms of q (waves 0-1) and k (waves 2-3) over 128 values
-    const float ss = group_sum<64>(y * y);
+    const float ss = wave_sum(yq * yq);
     if (lane == 0) red[wave] = ss;
-    if (tid < kDim) sv[tid] = vv;
-    __syncthreads();
+    if (has_v) sv[tid] = yv;
+    lds_barrier();
     const float tot = is_k ? red[2] + red[3] : red[0] + red[1];
     const float scale = is_k ? 1.0F : 1.0F / sqrtf(static_cast<float>(kDim));
     const float mul = scale / sqrtf(tot + 1.0e-6F);
     if (is_k)
-      sk[i] = y * mul;
+      sk[i] = yq * mul;
     else
-      sq[i] = y * mul;
+      sq[i] = yq * mul;
   } else {
+    load_state();
     const size_t qk = (static_cast<size_t>(r) * a.v_heads + vh) * kDim;
     if (tid < kDim) {
       sq[tid] = a.q[qk + tid];
@@ -115,7 +152,7 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
       s_beta = a.beta[static_cast<size_t>(r) * a.v_heads + vh];
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- 3. delta rule on the two rows of this thread
   const float alpha = s_alpha, beta = s_beta;
@@ -149,8 +186,6 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
       o0 += st0[m][e] * qc[e];
       o1 += st1[m][e] * qc[e];
     }
-    Q35_STORE_NT(st0[m], S0 + 4 * m);
-    Q35_STORE_NT(st1[m], S1 + 4 * m);
   }
   o0 += q35_quad_xor1(o0);
   o1 += q35_quad_xor1(o1);
@@ -160,11 +195,24 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
     so[rowp] = o0;
     so[rowp + 64] = o1;
   }
-  __syncthreads();
+  // the outputs are shared through LDS before the state goes back; waves
+  // 1-3 store their rows at once, wave 0 after the epilogue (a later load
+  // would wait for earlier stores: vmcnt counts both)
+  lds_barrier();
+  auto store_state = [&]() {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      Q35_STORE_NT(st0[m], S0 + 4 * m);
+      Q35_STORE_NT(st1[m], S1 + 4 * m);
+    }
+  };
+  if (wave != 0) {
+    store_state();
+    return;
+  }
 
   // ---- 4. outputs: wave 0, lane j = lane % 16 holds columns 8j .. 8j+7
   // (the four 16-lane rows compute the same values; row 0 stores)
-  if (wave != 0) return;
   const int j = lane & 15;
   const bool writer = lane < 16;
   float y[8];
@@ -181,7 +229,7 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
     ss += q35_row_xor(ss, 8);
     const float inv = 1.0F / sqrtf(ss / static_cast<float>(kDim) + a.eps);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) y[e] = silu_times(z[e], y[e] * inv * (a.norm_w[8 * j + e] + 0.0F));
+    for (int e = 0; e < 8; ++e) y[e] = silu_times(z[e], y[e] * inv * (nw[e] + 0.0F));
     if (a.out != nullptr && writer)
 #pragma unroll
       for (int e = 0; e < 8; ++e) a.out[static_cast<size_t>(r) * v_dim + vh * kDim + 8 * j + e] = y[e];
@@ -196,6 +244,7 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) a.out[o + e] = y[e];
   }
+  store_state();
 }
 
 }  // namespace
@@ -204,10 +253,17 @@ hipError_t launch_delta(const DeltaArgs &a, hipStream_t stream) {
   if (a.batch <= 0) return hipSuccess;
   if (a.kd != kDim || a.vd != kDim || a.v_heads % a.k_heads != 0) return hipErrorInvalidValue;
   const dim3 grid(a.v_heads, a.batch), block(kDeltaThreads);
-  if (a.fused)
-    Q35_LAUNCH((delta_kernel<true>), grid, block, 0, stream, a);
-  else
-    Q35_LAUNCH((delta_kernel<false>), grid, block, 0, stream, a);
+  if (!a.fused) {
+    Q35_LAUNCH((delta_kernel<false, 1>), grid, block, 0, stream, a);
+    return hipGetLastError();
+  }
+  if (a.kernel != kConvKernel) return hipErrorInvalidValue;
+  switch (split_bound(a.proj.splits)) {
+    case 1: Q35_LAUNCH((delta_kernel<true, 1>), grid, block, 0, stream, a); break;
+    case 4: Q35_LAUNCH((delta_kernel<true, 4>), grid, block, 0, stream, a); break;
+    case 8: Q35_LAUNCH((delta_kernel<true, 8>), grid, block, 0, stream, a); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

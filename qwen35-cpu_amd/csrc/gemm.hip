@@ -278,23 +278,34 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
   }
 }
 
-// One wavefront per token: the best key over all workgroups' candidates.
-__global__ __launch_bounds__(64) void argmax_finalize_kernel(const unsigned long long *cand, int ncand,
-                                                             int cand_stride, int tokens, int32_t *index,
-                                                             float *value) {
-  const int tok = blockIdx.x, lane = threadIdx.x;
-  if (tok >= tokens) return;
+// One workgroup per token: the best key over all workgroups' candidates,
+// eight loads per thread in flight, then the wave and workgroup maxima.
+constexpr int kFinalizeThreads = 256;
+__global__ __launch_bounds__(kFinalizeThreads) void argmax_finalize_kernel(const unsigned long long *cand, int ncand,
+                                                                           int cand_stride, int tokens,
+                                                                           int32_t *index, float *value) {
+  __shared__ unsigned long long wbest[kFinalizeThreads / 64];
+  const int tok = blockIdx.x, tid = threadIdx.x;
   unsigned long long key = 0ull;
-  for (int i = lane; i < ncand; i += 64) {
-    const unsigned long long k = cand[static_cast<size_t>(i) * cand_stride + tok];
-    key = k > key ? k : key;
+  for (int i0 = tid; i0 < ncand; i0 += 8 * kFinalizeThreads) {
+    unsigned long long k[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + u * kFinalizeThreads;
+      k[u] = i < ncand ? cand[static_cast<size_t>(i) * cand_stride + tok] : 0ull;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) key = k[u] > key ? k[u] : key;
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) {
     const unsigned long long o = __shfl_xor(key, m, 64);
     key = o > key ? o : key;
   }
-  if (lane == 0) {
+  if ((tid & 63) == 0) wbest[tid >> 6] = key;
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < kFinalizeThreads / 64; ++w) key = wbest[w] > key ? wbest[w] : key;
     if (index != nullptr) index[tok] = static_cast<int32_t>(argmax_key_index(key));
     if (value != nullptr) value[tok] = argmax_key_value(key);
   }
@@ -306,7 +317,9 @@ __global__ void split_reduce_kernel(SplitRows src, int tokens, float *out, int s
   const int row = blockIdx.x * blockDim.x + threadIdx.x, t = blockIdx.y;
   if (row >= src.width || t >= tokens) return;
   const size_t o = static_cast<size_t>(t) * stride + row;
-  const float v = src.at(t, row);
+  const float *q = src.p + static_cast<long long>(t) * src.width + row;
+  float v = q[0];
+  for (int s = 1; s < src.splits; ++s) v += q[s * src.split_stride];
   out[o] = residual != nullptr ? residual[o] + v : v;
 }
 
@@ -383,8 +396,8 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t stream) {
 
 hipError_t launch_argmax_finalize(const unsigned long long *cand, int ncand, int cand_stride, int tokens,
                                   int32_t *index, float *value, hipStream_t stream) {
-  Q35_LAUNCH((argmax_finalize_kernel), dim3(tokens), dim3(64), 0, stream, cand, ncand, cand_stride, tokens,
-             index, value);
+  Q35_LAUNCH((argmax_finalize_kernel), dim3(tokens), dim3(kFinalizeThreads), 0, stream, cand, ncand, cand_stride,
+             tokens, index, value);
   return hipGetLastError();
 }
 

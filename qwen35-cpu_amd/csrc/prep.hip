@@ -18,7 +18,7 @@ namespace {
 constexpr int kPrepThreads = 256;
 
 // Eight consecutive source values of token t from column c0 (c0 % 8 == 0).
-template <int SRC>
+template <int SRC, int MS>
 __device__ __forceinline__ void load_source8(const PrepArgs &a, int t, int c0, float v[8]) {
   if constexpr (SRC == kPrepPlain) {
     const q35_f32x4 *x = reinterpret_cast<const q35_f32x4 *>(a.x + static_cast<size_t>(t) * a.x_stride + c0);
@@ -30,15 +30,16 @@ __device__ __forceinline__ void load_source8(const PrepArgs &a, int t, int c0, f
     }
   } else {
     float g[8], u[8];
-    a.gate_up.at8(t, c0, g);
-    a.gate_up.at8(t, c0 + a.K, u);
+    a.gate_up.template sum8<MS>(t, c0, g);
+    a.gate_up.template sum8<MS>(t, c0 + a.K, u);
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = silu_times(g[e], u[e]);
   }
 }
 
-// 16 lanes per (token, 128-column block) item, 16 items per workgroup.
-template <int SRC>
+// 16 lanes per (token, 128-column block) item, 16 items per workgroup; MS
+// bounds the source's K splits.
+template <int SRC, int MS>
 __global__ __launch_bounds__(kPrepThreads) void prep_kernel(PrepArgs a) {
   const int K = a.K, nb = K >> 5, nblk = K >> 7;
   const int items = a.tokens * nblk;
@@ -47,7 +48,7 @@ __global__ __launch_bounds__(kPrepThreads) void prep_kernel(PrepArgs a) {
   const int item = active ? item0 : items - 1;  // idle rows redo a valid item and store nothing
   const int t = item / nblk, blk = item - t * nblk;
   float v[8];
-  load_source8<SRC>(a, t, blk * 128 + 8 * (threadIdx.x & 15), v);
+  load_source8<SRC, MS>(a, t, blk * 128 + 8 * (threadIdx.x & 15), v);
   QuantOut o;
   o.codes = a.codes;
   o.scales = a.scales;
@@ -62,6 +63,7 @@ __global__ __launch_bounds__(kPrepThreads) void prep_kernel(PrepArgs a) {
 constexpr int kRmsThreads = 256;
 constexpr int kRmsMaxK = 4096;
 
+template <int MS>  // bound on the added rows' K splits (0: nothing to add)
 __global__ __launch_bounds__(kRmsThreads) void rms_prep_kernel(RmsPrepArgs a) {
   __shared__ float y[kRmsMaxK];
   __shared__ float red[kRmsThreads / 64];
@@ -71,20 +73,18 @@ __global__ __launch_bounds__(kRmsThreads) void rms_prep_kernel(RmsPrepArgs a) {
   float ss = 0.0F;
   for (int i = tid; i < n4; i += kRmsThreads) {
     q35_f32x4 v = xin[i];
-    if (a.add.p != nullptr) {
-      // columns 4i..4i+3 of every split, eight splits per batch
+    if constexpr (MS > 0) {
+      // columns 4i..4i+3 of every split, all loads in flight together
       const float *pp = a.add.p + static_cast<size_t>(t) * a.add.width + 4 * i;
-      q35_f32x4 sum = q35_f32x4{0.0F, 0.0F, 0.0F, 0.0F};
-      for (int s0 = 0; s0 < a.add.splits; s0 += 8) {
-        q35_f32x4 x[8];
+      q35_f32x4 x[MS];
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-          x[u] = *reinterpret_cast<const q35_f32x4 *>(pp + static_cast<long long>(min(s0 + u, a.add.splits - 1)) *
-                                                                  a.add.split_stride);
+      for (int u = 0; u < MS; ++u)
+        x[u] = *reinterpret_cast<const q35_f32x4 *>(pp + static_cast<long long>(min(u, a.add.splits - 1)) *
+                                                             a.add.split_stride);
+      q35_f32x4 sum = x[0];
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-          if (s0 + u < a.add.splits) sum = (s0 + u == 0) ? x[u] : sum + x[u];
-      }
+      for (int u = 1; u < MS; ++u)
+        if (u < a.add.splits) sum += x[u];
       v += sum;
       reinterpret_cast<q35_f32x4 *>(a.x_out + static_cast<size_t>(t) * K)[i] = v;
     }
@@ -154,17 +154,32 @@ hipError_t launch_prep(const PrepArgs &a, hipStream_t stream) {
   if (a.tokens <= 0) return hipSuccess;
   const int items = a.tokens * (a.K >> 7);
   const dim3 grid((items + kPrepThreads / 16 - 1) / (kPrepThreads / 16)), block(kPrepThreads);
-  if (a.source == kPrepSiluMul)
-    Q35_LAUNCH((prep_kernel<kPrepSiluMul>), grid, block, 0, stream, a);
-  else
-    Q35_LAUNCH((prep_kernel<kPrepPlain>), grid, block, 0, stream, a);
+  if (a.source == kPrepSiluMul) {
+    switch (split_bound(a.gate_up.splits)) {
+      case 1: Q35_LAUNCH((prep_kernel<kPrepSiluMul, 1>), grid, block, 0, stream, a); break;
+      case 4: Q35_LAUNCH((prep_kernel<kPrepSiluMul, 4>), grid, block, 0, stream, a); break;
+      case 8: Q35_LAUNCH((prep_kernel<kPrepSiluMul, 8>), grid, block, 0, stream, a); break;
+      default: return hipErrorInvalidValue;
+    }
+  } else {
+    Q35_LAUNCH((prep_kernel<kPrepPlain, 1>), grid, block, 0, stream, a);
+  }
   return hipGetLastError();
 }
 
 hipError_t launch_rms_prep(const RmsPrepArgs &a, hipStream_t stream) {
   if (a.tokens <= 0) return hipSuccess;
   if (a.K % 128 != 0 || a.K > kRmsMaxK || (a.add.p != nullptr && a.x_out == nullptr)) return hipErrorInvalidValue;
-  Q35_LAUNCH((rms_prep_kernel), dim3(a.tokens), dim3(kRmsThreads), 0, stream, a);
+  const dim3 grid(a.tokens), block(kRmsThreads);
+  switch (a.add.p == nullptr ? 0 : split_bound(a.add.splits)) {
+    case 0: Q35_LAUNCH((rms_prep_kernel<0>), grid, block, 0, stream, a); break;
+    case 1: Q35_LAUNCH((rms_prep_kernel<1>), grid, block, 0, stream, a); break;
+    case 4: Q35_LAUNCH((rms_prep_kernel<4>), grid, block, 0, stream, a); break;
+    case 8: Q35_LAUNCH((rms_prep_kernel<8>), grid, block, 0, stream, a); break;
+    case 16: Q35_LAUNCH((rms_prep_kernel<16>), grid, block, 0, stream, a); break;
+    case 32: Q35_LAUNCH((rms_prep_kernel<32>), grid, block, 0, stream, a); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

@@ -35,6 +35,18 @@ __device__ __forceinline__ int group_sum_int(int v) {
   return v;
 }
 
+// Wavefront-wide sum: DPP exchanges inside each 16-lane row, then the two
+// cross-row steps; every lane gets the total.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += q35_row_xor(v, 1);
+  v += q35_row_xor(v, 2);
+  v += q35_row_xor(v, 4);
+  v += q35_row_xor(v, 8);
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
 // Sum over a whole workgroup of `Waves` wavefronts; every thread gets the result.
 template <int Waves>
 __device__ __forceinline__ float block_sum(float v, float *scratch) {

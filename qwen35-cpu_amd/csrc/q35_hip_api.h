@@ -48,6 +48,14 @@ __device__ __forceinline__ int q35_row_xor_i(int v, int m) {
 __device__ __forceinline__ float q35_row_xor(float v, int m) {
   return __int_as_float(q35_row_xor_i(__float_as_int(v), m));
 }
+// Workgroup barrier that orders LDS only: outstanding global loads and
+// stores keep flying (__syncthreads is a release fence at workgroup scope and
+// waits for them -- on gfx9 the vmcnt counter covers loads and stores).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 __device__ __forceinline__ float q35_quad_xor1(float v) { return q35_row_xor(v, 1); }
 __device__ __forceinline__ float q35_quad_xor2(float v) { return q35_row_xor(v, 2); }
 #endif

@@ -59,39 +59,50 @@ struct SplitRows {
   int splits = 1;
   long long split_stride = 0; // tokens * width
   int width = 0;              // floats per token row
-  // one value; the loads of each batch of 8 splits are issued together
-  __device__ __forceinline__ float at(int t, int col) const {
+  // One value, for splits <= MS (checked by the launchers): MS loads, index
+  // clamped, issued together; the first `splits` are summed in split order.
+  template <int MS>
+  __device__ __forceinline__ float sum(int t, int col) const {
     const float *q = p + static_cast<long long>(t) * width + col;
-    float v = 0.0F;
-    for (int s0 = 0; s0 < splits; s0 += 8) {
-      float x[8];
+    float x[MS];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) x[u] = q[static_cast<long long>(min(s0 + u, splits - 1)) * split_stride];
+    for (int u = 0; u < MS; ++u) x[u] = q[static_cast<long long>(min(u, splits - 1)) * split_stride];
+    float v = x[0];
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (s0 + u < splits) v = (s0 + u == 0) ? x[u] : v + x[u];
-    }
+    for (int u = 1; u < MS; ++u)
+      if (u < splits) v += x[u];
     return v;
   }
-  // eight consecutive values (col % 4 == 0, width % 4 == 0), batches of 4 splits
-  __device__ __forceinline__ void at8(int t, int col, float out[8]) const {
+  // Eight consecutive values (col % 4 == 0, width % 4 == 0), splits <= MS.
+  template <int MS>
+  __device__ __forceinline__ void sum8(int t, int col, float out[8]) const {
     const float *q = p + static_cast<long long>(t) * width + col;
-    for (int s0 = 0; s0 < splits; s0 += 4) {
-      float x[4][8];
+    q35_f32x4 x[MS][2];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float *r = q + static_cast<long long>(min(s0 + u, splits - 1)) * split_stride;
+    for (int u = 0; u < MS; ++u) {
+      const q35_f32x4 *r = reinterpret_cast<const q35_f32x4 *>(q + static_cast<long long>(min(u, splits - 1)) * split_stride);
+      x[u][0] = r[0];
+      x[u][1] = r[1];
+    }
+    q35_f32x4 lo = x[0][0], hi = x[0][1];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[u][e] = r[e];
+    for (int u = 1; u < MS; ++u)
+      if (u < splits) {
+        lo += x[u][0];
+        hi += x[u][1];
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (s0 + u < splits)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) out[e] = (s0 + u == 0) ? x[u][e] : out[e] + x[u][e];
+    for (int e = 0; e < 4; ++e) {
+      out[e] = lo[e];
+      out[4 + e] = hi[e];
     }
   }
 };
+
+// Smallest supported compile-time split bound >= splits (0 when too many).
+inline int split_bound(int splits) {
+  return splits <= 1 ? 1 : splits <= 4 ? 4 : splits <= 8 ? 8 : splits <= 16 ? 16 : splits <= 32 ? 32 : 0;
+}
 
 // Activation preparation source modes (one wavefront per token and 128-column block).
 enum PrepSource : int {

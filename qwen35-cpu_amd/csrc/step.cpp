@@ -83,7 +83,7 @@ extern "C" int q35_model_create(q35_context *ctx, const q35_model_dims *dims,
   if (d.n_layers <= 0 || d.hidden <= 0 || d.hidden % 128 || d.intermediate % 128 ||
       d.vocab <= 0 || d.vocab % 8 || d.n_heads <= 0 || d.n_kv_heads <= 0 ||
       d.n_heads % d.n_kv_heads || d.head_dim != 256 || d.lin_k_dim != 128 || d.lin_v_dim != 128 ||
-      d.lin_v_heads % d.lin_k_heads || d.lin_kernel < 2 || d.rope_dim <= 0 || d.rope_dim > d.head_dim ||
+      d.lin_v_heads % d.lin_k_heads || d.lin_kernel != 4 || d.rope_dim <= 0 || d.rope_dim > d.head_dim ||
       (d.lin_v_heads * d.lin_v_dim) % 128 || (d.n_heads * d.head_dim) % 128)
     return set_error(ctx, Q35_ERR_UNSUPPORTED, "model shape outside the kernels' support");
   auto *m = new (std::nothrow) q35_model();
