@@ -50,9 +50,15 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
 
   // state tile pointers (the loads are issued after this head's small inputs,
   // so those arrive first: on gfx9 loads retire in issue order)
-  float *state_r = a.state_base != nullptr
-                       ? a.state_base + static_cast<long long>(a.slots[r]) * a.state_slot_stride
-                       : a.states[r];
+  // (the fused step addresses slot-strided state only, so its loads stay
+  // global-address-space loads rather than FLAT ones that would also hold
+  // every LDS wait)
+  float *state_r;
+  if constexpr (FUSED)
+    state_r = a.state_base + static_cast<long long>(a.slots[r]) * a.state_slot_stride;
+  else
+    state_r = a.state_base != nullptr ? a.state_base + static_cast<long long>(a.slots[r]) * a.state_slot_stride
+                                      : a.states[r];
   q35_f32x4 *S = reinterpret_cast<q35_f32x4 *>(state_r + static_cast<size_t>(vh) * kDim * kDim);
   q35_f32x4 *S0 = S + rowp * (kDim / 4) + quad;         // row rowp
   q35_f32x4 *S1 = S + (rowp + 64) * (kDim / 4) + quad;  // row rowp + 64
@@ -82,8 +88,15 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
     const bool is_k = tid >= kDim, has_v = tid < kDim;
     const int chq = (is_k ? q_dim : 0) + kh * kDim + i;
     const int chv = has_v ? 2 * q_dim + vh * kDim + tid : chq;
-    const float xq = a.proj.template sum<MS>(r, chq);
-    const float xv = a.proj.template sum<MS>(r, chv);
+    // raw (split) loads of every small input first, then the state tile,
+    // then the reductions
+    float xq_s[MS], xv_s[MS], b_s[MS], a_s[MS];
+    q35_f32x4 z_s[MS][2];
+    a.proj.template load<MS>(r, chq, xq_s);
+    a.proj.template load<MS>(r, chv, xv_s);
+    a.proj.template load8<MS>(r, channels + vh * kDim + 8 * (lane & 15), z_s);
+    a.proj.template load<MS>(r, channels + v_dim + vh, b_s);
+    a.proj.template load<MS>(r, channels + v_dim + a.v_heads + vh, a_s);
     float hq[K - 1], hv[K - 1], wq[K], wv[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -96,19 +109,17 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
       hq[k] = conv[static_cast<size_t>(slot) * channels + chq];
       hv[k] = conv[static_cast<size_t>(slot) * channels + chv];
     }
-    if (wave == 0) {
-      a.proj.template sum8<MS>(r, channels + vh * kDim + 8 * (lane & 15), z);
+    // (every thread loads these; wave 0 / thread 0 use them)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) nw[e] = a.norm_w[8 * (lane & 15) + e];
-    }
-    float bval = 0.0F, aval = 0.0F, dtb = 0.0F, sa_ = 0.0F;
-    if (tid == 0) {
-      bval = a.proj.template sum<MS>(r, channels + v_dim + vh);
-      aval = a.proj.template sum<MS>(r, channels + v_dim + a.v_heads + vh);
-      dtb = a.dt_bias[vh];
-      sa_ = a.ssm_a[vh];
-    }
+    for (int e = 0; e < 8; ++e) nw[e] = a.norm_w[8 * (lane & 15) + e];
+    const float dtb = a.dt_bias[vh];
+    const float sa_ = a.ssm_a[vh];
     load_state();
+    const float xq = a.proj.template reduce<MS>(xq_s);
+    const float xv = a.proj.template reduce<MS>(xv_s);
+    a.proj.template reduce8<MS>(z_s, z);
+    const float bval = a.proj.template reduce<MS>(b_s);
+    const float aval = a.proj.template reduce<MS>(a_s);
     // causal conv1d + SiLU (activation.cpp:164-222: x * w[K-1] first, then
     // the history oldest first)
     float yq = xq * wq[K - 1], yv = xv * wv[K - 1];

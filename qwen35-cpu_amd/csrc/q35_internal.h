@@ -59,43 +59,59 @@ struct SplitRows {
   int splits = 1;
   long long split_stride = 0; // tokens * width
   int width = 0;              // floats per token row
-  // One value, for splits <= MS (checked by the launchers): MS loads, index
-  // clamped, issued together; the first `splits` are summed in split order.
+  // Loads for splits <= MS (checked by the launchers): MS loads, index
+  // clamped, issued together; reduce*() then sums the first `splits` in split
+  // order with selects (no branch, so loads issued after the load call are
+  // not held back by a wait).
   template <int MS>
-  __device__ __forceinline__ float sum(int t, int col) const {
+  __device__ __forceinline__ void load(int t, int col, float x[MS]) const {
     const float *q = p + static_cast<long long>(t) * width + col;
-    float x[MS];
 #pragma unroll
     for (int u = 0; u < MS; ++u) x[u] = q[static_cast<long long>(min(u, splits - 1)) * split_stride];
+  }
+  template <int MS>
+  __device__ __forceinline__ float reduce(const float x[MS]) const {
     float v = x[0];
 #pragma unroll
-    for (int u = 1; u < MS; ++u)
-      if (u < splits) v += x[u];
+    for (int u = 1; u < MS; ++u) v = u < splits ? v + x[u] : v;
     return v;
   }
-  // Eight consecutive values (col % 4 == 0, width % 4 == 0), splits <= MS.
   template <int MS>
-  __device__ __forceinline__ void sum8(int t, int col, float out[8]) const {
+  __device__ __forceinline__ float sum(int t, int col) const {
+    float x[MS];
+    load<MS>(t, col, x);
+    return reduce<MS>(x);
+  }
+  // Eight consecutive values (col % 4 == 0, width % 4 == 0).
+  template <int MS>
+  __device__ __forceinline__ void load8(int t, int col, q35_f32x4 x[MS][2]) const {
     const float *q = p + static_cast<long long>(t) * width + col;
-    q35_f32x4 x[MS][2];
 #pragma unroll
     for (int u = 0; u < MS; ++u) {
       const q35_f32x4 *r = reinterpret_cast<const q35_f32x4 *>(q + static_cast<long long>(min(u, splits - 1)) * split_stride);
       x[u][0] = r[0];
       x[u][1] = r[1];
     }
+  }
+  template <int MS>
+  __device__ __forceinline__ void reduce8(const q35_f32x4 x[MS][2], float out[8]) const {
     q35_f32x4 lo = x[0][0], hi = x[0][1];
 #pragma unroll
-    for (int u = 1; u < MS; ++u)
-      if (u < splits) {
-        lo += x[u][0];
-        hi += x[u][1];
-      }
+    for (int u = 1; u < MS; ++u) {
+      lo = u < splits ? lo + x[u][0] : lo;
+      hi = u < splits ? hi + x[u][1] : hi;
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       out[e] = lo[e];
       out[4 + e] = hi[e];
     }
+  }
+  template <int MS>
+  __device__ __forceinline__ void sum8(int t, int col, float out[8]) const {
+    q35_f32x4 x[MS][2];
+    load8<MS>(t, col, x);
+    reduce8<MS>(x, out);
   }
 };
 
