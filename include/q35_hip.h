@@ -288,7 +288,8 @@ int q35_runtime_last_hidden(q35_runtime *rt, float *out, size_t count);
  * until q35_runtime_profile_reset. */
 enum { Q35_KERNEL_EMBED = 0, Q35_KERNEL_PREP = 1, Q35_KERNEL_GEMM = 2, Q35_KERNEL_DELTA = 3,
        Q35_KERNEL_ATTN_PREP = 4, Q35_KERNEL_ATTENTION = 5, Q35_KERNEL_ARGMAX = 6,
-       Q35_KERNEL_CLASSES = 7 };
+       Q35_KERNEL_HEAD = 7, /* the vocabulary head's Q4 GEMV (greedy or full logits) */
+       Q35_KERNEL_CLASSES = 8 };
 int q35_runtime_set_profiling(q35_runtime *rt, int enable);
 int q35_runtime_profile_reset(q35_runtime *rt);
 int q35_runtime_profile_read(q35_runtime *rt, int kernel_class, double *total_ms,

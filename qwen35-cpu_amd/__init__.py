@@ -27,7 +27,7 @@ REQ_STATUS = {0: "prefill", 1: "decode", 2: "complete", 3: "cancelled", 4: "fail
 REQ_STATUS_INV = {v: k for k, v in REQ_STATUS.items()}
 ENC_F32, ENC_Q4_0_DOT4, ENC_Q4_H128_DOT4 = 0, 5, 6
 # kernel classes of the step profiler (q35_runtime_profile_read)
-KERNEL_CLASSES = ("embed", "prep", "gemm", "delta", "attn_prep", "attention", "argmax")
+KERNEL_CLASSES = ("embed", "prep", "gemm", "delta", "attn_prep", "attention", "argmax", "head")
 DEFAULT_SIGN_SEED = 0x5148333548313238  # q4_h128.h:25-26
 
 Q4X8_BYTES, Q8X4_BYTES, Q8X1_BYTES = 144, 152, 40

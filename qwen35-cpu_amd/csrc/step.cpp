@@ -752,7 +752,7 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
     g.stride = d.vocab;
     g.force_split = 1;  // rt->logits holds one [batch][vocab] copy: never split K here
     g.cu_count = ctx->cu_count;
-    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_algorithmic_bytes(d.vocab, H / 32, batch, true, false), launch_gemm(g, s),
+    Q35_KERNEL(Q35_KERNEL_HEAD, gemm_algorithmic_bytes(d.vocab, H / 32, batch, true, false), launch_gemm(g, s),
                "logits head");
   } else {
     GemmArgs g;
@@ -769,8 +769,8 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
     g.counts_stride = d.vocab;
     g.penalties = penalties;
     g.cu_count = ctx->cu_count;
-    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_algorithmic_bytes(d.vocab, H / 32, batch, false, false), launch_gemm(g, s),
-               "greedy head");
+    Q35_KERNEL(Q35_KERNEL_HEAD, gemm_algorithmic_bytes(d.vocab, H / 32, batch, false, false) + rt->cand_rows * B * 8.0,
+               launch_gemm(g, s), "greedy head");
     Q35_KERNEL(Q35_KERNEL_ARGMAX, rt->cand_rows * B * 8.0 + B * 4.0,
                launch_argmax_finalize(rt->cand, rt->cand_rows, kMaxTokens, batch, rt->tokens_out_dev, nullptr, s),
                "argmax finalize");
