@@ -278,6 +278,237 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
   }
 }
 
+// Streaming Q4 GEMV for the vocabulary head: a tall matrix, one K split.
+//
+// Each wavefront owns a contiguous run of `gpw` 64-row groups and walks it
+// chunk by chunk (KS blocks per chunk, all K blocks of a group before the
+// next group). A ring of R register buffers keeps the weight loads of the
+// next R-1 chunks in flight while the MFMAs of the current chunk run, so the
+// wavefronts never alternate between a load phase and a compute phase. Every
+// weight load is unconditional: past the wavefront's last chunk the ring
+// re-loads that chunk (an L2 hit) instead of branching, since a load under a
+// branch makes the compiler wait for every outstanding load at the join. The
+// A16 codes and scales of all NT token tiles are staged once per workgroup in
+// LDS, so the weights are the only HBM stream. Per block, row and token the
+// arithmetic is gemm_kernel's: the exact int32 block dot and the reference's
+// fp32 fma chain in block order (q4_dot4.cpp:53). ARGMAX leaves one best key
+// per wavefront and token in cand[wave][token] (0 for a wavefront past the
+// last group); otherwise the rows are stored to out[token][row].
+constexpr int kHeadWaves = 4;  // wavefronts per workgroup
+constexpr int kHeadKS = 4;     // blocks per chunk
+constexpr int kHeadRing = 3;   // chunks per wavefront: one computing, the rest in flight
+constexpr size_t kHeadMaxLds = 64 * 1024;
+// wavefronts per SIMD the register budget (and the grid) are sized for: the
+// accumulators of more token tiles need more registers
+constexpr int head_waves_per_simd(int nt) { return nt == 1 ? 3 : 2; }
+
+template <int KS>
+struct HeadChunk {
+  q35_u32x4 q[KS];
+  q35_u32x2 d[KS];
+};
+
+template <int KS, int R, int NT, bool ARGMAX, int OCC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void head_kernel(GemmArgs a,
+                                                                                               int gpw) {
+  static_assert(R >= 2, "the ring loads the next chunk before computing the current one");
+  Q35_DYNAMIC_SHARED(uint64_t, lcodes);  // [NT][nb][64] A16 words, then float [NT][nb][16]
+  const int nb = a.nb;
+  float *lscales = reinterpret_cast<float *>(lcodes + static_cast<size_t>(NT) * nb * 64);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int G = lane >> 4, c = lane & 15, h = c & 1, T = c >> 1;
+  const int ntiles = a.rows >> 3, groups = (ntiles + 7) >> 3;
+  const int gw = blockIdx.x * kHeadWaves + wave;
+  const int g0 = min(groups, gw * gpw), g1 = min(groups, g0 + gpw);
+  const int cpg = (nb + KS - 1) / KS;
+  const int iters = (g1 - g0) * cpg;
+  const uint8_t *wbase = reinterpret_cast<const uint8_t *>(a.w);
+  const size_t tile_bytes = static_cast<size_t>(nb) * 144;
+
+  // next chunk to load: group lg, chunk lch (advanced after every load);
+  // past the last chunk the last one is loaded again
+  int lg = g0, lch = 0;
+  auto load = [&](HeadChunk<KS> &buf) {
+    const bool past = lg >= g1;
+    const int gl = max(past ? g1 - 1 : lg, 0), cl = past ? cpg - 1 : lch;
+    const int rt = min(gl * 8 + T, ntiles - 1);
+    const uint8_t *tile = wbase + static_cast<size_t>(rt) * tile_bytes;
+#pragma unroll
+    for (int i = 0; i < KS; ++i) {
+      const size_t b = static_cast<size_t>(min(cl * KS + i, nb - 1));
+      buf.q[i] = *reinterpret_cast<const q35_u32x4 *>(tile + b * 144 + 16 + 16 * (2 * G + h));
+      buf.d[i] = *reinterpret_cast<const q35_u32x2 *>(tile + b * 144 + 8 * h);
+    }
+    if (++lch == cpg) {
+      lch = 0;
+      ++lg;
+    }
+  };
+
+  // per-token penalty and counts row (loop invariant; loaded before the
+  // weights so that the group epilogues never wait on a load)
+  float pen[NT][4];
+  int crow[NT][4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int tok = min(t * 16 + 4 * G + j, a.tokens - 1);
+      pen[t][j] = ARGMAX && a.penalties != nullptr ? a.penalties[tok] : 1.0F;
+      crow[t][j] = ARGMAX && a.count_rows != nullptr ? a.count_rows[tok] : tok;
+    }
+
+  HeadChunk<KS> buf[R];
+  load(buf[0]);
+  // stage the activations; the first pass is issued before chunks 1..R-2, so
+  // waiting for it leaves those chunks in flight
+  {
+    const int n16 = NT * nb * 32;  // 16-byte words of codes
+    const int s16 = NT * nb * 4;   // 16-byte words of scales
+    const q35_u32x4 *gc = reinterpret_cast<const q35_u32x4 *>(a.codes);
+    const q35_u32x4 *gs = reinterpret_cast<const q35_u32x4 *>(a.scales);
+    q35_u32x4 *lc = reinterpret_cast<q35_u32x4 *>(lcodes);
+    q35_u32x4 *ls = reinterpret_cast<q35_u32x4 *>(lscales);
+    auto pass = [&](int i0, bool first) {
+      q35_u32x4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = min(i0 + u * 256, n16 + s16 - 1);
+        v[u] = i < n16 ? gc[i] : gs[i - n16];
+      }
+      if (first) {
+#pragma unroll
+        for (int k = 1; k < R - 1; ++k) load(buf[k]);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * 256;
+        if (i < n16) lc[i] = v[u];
+        else if (i < n16 + s16) ls[i - n16] = v[u];
+      }
+    };
+    pass(threadIdx.x, true);
+    for (int i0 = threadIdx.x + 4 * 256; i0 < n16 + s16; i0 += 4 * 256) pass(i0, false);
+  }
+  lds_barrier();
+
+  float acc[NT][4][4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[t][i][j] = 0.0F;
+  unsigned long long run_best[NT][4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) run_best[t][j] = 0ull;
+  const bool vec_out = (a.stride & 3) == 0;
+
+  // group cg, chunk cch of the next compute
+  int cg = g0, cch = 0;
+  auto epilogue = [&]() {
+    const int row0 = cg * kRowsPerGroup + 4 * c;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int tok = t * 16 + 4 * G + j;
+        if constexpr (ARGMAX) {
+          unsigned long long key = 0ull;
+          if (tok < a.tokens) {
+            const float p = pen[t][j];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int row = row0 + r;
+              if (row >= a.rows) continue;
+              float val = acc[t][r][j];
+              if (p > 1.0F && a.counts != nullptr &&
+                  a.counts[static_cast<long long>(crow[t][j]) * a.counts_stride + row] > 0)
+                val = val > 0.0F ? val / p : val * p;
+              const unsigned long long k = argmax_key(val, static_cast<uint32_t>(row));
+              key = k > key ? k : key;
+            }
+          }
+#pragma unroll
+          for (int m = 1; m < 16; m <<= 1) {
+            const unsigned long long o = __shfl_xor(key, m, 64);
+            key = o > key ? o : key;
+          }
+          run_best[t][j] = key > run_best[t][j] ? key : run_best[t][j];
+        } else {
+          if (tok < a.tokens && row0 < a.rows)
+            store_row4(a.out + static_cast<size_t>(tok) * a.stride + row0, vec_out, acc[t][0][j], acc[t][1][j],
+                       acc[t][2][j], acc[t][3][j]);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[t][r][j] = 0.0F;
+      }
+  };
+  auto compute = [&](HeadChunk<KS> &cur) {
+#pragma unroll
+    for (int i = 0; i < KS; ++i) {
+      const int b = cch * KS + i;
+      // a slot past the last block re-reads it; a zero row scale makes its
+      // contribution exactly +0 (acc is never -0)
+      if (b >= nb) cur.d[i] = q35_u32x2{0u, 0u};
+      const int bl = min(b, nb - 1);
+      const long w0 = unpack_word(cur.q[i][0]), w1 = unpack_word(cur.q[i][1]);
+      const long w2 = unpack_word(cur.q[i][2]), w3 = unpack_word(cur.q[i][3]);
+      const float dw[4] = {half_bits_to_float(static_cast<uint16_t>(cur.d[i][0] & 0xffffu)),
+                           half_bits_to_float(static_cast<uint16_t>(cur.d[i][0] >> 16)),
+                           half_bits_to_float(static_cast<uint16_t>(cur.d[i][1] & 0xffffu)),
+                           half_bits_to_float(static_cast<uint16_t>(cur.d[i][1] >> 16))};
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const long act = static_cast<long>(lcodes[(static_cast<size_t>(t) * nb + bl) * 64 + lane]);
+        const q35_f32x4 sa =
+            *reinterpret_cast<const q35_f32x4 *>(lscales + (static_cast<size_t>(t) * nb + bl) * 16 + 4 * G);
+        const v4i zero = {0, 0, 0, 0};
+        const v4i corr = Q35_MFMA_I32_16X16X32_I8(act, kMinus8, zero, 0, 0, 0);
+        v4i D[4];
+        D[0] = Q35_MFMA_I32_16X16X32_I8(act, w0, corr, 0, 0, 0);
+        D[1] = Q35_MFMA_I32_16X16X32_I8(act, w1, corr, 0, 0, 0);
+        D[2] = Q35_MFMA_I32_16X16X32_I8(act, w2, corr, 0, 0, 0);
+        D[3] = Q35_MFMA_I32_16X16X32_I8(act, w3, corr, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[t][r][j] = fmaf(static_cast<float>(D[r][j]), dw[r] * sa[j], acc[t][r][j]);
+      }
+    }
+    if (++cch == cpg) {
+      epilogue();
+      cch = 0;
+      ++cg;
+    }
+  };
+
+  // at the top of each round chunks it .. it+R-2 are in flight in
+  // buf[0 .. R-2]; step k issues chunk it+k+R-1 into the buffer freed by
+  // step k-1, then computes chunk it+k
+  for (int it = 0; it < iters; it += R) {
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      load(buf[(k + R - 1) % R]);
+      if (it + k < iters) compute(buf[k]);
+    }
+  }
+
+  if constexpr (ARGMAX) {
+    if (c == 0) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int tok = t * 16 + 4 * G + j;
+          if (tok < a.tokens) a.cand[static_cast<size_t>(gw) * a.cand_stride + tok] = run_best[t][j];
+        }
+    }
+  }
+}
+
 // One workgroup per token: the best key over all workgroups' candidates,
 // eight loads per thread in flight, then the wave and workgroup maxima.
 constexpr int kFinalizeThreads = 256;
@@ -364,8 +595,39 @@ GemmPlan gemm_plan(int rows, int nb, bool exact, bool argmax, int cu_count, int 
   return p;
 }
 
-int gemm_argmax_grid(int rows, int cu_count) {
-  return gemm_plan(rows, 32, false, true, cu_count, 0, 0).grid;
+namespace {
+// Launch shape of head_kernel: token tiles, 64-row groups per wavefront,
+// workgroups and LDS bytes; `use` is false when the staged activations do
+// not fit (gemm_kernel then runs the shape).
+struct HeadPlan {
+  bool use;
+  int nt, gpw, grid;
+  size_t smem;
+};
+HeadPlan head_plan(int rows, int nb, int tokens, int cu_count, int force_gpw) {
+  HeadPlan p{};
+  const int groups = (rows / 8 + 7) / 8;
+  const int cus = cu_count > 0 ? cu_count : 256;
+  p.nt = (tokens + 15) / 16;
+  p.smem = static_cast<size_t>(p.nt) * nb * (64 * sizeof(uint64_t) + 16 * sizeof(float));
+  p.use = p.nt >= 1 && p.nt <= 4 && p.smem <= kHeadMaxLds;
+  // as few groups per wavefront as keep every wavefront resident at once
+  const int resident = cus * 4 * head_waves_per_simd(std::max(1, std::min(p.nt, 4)));
+  p.gpw = force_gpw > 0 ? force_gpw : std::max(1, (groups + resident - 1) / resident);
+  const int waves = (groups + p.gpw - 1) / p.gpw;
+  p.grid = (waves + kHeadWaves - 1) / kHeadWaves;
+  return p;
+}
+}  // namespace
+
+int gemm_argmax_cands(int rows, int nb, int tokens, int cu_count, int force_gpw) {
+  const HeadPlan hp = head_plan(rows, nb, tokens, cu_count, force_gpw);
+  return hp.use ? hp.grid * kHeadWaves : gemm_plan(rows, nb, false, true, cu_count, 0, 0).grid;
+}
+
+int gemm_argmax_cand_capacity(int rows, int cu_count) {
+  return std::max(head_plan(rows, 1, 16, cu_count, 0).grid * kHeadWaves,
+                  gemm_plan(rows, 32, false, true, cu_count, 0, 0).grid);
 }
 
 size_t gemm_partial_floats(int rows, int nb, int tokens, int cu_count) {
@@ -377,6 +639,28 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t stream) {
   if (a.tokens <= 0 || a.rows <= 0) return hipSuccess;
   const bool argmax = a.cand != nullptr;
   const bool exact = a.exact || a.block_dots != nullptr;
+  if ((argmax || a.head) && !exact && (argmax || a.out != nullptr)) {
+    const HeadPlan hp = head_plan(a.rows, a.nb, a.tokens, a.cu_count, a.force_gpw);
+    if (hp.use) {
+      const dim3 grid(hp.grid), block(64 * kHeadWaves);
+#define Q35_HEAD(NT)                                                                                       \
+  if (argmax) {                                                                                            \
+    Q35_LAUNCH((head_kernel<kHeadKS, kHeadRing, NT, true, head_waves_per_simd(NT)>), grid, block, hp.smem,  \
+               stream, a, hp.gpw);                                                                         \
+  } else {                                                                                                 \
+    Q35_LAUNCH((head_kernel<kHeadKS, kHeadRing, NT, false, head_waves_per_simd(NT)>), grid, block, hp.smem, \
+               stream, a, hp.gpw);                                                                         \
+  }
+      switch (hp.nt) {
+        case 1: Q35_HEAD(1) break;
+        case 2: Q35_HEAD(2) break;
+        case 3: Q35_HEAD(3) break;
+        default: Q35_HEAD(4) break;
+      }
+#undef Q35_HEAD
+      return hipGetLastError();
+    }
+  }
   const GemmPlan p = gemm_plan(a.rows, a.nb, exact, argmax, a.cu_count, a.force_ks, a.force_split);
   // a split plan writes [split][tokens][rows] partials; a single split writes `out`
   if ((p.split > 1 && a.partials == nullptr) || (p.split == 1 && a.out == nullptr && !argmax && a.block_dots == nullptr))

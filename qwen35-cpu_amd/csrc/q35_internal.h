@@ -189,6 +189,10 @@ struct GemmArgs {
   const float *penalties = nullptr;
   int cu_count = 0;
   int force_ks = 0, force_split = 0;  // plan overrides (0 = automatic)
+  // tall single-split matrix (the vocabulary head): the streaming kernel
+  // with activations staged in LDS; implied by `cand`
+  bool head = false;
+  int force_gpw = 0;  // head: 64-row groups per wavefront (0 = automatic)
 };
 // Launch plan of one GEMM: blocks per wavefront chunk, wavefronts per
 // workgroup, K splits across workgroups, workgroups along the rows, LDS bytes.
@@ -197,8 +201,12 @@ struct GemmPlan {
   size_t smem;
 };
 GemmPlan gemm_plan(int rows, int nb, bool exact, bool argmax, int cu_count, int force_ks, int force_split);
-// Workgroups of the greedy head launch (= candidate rows per token).
-int gemm_argmax_grid(int rows, int cu_count);
+// Candidate rows per token that the greedy head launch for this shape writes
+// (and argmax_finalize must read).
+int gemm_argmax_cands(int rows, int nb, int tokens, int cu_count, int force_gpw = 0);
+// Upper bound of gemm_argmax_cands over every nb <= 4096/32 and tokens <= 64
+// (the size of a candidate buffer).
+int gemm_argmax_cand_capacity(int rows, int cu_count);
 // Floats of partial sums a split launch writes (0 when it does not split).
 size_t gemm_partial_floats(int rows, int nb, int tokens, int cu_count);
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t stream);

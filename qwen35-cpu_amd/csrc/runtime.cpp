@@ -257,8 +257,10 @@ int matmul_entry(q35_context *ctx, const q35_q4_0_block_x8 *m, const q35_q8_0_bl
   const size_t chunk = kMaxTokens;
   const size_t code_bytes = align256(4 * 64 * static_cast<size_t>(nb) * sizeof(uint64_t));
   const size_t scale_bytes = align256(4 * 16 * static_cast<size_t>(nb) * sizeof(float));
-  const int grid = gemm_argmax_grid(static_cast<int>(rows), ctx->cu_count);
-  const size_t cand_bytes = index != nullptr ? align256(static_cast<size_t>(grid) * kMaxTokens * 8) : 0;
+  const size_t cand_bytes =
+      index != nullptr
+          ? align256(static_cast<size_t>(gemm_argmax_cand_capacity(static_cast<int>(rows), ctx->cu_count)) * kMaxTokens * 8)
+          : 0;
   const size_t part_bytes =
       align256(gemm_partial_floats(static_cast<int>(rows), nb, static_cast<int>(chunk), ctx->cu_count) * 4);
   void *scratch = nullptr;
@@ -311,7 +313,8 @@ int matmul_entry(q35_context *ctx, const q35_q4_0_block_x8 *m, const q35_q8_0_bl
       if (e != hipSuccess) return hip_error(ctx, e, "split reduce");
     }
     if (index != nullptr) {
-      e = launch_argmax_finalize(cand, grid, kMaxTokens, static_cast<int>(n), index + t0,
+      const int ncand = gemm_argmax_cands(g.rows, nb, static_cast<int>(n), ctx->cu_count);
+      e = launch_argmax_finalize(cand, ncand, kMaxTokens, static_cast<int>(n), index + t0,
                                  value ? value + t0 : nullptr, ctx->stream);
       if (e != hipSuccess) return hip_error(ctx, e, "argmax finalize");
     }

@@ -348,7 +348,7 @@ extern "C" int q35_runtime_create(q35_model *m, const q35_runtime_config *cfg, q
   const size_t kmax = std::max({H, I, rt->core_width});
   alloc(4 * 64 * (kmax / 32) * 8, reinterpret_cast<void **>(&rt->codes));
   alloc(4 * 16 * (kmax / 32) * sizeof(float), reinterpret_cast<void **>(&rt->scales));
-  rt->cand_rows = gemm_argmax_grid(d.vocab, ctx->cu_count);
+  rt->cand_rows = gemm_argmax_cand_capacity(d.vocab, ctx->cu_count);
   alloc(static_cast<size_t>(rt->cand_rows) * kMaxTokens * 8, reinterpret_cast<void **>(&rt->cand));
   alloc(kMaxTokens * 4, reinterpret_cast<void **>(&rt->tokens_out_dev));
   const MetaLayout ml = meta_layout(B, rt->max_pages_per_row);
@@ -750,6 +750,7 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
     g.tokens = batch;
     g.out = rt->logits;
     g.stride = d.vocab;
+    g.head = true;
     g.force_split = 1;  // rt->logits holds one [batch][vocab] copy: never split K here
     g.cu_count = ctx->cu_count;
     Q35_KERNEL(Q35_KERNEL_HEAD, gemm_algorithmic_bytes(d.vocab, H / 32, batch, true, false), launch_gemm(g, s),
@@ -769,10 +770,11 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
     g.counts_stride = d.vocab;
     g.penalties = penalties;
     g.cu_count = ctx->cu_count;
-    Q35_KERNEL(Q35_KERNEL_HEAD, gemm_algorithmic_bytes(d.vocab, H / 32, batch, false, false) + rt->cand_rows * B * 8.0,
+    const int ncand = gemm_argmax_cands(d.vocab, H / 32, batch, ctx->cu_count);
+    Q35_KERNEL(Q35_KERNEL_HEAD, gemm_algorithmic_bytes(d.vocab, H / 32, batch, false, false) + ncand * B * 8.0,
                launch_gemm(g, s), "greedy head");
-    Q35_KERNEL(Q35_KERNEL_ARGMAX, rt->cand_rows * B * 8.0 + B * 4.0,
-               launch_argmax_finalize(rt->cand, rt->cand_rows, kMaxTokens, batch, rt->tokens_out_dev, nullptr, s),
+    Q35_KERNEL(Q35_KERNEL_ARGMAX, ncand * B * 8.0 + B * 4.0,
+               launch_argmax_finalize(rt->cand, ncand, kMaxTokens, batch, rt->tokens_out_dev, nullptr, s),
                "argmax finalize");
     Q35_STEP(hipMemcpyAsync(rt->tokens_out_host, rt->tokens_out_dev, batch * 4, hipMemcpyDeviceToHost, s),
              "token copy");
