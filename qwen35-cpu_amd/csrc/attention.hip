@@ -25,26 +25,31 @@ __global__ __launch_bounds__(kAttnThreads) void attn_prep_kernel(AttnPrepArgs a)
   const int r = blockIdx.x, slot = blockIdx.y, d = threadIdx.x;
   const int hd = a.head_dim;
   const bool is_q = slot < a.heads;
-  float x = 0.0F;
-  if (d < hd) {
-    if (is_q) {
-      x = a.proj.template sum<MS>(r, slot * 2 * hd + d);
-      a.gate_out[(static_cast<size_t>(r) * a.heads + slot) * hd + d] = a.proj.template sum<MS>(r, slot * 2 * hd + hd + d);
-    } else {
-      x = a.proj.template sum<MS>(r, a.heads * 2 * hd + (slot - a.heads) * hd + d);
-    }
-  }
+  const int g = max(slot - a.heads, 0);
+  const int dd = min(d, hd - 1);  // threads past head_dim mirror a valid column and store nothing
+  // every load that does not depend on the projection is issued first, so
+  // the kernel waits on one round trip (the position's page and RoPE row
+  // behind the position itself)
+  const int pos = a.positions[r];
+  const float *w = is_q ? a.q_norm : a.k_norm;
+  const float w1 = w[dd] + 1.0F;
+  const int half = a.rope_dim / 2;
+  const int rd = min(d, a.rope_dim - 1) % half;
+  const float cs = a.rope_cos[static_cast<size_t>(pos) * half + rd];
+  const float sn = a.rope_sin[static_cast<size_t>(pos) * half + rd];
+  const int page = a.page_table[static_cast<size_t>(r) * a.max_pages + pos / a.page_tokens];
+  // q head: [q | gate] of the head; k head: its K row and its V row
+  const int col_x = is_q ? slot * 2 * hd + dd : a.heads * 2 * hd + g * hd + dd;
+  const int col_2 = is_q ? slot * 2 * hd + hd + dd : a.heads * 2 * hd + a.kv_heads * hd + g * hd + dd;
+  const float x = d < hd ? a.proj.template sum<MS>(r, col_x) : 0.0F;
+  const float second = a.proj.template sum<MS>(r, col_2);
+  if (is_q && d < hd) a.gate_out[(static_cast<size_t>(r) * a.heads + slot) * hd + d] = second;
   const float ss = block_sum<kAttnThreads / 64>(x * x, scratch);
   const float inv = 1.0F / sqrtf(ss / static_cast<float>(hd) + a.eps);
-  const float *w = is_q ? a.q_norm : a.k_norm;
-  float y = d < hd ? x * inv * (w[d] + 1.0F) : 0.0F;
+  float y = d < hd ? x * inv * w1 : 0.0F;
   if (d < hd) ybuf[d] = y;
-  __syncthreads();
-  const int pos = a.positions[r];
-  const int half = a.rope_dim / 2;
+  lds_barrier();
   if (d < a.rope_dim) {
-    const float cs = a.rope_cos[static_cast<size_t>(pos) * half + (d % half)];
-    const float sn = a.rope_sin[static_cast<size_t>(pos) * half + (d % half)];
     if (d < half) {
       const float x0 = ybuf[d], x1 = ybuf[d + half];
       y = x0 * cs - x1 * sn;
@@ -57,12 +62,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_prep_kernel(AttnPrepArgs a)
   if (is_q) {
     a.q_out[(static_cast<size_t>(r) * a.heads + slot) * hd + d] = y;
   } else {
-    const int g = slot - a.heads;
-    const int page = a.page_table[static_cast<size_t>(r) * a.max_pages + pos / a.page_tokens];
     const size_t row = (static_cast<size_t>(page) * a.page_tokens + pos % a.page_tokens) * a.kv_heads + g;
     a.k_pool[row * hd + d] = float_to_half_bits(y);
-    const float v = a.proj.template sum<MS>(r, a.heads * 2 * hd + a.kv_heads * hd + g * hd + d);
-    a.v_pool[row * hd + d] = float_to_half_bits(v);
+    a.v_pool[row * hd + d] = float_to_half_bits(second);
   }
 }
 
@@ -84,43 +86,50 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
   __shared__ float probs[QPK][kChunkTokens];
   __shared__ float s_m[QPK], s_l[QPK];
   __shared__ float red[4][QPK][kHeadDim];
+  static_assert(kAttnThreads == kHeadDim, "thread d stages dim d of every query head");
   const int sp = blockIdx.x, g = blockIdx.y, r = blockIdx.z;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  // Loads in the order they are consumed (the memory counter retires them in
+  // issue order): the group's query heads (with the context length), then
+  // the page table, K and V, so the query staging waits only for the
+  // queries and V keeps arriving during the scores and the softmax.
+  float qv[QPK];
+#pragma unroll
+  for (int u = 0; u < QPK; ++u) qv[u] = a.q[(static_cast<size_t>(r) * a.heads + g * QPK + u) * kHeadDim + tid];
   const int seq = a.seq_lens != nullptr ? a.seq_lens[r] : a.positions[r] + 1;
   const int t0 = sp * kChunkTokens;
   if (t0 >= seq) return;  // whole workgroup
   const int n = min(seq - t0, kChunkTokens);
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int kvw = a.kv_heads * kHeadDim;
   const int32_t *pt = a.page_table + static_cast<size_t>(r) * a.max_pages;
 
   // K: token ti = tid/4 (clamped into the chunk), dims 64*qq .. +63
   const int qq = tid & 3, ti = min(tid >> 2, n - 1);
   const int ktok = t0 + ti;
+  int vpage[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) vpage[j] = pt[(t0 + min(wave + 4 * j, n - 1)) / a.page_tokens];
   const int kpage = pt[ktok / a.page_tokens];
   const q35_u32x4 *krow = reinterpret_cast<const q35_u32x4 *>(
       a.k_pool + (static_cast<size_t>(kpage) * a.page_tokens + ktok % a.page_tokens) * kvw +
       static_cast<size_t>(g) * kHeadDim + 64 * qq);
+  q35_u32x4 kraw[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) kraw[i] = Q35_LOAD_NT(krow + i);
   // V: tokens wave + 4j (clamped), dims 4*lane .. +3
   q35_u32x2 vraw[16];
-  q35_u32x4 kraw[8];
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
     const int vt = t0 + min(wave + 4 * j, n - 1);
-    const int vpage = pt[vt / a.page_tokens];
     vraw[j] = Q35_LOAD_NT(reinterpret_cast<const q35_u32x2 *>(
-        a.v_pool + (static_cast<size_t>(vpage) * a.page_tokens + vt % a.page_tokens) * kvw +
+        a.v_pool + (static_cast<size_t>(vpage[j]) * a.page_tokens + vt % a.page_tokens) * kvw +
         static_cast<size_t>(g) * kHeadDim + 4 * lane));
   }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) kraw[i] = Q35_LOAD_NT(krow + i);
 
   // the group's query heads into LDS, quarter-padded
-  for (int e = tid; e < QPK * kHeadDim; e += kAttnThreads) {
-    const int u = e / kHeadDim, d = e % kHeadDim;
-    qs[(u * 4 + d / 64) * kQStride + d % 64] =
-        a.q[(static_cast<size_t>(r) * a.heads + g * QPK + u) * kHeadDim + d];
-  }
-  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < QPK; ++u) qs[(u * 4 + tid / 64) * kQStride + tid % 64] = qv[u];
+  lds_barrier();
 
   // ---- scores
   float part[QPK];
@@ -149,7 +158,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     part[u] += q35_quad_xor2(part[u]);
     if (qq == 0) probs[u][tid >> 2] = (tid >> 2) < n ? part[u] * a.scale : -INFINITY;
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- chunk softmax statistics (wave u handles head u, u += 4)
   for (int u = wave; u < QPK; u += kAttnThreads / 64) {
@@ -163,7 +172,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
       s_l[u] = l;
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- P*V over this wave's tokens, then the fixed-order wave sum
   float acc[QPK][4];
@@ -188,7 +197,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
 #pragma unroll
   for (int u = 0; u < QPK; ++u)
     *reinterpret_cast<q35_f32x4 *>(&red[wave][u][4 * lane]) = q35_f32x4{acc[u][0], acc[u][1], acc[u][2], acc[u][3]};
-  __syncthreads();
+  lds_barrier();
   for (int e = tid; e < QPK * kHeadDim; e += kAttnThreads) {
     const int u = e / kHeadDim, d = e % kHeadDim;
     const float v = ((red[0][u][d] + red[1][u][d]) + red[2][u][d]) + red[3][u][d];
@@ -208,59 +217,80 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
 // One wavefront per (128-dim block b, head h, request): lane j = lane % 16
 // holds dims 128b + 8j .. +7 -- one H128 block of the o projection's input --
 // and the result is stored as FP32 and/or prepared as A16 activations (the
-// four 16-lane rows compute the same values; row 0 stores).
+// four 16-lane rows compute the same values; row 0 stores). The gate row and
+// the partial rows of the first kMergeBatch chunks are loaded together with
+// the chunk statistics, right after the context length.
+constexpr int kMergeBatch = 16;
+
 __global__ __launch_bounds__(64) void attention_merge_kernel(AttnArgs a, const float *gates, float *out,
                                                             QuantOut qo, uint64_t seed) {
-  __shared__ float w_s[64];
   const int b = blockIdx.x & 1, h = blockIdx.x >> 1, r = blockIdx.y;
   const int lane = threadIdx.x, j = lane & 15;
-  const int seq = a.seq_lens != nullptr ? a.seq_lens[r] : a.positions[r] + 1;
-  const int splits = (seq + kChunkTokens - 1) / kChunkTokens;
   const size_t hs = (static_cast<size_t>(r) * a.heads + h) * a.max_splits;
   const int d0 = 128 * b + 8 * j;
-  // global max over the chunks, then their weights in batches of 64
-  float M = -INFINITY;
-  for (int s = lane; s < splits; s += 64) M = fmaxf(M, a.part_ml[(hs + s) * 2]);
+  const size_t o = (static_cast<size_t>(r) * a.heads + h) * kHeadDim + d0;
+  const q35_f32x4 gate_lo = *reinterpret_cast<const q35_f32x4 *>(gates + o);
+  const q35_f32x4 gate_hi = *reinterpret_cast<const q35_f32x4 *>(gates + o + 4);
+  const int seq = a.seq_lens != nullptr ? a.seq_lens[r] : a.positions[r] + 1;
+  const int splits = (seq + kChunkTokens - 1) / kChunkTokens;
+  q35_f32x4 rows[kMergeBatch][2];
+  auto load_rows = [&](int s0) {
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+      const q35_f32x4 *src = reinterpret_cast<const q35_f32x4 *>(a.part_o + (hs + min(s0 + u, splits - 1)) * kHeadDim + d0);
+      rows[u][0] = src[0];
+      rows[u][1] = src[1];
+    }
+  };
+  // chunk statistics of chunks lane, lane + 64, ...: the first batch of 64
+  // stays in registers
+  float m0 = -INFINITY, l0 = 0.0F;
+  {
+    const int s = min(lane, splits - 1);
+    m0 = a.part_ml[(hs + s) * 2];
+    l0 = a.part_ml[(hs + s) * 2 + 1];
+    if (lane >= splits) m0 = -INFINITY;
+  }
+  load_rows(0);
+  float M = m0;
+  for (int s = lane + 64; s < splits; s += 64) M = fmaxf(M, a.part_ml[(hs + s) * 2]);
   M = group_max<64>(M);
   float acc[8] = {0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F};
   float L = 0.0F;
   for (int s0 = 0; s0 < splits; s0 += 64) {
     const int cnt = min(64, splits - s0);
+    float m = m0, l = l0;
+    if (s0 > 0 && lane < cnt) {
+      m = a.part_ml[(hs + s0 + lane) * 2];
+      l = a.part_ml[(hs + s0 + lane) * 2 + 1];
+    }
     float w = 0.0F, lw = 0.0F;
     if (lane < cnt) {
-      w = expf(a.part_ml[(hs + s0 + lane) * 2] - M);
-      lw = w * a.part_ml[(hs + s0 + lane) * 2 + 1];
+      w = expf(m - M);
+      lw = w * l;
     }
     L += group_sum<64>(lw);
-    w_s[lane] = w;
-    __syncthreads();
-    for (int s = 0; s < cnt; s += 4) {
-      q35_f32x4 o[4][2];
+    for (int s = 0; s < cnt; s += kMergeBatch) {
+      if (s0 + s > 0) load_rows(s0 + s);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const q35_f32x4 *src = reinterpret_cast<const q35_f32x4 *>(
-            a.part_o + (hs + s0 + min(s + u, cnt - 1)) * kHeadDim + d0);
-        o[u][0] = src[0];
-        o[u][1] = src[1];
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < kMergeBatch; ++u) {
         if (s + u >= cnt) break;
-        const float ws = w_s[s + u];
+        const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), s + u));
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          acc[e] += ws * o[u][0][e];
-          acc[4 + e] += ws * o[u][1][e];
+          acc[e] += ws * rows[u][0][e];
+          acc[4 + e] += ws * rows[u][1][e];
         }
       }
     }
-    __syncthreads();
   }
   const float inv = 1.0F / (L > 0.0F ? L : 1.0F);
-  const size_t o = (static_cast<size_t>(r) * a.heads + h) * kHeadDim + d0;
   float y[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) y[e] = (acc[e] * inv) * sigmoid_stable(gates[o + e]);
+  for (int e = 0; e < 4; ++e) {
+    y[e] = (acc[e] * inv) * sigmoid_stable(gate_lo[e]);
+    y[4 + e] = (acc[4 + e] * inv) * sigmoid_stable(gate_hi[e]);
+  }
   if (out != nullptr && lane < 16)
 #pragma unroll
     for (int e = 0; e < 8; ++e) out[o + e] = y[e];

@@ -69,6 +69,20 @@ __global__ __launch_bounds__(kRmsThreads) void rms_prep_kernel(RmsPrepArgs a) {
   __shared__ float red[kRmsThreads / 64];
   const int t = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int K = a.K, n4 = K >> 2;
+  const int nblk = K >> 7, j = tid & 15;
+  // (1 + w) of this thread's first quantization item, loaded together with
+  // the row so that no load waits behind the barrier
+  float w1[8];
+  {
+    const int blk = min(tid >> 4, nblk - 1);
+    const q35_f32x4 *wp = reinterpret_cast<const q35_f32x4 *>(a.weight + blk * 128 + 8 * j);
+    const q35_f32x4 lo = wp[0], hi = wp[1];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      w1[e] = lo[e] + 1.0F;
+      w1[4 + e] = hi[e] + 1.0F;
+    }
+  }
   const q35_f32x4 *xin = reinterpret_cast<const q35_f32x4 *>(a.x_in + static_cast<size_t>(t) * K);
   float ss = 0.0F;
   for (int i = tid; i < n4; i += kRmsThreads) {
@@ -93,22 +107,26 @@ __global__ __launch_bounds__(kRmsThreads) void rms_prep_kernel(RmsPrepArgs a) {
   }
   ss = group_sum<64>(ss);
   if (lane == 0) red[wave] = ss;
-  __syncthreads();
+  // only LDS is shared: the x_out stores stay in flight
+  lds_barrier();
   const float total = (red[0] + red[1]) + (red[2] + red[3]);
   const float rms_inv = 1.0F / sqrtf(total / static_cast<float>(K) + a.eps);
   QuantOut o;
   o.codes = a.codes;
   o.scales = a.scales;
-  const int nblk = K >> 7, j = tid & 15;
   for (int blk0 = 0; blk0 < nblk; blk0 += kRmsThreads / 16) {
     if (blk0 + wave * 4 >= nblk) break;  // wave-uniform: all four rows idle
     const int want = blk0 + (tid >> 4);
     const bool active = want < nblk;
     const int blk = active ? want : nblk - 1;
     const int c0 = blk * 128 + 8 * j;
+    if (blk0 > 0) {  // widths above 2048 columns: a second item per thread
+#pragma unroll
+      for (int e = 0; e < 8; ++e) w1[e] = a.weight[c0 + e] + 1.0F;
+    }
     float v[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = y[c0 + e] * rms_inv * (a.weight[c0 + e] + 1.0F);
+    for (int e = 0; e < 8; ++e) v[e] = y[c0 + e] * rms_inv * w1[e];
     if (a.normed_out != nullptr && active)
 #pragma unroll
       for (int e = 0; e < 8; ++e) a.normed_out[static_cast<size_t>(t) * K + c0 + e] = v[e];

@@ -52,9 +52,9 @@ template <int Waves>
 __device__ __forceinline__ float block_sum(float v, float *scratch) {
   v = group_sum<64>(v);
   const int wave = threadIdx.x >> 6;
-  __syncthreads();
+  lds_barrier();  // an earlier call's readers are done with scratch
   if ((threadIdx.x & 63) == 0) scratch[wave] = v;
-  __syncthreads();
+  lds_barrier();
   float total = 0.0F;
 #pragma unroll
   for (int w = 0; w < Waves; ++w) total += scratch[w];

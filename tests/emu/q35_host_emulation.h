@@ -66,6 +66,16 @@ inline thread_local ThreadCtx t_ctx;
 
 inline void wave_sync() { t_ctx.launch->waves[t_ctx.wave]->arrive_and_wait(); }
 
+// value of `v` in lane `src` of the wavefront (every lane must call it)
+inline int readlane(int v, int src) {
+  auto &slots = t_ctx.launch->slots_a[t_ctx.wave];
+  slots[t_ctx.lane] = static_cast<uint32_t>(v);
+  wave_sync();
+  const int got = static_cast<int>(static_cast<uint32_t>(slots[src & 63]));
+  wave_sync();
+  return got;
+}
+
 template <typename T>
 inline T shfl_xor(T v, int mask) {
   static_assert(sizeof(T) <= 8, "shuffle of at most 8 bytes");
@@ -187,6 +197,9 @@ inline unsigned long long atomicMax(unsigned long long *p, unsigned long long v)
   return cur;
 }
 inline unsigned __float_as_uint(float f) { unsigned u; std::memcpy(&u, &f, 4); return u; }
+inline int __builtin_amdgcn_readlane(int v, int src) { return ::q35emu::readlane(v, src); }
+inline int __float_as_int(float f) { int u; std::memcpy(&u, &f, 4); return u; }
+inline float __int_as_float(int u) { float f; std::memcpy(&f, &u, 4); return f; }
 inline float __uint_as_float(unsigned u) { float f; std::memcpy(&f, &u, 4); return f; }
 
 struct __half { uint16_t bits; };
