@@ -142,7 +142,8 @@ int q35_gated_delta_net_update_batch(q35_context *ctx, float *const *states, con
  * and walking page tables instead of per-token row pointers.
  * K/V pools are FP16 [page][page_tokens][kv_heads][head_dim]; page_table is
  * [batch][max_pages] int32 page ids; seq_lens[batch] (>= 1) tokens to attend.
- * q, gates, output are [batch][heads][head_dim]. head_dim must be 256 or 128. */
+ * q, gates, output are [batch][heads][head_dim]. head_dim must be 256 and
+ * page_tokens a power of two (Q35_ERR_UNSUPPORTED otherwise). */
 int q35_attention_decode_paged(q35_context *ctx, const float *q, const float *gates,
                                const uint16_t *k_pool, const uint16_t *v_pool,
                                const int32_t *page_table, size_t max_pages,

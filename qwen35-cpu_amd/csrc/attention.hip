@@ -37,7 +37,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_prep_kernel(AttnPrepArgs a)
   const int rd = min(d, a.rope_dim - 1) % half;
   const float cs = a.rope_cos[static_cast<size_t>(pos) * half + rd];
   const float sn = a.rope_sin[static_cast<size_t>(pos) * half + rd];
-  const int page = a.page_table[static_cast<size_t>(r) * a.max_pages + pos / a.page_tokens];
+  const int pshift = __builtin_ctz(static_cast<unsigned>(a.page_tokens));  // a power of two
+  const int page = a.page_table[static_cast<size_t>(r) * a.max_pages + (pos >> pshift)];
   // q head: [q | gate] of the head; k head: its K row and its V row
   const int col_x = is_q ? slot * 2 * hd + dd : a.heads * 2 * hd + g * hd + dd;
   const int col_2 = is_q ? slot * 2 * hd + hd + dd : a.heads * 2 * hd + a.kv_heads * hd + g * hd + dd;
@@ -62,81 +63,96 @@ __global__ __launch_bounds__(kAttnThreads) void attn_prep_kernel(AttnPrepArgs a)
   if (is_q) {
     a.q_out[(static_cast<size_t>(r) * a.heads + slot) * hd + d] = y;
   } else {
-    const size_t row = (static_cast<size_t>(page) * a.page_tokens + pos % a.page_tokens) * a.kv_heads + g;
+    const size_t row = ((static_cast<size_t>(page) << pshift) + (pos & (a.page_tokens - 1))) * a.kv_heads + g;
     a.k_pool[row * hd + d] = float_to_half_bits(y);
     a.v_pool[row * hd + d] = float_to_half_bits(second);
   }
 }
 
 // ---------------------------------------------------------------- attention
-// One workgroup per (chunk of kChunkTokens context tokens, KV head, request)
-// serves the QPK query heads of the GQA group, so every K/V byte is read
-// once. Thread t scores token t/4 over dims 64*(t%4)..+63 (eight 16-byte K
-// loads) and accumulates P*V for dims 4*(t%64)..+3 over tokens t/64 + 4j
-// (sixteen 8-byte V loads); all 24 loads are issued right after the page
-// table lookup. Scores are FP32 dot products over FP16 keys
-// (full_attention.cpp:82-93); the chunk leaves its partial (max, sum,
-// sum p*V) for the merge.
+// One workgroup of 512 threads per (chunk of kChunkTokens context tokens, KV
+// head, request) serves the QPK query heads of the GQA group, so every K/V
+// byte is read once. Thread t scores token t/8 over dims 32*(t%8)..+31 (four
+// 16-byte K loads) and accumulates P*V for dims 4*(t%64)..+3 over tokens
+// t/64 + 8j (eight 8-byte V loads). The page-table entries are loaded together
+// with the context length (a slot past the context reads the chunk's first
+// page and gets probability zero), so K and V are issued after one round
+// trip. Scores are FP32 dot products over FP16 keys (full_attention.cpp:82-93);
+// the chunk leaves its partial (max, sum, sum p*V) for the merge.
 constexpr int kChunkTokens = 64;
-constexpr int kQStride = 68;  // 64 dims + 4: the four dim-quarters land on distinct LDS banks
+constexpr int kScoreThreads = 512;
+constexpr int kScoreWaves = kScoreThreads / 64;
+constexpr int kQStride = 36;  // 32 dims + 4: the eight dim slices land on distinct LDS banks
 
 template <int QPK>
-__global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
-  __shared__ float qs[QPK * 4 * kQStride];
+__global__ __launch_bounds__(kScoreThreads) __attribute__((amdgpu_waves_per_eu(4))) void attention_kernel(AttnArgs a) {
+  constexpr int NQ = (QPK * kHeadDim + kScoreThreads - 1) / kScoreThreads;  // query values staged per thread
+  __shared__ float qs[QPK * 8 * kQStride];
   __shared__ float probs[QPK][kChunkTokens];
   __shared__ float s_m[QPK], s_l[QPK];
-  __shared__ float red[4][QPK][kHeadDim];
-  static_assert(kAttnThreads == kHeadDim, "thread d stages dim d of every query head");
+  __shared__ float red[kScoreWaves][QPK][kHeadDim];
   const int sp = blockIdx.x, g = blockIdx.y, r = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  // Loads in the order they are consumed (the memory counter retires them in
-  // issue order): the group's query heads (with the context length), then
-  // the page table, K and V, so the query staging waits only for the
-  // queries and V keeps arriving during the scores and the softmax.
-  float qv[QPK];
-#pragma unroll
-  for (int u = 0; u < QPK; ++u) qv[u] = a.q[(static_cast<size_t>(r) * a.heads + g * QPK + u) * kHeadDim + tid];
-  const int seq = a.seq_lens != nullptr ? a.seq_lens[r] : a.positions[r] + 1;
+  const int kq = tid & 7, ti = tid >> 3;
   const int t0 = sp * kChunkTokens;
-  if (t0 >= seq) return;  // whole workgroup
-  const int n = min(seq - t0, kChunkTokens);
   const int kvw = a.kv_heads * kHeadDim;
   const int32_t *pt = a.page_table + static_cast<size_t>(r) * a.max_pages;
+  const int last_page = a.max_pages - 1;
+  // page_tokens is a power of two: shifts and masks, not integer division
+  const int pshift = __builtin_ctz(static_cast<unsigned>(a.page_tokens)), pmask = a.page_tokens - 1;
+  // one round trip: the query heads, the context length and the page-table
+  // entries of every token slot (clamped into the row)
+  float qv[NQ];
+#pragma unroll
+  for (int k = 0; k < NQ; ++k) {
+    const int e = min(tid + k * kScoreThreads, QPK * kHeadDim - 1);
+    qv[k] = a.q[(static_cast<size_t>(r) * a.heads + g * QPK + e / kHeadDim) * kHeadDim + e % kHeadDim];
+  }
+  const int seq = a.seq_lens != nullptr ? a.seq_lens[r] : a.positions[r] + 1;
+  const int pfirst = pt[min(t0 >> pshift, last_page)];
+  const int pk = pt[min((t0 + ti) >> pshift, last_page)];
+  int pv[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) pv[j] = pt[min((t0 + wave + 8 * j) >> pshift, last_page)];
+  if (t0 >= seq) return;  // whole workgroup
+  const int n = min(seq - t0, kChunkTokens);
 
-  // K: token ti = tid/4 (clamped into the chunk), dims 64*qq .. +63
-  const int qq = tid & 3, ti = min(tid >> 2, n - 1);
-  const int ktok = t0 + ti;
-  int vpage[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) vpage[j] = pt[(t0 + min(wave + 4 * j, n - 1)) / a.page_tokens];
-  const int kpage = pt[ktok / a.page_tokens];
+  // K, then V (the memory counter retires loads in issue order)
+  const bool kin = ti < n;
+  const int ktok = kin ? t0 + ti : t0;
   const q35_u32x4 *krow = reinterpret_cast<const q35_u32x4 *>(
-      a.k_pool + (static_cast<size_t>(kpage) * a.page_tokens + ktok % a.page_tokens) * kvw +
-      static_cast<size_t>(g) * kHeadDim + 64 * qq);
-  q35_u32x4 kraw[8];
+      a.k_pool + ((static_cast<size_t>(kin ? pk : pfirst) << pshift) + (ktok & pmask)) * kvw +
+      static_cast<size_t>(g) * kHeadDim + 32 * kq);
+  q35_u32x4 kraw[4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) kraw[i] = Q35_LOAD_NT(krow + i);
-  // V: tokens wave + 4j (clamped), dims 4*lane .. +3
-  q35_u32x2 vraw[16];
+  for (int i = 0; i < 4; ++i) kraw[i] = Q35_LOAD_NT(krow + i);
+  q35_u32x2 vraw[8];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const int vt = t0 + min(wave + 4 * j, n - 1);
+  for (int j = 0; j < 8; ++j) {
+    const bool vin = wave + 8 * j < n;
+    const int vt = vin ? t0 + wave + 8 * j : t0;
     vraw[j] = Q35_LOAD_NT(reinterpret_cast<const q35_u32x2 *>(
-        a.v_pool + (static_cast<size_t>(vpage[j]) * a.page_tokens + vt % a.page_tokens) * kvw +
+        a.v_pool + ((static_cast<size_t>(vin ? pv[j] : pfirst) << pshift) + (vt & pmask)) * kvw +
         static_cast<size_t>(g) * kHeadDim + 4 * lane));
   }
 
-  // the group's query heads into LDS, quarter-padded
+  // the group's query heads into LDS, in eight padded 32-dim slices
 #pragma unroll
-  for (int u = 0; u < QPK; ++u) qs[(u * 4 + tid / 64) * kQStride + tid % 64] = qv[u];
+  for (int k = 0; k < NQ; ++k) {
+    const int e = tid + k * kScoreThreads;
+    if (e < QPK * kHeadDim) {
+      const int u = e / kHeadDim, d = e % kHeadDim;
+      qs[(u * 8 + d / 32) * kQStride + d % 32] = qv[k];
+    }
+  }
   lds_barrier();
 
-  // ---- scores
+  // ---- scores: 32 dims per thread, then the 8 lanes of the token
   float part[QPK];
 #pragma unroll
   for (int u = 0; u < QPK; ++u) part[u] = 0.0F;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < 4; ++i) {
     float kf[8];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -145,23 +161,28 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     }
 #pragma unroll
     for (int u = 0; u < QPK; ++u) {
-      const float *qp = qs + (u * 4 + qq) * kQStride + 8 * i;
+      const float *qp = qs + (u * 8 + kq) * kQStride + 8 * i;
       const q35_f32x4 qa = *reinterpret_cast<const q35_f32x4 *>(qp);
       const q35_f32x4 qb = *reinterpret_cast<const q35_f32x4 *>(qp + 4);
       part[u] += qa[0] * kf[0] + qa[1] * kf[1] + qa[2] * kf[2] + qa[3] * kf[3] + qb[0] * kf[4] +
                  qb[1] * kf[5] + qb[2] * kf[6] + qb[3] * kf[7];
     }
+    // one iteration at a time: no hoisted query reads, no sunk dot products
+#pragma unroll
+    for (int u = 0; u < QPK; ++u) q35_materialize(part[u]);
+    q35_compiler_fence();
   }
 #pragma unroll
   for (int u = 0; u < QPK; ++u) {
-    part[u] += q35_quad_xor1(part[u]);
-    part[u] += q35_quad_xor2(part[u]);
-    if (qq == 0) probs[u][tid >> 2] = (tid >> 2) < n ? part[u] * a.scale : -INFINITY;
+    part[u] += q35_row_xor(part[u], 1);
+    part[u] += q35_row_xor(part[u], 2);
+    part[u] += q35_row_xor(part[u], 4);
+    if (kq == 0) probs[u][ti] = kin ? part[u] * a.scale : -INFINITY;
   }
   lds_barrier();
 
-  // ---- chunk softmax statistics (wave u handles head u, u += 4)
-  for (int u = wave; u < QPK; u += kAttnThreads / 64) {
+  // ---- chunk softmax statistics (wave u handles head u)
+  for (int u = wave; u < QPK; u += kScoreWaves) {
     const float s = probs[u][lane];
     const float m = group_max<64>(s);
     const float p = lane < n ? expf(s - m) : 0.0F;
@@ -179,8 +200,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
 #pragma unroll
   for (int u = 0; u < QPK; ++u) acc[u][0] = acc[u][1] = acc[u][2] = acc[u][3] = 0.0F;
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const int i = wave + 4 * j;
+  for (int j = 0; j < 8; ++j) {
+    const int i = wave + 8 * j;
     const float v0 = half_bits_to_float(static_cast<uint16_t>(vraw[j][0] & 0xffffu));
     const float v1 = half_bits_to_float(static_cast<uint16_t>(vraw[j][0] >> 16));
     const float v2 = half_bits_to_float(static_cast<uint16_t>(vraw[j][1] & 0xffffu));
@@ -193,14 +214,21 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
       acc[u][2] += p * v2;
       acc[u][3] += p * v3;
     }
+#pragma unroll
+    for (int u = 0; u < QPK; ++u)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) q35_materialize(acc[u][k]);
+    q35_compiler_fence();
   }
 #pragma unroll
   for (int u = 0; u < QPK; ++u)
     *reinterpret_cast<q35_f32x4 *>(&red[wave][u][4 * lane]) = q35_f32x4{acc[u][0], acc[u][1], acc[u][2], acc[u][3]};
   lds_barrier();
-  for (int e = tid; e < QPK * kHeadDim; e += kAttnThreads) {
+  for (int e = tid; e < QPK * kHeadDim; e += kScoreThreads) {
     const int u = e / kHeadDim, d = e % kHeadDim;
-    const float v = ((red[0][u][d] + red[1][u][d]) + red[2][u][d]) + red[3][u][d];
+    float v = red[0][u][d];
+#pragma unroll
+    for (int w = 1; w < kScoreWaves; ++w) v += red[w][u][d];
     const size_t hs = (static_cast<size_t>(r) * a.heads + g * QPK + u) * a.max_splits + sp;
     a.part_o[hs * kHeadDim + d] = v;
     if (d == 0) {
@@ -317,7 +345,7 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
   if (a.head_dim != kHeadDim || a.heads % a.kv_heads != 0 || a.split_tokens != kChunkTokens)
     return hipErrorInvalidValue;
   const int qpk = a.heads / a.kv_heads;
-  const dim3 grid(a.max_splits, a.kv_heads, a.batch), block(kAttnThreads);
+  const dim3 grid(a.max_splits, a.kv_heads, a.batch), block(kScoreThreads);
   switch (qpk) {
     case 1: Q35_LAUNCH((attention_kernel<1>), grid, block, 0, stream, a); break;
     case 2: Q35_LAUNCH((attention_kernel<2>), grid, block, 0, stream, a); break;

@@ -51,6 +51,14 @@ __device__ __forceinline__ float q35_row_xor(float v, int m) {
 // Workgroup barrier that orders LDS only: outstanding global loads and
 // stores keep flying (__syncthreads is a release fence at workgroup scope and
 // waits for them -- on gfx9 the vmcnt counter covers loads and stores).
+// Compiler-only fence: no memory access is moved across it (no instruction
+// is emitted). Bounds how far the compiler hoists loads out of unrolled loops.
+__device__ __forceinline__ void q35_compiler_fence() { asm volatile("" ::: "memory"); }
+// Forces `x` to be computed at this point (an empty asm reading and writing
+// it), so the compiler cannot sink the arithmetic that produces it past later
+// loads and keep their results live meanwhile.
+__device__ __forceinline__ void q35_materialize(float &x) { asm volatile("" : "+v"(x)); }
+
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();

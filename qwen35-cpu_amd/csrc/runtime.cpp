@@ -441,8 +441,10 @@ extern "C" int q35_attention_decode_paged(q35_context *ctx, const float *q, cons
                                           float *output, size_t batch, int heads, int kv_heads,
                                           int head_dim, float scale) {
   if (ctx == nullptr || q == nullptr || gates == nullptr || output == nullptr) return Q35_ERR_INVALID;
-  if (head_dim != 256 || kv_heads <= 0 || heads % kv_heads != 0 || batch == 0 || page_tokens == 0)
-    return set_error(ctx, Q35_ERR_UNSUPPORTED, "attention needs head_dim 256 and heads % kv_heads == 0");
+  if (head_dim != 256 || kv_heads <= 0 || heads % kv_heads != 0 || batch == 0 || page_tokens == 0 ||
+      (page_tokens & (page_tokens - 1)) != 0 || page_tokens > (1u << 20))
+    return set_error(ctx, Q35_ERR_UNSUPPORTED,
+                     "attention needs head_dim 256, heads % kv_heads == 0 and a power-of-two page size");
   std::vector<int32_t> lens(batch);
   Q35_HIP_TRY(ctx, hipMemcpyAsync(lens.data(), seq_lens, batch * 4, hipMemcpyDeviceToHost, ctx->stream));
   Q35_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));

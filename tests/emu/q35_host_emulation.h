@@ -238,6 +238,8 @@ typedef unsigned int q35_u32x2 __attribute__((vector_size(8)));
 typedef float q35_f32x4 __attribute__((vector_size(16)));
 #define Q35_LOAD_NT(ptr) (*(ptr))
 inline void lds_barrier() { __syncthreads(); }
+inline void q35_compiler_fence() { asm volatile("" ::: "memory"); }
+inline void q35_materialize(float &) {}
 inline int __lane_id() { return ::q35emu::t_ctx.lane; }
 inline float q35_quad_xor1(float v) { return ::q35emu::shfl_xor(v, 1); }
 inline float q35_quad_xor2(float v) { return ::q35emu::shfl_xor(v, 2); }
