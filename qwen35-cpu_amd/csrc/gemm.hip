@@ -582,9 +582,10 @@ GemmPlan gemm_plan(int rows, int nb, bool exact, bool argmax, int cu_count, int 
     p.grid = std::min(groups, 8 * cus);
   } else {
     // one wavefront per workgroup; K split across workgroups in chunks of 8
-    // blocks when the row groups alone give >= 64 workgroups, else of 4
-    // blocks (narrow outputs: more, shallower splits)
-    p.ks = force_ks > 0 ? force_ks : (groups >= 64 ? 8 : 4);
+    // blocks. (Chunks of 4 for narrow outputs give the GEMM more workgroups,
+    // but twice the split partials for the consumer to read: the decode step
+    // measured faster with 8 throughout.)
+    p.ks = force_ks > 0 ? force_ks : 8;
     const int chunks = (nb + p.ks - 1) / p.ks;
     p.split = force_split > 0 ? std::min(force_split, chunks) : std::min(chunks, 32);
     const int per_split = (chunks + p.split - 1) / p.split;
