@@ -54,14 +54,20 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
   // global-address-space loads rather than FLAT ones that would also hold
   // every LDS wait)
   float *state_r;
-  if constexpr (FUSED)
-    state_r = a.state_base + static_cast<long long>(a.slots[r]) * a.state_slot_stride;
-  else
+  long long write_offset = 0;  // floats from the loaded state to the stored one
+  if constexpr (FUSED) {
+    const int parity = a.state_copy_stride > 0 ? (a.positions[r] & 1) : 0;
+    state_r = a.state_base + static_cast<long long>(a.slots[r]) * a.state_slot_stride + parity * a.state_copy_stride;
+    write_offset = a.state_copy_stride > 0 ? (1 - 2 * parity) * a.state_copy_stride : 0;
+  } else {
     state_r = a.state_base != nullptr ? a.state_base + static_cast<long long>(a.slots[r]) * a.state_slot_stride
                                       : a.states[r];
+  }
   q35_f32x4 *S = reinterpret_cast<q35_f32x4 *>(state_r + static_cast<size_t>(vh) * kDim * kDim);
   q35_f32x4 *S0 = S + rowp * (kDim / 4) + quad;         // row rowp
   q35_f32x4 *S1 = S + (rowp + 64) * (kDim / 4) + quad;  // row rowp + 64
+  q35_f32x4 *W0 = reinterpret_cast<q35_f32x4 *>(reinterpret_cast<float *>(S0) + write_offset);
+  q35_f32x4 *W1 = reinterpret_cast<q35_f32x4 *>(reinterpret_cast<float *>(S1) + write_offset);
   q35_f32x4 st0[8], st1[8];
   auto load_state = [&]() {
 #pragma unroll
@@ -213,8 +219,8 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
   auto store_state = [&]() {
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
-      Q35_STORE_NT(st0[m], S0 + 4 * m);
-      Q35_STORE_NT(st1[m], S1 + 4 * m);
+      Q35_STORE_NT(st0[m], W0 + 4 * m);
+      Q35_STORE_NT(st1[m], W1 + 4 * m);
     }
   };
   if (wave != 0) {

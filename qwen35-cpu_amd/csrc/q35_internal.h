@@ -222,6 +222,12 @@ struct DeltaArgs {
   float *state_base = nullptr;     // alternative: slot-strided base
   const int32_t *slots = nullptr;  // [batch] slot of each row (with state_base)
   long long state_slot_stride = 0; // floats between slots
+  // fused mode: > 0 selects double-buffered state -- the row at position p
+  // reads the copy at (p & 1) * stride and writes the other one, so the
+  // update never stores over the lines it just loaded (such stores leave
+  // dirty lines in the last-level cache that a later streaming kernel pays
+  // to write back); 0 updates in place
+  long long state_copy_stride = 0;
   int batch = 0, k_heads = 0, v_heads = 0, kd = 0, vd = 0;
   // raw mode inputs
   const float *q = nullptr, *k = nullptr, *v = nullptr, *alpha = nullptr, *beta = nullptr;

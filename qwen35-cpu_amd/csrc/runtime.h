@@ -49,10 +49,10 @@ struct q35_runtime {
   int max_pages_per_row = 0;
   int split_tokens = q35::kAttnChunkTokens, max_splits = 1;
   // slot state
-  float *recurrent = nullptr;  // [slots][n_lin][vh][vd][kd]
+  float *recurrent = nullptr;  // [slots][2 copies][n_lin][vh][vd][kd]
   float *conv = nullptr;       // [slots][n_lin][kernel-1][channels]
   int32_t *counts = nullptr;   // [slots][vocab]
-  long long rec_slot_stride = 0, conv_slot_stride = 0;
+  long long rec_slot_stride = 0, rec_copy_stride = 0, conv_slot_stride = 0;
   std::vector<uint8_t> slot_used;
   // KV pool [n_full][pages][page_tokens][kvh][hd]
   uint16_t *k_pool = nullptr, *v_pool = nullptr;

@@ -312,7 +312,10 @@ extern "C" int q35_runtime_create(q35_model *m, const q35_runtime_config *cfg, q
     if (st == Q35_OK) st = rt_alloc(rt, bytes, p);
   };
   // slot state
-  rt->rec_slot_stride = static_cast<long long>(m->n_linear) * d.lin_v_heads * d.lin_v_dim * d.lin_k_dim;
+  // two copies of every slot's recurrent state: the step at position p reads
+  // copy p & 1 and writes the other one (see DeltaArgs::state_copy_stride)
+  rt->rec_copy_stride = static_cast<long long>(m->n_linear) * d.lin_v_heads * d.lin_v_dim * d.lin_k_dim;
+  rt->rec_slot_stride = 2 * rt->rec_copy_stride;
   // conv ring of lin_kernel slots per layer, slot = position % lin_kernel
   rt->conv_slot_stride = static_cast<long long>(m->n_linear) * d.lin_kernel * ch;
   alloc(static_cast<size_t>(cfg->max_slots) * rt->rec_slot_stride * 4, reinterpret_cast<void **>(&rt->recurrent));
@@ -640,6 +643,7 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
       a.state_base = rt->recurrent + static_cast<size_t>(li) * d.lin_v_heads * d.lin_v_dim * d.lin_k_dim;
       a.slots = slots;
       a.state_slot_stride = rt->rec_slot_stride;
+      a.state_copy_stride = rt->rec_copy_stride;
       a.batch = batch;
       a.k_heads = d.lin_k_heads;
       a.v_heads = d.lin_v_heads;
