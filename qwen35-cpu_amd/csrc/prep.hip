@@ -7,8 +7,8 @@
 //   signs + FWHT stage order 1,2,...,64     src/cpu/q4_h128.cpp:35-61
 //   absmax/127, unrounded 1/scale, round half away from zero, clamp +-127,
 //   stored scale = binary16(scale) * 1/sqrt(128)   q4_0.cpp:212-235, q4_h128.cpp:319-321
-// prep_kernel: 16 lanes per (token, 128-column block), sixteen blocks per
-// workgroup. rms_prep_kernel: one workgroup per token (the row's sum of
+// prep_kernel: 16 lanes per (token, 128-column block), four blocks per
+// one-wavefront workgroup. rms_prep_kernel: one workgroup per token (the row's sum of
 // squares is shared through LDS).
 #include "q35_quant.h"
 
@@ -37,7 +37,7 @@ __device__ __forceinline__ void load_source8(const PrepArgs &a, int t, int c0, f
   }
 }
 
-// 16 lanes per (token, 128-column block) item, 16 items per workgroup; MS
+// 16 lanes per (token, 128-column block) item, four items per wavefront; MS
 // bounds the source's K splits.
 template <int SRC, int MS>
 __global__ __launch_bounds__(kPrepThreads) void prep_kernel(PrepArgs a) {
@@ -170,8 +170,12 @@ __global__ void x1_to_a16_kernel(const q35_q8_0_block_x1 *x1, int nb, uint64_t *
 
 hipError_t launch_prep(const PrepArgs &a, hipStream_t stream) {
   if (a.tokens <= 0) return hipSuccess;
+  // one wavefront (four items) per workgroup: the split partials a SiLU
+  // preparation reads spread over 4x more compute units than with 256-thread
+  // workgroups (one unit keeps only a few tens of KiB in flight)
+  constexpr int kThreads = 64;
   const int items = a.tokens * (a.K >> 7);
-  const dim3 grid((items + kPrepThreads / 16 - 1) / (kPrepThreads / 16)), block(kPrepThreads);
+  const dim3 grid((items + kThreads / 16 - 1) / (kThreads / 16)), block(kThreads);
   if (a.source == kPrepSiluMul) {
     switch (split_bound(a.gate_up.splits)) {
       case 1: Q35_LAUNCH((prep_kernel<kPrepSiluMul, 1>), grid, block, 0, stream, a); break;

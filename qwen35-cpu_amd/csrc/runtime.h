@@ -70,7 +70,7 @@ struct q35_runtime {
   // greedy head: per-workgroup best keys [cand_rows][kMaxTokens]
   unsigned long long *cand = nullptr;
   int cand_rows = 0;
-  int32_t *tokens_out_dev = nullptr;
+  int32_t *tokens_out_dev = nullptr;  // device address of tokens_out_host (pinned, mapped)
   // step metadata (pinned host + device copy)
   size_t meta_bytes = 0;
   unsigned char *meta_host = nullptr, *meta_dev = nullptr;

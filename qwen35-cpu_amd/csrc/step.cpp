@@ -353,14 +353,18 @@ extern "C" int q35_runtime_create(q35_model *m, const q35_runtime_config *cfg, q
   alloc(4 * 16 * (kmax / 32) * sizeof(float), reinterpret_cast<void **>(&rt->scales));
   rt->cand_rows = gemm_argmax_cand_capacity(d.vocab, ctx->cu_count);
   alloc(static_cast<size_t>(rt->cand_rows) * kMaxTokens * 8, reinterpret_cast<void **>(&rt->cand));
-  alloc(kMaxTokens * 4, reinterpret_cast<void **>(&rt->tokens_out_dev));
   const MetaLayout ml = meta_layout(B, rt->max_pages_per_row);
   rt->meta_bytes = ml.total;
   alloc(ml.total, reinterpret_cast<void **>(&rt->meta_dev));
   if (st == Q35_OK && hipHostMalloc(reinterpret_cast<void **>(&rt->meta_host), ml.total) != hipSuccess)
     st = set_error(ctx, Q35_ERR_OOM, "pinned metadata");
+  // the greedy tokens are stored by the argmax kernel straight into pinned
+  // host memory (no copy node at the end of the step)
   if (st == Q35_OK && hipHostMalloc(reinterpret_cast<void **>(&rt->tokens_out_host), kMaxTokens * 4) != hipSuccess)
     st = set_error(ctx, Q35_ERR_OOM, "pinned output");
+  if (st == Q35_OK &&
+      hipHostGetDevicePointer(reinterpret_cast<void **>(&rt->tokens_out_dev), rt->tokens_out_host, 0) != hipSuccess)
+    st = set_error(ctx, Q35_ERR_HIP, "device address of the pinned output");
   if (st == Q35_OK) {
     std::vector<float> inv(half), cs(static_cast<size_t>(cfg->max_context) * half), sn(cs.size());
     for (size_t i = 0; i < half; ++i)
@@ -780,8 +784,6 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
     Q35_KERNEL(Q35_KERNEL_ARGMAX, ncand * B * 8.0 + B * 4.0,
                launch_argmax_finalize(rt->cand, ncand, kMaxTokens, batch, rt->tokens_out_dev, nullptr, s),
                "argmax finalize");
-    Q35_STEP(hipMemcpyAsync(rt->tokens_out_host, rt->tokens_out_dev, batch * 4, hipMemcpyDeviceToHost, s),
-             "token copy");
   }
 #undef Q35_KERNEL
 #undef Q35_STEP
