@@ -278,6 +278,19 @@ typedef struct {
 } q35_step_desc;
 int q35_runtime_step(q35_runtime *rt, const q35_step_desc *desc, int32_t *out_tokens,
                      float *out_logits);
+/* Chunked prefill of one request: prompt tokens tokens[0..count) at positions
+ * pos0 .. pos0 + count - 1 run through every layer in one pass -- the prefill
+ * chunk of CpuEngine::advance (cpu_engine.inl:668-790; run_forward_cpu_q8_batch,
+ * prefill.inl:599-791). The DeltaNet recurrence scans the chunk in order and
+ * attention is causal over the request's KV pages plus the chunk, so the
+ * resulting state equals count single-token steps. count <= max_batch;
+ * page_table[max_pages] covers positions 0 .. pos0 + count - 1. The prompt
+ * tokens must already be counted (q35_slot_alloc does). out_token (optional)
+ * receives the greedy token after the chunk's last position: the first
+ * generated token when the chunk ends the prompt. */
+int q35_runtime_prefill(q35_runtime *rt, int32_t slot, int32_t pos0, const int32_t *tokens,
+                        int32_t count, const int32_t *page_table, int32_t max_pages, float penalty,
+                        int32_t *out_token);
 /* Copies the final normalized hidden rows of the last step ([batch][hidden]). */
 int q35_runtime_last_hidden(q35_runtime *rt, float *out, size_t count);
 

@@ -135,6 +135,7 @@ _SIGS = {
     "q35_page_refcount": (c_int, [P, c_int32]),
     "q35_runtime_free_pages": (c_int, [P]),
     "q35_runtime_step": (c_int, [P, POINTER(StepDesc), P, P]),
+    "q35_runtime_prefill": (c_int, [P, c_int32, c_int32, P, c_int32, P, c_int32, c_float, P]),
     "q35_runtime_last_hidden": (c_int, [P, P, c_size_t]),
     "q35_runtime_set_profiling": (c_int, [P, c_int]),
     "q35_runtime_profile_reset": (c_int, [P]),
@@ -457,6 +458,17 @@ class Runtime(_Profiled):
         lg = np.empty((b, self.model.dims.vocab), np.float32) if logits else None
         self.ctx.check(lib.q35_runtime_step(self.handle, ctypes.byref(d), _ptr(out), _ptr(lg)), "runtime step")
         return (out, lg) if logits else out
+
+    def prefill(self, slot, pos0, tokens, page_table, penalty=1.0):
+        """Chunked prefill of one request (q35_runtime_prefill): returns the
+        greedy token after the chunk's last position."""
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        table = np.ascontiguousarray(page_table, np.int32).ravel()
+        out = np.empty(1, np.int32)
+        self.ctx.check(lib.q35_runtime_prefill(self.handle, int(slot), int(pos0), _ptr(tokens), tokens.size,
+                                               _ptr(table), table.size, float(penalty), _ptr(out)),
+                       "runtime prefill")
+        return int(out[0])
 
     def _rt(self):
         return self.handle

@@ -16,7 +16,6 @@ namespace {
 
 constexpr int kHeadDim = 256;
 constexpr int kAttnThreads = 256;
-constexpr int kMaxGroup = 8;  // query heads per KV head
 
 template <int MS>  // bound on the qkv projection's K splits
 __global__ __launch_bounds__(kAttnThreads) void attn_prep_kernel(AttnPrepArgs a) {

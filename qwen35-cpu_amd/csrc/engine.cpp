@@ -217,41 +217,38 @@ extern "C" int q35_engine_submit(q35_engine *e, const int32_t *prompt, size_t n,
   return Q35_OK;
 }
 
-// Prefill `rows` jointly, one prompt token per row per device step, until each
-// row has consumed `limit` more tokens or its prompt. The step that consumes
-// the last prompt token yields the first generated token.
-static int prefill_rows(q35_engine *e, std::vector<Request *> rows, size_t limit) {
+// Prefill one request for up to `limit` prompt tokens (one advance() chunk,
+// cpu_engine.inl:668-790) in device chunks of at most max_decode_batch_size
+// positions each (q35_runtime_prefill). The chunk that consumes the last
+// prompt token yields the first generated token.
+static int prefill_chunks(q35_engine *e, Request &r, size_t limit) {
   const auto t0 = std::chrono::steady_clock::now();
-  std::vector<Request *> all = rows;
-  while (!rows.empty()) {
-    std::vector<int32_t> in, out;
-    std::vector<uint8_t> cnt;
-    for (auto *r : rows) {
-      in.push_back(r->prompt[r->committed]);
-      cnt.push_back(0);
-    }
-    const int st = run_step(e, rows, in, cnt, out);
+  const size_t rows = static_cast<size_t>(e->cfg.max_decode_batch_size);
+  const int max_pages = (e->cfg.max_context + e->cfg.page_tokens - 1) / e->cfg.page_tokens;
+  std::vector<int32_t> table(max_pages, 0);
+  size_t done = 0;
+  while (done < limit && r.committed < r.prompt.size()) {
+    const size_t n = std::min({rows, limit - done, r.prompt.size() - r.committed});
+    int st = ensure_page(e, r, r.committed + n - 1);
     if (st != Q35_OK) {
-      fail_rows(all);
+      r.status = Q35_REQ_FAILED;
       return st;
     }
-    std::vector<Request *> next;
-    for (size_t i = 0; i < rows.size(); ++i) {
-      Request *r = rows[i];
-      ++r->result.prefill_tokens;
-      if (r->committed == r->prompt.size()) {
-        select_token(*r, out[i]);
-      } else if (r->result.prefill_tokens % limit != 0) {
-        next.push_back(r);
-      }
+    std::copy(r.pages.begin(), r.pages.end(), table.begin());
+    int32_t out = -1;
+    st = q35_runtime_prefill(e->rt, r.slot, static_cast<int32_t>(r.committed), r.prompt.data() + r.committed,
+                             static_cast<int32_t>(n), table.data(), max_pages, r.penalty, &out);
+    if (st != Q35_OK) {
+      r.status = Q35_REQ_FAILED;
+      return fail(e, st, e->model->ctx->error.c_str());
     }
-    rows.swap(next);
+    r.committed += n;
+    r.result.prefill_tokens += n;
+    done += n;
+    if (r.committed == r.prompt.size()) select_token(r, out);
   }
-  const double ms = ms_since(t0);
-  for (auto *r : all) {
-    r->result.prefill_ms += ms / all.size();
-    r->result.committed_tokens = r->committed;
-  }
+  r.result.prefill_ms += ms_since(t0);
+  r.result.committed_tokens = r.committed;
   return Q35_OK;
 }
 
@@ -261,7 +258,7 @@ extern "C" int q35_engine_advance(q35_engine *e, uint64_t id) {
   auto it = e->reqs.find(id);
   if (it == e->reqs.end()) return fail(e, Q35_ERR_STATE, "Unknown request ID.");
   Request &r = it->second;
-  if (r.status == Q35_REQ_PREFILL) return prefill_rows(e, {&r}, static_cast<size_t>(e->cfg.prefill_chunk_size));
+  if (r.status == Q35_REQ_PREFILL) return prefill_chunks(e, r, static_cast<size_t>(e->cfg.prefill_chunk_size));
   if (r.status != Q35_REQ_DECODE) return fail(e, Q35_ERR_STATE, "Request is not active.");
   return q35_engine_advance_batch(e, &id, 1);
 }
@@ -304,8 +301,9 @@ extern "C" int q35_engine_advance_batch(q35_engine *e, const uint64_t *ids, size
   return Q35_OK;
 }
 
-// Extension without a reference counterpart: prefill several requests in the
-// same device steps (the reference prefills one request per advance()).
+// Extension without a reference counterpart: prefill several requests to the
+// end of their prompts in one call (the reference prefills one chunk of one
+// request per advance()).
 extern "C" int q35_engine_prefill_batch(q35_engine *e, const uint64_t *ids, size_t count) {
   if (e == nullptr || (count && ids == nullptr)) return Q35_ERR_INVALID;
   e->error.clear();
@@ -319,7 +317,11 @@ extern "C" int q35_engine_prefill_batch(q35_engine *e, const uint64_t *ids, size
       return fail(e, Q35_ERR_INVALID, "Prefill batch requires distinct prefilling requests.");
     rows.push_back(&it->second);
   }
-  return prefill_rows(e, rows, static_cast<size_t>(e->cfg.max_context));
+  for (auto *r : rows) {
+    const int st = prefill_chunks(e, *r, r->prompt.size());
+    if (st != Q35_OK) return st;
+  }
+  return Q35_OK;
 }
 
 extern "C" int q35_engine_step(q35_engine *e, int32_t *progressed) {

@@ -248,6 +248,9 @@ struct DeltaArgs {
   uint64_t seed = 0;
 };
 hipError_t launch_delta(const DeltaArgs &a, hipStream_t stream);
+// Chunked prefill: the `batch` rows are consecutive positions of ONE request
+// (slots[0], positions[0] + r), scanned in order by one workgroup per head.
+hipError_t launch_delta_chunk(const DeltaArgs &a, hipStream_t stream);
 
 // Full attention
 struct AttnPrepArgs {

@@ -90,7 +90,9 @@ struct q35_runtime {
 };
 
 namespace q35 {
-int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits);
+// `prefill`: the rows are consecutive positions of one request (a prompt
+// chunk); the DeltaNet recurrence then scans them in order.
+int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool prefill);
 // Algorithmic HBM bytes of one GEMM launch: packed weights, A16 codes and
 // scales of every token, FP32 outputs (and the residual read when fused).
 double gemm_algorithmic_bytes(int rows, int nb, int tokens, bool stores, bool residual);

@@ -531,7 +531,7 @@ int profile_collect(q35_runtime *rt) {
 // Enqueues one decode step for `batch` rows whose metadata is already in
 // rt->meta_host; the host copy is part of the enqueued work so the whole
 // sequence can be captured as a graph.
-int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
+int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool prefill) {
   q35_model *m = rt->model;
   Context *ctx = rt->ctx;
   const q35_model_dims &d = m->d;
@@ -672,7 +672,7 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits) {
       const double delta_bytes =
           B * (2.0 * d.lin_v_heads * d.lin_v_dim * d.lin_k_dim * 4.0 + pending.splits * L.in_rows * 4.0 +
                static_cast<double>(d.lin_kernel) * ch * 4.0 + v_dim + v_dim / 32.0 * 4.0);
-      Q35_KERNEL(Q35_KERNEL_DELTA, delta_bytes, launch_delta(a, s), "DeltaNet");
+      Q35_KERNEL(Q35_KERNEL_DELTA, delta_bytes, (prefill ? launch_delta_chunk(a, s) : launch_delta(a, s)), "DeltaNet");
     } else {
       const int fi = m->full_index[l];
       AttnPrepArgs p;
@@ -851,7 +851,7 @@ extern "C" int q35_runtime_step(q35_runtime *rt, const q35_step_desc *desc, int3
     if (it == rt->graphs.end()) {
       Q35_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
       Q35_HIP_TRY(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
-      st = runtime_enqueue_step(rt, B, want_logits);
+      st = runtime_enqueue_step(rt, B, want_logits, false);
       hipGraph_t graph = nullptr;
       const hipError_t ce = hipStreamEndCapture(ctx->stream, &graph);
       if (st != Q35_OK) {
@@ -867,7 +867,7 @@ extern "C" int q35_runtime_step(q35_runtime *rt, const q35_step_desc *desc, int3
     }
     Q35_HIP_TRY(ctx, hipGraphLaunch(it->second, ctx->stream));
   } else {
-    st = runtime_enqueue_step(rt, B, want_logits);
+    st = runtime_enqueue_step(rt, B, want_logits, false);
     if (st != Q35_OK) return st;
   }
   if (want_logits)
@@ -925,6 +925,59 @@ extern "C" int q35_runtime_profile_read(q35_runtime *rt, int cls, double *total_
   if (total_ms) *total_ms = rt->prof_ms[cls];
   if (launches) *launches = rt->prof_launches[cls];
   if (bytes) *bytes = rt->prof_bytes[cls];
+  return Q35_OK;
+}
+
+extern "C" int q35_runtime_prefill(q35_runtime *rt, int32_t slot, int32_t pos0, const int32_t *tokens,
+                                   int32_t count, const int32_t *page_table, int32_t max_pages, float penalty,
+                                   int32_t *out_token) {
+  if (rt == nullptr) return Q35_ERR_INVALID;
+  Context *ctx = rt->ctx;
+  const q35_model_dims &d = rt->model->d;
+  if (tokens == nullptr || page_table == nullptr || count <= 0 || count > rt->cfg.max_batch || max_pages <= 0)
+    return set_error(ctx, Q35_ERR_INVALID, "invalid prefill chunk");
+  // validate on the host so no kernel ever sees an out-of-range index
+  if (slot < 0 || slot >= rt->cfg.max_slots || !rt->slot_used[slot])
+    return set_error(ctx, Q35_ERR_INVALID, "prefill needs an allocated slot");
+  if (pos0 < 0 || static_cast<long long>(pos0) + count > rt->cfg.max_context)
+    return set_error(ctx, Q35_ERR_INVALID, "prefill chunk outside max_context");
+  const int pos_last = pos0 + count - 1;
+  if (pos_last / rt->cfg.page_tokens >= max_pages)
+    return set_error(ctx, Q35_ERR_INVALID, "page table does not cover the chunk");
+  for (int p = 0; p <= pos_last / rt->cfg.page_tokens; ++p)
+    if (page_table[p] < 0 || page_table[p] >= rt->cfg.total_pages || rt->page_ref[page_table[p]] <= 0)
+      return set_error(ctx, Q35_ERR_INVALID, "page table names a free or invalid page");
+  for (int r = 0; r < count; ++r)
+    if (tokens[r] < 0 || tokens[r] >= d.vocab) return set_error(ctx, Q35_ERR_INVALID, "token out of range");
+  // one row per position of the chunk, all on the request's slot and pages
+  const MetaLayout ml = meta_layout(rt->cfg.max_batch, rt->max_pages_per_row);
+  unsigned char *h = rt->meta_host;
+  std::memset(h, 0, rt->meta_bytes);
+  auto *slots = reinterpret_cast<int32_t *>(h + ml.slots);
+  auto *positions = reinterpret_cast<int32_t *>(h + ml.positions);
+  auto *toks = reinterpret_cast<int32_t *>(h + ml.tokens);
+  auto *seq_lens = reinterpret_cast<int32_t *>(h + ml.seq_lens);
+  auto *penalties = reinterpret_cast<float *>(h + ml.penalties);
+  auto *pt = reinterpret_cast<int32_t *>(h + ml.page_table);
+  const int used = std::min(max_pages, rt->max_pages_per_row);
+  for (int r = 0; r < count; ++r) {
+    slots[r] = slot;
+    positions[r] = pos0 + r;
+    toks[r] = tokens[r];
+    seq_lens[r] = pos0 + r + 1;  // causal: the prefix and the chunk up to this position
+    penalties[r] = penalty;
+    for (int p = 0; p < used; ++p) pt[static_cast<size_t>(r) * rt->max_pages_per_row + p] = page_table[p];
+  }
+  // chunk sizes vary (the last chunk of a prompt is ragged): eager launches
+  int st = runtime_enqueue_step(rt, count, false, true);
+  if (st != Q35_OK) return st;
+  Q35_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  if (rt->profiling) {
+    st = profile_collect(rt);
+    if (st != Q35_OK) return st;
+  }
+  rt->last_batch = count;
+  if (out_token != nullptr) *out_token = rt->tokens_out_host[count - 1];
   return Q35_OK;
 }
 

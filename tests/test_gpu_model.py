@@ -79,3 +79,38 @@ def test_penalty_and_page_sizes(q, ctx, orc, small):
         results.append(got)
     # the page size only changes where KV rows live, never the arithmetic
     assert np.array_equal(results[0], results[1]) and np.array_equal(results[1], results[2])
+
+
+@pytest.mark.parametrize("chunks", [[24], [7, 1, 16], [3] * 8])
+def test_chunked_prefill_equals_single_steps(q, ctx, small, chunks):
+    """Chunked prefill (q35_runtime_prefill: prefill.inl:599-791 semantics)
+    leaves exactly the recurrent state, conv ring and KV pages that one
+    single-token step per position leaves: the greedy token after the prompt
+    agrees, and the logits of the decode steps that follow are bit-identical
+    (both requests decode in the same batch)."""
+    d, sched, tensors, model = small
+    plen, new, page_tokens = sum(chunks), 5, 16
+    prompt = np.random.default_rng(6).integers(0, d["vocab"], size=plen).astype(np.int32)
+    ctx_len = plen + new + 8
+    rt = q.Runtime(model, max_slots=2, max_batch=32, max_context=ctx_len, page_tokens=page_tokens, use_graphs=False)
+    sa, sb = rt.slot_alloc(prompt), rt.slot_alloc(prompt)
+    npages = (ctx_len + page_tokens - 1) // page_tokens
+    table = np.zeros((2, rt.max_pages), np.int32)
+    for r in range(2):
+        for p in range(npages):
+            table[r, p] = rt.page_alloc()
+    print(f"chunked prefill {chunks}", flush=True)
+    pos, tok_a = 0, None
+    for c in chunks:
+        tok_a = rt.prefill(sa, pos, prompt[pos:pos + c], table[0])
+        pos += c
+    for t in range(plen):
+        tok_b = int(rt.step([sb], [t], [prompt[t]], table[1:2])[0])
+    assert tok_a == tok_b
+    inp = np.array([tok_a, tok_b], np.int32)
+    for n in range(new):
+        out, lg = rt.step([sa, sb], [plen + n] * 2, inp, table, count_input=[1, 1], logits=True)
+        assert np.array_equal(lg[0].view(np.uint32), lg[1].view(np.uint32)), n
+        assert out[0] == out[1]
+        inp = out
+    rt.close()
