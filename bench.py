@@ -101,6 +101,87 @@ def cpu_baseline(model_dir, artifact, batch, prompt_len, new_tokens, threads):
                       f"same random-init 0.8B artifact"}
 
 
+def run_mixed4b(args, q, ctx):
+    """Config 5: the 4B-shaped model (hidden 2560, 32 layers 3:1, MLP 9216,
+    random-init Q4) with 64 decode requests at contexts ~U[128, 8192] and one
+    4096-token prompt. The reference cannot put both in one step either
+    (max_prefill_requests = 1, prefill and decode batches alternate), so the
+    mixed step is measured as one 64-row decode step (captured graph) plus the
+    chunked prefill of the 4096 tokens, and reported as their sum. Decode cost
+    does not depend on KV values, so the 64 rows' pages are allocated to their
+    context lengths without running their prompts."""
+    d, sched = q.model_dims(2)
+    path = os.path.join(tempfile.gettempdir(), f"q35_bench_4b_s{args.seed}")
+    os.makedirs(path, exist_ok=True)
+    art = os.path.join(path, "model.q35h128")
+    if not os.path.exists(art):
+        t = time.time()
+        log("writing the random-init 4B artifact (about a minute)")
+        q.write_random_artifact(art + ".part", d, sched, seed=args.seed, weight_std=0.02)
+        os.replace(art + ".part", art)
+        log(f"wrote {art} ({os.path.getsize(art) / 1e9:.2f} GB) in {time.time() - t:.1f}s")
+    t = time.time()
+    model = q.Model(ctx, d, sched, artifact=art)
+    log(f"4B model resident in HBM in {time.time() - t:.1f}s")
+    rows, prefill_len, page_tokens = 64, 4096, 16
+    rng = np.random.default_rng(20261205)
+    ctx_lens = rng.integers(128, 8193, size=rows)
+    steps = max(1, min(args.steps, 40))
+    max_ctx = 8192 + args.warmup + steps + 8
+    rt = q.Runtime(model, max_slots=rows + 1, max_batch=rows, max_context=max_ctx, page_tokens=page_tokens,
+                   use_graphs=True)
+    slots = np.array([rt.slot_alloc(np.array([1], np.int32)) for _ in range(rows)], np.int32)
+    table = np.zeros((rows, rt.max_pages), np.int32)
+    for r in range(rows):
+        # positions ctx - 1 .. ctx - 2 + warmup + steps are written
+        need = (int(ctx_lens[r]) + args.warmup + steps - 2) // page_tokens + 1
+        assert need <= rt.max_pages
+        for p in range(need):
+            table[r, p] = rt.page_alloc()
+    tokens = rng.integers(0, d.vocab, size=rows).astype(np.int32)
+    pos = ctx_lens.astype(np.int32) - 1
+    ones = np.ones(rows, np.uint8)
+    for _ in range(args.warmup):
+        tokens = rt.step(slots, pos, tokens, table, count_input=ones)
+        pos += 1
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tokens = rt.step(slots, pos, tokens, table, count_input=ones)
+        pos += 1
+    decode_ms = (time.perf_counter() - t0) * 1000 / steps
+    log(f"4B decode: {rows} rows, contexts {int(ctx_lens.min())}..{int(ctx_lens.max())} "
+        f"(sum {int(ctx_lens.sum())}): {decode_ms:.3f} ms/step")
+    prompt = rng.integers(0, d.vocab, size=prefill_len).astype(np.int32)
+    pslot = rt.slot_alloc(prompt)
+    ptable = np.zeros(rt.max_pages, np.int32)
+    for p in range(prefill_len // page_tokens + 1):
+        ptable[p] = rt.page_alloc()
+    chunk = rows
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    first = None
+    for c0 in range(0, prefill_len, chunk):
+        first = rt.prefill(pslot, c0, prompt[c0:c0 + chunk], ptable)
+    prefill_ms = (time.perf_counter() - t0) * 1000
+    log(f"4B chunked prefill: {prefill_len} tokens in {prefill_len // chunk} chunks: {prefill_ms:.1f} ms "
+        f"({prefill_len / prefill_ms * 1000:.0f} tok/s), first token {first}")
+    rt.close()
+    model.close()
+    total = decode_ms + prefill_ms
+    return {
+        "metric": "config 5 mixed step: 4B-shaped, 64 decode rows (ctx ~U[128,8192]) + one 4096-token chunked prefill",
+        "value": round((rows + prefill_len) / total * 1000, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": steps, "warmup": args.warmup, "ms_per_step": round(total, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "q4xi8->i32 (projections), f32 (DeltaNet, attention)",
+        "data": "synthetic: random-init 4B-shaped weights N(0,0.02) packed to Q4-G32-DOT4 H128, random tokens",
+        "config": {"workload": "config 5 (4B-shaped mixed decode + chunked prefill)", "decode_rows": rows,
+                   "decode_context_sum": int(ctx_lens.sum()), "prefill_tokens": prefill_len,
+                   "prefill_chunk": chunk, "decode_ms": round(decode_ms, 3), "prefill_ms": round(prefill_ms, 2)},
+        "roofline": None, "cpu_baseline": None,
+    }
+
+
 def roofline(name, stats, traffic, kernel=None):
     """Achieved HBM rate of one kernel class: algorithmic bytes per launch over
     the average launch duration (HIP events around each launch on the
@@ -136,6 +217,8 @@ def main():
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--calibration-copy-mb", type=int, default=0,
                     help="issue one device-to-device copy of this many MiB (a known-size kernel for HBM counters)")
+    ap.add_argument("--workload", choices=("decode0p8b", "mixed4b"), default="decode0p8b",
+                    help="decode0p8b: the headline metric (config 4); mixed4b: config 5")
     ap.add_argument("--graphs", choices=("on", "off"), default="on",
                     help="replay captured step graphs (off: eager launches, e.g. under rocprofv3)")
     args = ap.parse_args()
@@ -154,6 +237,11 @@ def main():
     ctx = q.Context(0)
     cu, arch = ctx.device_info()
     log(f"device {arch}, {cu} CUs")
+    if args.workload == "mixed4b":
+        line = run_mixed4b(args, q, ctx)
+        ctx.close()
+        print(json.dumps(line), flush=True)
+        return
     d, sched, model_dir, artifact = prepare_model_dir(q, args.seed, 0.02)
     if args.calibration_copy_mb > 0:
         n = args.calibration_copy_mb << 20

@@ -326,21 +326,27 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_chunk_kernel(DeltaArgs a)
   const int j = lane & 15;
   const bool writer = lane < 16;
 
-  for (int r = 0; r < count; ++r) {
-    // ---- inputs of the token at position pos0 + r
-    float xq_s[MS], xv_s[MS], b_s[MS], a_s[MS];
-    q35_f32x4 z_s[MS][2];
+  // raw inputs of one token; the next token's are issued as soon as the
+  // current ones are summed, so their latency hides behind this token's work
+  float xq_s[MS], xv_s[MS], b_s[MS], a_s[MS];
+  q35_f32x4 z_s[MS][2];
+  auto load_token = [&](int r) {
     a.proj.template load<MS>(r, chq, xq_s);
     a.proj.template load<MS>(r, chv, xv_s);
     a.proj.template load8<MS>(r, channels + vh * kDim + 8 * (lane & 15), z_s);
     a.proj.template load<MS>(r, channels + v_dim + vh, b_s);
     a.proj.template load<MS>(r, channels + v_dim + a.v_heads + vh, a_s);
+  };
+  load_token(0);
+  for (int r = 0; r < count; ++r) {
+    // ---- inputs of the token at position pos0 + r
     const float xq = a.proj.template reduce<MS>(xq_s);
     const float xv = a.proj.template reduce<MS>(xv_s);
     float z[8];
     a.proj.template reduce8<MS>(z_s, z);
     const float bval = a.proj.template reduce<MS>(b_s);
     const float aval = a.proj.template reduce<MS>(a_s);
+    load_token(min(r + 1, count - 1));
     // causal conv1d + SiLU (activation.cpp:164-222), then slide the history
     float yq = xq * wq[K - 1], yv = xv * wv[K - 1];
 #pragma unroll

@@ -564,7 +564,8 @@ hipError_t launch_split_reduce(const SplitRows &src, int tokens, float *out, int
   return hipGetLastError();
 }
 
-GemmPlan gemm_plan(int rows, int nb, bool exact, bool argmax, int cu_count, int force_ks, int force_split) {
+GemmPlan gemm_plan(int rows, int nb, bool exact, bool argmax, int cu_count, int force_ks, int force_split,
+                   int max_split) {
   GemmPlan p{};
   const int groups = (rows / 8 + 7) / 8;
   const int cus = cu_count > 0 ? cu_count : 256;
@@ -587,7 +588,7 @@ GemmPlan gemm_plan(int rows, int nb, bool exact, bool argmax, int cu_count, int 
     // measured faster with 8 throughout.)
     p.ks = force_ks > 0 ? force_ks : 8;
     const int chunks = (nb + p.ks - 1) / p.ks;
-    p.split = force_split > 0 ? std::min(force_split, chunks) : std::min(chunks, 32);
+    p.split = force_split > 0 ? std::min(force_split, chunks) : std::min({chunks, 32, std::max(1, max_split)});
     const int per_split = (chunks + p.split - 1) / p.split;
     p.waves = force_split > 0 ? std::min(kMaxWaves, per_split) : 1;
     p.grid = groups;
@@ -662,7 +663,8 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t stream) {
       return hipGetLastError();
     }
   }
-  const GemmPlan p = gemm_plan(a.rows, a.nb, exact, argmax, a.cu_count, a.force_ks, a.force_split);
+  const GemmPlan p = gemm_plan(a.rows, a.nb, exact, argmax, a.cu_count, a.force_ks, a.force_split,
+                               a.max_split > 0 ? a.max_split : 32);
   // a split plan writes [split][tokens][rows] partials; a single split writes `out`
   if ((p.split > 1 && a.partials == nullptr) || (p.split == 1 && a.out == nullptr && !argmax && a.block_dots == nullptr))
     return hipErrorInvalidValue;

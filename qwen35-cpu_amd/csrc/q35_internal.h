@@ -189,6 +189,7 @@ struct GemmArgs {
   const float *penalties = nullptr;
   int cu_count = 0;
   int force_ks = 0, force_split = 0;  // plan overrides (0 = automatic)
+  int max_split = 0;                  // bound on the K splits (0 = 32)
   // tall single-split matrix (the vocabulary head): the streaming kernel
   // with activations staged in LDS; implied by `cand`
   bool head = false;
@@ -200,7 +201,10 @@ struct GemmPlan {
   int ks, waves, split, grid;
   size_t smem;
 };
-GemmPlan gemm_plan(int rows, int nb, bool exact, bool argmax, int cu_count, int force_ks, int force_split);
+// max_split bounds the K splits (a consumer that sums at most that many
+// split partials); one wavefront then walks several chunks.
+GemmPlan gemm_plan(int rows, int nb, bool exact, bool argmax, int cu_count, int force_ks, int force_split,
+                   int max_split = 32);
 // Candidate rows per token that the greedy head launch for this shape writes
 // (and argmax_finalize must read).
 int gemm_argmax_cands(int rows, int nb, int tokens, int cu_count, int force_gpw = 0);

@@ -63,6 +63,7 @@ struct q35_runtime {
   // work buffers
   float *x[2] = {nullptr, nullptr};  // residual stream, ping-pong
   float *proj = nullptr, *core = nullptr, *q_rot = nullptr, *gates = nullptr;
+  float *rows_final = nullptr;  // prefill: summed in-projection rows [batch][proj_width]
   float *part_o = nullptr, *part_ml = nullptr, *logits = nullptr;
   float *hidden_out = nullptr;
   uint64_t *codes = nullptr;

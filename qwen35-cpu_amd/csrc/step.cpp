@@ -341,6 +341,8 @@ extern "C" int q35_runtime_create(q35_model *m, const q35_runtime_config *cfg, q
     proj_floats = std::max(proj_floats, gemm_partial_floats(d.hidden, d.intermediate / 32, B, ctx->cu_count));
   }
   alloc(proj_floats * 4, reinterpret_cast<void **>(&rt->proj));
+  // prefill: the in projection's split partials summed once, [batch][rows]
+  alloc(static_cast<size_t>(B) * rt->proj_width * 4, reinterpret_cast<void **>(&rt->rows_final));
   alloc(B * rt->core_width * 4, reinterpret_cast<void **>(&rt->core));
   alloc(B * static_cast<size_t>(d.n_heads) * d.head_dim * 4, reinterpret_cast<void **>(&rt->q_rot));
   alloc(B * static_cast<size_t>(d.n_heads) * d.head_dim * 4, reinterpret_cast<void **>(&rt->gates));
@@ -584,8 +586,11 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
   // GEMM outputs land in rt->proj as [split][batch][rows]; `pending` describes
   // the last one for its consumer.
   SplitRows pending;
-  auto gemm = [&](const q35_q4_0_block_x8 *w, int rows, int K) -> hipError_t {
-    const GemmPlan p = gemm_plan(rows, K / 32, false, false, ctx->cu_count, 0, 0);
+  // Consumers that sum at most kConsumerSplits partials (DeltaNet, the
+  // attention prep, the SiLU prep) get GEMMs split at most that many ways.
+  constexpr int kConsumerSplits = 8;
+  auto gemm = [&](const q35_q4_0_block_x8 *w, int rows, int K, int max_split = 32) -> hipError_t {
+    const GemmPlan p = gemm_plan(rows, K / 32, false, false, ctx->cu_count, 0, 0, max_split);
     GemmArgs g;
     g.w = w;
     g.rows = rows;
@@ -597,6 +602,7 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
     g.stride = rows;
     g.partials = rt->proj;
     g.cu_count = ctx->cu_count;
+    g.max_split = max_split;
     pending.p = rt->proj;
     pending.splits = p.split;
     pending.split_stride = static_cast<long long>(batch) * rows;
@@ -629,8 +635,8 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
   auto rms_bytes = [&](bool add) {
     return B * (H * 4.0 + (add ? pending.splits * H * 4.0 + H * 4.0 : 0.0) + H + H / 32.0 * 4.0) + H * 4.0;
   };
-  auto gemm_bytes = [&](int rows, int K) {
-    const GemmPlan p = gemm_plan(rows, K / 32, false, false, ctx->cu_count, 0, 0);
+  auto gemm_bytes = [&](int rows, int K, int max_split = 32) {
+    const GemmPlan p = gemm_plan(rows, K / 32, false, false, ctx->cu_count, 0, 0, max_split);
     return gemm_algorithmic_bytes(rows, K / 32, batch, true, false) + (p.split - 1) * B * rows * 4.0;
   };
 
@@ -639,7 +645,8 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
     const LayerDev &L = m->layers[l];
     Q35_KERNEL(Q35_KERNEL_PREP, rms_bytes(add_pending), rms_prep(L.input_norm, add_pending, true, nullptr),
                "input norm prep");
-    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(L.in_rows, H), gemm(L.in_proj, L.in_rows, H), "in projection");
+    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(L.in_rows, H, kConsumerSplits),
+               gemm(L.in_proj, L.in_rows, H, kConsumerSplits), "in projection");
     if (L.linear) {
       const int li = m->linear_index[l];
       DeltaArgs a;
@@ -655,6 +662,15 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
       a.vd = d.lin_v_dim;
       a.out = nullptr;
       a.proj = pending;
+      if (prefill && pending.splits > 1) {
+        // the chunk scan reads every token's inputs in order: sum the split
+        // partials once over the whole GPU, so each token is one load per channel
+        Q35_KERNEL(Q35_KERNEL_PREP, B * L.in_rows * (pending.splits + 1) * 4.0,
+                   launch_split_reduce(pending, batch, rt->rows_final, L.in_rows, nullptr, s), "prefill row sum");
+        a.proj.p = rt->rows_final;
+        a.proj.splits = 1;
+        a.proj.split_stride = 0;
+      }
       a.conv_base = rt->conv + static_cast<size_t>(li) * d.lin_kernel * ch;
       a.conv_slot_stride = rt->conv_slot_stride;
       a.positions = positions;
@@ -731,7 +747,8 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
     }
     Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(H, L.out_cols), gemm(L.out_proj, H, L.out_cols), "out projection");
     Q35_KERNEL(Q35_KERNEL_PREP, rms_bytes(true), rms_prep(L.post_norm, true, true, nullptr), "post norm prep");
-    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(2 * I, H), gemm(L.gate_up, 2 * I, H), "gate_up projection");
+    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(2 * I, H, kConsumerSplits), gemm(L.gate_up, 2 * I, H, kConsumerSplits),
+               "gate_up projection");
     PrepArgs sp;
     sp.source = kPrepSiluMul;
     sp.gate_up = pending;
