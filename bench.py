@@ -129,7 +129,7 @@ def run_mixed4b(args, q, ctx):
     steps = max(1, min(args.steps, 40))
     max_ctx = 8192 + args.warmup + steps + 8
     rt = q.Runtime(model, max_slots=rows + 1, max_batch=rows, max_context=max_ctx, page_tokens=page_tokens,
-                   use_graphs=True)
+                   use_graphs=args.graphs == "on")
     slots = np.array([rt.slot_alloc(np.array([1], np.int32)) for _ in range(rows)], np.int32)
     table = np.zeros((rows, rt.max_pages), np.int32)
     for r in range(rows):
@@ -307,8 +307,8 @@ def main():
     # the Q4 GEMV the metric names: the vocabulary head (248,320 x 1024 Q4,
     # 143 MB per launch, one launch per step); the per-layer projections are
     # reported beside it as one class
-    roof = roofline("head", prof["head"], traffic, "gemm_kernel<8, true, false> (greedy head Q4 GEMV + penalty + argmax)") if prof else None
-    gemm_roof = roofline("gemm", prof["gemm"], traffic, "gemm_kernel<*, false, false> (per-layer Q4 projections)") if prof else None
+    roof = roofline("head", prof["head"], traffic, "head_kernel<4, 3, NT, true, *> (greedy head: streaming Q4 GEMV + penalty + argmax, NT token tiles)") if prof else None
+    gemm_roof = roofline("gemm", prof["gemm"], traffic, "gemm_kernel<8, false, false> (per-layer Q4 projections, split-K)") if prof else None
     breakdown = ({k: {"us_per_step": round(v[0] / args.profile_steps * 1000.0, 1),
                       "launches_per_step": v[1] // args.profile_steps} for k, v in prof.items() if v[1]}
                  if prof else None)

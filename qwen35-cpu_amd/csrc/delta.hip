@@ -264,50 +264,48 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
   store_state();
 }
 
-// Chunked prefill scan (prefill.inl:599-791 runs the prompt in chunks; the
-// recurrence itself is delta_net.cpp:63-98 per token): one workgroup per value
-// head walks the `batch` rows of ONE request -- consecutive positions
-// positions[0] .. positions[0] + batch - 1 -- in order. The state tile stays
-// in registers for the whole chunk (one load, one store), and the conv
-// history slides in registers. Per token the arithmetic is delta_kernel<true>'s
-// in the same order, so a chunk leaves the state, ring and outputs that
-// token-by-token decoding of the same positions produces, bit for bit.
-template <int MS>
-__global__ __launch_bounds__(kDeltaThreads) void delta_chunk_kernel(DeltaArgs a) {
-  __shared__ float sq[kDim], sk[kDim], sv[kDim], so[kDim];
-  __shared__ float red[8];
-  __shared__ float s_alpha, s_beta;
+// Chunked prefill (prefill.inl:599-791 runs a prompt in chunks; the
+// recurrence itself is delta_net.cpp:63-98 per token). The `batch` rows are
+// consecutive positions positions[0] .. positions[0] + batch - 1 of ONE
+// request, and the in-projection rows arrive already summed (one split).
+// Only the state recurrence is sequential, so a chunk runs as three kernels:
+//   1. delta_chunk_inputs_kernel, one workgroup per (value head, token):
+//      causal conv + SiLU, L2 norms, beta and alpha of every token at once
+//      (the conv history of a token is the ring for positions before the
+//      chunk and the chunk's own rows after it);
+//   2. delta_scan_kernel, one wavefront per 16 value rows of a head: the rows
+//      are independent recurrences, so each wavefront walks the chunk's tokens
+//      with its rows' state in registers (one load, one store per chunk) and
+//      no workgroup barrier;
+//   3. delta_chunk_out_kernel, one wavefront per (value head, token): gated
+//      RMSNorm * SiLU(z) and the A16 preparation of the out projection's
+//      input, plus the ring update with the chunk's last K-1 inputs.
+// Each step is delta_kernel<true>'s arithmetic in the same order (the same
+// lanes own the same columns of a row), so a chunk leaves the state, ring and
+// outputs that token-by-token decoding of the same positions produces, bit
+// for bit. Scan entries are [token][value head][kDeltaScanStride] floats:
+// q (normalised, x 1/sqrt(d_k)) | k (normalised) | v | alpha | beta; the raw
+// head outputs follow at scan + batch * v_heads * kDeltaScanStride.
+__global__ __launch_bounds__(kDeltaThreads) void delta_chunk_inputs_kernel(DeltaArgs a) {
+  __shared__ float red[4];
   constexpr int K = kConvKernel;
-  const int vh = blockIdx.x;
+  const int vh = blockIdx.x, r = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int per = a.v_heads / a.k_heads;
   const int kh = vh / per;
-  const int quad = tid & 3, rowp = tid >> 2;
-  const int slot = a.slots[0];
-  const int pos0 = a.positions[0], count = a.batch;
-  // state copies: read the one for pos0, write the one for pos0 + count
-  const int rpar = a.state_copy_stride > 0 ? (pos0 & 1) : 0;
-  const int wpar = a.state_copy_stride > 0 ? ((pos0 + count) & 1) : 0;
-  float *state_slot = a.state_base + static_cast<long long>(slot) * a.state_slot_stride;
-  q35_f32x4 *S = reinterpret_cast<q35_f32x4 *>(state_slot + rpar * a.state_copy_stride +
-                                               static_cast<size_t>(vh) * kDim * kDim);
-  q35_f32x4 *W = reinterpret_cast<q35_f32x4 *>(state_slot + wpar * a.state_copy_stride +
-                                               static_cast<size_t>(vh) * kDim * kDim);
-  const int off0 = rowp * (kDim / 4) + quad, off1 = (rowp + 64) * (kDim / 4) + quad;
-  q35_f32x4 st0[8], st1[8];
-#pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    st0[m] = Q35_LOAD_NT(S + off0 + 4 * m);
-    st1[m] = Q35_LOAD_NT(S + off1 + 4 * m);
-  }
   const int q_dim = a.k_heads * kDim, v_dim = a.v_heads * kDim;
   const int channels = 2 * q_dim + v_dim;
-  float *conv = a.conv_base + static_cast<long long>(slot) * a.conv_slot_stride;
+  const int slot = a.slots[0], pos0 = a.positions[0], pos = pos0 + r;
+  const float *conv = a.conv_base + static_cast<long long>(slot) * a.conv_slot_stride;
   const int i = tid & (kDim - 1);
   const bool is_k = tid >= kDim, has_v = tid < kDim;
   const int chq = (is_k ? q_dim : 0) + kh * kDim + i;
   const int chv = has_v ? 2 * q_dim + vh * kDim + tid : chq;
-  float hq[K - 1], hv[K - 1], wq[K], wv[K], nw[8];
+  const float *row = a.proj.p + static_cast<long long>(r) * a.proj.width;
+  const float xq = row[chq], xv = row[chv];
+  const float bval = row[channels + v_dim + vh];
+  const float aval = row[channels + v_dim + a.v_heads + vh];
+  float hq[K - 1], hv[K - 1], wq[K], wv[K];
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     wq[k] = a.conv_w[static_cast<size_t>(k) * channels + chq];
@@ -315,156 +313,182 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_chunk_kernel(DeltaArgs a)
   }
 #pragma unroll
   for (int k = 0; k < K - 1; ++k) {
-    const int ring = (pos0 + 1 + k) & (K - 1);  // position pos0 - (K-1) + k
-    hq[k] = conv[static_cast<size_t>(ring) * channels + chq];
-    hv[k] = conv[static_cast<size_t>(ring) * channels + chv];
+    const int p = pos - (K - 1) + k;  // oldest first
+    if (p >= pos0) {
+      const float *hrow = a.proj.p + static_cast<long long>(p - pos0) * a.proj.width;
+      hq[k] = hrow[chq];
+      hv[k] = hrow[chv];
+    } else {
+      hq[k] = conv[static_cast<size_t>(p & (K - 1)) * channels + chq];
+      hv[k] = conv[static_cast<size_t>(p & (K - 1)) * channels + chv];
+    }
   }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) nw[e] = a.norm_w[8 * (lane & 15) + e];
   const float dtb = a.dt_bias[vh];
   const float sa_ = a.ssm_a[vh];
-  const int j = lane & 15;
-  const bool writer = lane < 16;
-
-  // raw inputs of one token; the next token's are issued as soon as the
-  // current ones are summed, so their latency hides behind this token's work
-  float xq_s[MS], xv_s[MS], b_s[MS], a_s[MS];
-  q35_f32x4 z_s[MS][2];
-  auto load_token = [&](int r) {
-    a.proj.template load<MS>(r, chq, xq_s);
-    a.proj.template load<MS>(r, chv, xv_s);
-    a.proj.template load8<MS>(r, channels + vh * kDim + 8 * (lane & 15), z_s);
-    a.proj.template load<MS>(r, channels + v_dim + vh, b_s);
-    a.proj.template load<MS>(r, channels + v_dim + a.v_heads + vh, a_s);
-  };
-  load_token(0);
-  for (int r = 0; r < count; ++r) {
-    // ---- inputs of the token at position pos0 + r
-    const float xq = a.proj.template reduce<MS>(xq_s);
-    const float xv = a.proj.template reduce<MS>(xv_s);
-    float z[8];
-    a.proj.template reduce8<MS>(z_s, z);
-    const float bval = a.proj.template reduce<MS>(b_s);
-    const float aval = a.proj.template reduce<MS>(a_s);
-    load_token(min(r + 1, count - 1));
-    // causal conv1d + SiLU (activation.cpp:164-222), then slide the history
-    float yq = xq * wq[K - 1], yv = xv * wv[K - 1];
-#pragma unroll
-    for (int k = 0; k < K - 1; ++k) {
-      yq += hq[k] * wq[k];
-      yv += hv[k] * wv[k];
-    }
-    yq = silu_times(yq, 1.0F);
-    yv = silu_times(yv, 1.0F);
-#pragma unroll
-    for (int k = 0; k < K - 2; ++k) {
-      hq[k] = hq[k + 1];
-      hv[k] = hv[k + 1];
-    }
-    hq[K - 2] = xq;
-    hv[K - 2] = xv;
-    if (tid == 0) {
-      s_beta = sigmoid_stable(bval);
-      const float pre = softplus_stable(aval + dtb);
-      s_alpha = expf(pre * sa_);
-    }
-    const float ss = wave_sum(yq * yq);
-    if (lane == 0) red[wave] = ss;
-    if (has_v) sv[tid] = yv;
-    lds_barrier();
-    const float tot = is_k ? red[2] + red[3] : red[0] + red[1];
-    const float scale = is_k ? 1.0F : 1.0F / sqrtf(static_cast<float>(kDim));
-    const float mul = scale / sqrtf(tot + 1.0e-6F);
-    if (is_k)
-      sk[i] = yq * mul;
-    else
-      sq[i] = yq * mul;
-    lds_barrier();
-
-    // ---- delta rule on this thread's two rows
-    const float alpha = s_alpha, beta = s_beta;
-    q35_f32x4 kc[8];
-#pragma unroll
-    for (int m = 0; m < 8; ++m) kc[m] = *reinterpret_cast<const q35_f32x4 *>(sk + 16 * m + 4 * quad);
-    float d0 = 0.0F, d1 = 0.0F;
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      st0[m] *= alpha;
-      st1[m] *= alpha;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        d0 += st0[m][e] * kc[m][e];
-        d1 += st1[m][e] * kc[m][e];
-      }
-    }
-    d0 += q35_quad_xor1(d0);
-    d1 += q35_quad_xor1(d1);
-    d0 += q35_quad_xor2(d0);
-    d1 += q35_quad_xor2(d1);
-    const float delta0 = (sv[rowp] - d0) * beta, delta1 = (sv[rowp + 64] - d1) * beta;
-    float o0 = 0.0F, o1 = 0.0F;
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      const q35_f32x4 qc = *reinterpret_cast<const q35_f32x4 *>(sq + 16 * m + 4 * quad);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        st0[m][e] += delta0 * kc[m][e];
-        st1[m][e] += delta1 * kc[m][e];
-        o0 += st0[m][e] * qc[e];
-        o1 += st1[m][e] * qc[e];
-      }
-    }
-    o0 += q35_quad_xor1(o0);
-    o1 += q35_quad_xor1(o1);
-    o0 += q35_quad_xor2(o0);
-    o1 += q35_quad_xor2(o1);
-    if (quad == 0) {
-      so[rowp] = o0;
-      so[rowp + 64] = o1;
-    }
-    lds_barrier();
-
-    // ---- outputs of the token (wave 0): gated RMSNorm * SiLU(z), A16 row r
-    if (wave == 0) {
-      float y[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) y[e] = so[8 * j + e];
-      float yss = 0.0F;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) yss += y[e] * y[e];
-      yss += q35_row_xor(yss, 1);
-      yss += q35_row_xor(yss, 2);
-      yss += q35_row_xor(yss, 4);
-      yss += q35_row_xor(yss, 8);
-      const float inv = 1.0F / sqrtf(yss / static_cast<float>(kDim) + a.eps);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) y[e] = silu_times(z[e], y[e] * inv * (nw[e] + 0.0F));
-      if (a.out != nullptr && writer)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) a.out[static_cast<size_t>(r) * v_dim + vh * kDim + 8 * j + e] = y[e];
-      if (a.codes != nullptr) {
-        QuantOut qo;
-        qo.codes = a.codes;
-        qo.scales = a.scales;
-        h128_quantize_row16(y, r, vh, v_dim / 32, true, a.seed, qo, writer);
-      }
-    }
-    // the next token rewrites sq, sk, sv, so, red and the gates
-    lds_barrier();
-  }
-
-  // ---- the chunk's state and the ring's last K-1 inputs go back once
-#pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    Q35_STORE_NT(st0[m], W + off0 + 4 * m);
-    Q35_STORE_NT(st1[m], W + off1 + 4 * m);
-  }
-  const int pos_last = pos0 + count - 1;
+  float yq = xq * wq[K - 1], yv = xv * wv[K - 1];
 #pragma unroll
   for (int k = 0; k < K - 1; ++k) {
-    const int ring = (pos_last - (K - 2) + k) & (K - 1);  // position pos_last - (K-2) + k
-    conv[static_cast<size_t>(ring) * channels + chq] = hq[k];
-    if (has_v) conv[static_cast<size_t>(ring) * channels + chv] = hv[k];
+    yq += hq[k] * wq[k];
+    yv += hv[k] * wv[k];
+  }
+  yq = silu_times(yq, 1.0F);
+  yv = silu_times(yv, 1.0F);
+  float *e = a.scan + (static_cast<size_t>(r) * a.v_heads + vh) * kDeltaScanStride;
+  if (tid == 0) {
+    e[3 * kDim + 1] = sigmoid_stable(bval);
+    const float pre = softplus_stable(aval + dtb);
+    e[3 * kDim] = expf(pre * sa_);
+  }
+  const float ss = wave_sum(yq * yq);
+  if (lane == 0) red[wave] = ss;
+  if (has_v) e[2 * kDim + tid] = yv;
+  lds_barrier();
+  const float tot = is_k ? red[2] + red[3] : red[0] + red[1];
+  const float scale = is_k ? 1.0F : 1.0F / sqrtf(static_cast<float>(kDim));
+  const float mul = scale / sqrtf(tot + 1.0e-6F);
+  e[(is_k ? kDim : 0) + i] = yq * mul;
+}
+
+// One wavefront per 16 value rows (grid: row blocks x value heads); lane
+// quad q = lane % 4 of row 16 * blockIdx.x + lane / 4 owns the float4 at
+// columns 16m + 4q (m = 0..7), as in delta_kernel. A token's q and k go
+// through LDS (one float4 per lane); the next kDeltaScanAhead tokens' loads
+// are in flight while a token is computed.
+constexpr int kDeltaScanAhead = 4;
+constexpr int kDeltaScanRows = 16;
+
+struct ScanToken {
+  q35_f32x4 qk;  // floats 4 * lane .. +3 of [q | k]
+  float v, alpha, beta;
+};
+
+__global__ __launch_bounds__(64) void delta_scan_kernel(DeltaArgs a) {
+  __shared__ q35_f32x4 qk_lds[2][2 * kDim / 4];
+  const int lane = threadIdx.x, vh = blockIdx.y;
+  const int quad = lane & 3, row = kDeltaScanRows * blockIdx.x + (lane >> 2);
+  const int slot = a.slots[0], pos0 = a.positions[0], count = a.batch;
+  const int rpar = a.state_copy_stride > 0 ? (pos0 & 1) : 0;
+  const int wpar = a.state_copy_stride > 0 ? ((pos0 + count) & 1) : 0;
+  float *state_slot = a.state_base + static_cast<long long>(slot) * a.state_slot_stride;
+  const size_t off = static_cast<size_t>(vh) * kDim * kDim + static_cast<size_t>(row) * kDim + 4 * quad;
+  const q35_f32x4 *S = reinterpret_cast<const q35_f32x4 *>(state_slot + rpar * a.state_copy_stride + off);
+  q35_f32x4 *W = reinterpret_cast<q35_f32x4 *>(state_slot + wpar * a.state_copy_stride + off);
+  q35_f32x4 st[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) st[m] = Q35_LOAD_NT(S + 4 * m);
+  const float *scan = a.scan + static_cast<size_t>(vh) * kDeltaScanStride;
+  const size_t tstride = static_cast<size_t>(a.v_heads) * kDeltaScanStride;
+  float *outs = a.scan + static_cast<size_t>(count) * tstride + static_cast<size_t>(vh) * kDim + row;
+  auto load = [&](ScanToken &t, int r) {
+    const float *e = scan + static_cast<size_t>(r) * tstride;
+    t.qk = reinterpret_cast<const q35_f32x4 *>(e)[lane];
+    t.v = e[2 * kDim + row];
+    t.alpha = e[3 * kDim];
+    t.beta = e[3 * kDim + 1];
+  };
+  ScanToken buf[kDeltaScanAhead];
+#pragma unroll
+  for (int d = 0; d < kDeltaScanAhead; ++d) load(buf[d], min(d, count - 1));
+  for (int r0 = 0; r0 < count; r0 += kDeltaScanAhead) {
+#pragma unroll
+    for (int d = 0; d < kDeltaScanAhead; ++d) {
+      const int r = r0 + d;
+      if (r >= count) break;
+      q35_f32x4 *lds = qk_lds[d & 1];
+      lds[lane] = buf[d].qk;
+      const float v = buf[d].v, alpha = buf[d].alpha, beta = buf[d].beta;
+      load(buf[d], min(r + kDeltaScanAhead, count - 1));
+      lds_barrier();
+      q35_f32x4 kc[8];
+#pragma unroll
+      for (int m = 0; m < 8; ++m) kc[m] = lds[kDim / 4 + 4 * m + quad];
+      float dot = 0.0F;
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        st[m] *= alpha;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dot += st[m][e] * kc[m][e];
+      }
+      dot += q35_quad_xor1(dot);
+      dot += q35_quad_xor2(dot);
+      const float delta = (v - dot) * beta;
+      float o = 0.0F;
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const q35_f32x4 qc = lds[4 * m + quad];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          st[m][e] += delta * kc[m][e];
+          o += st[m][e] * qc[e];
+        }
+      }
+      o += q35_quad_xor1(o);
+      o += q35_quad_xor2(o);
+      if (quad == 0) outs[static_cast<size_t>(r) * a.v_heads * kDim] = o;
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < 8; ++m) Q35_STORE_NT(st[m], W + 4 * m);
+}
+
+// Lane j = lane % 16 holds columns 8j .. 8j+7 of the head's outputs (the four
+// 16-lane rows compute the same values; row 0 stores), as delta_kernel's
+// epilogue.
+__global__ __launch_bounds__(64) void delta_chunk_out_kernel(DeltaArgs a) {
+  constexpr int K = kConvKernel;
+  const int vh = blockIdx.x, r = blockIdx.y, lane = threadIdx.x;
+  const int q_dim = a.k_heads * kDim, v_dim = a.v_heads * kDim;
+  const int channels = 2 * q_dim + v_dim;
+  const int j = lane & 15;
+  const bool writer = lane < 16;
+  const float *prow = a.proj.p + static_cast<long long>(r) * a.proj.width;
+  const q35_f32x4 *zp = reinterpret_cast<const q35_f32x4 *>(prow + channels + vh * kDim + 8 * j);
+  const q35_f32x4 *op = reinterpret_cast<const q35_f32x4 *>(
+      a.scan + static_cast<size_t>(a.batch) * a.v_heads * kDeltaScanStride + (static_cast<size_t>(r) * a.v_heads + vh) * kDim + 8 * j);
+  const q35_f32x4 *wp = reinterpret_cast<const q35_f32x4 *>(a.norm_w + 8 * j);
+  const q35_f32x4 z0 = zp[0], z1 = zp[1], o0 = op[0], o1 = op[1], w0 = wp[0], w1 = wp[1];
+  float y[8], z[8], nw[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    y[e] = o0[e];
+    y[4 + e] = o1[e];
+    z[e] = z0[e];
+    z[4 + e] = z1[e];
+    nw[e] = w0[e];
+    nw[4 + e] = w1[e];
+  }
+  float yss = 0.0F;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) yss += y[e] * y[e];
+  yss += q35_row_xor(yss, 1);
+  yss += q35_row_xor(yss, 2);
+  yss += q35_row_xor(yss, 4);
+  yss += q35_row_xor(yss, 8);
+  const float inv = 1.0F / sqrtf(yss / static_cast<float>(kDim) + a.eps);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = silu_times(z[e], y[e] * inv * (nw[e] + 0.0F));
+  if (a.out != nullptr && writer)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a.out[static_cast<size_t>(r) * v_dim + vh * kDim + 8 * j + e] = y[e];
+  if (a.codes != nullptr) {
+    QuantOut qo;
+    qo.codes = a.codes;
+    qo.scales = a.scales;
+    h128_quantize_row16(y, r, vh, v_dim / 32, true, a.seed, qo, writer);
+  }
+  // the chunk's last K-1 raw inputs into the ring (slot = position % K); the
+  // inputs kernel read the ring before this launch
+  if (r >= a.batch - (K - 1)) {
+    const int per = a.v_heads / a.k_heads, kh = vh / per;
+    float *ring = a.conv_base + static_cast<long long>(a.slots[0]) * a.conv_slot_stride +
+                  static_cast<size_t>((a.positions[0] + r) & (K - 1)) * channels;
+    for (int c = lane; c < kDim; c += 64) {
+      if (vh % per == 0) {
+        ring[kh * kDim + c] = prow[kh * kDim + c];
+        ring[q_dim + kh * kDim + c] = prow[q_dim + kh * kDim + c];
+      }
+      ring[2 * q_dim + vh * kDim + c] = prow[2 * q_dim + vh * kDim + c];
+    }
   }
 }
 
@@ -491,15 +515,12 @@ hipError_t launch_delta(const DeltaArgs &a, hipStream_t stream) {
 hipError_t launch_delta_chunk(const DeltaArgs &a, hipStream_t stream) {
   if (a.batch <= 0) return hipSuccess;
   if (!a.fused || a.kd != kDim || a.vd != kDim || a.v_heads % a.k_heads != 0 || a.kernel != kConvKernel ||
-      a.state_base == nullptr || a.slots == nullptr || a.positions == nullptr)
+      a.state_base == nullptr || a.slots == nullptr || a.positions == nullptr || a.scan == nullptr ||
+      a.proj.splits != 1)
     return hipErrorInvalidValue;
-  const dim3 grid(a.v_heads), block(kDeltaThreads);
-  switch (split_bound(a.proj.splits)) {
-    case 1: Q35_LAUNCH((delta_chunk_kernel<1>), grid, block, 0, stream, a); break;
-    case 4: Q35_LAUNCH((delta_chunk_kernel<4>), grid, block, 0, stream, a); break;
-    case 8: Q35_LAUNCH((delta_chunk_kernel<8>), grid, block, 0, stream, a); break;
-    default: return hipErrorInvalidValue;
-  }
+  Q35_LAUNCH((delta_chunk_inputs_kernel), dim3(a.v_heads, a.batch), dim3(kDeltaThreads), 0, stream, a);
+  Q35_LAUNCH((delta_scan_kernel), dim3(kDim / kDeltaScanRows, a.v_heads), dim3(64), 0, stream, a);
+  Q35_LAUNCH((delta_chunk_out_kernel), dim3(a.v_heads, a.batch), dim3(64), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -87,7 +87,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
   const uint8_t *wbase = reinterpret_cast<const uint8_t *>(a.w);
   const bool vec_out = (a.stride & 3) == 0;
 
-  for (int tt = 0; tt < token_tiles; ++tt) {
+  // token tiles: one per grid.z slice (the argmax path walks them all)
+  for (int tt = blockIdx.z; tt < token_tiles; tt += gridDim.z) {
     const uint64_t *acodes = a.codes + static_cast<size_t>(tt) * nb * 64 + lane;
     const float *ascale = a.scales + static_cast<size_t>(tt) * nb * 16 + 4 * G;
     unsigned long long run_best[4] = {0ull, 0ull, 0ull, 0ull};  // single-wave argmax
@@ -668,7 +669,7 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t stream) {
   // a split plan writes [split][tokens][rows] partials; a single split writes `out`
   if ((p.split > 1 && a.partials == nullptr) || (p.split == 1 && a.out == nullptr && !argmax && a.block_dots == nullptr))
     return hipErrorInvalidValue;
-  const dim3 grid(p.grid, p.split), block(64 * p.waves);
+  const dim3 grid(p.grid, p.split, argmax ? 1 : (a.tokens + 15) / 16), block(64 * p.waves);
   if (argmax) {
     Q35_LAUNCH((gemm_kernel<8, true, false>), grid, block, p.smem, stream, a);
   } else if (a.block_dots != nullptr) {

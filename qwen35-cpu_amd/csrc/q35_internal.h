@@ -250,10 +250,18 @@ struct DeltaArgs {
   uint64_t *codes = nullptr;
   float *scales = nullptr;
   uint64_t seed = 0;
+  // chunked prefill: per-token scan entries, then the raw head outputs
+  // (delta_chunk_scan_floats(batch, v_heads) floats)
+  float *scan = nullptr;
 };
 hipError_t launch_delta(const DeltaArgs &a, hipStream_t stream);
 // Chunked prefill: the `batch` rows are consecutive positions of ONE request
-// (slots[0], positions[0] + r), scanned in order by one workgroup per head.
+// (slots[0], positions[0] + r) with the in-projection rows summed (one split);
+// the state recurrence is scanned in order, everything else runs per token.
+constexpr int kDeltaScanStride = 3 * 128 + 4;  // q | k | v | alpha | beta | pad
+inline size_t delta_chunk_scan_floats(int batch, int v_heads) {
+  return static_cast<size_t>(batch) * v_heads * (kDeltaScanStride + 128);
+}
 hipError_t launch_delta_chunk(const DeltaArgs &a, hipStream_t stream);
 
 // Full attention

@@ -64,6 +64,7 @@ struct q35_runtime {
   float *x[2] = {nullptr, nullptr};  // residual stream, ping-pong
   float *proj = nullptr, *core = nullptr, *q_rot = nullptr, *gates = nullptr;
   float *rows_final = nullptr;  // prefill: summed in-projection rows [batch][proj_width]
+  float *delta_scan = nullptr;  // prefill: DeltaNet chunk scan entries and raw outputs
   float *part_o = nullptr, *part_ml = nullptr, *logits = nullptr;
   float *hidden_out = nullptr;
   uint64_t *codes = nullptr;

@@ -343,6 +343,8 @@ extern "C" int q35_runtime_create(q35_model *m, const q35_runtime_config *cfg, q
   alloc(proj_floats * 4, reinterpret_cast<void **>(&rt->proj));
   // prefill: the in projection's split partials summed once, [batch][rows]
   alloc(static_cast<size_t>(B) * rt->proj_width * 4, reinterpret_cast<void **>(&rt->rows_final));
+  if (d.lin_v_heads > 0)
+    alloc(delta_chunk_scan_floats(B, d.lin_v_heads) * 4, reinterpret_cast<void **>(&rt->delta_scan));
   alloc(B * rt->core_width * 4, reinterpret_cast<void **>(&rt->core));
   alloc(B * static_cast<size_t>(d.n_heads) * d.head_dim * 4, reinterpret_cast<void **>(&rt->q_rot));
   alloc(B * static_cast<size_t>(d.n_heads) * d.head_dim * 4, reinterpret_cast<void **>(&rt->gates));
@@ -668,6 +670,7 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
         Q35_KERNEL(Q35_KERNEL_PREP, B * L.in_rows * (pending.splits + 1) * 4.0,
                    launch_split_reduce(pending, batch, rt->rows_final, L.in_rows, nullptr, s), "prefill row sum");
         a.proj.p = rt->rows_final;
+        a.proj.width = L.in_rows;
         a.proj.splits = 1;
         a.proj.split_stride = 0;
       }
@@ -683,6 +686,7 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
       a.codes = rt->codes;
       a.scales = rt->scales;
       a.seed = d.sign_seed;
+      a.scan = rt->delta_scan;
       // recurrent state read + written, projection row in (per split), conv
       // ring (K-1 rows read, one written), prepared out-projection activations
       const double delta_bytes =
@@ -763,8 +767,32 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
     Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(H, I), gemm(L.down, H, I), "down projection");
     add_pending = true;
   }
-  Q35_KERNEL(Q35_KERNEL_PREP, rms_bytes(true) + B * H * 4.0, rms_prep(m->final_norm, true, false, rt->hidden_out),
-             "final norm prep");
+  // A prefill chunk needs the head only for its last position: the final
+  // norm and the head run on that one row (row 0 of hidden_out afterwards).
+  const int head_tokens = prefill ? 1 : batch;
+  const int head_row0 = prefill ? batch - 1 : 0;
+  if (prefill) {
+    RmsPrepArgs a;
+    a.x_in = rt->x[cur] + static_cast<size_t>(head_row0) * H;
+    a.add = pending;
+    a.add.p = pending.p + static_cast<size_t>(head_row0) * pending.width;
+    a.x_out = rt->x[cur ^ 1] + static_cast<size_t>(head_row0) * H;
+    a.weight = m->final_norm;
+    a.eps = d.rms_eps;
+    a.tokens = 1;
+    a.K = H;
+    a.h128 = false;
+    a.seed = d.sign_seed;
+    a.codes = rt->codes;
+    a.scales = rt->scales;
+    a.normed_out = rt->hidden_out;
+    Q35_KERNEL(Q35_KERNEL_PREP, pending.splits * H * 4.0 + 3.0 * H * 4.0, launch_rms_prep(a, s), "final norm prep");
+    cur ^= 1;
+  } else {
+    Q35_KERNEL(Q35_KERNEL_PREP, rms_bytes(true) + B * H * 4.0, rms_prep(m->final_norm, true, false, rt->hidden_out),
+               "final norm prep");
+  }
+  const double HB = head_tokens;
   if (want_logits) {
     GemmArgs g;
     g.w = m->embed;
@@ -772,13 +800,13 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
     g.nb = H / 32;
     g.codes = rt->codes;
     g.scales = rt->scales;
-    g.tokens = batch;
+    g.tokens = head_tokens;
     g.out = rt->logits;
     g.stride = d.vocab;
     g.head = true;
     g.force_split = 1;  // rt->logits holds one [batch][vocab] copy: never split K here
     g.cu_count = ctx->cu_count;
-    Q35_KERNEL(Q35_KERNEL_HEAD, gemm_algorithmic_bytes(d.vocab, H / 32, batch, true, false), launch_gemm(g, s),
+    Q35_KERNEL(Q35_KERNEL_HEAD, gemm_algorithmic_bytes(d.vocab, H / 32, head_tokens, true, false), launch_gemm(g, s),
                "logits head");
   } else {
     GemmArgs g;
@@ -787,19 +815,19 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
     g.nb = H / 32;
     g.codes = rt->codes;
     g.scales = rt->scales;
-    g.tokens = batch;
+    g.tokens = head_tokens;
     g.cand = rt->cand;
     g.cand_stride = kMaxTokens;
     g.counts = rt->counts;
-    g.count_rows = slots;
+    g.count_rows = slots + head_row0;
     g.counts_stride = d.vocab;
-    g.penalties = penalties;
+    g.penalties = penalties + head_row0;
     g.cu_count = ctx->cu_count;
-    const int ncand = gemm_argmax_cands(d.vocab, H / 32, batch, ctx->cu_count);
-    Q35_KERNEL(Q35_KERNEL_HEAD, gemm_algorithmic_bytes(d.vocab, H / 32, batch, false, false) + ncand * B * 8.0,
+    const int ncand = gemm_argmax_cands(d.vocab, H / 32, head_tokens, ctx->cu_count);
+    Q35_KERNEL(Q35_KERNEL_HEAD, gemm_algorithmic_bytes(d.vocab, H / 32, head_tokens, false, false) + ncand * HB * 8.0,
                launch_gemm(g, s), "greedy head");
-    Q35_KERNEL(Q35_KERNEL_ARGMAX, ncand * B * 8.0 + B * 4.0,
-               launch_argmax_finalize(rt->cand, ncand, kMaxTokens, batch, rt->tokens_out_dev, nullptr, s),
+    Q35_KERNEL(Q35_KERNEL_ARGMAX, ncand * HB * 8.0 + HB * 4.0,
+               launch_argmax_finalize(rt->cand, ncand, kMaxTokens, head_tokens, rt->tokens_out_dev, nullptr, s),
                "argmax finalize");
   }
 #undef Q35_KERNEL
@@ -993,8 +1021,8 @@ extern "C" int q35_runtime_prefill(q35_runtime *rt, int32_t slot, int32_t pos0, 
     st = profile_collect(rt);
     if (st != Q35_OK) return st;
   }
-  rt->last_batch = count;
-  if (out_token != nullptr) *out_token = rt->tokens_out_host[count - 1];
+  rt->last_batch = 1;  // the head ran on the chunk's last position only
+  if (out_token != nullptr) *out_token = rt->tokens_out_host[0];
   return Q35_OK;
 }
 
