@@ -5,7 +5,9 @@
 // so the 32-bit word 8t+r of a tile body holds row r's columns 8t..8t+3 (low
 // nibbles) and 8t+4..8t+7 (high nibbles).
 //
-// Work decomposition. The rows form 64-row groups (eight 8-row tiles). A
+// Work decomposition (gemm_kernel; the single-token-tile split path of the
+// decode step runs gemm_rows_kernel below, the same scheme with 16- or
+// 32-row groups). The rows form 64-row groups (eight 8-row tiles). A
 // workgroup owns one group and one of S contiguous K ranges (split-K across
 // workgroups, grid.y); its W wavefronts split that range, and every wavefront
 // issues the loads of all blocks of a chunk (KS blocks: weights, row scales,
@@ -275,6 +277,104 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
         const int tok = tt * 16 + threadIdx.x;
         if (tok < a.tokens) a.cand[static_cast<size_t>(blockIdx.x) * a.cand_stride + tok] = best[threadIdx.x];
       }
+    }
+  }
+}
+
+// Split-K projection kernel with 16·RM-row groups (RM = 1 or 2 MFMAs per
+// block): one wavefront per (row group, K split, token tile). Fewer rows per
+// wavefront shorten each wavefront's serial epilogue (the fp32 chain is 3
+// VALU ops per output and block) at the same split partials.
+// Lane l = (G = l/16, c = l%16) covers rows r0 .. r0+RM-1 of tile c/(8/RM),
+// r0 = RM·(c % (8/RM)): per block it loads the body words 8G + r0 .. +RM-1
+// (k-group G) and those rows' FP16 scales; word i is the B operand of MFMA #i
+// for column c, i.e. output row RM·c + i of the group. The int32 block dot
+// and the fp32 chain per block are gemm_kernel's.
+template <int RM>
+struct RowWords;
+template <>
+struct RowWords<1> {
+  typedef uint32_t Q;
+  typedef uint16_t D;
+  static __device__ __forceinline__ uint32_t word(const Q &q, int) { return q; }
+  static __device__ __forceinline__ uint16_t scale(const D &d, int) { return d; }
+};
+template <>
+struct RowWords<2> {
+  typedef q35_u32x2 Q;
+  typedef uint32_t D;
+  static __device__ __forceinline__ uint32_t word(const Q &q, int i) { return q[i]; }
+  static __device__ __forceinline__ uint16_t scale(const D &d, int i) { return static_cast<uint16_t>(d >> (16 * i)); }
+};
+template <int KS, int RM>
+__global__ __launch_bounds__(64) void gemm_rows_kernel(GemmArgs a) {
+  typedef RowWords<RM> RW;
+  constexpr int kLanesPerTile = 8 / RM, kGroupRows = 16 * RM;
+  const int lane = threadIdx.x;
+  const int G = lane >> 4, c = lane & 15;
+  const int nb = a.nb, ntiles = a.rows >> 3;
+  const int S = gridDim.y, split = blockIdx.y, g = blockIdx.x, tt = blockIdx.z;
+  const int b0 = (split * nb) / S, b1 = ((split + 1) * nb) / S;
+  const int bl = b1 - 1;
+  const uint64_t *acodes = a.codes + static_cast<size_t>(tt) * nb * 64 + lane;
+  const float *ascale = a.scales + static_cast<size_t>(tt) * nb * 16 + 4 * G;
+  // rows past the matrix read a valid tile (the last); they are never stored
+  const int rt = min(g * (kGroupRows / 8) + c / kLanesPerTile, ntiles - 1);
+  const int r0 = RM * (c % kLanesPerTile);
+  const uint8_t *tile = reinterpret_cast<const uint8_t *>(a.w) + static_cast<size_t>(rt) * nb * 144;
+  const uint8_t *qrow = tile + 16 + 32 * G + 4 * r0;
+  const uint8_t *drow = tile + 2 * r0;
+  float acc[RM][4];
+#pragma unroll
+  for (int i = 0; i < RM; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0F;
+  for (int cb = b0; cb < b1; cb += KS) {
+    typename RW::Q q[KS];
+    typename RW::D d[KS];
+    long act[KS];
+    q35_f32x4 sa[KS];
+#pragma unroll
+    for (int i = 0; i < KS; ++i) {
+      const size_t b = static_cast<size_t>(min(cb + i, bl));
+      q[i] = *reinterpret_cast<const typename RW::Q *>(qrow + b * 144);
+      d[i] = *reinterpret_cast<const typename RW::D *>(drow + b * 144);
+      act[i] = static_cast<long>(acodes[b * 64]);
+      sa[i] = *reinterpret_cast<const q35_f32x4 *>(ascale + b * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < KS; ++i) {
+      // a slot past the range re-reads its last block; a zero row scale makes
+      // its contribution exactly +0 (acc is never -0)
+      const bool valid = cb + i < b1;
+      const v4i zero = {0, 0, 0, 0};
+      const v4i corr = Q35_MFMA_I32_16X16X32_I8(act[i], kMinus8, zero, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < RM; ++r) {
+        const v4i D = Q35_MFMA_I32_16X16X32_I8(act[i], unpack_word(RW::word(q[i], r)), corr, 0, 0, 0);
+        const float dw = valid ? half_bits_to_float(RW::scale(d[i], r)) : 0.0F;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[r][j] = fmaf(static_cast<float>(D[j]), dw * sa[i][j], acc[r][j]);
+      }
+    }
+  }
+  // rows RM·c .. RM·c + RM-1 of tokens 4G..4G+3
+  const int row = g * kGroupRows + RM * c;
+  if (row >= a.rows) return;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int tok = tt * 16 + 4 * G + j;
+    if (tok >= a.tokens) continue;
+    if (S > 1) {
+      float *dst = a.partials + (static_cast<size_t>(split) * a.tokens + tok) * a.rows + row;
+      if constexpr (RM == 1)
+        *dst = acc[0][j];
+      else
+        *reinterpret_cast<q35_f32x2 *>(dst) = q35_f32x2{acc[0][j], acc[1][j]};
+    } else {
+      const size_t o = static_cast<size_t>(tok) * a.stride + row;
+#pragma unroll
+      for (int r = 0; r < RM; ++r) a.out[o + r] = a.residual != nullptr ? a.residual[o + r] + acc[r][j] : acc[r][j];
     }
   }
 }
@@ -670,6 +770,24 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t stream) {
   if ((p.split > 1 && a.partials == nullptr) || (p.split == 1 && a.out == nullptr && !argmax && a.block_dots == nullptr))
     return hipErrorInvalidValue;
   const dim3 grid(p.grid, p.split, argmax ? 1 : (a.tokens + 15) / 16), block(64 * p.waves);
+  if (!argmax && a.block_dots == nullptr && !exact && p.waves == 1 && (a.tokens <= 16 || a.group_rows > 0)) {
+    // one token tile: row groups of 16·RM rows per wavefront -- 32 rows, or
+    // 16 where 32-row groups would leave fewer than two wavefronts per CU
+    // (narrow outputs). Several token tiles (4B-sized chunks at B = 64)
+    // measured faster with gemm_kernel's 64-row groups.
+    const int cus = a.cu_count > 0 ? a.cu_count : 256;
+    const int waves32 = ((a.rows >> 3) + 3) / 4 * p.split * ((a.tokens + 15) / 16);
+    const int rm = a.group_rows == 32 ? 2 : a.group_rows == 16 ? 1 : (waves32 < 2 * cus ? 1 : 2);
+    const dim3 grid_r(((a.rows >> 3) + 2 * rm - 1) / (2 * rm), p.split, (a.tokens + 15) / 16);
+#define Q35_ROWS(KS, RM) Q35_LAUNCH((gemm_rows_kernel<KS, RM>), grid_r, dim3(64), 0, stream, a)
+    if (p.ks == 4) {
+      if (rm == 1) Q35_ROWS(4, 1); else Q35_ROWS(4, 2);
+    } else {
+      if (rm == 1) Q35_ROWS(8, 1); else Q35_ROWS(8, 2);
+    }
+#undef Q35_ROWS
+    return hipGetLastError();
+  }
   if (argmax) {
     Q35_LAUNCH((gemm_kernel<8, true, false>), grid, block, p.smem, stream, a);
   } else if (a.block_dots != nullptr) {

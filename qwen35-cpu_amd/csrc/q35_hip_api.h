@@ -21,6 +21,7 @@
 typedef unsigned int q35_u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int q35_u32x2 __attribute__((ext_vector_type(2)));
 typedef float q35_f32x4 __attribute__((ext_vector_type(4)));
+typedef float q35_f32x2 __attribute__((ext_vector_type(2)));
 #define Q35_LOAD_NT(ptr) __builtin_nontemporal_load(ptr)
 #define Q35_STORE_NT(value, ptr) __builtin_nontemporal_store(value, ptr)
 #endif

@@ -190,6 +190,7 @@ struct GemmArgs {
   int cu_count = 0;
   int force_ks = 0, force_split = 0;  // plan overrides (0 = automatic)
   int max_split = 0;                  // bound on the K splits (0 = 32)
+  int group_rows = 0;                 // split path: rows per wavefront, 16 or 32 (0 = by shape)
   // tall single-split matrix (the vocabulary head): the streaming kernel
   // with activations staged in LDS; implied by `cand`
   bool head = false;

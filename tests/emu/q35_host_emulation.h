@@ -236,6 +236,7 @@ inline q35emu_v4i q35emu_mfma_i8(long a, long b, q35emu_v4i c) {
 typedef unsigned int q35_u32x4 __attribute__((vector_size(16)));
 typedef unsigned int q35_u32x2 __attribute__((vector_size(8)));
 typedef float q35_f32x4 __attribute__((vector_size(16)));
+typedef float q35_f32x2 __attribute__((vector_size(8)));
 #define Q35_LOAD_NT(ptr) (*(ptr))
 inline void lds_barrier() { __syncthreads(); }
 inline void q35_compiler_fence() { asm volatile("" ::: "memory"); }
