@@ -291,8 +291,33 @@ int q35_runtime_step(q35_runtime *rt, const q35_step_desc *desc, int32_t *out_to
 int q35_runtime_prefill(q35_runtime *rt, int32_t slot, int32_t pos0, const int32_t *tokens,
                         int32_t count, const int32_t *page_table, int32_t max_pages, float penalty,
                         int32_t *out_token);
-/* Copies the final normalized hidden rows of the last step ([batch][hidden]). */
+/* Copies the final normalized hidden rows of the last step ([batch][hidden]);
+ * after q35_runtime_prefill, row 0 is the chunk's last position. */
 int q35_runtime_last_hidden(q35_runtime *rt, float *out, size_t count);
+/* Greedy head of one final normalized hidden row with a slot's penalty counts:
+ * greedy_q4_token (weights.inl:1217-1295), the head a complete prefix hit runs
+ * on the prefix's stored hidden row (cpu_engine.inl:711-726). hidden is HOST
+ * memory [hidden]; the row is prepared exactly as the step's final norm
+ * prepares it, so the token equals the one a full prefill would select. */
+int q35_runtime_head(q35_runtime *rt, int32_t slot, const float *hidden, float penalty,
+                     int32_t *out_token);
+
+/* Hybrid prefix snapshot: CpuPrefix (cpu_engine.h:32-45), captured by
+ * CpuEngine::register_prefix (cpu_engine_prefix.inl:31-96) and restored by
+ * initialize (cpu_engine.inl:386-407). It copies, in device memory, a slot's
+ * DeltaNet state and conv ring after `tokens` positions and keeps the final
+ * normalized hidden row of position tokens - 1 (host memory, optional). KV
+ * pages are not copied: the owner retains the pages that cover the prefix
+ * (q35_page_retain) and shares them; the first append to a shared, partly
+ * filled page copies it (q35_page_copy). Destroy snapshots before their runtime. */
+typedef struct q35_state_snapshot q35_state_snapshot;
+int q35_state_snapshot_create(q35_runtime *rt, int32_t slot, int32_t tokens, const float *hidden,
+                              q35_state_snapshot **out);
+int q35_state_snapshot_restore(q35_runtime *rt, const q35_state_snapshot *snap, int32_t slot);
+int32_t q35_state_snapshot_tokens(const q35_state_snapshot *snap);
+size_t q35_state_snapshot_bytes(const q35_state_snapshot *snap);
+int q35_state_snapshot_hidden(const q35_state_snapshot *snap, float *out, size_t count);
+void q35_state_snapshot_destroy(q35_state_snapshot *snap);
 
 /* Kernel-level timing, no reference counterpart (the reference reports only
  * request-level prefill_ms/decode_ms, cpu_engine.h:147). While enabled,
@@ -324,11 +349,14 @@ typedef struct {
   int32_t prefill_chunk_size;  /* prompt tokens per advance() of a prefilling request */
   int32_t page_tokens;
   int32_t use_graphs;
+  uint64_t max_prefix_bytes;   /* CpuEngineConfig::max_prefix_bytes; 0 = 256 MiB */
 } q35_engine_config;
 typedef struct {
   int32_t status;
   uint64_t generated_tokens, committed_tokens, prefill_tokens, decode_forwards;
   double prefill_ms, decode_ms;
+  uint64_t cached_prefix_tokens;  /* prompt tokens restored from a prefix snapshot */
+  double prefix_restore_ms;
 } q35_request_result;
 
 int q35_engine_create(q35_model *model, const q35_engine_config *config, q35_engine **out);
@@ -339,9 +367,9 @@ int q35_engine_submit(q35_engine *engine, const int32_t *prompt_tokens, size_t p
 int q35_engine_advance(q35_engine *engine, uint64_t id);
 int q35_engine_advance_batch(q35_engine *engine, const uint64_t *ids, size_t count);
 int q35_engine_step(q35_engine *engine, int32_t *progressed);
-/* No reference counterpart: prefill several requests together, one prompt
- * token per request per device step, until every prompt is consumed (the
- * reference prefills one request per advance(), cpu_engine.inl:668-790). */
+/* No reference counterpart: prefill several requests, each to the end of its
+ * prompt in chunks of up to max_decode_batch_size positions (the reference
+ * prefills one chunk of one request per advance(), cpu_engine.inl:668-790). */
 int q35_engine_prefill_batch(q35_engine *engine, const uint64_t *ids, size_t count);
 int q35_engine_result(q35_engine *engine, uint64_t id, q35_request_result *out,
                       int32_t *tokens, size_t token_capacity, size_t *token_count);
@@ -350,6 +378,35 @@ int q35_engine_cancel(q35_engine *engine, uint64_t id);
 q35_runtime *q35_engine_runtime(q35_engine *engine);
 int q35_engine_release(q35_engine *engine, uint64_t id);
 const char *q35_engine_last_error(const q35_engine *engine);
+
+/* Prefix cache: CpuEngine::register_prefix / find_prefix (cpu_engine.h:181-193,
+ * cpu_engine_prefix.inl:11-96) and CpuRequestSpec::prefix (cpu_engine.h:124).
+ * A prefix is a state snapshot (q35_state_snapshot) plus the KV pages of its
+ * tokens, shared by every request that attaches it. Handles are nonzero ids;
+ * each handle returned by register/find pins the snapshot until
+ * q35_engine_release_prefix. Unpinned snapshots stay cached and are evicted
+ * least recently used first when max_prefix_bytes would be exceeded
+ * (cpu_engine.inl:112-143). Matching is by exact tokens and trust namespace. */
+int q35_engine_register_prefix(q35_engine *engine, const int32_t *tokens, size_t count,
+                               const char *trust_namespace, uint64_t *out_prefix);
+/* Longest cached prefix of tokens[0..count) in the namespace; *out_prefix = 0
+ * (and *out_tokens = 0) when none matches. */
+int q35_engine_find_prefix(q35_engine *engine, const int32_t *tokens, size_t count,
+                           const char *trust_namespace, uint64_t *out_prefix, size_t *out_tokens);
+int q35_engine_release_prefix(q35_engine *engine, uint64_t prefix);
+/* submit with CpuRequestSpec::prefix: the prompt must start with the prefix's
+ * tokens; the request restores the snapshot instead of prefilling them
+ * (cpu_engine.inl:386-407, validation :895-910). prefix 0 = none. */
+int q35_engine_submit_prefixed(q35_engine *engine, const int32_t *prompt_tokens, size_t prompt_count,
+                               size_t max_new_tokens, float repetition_penalty,
+                               const int32_t *stop_token_ids, size_t stop_count, uint64_t prefix,
+                               uint64_t *out_id);
+/* CpuEngineStats' prefix counters (cpu_engine.h:160-162). */
+typedef struct {
+  uint64_t prefix_builds, prefix_build_fallbacks, prefix_hits, prefix_cached_tokens, prefix_evictions;
+  uint64_t prefix_entries, prefix_bytes;
+} q35_prefix_stats;
+int q35_engine_prefix_stats(const q35_engine *engine, q35_prefix_stats *out);
 
 #ifdef __cplusplus
 }

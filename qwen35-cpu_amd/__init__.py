@@ -69,13 +69,20 @@ class StepDesc(ctypes.Structure):
 class EngineConfig(ctypes.Structure):
     _fields_ = [("max_resident_requests", c_int32), ("max_context", c_int32),
                 ("max_decode_batch_size", c_int32), ("prefill_chunk_size", c_int32),
-                ("page_tokens", c_int32), ("use_graphs", c_int32)]
+                ("page_tokens", c_int32), ("use_graphs", c_int32), ("max_prefix_bytes", c_uint64)]
 
 
 class RequestResult(ctypes.Structure):
     _fields_ = [("status", c_int32), ("generated_tokens", c_uint64), ("committed_tokens", c_uint64),
                 ("prefill_tokens", c_uint64), ("decode_forwards", c_uint64),
-                ("prefill_ms", c_double), ("decode_ms", c_double)]
+                ("prefill_ms", c_double), ("decode_ms", c_double),
+                ("cached_prefix_tokens", c_uint64), ("prefix_restore_ms", c_double)]
+
+
+class PrefixStats(ctypes.Structure):
+    _fields_ = [("prefix_builds", c_uint64), ("prefix_build_fallbacks", c_uint64), ("prefix_hits", c_uint64),
+                ("prefix_cached_tokens", c_uint64), ("prefix_evictions", c_uint64), ("prefix_entries", c_uint64),
+                ("prefix_bytes", c_uint64)]
 
 
 P = c_void_p
@@ -152,6 +159,19 @@ _SIGS = {
     "q35_engine_release": (c_int, [P, c_uint64]),
     "q35_engine_last_error": (c_char_p, [P]),
     "q35_engine_runtime": (P, [P]),
+    "q35_engine_register_prefix": (c_int, [P, P, c_size_t, c_char_p, POINTER(c_uint64)]),
+    "q35_engine_find_prefix": (c_int, [P, P, c_size_t, c_char_p, POINTER(c_uint64), POINTER(c_size_t)]),
+    "q35_engine_release_prefix": (c_int, [P, c_uint64]),
+    "q35_engine_submit_prefixed": (c_int, [P, P, c_size_t, c_size_t, c_float, P, c_size_t, c_uint64,
+                                           POINTER(c_uint64)]),
+    "q35_engine_prefix_stats": (c_int, [P, POINTER(PrefixStats)]),
+    "q35_runtime_head": (c_int, [P, c_int32, P, c_float, P]),
+    "q35_state_snapshot_create": (c_int, [P, c_int32, c_int32, P, POINTER(P)]),
+    "q35_state_snapshot_restore": (c_int, [P, P, c_int32]),
+    "q35_state_snapshot_tokens": (c_int32, [P]),
+    "q35_state_snapshot_bytes": (c_size_t, [P]),
+    "q35_state_snapshot_hidden": (c_int, [P, P, c_size_t]),
+    "q35_state_snapshot_destroy": (None, [P]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _f = getattr(lib, _name)
@@ -488,10 +508,10 @@ class Engine(_Profiled):
     """CpuEngine mirror (include/qwen35x/runtime/cpu_engine.h:173-215), greedy requests."""
 
     def __init__(self, model, max_resident_requests=32, max_context=8192, max_decode_batch_size=32,
-                 prefill_chunk_size=128, page_tokens=16, use_graphs=True):
+                 prefill_chunk_size=128, page_tokens=16, use_graphs=True, max_prefix_bytes=0):
         self.model, self.ctx = model, model.ctx
         cfg = EngineConfig(max_resident_requests, max_context, max_decode_batch_size, prefill_chunk_size,
-                           page_tokens, int(use_graphs))
+                           page_tokens, int(use_graphs), max_prefix_bytes)
         h = c_void_p()
         self.ctx.check(lib.q35_engine_create(model.handle, ctypes.byref(cfg), ctypes.byref(h)), "engine create")
         self.handle = h
@@ -504,14 +524,42 @@ class Engine(_Profiled):
             raise Q35Error(f"{what}: {STATUS.get(status, status)} "
                            f"{lib.q35_engine_last_error(self.handle).decode(errors='replace')}")
 
-    def submit(self, prompt, max_new_tokens=128, repetition_penalty=1.0, stop_token_ids=()):
+    def submit(self, prompt, max_new_tokens=128, repetition_penalty=1.0, stop_token_ids=(), prefix=0):
         prompt = np.ascontiguousarray(prompt, np.int32)
         stops = np.ascontiguousarray(stop_token_ids, np.int32)
         rid = c_uint64()
-        self._check(lib.q35_engine_submit(self.handle, _ptr(prompt), prompt.size, max_new_tokens,
-                                          repetition_penalty, _ptr(stops) if stops.size else None, stops.size,
-                                          ctypes.byref(rid)), "submit")
+        self._check(lib.q35_engine_submit_prefixed(self.handle, _ptr(prompt), prompt.size, max_new_tokens,
+                                                   repetition_penalty, _ptr(stops) if stops.size else None,
+                                                   stops.size, prefix, ctypes.byref(rid)), "submit")
         return rid.value
+
+    def register_prefix(self, tokens, trust_namespace):
+        """CpuEngine::register_prefix: a pinned prefix handle (release_prefix unpins)."""
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        h = c_uint64()
+        self._check(lib.q35_engine_register_prefix(self.handle, _ptr(tokens), tokens.size,
+                                                   trust_namespace.encode(), ctypes.byref(h)), "register_prefix")
+        return h.value
+
+    def find_prefix(self, tokens, trust_namespace):
+        """CpuEngine::find_prefix: (handle, token count) of the longest cached match, (0, 0) if none."""
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        h, n = c_uint64(), c_size_t()
+        self._check(lib.q35_engine_find_prefix(self.handle, _ptr(tokens), tokens.size, trust_namespace.encode(),
+                                               ctypes.byref(h), ctypes.byref(n)), "find_prefix")
+        return h.value, n.value
+
+    def release_prefix(self, handle):
+        self._check(lib.q35_engine_release_prefix(self.handle, handle), "release_prefix")
+
+    def free_pages(self):
+        """Free pages of the engine's KV pool (q35_runtime_free_pages)."""
+        return lib.q35_runtime_free_pages(self._rt())
+
+    def prefix_stats(self):
+        st = PrefixStats()
+        self._check(lib.q35_engine_prefix_stats(self.handle, ctypes.byref(st)), "prefix_stats")
+        return {f: getattr(st, f) for f, _ in st._fields_}
 
     def advance(self, rid):
         self._check(lib.q35_engine_advance(self.handle, rid), "advance")

@@ -9,12 +9,18 @@
 //   step            serving scheduler: retire, admit, alternate decode batches
 //                   with prefill chunks, rotate for fairness
 //                   (cpu_engine_scheduler.inl:2-105)
+//   register_prefix / find_prefix   cpu_engine_prefix.inl:11-96: a state
+//                   snapshot plus the prefix's KV pages, shared by the
+//                   requests that attach it (CpuRequestSpec::prefix)
 // Request state lives on the device: a slot (DeltaNet state, conv ring,
 // penalty counts) and a list of KV pages that grows as positions advance.
+// Pages shared with a prefix are copied before the first write into them
+// (KvPagesF16::append on a shared tail, kv_pages.h:52-60).
 #include <algorithm>
 #include <chrono>
 #include <cstring>
 #include <map>
+#include <memory>
 #include <new>
 #include <string>
 #include <vector>
@@ -37,6 +43,19 @@ struct Request {
   std::vector<int32_t> output;
   q35_request_result result{};
   bool resident = false;
+  uint64_t prefix = 0;  // attached prefix, pinned until the request retires
+};
+
+// A cached prefix (CpuPrefix): snapshot, the pages of its tokens (one
+// reference each) and the pins of handles and attached requests.
+struct Prefix {
+  uint64_t id = 0;
+  std::vector<int32_t> tokens;
+  std::string ns;
+  q35_state_snapshot *snap = nullptr;
+  std::vector<int32_t> pages;
+  size_t bytes = 0;
+  int pins = 0;
 };
 
 double ms_since(std::chrono::steady_clock::time_point t) {
@@ -55,6 +74,11 @@ struct q35_engine {
   std::string error;
   bool prefer_decode = true, scheduling = false;
   uint64_t last_prefill = 0, last_decode = 0;
+  // prefix cache in least-recently-used order (back = most recent)
+  std::vector<std::unique_ptr<Prefix>> prefixes;
+  uint64_t next_prefix = 1;
+  size_t max_prefix_bytes = 0, prefix_bytes = 0;
+  q35_prefix_stats prefix_stats{};
 };
 
 namespace {
@@ -68,6 +92,47 @@ bool terminal(const Request &r) {
   return r.status == Q35_REQ_COMPLETE || r.status == Q35_REQ_CANCELLED || r.status == Q35_REQ_FAILED;
 }
 
+Prefix *find_prefix_id(q35_engine *e, uint64_t id) {
+  for (auto &p : e->prefixes)
+    if (p->id == id) return p.get();
+  return nullptr;
+}
+
+// Moves a prefix to the most recently used end.
+void touch_prefix(q35_engine *e, Prefix *p) {
+  auto it = std::find_if(e->prefixes.begin(), e->prefixes.end(), [&](const auto &q) { return q.get() == p; });
+  if (it != e->prefixes.end()) std::rotate(it, it + 1, e->prefixes.end());
+}
+
+void destroy_prefix(q35_engine *e, Prefix &p) {
+  for (int32_t page : p.pages) (void)q35_page_release(e->rt, page);
+  p.pages.clear();
+  q35_state_snapshot_destroy(p.snap);
+  p.snap = nullptr;
+}
+
+// prefix_room (cpu_engine.inl:112-131): evict unpinned prefixes, least
+// recently used first, until `bytes` fit.
+bool prefix_room(q35_engine *e, size_t bytes) {
+  if (bytes > e->max_prefix_bytes) return false;
+  for (auto it = e->prefixes.begin(); e->prefix_bytes > e->max_prefix_bytes - bytes && it != e->prefixes.end();) {
+    if ((*it)->pins == 0) {
+      e->prefix_bytes -= (*it)->bytes;
+      destroy_prefix(e, **it);
+      ++e->prefix_stats.prefix_evictions;
+      it = e->prefixes.erase(it);
+    } else {
+      ++it;
+    }
+  }
+  return e->prefix_bytes <= e->max_prefix_bytes - bytes;
+}
+
+void unpin_prefix(q35_engine *e, uint64_t id) {
+  Prefix *p = find_prefix_id(e, id);
+  if (p != nullptr && p->pins > 0) --p->pins;
+}
+
 void retire(q35_engine *e, Request &r) {
   if (!r.resident || !terminal(r)) return;
   for (int32_t p : r.pages) (void)q35_page_release(e->rt, p);
@@ -75,6 +140,8 @@ void retire(q35_engine *e, Request &r) {
   if (r.slot >= 0) (void)q35_slot_free(e->rt, r.slot);
   r.slot = -1;
   r.resident = false;
+  if (r.prefix != 0) unpin_prefix(e, r.prefix);
+  r.prefix = 0;
 }
 
 int activate(q35_engine *e, Request &r) {
@@ -84,6 +151,47 @@ int activate(q35_engine *e, Request &r) {
   r.slot = slot;
   r.resident = true;
   r.status = Q35_REQ_PREFILL;
+  if (r.prefix != 0) {
+    // initialize with spec.prefix (cpu_engine.inl:386-407): restore the
+    // state, share the prefix's pages
+    const auto t0 = std::chrono::steady_clock::now();
+    Prefix *p = find_prefix_id(e, r.prefix);
+    int rs = p == nullptr ? Q35_ERR_STATE : q35_state_snapshot_restore(e->rt, p->snap, slot);
+    if (rs != Q35_OK) {
+      r.status = Q35_REQ_FAILED;
+      (void)q35_slot_free(e->rt, slot);
+      r.slot = -1;
+      r.resident = false;
+      return fail(e, rs, "Invalid prefix snapshot.");
+    }
+    for (int32_t page : p->pages) (void)q35_page_retain(e->rt, page);
+    r.pages = p->pages;
+    r.committed = p->tokens.size();
+    r.result.cached_prefix_tokens = p->tokens.size();
+    r.result.committed_tokens = r.committed;
+    r.result.prefix_restore_ms = ms_since(t0);
+    ++e->prefix_stats.prefix_hits;
+    e->prefix_stats.prefix_cached_tokens += p->tokens.size();
+    touch_prefix(e, p);
+  }
+  return Q35_OK;
+}
+
+// Copy-on-write of the page that receives position `pos` when it is shared
+// (a prefix's partly filled tail page).
+int own_page(q35_engine *e, Request &r, size_t pos) {
+  const size_t idx = pos / static_cast<size_t>(e->cfg.page_tokens);
+  if (idx >= r.pages.size() || q35_page_refcount(e->rt, r.pages[idx]) <= 1) return Q35_OK;
+  int32_t fresh = -1;
+  int st = q35_page_alloc(e->rt, &fresh);
+  if (st != Q35_OK) return fail(e, st, "KV page pool exhausted");
+  st = q35_page_copy(e->rt, r.pages[idx], fresh, static_cast<int32_t>(pos % e->cfg.page_tokens));
+  if (st != Q35_OK) {
+    (void)q35_page_release(e->rt, fresh);
+    return fail(e, st, "KV page copy failed");
+  }
+  (void)q35_page_release(e->rt, r.pages[idx]);
+  r.pages[idx] = fresh;
   return Q35_OK;
 }
 
@@ -122,7 +230,8 @@ int run_step(q35_engine *e, const std::vector<Request *> &rows, const std::vecto
   std::vector<float> pen(B);
   for (int b = 0; b < B; ++b) {
     Request &r = *rows[b];
-    int st = ensure_page(e, r, r.committed);
+    int st = own_page(e, r, r.committed);
+    if (st == Q35_OK) st = ensure_page(e, r, r.committed);
     if (st != Q35_OK) return st;
     slots[b] = r.slot;
     positions[b] = static_cast<int32_t>(r.committed);
@@ -162,6 +271,7 @@ extern "C" int q35_engine_create(q35_model *m, const q35_engine_config *cfg, q35
   e->model = m;
   e->cfg = *cfg;
   if (e->cfg.prefill_chunk_size <= 0) e->cfg.prefill_chunk_size = 128;
+  e->max_prefix_bytes = cfg->max_prefix_bytes ? static_cast<size_t>(cfg->max_prefix_bytes) : size_t(256) << 20;
   q35_runtime_config rc{};
   rc.max_slots = cfg->max_resident_requests;
   rc.max_batch = std::max(cfg->max_decode_batch_size, 1);
@@ -179,6 +289,8 @@ extern "C" int q35_engine_create(q35_model *m, const q35_engine_config *cfg, q35
 
 extern "C" void q35_engine_destroy(q35_engine *e) {
   if (e == nullptr) return;
+  for (auto &p : e->prefixes) destroy_prefix(e, *p);
+  e->prefixes.clear();
   q35_runtime_destroy(e->rt);
   delete e;
 }
@@ -189,6 +301,12 @@ extern "C" const char *q35_engine_last_error(const q35_engine *e) {
 
 extern "C" int q35_engine_submit(q35_engine *e, const int32_t *prompt, size_t n, size_t max_new,
                                  float penalty, const int32_t *stops, size_t n_stops, uint64_t *out_id) {
+  return q35_engine_submit_prefixed(e, prompt, n, max_new, penalty, stops, n_stops, 0, out_id);
+}
+
+extern "C" int q35_engine_submit_prefixed(q35_engine *e, const int32_t *prompt, size_t n, size_t max_new,
+                                          float penalty, const int32_t *stops, size_t n_stops, uint64_t prefix,
+                                          uint64_t *out_id) {
   if (e == nullptr || out_id == nullptr) return Q35_ERR_INVALID;
   *out_id = 0;
   e->error.clear();
@@ -201,6 +319,13 @@ extern "C" int q35_engine_submit(q35_engine *e, const int32_t *prompt, size_t n,
     return fail(e, Q35_ERR_INVALID, "Invalid request or resident/context limit reached.");
   for (size_t i = 0; i < n; ++i)
     if (prompt[i] < 0 || prompt[i] >= vocab) return fail(e, Q35_ERR_INVALID, "Invalid request token.");
+  Prefix *pre = nullptr;
+  if (prefix != 0) {
+    // the attached prefix must be a prefix of the prompt (cpu_engine.inl:895-910)
+    pre = find_prefix_id(e, prefix);
+    if (pre == nullptr || pre->tokens.size() > n || !std::equal(pre->tokens.begin(), pre->tokens.end(), prompt))
+      return fail(e, Q35_ERR_INVALID, "Prefix does not match the request.");
+  }
   Request r;
   r.id = e->next_id++;
   r.prompt.assign(prompt, prompt + n);
@@ -208,9 +333,16 @@ extern "C" int q35_engine_submit(q35_engine *e, const int32_t *prompt, size_t n,
   r.penalty = penalty;
   if (stops && n_stops) r.stops.assign(stops, stops + n_stops);
   r.status = Q35_REQ_QUEUED;
+  if (pre != nullptr) {
+    r.prefix = prefix;
+    ++pre->pins;
+  }
   if (resident < static_cast<size_t>(e->cfg.max_resident_requests)) {
     const int st = activate(e, r);
-    if (st != Q35_OK) return st;
+    if (st != Q35_OK) {
+      if (r.prefix != 0) unpin_prefix(e, r.prefix);
+      return st;
+    }
   }
   *out_id = r.id;
   e->reqs.emplace(r.id, std::move(r));
@@ -226,10 +358,27 @@ static int prefill_chunks(q35_engine *e, Request &r, size_t limit) {
   const size_t rows = static_cast<size_t>(e->cfg.max_decode_batch_size);
   const int max_pages = (e->cfg.max_context + e->cfg.page_tokens - 1) / e->cfg.page_tokens;
   std::vector<int32_t> table(max_pages, 0);
+  if (r.committed == r.prompt.size() && r.status == Q35_REQ_PREFILL) {
+    // complete prefix hit: the request's own greedy head on the prefix's
+    // final hidden row (cpu_engine.inl:711-726)
+    Prefix *p = find_prefix_id(e, r.prefix);
+    std::vector<float> hidden(e->model->d.hidden);
+    int32_t out = -1;
+    int st = p == nullptr ? Q35_ERR_STATE : q35_state_snapshot_hidden(p->snap, hidden.data(), hidden.size());
+    if (st == Q35_OK) st = q35_runtime_head(e->rt, r.slot, hidden.data(), r.penalty, &out);
+    if (st != Q35_OK) {
+      r.status = Q35_REQ_FAILED;
+      return fail(e, st, "Prefix head selection failed.");
+    }
+    select_token(r, out);
+    r.result.prefill_ms += ms_since(t0);
+    return Q35_OK;
+  }
   size_t done = 0;
   while (done < limit && r.committed < r.prompt.size()) {
     const size_t n = std::min({rows, limit - done, r.prompt.size() - r.committed});
-    int st = ensure_page(e, r, r.committed + n - 1);
+    int st = own_page(e, r, r.committed);
+    if (st == Q35_OK) st = ensure_page(e, r, r.committed + n - 1);
     if (st != Q35_OK) {
       r.status = Q35_REQ_FAILED;
       return st;
@@ -416,6 +565,98 @@ extern "C" int q35_engine_release(q35_engine *e, uint64_t id) {
   Request &r = it->second;
   if (!terminal(r)) r.status = Q35_REQ_CANCELLED;
   retire(e, r);
+  if (r.prefix != 0) unpin_prefix(e, r.prefix);  // a queued request never became resident
   e->reqs.erase(it);
+  return Q35_OK;
+}
+
+// ---------------------------------------------------------------- prefixes
+
+extern "C" int q35_engine_register_prefix(q35_engine *e, const int32_t *tokens, size_t n, const char *ns,
+                                          uint64_t *out) {
+  if (e == nullptr || out == nullptr) return Q35_ERR_INVALID;
+  *out = 0;
+  e->error.clear();
+  const int vocab = e->model->d.vocab;
+  if (tokens == nullptr || n == 0 || n > static_cast<size_t>(e->cfg.max_context) || ns == nullptr || ns[0] == 0 ||
+      !std::all_of(tokens, tokens + n, [&](int32_t t) { return t >= 0 && t < vocab; }))
+    return fail(e, Q35_ERR_INVALID, "Invalid registered prefix tokens or trust namespace.");
+  for (auto &p : e->prefixes)
+    if (p->ns == ns && p->tokens.size() == n && std::equal(tokens, tokens + n, p->tokens.begin())) {
+      ++p->pins;
+      touch_prefix(e, p.get());
+      *out = p->id;
+      return Q35_OK;
+    }
+  // snapshot (one state copy and the conv ring) plus the prefix's KV rows
+  const q35_model_dims &d = e->model->d;
+  const size_t pages = (n + e->cfg.page_tokens - 1) / e->cfg.page_tokens;
+  const size_t bytes = (static_cast<size_t>(e->rt->rec_copy_stride) + e->rt->conv_slot_stride + d.hidden) * 4 +
+                       pages * e->cfg.page_tokens * static_cast<size_t>(d.n_kv_heads) * d.head_dim * 2 * 2 *
+                           e->model->n_full;
+  if (!prefix_room(e, bytes)) return fail(e, Q35_ERR_OOM, "Prefix store is full; active handles pin its snapshots.");
+  // build: prefill the tokens on a private slot (cpu_engine_prefix.inl:56-94)
+  Request tmp;
+  tmp.prompt.assign(tokens, tokens + n);
+  tmp.max_new = 1;
+  int st = activate(e, tmp);
+  if (st != Q35_OK) return st;
+  st = prefill_chunks(e, tmp, n);
+  std::vector<float> hidden(d.hidden);
+  if (st == Q35_OK) st = q35_runtime_last_hidden(e->rt, hidden.data(), hidden.size());
+  q35_state_snapshot *snap = nullptr;
+  if (st == Q35_OK) st = q35_state_snapshot_create(e->rt, tmp.slot, static_cast<int32_t>(n), hidden.data(), &snap);
+  (void)q35_slot_free(e->rt, tmp.slot);
+  if (st != Q35_OK) {
+    for (int32_t p : tmp.pages) (void)q35_page_release(e->rt, p);
+    ++e->prefix_stats.prefix_build_fallbacks;
+    return fail(e, st, e->error.empty() ? "Could not build the prefix." : e->error);
+  }
+  auto p = std::make_unique<Prefix>();
+  p->id = e->next_prefix++;
+  p->tokens = tmp.prompt;
+  p->ns = ns;
+  p->snap = snap;
+  p->pages = std::move(tmp.pages);
+  p->bytes = bytes;
+  p->pins = 1;
+  *out = p->id;
+  e->prefix_bytes += bytes;
+  ++e->prefix_stats.prefix_builds;
+  e->prefixes.push_back(std::move(p));
+  return Q35_OK;
+}
+
+extern "C" int q35_engine_find_prefix(q35_engine *e, const int32_t *tokens, size_t n, const char *ns,
+                                      uint64_t *out, size_t *out_tokens) {
+  if (e == nullptr || out == nullptr || (n && tokens == nullptr) || ns == nullptr) return Q35_ERR_INVALID;
+  *out = 0;
+  if (out_tokens) *out_tokens = 0;
+  Prefix *best = nullptr;
+  for (auto &p : e->prefixes)
+    if (p->ns == ns && p->tokens.size() <= n && (best == nullptr || p->tokens.size() > best->tokens.size()) &&
+        std::equal(p->tokens.begin(), p->tokens.end(), tokens))
+      best = p.get();
+  if (best == nullptr) return Q35_OK;
+  ++best->pins;
+  touch_prefix(e, best);
+  *out = best->id;
+  if (out_tokens) *out_tokens = best->tokens.size();
+  return Q35_OK;
+}
+
+extern "C" int q35_engine_release_prefix(q35_engine *e, uint64_t id) {
+  if (e == nullptr) return Q35_ERR_INVALID;
+  Prefix *p = find_prefix_id(e, id);
+  if (p == nullptr || p->pins <= 0) return fail(e, Q35_ERR_STATE, "Unknown or unpinned prefix.");
+  --p->pins;
+  return Q35_OK;
+}
+
+extern "C" int q35_engine_prefix_stats(const q35_engine *e, q35_prefix_stats *out) {
+  if (e == nullptr || out == nullptr) return Q35_ERR_INVALID;
+  *out = e->prefix_stats;
+  out->prefix_entries = e->prefixes.size();
+  out->prefix_bytes = e->prefix_bytes;
   return Q35_OK;
 }

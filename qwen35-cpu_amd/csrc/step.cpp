@@ -535,6 +535,27 @@ int profile_collect(q35_runtime *rt) {
 // Enqueues one decode step for `batch` rows whose metadata is already in
 // rt->meta_host; the host copy is part of the enqueued work so the whole
 // sequence can be captured as a graph.
+// The greedy head over `tokens` rows of A16 activations in rt->codes/scales:
+// penalty counts of slot count_rows[t], penalty penalties[t] (device arrays).
+static GemmArgs greedy_head_args(q35_runtime *rt, int tokens, const int32_t *count_rows, const float *penalties) {
+  const q35_model_dims &d = rt->model->d;
+  GemmArgs g;
+  g.w = rt->model->embed;
+  g.rows = d.vocab;
+  g.nb = d.hidden / 32;
+  g.codes = rt->codes;
+  g.scales = rt->scales;
+  g.tokens = tokens;
+  g.cand = rt->cand;
+  g.cand_stride = kMaxTokens;
+  g.counts = rt->counts;
+  g.count_rows = count_rows;
+  g.counts_stride = d.vocab;
+  g.penalties = penalties;
+  g.cu_count = rt->ctx->cu_count;
+  return g;
+}
+
 int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool prefill) {
   q35_model *m = rt->model;
   Context *ctx = rt->ctx;
@@ -809,20 +830,7 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
     Q35_KERNEL(Q35_KERNEL_HEAD, gemm_algorithmic_bytes(d.vocab, H / 32, head_tokens, true, false), launch_gemm(g, s),
                "logits head");
   } else {
-    GemmArgs g;
-    g.w = m->embed;
-    g.rows = d.vocab;
-    g.nb = H / 32;
-    g.codes = rt->codes;
-    g.scales = rt->scales;
-    g.tokens = head_tokens;
-    g.cand = rt->cand;
-    g.cand_stride = kMaxTokens;
-    g.counts = rt->counts;
-    g.count_rows = slots + head_row0;
-    g.counts_stride = d.vocab;
-    g.penalties = penalties + head_row0;
-    g.cu_count = ctx->cu_count;
+    const GemmArgs g = greedy_head_args(rt, head_tokens, slots + head_row0, penalties + head_row0);
     const int ncand = gemm_argmax_cands(d.vocab, H / 32, head_tokens, ctx->cu_count);
     Q35_KERNEL(Q35_KERNEL_HEAD, gemm_algorithmic_bytes(d.vocab, H / 32, head_tokens, false, false) + ncand * HB * 8.0,
                launch_gemm(g, s), "greedy head");
@@ -1030,5 +1038,124 @@ extern "C" int q35_runtime_last_hidden(q35_runtime *rt, float *out, size_t count
   if (rt == nullptr || out == nullptr) return Q35_ERR_INVALID;
   const size_t n = std::min(count, static_cast<size_t>(rt->last_batch) * rt->model->d.hidden);
   Q35_HIP_TRY(rt->ctx, hipMemcpy(out, rt->hidden_out, n * 4, hipMemcpyDeviceToHost));
+  return Q35_OK;
+}
+
+// ============================================================ prefix snapshots
+// CpuPrefix (cpu_engine.h:32-45): captured by register_prefix
+// (cpu_engine_prefix.inl:31-96), restored in initialize (cpu_engine.inl:386-407).
+struct q35_state_snapshot {
+  q35_runtime *rt = nullptr;
+  int32_t tokens = 0;
+  float *state = nullptr;     // one recurrent copy, then the conv ring
+  std::vector<float> hidden;  // final normalized row of position tokens - 1
+  size_t bytes = 0;
+};
+
+extern "C" int q35_state_snapshot_create(q35_runtime *rt, int32_t slot, int32_t tokens, const float *hidden,
+                                         q35_state_snapshot **out) {
+  if (rt == nullptr || out == nullptr) return Q35_ERR_INVALID;
+  *out = nullptr;
+  if (slot < 0 || slot >= rt->cfg.max_slots || !rt->slot_used[slot] || tokens <= 0 || tokens > rt->cfg.max_context)
+    return set_error(rt->ctx, Q35_ERR_INVALID, "snapshot needs an allocated slot and a token count");
+  auto *snap = new (std::nothrow) q35_state_snapshot();
+  if (snap == nullptr) return Q35_ERR_OOM;
+  const size_t rec = static_cast<size_t>(rt->rec_copy_stride), conv = static_cast<size_t>(rt->conv_slot_stride);
+  snap->rt = rt;
+  snap->tokens = tokens;
+  snap->bytes = (rec + conv) * 4 + (hidden != nullptr ? rt->model->d.hidden * 4 : 0);
+  if (hidden != nullptr) snap->hidden.assign(hidden, hidden + rt->model->d.hidden);
+  Context *ctx = rt->ctx;
+  const hipError_t e = hipMalloc(reinterpret_cast<void **>(&snap->state), (rec + conv) * 4);
+  if (e != hipSuccess) {
+    delete snap;
+    return hip_error(ctx, e, "snapshot allocation");
+  }
+  // the state after `tokens` positions is copy (tokens & 1): position p reads
+  // copy p & 1 and writes the other
+  const float *src = rt->recurrent + slot * rt->rec_slot_stride + (tokens & 1) * rt->rec_copy_stride;
+  hipError_t c = hipMemcpyAsync(snap->state, src, rec * 4, hipMemcpyDeviceToDevice, ctx->stream);
+  if (c == hipSuccess)
+    c = hipMemcpyAsync(snap->state + rec, rt->conv + slot * rt->conv_slot_stride, conv * 4, hipMemcpyDeviceToDevice,
+                       ctx->stream);
+  if (c == hipSuccess) c = hipStreamSynchronize(ctx->stream);
+  if (c != hipSuccess) {
+    (void)hipFree(snap->state);
+    delete snap;
+    return hip_error(ctx, c, "snapshot copy");
+  }
+  *out = snap;
+  return Q35_OK;
+}
+
+extern "C" int q35_state_snapshot_restore(q35_runtime *rt, const q35_state_snapshot *snap, int32_t slot) {
+  if (rt == nullptr || snap == nullptr || snap->rt != rt) return Q35_ERR_INVALID;
+  if (slot < 0 || slot >= rt->cfg.max_slots || !rt->slot_used[slot])
+    return set_error(rt->ctx, Q35_ERR_INVALID, "restore needs an allocated slot");
+  Context *ctx = rt->ctx;
+  const size_t rec = static_cast<size_t>(rt->rec_copy_stride), conv = static_cast<size_t>(rt->conv_slot_stride);
+  float *dst = rt->recurrent + slot * rt->rec_slot_stride + (snap->tokens & 1) * rt->rec_copy_stride;
+  Q35_HIP_TRY(ctx, hipMemcpyAsync(dst, snap->state, rec * 4, hipMemcpyDeviceToDevice, ctx->stream));
+  Q35_HIP_TRY(ctx, hipMemcpyAsync(rt->conv + slot * rt->conv_slot_stride, snap->state + rec, conv * 4,
+                                  hipMemcpyDeviceToDevice, ctx->stream));
+  Q35_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  return Q35_OK;
+}
+
+extern "C" int32_t q35_state_snapshot_tokens(const q35_state_snapshot *snap) { return snap ? snap->tokens : 0; }
+extern "C" size_t q35_state_snapshot_bytes(const q35_state_snapshot *snap) { return snap ? snap->bytes : 0; }
+
+extern "C" void q35_state_snapshot_destroy(q35_state_snapshot *snap) {
+  if (snap == nullptr) return;
+  (void)hipSetDevice(snap->rt->ctx->device);
+  (void)hipStreamSynchronize(snap->rt->ctx->stream);
+  (void)hipFree(snap->state);
+  delete snap;
+}
+
+extern "C" int q35_state_snapshot_hidden(const q35_state_snapshot *snap, float *out, size_t count) {
+  if (snap == nullptr || out == nullptr || snap->hidden.empty() || count < snap->hidden.size()) return Q35_ERR_INVALID;
+  std::memcpy(out, snap->hidden.data(), snap->hidden.size() * 4);
+  return Q35_OK;
+}
+
+// Greedy head of one final normalized hidden row (greedy_q4_token,
+// weights.inl:1217-1295): identity-basis q8 preparation of the row (the same
+// codes the step's final norm writes for it), the Q4 head with the slot's
+// penalty counts, argmax.
+extern "C" int q35_runtime_head(q35_runtime *rt, int32_t slot, const float *hidden, float penalty,
+                                int32_t *out_token) {
+  if (rt == nullptr || hidden == nullptr || out_token == nullptr) return Q35_ERR_INVALID;
+  if (slot < 0 || slot >= rt->cfg.max_slots || !rt->slot_used[slot])
+    return set_error(rt->ctx, Q35_ERR_INVALID, "head needs an allocated slot");
+  if (!(penalty >= 1.0F)) return set_error(rt->ctx, Q35_ERR_INVALID, "penalty must be >= 1");
+  Context *ctx = rt->ctx;
+  const q35_model_dims &d = rt->model->d;
+  const MetaLayout ml = meta_layout(rt->cfg.max_batch, rt->max_pages_per_row);
+  std::memset(rt->meta_host, 0, rt->meta_bytes);
+  reinterpret_cast<int32_t *>(rt->meta_host + ml.slots)[0] = slot;
+  reinterpret_cast<float *>(rt->meta_host + ml.penalties)[0] = penalty;
+  hipStream_t s = ctx->stream;
+  Q35_HIP_TRY(ctx, hipMemcpyAsync(rt->meta_dev, rt->meta_host, rt->meta_bytes, hipMemcpyHostToDevice, s));
+  Q35_HIP_TRY(ctx, hipMemcpyAsync(rt->hidden_out, hidden, static_cast<size_t>(d.hidden) * 4, hipMemcpyHostToDevice, s));
+  PrepArgs p;
+  p.source = kPrepPlain;
+  p.x = rt->hidden_out;
+  p.x_stride = d.hidden;
+  p.tokens = 1;
+  p.K = d.hidden;
+  p.h128 = false;
+  p.seed = d.sign_seed;
+  p.codes = rt->codes;
+  p.scales = rt->scales;
+  Q35_HIP_TRY(ctx, launch_prep(p, s));
+  const GemmArgs g = greedy_head_args(rt, 1, reinterpret_cast<const int32_t *>(rt->meta_dev + ml.slots),
+                                      reinterpret_cast<const float *>(rt->meta_dev + ml.penalties));
+  Q35_HIP_TRY(ctx, launch_gemm(g, s));
+  const int ncand = gemm_argmax_cands(d.vocab, d.hidden / 32, 1, ctx->cu_count);
+  Q35_HIP_TRY(ctx, launch_argmax_finalize(rt->cand, ncand, kMaxTokens, 1, rt->tokens_out_dev, nullptr, s));
+  Q35_HIP_TRY(ctx, hipStreamSynchronize(s));
+  rt->last_batch = 1;
+  *out_token = rt->tokens_out_host[0];
   return Q35_OK;
 }

@@ -1,0 +1,139 @@
+"""Prefix cache of the engine (CpuEngine::register_prefix / find_prefix,
+cpu_engine_prefix.inl:11-96; CpuRequestSpec::prefix restored in initialize,
+cpu_engine.inl:386-407) on the small hybrid model.
+
+Chunked prefill leaves the state that single-token steps leave, bit for bit,
+so a request that restores a prefix snapshot and shares its KV pages must
+produce exactly the tokens of the same request prefilled from scratch: with
+the prefix ending inside a page (the shared tail page is copied on the first
+write, kv_pages.h:52-60) or on a page boundary, with two requests sharing one
+prefix in the same decode batch, and for a complete hit (prompt == prefix)
+whose first token comes from its own greedy head on the stored hidden row
+(cpu_engine.inl:711-726), with and without a repetition penalty."""
+import numpy as np
+import pytest
+
+from tests.model_util import build_small_model, small_dims, upload_model
+
+pytestmark = pytest.mark.gpu
+
+NEW = 6
+
+
+@pytest.fixture(scope="module")
+def small(q, ctx):
+    d, sched = small_dims()
+    tensors = build_small_model(d, sched, seed=13)
+    model = upload_model(q, ctx, d, sched, tensors)
+    yield d, model
+    model.close()
+
+
+def engine(q, model, **kw):
+    cfg = dict(max_resident_requests=4, max_context=96, max_decode_batch_size=4, prefill_chunk_size=8,
+               page_tokens=16, use_graphs=False)
+    cfg.update(kw)
+    return q.Engine(model, **cfg)
+
+
+def drain(q, eng, ids):
+    """Prefill every request, then decode them together until all finish."""
+    eng.prefill_batch([i for i in ids if q.REQ_STATUS[eng.result(i)[0].status] == "prefill"])
+    while True:
+        active = [i for i in ids if q.REQ_STATUS[eng.result(i)[0].status] == "decode"]
+        if not active:
+            break
+        eng.advance_batch(active)
+    return [eng.result(i) for i in ids]
+
+
+def reference_tokens(q, model, prompts, penalty=1.0):
+    eng = engine(q, model)
+    ids = [eng.submit(p, NEW, penalty) for p in prompts]
+    out = [toks for _, toks in drain(q, eng, ids)]
+    eng.close()
+    return out
+
+
+@pytest.mark.parametrize("plen", [24, 32])
+def test_prefix_hit_equals_full_prefill(q, small, plen):
+    d, model = small
+    rng = np.random.default_rng(plen)
+    shared = rng.integers(0, d["vocab"], size=plen).astype(np.int32)
+    prompts = [np.concatenate([shared, rng.integers(0, d["vocab"], size=n).astype(np.int32)]) for n in (9, 14)]
+    want = reference_tokens(q, model, prompts)
+    eng = engine(q, model)
+    free0 = eng.free_pages()
+    print(f"prefix hit plen={plen}", flush=True)
+    h = eng.register_prefix(shared, "tenant-a")
+    assert h != 0
+    ids = [eng.submit(p, NEW, prefix=h) for p in prompts]
+    results = drain(q, eng, ids)
+    for (res, toks), ref, p in zip(results, want, prompts):
+        np.testing.assert_array_equal(toks, ref)
+        assert res.cached_prefix_tokens == plen
+        assert res.prefill_tokens == p.size - plen
+    # the prefix's pages stay shared and intact: a third request still matches
+    rid = eng.submit(prompts[0], NEW, prefix=h)
+    np.testing.assert_array_equal(drain(q, eng, [rid])[0][1], want[0])
+    for i in ids + [rid]:
+        eng.release(i)
+    eng.release_prefix(h)
+    # only the cached prefix's own pages remain allocated
+    assert eng.free_pages() == free0 - (plen + 15) // 16
+    st = eng.prefix_stats()
+    assert st["prefix_builds"] == 1 and st["prefix_hits"] == 3 and st["prefix_entries"] == 1
+    eng.close()
+
+
+@pytest.mark.parametrize("penalty", [1.0, 1.3])
+def test_complete_hit_runs_its_own_head(q, small, penalty):
+    d, model = small
+    prompt = np.random.default_rng(7).integers(0, d["vocab"], size=21).astype(np.int32)
+    want = reference_tokens(q, model, [prompt], penalty)[0]
+    eng = engine(q, model)
+    print(f"complete prefix hit penalty={penalty}", flush=True)
+    h = eng.register_prefix(prompt, "tenant-a")
+    rid = eng.submit(prompt, NEW, penalty, prefix=h)
+    res, toks = drain(q, eng, [rid])[0]
+    np.testing.assert_array_equal(toks, want)
+    assert res.cached_prefix_tokens == prompt.size and res.prefill_tokens == 0
+    eng.close()
+
+
+def test_find_dedup_evict_and_errors(q, small):
+    d, model = small
+    t = np.random.default_rng(3).integers(0, d["vocab"], size=40).astype(np.int32)
+    eng = engine(q, model)
+    free0 = eng.free_pages()
+    print("prefix find / dedup / errors", flush=True)
+    h16 = eng.register_prefix(t[:16], "a")
+    h24 = eng.register_prefix(t[:24], "a")
+    assert eng.register_prefix(t[:24], "a") == h24  # exact tokens and namespace: the same snapshot
+    assert eng.find_prefix(t[:30], "a") == (h24, 24)
+    assert eng.find_prefix(t[:20], "a") == (h16, 16)
+    assert eng.find_prefix(t, "b") == (0, 0)
+    assert eng.find_prefix(t[1:], "a") == (0, 0)
+    with pytest.raises(q.Q35Error):
+        eng.submit(t[1:30], NEW, prefix=h24)  # the prompt does not start with the prefix
+    with pytest.raises(q.Q35Error):
+        eng.register_prefix(t[:8], "")  # a trust namespace is required
+    for h in (h16, h24, h24, h24, h16):  # register x3 + find x2 pins
+        eng.release_prefix(h)
+    with pytest.raises(q.Q35Error):
+        eng.release_prefix(h24)  # no pins left
+    assert eng.prefix_stats()["prefix_builds"] == 2
+    eng.close()
+    # a budget that holds one prefix: the unpinned one is evicted for the next
+    eng = engine(q, model, max_prefix_bytes=1_000_000)
+    free0 = eng.free_pages()
+    a = eng.register_prefix(t[:16], "a")
+    with pytest.raises(q.Q35Error):
+        eng.register_prefix(t[:12], "a")  # the pinned prefix cannot be evicted
+    eng.release_prefix(a)
+    b = eng.register_prefix(t[:12], "a")
+    st = eng.prefix_stats()
+    assert st["prefix_evictions"] == 1 and st["prefix_entries"] == 1
+    assert eng.find_prefix(t, "a") == (b, 12)
+    assert eng.free_pages() == free0 - 1
+    eng.close()
