@@ -229,6 +229,13 @@ typedef struct {
   int32_t use_graphs;     /* capture each step shape as a hipGraph and replay it        */
 } q35_runtime_config;
 
+/* One sampling candidate: a penalized, temperature-scaled logit and its token. */
+typedef struct {
+  float value;
+  int32_t token;
+} q35_candidate;
+#define Q35_MAX_CANDIDATES 64
+
 typedef struct q35_runtime q35_runtime;
 
 int q35_runtime_create(q35_model *model, const q35_runtime_config *config, q35_runtime **out);
@@ -291,6 +298,34 @@ int q35_runtime_step(q35_runtime *rt, const q35_step_desc *desc, int32_t *out_to
 int q35_runtime_prefill(q35_runtime *rt, int32_t slot, int32_t pos0, const int32_t *tokens,
                         int32_t count, const int32_t *page_table, int32_t max_pages, float penalty,
                         int32_t *out_token);
+/* Sampled decoding (sample_token_from_logits, layers.inl:491-600). Per row:
+ * top_k candidates (1..Q35_MAX_CANDIDATES; 1 with inv_temperature 1 is the
+ * greedy argmax) of the logits after the repetition penalty
+ * (apply_repetition_penalty_inplace, layers.inl:471-489) and the scaling
+ * v *= inv_temperature (layers.inl:546-549), in descending order, ties to the
+ * lower token (layers.inl:552-568). The host finishes softmax, top_p and the
+ * draw in the reference's order. */
+typedef struct {
+  int32_t top_k;
+  float inv_temperature;  /* 1 / SamplingOptions::temperature */
+} q35_row_sampling;
+/* One decode step (as q35_runtime_step) whose head writes the raw logits on
+ * the device; out_candidates [batch][Q35_MAX_CANDIDATES] receives each row's
+ * candidate list (unused entries: token -1, value -inf). raw_logits (HOST,
+ * [batch][vocab], optional) receives the raw logits, for logits callbacks
+ * and for samplers that need every token (top_k 0). */
+int q35_runtime_step_candidates(q35_runtime *rt, const q35_step_desc *desc, const q35_row_sampling *sampling,
+                                q35_candidate *out_candidates, float *raw_logits);
+/* The same for one final normalized hidden row (HOST [hidden]) with a slot's
+ * counts: the first token after a prefill (q35_runtime_last_hidden row 0) or
+ * a complete prefix hit. out_candidates [Q35_MAX_CANDIDATES], raw_logits
+ * [vocab] (optional). */
+int q35_runtime_head_candidates(q35_runtime *rt, int32_t slot, const float *hidden, float penalty,
+                                const q35_row_sampling *sampling, q35_candidate *out_candidates,
+                                float *raw_logits);
+/* A slot's penalty counts (HOST int32 [vocab]): the prompt tokens plus every
+ * token fed back with count_input (CpuEngine's Sequence::counts). */
+int q35_slot_counts(q35_runtime *rt, int32_t slot, int32_t *out, size_t count);
 /* Copies the final normalized hidden rows of the last step ([batch][hidden]);
  * after q35_runtime_prefill, row 0 is the chunk's last position. */
 int q35_runtime_last_hidden(q35_runtime *rt, float *out, size_t count);
@@ -359,11 +394,44 @@ typedef struct {
   double prefix_restore_ms;
 } q35_request_result;
 
+/* ReferenceLogitsCallback (options.h:20) in C: called synchronously with a
+ * row's raw logits before penalties and sampling; index is the output token
+ * index, forced_token the forced output token or -1. Returns nonzero to go on;
+ * zero fails the request. It must not call back into the engine. */
+typedef int (*q35_logits_callback)(void *context, size_t index, int32_t forced_token, const float *logits,
+                                   size_t count);
+/* CpuRequestSpec (cpu_engine.h:105-133) without constraints, selected readout
+ * and drafting. Sampling follows SamplingOptions (options.h:10-13): temperature
+ * <= 1e-6 is greedy; seed < 0 seeds the request's mt19937 from random_device
+ * (cpu_engine.inl:379-381). stop_sequences holds stop_sequence_count
+ * sequences back to back, of the given lengths. */
+typedef struct {
+  const int32_t *prompt_tokens;
+  size_t prompt_count;
+  size_t max_new_tokens;
+  float temperature, top_p;
+  int32_t top_k;
+  float repetition_penalty;
+  int64_t seed;
+  const int32_t *stop_token_ids;
+  size_t stop_count;
+  const int32_t *stop_sequences;
+  const size_t *stop_sequence_lengths;
+  size_t stop_sequence_count;
+  const int32_t *forced_output_tokens; /* empty, or exactly max_new_tokens tokens */
+  size_t forced_count;
+  q35_logits_callback logits_callback;
+  void *logits_callback_context;
+  uint64_t prefix;                     /* 0 = none (q35_engine_register_prefix) */
+} q35_request_spec;
+
 int q35_engine_create(q35_model *model, const q35_engine_config *config, q35_engine **out);
 void q35_engine_destroy(q35_engine *engine);
 int q35_engine_submit(q35_engine *engine, const int32_t *prompt_tokens, size_t prompt_count,
                       size_t max_new_tokens, float repetition_penalty,
                       const int32_t *stop_token_ids, size_t stop_count, uint64_t *out_id);
+/* CpuEngine::submit (cpu_engine.inl:832-930) with a full request spec. */
+int q35_engine_submit_spec(q35_engine *engine, const q35_request_spec *spec, uint64_t *out_id);
 int q35_engine_advance(q35_engine *engine, uint64_t id);
 int q35_engine_advance_batch(q35_engine *engine, const uint64_t *ids, size_t count);
 int q35_engine_step(q35_engine *engine, int32_t *progressed);

@@ -374,6 +374,9 @@ def ref():
             "ref_l2_normalize_f32": (None, [P, c_size_t, c_size_t, c_float, c_float, c_int]),
             "ref_silu_mul_f32": (None, [P, P, P, c_size_t, c_int]),
             "ref_engine_set_probe": (None, [P, c_size_t, P]),
+            "ref_engine_sample": (c_int, [ctypes.c_char_p, ctypes.c_char_p, c_int, P, c_size_t, c_size_t, c_float,
+                                          c_float, c_int, c_float, ctypes.c_int64, P, P, c_size_t, ctypes.c_char_p,
+                                          c_size_t]),
             "ref_engine_greedy": (c_int, [ctypes.c_char_p, ctypes.c_char_p, c_int, c_int, P, c_size_t, c_size_t, c_size_t,
                                           c_float, P, P, P, P, P, ctypes.c_char_p, c_size_t]),
         }
@@ -382,3 +385,20 @@ def ref():
             f.restype, f.argtypes = res, args
         _ref = r
     return _ref
+
+
+def ref_engine_sample(model_dir, artifact, prompt, new_tokens, vocab, temperature, top_p, top_k, penalty, seed,
+                      threads=8):
+    """One sampled request through the reference CpuEngine (oracle/_ref):
+    returns (tokens [new_tokens], raw logits [new_tokens][vocab]) as its
+    logits callback saw them."""
+    prompt = np.ascontiguousarray(prompt, np.int32)
+    out = np.zeros(new_tokens, np.int32)
+    logits = np.zeros((new_tokens, vocab), np.float32)
+    err = ctypes.create_string_buffer(512)
+    rc = ref().ref_engine_sample(os.fsencode(model_dir), os.fsencode(artifact), threads, prompt.ctypes.data,
+                                 prompt.size, new_tokens, temperature, top_p, top_k, penalty, seed, out.ctypes.data,
+                                 logits.ctypes.data, vocab, err, 512)
+    if rc != 0:
+        raise RuntimeError(err.value.decode())
+    return out, logits

@@ -27,6 +27,7 @@
 using namespace qwen35x;
 using namespace qwen35x::cpu;
 
+
 namespace {
 Q8_0Backend be(int b) { return static_cast<Q8_0Backend>(b); }
 }
@@ -286,6 +287,70 @@ int ref_engine_greedy(const char *model_dir, const char *artifact, int threads, 
     std::memcpy(out_tokens + r * new_tokens, state.output_tokens.data(),
                 new_tokens * sizeof(std::int32_t));
   }
+  return 0;
+}
+
+// Sampled decode of one request through the reference engine: the request's
+// SamplingOptions (options.h:10-13, seed >= 0 seeds its mt19937,
+// cpu_engine.inl:379-381), a logits callback (cpu_engine.h:119-121) copying
+// every raw logits row into logits[new_tokens][vocab], and the sampled tokens
+// into out_tokens[new_tokens] (sample_token_from_logits, layers.inl:491-600,
+// through select, cpu_engine.inl:441-487). Returns 0, or 1 with the error.
+int ref_engine_sample(const char *model_dir, const char *artifact, int threads, const std::int32_t *prompt,
+                      std::size_t prompt_len, std::size_t new_tokens, float temperature, float top_p, int top_k,
+                      float penalty, std::int64_t seed, std::int32_t *out_tokens, float *logits, std::size_t vocab,
+                      char *error, std::size_t error_size) {
+  std::string err;
+  auto fail = [&](const std::string &message) {
+    if (error && error_size) {
+      std::strncpy(error, message.c_str(), error_size - 1);
+      error[error_size - 1] = 0;
+    }
+    return 1;
+  };
+  auto profile = ProfileLoader::load_from_hf_directory(model_dir, err);
+  if (!profile) return fail(err);
+  CpuLoadOptions options;
+  options.model_dir = model_dir;
+  options.cpu_q4_h128_path = artifact;
+  auto model = CpuModel::load(*profile, options, err);
+  if (!model) return fail(err);
+  CpuEngineConfig config;
+  config.threads = threads;
+  config.max_resident_requests = 1;
+  config.max_context = prompt_len + new_tokens + 8;
+  auto engine = CpuEngine::create(model, config, err);
+  if (!engine) return fail(err);
+  struct Capture {
+    float *logits;
+    std::size_t vocab;
+  } capture{logits, vocab};
+  auto callback = [](void *opaque, std::size_t step, std::int32_t, const float *row, std::size_t count,
+                     std::string &) -> bool {
+    auto &c = *static_cast<Capture *>(opaque);
+    if (count != c.vocab) return false;
+    std::memcpy(c.logits + step * c.vocab, row, count * sizeof(float));
+    return true;
+  };
+  CpuRequestSpec spec;
+  spec.prompt_tokens.assign(prompt, prompt + prompt_len);
+  spec.max_new_tokens = new_tokens;
+  spec.sampling.temperature = temperature;
+  spec.sampling.top_p = top_p;
+  spec.sampling.top_k = top_k;
+  spec.sampling.repetition_penalty = penalty;
+  spec.sampling.seed = seed;
+  spec.logits_callback = callback;
+  spec.logits_callback_context = &capture;
+  const auto id = engine->submit(std::move(spec), err);
+  if (!id) return fail(err);
+  CpuRequestResult state;
+  do {
+    if (!engine->advance(id, err) || !engine->result(id, state)) return fail(err);
+  } while (state.status == CpuRequestStatus::prefill || state.status == CpuRequestStatus::decode);
+  if (state.status != CpuRequestStatus::complete || state.output_tokens.size() != new_tokens)
+    return fail("incomplete sampled output: " + state.error);
+  std::memcpy(out_tokens, state.output_tokens.data(), new_tokens * sizeof(std::int32_t));
   return 0;
 }
 

@@ -79,6 +79,31 @@ class RequestResult(ctypes.Structure):
                 ("cached_prefix_tokens", c_uint64), ("prefix_restore_ms", c_double)]
 
 
+class Candidate(ctypes.Structure):
+    _fields_ = [("value", c_float), ("token", c_int32)]
+
+
+class RowSampling(ctypes.Structure):
+    _fields_ = [("top_k", c_int32), ("inv_temperature", c_float)]
+
+
+MAX_CANDIDATES = 64
+# q35_logits_callback: (context, index, forced_token, logits, count) -> nonzero to continue
+LOGITS_CALLBACK = ctypes.CFUNCTYPE(c_int, c_void_p, c_size_t, c_int32, POINTER(c_float), c_size_t)
+
+
+class RequestSpec(ctypes.Structure):
+    _fields_ = [("prompt_tokens", POINTER(c_int32)), ("prompt_count", c_size_t), ("max_new_tokens", c_size_t),
+                ("temperature", c_float), ("top_p", c_float), ("top_k", c_int32),
+                ("repetition_penalty", c_float), ("seed", ctypes.c_int64),
+                ("stop_token_ids", POINTER(c_int32)), ("stop_count", c_size_t),
+                ("stop_sequences", POINTER(c_int32)), ("stop_sequence_lengths", POINTER(c_size_t)),
+                ("stop_sequence_count", c_size_t),
+                ("forced_output_tokens", POINTER(c_int32)), ("forced_count", c_size_t),
+                ("logits_callback", LOGITS_CALLBACK), ("logits_callback_context", c_void_p),
+                ("prefix", c_uint64)]
+
+
 class PrefixStats(ctypes.Structure):
     _fields_ = [("prefix_builds", c_uint64), ("prefix_build_fallbacks", c_uint64), ("prefix_hits", c_uint64),
                 ("prefix_cached_tokens", c_uint64), ("prefix_evictions", c_uint64), ("prefix_entries", c_uint64),
@@ -166,6 +191,10 @@ _SIGS = {
                                            POINTER(c_uint64)]),
     "q35_engine_prefix_stats": (c_int, [P, POINTER(PrefixStats)]),
     "q35_runtime_head": (c_int, [P, c_int32, P, c_float, P]),
+    "q35_runtime_step_candidates": (c_int, [P, POINTER(StepDesc), P, P, P]),
+    "q35_runtime_head_candidates": (c_int, [P, c_int32, P, c_float, P, P, P]),
+    "q35_slot_counts": (c_int, [P, c_int32, P, c_size_t]),
+    "q35_engine_submit_spec": (c_int, [P, POINTER(RequestSpec), POINTER(c_uint64)]),
     "q35_state_snapshot_create": (c_int, [P, c_int32, c_int32, P, POINTER(P)]),
     "q35_state_snapshot_restore": (c_int, [P, P, c_int32]),
     "q35_state_snapshot_tokens": (c_int32, [P]),
@@ -479,6 +508,36 @@ class Runtime(_Profiled):
         self.ctx.check(lib.q35_runtime_step(self.handle, ctypes.byref(d), _ptr(out), _ptr(lg)), "runtime step")
         return (out, lg) if logits else out
 
+    def step_candidates(self, slots, positions, tokens, page_table, top_k, inv_temperature, count_input=None,
+                        penalties=None, raw_logits=False):
+        """A decode step returning each row's sampling candidates
+        (q35_runtime_step_candidates): arrays [batch][64] of values and tokens,
+        and the raw logits [batch][vocab] when asked."""
+        slots = np.ascontiguousarray(slots, np.int32)
+        positions = np.ascontiguousarray(positions, np.int32)
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        b = slots.size
+        table = np.ascontiguousarray(page_table, np.int32).reshape(b, -1)
+        ci = np.ascontiguousarray(count_input if count_input is not None else np.zeros(b), np.uint8)
+        pen = np.ascontiguousarray(penalties if penalties is not None else np.ones(b), np.float32)
+        d = StepDesc(b, slots.ctypes.data_as(POINTER(c_int32)), positions.ctypes.data_as(POINTER(c_int32)),
+                     tokens.ctypes.data_as(POINTER(c_int32)), ci.ctypes.data_as(POINTER(c_uint8)),
+                     pen.ctypes.data_as(POINTER(c_float)), table.ctypes.data_as(POINTER(c_int32)), table.shape[1])
+        rs = (RowSampling * b)(*[RowSampling(int(k), float(t)) for k, t in zip(
+            np.broadcast_to(top_k, b), np.broadcast_to(inv_temperature, b))])
+        cand = (Candidate * (b * MAX_CANDIDATES))()
+        lg = np.empty((b, self.model.dims.vocab), np.float32) if raw_logits else None
+        self.ctx.check(lib.q35_runtime_step_candidates(self.handle, ctypes.byref(d), ctypes.byref(rs),
+                                                       ctypes.byref(cand), _ptr(lg)), "step candidates")
+        arr = np.frombuffer(cand, dtype=np.dtype([("value", np.float32), ("token", np.int32)])).reshape(
+            b, MAX_CANDIDATES).copy()
+        return (arr, lg) if raw_logits else arr
+
+    def slot_counts(self, slot):
+        out = np.empty(self.model.dims.vocab, np.int32)
+        self.ctx.check(lib.q35_slot_counts(self.handle, int(slot), _ptr(out), out.size), "slot counts")
+        return out
+
     def prefill(self, slot, pos0, tokens, page_table, penalty=1.0):
         """Chunked prefill of one request (q35_runtime_prefill): returns the
         greedy token after the chunk's last position."""
@@ -531,6 +590,41 @@ class Engine(_Profiled):
         self._check(lib.q35_engine_submit_prefixed(self.handle, _ptr(prompt), prompt.size, max_new_tokens,
                                                    repetition_penalty, _ptr(stops) if stops.size else None,
                                                    stops.size, prefix, ctypes.byref(rid)), "submit")
+        return rid.value
+
+    def submit_spec(self, prompt, max_new_tokens=128, temperature=0.7, top_p=0.8, top_k=20,
+                    repetition_penalty=1.05, seed=-1, stop_token_ids=(), stop_sequences=(), forced_output_tokens=(),
+                    logits_callback=None, prefix=0):
+        """CpuEngine::submit with a CpuRequestSpec (q35_engine_submit_spec); the
+        sampling defaults are SamplingOptions' (options.h:10-13). logits_callback,
+        when given, is a Python callable (index, forced_token, logits ndarray) ->
+        bool, called with each row's raw logits."""
+        keep = []  # arrays and the callback must outlive the call
+
+        def arr(values, dtype, ctype):
+            a = np.ascontiguousarray(values, dtype)
+            keep.append(a)
+            return a.ctypes.data_as(POINTER(ctype)) if a.size else None, a.size
+
+        prompt_p, n = arr(prompt, np.int32, c_int32)
+        stops_p, ns = arr(stop_token_ids, np.int32, c_int32)
+        seqs = [np.asarray(q, np.int32) for q in stop_sequences]
+        flat_p, _ = arr(np.concatenate(seqs) if seqs else np.zeros(0, np.int32), np.int32, c_int32)
+        lens_p, nseq = arr([q.size for q in seqs], np.uintp, c_size_t)
+        forced_p, nf = arr(forced_output_tokens, np.int32, c_int32)
+        cb = LOGITS_CALLBACK()
+        if logits_callback is not None:
+            def trampoline(_ctx, index, forced, logits, count):
+                try:
+                    return 1 if logits_callback(index, forced, np.ctypeslib.as_array(logits, (count,)).copy()) else 0
+                except Exception:  # a raising callback fails the request, as returning false does
+                    return 0
+            cb = LOGITS_CALLBACK(trampoline)
+            self._callbacks = getattr(self, "_callbacks", []) + [cb]
+        spec = RequestSpec(prompt_p, n, max_new_tokens, temperature, top_p, top_k, repetition_penalty, seed,
+                           stops_p, ns, flat_p, lens_p, nseq, forced_p, nf, cb, None, prefix)
+        rid = c_uint64()
+        self._check(lib.q35_engine_submit_spec(self.handle, ctypes.byref(spec), ctypes.byref(rid)), "submit")
         return rid.value
 
     def register_prefix(self, tokens, trust_namespace):

@@ -18,10 +18,13 @@
 // (KvPagesF16::append on a shared tail, kv_pages.h:52-60).
 #include <algorithm>
 #include <chrono>
+#include <cmath>
 #include <cstring>
 #include <map>
 #include <memory>
 #include <new>
+#include <numeric>
+#include <random>
 #include <string>
 #include <vector>
 
@@ -34,7 +37,15 @@ struct Request {
   std::vector<int32_t> prompt;
   size_t max_new = 0;
   float penalty = 1.0F;
+  // SamplingOptions (options.h:10-13); temperature <= 1e-6 is greedy
+  float temperature = 0.0F, top_p = 1.0F;
+  int32_t top_k = 0;
+  std::mt19937 rng;
+  std::vector<int32_t> forced;  // forced_output_tokens
+  q35_logits_callback callback = nullptr;
+  void *callback_context = nullptr;
   std::vector<int32_t> stops;
+  std::vector<std::vector<int32_t>> stop_sequences;
   int status = Q35_REQ_QUEUED;
   int slot = -1;
   std::vector<int32_t> pages;
@@ -207,13 +218,129 @@ int ensure_page(q35_engine *e, Request &r, size_t position) {
   return Q35_OK;
 }
 
-// select() (cpu_engine.inl:441-487): append, stop ids, completion.
+// The fused greedy head serves a request (cpu_engine.inl:307-313, 676-678).
+bool is_greedy(const Request &r) { return r.temperature <= 1e-6F && r.forced.empty() && r.callback == nullptr; }
+
+// Device candidate settings of a request: greedy argmax (k = 1, scale 1) at
+// temperature ~0, top_k candidates when 1 <= top_k <= 64, else one
+// placeholder candidate while the host samples from the raw logits.
+q35_row_sampling row_sampling(const Request &r) {
+  q35_row_sampling s{1, 1.0F};
+  if (r.temperature > 1e-6F) {
+    s.inv_temperature = 1.0F / r.temperature;
+    if (r.top_k >= 1 && r.top_k <= Q35_MAX_CANDIDATES) s.top_k = r.top_k;
+  }
+  return s;
+}
+bool needs_raw_logits(const Request &r) {
+  return r.callback != nullptr ||
+         (r.temperature > 1e-6F && (r.top_k <= 0 || r.top_k > Q35_MAX_CANDIDATES) && r.forced.empty());
+}
+
+// sample_token_from_logits (layers.inl:570-615) from the descending candidate
+// list: softmax, nucleus cut, one draw of uniform_real_distribution<float>.
+int32_t sample_candidates(const q35_candidate *c, int k, float top_p, std::mt19937 &rng) {
+  int n = 0;
+  while (n < k && c[n].token >= 0) ++n;
+  if (n == 0) return -1;
+  float max_logit = -INFINITY;
+  for (int i = 0; i < n; ++i) max_logit = std::max(max_logit, c[i].value);
+  std::vector<float> probs(n);
+  float denom = 0.0F;
+  for (int i = 0; i < n; ++i) {
+    probs[i] = std::exp(c[i].value - max_logit);
+    denom += probs[i];
+  }
+  if (!(denom > 0.0F)) return c[0].token;
+  for (float &p : probs) p /= denom;
+  size_t keep = probs.size();
+  if (top_p < 1.0F) {
+    float cumulative = 0.0F;
+    keep = 0;
+    for (; keep < probs.size(); ++keep) {
+      cumulative += probs[keep];
+      if (cumulative >= top_p) {
+        ++keep;
+        break;
+      }
+    }
+    keep = std::max<size_t>(1, std::min(keep, probs.size()));
+  }
+  probs.resize(keep);
+  float renorm = 0.0F;
+  for (float p : probs) renorm += p;
+  if (!(renorm > 0.0F)) return c[0].token;
+  for (float &p : probs) p /= renorm;
+  std::uniform_real_distribution<float> dist(0.0F, 1.0F);
+  const float draw = dist(rng);
+  float cumulative = 0.0F;
+  for (size_t i = 0; i < probs.size(); ++i) {
+    cumulative += probs[i];
+    if (draw <= cumulative || i + 1 == probs.size()) return c[i].token;
+  }
+  return c[probs.size() - 1].token;
+}
+
+// sample_token_from_logits (layers.inl:491-600) on the full raw logits row,
+// for samplers that see every token (top_k 0 or above the device list).
+int32_t sample_full(const float *raw, int vocab, const std::vector<int32_t> &counts, Request &r) {
+  std::vector<float> logits(raw, raw + vocab);
+  if (r.penalty > 1.0F)
+    for (int i = 0; i < vocab; ++i)
+      if (counts[i] > 0) logits[i] = logits[i] > 0.0F ? logits[i] / r.penalty : logits[i] * r.penalty;
+  const float inv_temp = 1.0F / r.temperature;
+  for (float &v : logits) v *= inv_temp;
+  std::vector<int> ids(vocab);
+  std::iota(ids.begin(), ids.end(), 0);
+  auto greater = [&](int a, int b) { return logits[a] > logits[b]; };
+  if (r.top_k > 0 && r.top_k < vocab) {
+    std::nth_element(ids.begin(), ids.begin() + r.top_k, ids.end(), greater);
+    ids.resize(r.top_k);
+  }
+  std::sort(ids.begin(), ids.end(), greater);
+  std::vector<q35_candidate> c(ids.size());
+  for (size_t i = 0; i < ids.size(); ++i) c[i] = {logits[ids[i]], ids[i]};
+  return sample_candidates(c.data(), static_cast<int>(c.size()), r.top_p, r.rng);
+}
+
+// The token of one row (select, cpu_engine.inl:441-465): the logits callback
+// on the raw logits, then the forced token, the greedy candidate, a draw from
+// the device candidates, or a draw over the full row.
+int choose_token(q35_engine *e, Request &r, const q35_candidate *cands, const float *raw, int32_t &token) {
+  const int vocab = e->model->d.vocab;
+  const size_t index = r.output.size();
+  if (r.callback != nullptr &&
+      !r.callback(r.callback_context, index, r.forced.empty() ? -1 : r.forced[index], raw, static_cast<size_t>(vocab)))
+    return fail(e, Q35_ERR_STATE, "Logits callback failed.");
+  if (!r.forced.empty()) {
+    token = r.forced[index];
+  } else if (r.temperature <= 1e-6F) {
+    token = cands[0].token;  // argmax with the penalty (layers.inl:519-541)
+  } else if (r.top_k >= 1 && r.top_k <= Q35_MAX_CANDIDATES) {
+    token = sample_candidates(cands, r.top_k, r.top_p, r.rng);
+  } else {
+    std::vector<int32_t> counts(vocab);
+    const int st = q35_slot_counts(e->rt, r.slot, counts.data(), counts.size());
+    if (st != Q35_OK) return fail(e, st, e->model->ctx->error.c_str());
+    token = sample_full(raw, vocab, counts, r);
+  }
+  if (token < 0 || token >= vocab) return fail(e, Q35_ERR_STATE, "Invalid sampled token.");
+  return Q35_OK;
+}
+
+// select() (cpu_engine.inl:441-487): append, stop ids and stop sequences
+// (trimmed from the output), completion.
 void select_token(Request &r, int32_t token) {
   ++r.result.generated_tokens;
   r.output.push_back(token);
   r.pending = token;
-  if (std::find(r.stops.begin(), r.stops.end(), token) != r.stops.end()) {
-    r.output.pop_back();
+  size_t trim = std::find(r.stops.begin(), r.stops.end(), token) != r.stops.end() ? 1 : 0;
+  for (const auto &stop : r.stop_sequences)
+    if (!stop.empty() && stop.size() <= r.output.size() &&
+        std::equal(stop.begin(), stop.end(), r.output.end() - static_cast<std::ptrdiff_t>(stop.size())))
+      trim = std::max(trim, stop.size());
+  if (trim) {
+    r.output.resize(r.output.size() - trim);
     r.status = Q35_REQ_COMPLETE;
   } else {
     r.status = r.output.size() == r.max_new ? Q35_REQ_COMPLETE : Q35_REQ_DECODE;
@@ -221,9 +348,12 @@ void select_token(Request &r, int32_t token) {
 }
 
 // One device step over `rows`: each row feeds `inputs[i]` at position
-// rows[i]->committed. count_input marks generated tokens.
+// rows[i]->committed. count_input marks generated tokens. With `sample` the
+// head keeps the logits and returns each row's candidates (and the raw logits
+// when a row needs them); the tokens are chosen afterwards by choose_token.
 int run_step(q35_engine *e, const std::vector<Request *> &rows, const std::vector<int32_t> &inputs,
-             const std::vector<uint8_t> &count_input, std::vector<int32_t> &out) {
+             const std::vector<uint8_t> &count_input, std::vector<int32_t> &out, bool sample,
+             std::vector<q35_candidate> *cands, std::vector<float> *raw) {
   const int B = static_cast<int>(rows.size());
   const int max_pages = (e->cfg.max_context + e->cfg.page_tokens - 1) / e->cfg.page_tokens;
   std::vector<int32_t> slots(B), positions(B), table(static_cast<size_t>(B) * max_pages, 0);
@@ -248,10 +378,35 @@ int run_step(q35_engine *e, const std::vector<Request *> &rows, const std::vecto
   d.page_table = table.data();
   d.max_pages = max_pages;
   out.assign(B, -1);
-  const int st = q35_runtime_step(e->rt, &d, out.data(), nullptr);
+  int st;
+  if (!sample) {
+    st = q35_runtime_step(e->rt, &d, out.data(), nullptr);
+  } else {
+    std::vector<q35_row_sampling> rs(B);
+    bool need_raw = false;
+    for (int b = 0; b < B; ++b) {
+      rs[b] = row_sampling(*rows[b]);
+      need_raw = need_raw || needs_raw_logits(*rows[b]);
+    }
+    cands->assign(static_cast<size_t>(B) * Q35_MAX_CANDIDATES, q35_candidate{});
+    raw->assign(need_raw ? static_cast<size_t>(B) * e->model->d.vocab : 0, 0.0F);
+    st = q35_runtime_step_candidates(e->rt, &d, rs.data(), cands->data(), need_raw ? raw->data() : nullptr);
+  }
   if (st != Q35_OK) return fail(e, st, e->model->ctx->error.c_str());
   for (auto *r : rows) ++r->committed;
   return Q35_OK;
+}
+
+// The first token after a prompt (or a complete prefix hit) of a request the
+// fused greedy head does not serve: candidates from the final hidden row.
+int choose_after_prompt(q35_engine *e, Request &r, const float *hidden, int32_t &token) {
+  const q35_row_sampling rs = row_sampling(r);
+  std::vector<q35_candidate> cands(Q35_MAX_CANDIDATES);
+  std::vector<float> raw(needs_raw_logits(r) ? e->model->d.vocab : 0);
+  const int st = q35_runtime_head_candidates(e->rt, r.slot, hidden, r.penalty, &rs, cands.data(),
+                                             raw.empty() ? nullptr : raw.data());
+  if (st != Q35_OK) return fail(e, st, e->model->ctx->error.c_str());
+  return choose_token(e, r, cands.data(), raw.empty() ? nullptr : raw.data(), token);
 }
 
 void fail_rows(const std::vector<Request *> &rows) {
@@ -307,18 +462,44 @@ extern "C" int q35_engine_submit(q35_engine *e, const int32_t *prompt, size_t n,
 extern "C" int q35_engine_submit_prefixed(q35_engine *e, const int32_t *prompt, size_t n, size_t max_new,
                                           float penalty, const int32_t *stops, size_t n_stops, uint64_t prefix,
                                           uint64_t *out_id) {
-  if (e == nullptr || out_id == nullptr) return Q35_ERR_INVALID;
+  q35_request_spec spec{};
+  spec.prompt_tokens = prompt;
+  spec.prompt_count = n;
+  spec.max_new_tokens = max_new;
+  spec.temperature = 0.0F;  // greedy
+  spec.top_p = 1.0F;
+  spec.repetition_penalty = penalty;
+  spec.seed = 0;
+  spec.stop_token_ids = stops;
+  spec.stop_count = n_stops;
+  spec.prefix = prefix;
+  return q35_engine_submit_spec(e, &spec, out_id);
+}
+
+extern "C" int q35_engine_submit_spec(q35_engine *e, const q35_request_spec *spec, uint64_t *out_id) {
+  if (e == nullptr || out_id == nullptr || spec == nullptr) return Q35_ERR_INVALID;
   *out_id = 0;
   e->error.clear();
   const int vocab = e->model->d.vocab;
   const size_t ctx = static_cast<size_t>(e->cfg.max_context);
+  const int32_t *prompt = spec->prompt_tokens;
+  const size_t n = spec->prompt_count, max_new = spec->max_new_tokens;
+  const float penalty = spec->repetition_penalty;
+  const uint64_t prefix = spec->prefix;
   size_t resident = 0;
   for (auto &kv : e->reqs) resident += kv.second.resident;
+  auto valid_token = [&](int32_t t) { return t >= 0 && t < vocab; };
   if (prompt == nullptr || n == 0 || max_new == 0 || n > ctx || max_new - 1 > ctx - n ||
-      !(penalty >= 1.0F) || e->reqs.size() >= static_cast<size_t>(e->cfg.max_resident_requests) + 64)
+      e->reqs.size() >= static_cast<size_t>(e->cfg.max_resident_requests) + 64 ||
+      (spec->forced_count != 0 && (spec->forced_output_tokens == nullptr || spec->forced_count != max_new)) ||
+      !std::isfinite(spec->temperature) || spec->temperature < 0 || !std::isfinite(spec->top_p) ||
+      spec->top_p <= 0 || spec->top_p > 1 || spec->top_k < 0 || !std::isfinite(penalty) || penalty < 1 ||
+      (spec->stop_count && spec->stop_token_ids == nullptr) ||
+      (spec->stop_sequence_count && (spec->stop_sequences == nullptr || spec->stop_sequence_lengths == nullptr)))
     return fail(e, Q35_ERR_INVALID, "Invalid request or resident/context limit reached.");
-  for (size_t i = 0; i < n; ++i)
-    if (prompt[i] < 0 || prompt[i] >= vocab) return fail(e, Q35_ERR_INVALID, "Invalid request token.");
+  if (!std::all_of(prompt, prompt + n, valid_token) ||
+      !std::all_of(spec->forced_output_tokens, spec->forced_output_tokens + spec->forced_count, valid_token))
+    return fail(e, Q35_ERR_INVALID, "Invalid request token.");
   Prefix *pre = nullptr;
   if (prefix != 0) {
     // the attached prefix must be a prefix of the prompt (cpu_engine.inl:895-910)
@@ -331,7 +512,16 @@ extern "C" int q35_engine_submit_prefixed(q35_engine *e, const int32_t *prompt, 
   r.prompt.assign(prompt, prompt + n);
   r.max_new = max_new;
   r.penalty = penalty;
-  if (stops && n_stops) r.stops.assign(stops, stops + n_stops);
+  r.temperature = spec->temperature;
+  r.top_p = spec->top_p;
+  r.top_k = spec->top_k;
+  r.rng.seed(spec->seed < 0 ? std::random_device{}() : static_cast<std::uint32_t>(spec->seed));
+  r.forced.assign(spec->forced_output_tokens, spec->forced_output_tokens + spec->forced_count);
+  r.callback = spec->logits_callback;
+  r.callback_context = spec->logits_callback_context;
+  if (spec->stop_count) r.stops.assign(spec->stop_token_ids, spec->stop_token_ids + spec->stop_count);
+  for (size_t i = 0, at = 0; i < spec->stop_sequence_count; at += spec->stop_sequence_lengths[i++])
+    r.stop_sequences.emplace_back(spec->stop_sequences + at, spec->stop_sequences + at + spec->stop_sequence_lengths[i]);
   r.status = Q35_REQ_QUEUED;
   if (pre != nullptr) {
     r.prefix = prefix;
@@ -365,10 +555,12 @@ static int prefill_chunks(q35_engine *e, Request &r, size_t limit) {
     std::vector<float> hidden(e->model->d.hidden);
     int32_t out = -1;
     int st = p == nullptr ? Q35_ERR_STATE : q35_state_snapshot_hidden(p->snap, hidden.data(), hidden.size());
-    if (st == Q35_OK) st = q35_runtime_head(e->rt, r.slot, hidden.data(), r.penalty, &out);
+    if (st == Q35_OK)
+      st = is_greedy(r) ? q35_runtime_head(e->rt, r.slot, hidden.data(), r.penalty, &out)
+                        : choose_after_prompt(e, r, hidden.data(), out);
     if (st != Q35_OK) {
       r.status = Q35_REQ_FAILED;
-      return fail(e, st, "Prefix head selection failed.");
+      return fail(e, st, e->error.empty() ? "Prefix head selection failed." : e->error);
     }
     select_token(r, out);
     r.result.prefill_ms += ms_since(t0);
@@ -394,7 +586,18 @@ static int prefill_chunks(q35_engine *e, Request &r, size_t limit) {
     r.committed += n;
     r.result.prefill_tokens += n;
     done += n;
-    if (r.committed == r.prompt.size()) select_token(r, out);
+    if (r.committed == r.prompt.size()) {
+      if (!is_greedy(r)) {
+        std::vector<float> hidden(e->model->d.hidden);
+        st = q35_runtime_last_hidden(e->rt, hidden.data(), hidden.size());
+        if (st == Q35_OK) st = choose_after_prompt(e, r, hidden.data(), out);
+        if (st != Q35_OK) {
+          r.status = Q35_REQ_FAILED;
+          return e->error.empty() ? fail(e, st, e->model->ctx->error.c_str()) : st;
+        }
+      }
+      select_token(r, out);
+    }
   }
   r.result.prefill_ms += ms_since(t0);
   r.result.committed_tokens = r.committed;
@@ -433,21 +636,40 @@ extern "C" int q35_engine_advance_batch(q35_engine *e, const uint64_t *ids, size
     in.push_back(r->pending);
     cnt.push_back(1);
   }
-  const int st = run_step(e, rows, in, cnt, out);
+  // the fused greedy head only when every row is greedy (cpu_engine.inl:307-313)
+  const bool sample = !std::all_of(rows.begin(), rows.end(), [](const Request *r) { return is_greedy(*r); });
+  std::vector<q35_candidate> cands;
+  std::vector<float> raw;
+  const int st = run_step(e, rows, in, cnt, out, sample, &cands, &raw);
   if (st != Q35_OK) {
     // A failed forward may have updated state: never retry it.
     fail_rows(rows);
     return st;
   }
   const double ms = ms_since(t0);
+  const int vocab = e->model->d.vocab;
+  int result = Q35_OK;
+  std::string first_error;
   for (size_t i = 0; i < rows.size(); ++i) {
     Request *r = rows[i];
     ++r->result.decode_forwards;
     r->result.decode_ms += ms / rows.size();
     r->result.committed_tokens = r->committed;
+    if (sample) {
+      const int cs = choose_token(e, *r, cands.data() + i * Q35_MAX_CANDIDATES,
+                                  raw.empty() ? nullptr : raw.data() + i * static_cast<size_t>(vocab), out[i]);
+      if (cs != Q35_OK) {
+        // this row fails; the others keep their tokens (cpu_engine.inl:1006-1013)
+        r->status = Q35_REQ_FAILED;
+        if (result == Q35_OK) first_error = e->error;
+        result = cs;
+        continue;
+      }
+    }
     select_token(*r, out[i]);
   }
-  return Q35_OK;
+  if (result != Q35_OK) e->error = first_error;
+  return result;
 }
 
 // Extension without a reference counterpart: prefill several requests to the

@@ -265,6 +265,23 @@ inline size_t delta_chunk_scan_floats(int batch, int v_heads) {
 }
 hipError_t launch_delta_chunk(const DeltaArgs &a, hipStream_t stream);
 
+// Sampling candidates: per row, the top_k (<= kMaxCandidates) penalized,
+// temperature-scaled logits, descending (ties: lower token first).
+constexpr int kMaxCandidates = 64;
+struct SampleArgs {
+  const float *logits = nullptr;      // [rows][logits_stride]
+  long long logits_stride = 0;
+  int rows = 0, vocab = 0;
+  const int32_t *counts = nullptr;    // penalty counts [count_rows[r]][vocab] (optional)
+  const int32_t *count_rows = nullptr;
+  const float *penalties = nullptr;   // [rows] (optional: 1)
+  const float *inv_temperature = nullptr;  // [rows] (optional: 1)
+  const int32_t *top_k = nullptr;     // [rows], 1..kMaxCandidates (optional: 1)
+  q35_candidate *out = nullptr;       // [rows][kMaxCandidates]
+};
+size_t sample_scratch_bytes(int rows);
+hipError_t launch_sample_candidates(const SampleArgs &a, unsigned long long *scratch, hipStream_t stream);
+
 // Full attention
 struct AttnPrepArgs {
   SplitRows proj;               // [splits][batch][in_rows] = [q|gate interleaved per head | k | v]

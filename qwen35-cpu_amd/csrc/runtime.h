@@ -65,6 +65,8 @@ struct q35_runtime {
   float *proj = nullptr, *core = nullptr, *q_rot = nullptr, *gates = nullptr;
   float *rows_final = nullptr;  // prefill: summed in-projection rows [batch][proj_width]
   float *delta_scan = nullptr;  // prefill: DeltaNet chunk scan entries and raw outputs
+  unsigned long long *sample_scratch = nullptr;  // sampling: the slices' surviving keys
+  q35_candidate *candidates = nullptr;           // sampling: [max_batch][kMaxCandidates]
   float *part_o = nullptr, *part_ml = nullptr, *logits = nullptr;
   float *hidden_out = nullptr;
   uint64_t *codes = nullptr;

@@ -260,7 +260,7 @@ extern "C" int q35_model_finalize(q35_model *m) {
 namespace {
 
 struct MetaLayout {
-  size_t slots, positions, tokens, seq_lens, penalties, count_input, page_table, total;
+  size_t slots, positions, tokens, seq_lens, penalties, count_input, inv_temperature, top_k, page_table, total;
 };
 
 MetaLayout meta_layout(int max_batch, int max_pages) {
@@ -273,6 +273,8 @@ MetaLayout meta_layout(int max_batch, int max_pages) {
   L.seq_lens = take(max_batch * 4);
   L.penalties = take(max_batch * 4);
   L.count_input = take(max_batch);
+  L.inv_temperature = take(max_batch * 4);
+  L.top_k = take(max_batch * 4);
   L.page_table = take(static_cast<size_t>(max_batch) * max_pages * 4);
   L.total = o;
   return L;
@@ -345,6 +347,9 @@ extern "C" int q35_runtime_create(q35_model *m, const q35_runtime_config *cfg, q
   alloc(static_cast<size_t>(B) * rt->proj_width * 4, reinterpret_cast<void **>(&rt->rows_final));
   if (d.lin_v_heads > 0)
     alloc(delta_chunk_scan_floats(B, d.lin_v_heads) * 4, reinterpret_cast<void **>(&rt->delta_scan));
+  // sampling: per-row candidate lists and the slices' survivors
+  alloc(sample_scratch_bytes(B), reinterpret_cast<void **>(&rt->sample_scratch));
+  alloc(static_cast<size_t>(B) * kMaxCandidates * sizeof(q35_candidate), reinterpret_cast<void **>(&rt->candidates));
   alloc(B * rt->core_width * 4, reinterpret_cast<void **>(&rt->core));
   alloc(B * static_cast<size_t>(d.n_heads) * d.head_dim * 4, reinterpret_cast<void **>(&rt->q_rot));
   alloc(B * static_cast<size_t>(d.n_heads) * d.head_dim * 4, reinterpret_cast<void **>(&rt->gates));
@@ -845,9 +850,11 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
 
 }  // namespace q35
 
-extern "C" int q35_runtime_step(q35_runtime *rt, const q35_step_desc *desc, int32_t *out_tokens,
-                                float *out_logits) {
-  if (rt == nullptr || desc == nullptr) return Q35_ERR_INVALID;
+namespace {
+
+// Validates a step descriptor on the host (no kernel ever sees an
+// out-of-range index) and packs it into the pinned metadata block.
+int pack_step(q35_runtime *rt, const q35_step_desc *desc) {
   Context *ctx = rt->ctx;
   const q35_model_dims &d = rt->model->d;
   const int B = desc->batch;
@@ -892,11 +899,18 @@ extern "C" int q35_runtime_step(q35_runtime *rt, const q35_step_desc *desc, int3
     for (int p = 0; p < used; ++p)
       pt[static_cast<size_t>(b) * rt->max_pages_per_row + p] = desc->page_table[static_cast<size_t>(b) * desc->max_pages + p];
   }
-  const bool want_logits = out_logits != nullptr;
-  if (want_logits && rt->logits == nullptr) {
-    int st = rt_alloc(rt, static_cast<size_t>(rt->cfg.max_batch) * d.vocab * 4, reinterpret_cast<void **>(&rt->logits));
-    if (st != Q35_OK) return st;
-  }
+  return Q35_OK;
+}
+
+int ensure_logits(q35_runtime *rt) {
+  if (rt->logits != nullptr) return Q35_OK;
+  return rt_alloc(rt, static_cast<size_t>(rt->cfg.max_batch) * rt->model->d.vocab * 4,
+                  reinterpret_cast<void **>(&rt->logits));
+}
+
+// Runs the packed step: replays (or captures) its graph, or launches eagerly.
+int launch_step(q35_runtime *rt, int B, bool want_logits) {
+  Context *ctx = rt->ctx;
   int st = Q35_OK;
   if (rt->cfg.use_graphs && !rt->profiling) {
     const auto key = std::make_pair(B, want_logits ? 1 : 0);
@@ -923,6 +937,22 @@ extern "C" int q35_runtime_step(q35_runtime *rt, const q35_step_desc *desc, int3
     st = runtime_enqueue_step(rt, B, want_logits, false);
     if (st != Q35_OK) return st;
   }
+  return Q35_OK;
+}
+
+}  // namespace
+
+extern "C" int q35_runtime_step(q35_runtime *rt, const q35_step_desc *desc, int32_t *out_tokens,
+                                float *out_logits) {
+  if (rt == nullptr || desc == nullptr) return Q35_ERR_INVALID;
+  Context *ctx = rt->ctx;
+  const q35_model_dims &d = rt->model->d;
+  const int B = desc->batch;
+  int st = pack_step(rt, desc);
+  if (st != Q35_OK) return st;
+  const bool want_logits = out_logits != nullptr;
+  if (want_logits && (st = ensure_logits(rt)) != Q35_OK) return st;
+  if ((st = launch_step(rt, B, want_logits)) != Q35_OK) return st;
   if (want_logits)
     Q35_HIP_TRY(ctx, hipMemcpyAsync(out_logits, rt->logits, static_cast<size_t>(B) * d.vocab * 4,
                                     hipMemcpyDeviceToHost, ctx->stream));
@@ -956,6 +986,125 @@ extern "C" int q35_runtime_step(q35_runtime *rt, const q35_step_desc *desc, int3
       std::memcpy(out_tokens, rt->tokens_out_host, B * 4);
     }
   }
+  return Q35_OK;
+}
+
+namespace {
+
+// Per-row candidate settings into the metadata block (rows 0..B-1).
+int pack_sampling(q35_runtime *rt, int B, const q35_row_sampling *sampling) {
+  if (sampling == nullptr) return set_error(rt->ctx, Q35_ERR_INVALID, "missing sampling rows");
+  const MetaLayout ml = meta_layout(rt->cfg.max_batch, rt->max_pages_per_row);
+  auto *inv_t = reinterpret_cast<float *>(rt->meta_host + ml.inv_temperature);
+  auto *top_k = reinterpret_cast<int32_t *>(rt->meta_host + ml.top_k);
+  for (int b = 0; b < B; ++b) {
+    const q35_row_sampling &r = sampling[b];
+    if (r.top_k < 1 || r.top_k > kMaxCandidates || !std::isfinite(r.inv_temperature) || !(r.inv_temperature > 0.0F))
+      return set_error(rt->ctx, Q35_ERR_INVALID, "candidate count must be 1..64 and the scale finite and positive");
+    inv_t[b] = r.inv_temperature;
+    top_k[b] = r.top_k;
+  }
+  return Q35_OK;
+}
+
+// Candidate selection over rows 0..rows-1 of rt->logits with the metadata
+// block's slots, penalties and sampling settings, then the copies back.
+int finish_candidates(q35_runtime *rt, int rows, q35_candidate *out, float *raw_logits) {
+  Context *ctx = rt->ctx;
+  const q35_model_dims &d = rt->model->d;
+  const MetaLayout ml = meta_layout(rt->cfg.max_batch, rt->max_pages_per_row);
+  SampleArgs a;
+  a.logits = rt->logits;
+  a.logits_stride = d.vocab;
+  a.rows = rows;
+  a.vocab = d.vocab;
+  a.counts = rt->counts;
+  a.count_rows = reinterpret_cast<const int32_t *>(rt->meta_dev + ml.slots);
+  a.penalties = reinterpret_cast<const float *>(rt->meta_dev + ml.penalties);
+  a.inv_temperature = reinterpret_cast<const float *>(rt->meta_dev + ml.inv_temperature);
+  a.top_k = reinterpret_cast<const int32_t *>(rt->meta_dev + ml.top_k);
+  a.out = rt->candidates;
+  Q35_HIP_TRY(ctx, launch_sample_candidates(a, rt->sample_scratch, ctx->stream));
+  Q35_HIP_TRY(ctx, hipMemcpyAsync(out, rt->candidates, static_cast<size_t>(rows) * kMaxCandidates * sizeof(q35_candidate),
+                                  hipMemcpyDeviceToHost, ctx->stream));
+  if (raw_logits != nullptr)
+    Q35_HIP_TRY(ctx, hipMemcpyAsync(raw_logits, rt->logits, static_cast<size_t>(rows) * d.vocab * 4,
+                                    hipMemcpyDeviceToHost, ctx->stream));
+  Q35_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  rt->last_batch = rows;
+  return Q35_OK;
+}
+
+}  // namespace
+
+extern "C" int q35_runtime_step_candidates(q35_runtime *rt, const q35_step_desc *desc,
+                                           const q35_row_sampling *sampling, q35_candidate *out_candidates,
+                                           float *raw_logits) {
+  if (rt == nullptr || desc == nullptr || out_candidates == nullptr) return Q35_ERR_INVALID;
+  int st = pack_step(rt, desc);
+  if (st == Q35_OK) st = pack_sampling(rt, desc->batch, sampling);
+  if (st == Q35_OK) st = ensure_logits(rt);
+  if (st == Q35_OK) st = launch_step(rt, desc->batch, true);
+  if (st != Q35_OK) return st;
+  if (rt->profiling) {
+    Q35_HIP_TRY(rt->ctx, hipStreamSynchronize(rt->ctx->stream));
+    if ((st = profile_collect(rt)) != Q35_OK) return st;
+  }
+  return finish_candidates(rt, desc->batch, out_candidates, raw_logits);
+}
+
+extern "C" int q35_runtime_head_candidates(q35_runtime *rt, int32_t slot, const float *hidden, float penalty,
+                                           const q35_row_sampling *sampling, q35_candidate *out_candidates,
+                                           float *raw_logits) {
+  if (rt == nullptr || hidden == nullptr || out_candidates == nullptr) return Q35_ERR_INVALID;
+  if (slot < 0 || slot >= rt->cfg.max_slots || !rt->slot_used[slot])
+    return set_error(rt->ctx, Q35_ERR_INVALID, "head needs an allocated slot");
+  if (!(penalty >= 1.0F)) return set_error(rt->ctx, Q35_ERR_INVALID, "penalty must be >= 1");
+  Context *ctx = rt->ctx;
+  const q35_model_dims &d = rt->model->d;
+  const MetaLayout ml = meta_layout(rt->cfg.max_batch, rt->max_pages_per_row);
+  std::memset(rt->meta_host, 0, rt->meta_bytes);
+  int st = pack_sampling(rt, 1, sampling);
+  if (st == Q35_OK) st = ensure_logits(rt);
+  if (st != Q35_OK) return st;
+  reinterpret_cast<int32_t *>(rt->meta_host + ml.slots)[0] = slot;
+  reinterpret_cast<float *>(rt->meta_host + ml.penalties)[0] = penalty;
+  hipStream_t s = ctx->stream;
+  Q35_HIP_TRY(ctx, hipMemcpyAsync(rt->meta_dev, rt->meta_host, rt->meta_bytes, hipMemcpyHostToDevice, s));
+  Q35_HIP_TRY(ctx, hipMemcpyAsync(rt->hidden_out, hidden, static_cast<size_t>(d.hidden) * 4, hipMemcpyHostToDevice, s));
+  PrepArgs p;
+  p.source = kPrepPlain;
+  p.x = rt->hidden_out;
+  p.x_stride = d.hidden;
+  p.tokens = 1;
+  p.K = d.hidden;
+  p.h128 = false;
+  p.seed = d.sign_seed;
+  p.codes = rt->codes;
+  p.scales = rt->scales;
+  Q35_HIP_TRY(ctx, launch_prep(p, s));
+  GemmArgs g;
+  g.w = rt->model->embed;
+  g.rows = d.vocab;
+  g.nb = d.hidden / 32;
+  g.codes = rt->codes;
+  g.scales = rt->scales;
+  g.tokens = 1;
+  g.out = rt->logits;
+  g.stride = d.vocab;
+  g.head = true;
+  g.force_split = 1;
+  g.cu_count = ctx->cu_count;
+  Q35_HIP_TRY(ctx, launch_gemm(g, s));
+  return finish_candidates(rt, 1, out_candidates, raw_logits);
+}
+
+extern "C" int q35_slot_counts(q35_runtime *rt, int32_t slot, int32_t *out, size_t count) {
+  if (rt == nullptr || out == nullptr) return Q35_ERR_INVALID;
+  if (slot < 0 || slot >= rt->cfg.max_slots || !rt->slot_used[slot] || count < static_cast<size_t>(rt->model->d.vocab))
+    return set_error(rt->ctx, Q35_ERR_INVALID, "counts need an allocated slot and vocab entries");
+  Q35_HIP_TRY(rt->ctx, hipMemcpy(out, rt->counts + static_cast<size_t>(slot) * rt->model->d.vocab,
+                                 static_cast<size_t>(rt->model->d.vocab) * 4, hipMemcpyDeviceToHost));
   return Q35_OK;
 }
 
