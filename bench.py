@@ -239,6 +239,157 @@ def run_prefix0p8b(args, q, ctx):
     }
 
 
+def run_kernels(args, q, ctx):
+    """Configs 1-3 at kernel level, each entry point called on its own
+    (median of HIP-event brackets around single calls, so a figure is the
+    call's kernels plus their launch gaps; pure kernel durations come from
+    rocprofv3). Beside each, the reference's own kernel (oracle/_ref, one host
+    thread) on the same inputs. Algorithmic bytes as in the reference's
+    q4_dot4 / delta_net / full_attention tests' shapes:
+      config 1: W 3584 x 1024 DOT4 (2,064,384 B), 512 distinct copies rotated,
+                X1 (B=1) and X4 (B=16) activations, fp32 outputs;
+      config 2: DeltaNet B=16 x 16 heads x 128 x 128 fp32 state read + written;
+      config 3: paged GQA attention B=16, contexts ~U[64, 4096], 8/2 heads,
+                head_dim 256, fp16 K/V in shuffled 16-token pages."""
+    sys.path.insert(0, ROOT)
+    from oracle import q35_oracle as orc
+    rng = np.random.default_rng(20261207)
+    res = {}
+
+    def gpu_us(call, reps):
+        times = []
+        for i in range(reps):
+            ctx.synchronize()
+            ctx.timer_begin()
+            call(i)
+            times.append(ctx.timer_end() * 1000.0)
+        return float(np.median(times))
+
+    def cpu_us(call, reps):
+        t = time.perf_counter()
+        for i in range(reps):
+            call(i)
+        return (time.perf_counter() - t) / reps * 1e6
+
+    ref = orc.ref() if orc.ref_available() else None
+    # ---- config 1
+    rows, cols, copies = 3584, 1024, 512
+    nb = cols // 32
+    canon = orc.random_q4_blocks(rng, rows, cols)
+    packed = orc.dot4_pack(canon, rows, nb)
+    wbytes = packed.nbytes
+    dw = ctx.array(shape=(copies * wbytes,), dtype=np.uint8)
+    for c in range(copies):
+        q.lib.q35_memcpy_h2d(ctx.handle, dw.address + c * wbytes, packed.ctypes.data, wbytes)
+    ctx.synchronize()
+    for B in (1, 16):
+        x = rng.standard_normal((B, cols)).astype(np.float32)
+        act = orc.q8_quantize_1(x[0]) if B == 1 else orc.h128_prepare_4(x)
+        da = ctx.array(act)
+        out = ctx.array(shape=(B, rows), dtype=np.float32)
+        if B == 1:
+            call = lambda i: q.lib.q35_q4_dot4_matvec(ctx.handle, dw.address + (i % copies) * wbytes, da.address,
+                                                      out.address, rows, nb)
+        else:
+            call = lambda i: q.lib.q35_q4_dot4_matmul(ctx.handle, dw.address + (i % copies) * wbytes, da.address,
+                                                      out.address, rows, B, nb, rows)
+        us = gpu_us(call, copies)
+        nbytes = wbytes + B * cols * 4 + B * rows * 4
+        entry = {"gpu_us_per_call": round(us, 2), "algorithmic_bytes": nbytes,
+                 "gpu_GBps": round(nbytes / us / 1e3, 1)}
+        if ref is not None:
+            ho = np.empty((B, rows), np.float32)
+            if B == 1:
+                c_us = cpu_us(lambda i: ref.ref_q4_dot4_matvec(packed.ctypes.data, act.ctypes.data, ho.ctypes.data,
+                                                               rows, nb, 0), 200)
+            else:
+                c_us = cpu_us(lambda i: ref.ref_q4_dot4_matmul(packed.ctypes.data, act.ctypes.data, ho.ctypes.data,
+                                                               rows, B, nb, rows, 0), 100)
+            entry["cpu_us_per_call_1thread"] = round(c_us, 1)
+        res[f"config1_B{B}"] = entry
+        log(f"config 1 B={B}: {entry}")
+    dw.free()
+    # ---- config 2 (one step; chained steps repeat it on the updated state)
+    B, H, D = 16, 16, 128
+    state = (rng.standard_normal((B, H, D, D)) * 0.02).astype(np.float32)
+    ds = ctx.array(state)
+    ptrs = ctx.array(np.array([ds.address + b * H * D * D * 4 for b in range(B)], np.uint64))
+
+    def l2n(a):
+        return (a / np.linalg.norm(a, axis=-1, keepdims=True)).astype(np.float32)
+
+    qq = l2n(rng.standard_normal((B, H, D)))
+    kk = l2n(rng.standard_normal((B, H, D)))
+    vv = rng.standard_normal((B, H, D)).astype(np.float32)
+    be = (1 / (1 + np.exp(-rng.standard_normal((B, H))))).astype(np.float32)
+    al = np.exp(-np.log1p(np.exp(rng.standard_normal((B, H))))).astype(np.float32)
+    bufs = [ctx.array(a) for a in (qq, kk, vv, al, be)]
+    out = ctx.array(shape=(B, H, D), dtype=np.float32)
+    us = gpu_us(lambda i: q.gated_delta_net_update_batch(ctx, ptrs, *bufs, out, B, H, D, D), 64)
+    nbytes = 2 * B * H * D * D * 4 + 4 * B * H * D * 4 + 2 * B * H * 4
+    entry = {"gpu_us_per_step": round(us, 2), "algorithmic_bytes": nbytes, "gpu_GBps": round(nbytes / us / 1e3, 1)}
+    if ref is not None:
+        hs, ho = state.copy(), np.empty((B, H, D), np.float32)
+
+        def one(i):
+            for b in range(B):
+                ref.ref_gated_delta_net_update_rows(hs[b].ctypes.data, qq[b].ctypes.data, kk[b].ctypes.data,
+                                                    vv[b].ctypes.data, al[b].ctypes.data, be[b].ctypes.data,
+                                                    ho[b].ctypes.data, H, D, D, 0, H * D, 0)
+        entry["cpu_us_per_step_1thread"] = round(cpu_us(one, 5), 1)
+    res["config2_B16"] = entry
+    log(f"config 2: {entry}")
+    # ---- config 3
+    heads, kvh, hd, pt = 8, 2, 256, 16
+    lens = rng.integers(64, 4097, size=16).astype(np.int32)
+    pages = [(n + pt - 1) // pt for n in lens]
+    perm = rng.permutation(sum(pages)).astype(np.int32)
+    table = np.zeros((16, max(pages)), np.int32)
+    o = 0
+    for b in range(16):
+        table[b, :pages[b]] = perm[o:o + pages[b]]
+        o += pages[b]
+    kp = rng.standard_normal((sum(pages), pt, kvh * hd)).astype(np.float16).view(np.uint16)
+    vp = rng.standard_normal((sum(pages), pt, kvh * hd)).astype(np.float16).view(np.uint16)
+    qv = rng.standard_normal((16, heads * hd)).astype(np.float32)
+    gates = rng.standard_normal((16, heads * hd)).astype(np.float32)
+    dq, dg, dk, dv, dt, dl = (ctx.array(a) for a in (qv, gates, kp, vp, table, lens))
+    out = ctx.array(shape=(16, heads * hd), dtype=np.float32)
+    us = gpu_us(lambda i: q.attention_decode_paged(ctx, dq, dg, dk, dv, dt, table.shape[1], dl, pt, out, 16, heads,
+                                                   kvh, hd, 1.0 / 16.0), 64)
+    nbytes = int(lens.sum()) * kvh * hd * 2 * 2 + 16 * heads * hd * 4 * 3
+    entry = {"gpu_us_per_call": round(us, 2), "context_sum": int(lens.sum()), "algorithmic_bytes": nbytes,
+             "gpu_GBps": round(nbytes / us / 1e3, 1)}
+    if ref is not None:
+        ho = np.empty((16, heads * hd), np.float32)
+        scores = np.empty(int(lens.max()) * heads, np.float32)
+        krows, vrows = [], []
+        for b in range(16):
+            kr = (ctypes.c_void_p * int(lens[b]))(*[kp[table[b, t // pt], t % pt].ctypes.data for t in range(lens[b])])
+            vr = (ctypes.c_void_p * int(lens[b]))(*[vp[table[b, t // pt], t % pt].ctypes.data for t in range(lens[b])])
+            krows.append(kr)
+            vrows.append(vr)
+
+        def one(i):
+            for b in range(16):
+                ref.ref_causal_attention_decode_gqa_pairs(qv[b].ctypes.data, gates[b].ctypes.data,
+                                                          ctypes.addressof(krows[b]), ctypes.addressof(vrows[b]),
+                                                          scores.ctypes.data, ho[b].ctypes.data, int(lens.max()),
+                                                          heads * hd, kvh * hd, int(lens[b]), heads, kvh, hd,
+                                                          1.0 / 16.0, 0, heads // 2, 0)
+        entry["cpu_us_per_call_1thread"] = round(cpu_us(one, 3), 1)
+    res["config3_B16"] = entry
+    log(f"config 3: {entry}")
+    return {
+        "metric": "kernel-level configs 1-3: per-call GPU latency and algorithmic HBM GB/s (1 GPU)",
+        "value": res["config1_B16"]["gpu_GBps"], "unit": "GB/s (config 1, B=16)", "n_gpus": 1, "steps": 1,
+        "warmup": 0, "ms_per_step": round(res["config1_B16"]["gpu_us_per_call"] / 1000, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4xi8->i32 (config 1), f32 (configs 2, 3)", "data": "synthetic, seeded",
+        "config": {"workload": "kernel-level configs 1-3", **res}, "roofline": None, "cpu_baseline": None,
+    }
+
+
 def roofline(name, stats, traffic, kernel=None):
     """Achieved HBM rate of one kernel class: algorithmic bytes per launch over
     the average launch duration (HIP events around each launch on the
@@ -274,7 +425,7 @@ def main():
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--calibration-copy-mb", type=int, default=0,
                     help="issue one device-to-device copy of this many MiB (a known-size kernel for HBM counters)")
-    ap.add_argument("--workload", choices=("decode0p8b", "mixed4b", "prefix0p8b"), default="decode0p8b",
+    ap.add_argument("--workload", choices=("decode0p8b", "mixed4b", "prefix0p8b", "kernels"), default="decode0p8b",
                     help="decode0p8b: the headline metric (config 4); mixed4b: config 5; "
                          "prefix0p8b: prefill with a prefix-cache hit")
     ap.add_argument("--graphs", choices=("on", "off"), default="on",
@@ -296,7 +447,8 @@ def main():
     cu, arch = ctx.device_info()
     log(f"device {arch}, {cu} CUs")
     if args.workload != "decode0p8b":
-        line = run_mixed4b(args, q, ctx) if args.workload == "mixed4b" else run_prefix0p8b(args, q, ctx)
+        runs = {"mixed4b": run_mixed4b, "prefix0p8b": run_prefix0p8b, "kernels": run_kernels}
+        line = runs[args.workload](args, q, ctx)
         ctx.close()
         print(json.dumps(line), flush=True)
         return
