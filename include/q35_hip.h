@@ -182,7 +182,13 @@ typedef struct {
 } q35_model_dims;
 
 /* Tensor encodings of the Q35H128 artifact (include/qwen35x/weights/q4_h128_artifact.h:13-29). */
-enum { Q35_ENC_F32 = 0, Q35_ENC_Q4_0_DOT4 = 5, Q35_ENC_Q4_H128_DOT4 = 6 };
+enum {
+  Q35_ENC_F32 = 0,
+  Q35_ENC_Q4_0_DOT4 = 5,
+  Q35_ENC_Q4_H128_DOT4 = 6,
+  Q35_ENC_Q8_0 = 7,          /* row-major Q8_0Block: Q8 gate rows (linear_attn.in_proj_ba) */
+  Q35_ENC_Q4_G16_DOT4 = 8    /* Q4G16Tile, identity basis: the tied embedding / head */
+};
 
 typedef struct q35_model q35_model;
 

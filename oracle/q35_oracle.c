@@ -512,6 +512,50 @@ void q35o_rope_tables(float theta, int rope_dim, size_t positions, float *cosine
   free(inv);
 }
 
+static int g16_code(const q35o_g16 *t, int row, int i) {
+  return ((t->qs[32 * (i / 8) + 4 * row + i % 4] >> (i % 8 < 4 ? 0 : 4)) & 15) - 8;
+}
+
+void q35o_g16_dequantize_row(const q35o_g16 *m, size_t row, float *out, size_t blocks) {
+  for (size_t b = 0; b < blocks; ++b) {
+    const q35o_g16 *t = &m[(row / 8) * blocks + b];
+    for (int i = 0; i < 32; ++i)
+      out[b * 32 + i] = q35o_half_to_float(t->d[i / 16][row % 8]) * (float)g16_code(t, (int)(row % 8), i);
+  }
+}
+
+void q35o_g16_matmul(const q35o_g16 *m, const q35o_q8x1 *v, float *out, size_t rows, size_t count,
+                     size_t blocks, size_t stride) {
+  for (size_t t = 0; t < count; ++t)
+    for (size_t r = 0; r < rows; ++r) {
+      float acc = 0.0f;
+      for (size_t b = 0; b < blocks; ++b) {
+        const q35o_g16 *tile = &m[(r / 8) * blocks + b];
+        const q35o_q8x1 *a = &v[t * blocks + b];
+        for (int half = 0; half < 2; ++half) {
+          int32_t dot = 0;
+          for (int i = 16 * half; i < 16 * half + 16; ++i) dot += g16_code(tile, (int)(r % 8), i) * a->qs[i];
+          acc = fmaf((float)dot, q35o_half_to_float(tile->d[half][r % 8]) * a->scales[0], acc);
+        }
+      }
+      out[t * stride + r] = acc;
+    }
+}
+
+void q35o_q8_matmul(const q35o_q8_0 *m, const float *mscales, const q35o_q8x1 *v, float *out, size_t rows,
+                    size_t count, size_t blocks, size_t stride) {
+  for (size_t t = 0; t < count; ++t)
+    for (size_t r = 0; r < rows; ++r) {
+      float acc = 0.0f;
+      for (size_t b = 0; b < blocks; ++b) {
+        int32_t dot = 0;
+        for (int i = 0; i < 32; ++i) dot += (int32_t)m[r * blocks + b].qs[i] * v[t * blocks + b].qs[i];
+        acc = fmaf((float)dot, mscales[r * blocks + b] * v[t * blocks + b].scales[0], acc);
+      }
+      out[t * stride + r] = acc;
+    }
+}
+
 /* One projection row: matmul_2d_quantized_batch (weights.inl:1297-1502) per
  * row is prepare (H128 or identity) then the DOT4 fma chain. */
 static void project_row(const q35o_q4x8 *w, size_t rows, size_t cols, const float *x, int h128,
@@ -636,13 +680,23 @@ int q35o_forward_batch(const q35o_dims *d, const q35o_weights *w, q35o_state *co
   if (ok) q35o_rope_tables(d->rope_theta, d->rope_dim, max_pos, cosine, sine);
   for (size_t r = 0; ok && r < batch; ++r) {
     q35o_state *s = states[r];
-    q35o_dot4_dequantize_row(w->embed, (size_t)tokens[r], x, H / 32);
+    if (w->embed_g16)
+      q35o_g16_dequantize_row(w->embed_g16, (size_t)tokens[r], x, H / 32);
+    else
+      q35o_dot4_dequantize_row(w->embed, (size_t)tokens[r], x, H / 32);
     size_t li = 0, fi = 0;
     for (int l = 0; l < d->n_layers; ++l) {
       const q35o_layer *L = &w->layers[l];
       q35o_rms_norm(x, L->input_norm, normed, 1, H, d->rms_eps, 1.0f);
       if (L->is_linear) {
-        project_row(L->in_proj, lin_in, H, normed, 1, d->sign_seed, proj, prep);
+        /* a Q8 gate tail: the Q4 rows, then the gate rows from the
+         * identity-basis input (run_q8_gate_tail, weights.inl:1015-1034) */
+        project_row(L->in_proj, lin_in - (size_t)L->gate_rows, H, normed, 1, d->sign_seed, proj, prep);
+        if (L->gate_rows > 0) {
+          q35o_q8_quantize_vector_1(normed, prep, H / 32);
+          q35o_q8_matmul(L->gate_q8, L->gate_scales, prep, proj + lin_in - (size_t)L->gate_rows,
+                         (size_t)L->gate_rows, 1, H / 32, 0);
+        }
         linear_step(d, L, s->conv_state[li], &s->conv_ring[li], s->recurrent[li], proj, core, tmp);
         project_row(L->out_proj, H, v_dim, core, 1, d->sign_seed, hbuf, prep);
         ++li;
@@ -662,7 +716,13 @@ int q35o_forward_batch(const q35o_dims *d, const q35o_weights *w, q35o_state *co
     }
     q35o_rms_norm(x, w->final_norm, normed, 1, H, d->rms_eps, 1.0f);
     if (out_hidden) memcpy(out_hidden + r * H, normed, H * sizeof(float));
-    project_row(w->embed, V, H, normed, 0, 0, logits, prep);
+    if (w->embed_g16) {
+      /* g16_matmul (gguf_matrix.inl:105-138): identity-basis X1 activations */
+      q35o_q8_quantize_vector_1(normed, prep, H / 32);
+      q35o_g16_matmul(w->embed_g16, prep, logits, V, 1, H / 32, V);
+    } else {
+      project_row(w->embed, V, H, normed, 0, 0, logits, prep);
+    }
     if (out_logits) memcpy(out_logits + r * V, logits, V * sizeof(float));
     /* cpu_engine_greedy.inl:45-57 and :115-124: penalty, lowest index on ties */
     float best = -INFINITY;

@@ -18,6 +18,11 @@ typedef struct { uint16_t d[8]; uint8_t qs[128]; } q35o_q4x8;          /* 144 B 
 typedef struct { float scales[4]; int16_t sums[4]; int8_t qs[128]; } q35o_q8x4; /* 152 B */
 typedef struct { float scales[1]; int16_t sums[1]; int8_t qs[32]; int16_t pad; } q35o_q8x1; /* 40 B */
 typedef struct { uint16_t d; uint8_t qs[16]; } q35o_q4_0;              /* 18 B */
+/* Q4G16Tile (q4_g16.h:5-6): per 8-row x 32-column tile, binary16 scales
+ * d[half][row] for columns 0-15 and 16-31, then the DOT4 code bytes */
+typedef struct { uint16_t d[2][8]; uint8_t qs[128]; } q35o_g16;         /* 160 B */
+/* Q8_0Block (q4_0.h:13-16): binary16 scale, 32 signed codes */
+typedef struct { uint16_t d; int8_t qs[32]; } q35o_q8_0;                /* 34 B */
 
 uint16_t q35o_float_to_half(float value);
 float q35o_half_to_float(uint16_t value);
@@ -48,6 +53,18 @@ void q35o_dot4_matmul(const q35o_q4x8 *m, const q35o_q8x4 *v, float *out, size_t
 void q35o_dot4_argmax(const q35o_q4x8 *m, const q35o_q8x1 *v, const int *counts, float penalty,
                       size_t offset, size_t rows, size_t blocks, float *value, size_t *index);
 
+/* q4_g16.cpp:98-103 */
+void q35o_g16_dequantize_row(const q35o_g16 *m, size_t row, float *out, size_t blocks);
+/* q4_g16_matmul_wide (q4_g16_evex.cpp:25-49) and q4_g16_matvec_avx2: per
+ * block, half 0 then half 1, acc = fma(float(dot_half), half(d) * s, acc);
+ * out[t * stride + r] for `count` X1 activation rows */
+void q35o_g16_matmul(const q35o_g16 *m, const q35o_q8x1 *v, float *out, size_t rows, size_t count,
+                     size_t blocks, size_t stride);
+/* q8_0_matmul with matrix scales (q8_0.cpp:160-193, the VNNI path's fma
+ * chain): out[t * stride + r] = chain over blocks of fma(float(dot),
+ * mscale * vscale, acc) */
+void q35o_q8_matmul(const q35o_q8_0 *m, const float *mscales, const q35o_q8x1 *v, float *out, size_t rows,
+                    size_t count, size_t blocks, size_t stride);
 void q35o_delta_net_update_rows(float *state, const float *q, const float *k, const float *v,
                                 const float *alpha, const float *beta, float *out, size_t kdim,
                                 size_t vdim, size_t row_begin, size_t row_end);
@@ -88,10 +105,16 @@ typedef struct {
   const float *conv_w;   /* [channels][kernel] as stored (HF layout) */
   const float *lin_norm, *a_log, *dt_bias;
   const float *q_norm, *k_norm;
+  /* optional Q8 gate rows of in_proj_all (weights.inl:1015-1034): the last
+   * gate_rows outputs come from Q8_0 rows over the identity-basis input */
+  int gate_rows;
+  const q35o_q8_0 *gate_q8;
+  const float *gate_scales; /* [gate_rows][hidden / 32] */
 } q35o_layer;
 
 typedef struct {
   const q35o_q4x8 *embed;  /* tied identity-basis head [vocab, hidden] */
+  const q35o_g16 *embed_g16;  /* when set: the head and embedding as G16 tiles */
   const float *final_norm;
   const q35o_layer *layers;
 } q35o_weights;

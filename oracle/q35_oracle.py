@@ -32,7 +32,10 @@ Q4X8 = np.dtype([("d", "<u2", (8,)), ("qs", "u1", (128,))])
 Q8X4 = np.dtype([("scales", "<f4", (4,)), ("sums", "<i2", (4,)), ("qs", "i1", (128,))])
 Q8X1 = np.dtype([("scales", "<f4", (1,)), ("sums", "<i2", (1,)), ("qs", "i1", (32,)), ("pad", "<i2")])
 Q4_0 = np.dtype([("d", "<u2"), ("qs", "u1", (16,))])
+G16 = np.dtype([("d", "<u2", (2, 8)), ("qs", "u1", (128,))])      # q4_g16.h:5-6
+Q8_0 = np.dtype([("d", "<u2"), ("qs", "i1", (32,))])                # q4_0.h:13-16
 assert Q4X8.itemsize == 144 and Q8X4.itemsize == 152 and Q8X1.itemsize == 40 and Q4_0.itemsize == 18
+assert G16.itemsize == 160 and Q8_0.itemsize == 34
 
 P = c_void_p
 for name, res, args in [
@@ -66,6 +69,9 @@ for name, res, args in [
     ("q35o_sigmoid", c_float, [c_float]),
     ("q35o_softplus", c_float, [c_float]),
     ("q35o_rope_tables", None, [c_float, c_int, c_size_t, P, P]),
+    ("q35o_g16_dequantize_row", None, [P, c_size_t, P, c_size_t]),
+    ("q35o_g16_matmul", None, [P, P, P, c_size_t, c_size_t, c_size_t, c_size_t]),
+    ("q35o_q8_matmul", None, [P, P, P, P, c_size_t, c_size_t, c_size_t, c_size_t]),
 ]:
     f = getattr(lib, name)
     f.restype, f.argtypes = res, args
@@ -153,6 +159,69 @@ def q4_quantize(w):
     return out
 
 
+def g16_pack(w):
+    """Fixture packer for Q4G16Tile [rows/8, cols/32] (q4_g16.h:5-6): per row,
+    block and 16-column half an absmax/7 binary16 scale and codes
+    round(x / d) + 8 clamped to 0..15, in the DOT4 nibble order
+    (q4_g16.cpp:31-34). Any such tile is a valid G16 input; the reference's
+    MSE16 quantizer only chooses scales differently."""
+    w = np.asarray(w, np.float32)
+    rows, cols = w.shape
+    nb = cols // 32
+    x = w.reshape(rows, nb, 2, 16)
+    d = (np.abs(x).max(axis=3) / 7.0).astype(np.float16)
+    df = d.astype(np.float32)
+    inv = np.where(df > 0, 1.0 / np.where(df > 0, df, 1), 0.0).astype(np.float32)
+    q = (np.clip(np.round(x * inv[..., None]), -8, 7) + 8).astype(np.uint8).reshape(rows, nb, 32)
+    out = np.zeros((rows // 8, nb), G16)
+    dd = d.view(np.uint16).reshape(rows // 8, 8, nb, 2)
+    out["d"] = dd.transpose(0, 2, 3, 1)
+    i = np.arange(32)
+    byte = 32 * (i // 8) + (i % 4)   # + 4 * row
+    shift = np.where(i % 8 < 4, 0, 4)
+    qs = np.zeros((rows // 8, nb, 128), np.uint16)
+    qr = q.reshape(rows // 8, 8, nb, 32)
+    for r in range(8):
+        for k in range(32):
+            qs[:, :, byte[k] + 4 * r] |= (qr[:, r, :, k].astype(np.uint16) << np.uint16(shift[k])).astype(np.uint16)
+    out["qs"] = qs.astype(np.uint8)
+    return out
+
+
+def g16_dequantize_row(tiles, row, blocks):
+    out = np.zeros(blocks * 32, np.float32)
+    lib.q35o_g16_dequantize_row(ptr(tiles), row, ptr(out), blocks)
+    return out
+
+
+def g16_matmul(tiles, act1, rows, count, blocks, stride=None):
+    """act1: X1 blocks [count * blocks] -> float32 [count, stride]."""
+    stride = stride or rows
+    out = np.zeros((count, stride), np.float32)
+    lib.q35o_g16_matmul(ptr(tiles), ptr(act1), ptr(out), rows, count, blocks, stride)
+    return out
+
+
+def q8_rows_pack(w):
+    """Row-major Q8_0 blocks [rows, cols/32] (q8_0_quantize, q8_0.cpp:86-110,
+    the same rounding as q8_0_quantize_vector_1) and their F32 scales
+    (q8_0_scales_to_f32, as the loader keeps them, weights.inl:741-742)."""
+    w = np.ascontiguousarray(w, np.float32)
+    rows, cols = w.shape
+    x1 = q8_quantize_1(w.reshape(-1)).reshape(rows, cols // 32)
+    out = np.zeros((rows, cols // 32), Q8_0)
+    out["qs"] = x1["qs"]
+    out["d"] = x1["scales"][..., 0].astype(np.float16).view(np.uint16)
+    return out, np.ascontiguousarray(x1["scales"][..., 0], np.float32)
+
+
+def q8_matmul(blocks8, mscales, act1, rows, count, blocks, stride=None):
+    stride = stride or rows
+    out = np.zeros((count, stride), np.float32)
+    lib.q35o_q8_matmul(ptr(blocks8), ptr(mscales), ptr(act1), ptr(out), rows, count, blocks, stride)
+    return out
+
+
 def dot4_matvec(packed, act1, rows, blocks):
     out = np.zeros(rows, np.float32)
     lib.q35o_dot4_matvec(ptr(packed), ptr(act1), ptr(out), rows, blocks)
@@ -235,11 +304,12 @@ class Dims(ctypes.Structure):
 class Layer(ctypes.Structure):
     _fields_ = [("is_linear", c_int), ("in_proj", P), ("out_proj", P), ("gate_up", P), ("down", P),
                 ("input_norm", P), ("post_norm", P), ("conv_w", P), ("lin_norm", P), ("a_log", P),
-                ("dt_bias", P), ("q_norm", P), ("k_norm", P)]
+                ("dt_bias", P), ("q_norm", P), ("k_norm", P), ("gate_rows", c_int), ("gate_q8", P),
+                ("gate_scales", P)]
 
 
 class Weights(ctypes.Structure):
-    _fields_ = [("embed", P), ("final_norm", P), ("layers", POINTER(Layer))]
+    _fields_ = [("embed", P), ("embed_g16", P), ("final_norm", P), ("layers", POINTER(Layer))]
 
 
 class State(ctypes.Structure):
@@ -287,11 +357,19 @@ class OracleModel:
                 L.in_proj, L.out_proj = get(p + "linear_attn.in_proj_all.weight"), get(p + "linear_attn.out_proj.weight")
                 L.conv_w, L.lin_norm = get(p + "linear_attn.conv1d.weight"), get(p + "linear_attn.norm.weight")
                 L.a_log, L.dt_bias = get(p + "linear_attn.A_log"), get(p + "linear_attn.dt_bias")
+                ba = p + "linear_attn.in_proj_ba.weight"
+                if ba in t:  # Q8 gate rows (weights.inl:1700-1747)
+                    blocks8 = np.ascontiguousarray(t[ba][2]).view(Q8_0).reshape(-1)
+                    sc = blocks8["d"].view(np.float16).astype(np.float32)
+                    self.keep.append(sc)
+                    L.gate_rows, L.gate_q8, L.gate_scales = int(t[ba][1][0]), get(ba), c_void_p(sc.ctypes.data)
             else:
                 L.in_proj, L.out_proj = get(p + "self_attn.qkv_proj.weight"), get(p + "self_attn.o_proj.weight")
                 L.q_norm, L.k_norm = get(p + "self_attn.q_norm.weight"), get(p + "self_attn.k_norm.weight")
-        self.w = Weights(get("model.language_model.embed_tokens.weight"), get("model.language_model.norm.weight"),
-                         self.layers)
+        emb = "model.language_model.embed_tokens.weight"
+        g16 = t[emb][0] == 8  # q4_g16_cpu_dot4
+        self.w = Weights(None if g16 else get(emb), get(emb) if g16 else None,
+                         get("model.language_model.norm.weight"), self.layers)
 
     def new_state(self, capacity, prompt):
         d = self.d
@@ -373,6 +451,11 @@ def ref():
             "ref_rms_norm_f32": (None, [P, P, P, c_size_t, c_size_t, c_float, c_float, c_int]),
             "ref_l2_normalize_f32": (None, [P, c_size_t, c_size_t, c_float, c_float, c_int]),
             "ref_silu_mul_f32": (None, [P, P, P, c_size_t, c_int]),
+            "ref_q4_g16_dequantize_row": (None, [P, c_size_t, P, c_size_t]),
+            "ref_q4_g16_matvec": (None, [P, P, P, c_size_t, c_size_t, c_int]),
+            "ref_q4_g16_pack_activations": (None, [P, P, c_size_t, c_size_t]),
+            "ref_q4_g16_matmul": (None, [P, P, P, c_size_t, c_size_t, c_size_t, c_size_t, c_int]),
+            "ref_q8_0_matmul": (None, [P, P, P, c_size_t, c_size_t, c_size_t, c_size_t, c_int, P]),
             "ref_engine_set_probe": (None, [P, c_size_t, P]),
             "ref_engine_sample": (c_int, [ctypes.c_char_p, ctypes.c_char_p, c_int, P, c_size_t, c_size_t, c_float,
                                           c_float, c_int, c_float, ctypes.c_int64, P, P, c_size_t, ctypes.c_char_p,

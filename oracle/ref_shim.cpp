@@ -12,6 +12,7 @@
 #include "qwen35x/cpu/full_attention.h"
 #include "qwen35x/cpu/q4_0.h"
 #include "qwen35x/cpu/q4_dot4.h"
+#include "qwen35x/cpu/q4_g16.h"
 #include "qwen35x/cpu/q4_h128.h"
 #include "qwen35x/cpu/q8_0.h"
 #include "qwen35x/compiler/compiler.h"
@@ -73,6 +74,29 @@ int ref_q4_h128_quantize_matrix(const float *x, void *out, std::size_t rows, std
 // q4_h128.h:66-70
 void ref_q4_h128_quantize_transformed(const float *x, void *out, std::size_t blocks) {
   q4_h128_quantize_transformed(x, static_cast<Q4_0Block *>(out), blocks);
+}
+
+// q4_g16.h:10-25
+void ref_q4_g16_dequantize_row(const void *w, std::size_t row, float *out, std::size_t blocks) {
+  q4_g16_dequantize_row(static_cast<const Q4G16Tile *>(w), row, out, blocks);
+}
+void ref_q4_g16_matvec(const void *w, const void *a, float *out, std::size_t rows, std::size_t blocks, int b) {
+  q4_g16_matvec(static_cast<const Q4G16Tile *>(w), static_cast<const Q8_0BlockX1 *>(a), out, rows, blocks, be(b));
+}
+void ref_q4_g16_pack_activations(const void *a, void *out, std::size_t count, std::size_t blocks) {
+  q4_g16_pack_activations(static_cast<const Q8_0BlockX1 *>(a), static_cast<Q4G16ActivationTile *>(out), count,
+                          blocks);
+}
+void ref_q4_g16_matmul(const void *w, const void *a, float *out, std::size_t rows, std::size_t count,
+                       std::size_t blocks, std::size_t stride, int b) {
+  q4_g16_matmul(static_cast<const Q4G16Tile *>(w), static_cast<const Q4G16ActivationTile *>(a), out, rows, count,
+                blocks, stride, be(b));
+}
+// q8_0.h:115-125, matrix scales as run_q8_gate_tail passes them (weights.inl:1030-1032)
+void ref_q8_0_matmul(const void *m, const void *v, float *out, std::size_t rows, std::size_t count,
+                     std::size_t blocks, std::size_t stride, int b, const float *mscales) {
+  q8_0_matmul(static_cast<const Q8_0Block *>(m), static_cast<const Q8_0Block *>(v), out, rows, count, blocks, stride,
+              be(b), nullptr, mscales);
 }
 
 // q4_dot4.h:7-21

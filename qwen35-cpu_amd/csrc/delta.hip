@@ -101,8 +101,10 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
     a.proj.template load<MS>(r, chq, xq_s);
     a.proj.template load<MS>(r, chv, xv_s);
     a.proj.template load8<MS>(r, channels + vh * kDim + 8 * (lane & 15), z_s);
-    a.proj.template load<MS>(r, channels + v_dim + vh, b_s);
-    a.proj.template load<MS>(r, channels + v_dim + a.v_heads + vh, a_s);
+    // with separate gate rows the projection row is [qkv | z] only
+    const bool sep = a.gates != nullptr;
+    a.proj.template load<MS>(r, sep ? chq : channels + v_dim + vh, b_s);
+    a.proj.template load<MS>(r, sep ? chq : channels + v_dim + a.v_heads + vh, a_s);
     float hq[K - 1], hv[K - 1], wq[K], wv[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -124,8 +126,9 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
     const float xq = a.proj.template reduce<MS>(xq_s);
     const float xv = a.proj.template reduce<MS>(xv_s);
     a.proj.template reduce8<MS>(z_s, z);
-    const float bval = a.proj.template reduce<MS>(b_s);
-    const float aval = a.proj.template reduce<MS>(a_s);
+    const float bval = sep ? a.gates[static_cast<size_t>(r) * 2 * a.v_heads + vh] : a.proj.template reduce<MS>(b_s);
+    const float aval =
+        sep ? a.gates[static_cast<size_t>(r) * 2 * a.v_heads + a.v_heads + vh] : a.proj.template reduce<MS>(a_s);
     // causal conv1d + SiLU (activation.cpp:164-222: x * w[K-1] first, then
     // the history oldest first)
     float yq = xq * wq[K - 1], yv = xv * wv[K - 1];
@@ -303,8 +306,9 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_chunk_inputs_kernel(Delta
   const int chv = has_v ? 2 * q_dim + vh * kDim + tid : chq;
   const float *row = a.proj.p + static_cast<long long>(r) * a.proj.width;
   const float xq = row[chq], xv = row[chv];
-  const float bval = row[channels + v_dim + vh];
-  const float aval = row[channels + v_dim + a.v_heads + vh];
+  const float bval = a.gates != nullptr ? a.gates[static_cast<size_t>(r) * 2 * a.v_heads + vh] : row[channels + v_dim + vh];
+  const float aval = a.gates != nullptr ? a.gates[static_cast<size_t>(r) * 2 * a.v_heads + a.v_heads + vh]
+                                        : row[channels + v_dim + a.v_heads + vh];
   float hq[K - 1], hv[K - 1], wq[K], wv[K];
 #pragma unroll
   for (int k = 0; k < K; ++k) {

@@ -403,13 +403,19 @@ constexpr size_t kHeadMaxLds = 64 * 1024;
 // accumulators of more token tiles need more registers
 constexpr int head_waves_per_simd(int nt) { return nt == 1 ? 3 : 2; }
 
-template <int KS>
+template <int KS, bool G16>
 struct HeadChunk {
   q35_u32x4 q[KS];
   q35_u32x2 d[KS];
+  q35_u32x2 d2[G16 ? KS : 1];  // G16: the scales of columns 16-31
 };
 
-template <int KS, int R, int NT, bool ARGMAX, int OCC>
+// G16: Q4G16Tile weights (q4_g16.h:5-6, 160-byte tiles: d[2][8] then the
+// DOT4 codes). Each block's two 16-column halves are separate int8 dots:
+// MFMAs over the activations with the other half's K lanes zeroed, chained
+// per block as half 0 then half 1, acc = fma(float(dot), d_half * s, acc)
+// (q4_g16_matmul_wide, q4_g16_evex.cpp:25-49).
+template <int KS, int R, int NT, bool ARGMAX, int OCC, bool G16>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void head_kernel(GemmArgs a,
                                                                                                int gpw) {
   static_assert(R >= 2, "the ring loads the next chunk before computing the current one");
@@ -424,12 +430,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
   const int cpg = (nb + KS - 1) / KS;
   const int iters = (g1 - g0) * cpg;
   const uint8_t *wbase = reinterpret_cast<const uint8_t *>(a.w);
-  const size_t tile_bytes = static_cast<size_t>(nb) * 144;
+  constexpr int kTile = G16 ? 160 : 144, kCodes = G16 ? 32 : 16;
+  const size_t tile_bytes = static_cast<size_t>(nb) * kTile;
 
   // next chunk to load: group lg, chunk lch (advanced after every load);
   // past the last chunk the last one is loaded again
   int lg = g0, lch = 0;
-  auto load = [&](HeadChunk<KS> &buf) {
+  auto load = [&](HeadChunk<KS, G16> &buf) {
     const bool past = lg >= g1;
     const int gl = max(past ? g1 - 1 : lg, 0), cl = past ? cpg - 1 : lch;
     const int rt = min(gl * 8 + T, ntiles - 1);
@@ -437,8 +444,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
 #pragma unroll
     for (int i = 0; i < KS; ++i) {
       const size_t b = static_cast<size_t>(min(cl * KS + i, nb - 1));
-      buf.q[i] = *reinterpret_cast<const q35_u32x4 *>(tile + b * 144 + 16 + 16 * (2 * G + h));
-      buf.d[i] = *reinterpret_cast<const q35_u32x2 *>(tile + b * 144 + 8 * h);
+      buf.q[i] = *reinterpret_cast<const q35_u32x4 *>(tile + b * kTile + kCodes + 16 * (2 * G + h));
+      buf.d[i] = *reinterpret_cast<const q35_u32x2 *>(tile + b * kTile + 8 * h);
+      if constexpr (G16) buf.d2[i] = *reinterpret_cast<const q35_u32x2 *>(tile + b * kTile + 16 + 8 * h);
     }
     if (++lch == cpg) {
       lch = 0;
@@ -459,7 +467,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
       crow[t][j] = ARGMAX && a.count_rows != nullptr ? a.count_rows[tok] : tok;
     }
 
-  HeadChunk<KS> buf[R];
+  HeadChunk<KS, G16> buf[R];
   load(buf[0]);
   // stage the activations; the first pass is issued before chunks 1..R-2, so
   // waiting for it leaves those chunks in flight
@@ -547,13 +555,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
         for (int r = 0; r < 4; ++r) acc[t][r][j] = 0.0F;
       }
   };
-  auto compute = [&](HeadChunk<KS> &cur) {
+  auto compute = [&](HeadChunk<KS, G16> &cur) {
 #pragma unroll
     for (int i = 0; i < KS; ++i) {
       const int b = cch * KS + i;
       // a slot past the last block re-reads it; a zero row scale makes its
       // contribution exactly +0 (acc is never -0)
-      if (b >= nb) cur.d[i] = q35_u32x2{0u, 0u};
+      if (b >= nb) {
+        cur.d[i] = q35_u32x2{0u, 0u};
+        if constexpr (G16) cur.d2[i] = q35_u32x2{0u, 0u};
+      }
       const int bl = min(b, nb - 1);
       const long w0 = unpack_word(cur.q[i][0]), w1 = unpack_word(cur.q[i][1]);
       const long w2 = unpack_word(cur.q[i][2]), w3 = unpack_word(cur.q[i][3]);
@@ -567,16 +578,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
         const q35_f32x4 sa =
             *reinterpret_cast<const q35_f32x4 *>(lscales + (static_cast<size_t>(t) * nb + bl) * 16 + 4 * G);
         const v4i zero = {0, 0, 0, 0};
-        const v4i corr = Q35_MFMA_I32_16X16X32_I8(act, kMinus8, zero, 0, 0, 0);
-        v4i D[4];
-        D[0] = Q35_MFMA_I32_16X16X32_I8(act, w0, corr, 0, 0, 0);
-        D[1] = Q35_MFMA_I32_16X16X32_I8(act, w1, corr, 0, 0, 0);
-        D[2] = Q35_MFMA_I32_16X16X32_I8(act, w2, corr, 0, 0, 0);
-        D[3] = Q35_MFMA_I32_16X16X32_I8(act, w3, corr, 0, 0, 0);
+        if constexpr (G16) {
+          // lanes G = 0, 1 hold columns 0-15 of the block, G = 2, 3 columns 16-31
+          const long lo = G < 2 ? act : 0l, hi = G < 2 ? 0l : act;
+          const float dh[4] = {half_bits_to_float(static_cast<uint16_t>(cur.d2[i][0] & 0xffffu)),
+                               half_bits_to_float(static_cast<uint16_t>(cur.d2[i][0] >> 16)),
+                               half_bits_to_float(static_cast<uint16_t>(cur.d2[i][1] & 0xffffu)),
+                               half_bits_to_float(static_cast<uint16_t>(cur.d2[i][1] >> 16))};
+          const v4i corr_lo = Q35_MFMA_I32_16X16X32_I8(lo, kMinus8, zero, 0, 0, 0);
+          const v4i corr_hi = Q35_MFMA_I32_16X16X32_I8(hi, kMinus8, zero, 0, 0, 0);
+          const long wr[4] = {w0, w1, w2, w3};
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+          for (int r = 0; r < 4; ++r) {
+            const v4i Dl = Q35_MFMA_I32_16X16X32_I8(lo, wr[r], corr_lo, 0, 0, 0);
+            const v4i Dh = Q35_MFMA_I32_16X16X32_I8(hi, wr[r], corr_hi, 0, 0, 0);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[t][r][j] = fmaf(static_cast<float>(D[r][j]), dw[r] * sa[j], acc[t][r][j]);
+            for (int j = 0; j < 4; ++j) {
+              acc[t][r][j] = fmaf(static_cast<float>(Dl[j]), dw[r] * sa[j], acc[t][r][j]);
+              acc[t][r][j] = fmaf(static_cast<float>(Dh[j]), dh[r] * sa[j], acc[t][r][j]);
+            }
+          }
+        } else {
+          const v4i corr = Q35_MFMA_I32_16X16X32_I8(act, kMinus8, zero, 0, 0, 0);
+          v4i D[4];
+          D[0] = Q35_MFMA_I32_16X16X32_I8(act, w0, corr, 0, 0, 0);
+          D[1] = Q35_MFMA_I32_16X16X32_I8(act, w1, corr, 0, 0, 0);
+          D[2] = Q35_MFMA_I32_16X16X32_I8(act, w2, corr, 0, 0, 0);
+          D[3] = Q35_MFMA_I32_16X16X32_I8(act, w3, corr, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              acc[t][r][j] = fmaf(static_cast<float>(D[r][j]), dw[r] * sa[j], acc[t][r][j]);
+        }
       }
     }
     if (++cch == cpg) {
@@ -723,9 +757,19 @@ HeadPlan head_plan(int rows, int nb, int tokens, int cu_count, int force_gpw) {
 }
 }  // namespace
 
-int gemm_argmax_cands(int rows, int nb, int tokens, int cu_count, int force_gpw) {
+// Token tiles whose staged activations fit one head workgroup's LDS.
+int head_fit_tiles(int nb) {
+  int nt = 4;
+  while (nt > 0 && static_cast<size_t>(nt) * nb * (64 * sizeof(uint64_t) + 16 * sizeof(float)) > kHeadMaxLds) --nt;
+  return nt;
+}
+
+int gemm_argmax_cands(int rows, int nb, int tokens, int cu_count, int force_gpw, bool g16) {
   const HeadPlan hp = head_plan(rows, nb, tokens, cu_count, force_gpw);
-  return hp.use ? hp.grid * kHeadWaves : gemm_plan(rows, nb, false, true, cu_count, 0, 0).grid;
+  if (hp.use) return hp.grid * kHeadWaves;
+  // G16: launches of head_fit_tiles token tiles at one plan's grid
+  if (g16) return head_plan(rows, nb, 16 * std::max(1, head_fit_tiles(nb)), cu_count, force_gpw).grid * kHeadWaves;
+  return gemm_plan(rows, nb, false, true, cu_count, 0, 0).grid;
 }
 
 int gemm_argmax_cand_capacity(int rows, int cu_count) {
@@ -742,17 +786,49 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t stream) {
   if (a.tokens <= 0 || a.rows <= 0) return hipSuccess;
   const bool argmax = a.cand != nullptr;
   const bool exact = a.exact || a.block_dots != nullptr;
+  if (a.g16 && (!(argmax || a.head) || exact || (!argmax && a.out == nullptr))) return hipErrorInvalidValue;
   if ((argmax || a.head) && !exact && (argmax || a.out != nullptr)) {
     const HeadPlan hp = head_plan(a.rows, a.nb, a.tokens, a.cu_count, a.force_gpw);
+    if (!hp.use && a.g16) {
+      // G16 has only the staged-activation kernel: launches over groups of
+      // token tiles that fit, all at one grid so that the candidate rows
+      // (argmax) line up with gemm_argmax_cands
+      const int fit = head_fit_tiles(a.nb);
+      if (fit < 1) return hipErrorInvalidValue;
+      const int gpw = head_plan(a.rows, a.nb, 16 * fit, a.cu_count, a.force_gpw).gpw;
+      for (int t0 = 0; t0 < a.tokens; t0 += 16 * fit) {
+        GemmArgs c = a;
+        c.tokens = std::min(16 * fit, a.tokens - t0);
+        c.force_gpw = gpw;
+        c.codes = a.codes + static_cast<size_t>(t0 / 16) * a.nb * 64;
+        c.scales = a.scales + static_cast<size_t>(t0 / 16) * a.nb * 16;
+        if (a.out != nullptr) c.out = a.out + static_cast<size_t>(t0) * a.stride;
+        if (a.cand != nullptr) c.cand = a.cand + t0;
+        if (a.penalties != nullptr) c.penalties = a.penalties + t0;
+        if (a.count_rows != nullptr)
+          c.count_rows = a.count_rows + t0;
+        else if (a.counts != nullptr)
+          c.counts = a.counts + static_cast<long long>(t0) * a.counts_stride;
+        const hipError_t e = launch_gemm(c, stream);
+        if (e != hipSuccess) return e;
+      }
+      return hipSuccess;
+    }
     if (hp.use) {
       const dim3 grid(hp.grid), block(64 * kHeadWaves);
-#define Q35_HEAD(NT)                                                                                       \
-  if (argmax) {                                                                                            \
-    Q35_LAUNCH((head_kernel<kHeadKS, kHeadRing, NT, true, head_waves_per_simd(NT)>), grid, block, hp.smem,  \
-               stream, a, hp.gpw);                                                                         \
-  } else {                                                                                                 \
-    Q35_LAUNCH((head_kernel<kHeadKS, kHeadRing, NT, false, head_waves_per_simd(NT)>), grid, block, hp.smem, \
-               stream, a, hp.gpw);                                                                         \
+#define Q35_HEAD_G(NT, G16)                                                                                     \
+  if (argmax) {                                                                                                 \
+    Q35_LAUNCH((head_kernel<kHeadKS, kHeadRing, NT, true, (G16 ? 2 : head_waves_per_simd(NT)), G16>), grid, block, hp.smem,  \
+               stream, a, hp.gpw);                                                                              \
+  } else {                                                                                                      \
+    Q35_LAUNCH((head_kernel<kHeadKS, kHeadRing, NT, false, (G16 ? 2 : head_waves_per_simd(NT)), G16>), grid, block, hp.smem, \
+               stream, a, hp.gpw);                                                                              \
+  }
+#define Q35_HEAD(NT)         \
+  if (a.g16) {               \
+    Q35_HEAD_G(NT, true)     \
+  } else {                   \
+    Q35_HEAD_G(NT, false)    \
   }
       switch (hp.nt) {
         case 1: Q35_HEAD(1) break;
@@ -761,6 +837,7 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t stream) {
         default: Q35_HEAD(4) break;
       }
 #undef Q35_HEAD
+#undef Q35_HEAD_G
       return hipGetLastError();
     }
   }

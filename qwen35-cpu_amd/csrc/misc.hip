@@ -10,12 +10,20 @@ namespace {
 // (src/runtime/gguf_matrix.inl:21-26, q4_dot4.cpp:31-40): x = half(d[r]) * (u - 8).
 __global__ void embed_kernel(const q35_q4_0_block_x8 *embed, int nb, const int32_t *tokens,
                              float *x, int hidden, int32_t *counts, long long counts_stride,
-                             const int32_t *slots, const uint8_t *count_input) {
+                             const int32_t *slots, const uint8_t *count_input, bool g16) {
   const int r = blockIdx.x;
   const int token = tokens[r];
   const int rt = token >> 3, row = token & 7;
   for (int k = threadIdx.x; k < hidden; k += blockDim.x) {
     const int b = k >> 5, kk = k & 31;
+    if (g16) {
+      // Q4G16Tile: d[half][row] then the DOT4 codes (q4_g16_dequantize_row, q4_g16.cpp:98-103)
+      const uint8_t *tile = reinterpret_cast<const uint8_t *>(embed) + (static_cast<size_t>(rt) * nb + b) * 160;
+      const uint16_t dh = *reinterpret_cast<const uint16_t *>(tile + 2 * (8 * (kk >> 4) + row));
+      const int u = (tile[32 + 32 * (kk >> 3) + 4 * row + (kk & 3)] >> (4 * ((kk & 7) >> 2))) & 15;
+      x[static_cast<size_t>(r) * hidden + k] = half_bits_to_float(dh) * static_cast<float>(u - 8);
+      continue;
+    }
     const q35_q4_0_block_x8 &w = embed[static_cast<size_t>(rt) * nb + b];
     const int u = (w.qs[32 * (kk >> 3) + 4 * row + (kk & 3)] >> (4 * ((kk & 7) >> 2))) & 15;
     x[static_cast<size_t>(r) * hidden + k] = half_bits_to_float(w.d[row]) * static_cast<float>(u - 8);
@@ -88,10 +96,10 @@ __global__ void store_f16_kernel(const float *x, uint16_t *y, long long n) {
 
 hipError_t launch_embed(const q35_q4_0_block_x8 *embed, int nb, const int32_t *tokens, int batch,
                         float *x, int hidden, int32_t *counts, long long counts_stride,
-                        const int32_t *slots, const uint8_t *count_input, hipStream_t stream) {
+                        const int32_t *slots, const uint8_t *count_input, hipStream_t stream, bool g16) {
   if (batch <= 0) return hipSuccess;
   Q35_LAUNCH((embed_kernel), batch, 256, 0, stream, embed, nb, tokens, x, hidden, counts, counts_stride,
-                                          slots, count_input);
+                                          slots, count_input, g16);
   return hipGetLastError();
 }
 

@@ -63,10 +63,18 @@ __global__ __launch_bounds__(kPrepThreads) void prep_kernel(PrepArgs a) {
 constexpr int kRmsThreads = 256;
 constexpr int kRmsMaxK = 4096;
 
-template <int MS>  // bound on the added rows' K splits (0: nothing to add)
+// GATES: the Q8 gate rows of the in projection are computed here as well
+// (run_q8_gate_tail, weights.inl:1015-1034): the normalized row's
+// identity-basis codes go to LDS, each thread takes whole (row, block) int8
+// dots, and one thread per gate row runs the block chain
+// acc = fma(float(dot), mscale * vscale, acc) in block order.
+template <int MS, bool GATES>  // MS: bound on the added rows' K splits (0: nothing to add)
 __global__ __launch_bounds__(kRmsThreads) void rms_prep_kernel(RmsPrepArgs a) {
   __shared__ float y[kRmsMaxK];
   __shared__ float red[kRmsThreads / 64];
+  __shared__ __align__(16) int8_t gq[GATES ? kRmsMaxK : 8];
+  __shared__ float gsc[GATES ? kRmsMaxK / 32 : 1];
+  __shared__ float gdot[GATES ? kMaxGateRows * (kRmsMaxK / 32) : 1];
   const int t = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int K = a.K, n4 = K >> 2;
   const int nblk = K >> 7, j = tid & 15;
@@ -130,7 +138,43 @@ __global__ __launch_bounds__(kRmsThreads) void rms_prep_kernel(RmsPrepArgs a) {
     if (a.normed_out != nullptr && active)
 #pragma unroll
       for (int e = 0; e < 8; ++e) a.normed_out[static_cast<size_t>(t) * K + c0 + e] = v[e];
+    if constexpr (GATES) {
+      uint64_t word;
+      int sum;
+      float stored;
+      q8_block_codes8(v, word, sum, stored);
+      if (active) {
+        *reinterpret_cast<uint64_t *>(&gq[c0]) = word;
+        if ((j & 3) == 0) gsc[c0 >> 5] = stored;
+      }
+    }
     h128_quantize_row16(v, t, blk, K >> 5, a.h128, a.seed, o, active);
+  }
+  if constexpr (GATES) {
+    __syncthreads();
+    const int nb = K >> 5, items = a.gate_rows * nb;
+    for (int i = tid; i < items; i += kRmsThreads) {
+      const int r = i / nb, b = i - r * nb;
+      const q35_u32x4 *wp = reinterpret_cast<const q35_u32x4 *>(a.gate_codes + static_cast<size_t>(r) * K + 32 * b);
+      const q35_u32x4 wa = wp[0], wb = wp[1];
+      const uint32_t *cp = reinterpret_cast<const uint32_t *>(&gq[32 * b]);
+      int dot = 0;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const uint32_t wu = u < 4 ? wa[u] : wb[u - 4], cu = cp[u];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          dot += static_cast<int>(static_cast<int8_t>(wu >> (8 * e))) * static_cast<int>(static_cast<int8_t>(cu >> (8 * e)));
+      }
+      gdot[i] = static_cast<float>(dot);
+    }
+    __syncthreads();
+    for (int r = tid; r < a.gate_rows; r += kRmsThreads) {
+      const float *ms = a.gate_scales + static_cast<size_t>(r) * nb;
+      float acc = 0.0F;
+      for (int b = 0; b < nb; ++b) acc = fmaf(gdot[r * nb + b], ms[b] * gsc[b], acc);
+      a.gates[static_cast<size_t>(t) * a.gate_rows + r] = acc;
+    }
   }
 }
 
@@ -192,16 +236,26 @@ hipError_t launch_prep(const PrepArgs &a, hipStream_t stream) {
 hipError_t launch_rms_prep(const RmsPrepArgs &a, hipStream_t stream) {
   if (a.tokens <= 0) return hipSuccess;
   if (a.K % 128 != 0 || a.K > kRmsMaxK || (a.add.p != nullptr && a.x_out == nullptr)) return hipErrorInvalidValue;
+  const bool gates = a.gate_rows > 0;
+  if (gates && (a.gate_rows > kMaxGateRows || a.gate_codes == nullptr || a.gate_scales == nullptr || a.gates == nullptr))
+    return hipErrorInvalidValue;
   const dim3 grid(a.tokens), block(kRmsThreads);
+#define Q35_RMS(MS)                                                                     \
+  if (gates) {                                                                          \
+    Q35_LAUNCH((rms_prep_kernel<MS, true>), grid, block, 0, stream, a);                 \
+  } else {                                                                              \
+    Q35_LAUNCH((rms_prep_kernel<MS, false>), grid, block, 0, stream, a);                \
+  }
   switch (a.add.p == nullptr ? 0 : split_bound(a.add.splits)) {
-    case 0: Q35_LAUNCH((rms_prep_kernel<0>), grid, block, 0, stream, a); break;
-    case 1: Q35_LAUNCH((rms_prep_kernel<1>), grid, block, 0, stream, a); break;
-    case 4: Q35_LAUNCH((rms_prep_kernel<4>), grid, block, 0, stream, a); break;
-    case 8: Q35_LAUNCH((rms_prep_kernel<8>), grid, block, 0, stream, a); break;
-    case 16: Q35_LAUNCH((rms_prep_kernel<16>), grid, block, 0, stream, a); break;
-    case 32: Q35_LAUNCH((rms_prep_kernel<32>), grid, block, 0, stream, a); break;
+    case 0: Q35_RMS(0) break;
+    case 1: Q35_RMS(1) break;
+    case 4: Q35_RMS(4) break;
+    case 8: Q35_RMS(8) break;
+    case 16: Q35_RMS(16) break;
+    case 32: Q35_RMS(32) break;
     default: return hipErrorInvalidValue;
   }
+#undef Q35_RMS
   return hipGetLastError();
 }
 

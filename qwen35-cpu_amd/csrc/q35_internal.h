@@ -158,7 +158,16 @@ struct RmsPrepArgs {
   uint64_t *codes = nullptr;
   float *scales = nullptr;
   float *normed_out = nullptr;   // optional [tokens][K]
+  // optional Q8 gate rows (run_q8_gate_tail, weights.inl:1015-1034): the
+  // normalized row quantized in the identity basis, then gate_rows Q8 rows
+  // (codes [gate_rows][K], F32 block scales [gate_rows][K/32]) written as
+  // gates[token][gate_rows]
+  const int8_t *gate_codes = nullptr;
+  const float *gate_scales = nullptr;
+  int gate_rows = 0;
+  float *gates = nullptr;
 };
+constexpr int kMaxGateRows = 64;
 hipError_t launch_rms_prep(const RmsPrepArgs &a, hipStream_t stream);
 
 
@@ -195,6 +204,7 @@ struct GemmArgs {
   // with activations staged in LDS; implied by `cand`
   bool head = false;
   int force_gpw = 0;  // head: 64-row groups per wavefront (0 = automatic)
+  bool g16 = false;   // head: `w` holds Q4G16Tile (160-byte) tiles
 };
 // Launch plan of one GEMM: blocks per wavefront chunk, wavefronts per
 // workgroup, K splits across workgroups, workgroups along the rows, LDS bytes.
@@ -208,7 +218,7 @@ GemmPlan gemm_plan(int rows, int nb, bool exact, bool argmax, int cu_count, int 
                    int max_split = 32);
 // Candidate rows per token that the greedy head launch for this shape writes
 // (and argmax_finalize must read).
-int gemm_argmax_cands(int rows, int nb, int tokens, int cu_count, int force_gpw = 0);
+int gemm_argmax_cands(int rows, int nb, int tokens, int cu_count, int force_gpw = 0, bool g16 = false);
 // Upper bound of gemm_argmax_cands over every nb <= 4096/32 and tokens <= 64
 // (the size of a candidate buffer).
 int gemm_argmax_cand_capacity(int rows, int cu_count);
@@ -239,6 +249,7 @@ struct DeltaArgs {
   float *out = nullptr;            // raw: [batch][v_heads][vd]; fused: core [batch][v_heads*vd]
   // fused mode inputs
   SplitRows proj;                  // [splits][batch][in_rows] = [qkv | z | b | a]
+  const float *gates = nullptr;    // when set: b and a rows as [batch][2 v_heads] (Q8 gate tail), proj = [qkv | z]
   float *conv_base = nullptr;      // slot-strided conv ring [kernel][channels], slot = position % kernel
   long long conv_slot_stride = 0;
   const int32_t *positions = nullptr;
@@ -334,6 +345,6 @@ hipError_t launch_store_f16(const float *x, uint16_t *y, long long n, hipStream_
 // the penalty-count increment of the step's input tokens.
 hipError_t launch_embed(const q35_q4_0_block_x8 *embed, int nb, const int32_t *tokens,
                         int batch, float *x, int hidden, int32_t *counts, long long counts_stride,
-                        const int32_t *slots, const uint8_t *count_input, hipStream_t stream);
+                        const int32_t *slots, const uint8_t *count_input, hipStream_t stream, bool g16 = false);
 
 }  // namespace q35

@@ -31,6 +31,36 @@ struct QuantOut {
   q35_q8_0_block_x1 *x1 = nullptr;  // reference X1 layout (optional)
 };
 
+// Int8 quantization of one 32-value block held by four consecutive lanes,
+// eight values each (q8_0_quantize_vector_1, q4_0.cpp:212-235): absmax over
+// the block, scale = absmax / 127, codes round(x / scale) clamped to +-127
+// (packed little-endian into `word`), the block's code sum, and the
+// binary16-rounded scale as stored. Every lane of the row calls it. (The
+// same steps as the quantization in h128_quantize_row16, kept separate so
+// that the hot preparation kernels compile as they are.)
+__device__ __forceinline__ void q8_block_codes8(const float v[8], uint64_t &word, int &sum, float &stored) {
+  float amax = 0.0F;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+  amax = fmaxf(amax, q35_row_xor(amax, 1));
+  amax = fmaxf(amax, q35_row_xor(amax, 2));
+  const float scale = amax / 127.0F;
+  const float inv = scale == 0.0F ? 0.0F : 1.0F / scale;
+  word = 0;
+  sum = 0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float r = roundf(v[e] * inv);
+    r = fminf(fmaxf(r, -127.0F), 127.0F);
+    const int code = static_cast<int>(r);
+    sum += code;
+    word |= static_cast<uint64_t>(static_cast<uint8_t>(static_cast<int8_t>(code))) << (8 * e);
+  }
+  sum += q35_row_xor_i(sum, 1);
+  sum += q35_row_xor_i(sum, 2);
+  stored = half_bits_to_float(float_to_half_bits(scale));
+}
+
 // All 64 lanes of the wavefront call this (the DPP moves need every lane of
 // each row); rows whose `active` is false store nothing.
 __device__ __forceinline__ void h128_quantize_row16(float v[8], int t, int blk, int nb, bool h128,

@@ -22,6 +22,11 @@ struct LayerDev {
   const float *input_norm = nullptr, *post_norm = nullptr;
   const float *conv_w = nullptr, *lin_norm = nullptr, *dt_bias = nullptr, *ssm_a = nullptr;
   const float *q_norm = nullptr, *k_norm = nullptr;
+  // Q8 gate rows (linear_attn.in_proj_ba): int8 codes [gate_rows][hidden],
+  // F32 block scales [gate_rows][hidden / 32]; in_proj then holds [qkv | z]
+  int gate_rows = 0;
+  const int8_t *gate_codes = nullptr;
+  const float *gate_scales = nullptr;
 };
 
 }  // namespace q35
@@ -31,6 +36,7 @@ struct q35_model {
   q35_model_dims d{};
   std::vector<uint8_t> is_linear;
   const q35_q4_0_block_x8 *embed = nullptr;
+  bool embed_g16 = false;  // embed holds Q4G16Tile tiles (160 bytes per 8 x 32)
   const float *final_norm = nullptr;
   std::vector<q35::LayerDev> layers;
   std::vector<void *> allocations;
@@ -63,6 +69,7 @@ struct q35_runtime {
   // work buffers
   float *x[2] = {nullptr, nullptr};  // residual stream, ping-pong
   float *proj = nullptr, *core = nullptr, *q_rot = nullptr, *gates = nullptr;
+  float *q8_gates = nullptr;      // Q8 gate rows of the in projection [batch][kMaxGateRows]
   float *rows_final = nullptr;  // prefill: summed in-projection rows [batch][proj_width]
   float *delta_scan = nullptr;  // prefill: DeltaNet chunk scan entries and raw outputs
   unsigned long long *sample_scratch = nullptr;  // sampling: the slices' surviving keys

@@ -17,6 +17,25 @@ namespace {
 
 size_t align256(size_t n) { return (n + 255) & ~static_cast<size_t>(255); }
 
+// IEEE binary16 -> float (subnormals, infinities and NaN included)
+float half_bits_to_float_host(uint16_t h) {
+  const uint32_t sign = static_cast<uint32_t>(h & 0x8000u) << 16;
+  const int e = (h >> 10) & 0x1f;
+  const uint32_t mant = h & 0x3ffu;
+  float v;
+  if (e == 0)
+    v = std::ldexp(static_cast<float>(mant), -24);
+  else if (e == 31)
+    v = mant != 0 ? std::nanf("") : INFINITY;
+  else
+    v = std::ldexp(static_cast<float>(mant | 0x400u), e - 25);
+  uint32_t bits;
+  std::memcpy(&bits, &v, 4);
+  bits |= sign;
+  std::memcpy(&v, &bits, 4);
+  return v;
+}
+
 std::string layer_prefix(int i) {
   return "model.language_model.layers." + std::to_string(i) + ".";
 }
@@ -183,7 +202,30 @@ extern "C" int q35_model_upload_tensor(q35_model *m, const char *name_c, int enc
     return upload(m, bytes, count, reinterpret_cast<const void **>(dst));
   };
   int st = Q35_ERR_INVALID;
-  if (name == "model.language_model.embed_tokens.weight") {
+  if (name == "model.language_model.embed_tokens.weight" && encoding == Q35_ENC_Q4_G16_DOT4) {
+    // Q4G16Tile head (weights.inl:724-734): 160 bytes per 8-row x 32-column
+    // tile, every binary16 scale finite
+    st = expect_shape(m, name, shape, rank, {static_cast<uint64_t>(d.vocab), H});
+    if (st == Q35_OK && (d.vocab % 8 != 0 || H % 32 != 0 || count != static_cast<size_t>(d.vocab) / 8 * (H / 32) * 160))
+      st = set_error(m->ctx, Q35_ERR_INVALID, "wrong G16 payload size for " + name);
+    if (st == Q35_OK) {
+      const uint8_t *b = static_cast<const uint8_t *>(bytes);
+      for (size_t t = 0; t < count / 160 && st == Q35_OK; ++t)
+        for (int i = 0; i < 16; ++i) {
+          uint16_t s;
+          std::memcpy(&s, b + t * 160 + 2 * i, 2);
+          if ((s & 0x7c00u) == 0x7c00u) {
+            st = set_error(m->ctx, Q35_ERR_INVALID, "non-finite G16 scale in " + name);
+            break;
+          }
+        }
+    }
+    if (st == Q35_OK) {
+      m->weight_bytes += count;
+      st = upload(m, bytes, count, reinterpret_cast<const void **>(&m->embed));
+      m->embed_g16 = st == Q35_OK;
+    }
+  } else if (name == "model.language_model.embed_tokens.weight") {
     st = q4({static_cast<uint64_t>(d.vocab), H}, Q35_ENC_Q4_0_DOT4, &m->embed, &m->weight_bytes);
   } else if (name == "model.language_model.norm.weight") {
     st = f32({H}, &m->final_norm);
@@ -200,9 +242,40 @@ extern "C" int q35_model_upload_tensor(q35_model *m, const char *name_c, int enc
     else if (leaf == "mlp.gate_up_proj.weight") st = q4({2 * I, H}, Q35_ENC_Q4_H128_DOT4, &L.gate_up, &m->weight_bytes);
     else if (leaf == "mlp.down_proj.weight") st = q4({H, I}, Q35_ENC_Q4_H128_DOT4, &L.down, &m->weight_bytes);
     else if (L.linear && leaf == "linear_attn.in_proj_all.weight") {
-      st = q4({ch + v_dim + 2 * static_cast<uint64_t>(d.lin_v_heads), H}, Q35_ENC_Q4_H128_DOT4,
-              &L.in_proj, &m->weight_bytes);
-      L.in_rows = static_cast<int>(shape[0]);
+      // [qkv | z | b | a], or [qkv | z] when the gate rows are a separate
+      // Q8 tensor (weights.inl:1700-1747)
+      const bool split_gates = rank == 2 && shape[0] == ch + v_dim;
+      st = q4({split_gates ? ch + v_dim : ch + v_dim + 2 * static_cast<uint64_t>(d.lin_v_heads), H},
+              Q35_ENC_Q4_H128_DOT4, &L.in_proj, &m->weight_bytes);
+      if (st == Q35_OK) {
+        L.in_rows = static_cast<int>(shape[0]);
+        if (split_gates) m->required.insert(layer_prefix(li) + "linear_attn.in_proj_ba.weight");
+      }
+    } else if (L.linear && leaf == "linear_attn.in_proj_ba.weight") {
+      // Q8_0 gate rows [b | a] over the identity-basis input: F32 scales as
+      // q8_0_scales_to_f32 keeps them, finite and non-negative (weights.inl:735-746)
+      const uint64_t rows = 2 * static_cast<uint64_t>(d.lin_v_heads), nb = H / 32;
+      st = expect_shape(m, name, shape, rank, {rows, H});
+      if (st == Q35_OK && (encoding != Q35_ENC_Q8_0 || H % 32 != 0 || rows > static_cast<uint64_t>(kMaxGateRows) ||
+                           count != rows * nb * 34))
+        st = set_error(m->ctx, Q35_ERR_INVALID, "wrong Q8_0 payload for " + name);
+      std::vector<int8_t> codes(rows * H);
+      std::vector<float> scales(rows * nb);
+      const uint8_t *b = static_cast<const uint8_t *>(bytes);
+      for (uint64_t i = 0; st == Q35_OK && i < rows * nb; ++i) {
+        uint16_t h;
+        std::memcpy(&h, b + i * 34, 2);
+        scales[i] = half_bits_to_float_host(h);
+        if (!std::isfinite(scales[i]) || scales[i] < 0.0F)
+          st = set_error(m->ctx, Q35_ERR_INVALID, "invalid Q8 weight scale in " + name);
+        std::memcpy(&codes[i * 32], b + i * 34 + 2, 32);
+      }
+      if (st == Q35_OK) st = upload(m, codes.data(), codes.size(), reinterpret_cast<const void **>(&L.gate_codes));
+      if (st == Q35_OK) st = upload(m, scales.data(), scales.size() * 4, reinterpret_cast<const void **>(&L.gate_scales));
+      if (st == Q35_OK) {
+        L.gate_rows = static_cast<int>(rows);
+        m->weight_bytes += count;
+      }
     } else if (L.linear && leaf == "linear_attn.out_proj.weight") {
       st = q4({H, v_dim}, Q35_ENC_Q4_H128_DOT4, &L.out_proj, &m->weight_bytes);
       L.out_cols = static_cast<int>(v_dim);
@@ -252,6 +325,10 @@ extern "C" int q35_model_finalize(q35_model *m) {
   if (m == nullptr) return Q35_ERR_INVALID;
   for (const auto &n : m->required)
     if (!m->uploaded.count(n)) return set_error(m->ctx, Q35_ERR_STATE, "missing tensor " + n);
+  const int full_in = 2 * m->d.lin_k_heads * m->d.lin_k_dim + 2 * m->d.lin_v_heads * m->d.lin_v_dim;
+  for (const auto &L : m->layers)
+    if (L.linear && (L.gate_rows > 0) != (L.in_rows == full_in))
+      return set_error(m->ctx, Q35_ERR_STATE, "in_proj_all rows do not match the Q8 gate rows");
   m->finalized = true;
   return Q35_OK;
 }
@@ -345,6 +422,7 @@ extern "C" int q35_runtime_create(q35_model *m, const q35_runtime_config *cfg, q
   alloc(proj_floats * 4, reinterpret_cast<void **>(&rt->proj));
   // prefill: the in projection's split partials summed once, [batch][rows]
   alloc(static_cast<size_t>(B) * rt->proj_width * 4, reinterpret_cast<void **>(&rt->rows_final));
+  alloc(static_cast<size_t>(B) * kMaxGateRows * 4, reinterpret_cast<void **>(&rt->q8_gates));
   if (d.lin_v_heads > 0)
     alloc(delta_chunk_scan_floats(B, d.lin_v_heads) * 4, reinterpret_cast<void **>(&rt->delta_scan));
   // sampling: per-row candidate lists and the slices' survivors
@@ -546,6 +624,7 @@ static GemmArgs greedy_head_args(q35_runtime *rt, int tokens, const int32_t *cou
   const q35_model_dims &d = rt->model->d;
   GemmArgs g;
   g.w = rt->model->embed;
+  g.g16 = rt->model->embed_g16;
   g.rows = d.vocab;
   g.nb = d.hidden / 32;
   g.codes = rt->codes;
@@ -605,7 +684,8 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
 
   Q35_STEP(hipMemcpyAsync(rt->meta_dev, rt->meta_host, rt->meta_bytes, hipMemcpyHostToDevice, s), "metadata copy");
   Q35_KERNEL(Q35_KERNEL_EMBED, B * (H / 32 * 18.0 + H * 4.0 + 8.0),
-             launch_embed(m->embed, H / 32, tokens, batch, rt->x[0], H, rt->counts, d.vocab, slots, count_input, s),
+             launch_embed(m->embed, H / 32, tokens, batch, rt->x[0], H, rt->counts, d.vocab, slots, count_input, s,
+                          m->embed_g16),
              "embedding");
 
   // Residual stream: x[cur] holds it; a residual update writes x[cur ^ 1]
@@ -638,8 +718,15 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
     return launch_gemm(g, s);
   };
   // Residual update with the pending split rows (if `add`) + RMSNorm + prep.
-  auto rms_prep = [&](const float *w, bool add, bool h128, float *normed) -> hipError_t {
+  auto rms_prep = [&](const float *w, bool add, bool h128, float *normed,
+                      const LayerDev *gate_layer = nullptr) -> hipError_t {
     RmsPrepArgs a;
+    if (gate_layer != nullptr && gate_layer->gate_rows > 0) {
+      a.gate_codes = gate_layer->gate_codes;
+      a.gate_scales = gate_layer->gate_scales;
+      a.gate_rows = gate_layer->gate_rows;
+      a.gates = rt->q8_gates;
+    }
     a.x_in = rt->x[cur];
     if (add) {
       a.add = pending;
@@ -671,7 +758,7 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
   bool add_pending = false;  // the previous layer's down projection is still split
   for (int l = 0; l < d.n_layers; ++l) {
     const LayerDev &L = m->layers[l];
-    Q35_KERNEL(Q35_KERNEL_PREP, rms_bytes(add_pending), rms_prep(L.input_norm, add_pending, true, nullptr),
+    Q35_KERNEL(Q35_KERNEL_PREP, rms_bytes(add_pending), rms_prep(L.input_norm, add_pending, true, nullptr, L.linear ? &L : nullptr),
                "input norm prep");
     Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(L.in_rows, H, kConsumerSplits),
                gemm(L.in_proj, L.in_rows, H, kConsumerSplits), "in projection");
@@ -690,6 +777,7 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
       a.vd = d.lin_v_dim;
       a.out = nullptr;
       a.proj = pending;
+      a.gates = L.gate_rows > 0 ? rt->q8_gates : nullptr;
       if (prefill && pending.splits > 1) {
         // the chunk scan reads every token's inputs in order: sum the split
         // partials once over the whole GPU, so each token is one load per channel
@@ -822,6 +910,7 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
   if (want_logits) {
     GemmArgs g;
     g.w = m->embed;
+    g.g16 = m->embed_g16;
     g.rows = d.vocab;
     g.nb = H / 32;
     g.codes = rt->codes;
@@ -836,7 +925,7 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
                "logits head");
   } else {
     const GemmArgs g = greedy_head_args(rt, head_tokens, slots + head_row0, penalties + head_row0);
-    const int ncand = gemm_argmax_cands(d.vocab, H / 32, head_tokens, ctx->cu_count);
+    const int ncand = gemm_argmax_cands(d.vocab, H / 32, head_tokens, ctx->cu_count, 0, m->embed_g16);
     Q35_KERNEL(Q35_KERNEL_HEAD, gemm_algorithmic_bytes(d.vocab, H / 32, head_tokens, false, false) + ncand * HB * 8.0,
                launch_gemm(g, s), "greedy head");
     Q35_KERNEL(Q35_KERNEL_ARGMAX, ncand * HB * 8.0 + HB * 4.0,
@@ -1301,7 +1390,7 @@ extern "C" int q35_runtime_head(q35_runtime *rt, int32_t slot, const float *hidd
   const GemmArgs g = greedy_head_args(rt, 1, reinterpret_cast<const int32_t *>(rt->meta_dev + ml.slots),
                                       reinterpret_cast<const float *>(rt->meta_dev + ml.penalties));
   Q35_HIP_TRY(ctx, launch_gemm(g, s));
-  const int ncand = gemm_argmax_cands(d.vocab, d.hidden / 32, 1, ctx->cu_count);
+  const int ncand = gemm_argmax_cands(d.vocab, d.hidden / 32, 1, ctx->cu_count, 0, rt->model->embed_g16);
   Q35_HIP_TRY(ctx, launch_argmax_finalize(rt->cand, ncand, kMaxTokens, 1, rt->tokens_out_dev, nullptr, s));
   Q35_HIP_TRY(ctx, hipStreamSynchronize(s));
   rt->last_batch = 1;

@@ -26,10 +26,12 @@ def _h128_dot4(rng, rows, cols, std):
     return orc.dot4_pack(orc.h128_quantize_matrix(w), rows, cols // 32)
 
 
-def build_small_model(d, sched, seed=0, std=0.1, head_std=0.2):
+def build_small_model(d, sched, seed=0, std=0.1, head_std=0.2, head_g16=False, q8_gates=False):
     """{hf_name: (encoding, shape, payload)} in the Q35H128 artifact naming.
     The scales keep the layers (not the tied embedding) in charge of the next
-    token, so greedy tokens vary from step to step."""
+    token, so greedy tokens vary from step to step. head_g16 stores the tied
+    embedding as Q4G16Tile (encoding 8); q8_gates moves each linear layer's
+    b and a rows into a Q8_0 linear_attn.in_proj_ba tensor (encoding 7)."""
     rng = np.random.default_rng(seed)
     H, I, hd = d["hidden"], d["intermediate"], d["head_dim"]
     q_dim = d["lin_k_heads"] * d["lin_k_dim"]
@@ -44,8 +46,11 @@ def build_small_model(d, sched, seed=0, std=0.1, head_std=0.2):
         t[name] = (6, [rows, cols], _h128_dot4(rng, rows, cols, std))
 
     head = (rng.standard_normal((d["vocab"], H)) * head_std).astype(np.float32)
-    t["model.language_model.embed_tokens.weight"] = (5, [d["vocab"], H],
-                                                     orc.dot4_pack(orc.q4_quantize(head), d["vocab"], H // 32))
+    if head_g16:
+        t["model.language_model.embed_tokens.weight"] = (8, [d["vocab"], H], orc.g16_pack(head))
+    else:
+        t["model.language_model.embed_tokens.weight"] = (5, [d["vocab"], H],
+                                                         orc.dot4_pack(orc.q4_quantize(head), d["vocab"], H // 32))
     f32("model.language_model.norm.weight", [H], rng.standard_normal(H) * 0.1)
     for i in range(d["n_layers"]):
         p = f"model.language_model.layers.{i}."
@@ -54,7 +59,12 @@ def build_small_model(d, sched, seed=0, std=0.1, head_std=0.2):
         q4(p + "mlp.gate_up_proj.weight", 2 * I, H)
         q4(p + "mlp.down_proj.weight", H, I)
         if sched[i]:
-            q4(p + "linear_attn.in_proj_all.weight", ch + v_dim + 2 * d["lin_v_heads"], H)
+            if q8_gates:
+                q4(p + "linear_attn.in_proj_all.weight", ch + v_dim, H)
+                gw = (rng.standard_normal((2 * d["lin_v_heads"], H)) * std).astype(np.float32)
+                t[p + "linear_attn.in_proj_ba.weight"] = (7, [2 * d["lin_v_heads"], H], orc.q8_rows_pack(gw)[0])
+            else:
+                q4(p + "linear_attn.in_proj_all.weight", ch + v_dim + 2 * d["lin_v_heads"], H)
             f32(p + "linear_attn.conv1d.weight", [ch, 1, d["lin_kernel"]],
                 rng.standard_normal(ch * d["lin_kernel"]) * 0.3)
             q4(p + "linear_attn.out_proj.weight", H, v_dim)

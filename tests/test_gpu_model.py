@@ -21,10 +21,13 @@ from tests.model_util import (build_small_model, hip_greedy, oracle_envelope, or
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(scope="module")
-def small(q, ctx):
+@pytest.fixture(scope="module", params=["q4", "g16_q8gates"])
+def small(q, ctx, request):
+    """The Q4 model, and the same shapes with the optional encodings: a G16
+    tied head / embedding and Q8 gate rows (weights.inl:724-734, :1700-1747)."""
     d, sched = small_dims()
-    tensors = build_small_model(d, sched, seed=5)
+    alt = request.param != "q4"
+    tensors = build_small_model(d, sched, seed=5, head_g16=alt, q8_gates=alt)
     model = upload_model(q, ctx, d, sched, tensors)
     yield d, sched, tensors, model
     model.close()
