@@ -54,15 +54,19 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def prepare_model_dir(q, seed, weight_std):
-    """Writes the random-init artifact (and the reference's config.json) once per host."""
+def prepare_model_dir(q, seed, weight_std, encodings="q4"):
+    """Writes the random-init artifact (and the reference's config.json) once per host;
+    encodings "g16q8" selects the G16 tied head and the Q8_0 gate rows."""
     d, sched = q.model_dims(0)
-    path = os.path.join(tempfile.gettempdir(), f"q35_bench_0p8b_s{seed}")
+    suffix = "" if encodings == "q4" else f"_{encodings}"
+    path = os.path.join(tempfile.gettempdir(), f"q35_bench_0p8b_s{seed}{suffix}")
     os.makedirs(path, exist_ok=True)
     art = os.path.join(path, "model.q35h128")
     if not os.path.exists(art):
         t = time.time()
-        q.write_random_artifact(art + ".part", d, sched, seed=seed, weight_std=weight_std)
+        alt = encodings != "q4"
+        q.write_random_artifact(art + ".part", d, sched, seed=seed, weight_std=weight_std, head_g16=alt,
+                                q8_gates=alt)
         os.replace(art + ".part", art)
         log(f"wrote random-init artifact {art} ({os.path.getsize(art) / 1e6:.1f} MB) in {time.time() - t:.1f}s")
     with open(os.path.join(path, "config.json"), "w") as f:
@@ -428,6 +432,8 @@ def main():
     ap.add_argument("--workload", choices=("decode0p8b", "mixed4b", "prefix0p8b", "kernels"), default="decode0p8b",
                     help="decode0p8b: the headline metric (config 4); mixed4b: config 5; "
                          "prefix0p8b: prefill with a prefix-cache hit")
+    ap.add_argument("--encodings", choices=("q4", "g16q8"), default="q4",
+                    help="decode0p8b artifact: Q4 throughout, or the G16 tied head with Q8_0 gate rows")
     ap.add_argument("--graphs", choices=("on", "off"), default="on",
                     help="replay captured step graphs (off: eager launches, e.g. under rocprofv3)")
     args = ap.parse_args()
@@ -452,7 +458,7 @@ def main():
         ctx.close()
         print(json.dumps(line), flush=True)
         return
-    d, sched, model_dir, artifact = prepare_model_dir(q, args.seed, 0.02)
+    d, sched, model_dir, artifact = prepare_model_dir(q, args.seed, 0.02, args.encodings)
     if args.calibration_copy_mb > 0:
         n = args.calibration_copy_mb << 20
         src, dst = ctx.array(shape=(n,), dtype=np.uint8), ctx.array(shape=(n,), dtype=np.uint8)
@@ -517,8 +523,13 @@ def main():
     # the Q4 GEMV the metric names: the vocabulary head (248,320 x 1024 Q4,
     # 143 MB per launch, one launch per step); the per-layer projections are
     # reported beside it as one class
-    roof = roofline("head", prof["head"], traffic, "head_kernel<4, 3, NT, true, *> (greedy head: streaming Q4 GEMV + penalty + argmax, NT token tiles)") if prof else None
-    gemm_roof = roofline("gemm", prof["gemm"], traffic, "gemm_kernel<8, false, false> (per-layer Q4 projections, split-K)") if prof else None
+    # traffic.json keys carry the artifact encodings ("head", "head_g16q8")
+    sfx = "" if args.encodings == "q4" else f"_{args.encodings}"
+    head_name = ("head_kernel<4, 3, NT, true, *> (greedy head: streaming Q4 GEMV + penalty + argmax, NT token tiles)"
+                 if not sfx else "head_kernel<4, 3, NT, true, 2, true> (greedy G16 head: Q4G16Tile GEMV, per-half "
+                 "MFMA dots + penalty + argmax)")
+    roof = roofline("head" + sfx, prof["head"], traffic, head_name) if prof else None
+    gemm_roof = roofline("gemm" + sfx, prof["gemm"], traffic, "gemm_kernel<8, false, false> (per-layer Q4 projections, split-K)") if prof else None
     breakdown = ({k: {"us_per_step": round(v[0] / args.profile_steps * 1000.0, 1),
                       "launches_per_step": v[1] // args.profile_steps} for k, v in prof.items() if v[1]}
                  if prof else None)
@@ -534,7 +545,7 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": "q4xi8->i32 (projections), f32 (DeltaNet, attention)",
         "data": "synthetic: random-init weights N(0,0.02) packed to Q4-G32-DOT4 H128, random-token prompts",
         "config": {"workload": "random-init Qwen3.5-0.8B-shaped hybrid, batched greedy decode",
-                   "batch": args.batch, "prompt_tokens": args.prompt,
+                   "batch": args.batch, "prompt_tokens": args.prompt, "encodings": args.encodings,
                    "decode_forwards_timed": args.steps, "graphs": args.graphs == "on"},
         "roofline": roof, "q4_projection_roofline": gemm_roof, "step_kernel_breakdown": breakdown,
         "cpu_baseline": base,

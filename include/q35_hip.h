@@ -217,6 +217,14 @@ int q35_model_dims_preset(int which, q35_model_dims *dims, uint8_t *layer_is_lin
  * attention norm 1, seeded A_log/dt_bias/conv weights. Host-only. */
 int q35_write_random_artifact(const char *path, const q35_model_dims *dims,
                               const uint8_t *layer_is_linear, uint64_t seed, float weight_std);
+/* q35_write_random_artifact with the optional encodings of the reference
+ * packer (q4_h128_convert_main.cpp --head-g16 / --q8-gates): the tied head as
+ * q4_g16_cpu_dot4 (encoding 8, identity basis, scale group 16) and each linear
+ * layer's b, a rows as a separate q8_0 tensor linear_attn.in_proj_ba.weight
+ * (encoding 7) with in_proj_all holding [qkv | z]. Host-only. */
+enum { Q35_ARTIFACT_HEAD_G16 = 1u, Q35_ARTIFACT_Q8_GATES = 2u };
+int q35_write_random_artifact_ex(const char *path, const q35_model_dims *dims, const uint8_t *layer_is_linear,
+                                 uint64_t seed, float weight_std, uint32_t flags);
 /* The FP32 rows [row0, row0+rows) x cols that the generator draws for tensor
  * `name` before packing (no reference counterpart; lets tests run the same
  * rows through the reference packer). */

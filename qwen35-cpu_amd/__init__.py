@@ -155,6 +155,7 @@ _SIGS = {
     "q35_model_load_artifact": (c_int, [P, c_char_p, POINTER(ModelDims), P, POINTER(P)]),
     "q35_model_dims_preset": (c_int, [c_int, POINTER(ModelDims), P, c_size_t]),
     "q35_write_random_artifact": (c_int, [c_char_p, POINTER(ModelDims), P, c_uint64, c_float]),
+    "q35_write_random_artifact_ex": (c_int, [c_char_p, POINTER(ModelDims), P, c_uint64, c_float, ctypes.c_uint32]),
     "q35_random_weight_rows": (c_int, [c_char_p, c_uint64, c_uint64, c_uint64, c_uint64, c_float, P]),
     "q35_runtime_create": (c_int, [P, POINTER(RuntimeConfig), POINTER(P)]),
     "q35_runtime_destroy": (None, [P]),
@@ -395,11 +396,13 @@ def rope_f32(ctx, x, heads, head_dim, rope_dim, cos, sin):
 
 # --------------------------------------------------------------- model level
 
-def write_random_artifact(path, dims, schedule, seed=1, weight_std=0.02):
-    """Random-init Q35H128 artifact (weights ~N(0, weight_std) through the H128/Q4 packer)."""
+def write_random_artifact(path, dims, schedule, seed=1, weight_std=0.02, head_g16=False, q8_gates=False):
+    """Random-init Q35H128 artifact (weights ~N(0, weight_std) through the H128/Q4 packer);
+    head_g16 / q8_gates select the optional encodings (G16 tied head, Q8_0 gate rows)."""
     sched = np.ascontiguousarray(schedule, np.uint8)
-    _check(lib.q35_write_random_artifact(os.fsencode(path), ctypes.byref(dims), _ptr(sched), seed, weight_std),
-           "write_random_artifact")
+    flags = (1 if head_g16 else 0) | (2 if q8_gates else 0)
+    _check(lib.q35_write_random_artifact_ex(os.fsencode(path), ctypes.byref(dims), _ptr(sched), seed, weight_std,
+                                            flags), "write_random_artifact")
 
 
 def random_weight_rows(name, seed, row0, rows, cols, weight_std=0.02):

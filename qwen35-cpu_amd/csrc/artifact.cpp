@@ -193,6 +193,62 @@ std::vector<uint8_t> random_dot4(const std::string &name, uint64_t seed, uint64_
   return out;
 }
 
+// Random [rows, cols] identity-basis matrix -> Q4G16Tile bytes (q4_g16.h:5-6):
+// per row, block and 16-column half an absmax/7 binary16 scale, codes
+// round(x / d) + 8 clamped to 0..15, in the DOT4 nibble order.
+std::vector<uint8_t> random_g16(const std::string &name, uint64_t seed, uint64_t rows, uint64_t cols, float stdev) {
+  const uint64_t blocks = cols / 32;
+  std::vector<uint8_t> out(rows / 8 * blocks * 160, 0);
+  const uint64_t base = seed ^ name_hash(name);
+  std::vector<float> row(cols);
+  for (uint64_t r = 0; r < rows; ++r) {
+    Normal g(mix64(base + r * 0x632be59bd9b4e019ull));
+    for (uint64_t c = 0; c < cols; ++c) row[c] = g.next() * stdev;
+    for (uint64_t b = 0; b < blocks; ++b) {
+      uint8_t *tile = &out[((r / 8) * blocks + b) * 160];
+      for (int half = 0; half < 2; ++half) {
+        const float *x = row.data() + b * 32 + 16 * half;
+        float amax = 0.0F;
+        for (int i = 0; i < 16; ++i) amax = std::max(amax, std::fabs(x[i]));
+        const uint16_t d = f2h(amax / 7.0F);
+        std::memcpy(tile + 2 * (8 * half + r % 8), &d, 2);
+        const float stored = h2f(d), inv = stored > 0.0F ? 1.0F / stored : 0.0F;
+        for (int i = 0; i < 16; ++i) {
+          const int k = 16 * half + i;
+          const int q = static_cast<int>(std::clamp(std::round(x[i] * inv), -8.0F, 7.0F)) + 8;
+          tile[32 + 32 * (k / 8) + 4 * (r % 8) + k % 4] |= static_cast<uint8_t>(q << (k % 8 < 4 ? 0 : 4));
+        }
+      }
+    }
+  }
+  return out;
+}
+
+// Random [rows, cols] matrix -> row-major Q8_0 blocks (binary16 scale + 32
+// codes; q8_0_quantize, q8_0.cpp:86-110).
+std::vector<uint8_t> random_q8(const std::string &name, uint64_t seed, uint64_t rows, uint64_t cols, float stdev) {
+  const uint64_t blocks = cols / 32;
+  std::vector<uint8_t> out(rows * blocks * 34);
+  const uint64_t base = seed ^ name_hash(name);
+  std::vector<float> row(cols);
+  for (uint64_t r = 0; r < rows; ++r) {
+    Normal g(mix64(base + r * 0x632be59bd9b4e019ull));
+    for (uint64_t c = 0; c < cols; ++c) row[c] = g.next() * stdev;
+    for (uint64_t b = 0; b < blocks; ++b) {
+      const float *x = row.data() + b * 32;
+      float amax = 0.0F;
+      for (int i = 0; i < 32; ++i) amax = std::max(amax, std::fabs(x[i]));
+      const float scale = amax / 127.0F, inv = scale == 0.0F ? 0.0F : 1.0F / scale;
+      uint8_t *dst = &out[(r * blocks + b) * 34];
+      const uint16_t d = f2h(scale);
+      std::memcpy(dst, &d, 2);
+      for (int i = 0; i < 32; ++i)
+        dst[2 + i] = static_cast<uint8_t>(static_cast<int8_t>(std::clamp(std::round(x[i] * inv), -127.0F, 127.0F)));
+    }
+  }
+  return out;
+}
+
 struct Entry {
   std::string name;
   std::vector<uint64_t> shape;
@@ -204,7 +260,7 @@ uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
 
 // Tensor plan of the packed artifact (q4_h128_convert_main.cpp:52-170 names,
 // fused rows as loaded by weights.inl:1697-1771).
-std::vector<Entry> plan(const q35_model_dims &d, const uint8_t *is_linear) {
+std::vector<Entry> plan(const q35_model_dims &d, const uint8_t *is_linear, uint32_t flags) {
   std::vector<Entry> e;
   const uint64_t H = d.hidden, I = d.intermediate, hd = d.head_dim;
   const uint64_t q_dim = static_cast<uint64_t>(d.lin_k_heads) * d.lin_k_dim;
@@ -231,7 +287,18 @@ std::vector<Entry> plan(const q35_model_dims &d, const uint8_t *is_linear) {
     x.size = k * 4;
     e.push_back(x);
   };
-  q4("model.language_model.embed_tokens.weight", d.vocab, H, false);
+  if (flags & Q35_ARTIFACT_HEAD_G16) {
+    // q4_g16_cpu_dot4: identity basis, 16-column scale groups
+    Entry x;
+    x.name = "model.language_model.embed_tokens.weight";
+    x.shape = {static_cast<uint64_t>(d.vocab), H};
+    x.encoding = Q35_ENC_Q4_G16_DOT4;
+    x.group = 16;
+    x.size = static_cast<uint64_t>(d.vocab) / 8 * (H / 32) * 160;
+    e.push_back(x);
+  } else {
+    q4("model.language_model.embed_tokens.weight", d.vocab, H, false);
+  }
   f32("model.language_model.norm.weight", {H});
   for (int i = 0; i < d.n_layers; ++i) {
     const std::string p = "model.language_model.layers." + std::to_string(i) + ".";
@@ -240,7 +307,19 @@ std::vector<Entry> plan(const q35_model_dims &d, const uint8_t *is_linear) {
     q4(p + "mlp.gate_up_proj.weight", 2 * I, H, true);
     q4(p + "mlp.down_proj.weight", H, I, true);
     if (is_linear[i]) {
-      q4(p + "linear_attn.in_proj_all.weight", ch + v_dim + 2 * static_cast<uint64_t>(d.lin_v_heads), H, true);
+      if (flags & Q35_ARTIFACT_Q8_GATES) {
+        // [qkv | z] as Q4 and the b, a rows as Q8_0 (weights.inl:1700-1747)
+        q4(p + "linear_attn.in_proj_all.weight", ch + v_dim, H, true);
+        Entry x;
+        x.name = p + "linear_attn.in_proj_ba.weight";
+        x.shape = {2 * static_cast<uint64_t>(d.lin_v_heads), H};
+        x.encoding = Q35_ENC_Q8_0;
+        x.group = 32;
+        x.size = x.shape[0] * (H / 32) * 34;
+        e.push_back(x);
+      } else {
+        q4(p + "linear_attn.in_proj_all.weight", ch + v_dim + 2 * static_cast<uint64_t>(d.lin_v_heads), H, true);
+      }
       f32(p + "linear_attn.conv1d.weight", {ch, 1, static_cast<uint64_t>(d.lin_kernel)});
       q4(p + "linear_attn.out_proj.weight", H, v_dim, true);
       f32(p + "linear_attn.norm.weight", {static_cast<uint64_t>(d.lin_v_dim)});
@@ -302,8 +381,13 @@ extern "C" int q35_random_weight_rows(const char *name, uint64_t seed, uint64_t 
 
 extern "C" int q35_write_random_artifact(const char *path, const q35_model_dims *d,
                                          const uint8_t *is_linear, uint64_t seed, float stdev) {
+  return q35_write_random_artifact_ex(path, d, is_linear, seed, stdev, 0);
+}
+
+extern "C" int q35_write_random_artifact_ex(const char *path, const q35_model_dims *d, const uint8_t *is_linear,
+                                            uint64_t seed, float stdev, uint32_t flags) {
   if (path == nullptr || d == nullptr || is_linear == nullptr) return Q35_ERR_INVALID;
-  std::vector<Entry> e = plan(*d, is_linear);
+  std::vector<Entry> e = plan(*d, is_linear, flags);
   uint64_t dir_bytes = 0;
   for (auto &x : e) dir_bytes += 64 + x.name.size() + 8 * x.shape.size();
   const uint64_t data_offset = align_up(kHeaderSize + dir_bytes, kAlignment);
@@ -320,6 +404,10 @@ extern "C" int q35_write_random_artifact(const char *path, const q35_model_dims 
     std::vector<uint8_t> payload;
     if (x.encoding == Q35_ENC_F32)
       payload = f32_payload(x, seed);
+    else if (x.encoding == Q35_ENC_Q4_G16_DOT4)
+      payload = random_g16(x.name, seed, x.shape[0], x.shape[1], stdev);
+    else if (x.encoding == Q35_ENC_Q8_0)
+      payload = random_q8(x.name, seed, x.shape[0], x.shape[1], stdev);
     else
       payload = random_dot4(x.name, seed, x.shape[0], x.shape[1], stdev, x.encoding == Q35_ENC_Q4_H128_DOT4,
                             d->sign_seed);

@@ -74,7 +74,8 @@ __global__ __launch_bounds__(kRmsThreads) void rms_prep_kernel(RmsPrepArgs a) {
   __shared__ float red[kRmsThreads / 64];
   __shared__ __align__(16) int8_t gq[GATES ? kRmsMaxK : 8];
   __shared__ float gsc[GATES ? kRmsMaxK / 32 : 1];
-  __shared__ float gdot[GATES ? kMaxGateRows * (kRmsMaxK / 32) : 1];
+  __shared__ float gdot[GATES ? kMaxGateItems : 1];
+  __shared__ float gmul[GATES ? kMaxGateItems : 1];
   const int t = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int K = a.K, n4 = K >> 2;
   const int nblk = K >> 7, j = tid & 15;
@@ -167,12 +168,14 @@ __global__ __launch_bounds__(kRmsThreads) void rms_prep_kernel(RmsPrepArgs a) {
           dot += static_cast<int>(static_cast<int8_t>(wu >> (8 * e))) * static_cast<int>(static_cast<int8_t>(cu >> (8 * e)));
       }
       gdot[i] = static_cast<float>(dot);
+      gmul[i] = a.gate_scales[i] * gsc[b];  // mscale * vscale, [row][block] as the scales are stored
     }
     __syncthreads();
+    // the serial chains read LDS only
     for (int r = tid; r < a.gate_rows; r += kRmsThreads) {
-      const float *ms = a.gate_scales + static_cast<size_t>(r) * nb;
       float acc = 0.0F;
-      for (int b = 0; b < nb; ++b) acc = fmaf(gdot[r * nb + b], ms[b] * gsc[b], acc);
+#pragma unroll 8
+      for (int b = 0; b < nb; ++b) acc = fmaf(gdot[r * nb + b], gmul[r * nb + b], acc);
       a.gates[static_cast<size_t>(t) * a.gate_rows + r] = acc;
     }
   }
@@ -237,7 +240,8 @@ hipError_t launch_rms_prep(const RmsPrepArgs &a, hipStream_t stream) {
   if (a.tokens <= 0) return hipSuccess;
   if (a.K % 128 != 0 || a.K > kRmsMaxK || (a.add.p != nullptr && a.x_out == nullptr)) return hipErrorInvalidValue;
   const bool gates = a.gate_rows > 0;
-  if (gates && (a.gate_rows > kMaxGateRows || a.gate_codes == nullptr || a.gate_scales == nullptr || a.gates == nullptr))
+  if (gates && (a.gate_rows > kMaxGateRows || a.gate_rows * (a.K / 32) > kMaxGateItems || a.gate_codes == nullptr ||
+                a.gate_scales == nullptr || a.gates == nullptr))
     return hipErrorInvalidValue;
   const dim3 grid(a.tokens), block(kRmsThreads);
 #define Q35_RMS(MS)                                                                     \

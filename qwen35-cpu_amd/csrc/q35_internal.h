@@ -168,6 +168,7 @@ struct RmsPrepArgs {
   float *gates = nullptr;
 };
 constexpr int kMaxGateRows = 64;
+constexpr int kMaxGateItems = 6144;  // gate rows x K/32 blocks staged in LDS (4B: 64 x 80)
 hipError_t launch_rms_prep(const RmsPrepArgs &a, hipStream_t stream);
 
 

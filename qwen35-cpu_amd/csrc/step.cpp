@@ -683,7 +683,9 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
   // activation prep: FP32 rows in (x_cols wide), A16 codes + scales out
 
   Q35_STEP(hipMemcpyAsync(rt->meta_dev, rt->meta_host, rt->meta_bytes, hipMemcpyHostToDevice, s), "metadata copy");
-  Q35_KERNEL(Q35_KERNEL_EMBED, B * (H / 32 * 18.0 + H * 4.0 + 8.0),
+  // a G16 head tile is 160 bytes per 8 x 32 (20 per row block) against 144 (18)
+  const double g16_extra = m->embed_g16 ? static_cast<double>(d.vocab / 8) * (H / 32) * 16.0 : 0.0;
+  Q35_KERNEL(Q35_KERNEL_EMBED, B * (H / 32 * (m->embed_g16 ? 20.0 : 18.0) + H * 4.0 + 8.0),
              launch_embed(m->embed, H / 32, tokens, batch, rt->x[0], H, rt->counts, d.vocab, slots, count_input, s,
                           m->embed_g16),
              "embedding");
@@ -921,12 +923,12 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
     g.head = true;
     g.force_split = 1;  // rt->logits holds one [batch][vocab] copy: never split K here
     g.cu_count = ctx->cu_count;
-    Q35_KERNEL(Q35_KERNEL_HEAD, gemm_algorithmic_bytes(d.vocab, H / 32, head_tokens, true, false), launch_gemm(g, s),
+    Q35_KERNEL(Q35_KERNEL_HEAD, gemm_algorithmic_bytes(d.vocab, H / 32, head_tokens, true, false) + g16_extra, launch_gemm(g, s),
                "logits head");
   } else {
     const GemmArgs g = greedy_head_args(rt, head_tokens, slots + head_row0, penalties + head_row0);
     const int ncand = gemm_argmax_cands(d.vocab, H / 32, head_tokens, ctx->cu_count, 0, m->embed_g16);
-    Q35_KERNEL(Q35_KERNEL_HEAD, gemm_algorithmic_bytes(d.vocab, H / 32, head_tokens, false, false) + ncand * HB * 8.0,
+    Q35_KERNEL(Q35_KERNEL_HEAD, gemm_algorithmic_bytes(d.vocab, H / 32, head_tokens, false, false) + g16_extra + ncand * HB * 8.0,
                launch_gemm(g, s), "greedy head");
     Q35_KERNEL(Q35_KERNEL_ARGMAX, ncand * HB * 8.0 + HB * 4.0,
                launch_argmax_finalize(rt->cand, ncand, kMaxTokens, head_tokens, rt->tokens_out_dev, nullptr, s),

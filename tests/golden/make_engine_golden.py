@@ -19,7 +19,10 @@ Two record sets:
             logits of every generated position.
 
 Run in the container that has the reference checkout:
-    make -C oracle ref && python tests/golden/make_engine_golden.py
+    make -C oracle ref && python tests/golden/make_engine_golden.py [g16q8]
+With g16q8 the artifact carries the optional encodings (G16 tied head,
+Q8_0 gate rows; q35_write_random_artifact_ex) and the records go to
+engine_0p8b_g16q8.npz (auto and scalar backends only).
 The tests regenerate the same artifact (the generator is deterministic and
 host-only) and compare against these vectors.
 """
@@ -67,12 +70,17 @@ def main():
     import __graft_entry__ as entry
     import bench
 
+    variant = sys.argv[1] if len(sys.argv) > 1 else "q4"
+    assert variant in ("q4", "g16q8")
+    alt = variant == "g16q8"
+    backends = BACKENDS[:2] if alt else BACKENDS
+
     q = entry.load()
     assert orc.ref_available(), "build oracle/_ref first: make -C oracle ref"
     d, sched = q.model_dims(0)
     tmp = tempfile.mkdtemp(prefix="q35_golden_")
     art = os.path.join(tmp, "model.q35h128")
-    q.write_random_artifact(art, d, sched, seed=SEED, weight_std=STD)
+    q.write_random_artifact(art, d, sched, seed=SEED, weight_std=STD, head_g16=alt, q8_gates=alt)
     with open(os.path.join(tmp, "config.json"), "w") as f:
         json.dump(bench.CONFIG_08B, f)
     rng = np.random.default_rng(77)
@@ -80,19 +88,20 @@ def main():
     forced = np.ascontiguousarray(seq[:, 1:])
     probe = np.sort(np.random.default_rng(99).choice(d.vocab, PROBES, replace=False)).astype(np.int32)
     rec = {}
-    for bk in BACKENDS:
+    for bk in backends:
         out, fv, fi, pv = run(tmp, art, np.ascontiguousarray(seq[:, :1]), SEQ - 1, forced, bk, probe)
         assert np.array_equal(out, forced)
         rec.update({f"forced_b{bk}_top_values": fv, f"forced_b{bk}_top_index": fi, f"forced_b{bk}_probe": pv})
-    for bk in BACKENDS[1:]:
+    for bk in backends[1:]:
         diff = np.abs(rec[f"forced_b{bk}_probe"] - rec["forced_b0_probe"])
         print(f"backend {bk} vs auto: probe logits max-abs {diff.max():.4f}, mean-abs {diff.mean():.5f}")
     prompts = rng.integers(0, d.vocab, size=(BATCH, PROMPT)).astype(np.int32)
     gt, gv, gi, _ = run(tmp, art, prompts, NEW)
     assert np.array_equal(gt, gi[:, :, 0]), "greedy token is the top logit at penalty 1"
-    np.savez_compressed(os.path.join(os.path.dirname(os.path.abspath(__file__)), "engine_0p8b.npz"),
+    name = "engine_0p8b_g16q8.npz" if alt else "engine_0p8b.npz"
+    np.savez_compressed(os.path.join(os.path.dirname(os.path.abspath(__file__)), name),
                         seed=np.array([SEED]), weight_std=np.array([STD], np.float32),
-                        forced_sequence=seq, probe_index=probe, backends=np.array(BACKENDS), **rec,
+                        forced_sequence=seq, probe_index=probe, backends=np.array(backends), **rec,
                         greedy_prompts=prompts, greedy_tokens=gt, greedy_top_values=gv, greedy_top_index=gi)
     os.remove(art)
     fv = rec["forced_b0_top_values"]

@@ -193,19 +193,23 @@ def artifact_tensors(path):
     return {k: (v["enc"], list(v["shape"]), np.frombuffer(v["data"], np.uint8)) for k, v in t.items()}
 
 
-GOLDEN_0P8B = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "engine_0p8b.npz")
+GOLDEN_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+GOLDEN_0P8B = os.path.join(GOLDEN_DIR, "engine_0p8b.npz")
 
 
-def golden_0p8b():
-    """Reference-engine greedy tokens and top-8 logits (tests/golden/make_engine_golden.py)."""
-    with np.load(GOLDEN_0P8B) as f:
+def golden_0p8b(variant="q4"):
+    """Reference-engine greedy tokens and top-8 logits (tests/golden/make_engine_golden.py);
+    variant "g16q8" is the artifact with the G16 head and Q8 gate rows."""
+    path = GOLDEN_0P8B if variant == "q4" else os.path.join(GOLDEN_DIR, f"engine_0p8b_{variant}.npz")
+    with np.load(path) as f:
         return {k: np.ascontiguousarray(f[k]) for k in f.files}
 
 
-def write_0p8b_artifact(q, directory, seed, weight_std):
+def write_0p8b_artifact(q, directory, seed, weight_std, variant="q4"):
     d, sched = q.model_dims(0)
     path = os.path.join(directory, "model.q35h128")
-    q.write_random_artifact(path, d, sched, seed=seed, weight_std=weight_std)
+    alt = variant != "q4"
+    q.write_random_artifact(path, d, sched, seed=seed, weight_std=weight_std, head_g16=alt, q8_gates=alt)
     return d, sched, path
 
 

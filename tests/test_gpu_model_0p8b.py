@@ -20,12 +20,14 @@ from tests.model_util import (check_within_envelope, golden_0p8b, reference_enve
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(scope="module")
-def m08(q, ctx, tmp_path_factory):
-    g = golden_0p8b()
-    print("0.8B: writing the random-init artifact", flush=True)
+@pytest.fixture(scope="module", params=["q4", "g16q8"])
+def m08(q, ctx, tmp_path_factory, request):
+    """The random-init 0.8B artifact, and the same model with the optional
+    encodings (G16 tied head, Q8_0 gate rows), each with its reference golden."""
+    g = golden_0p8b(request.param)
+    print(f"0.8B ({request.param}): writing the random-init artifact", flush=True)
     d, sched, path = write_0p8b_artifact(q, str(tmp_path_factory.mktemp("m08")), int(g["seed"][0]),
-                                         float(g["weight_std"][0]))
+                                         float(g["weight_std"][0]), request.param)
     print("0.8B: loading", flush=True)
     model = q.Model(ctx, d, sched, artifact=path)
     yield d, sched, model, g

@@ -17,11 +17,13 @@ from tests.model_util import (artifact_tensors, check_within_envelope, golden_0p
 ROWS = 2
 
 
-@pytest.fixture(scope="module")
-def artifact(q, tmp_path_factory):
-    g = golden_0p8b()
+@pytest.fixture(scope="module", params=["q4", "g16q8"])
+def artifact(q, tmp_path_factory, request):
+    """Both artifact variants: Q4 throughout, and the G16 tied head with Q8_0
+    gate rows (weights.inl:724-734, :1700-1747), each with its reference golden."""
+    g = golden_0p8b(request.param)
     d, sched, path = write_0p8b_artifact(q, str(tmp_path_factory.mktemp("m08")), int(g["seed"][0]),
-                                         float(g["weight_std"][0]))
+                                         float(g["weight_std"][0]), request.param)
     yield d, sched, path, g
     os.remove(path)
 
