@@ -526,7 +526,7 @@ def main():
     # traffic.json keys carry the artifact encodings ("head", "head_g16q8")
     sfx = "" if args.encodings == "q4" else f"_{args.encodings}"
     head_name = ("head_kernel<4, 3, NT, true, *> (greedy head: streaming Q4 GEMV + penalty + argmax, NT token tiles)"
-                 if not sfx else "head_kernel<4, 3, NT, true, 2, true> (greedy G16 head: Q4G16Tile GEMV, per-half "
+                 if not sfx else "head_kernel<4, 2, NT, true, *, true> (greedy G16 head: Q4G16Tile GEMV, per-half "
                  "MFMA dots + penalty + argmax)")
     roof = roofline("head" + sfx, prof["head"], traffic, head_name) if prof else None
     gemm_roof = roofline("gemm" + sfx, prof["gemm"], traffic, "gemm_kernel<8, false, false> (per-layer Q4 projections, split-K)") if prof else None

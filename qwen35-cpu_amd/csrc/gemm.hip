@@ -414,7 +414,8 @@ struct HeadChunk {
 // DOT4 codes). Each block's two 16-column halves are separate int8 dots:
 // MFMAs over the activations with the other half's K lanes zeroed, chained
 // per block as half 0 then half 1, acc = fma(float(dot), d_half * s, acc)
-// (q4_g16_matmul_wide, q4_g16_evex.cpp:25-49).
+// (q4_g16_matmul_wide, q4_g16_evex.cpp:25-49). G16 launches use a two-chunk
+// ring: with three, the second scale words spill at the head's occupancy.
 template <int KS, int R, int NT, bool ARGMAX, int OCC, bool G16>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void head_kernel(GemmArgs a,
                                                                                                int gpw) {
@@ -818,10 +819,10 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t stream) {
       const dim3 grid(hp.grid), block(64 * kHeadWaves);
 #define Q35_HEAD_G(NT, G16)                                                                                     \
   if (argmax) {                                                                                                 \
-    Q35_LAUNCH((head_kernel<kHeadKS, kHeadRing, NT, true, (G16 ? 2 : head_waves_per_simd(NT)), G16>), grid, block, hp.smem,  \
+    Q35_LAUNCH((head_kernel<kHeadKS, (G16 ? 2 : kHeadRing), NT, true, head_waves_per_simd(NT), G16>), grid, block, hp.smem,  \
                stream, a, hp.gpw);                                                                              \
   } else {                                                                                                      \
-    Q35_LAUNCH((head_kernel<kHeadKS, kHeadRing, NT, false, (G16 ? 2 : head_waves_per_simd(NT)), G16>), grid, block, hp.smem, \
+    Q35_LAUNCH((head_kernel<kHeadKS, (G16 ? 2 : kHeadRing), NT, false, head_waves_per_simd(NT), G16>), grid, block, hp.smem, \
                stream, a, hp.gpw);                                                                              \
   }
 #define Q35_HEAD(NT)         \
