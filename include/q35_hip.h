@@ -383,6 +383,38 @@ int q35_runtime_profile_reset(q35_runtime *rt);
 int q35_runtime_profile_read(q35_runtime *rt, int kernel_class, double *total_ms,
                              uint64_t *launches, double *algorithmic_bytes);
 
+/* Stage trace of the decode step (no reference counterpart: a test hook for
+ * stage-wise parity). While enabled, q35_runtime_step launches eagerly and,
+ * for every layer, keeps a device copy of each stage's input and output --
+ * the buffers the next kernel reads, plus the FP32 values a fused kernel
+ * quantizes -- so that a checker can restart every stage from the GPU's own
+ * input. Copies are addressed by (layer, point); the final norm's points use
+ * layer = n_layers. Shapes ([batch] rows unless noted):
+ *   X_IN      residual entering the layer [hidden]      NORMED_IN  input RMSNorm [hidden]
+ *   CODES_*   A16 codes [tiles][hidden-or-K / 32][64] u64, SCALES_* [tiles][K / 32][16] f32
+ *             (tiles = ceil(batch / 16); lane l of a block: token l % 16, columns 8(l / 16)..+7)
+ *   GATES     Q8 gate rows [gate_rows]                  PROJ_IN    in projection rows [in_rows]
+ *   STATE_*   linear: recurrent state read / written [v_heads][v_dim][k_dim]
+ *   CONV_*    linear: conv ring [kernel][channels] before / after (slot = position % kernel)
+ *   CORE      linear: gated-norm output [v_dim]; full: gated attention output [heads * head_dim]
+ *   Q_ROT, ATTN_GATE  full: [heads][head_dim]           K_POOL, V_POOL  full: the layer's pools
+ *   PROJ_OUT  out projection rows [hidden]              X_MID      residual after the attention block
+ *   NORMED_POST [hidden]   GATE_UP [2 * intermediate]   SILU [intermediate]   DOWN [hidden]
+ *   X_FINAL, HIDDEN (layer n_layers) final residual and final normalized rows [hidden] */
+enum {
+  Q35_TRACE_X_IN = 0, Q35_TRACE_NORMED_IN, Q35_TRACE_CODES_IN, Q35_TRACE_SCALES_IN, Q35_TRACE_GATES,
+  Q35_TRACE_PROJ_IN, Q35_TRACE_STATE_BEFORE, Q35_TRACE_STATE_AFTER, Q35_TRACE_CONV_BEFORE,
+  Q35_TRACE_CONV_AFTER, Q35_TRACE_CORE, Q35_TRACE_CODES_CORE, Q35_TRACE_SCALES_CORE, Q35_TRACE_Q_ROT,
+  Q35_TRACE_ATTN_GATE, Q35_TRACE_K_POOL, Q35_TRACE_V_POOL, Q35_TRACE_PROJ_OUT, Q35_TRACE_X_MID,
+  Q35_TRACE_NORMED_POST, Q35_TRACE_CODES_POST, Q35_TRACE_SCALES_POST, Q35_TRACE_GATE_UP, Q35_TRACE_SILU,
+  Q35_TRACE_CODES_DOWN, Q35_TRACE_SCALES_DOWN, Q35_TRACE_DOWN, Q35_TRACE_X_FINAL, Q35_TRACE_HIDDEN,
+  Q35_TRACE_CODES_HEAD, Q35_TRACE_SCALES_HEAD, Q35_TRACE_POINTS
+};
+int q35_runtime_set_trace(q35_runtime *rt, int enable);
+/* Copies the traced bytes of (layer, point) of the last step into `out`
+ * (at most `capacity` bytes); *bytes receives the traced size (0: none). */
+int q35_runtime_trace_read(q35_runtime *rt, int layer, int point, void *out, size_t capacity, size_t *bytes);
+
 /* ================================================================= engine
  * C mirror of qwen35x::CpuEngine (include/qwen35x/runtime/cpu_engine.h:173-215)
  * for greedy requests, built on the runtime above. IDs are monotonic and never

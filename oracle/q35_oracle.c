@@ -643,6 +643,33 @@ static void full_step(const q35o_dims *d, const q35o_layer *L, uint16_t *keys, u
   free(vrow);
 }
 
+/* Stage entry points for stage-wise parity: one row of one layer's
+ * attention block from given inputs (the same routines the whole step runs). */
+int q35o_linear_attention_row(const q35o_dims *d, const q35o_layer *L, float *conv_state, size_t *ring,
+                              float *recurrent, const float *projected, float *core) {
+  const size_t q_dim = (size_t)d->lin_k_heads * d->lin_k_dim;
+  const size_t v_dim = (size_t)d->lin_v_heads * d->lin_v_dim;
+  const size_t ch = 2 * q_dim + v_dim;
+  const size_t n = 16 * (ch + 2 * v_dim) + (size_t)d->lin_kernel * ch + 4 * v_dim + 64;
+  float *tmp = (float *)malloc(n * sizeof(float));
+  if (!tmp) return -1;
+  linear_step(d, L, conv_state, ring, recurrent, projected, core, tmp);
+  free(tmp);
+  return 0;
+}
+
+int q35o_full_attention_row(const q35o_dims *d, const q35o_layer *L, uint16_t *keys, uint16_t *values,
+                            size_t position, const float *cosine, const float *sine, const float *projected,
+                            float *core) {
+  const size_t full_core = (size_t)d->n_heads * d->head_dim;
+  const size_t n = 4 * full_core + (size_t)d->n_kv_heads * d->head_dim + (size_t)d->n_heads * (position + 1) + 64;
+  float *tmp = (float *)malloc(n * sizeof(float));
+  if (!tmp) return -1;
+  full_step(d, L, keys, values, position, cosine, sine, projected, core, tmp);
+  free(tmp);
+  return 0;
+}
+
 int q35o_forward_batch(const q35o_dims *d, const q35o_weights *w, q35o_state *const *states,
                        const int32_t *tokens, size_t batch, float penalty, int32_t *out_tokens,
                        float *out_logits, float *out_hidden) {

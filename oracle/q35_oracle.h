@@ -140,6 +140,22 @@ int q35o_forward_batch(const q35o_dims *d, const q35o_weights *w, q35o_state *co
                        const int32_t *tokens, size_t batch, float penalty, int32_t *out_tokens,
                        float *out_logits, float *out_hidden);
 
+/* Stage entry points (stage-wise parity): one row of one layer.
+ * linear: run_linear_attention_step (layers.inl:36-217) from the projected
+ * row [qkv | z | b | a] (with Q8 gate rows, their two outputs take the
+ * place of b and a), the conv state [(kernel-1)][channels] with its ring
+ * index (both advanced) and the recurrent state [v_heads][v_dim][k_dim]
+ * (updated); core receives the gated-norm output [v_heads * v_dim].
+ * full: prepare_full_attention_row + run_full_attention_step
+ * (layers.inl:221-395) at `position`; keys/values [position + 1][kv_width]
+ * binary16 receive the new row; cosine/sine are the RoPE row of `position`.
+ * Both return 0, or -1 when the scratch allocation fails. */
+int q35o_linear_attention_row(const q35o_dims *d, const q35o_layer *L, float *conv_state, size_t *ring,
+                              float *recurrent, const float *projected, float *core);
+int q35o_full_attention_row(const q35o_dims *d, const q35o_layer *L, uint16_t *keys, uint16_t *values,
+                            size_t position, const float *cosine, const float *sine, const float *projected,
+                            float *core);
+
 #ifdef __cplusplus
 }
 #endif

@@ -222,6 +222,25 @@ def q8_matmul(blocks8, mscales, act1, rows, count, blocks, stride=None):
     return out
 
 
+def silu_mul(gate, up):
+    """silu_mul_f32 (activation.cpp:329-357) over matching FP32 vectors."""
+    gate = np.ascontiguousarray(gate, np.float32)
+    up = np.ascontiguousarray(up, np.float32)
+    out = np.zeros_like(gate)
+    lib.q35o_silu_mul(ptr(gate), ptr(up), ptr(out), gate.size)
+    return out
+
+
+def rms_norm(x, w, eps, offset):
+    """rms_norm_f32 (activation.cpp:224-262) over the rows of x [rows][width]."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    rows, width = x.reshape(-1, x.shape[-1]).shape
+    out = np.zeros_like(x)
+    lib.q35o_rms_norm(ptr(x), ptr(w), ptr(out), rows, width, eps, offset)
+    return out
+
+
 def dot4_matvec(packed, act1, rows, blocks):
     out = np.zeros(rows, np.float32)
     lib.q35o_dot4_matvec(ptr(packed), ptr(act1), ptr(out), rows, blocks)
@@ -318,6 +337,10 @@ class State(ctypes.Structure):
                 ("position", c_size_t), ("capacity", c_size_t)]
 
 
+lib.q35o_linear_attention_row.restype = c_int
+lib.q35o_linear_attention_row.argtypes = [POINTER(Dims), POINTER(Layer), P, POINTER(c_size_t), P, P, P]
+lib.q35o_full_attention_row.restype = c_int
+lib.q35o_full_attention_row.argtypes = [POINTER(Dims), POINTER(Layer), P, P, c_size_t, P, P, P, P]
 lib.q35o_forward_batch.restype = c_int
 lib.q35o_forward_batch.argtypes = [POINTER(Dims), POINTER(Weights), POINTER(POINTER(State)), P, c_size_t,
                                    c_float, P, P, P]
@@ -370,6 +393,39 @@ class OracleModel:
         g16 = t[emb][0] == 8  # q4_g16_cpu_dot4
         self.w = Weights(None if g16 else get(emb), get(emb) if g16 else None,
                          get("model.language_model.norm.weight"), self.layers)
+
+    def linear_row(self, layer, conv_state, ring, recurrent, projected):
+        """run_linear_attention_step for one row from given inputs: returns
+        (core, conv_state, ring, recurrent) after the step (inputs are copied)."""
+        d = self.d
+        conv = np.array(conv_state, np.float32).ravel()
+        rec = np.array(recurrent, np.float32).ravel()
+        proj = np.ascontiguousarray(projected, np.float32)
+        core = np.zeros(d.lin_v_heads * d.lin_v_dim, np.float32)
+        r = c_size_t(int(ring))
+        rc = lib.q35o_linear_attention_row(ctypes.byref(self.d), ctypes.byref(self.layers[layer]), ptr(conv),
+                                           ctypes.byref(r), ptr(rec), ptr(proj), ptr(core))
+        assert rc == 0
+        return core, conv, r.value, rec
+
+    def full_row(self, layer, keys, values, position, projected):
+        """prepare_full_attention_row + run_full_attention_step for one row:
+        keys/values [position + 1][kv_width] binary16 (the row at `position`
+        is written); returns (core, keys, values)."""
+        d = self.d
+        half = d.rope_dim // 2
+        cs = np.zeros((position + 1) * half, np.float32)
+        sn = np.zeros_like(cs)
+        lib.q35o_rope_tables(c_float(d.rope_theta), d.rope_dim, position + 1, ptr(cs), ptr(sn))
+        k = np.array(keys, np.uint16).ravel()
+        v = np.array(values, np.uint16).ravel()
+        proj = np.ascontiguousarray(projected, np.float32)
+        core = np.zeros(d.n_heads * d.head_dim, np.float32)
+        rc = lib.q35o_full_attention_row(ctypes.byref(self.d), ctypes.byref(self.layers[layer]), ptr(k), ptr(v),
+                                         position, ptr(cs[position * half:]), ptr(sn[position * half:]), ptr(proj),
+                                         ptr(core))
+        assert rc == 0
+        return core, k, v
 
     def new_state(self, capacity, prompt):
         d = self.d

@@ -110,6 +110,13 @@ class PrefixStats(ctypes.Structure):
                 ("prefix_bytes", c_uint64)]
 
 
+# Stage trace points (include/q35_hip.h, Q35_TRACE_*), in enum order.
+TRACE_POINTS = ["X_IN", "NORMED_IN", "CODES_IN", "SCALES_IN", "GATES", "PROJ_IN", "STATE_BEFORE", "STATE_AFTER",
+                "CONV_BEFORE", "CONV_AFTER", "CORE", "CODES_CORE", "SCALES_CORE", "Q_ROT", "ATTN_GATE", "K_POOL",
+                "V_POOL", "PROJ_OUT", "X_MID", "NORMED_POST", "CODES_POST", "SCALES_POST", "GATE_UP", "SILU",
+                "CODES_DOWN", "SCALES_DOWN", "DOWN", "X_FINAL", "HIDDEN", "CODES_HEAD", "SCALES_HEAD"]
+TRACE = {name: i for i, name in enumerate(TRACE_POINTS)}
+
 P = c_void_p
 _SIGS = {
     "q35_context_create": (c_int, [c_int, P, POINTER(P)]),
@@ -171,6 +178,8 @@ _SIGS = {
     "q35_runtime_prefill": (c_int, [P, c_int32, c_int32, P, c_int32, P, c_int32, c_float, P]),
     "q35_runtime_last_hidden": (c_int, [P, P, c_size_t]),
     "q35_runtime_set_profiling": (c_int, [P, c_int]),
+    "q35_runtime_set_trace": (c_int, [P, c_int]),
+    "q35_runtime_trace_read": (c_int, [P, c_int, c_int, P, c_size_t, POINTER(c_size_t)]),
     "q35_runtime_profile_reset": (c_int, [P]),
     "q35_runtime_profile_read": (c_int, [P, c_int, POINTER(c_double), POINTER(c_uint64), POINTER(c_double)]),
     "q35_engine_create": (c_int, [P, POINTER(EngineConfig), POINTER(P)]),
@@ -551,6 +560,46 @@ class Runtime(_Profiled):
                                                _ptr(table), table.size, float(penalty), _ptr(out)),
                        "runtime prefill")
         return int(out[0])
+
+    def head(self, slot, hidden, penalty=1.0):
+        """Greedy head of one final normalized hidden row with the slot's
+        penalty counts (q35_runtime_head)."""
+        hidden = np.ascontiguousarray(hidden, np.float32)
+        out = c_int32()
+        self.ctx.check(lib.q35_runtime_head(self.handle, int(slot), _ptr(hidden), float(penalty), ctypes.byref(out)),
+                       "runtime head")
+        return out.value
+
+    def head_candidates(self, slot, hidden, top_k, inv_temperature, penalty=1.0, raw_logits=False):
+        """Sampling candidates of one final normalized hidden row
+        (q35_runtime_head_candidates): [64] values and tokens, and the raw
+        logits [vocab] when asked."""
+        hidden = np.ascontiguousarray(hidden, np.float32)
+        rs = RowSampling(int(top_k), float(inv_temperature))
+        cand = (Candidate * MAX_CANDIDATES)()
+        lg = np.empty(self.model.dims.vocab, np.float32) if raw_logits else None
+        self.ctx.check(lib.q35_runtime_head_candidates(self.handle, int(slot), _ptr(hidden), float(penalty),
+                                                       ctypes.byref(rs), ctypes.byref(cand), _ptr(lg)),
+                       "head candidates")
+        arr = np.frombuffer(cand, dtype=np.dtype([("value", np.float32), ("token", np.int32)])).copy()
+        return (arr, lg) if raw_logits else arr
+
+    def set_trace(self, enable=True):
+        """Stage trace of the next steps (q35_runtime_set_trace, a test hook)."""
+        self.ctx.check(lib.q35_runtime_set_trace(self.handle, int(enable)), "set trace")
+
+    def trace(self, layer, point, dtype=np.float32):
+        """The traced bytes of (layer, point) of the last step as a flat array
+        of `dtype` (None when the step did not trace that point)."""
+        n = c_size_t()
+        self.ctx.check(lib.q35_runtime_trace_read(self.handle, int(layer), int(point), None, 0, ctypes.byref(n)),
+                       "trace size")
+        if n.value == 0:
+            return None
+        out = np.empty(n.value // np.dtype(dtype).itemsize, dtype)
+        self.ctx.check(lib.q35_runtime_trace_read(self.handle, int(layer), int(point), _ptr(out), out.nbytes,
+                                                  ctypes.byref(n)), "trace read")
+        return out
 
     def _rt(self):
         return self.handle

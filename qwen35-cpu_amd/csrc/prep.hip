@@ -48,7 +48,11 @@ __global__ __launch_bounds__(kPrepThreads) void prep_kernel(PrepArgs a) {
   const int item = active ? item0 : items - 1;  // idle rows redo a valid item and store nothing
   const int t = item / nblk, blk = item - t * nblk;
   float v[8];
-  load_source8<SRC, MS>(a, t, blk * 128 + 8 * (threadIdx.x & 15), v);
+  const int c0 = blk * 128 + 8 * (threadIdx.x & 15);
+  load_source8<SRC, MS>(a, t, c0, v);
+  if (a.y_out != nullptr && active)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a.y_out[static_cast<size_t>(t) * K + c0 + e] = v[e];
   QuantOut o;
   o.codes = a.codes;
   o.scales = a.scales;

@@ -139,6 +139,7 @@ struct PrepArgs {
   float *scales = nullptr;
   q35_q8_0_block_x4 *x4 = nullptr; // reference X4 layout (optional)
   q35_q8_0_block_x1 *x1 = nullptr; // reference X1 layout (optional)
+  float *y_out = nullptr;          // optional FP32 source rows [tokens][K] (before the rotation)
 };
 hipError_t launch_prep(const PrepArgs &a, hipStream_t stream);
 

@@ -61,10 +61,14 @@ __device__ __forceinline__ void q8_block_codes8(const float v[8], uint64_t &word
   stored = half_bits_to_float(float_to_half_bits(scale));
 }
 
-// All 64 lanes of the wavefront call this (the DPP moves need every lane of
-// each row); rows whose `active` is false store nothing.
-__device__ __forceinline__ void h128_quantize_row16(float v[8], int t, int blk, int nb, bool h128,
-                                                    uint64_t seed, const QuantOut &o, bool active) {
+// The rotation and quantization of one (token, 128-column block) item held
+// by a 16-lane row, lane j = lane % 16 holding columns 8j .. 8j+7: `word`
+// receives the lane's eight int8 codes (one A16 word: k-group j % 4 of block
+// 4*blk + j/4), `sum` their block's code sum and `stored` the block's
+// binary16-rounded scale (times 1/sqrt(128) in the H128 basis). All 64 lanes
+// of the wavefront call it (the DPP moves need every lane of each row).
+__device__ __forceinline__ void h128_quantize_core(float v[8], int blk, bool h128, uint64_t seed, uint64_t &word,
+                                                   int &sum, float &stored) {
   const int j = __lane_id() & 15;
   if (h128) {
     const uint64_t w = h128_sign_word(blk, j >> 3, seed);
@@ -98,8 +102,8 @@ __device__ __forceinline__ void h128_quantize_row16(float v[8], int t, int blk, 
   amax = fmaxf(amax, q35_row_xor(amax, 2));
   const float scale = amax / 127.0F;
   const float inv = scale == 0.0F ? 0.0F : 1.0F / scale;
-  uint64_t word = 0;
-  int sum = 0;
+  word = 0;
+  sum = 0;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     float r = roundf(v[e] * inv);
@@ -110,9 +114,20 @@ __device__ __forceinline__ void h128_quantize_row16(float v[8], int t, int blk, 
   }
   sum += q35_row_xor_i(sum, 1);
   sum += q35_row_xor_i(sum, 2);
-  if (!active) return;
-  float stored = half_bits_to_float(float_to_half_bits(scale));
+  stored = half_bits_to_float(float_to_half_bits(scale));
   if (h128) stored *= kH128InvSqrt;
+}
+
+// All 64 lanes of the wavefront call this (the DPP moves need every lane of
+// each row); rows whose `active` is false store nothing.
+__device__ __forceinline__ void h128_quantize_row16(float v[8], int t, int blk, int nb, bool h128,
+                                                    uint64_t seed, const QuantOut &o, bool active) {
+  const int j = __lane_id() & 15;
+  uint64_t word;
+  int sum;
+  float stored;
+  h128_quantize_core(v, blk, h128, seed, word, sum, stored);
+  if (!active) return;
   const int b = blk * 4 + (j >> 2), kg = j & 3;
   const int tile = t >> 4, tok = t & 15;
   if (o.codes != nullptr) {

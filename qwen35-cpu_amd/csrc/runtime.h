@@ -95,6 +95,9 @@ struct q35_runtime {
   bool profiling = false;
   std::vector<std::pair<hipEvent_t, hipEvent_t>> prof_events;
   std::vector<std::pair<int, double>> prof_pending;
+  // stage trace (test hook): (layer, point) -> device copy and its size
+  bool tracing = false;
+  std::map<std::pair<int, int>, std::pair<void *, size_t>> trace;
   double prof_ms[Q35_KERNEL_CLASSES] = {};
   double prof_bytes[Q35_KERNEL_CLASSES] = {};
   uint64_t prof_launches[Q35_KERNEL_CLASSES] = {};

@@ -259,6 +259,11 @@ extern "C" int q35_model_upload_tensor(q35_model *m, const char *name_c, int enc
       if (st == Q35_OK && (encoding != Q35_ENC_Q8_0 || H % 32 != 0 || rows > static_cast<uint64_t>(kMaxGateRows) ||
                            count != rows * nb * 34))
         st = set_error(m->ctx, Q35_ERR_INVALID, "wrong Q8_0 payload for " + name);
+      // the input-norm kernel stages every (gate row, 32-column block) dot in LDS
+      if (st == Q35_OK && rows * nb > static_cast<uint64_t>(kMaxGateItems))
+        st = set_error(m->ctx, Q35_ERR_UNSUPPORTED,
+                       name + ": gate rows x hidden/32 exceeds the " + std::to_string(kMaxGateItems) +
+                           " (row, block) items the input-norm kernel stages");
       std::vector<int8_t> codes(rows * H);
       std::vector<float> scales(rows * nb);
       const uint8_t *b = static_cast<const uint8_t *>(bytes);
@@ -487,6 +492,7 @@ extern "C" void q35_runtime_destroy(q35_runtime *rt) {
   for (auto &kv : rt->graphs) (void)hipGraphExecDestroy(kv.second);
   for (auto &ev : rt->prof_events) (void)hipEventDestroy(ev.first), (void)hipEventDestroy(ev.second);
   for (void *p : rt->allocations) (void)hipFree(p);
+  for (auto &kv : rt->trace) (void)hipFree(kv.second.first);
   if (rt->meta_host) (void)hipHostFree(rt->meta_host);
   if (rt->tokens_out_host) (void)hipHostFree(rt->tokens_out_host);
   delete rt;
@@ -640,6 +646,27 @@ static GemmArgs greedy_head_args(q35_runtime *rt, int tokens, const int32_t *cou
   return g;
 }
 
+// Stage trace: the device copy of (layer, point), grown to `bytes`.
+static hipError_t trace_slot(q35_runtime *rt, int layer, int point, size_t bytes, void **out) {
+  auto &e = rt->trace[std::make_pair(layer, point)];
+  if (e.first == nullptr || e.second < bytes) {
+    if (e.first != nullptr) (void)hipFree(e.first);
+    e.first = nullptr;
+    const hipError_t err = hipMalloc(&e.first, bytes ? bytes : 1);
+    if (err != hipSuccess) return err;
+  }
+  e.second = bytes;
+  *out = e.first;
+  return hipSuccess;
+}
+
+static hipError_t trace_copy(q35_runtime *rt, int layer, int point, const void *src, size_t bytes, hipStream_t s) {
+  void *dst = nullptr;
+  hipError_t e = trace_slot(rt, layer, point, bytes, &dst);
+  if (e == hipSuccess) e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s);
+  return e;
+}
+
 int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool prefill) {
   q35_model *m = rt->model;
   Context *ctx = rt->ctx;
@@ -757,13 +784,70 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
     return gemm_algorithmic_bytes(rows, K / 32, batch, true, false) + (p.split - 1) * B * rows * 4.0;
   };
 
+  // Stage trace (test hook, decode steps only): copies of the stage inputs
+  // and outputs; the split GEMM outputs are summed in split order into the
+  // copy, exactly as their consumer sums them.
+  const bool tracing = rt->tracing && !prefill;
+  const auto *host_slots = reinterpret_cast<const int32_t *>(rt->meta_host + ml.slots);
+  const auto *host_pos = reinterpret_cast<const int32_t *>(rt->meta_host + ml.positions);
+  const size_t code_tiles = (batch + 15) / 16;
+  auto trace_codes = [&](int layer, int point_codes, int K) -> hipError_t {
+    hipError_t te = trace_copy(rt, layer, point_codes, rt->codes, code_tiles * (K / 32) * 64 * 8, s);
+    if (te == hipSuccess) te = trace_copy(rt, layer, point_codes + 1, rt->scales, code_tiles * (K / 32) * 16 * 4, s);
+    return te;
+  };
+  auto trace_rows = [&](int layer, int point, int width) -> hipError_t {
+    void *dst = nullptr;
+    hipError_t te = trace_slot(rt, layer, point, static_cast<size_t>(batch) * width * 4, &dst);
+    if (te == hipSuccess) te = launch_split_reduce(pending, batch, static_cast<float *>(dst), width, nullptr, s);
+    return te;
+  };
+  auto trace_fp32 = [&](int layer, int point, int width) -> float * {
+    void *dst = nullptr;
+    return trace_slot(rt, layer, point, static_cast<size_t>(batch) * width * 4, &dst) == hipSuccess
+               ? static_cast<float *>(dst) : nullptr;
+  };
+  // per-row copies of a linear layer's recurrent state (copy `which` of the
+  // position: 0 = read, 1 = written) and conv ring
+  auto trace_state = [&](int l, int li, int point, int which) -> hipError_t {
+    const size_t head_floats = static_cast<size_t>(d.lin_v_heads) * d.lin_v_dim * d.lin_k_dim;
+    void *dst = nullptr;
+    hipError_t te = trace_slot(rt, l, point, batch * head_floats * 4, &dst);
+    for (int b = 0; te == hipSuccess && b < batch; ++b) {
+      const int copy = (host_pos[b] & 1) ^ which;
+      const float *src = rt->recurrent + host_slots[b] * rt->rec_slot_stride + copy * rt->rec_copy_stride +
+                         static_cast<size_t>(li) * head_floats;
+      te = hipMemcpyAsync(static_cast<float *>(dst) + b * head_floats, src, head_floats * 4, hipMemcpyDeviceToDevice, s);
+    }
+    return te;
+  };
+  auto trace_conv = [&](int l, int li, int point) -> hipError_t {
+    const size_t ring = static_cast<size_t>(d.lin_kernel) * ch;
+    void *dst = nullptr;
+    hipError_t te = trace_slot(rt, l, point, batch * ring * 4, &dst);
+    for (int b = 0; te == hipSuccess && b < batch; ++b) {
+      const float *src = rt->conv + host_slots[b] * rt->conv_slot_stride + static_cast<size_t>(li) * ring;
+      te = hipMemcpyAsync(static_cast<float *>(dst) + b * ring, src, ring * 4, hipMemcpyDeviceToDevice, s);
+    }
+    return te;
+  };
+
   bool add_pending = false;  // the previous layer's down projection is still split
   for (int l = 0; l < d.n_layers; ++l) {
     const LayerDev &L = m->layers[l];
-    Q35_KERNEL(Q35_KERNEL_PREP, rms_bytes(add_pending), rms_prep(L.input_norm, add_pending, true, nullptr, L.linear ? &L : nullptr),
+    float *normed_in = tracing ? trace_fp32(l, Q35_TRACE_NORMED_IN, H) : nullptr;
+    Q35_KERNEL(Q35_KERNEL_PREP, rms_bytes(add_pending), rms_prep(L.input_norm, add_pending, true, normed_in, L.linear ? &L : nullptr),
                "input norm prep");
+    if (tracing) {
+      Q35_STEP(trace_copy(rt, l, Q35_TRACE_X_IN, rt->x[cur], static_cast<size_t>(batch) * H * 4, s), "trace");
+      Q35_STEP(trace_codes(l, Q35_TRACE_CODES_IN, H), "trace");
+      if (L.gate_rows > 0)
+        Q35_STEP(trace_copy(rt, l, Q35_TRACE_GATES, rt->q8_gates, static_cast<size_t>(batch) * L.gate_rows * 4, s),
+                 "trace");
+    }
     Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(L.in_rows, H, kConsumerSplits),
                gemm(L.in_proj, L.in_rows, H, kConsumerSplits), "in projection");
+    if (tracing) Q35_STEP(trace_rows(l, Q35_TRACE_PROJ_IN, L.in_rows), "trace");
     if (L.linear) {
       const int li = m->linear_index[l];
       DeltaArgs a;
@@ -808,7 +892,17 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
       const double delta_bytes =
           B * (2.0 * d.lin_v_heads * d.lin_v_dim * d.lin_k_dim * 4.0 + pending.splits * L.in_rows * 4.0 +
                static_cast<double>(d.lin_kernel) * ch * 4.0 + v_dim + v_dim / 32.0 * 4.0);
+      if (tracing) {
+        Q35_STEP(trace_state(l, li, Q35_TRACE_STATE_BEFORE, 0), "trace");
+        Q35_STEP(trace_conv(l, li, Q35_TRACE_CONV_BEFORE), "trace");
+        a.out = trace_fp32(l, Q35_TRACE_CORE, v_dim);
+      }
       Q35_KERNEL(Q35_KERNEL_DELTA, delta_bytes, (prefill ? launch_delta_chunk(a, s) : launch_delta(a, s)), "DeltaNet");
+      if (tracing) {
+        Q35_STEP(trace_state(l, li, Q35_TRACE_STATE_AFTER, 1), "trace");
+        Q35_STEP(trace_conv(l, li, Q35_TRACE_CONV_AFTER), "trace");
+        Q35_STEP(trace_codes(l, Q35_TRACE_CODES_CORE, v_dim), "trace");
+      }
     } else {
       const int fi = m->full_index[l];
       AttnPrepArgs p;
@@ -835,6 +929,13 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
       Q35_KERNEL(Q35_KERNEL_ATTN_PREP,
                  B * (pending.splits * L.in_rows * 4.0 + 2.0 * d.n_heads * d.head_dim * 4.0 + 2.0 * kvw * 2.0),
                  launch_attn_prep(p, s), "attention prep");
+      if (tracing) {
+        const size_t qb = static_cast<size_t>(batch) * d.n_heads * d.head_dim * 4;
+        Q35_STEP(trace_copy(rt, l, Q35_TRACE_Q_ROT, rt->q_rot, qb, s), "trace");
+        Q35_STEP(trace_copy(rt, l, Q35_TRACE_ATTN_GATE, rt->gates, qb, s), "trace");
+        Q35_STEP(trace_copy(rt, l, Q35_TRACE_K_POOL, p.k_pool, rt->layer_pool_elems * 2, s), "trace");
+        Q35_STEP(trace_copy(rt, l, Q35_TRACE_V_POOL, p.v_pool, rt->layer_pool_elems * 2, s), "trace");
+      }
       AttnArgs a;
       a.q = rt->q_rot;
       a.k_pool = p.k_pool;
@@ -862,13 +963,23 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
       Q35_KERNEL(Q35_KERNEL_PREP,
                  splits_used * d.n_heads * (d.head_dim + 2) * 4.0 + B * d.n_heads * d.head_dim * (4.0 + 1.0) +
                      B * d.n_heads * d.head_dim / 32.0 * 4.0,
-                 launch_attention_merge(a, rt->gates, nullptr, rt->codes, rt->scales, d.sign_seed, s),
+                 launch_attention_merge(a, rt->gates, tracing ? trace_fp32(l, Q35_TRACE_CORE, d.n_heads * d.head_dim)
+                                                              : nullptr,
+                                        rt->codes, rt->scales, d.sign_seed, s),
                  "attention merge");
+      if (tracing) Q35_STEP(trace_codes(l, Q35_TRACE_CODES_CORE, d.n_heads * d.head_dim), "trace");
     }
     Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(H, L.out_cols), gemm(L.out_proj, H, L.out_cols), "out projection");
-    Q35_KERNEL(Q35_KERNEL_PREP, rms_bytes(true), rms_prep(L.post_norm, true, true, nullptr), "post norm prep");
+    if (tracing) Q35_STEP(trace_rows(l, Q35_TRACE_PROJ_OUT, H), "trace");
+    float *normed_post = tracing ? trace_fp32(l, Q35_TRACE_NORMED_POST, H) : nullptr;
+    Q35_KERNEL(Q35_KERNEL_PREP, rms_bytes(true), rms_prep(L.post_norm, true, true, normed_post), "post norm prep");
+    if (tracing) {
+      Q35_STEP(trace_copy(rt, l, Q35_TRACE_X_MID, rt->x[cur], static_cast<size_t>(batch) * H * 4, s), "trace");
+      Q35_STEP(trace_codes(l, Q35_TRACE_CODES_POST, H), "trace");
+    }
     Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(2 * I, H, kConsumerSplits), gemm(L.gate_up, 2 * I, H, kConsumerSplits),
                "gate_up projection");
+    if (tracing) Q35_STEP(trace_rows(l, Q35_TRACE_GATE_UP, 2 * I), "trace");
     PrepArgs sp;
     sp.source = kPrepSiluMul;
     sp.gate_up = pending;
@@ -878,9 +989,12 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
     sp.seed = d.sign_seed;
     sp.codes = rt->codes;
     sp.scales = rt->scales;
+    if (tracing) sp.y_out = trace_fp32(l, Q35_TRACE_SILU, I);
     Q35_KERNEL(Q35_KERNEL_PREP, B * (pending.splits * 2.0 * I * 4.0 + I + I / 32.0 * 4.0), launch_prep(sp, s),
                "silu prep");
+    if (tracing) Q35_STEP(trace_codes(l, Q35_TRACE_CODES_DOWN, I), "trace");
     Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(H, I), gemm(L.down, H, I), "down projection");
+    if (tracing) Q35_STEP(trace_rows(l, Q35_TRACE_DOWN, H), "trace");
     add_pending = true;
   }
   // A prefill chunk needs the head only for its last position: the final
@@ -907,6 +1021,12 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
   } else {
     Q35_KERNEL(Q35_KERNEL_PREP, rms_bytes(true) + B * H * 4.0, rms_prep(m->final_norm, true, false, rt->hidden_out),
                "final norm prep");
+    if (tracing) {
+      const int fl = d.n_layers;
+      Q35_STEP(trace_copy(rt, fl, Q35_TRACE_X_FINAL, rt->x[cur], static_cast<size_t>(batch) * H * 4, s), "trace");
+      Q35_STEP(trace_copy(rt, fl, Q35_TRACE_HIDDEN, rt->hidden_out, static_cast<size_t>(batch) * H * 4, s), "trace");
+      Q35_STEP(trace_codes(fl, Q35_TRACE_CODES_HEAD, H), "trace");
+    }
   }
   const double HB = head_tokens;
   if (want_logits) {
@@ -1003,7 +1123,7 @@ int ensure_logits(q35_runtime *rt) {
 int launch_step(q35_runtime *rt, int B, bool want_logits) {
   Context *ctx = rt->ctx;
   int st = Q35_OK;
-  if (rt->cfg.use_graphs && !rt->profiling) {
+  if (rt->cfg.use_graphs && !rt->profiling && !rt->tracing) {
     const auto key = std::make_pair(B, want_logits ? 1 : 0);
     auto it = rt->graphs.find(key);
     if (it == rt->graphs.end()) {
@@ -1176,6 +1296,7 @@ extern "C" int q35_runtime_head_candidates(q35_runtime *rt, int32_t slot, const 
   Q35_HIP_TRY(ctx, launch_prep(p, s));
   GemmArgs g;
   g.w = rt->model->embed;
+  g.g16 = rt->model->embed_g16;
   g.rows = d.vocab;
   g.nb = d.hidden / 32;
   g.codes = rt->codes;
@@ -1218,6 +1339,24 @@ extern "C" int q35_runtime_profile_read(q35_runtime *rt, int cls, double *total_
   if (total_ms) *total_ms = rt->prof_ms[cls];
   if (launches) *launches = rt->prof_launches[cls];
   if (bytes) *bytes = rt->prof_bytes[cls];
+  return Q35_OK;
+}
+
+extern "C" int q35_runtime_set_trace(q35_runtime *rt, int enable) {
+  if (rt == nullptr) return Q35_ERR_INVALID;
+  rt->tracing = enable != 0;
+  return Q35_OK;
+}
+
+extern "C" int q35_runtime_trace_read(q35_runtime *rt, int layer, int point, void *out, size_t capacity,
+                                      size_t *bytes) {
+  if (rt == nullptr || point < 0 || point >= Q35_TRACE_POINTS) return Q35_ERR_INVALID;
+  auto it = rt->trace.find(std::make_pair(layer, point));
+  const size_t n = it == rt->trace.end() ? 0 : it->second.second;
+  if (bytes != nullptr) *bytes = n;
+  if (n == 0 || out == nullptr) return Q35_OK;
+  Q35_HIP_TRY(rt->ctx, hipStreamSynchronize(rt->ctx->stream));
+  Q35_HIP_TRY(rt->ctx, hipMemcpy(out, it->second.first, std::min(n, capacity), hipMemcpyDeviceToHost));
   return Q35_OK;
 }
 

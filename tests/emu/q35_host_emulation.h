@@ -34,6 +34,7 @@ using std::isnan;
 #define __host__
 #define __forceinline__ inline
 #define __launch_bounds__(...)
+#define __align__(n) alignas(n)
 // Blocks of one launch run one after another, so a function-local static is a
 // faithful per-block shared array.
 #define __shared__ static
@@ -198,6 +199,22 @@ inline unsigned long long atomicMax(unsigned long long *p, unsigned long long v)
 }
 inline unsigned __float_as_uint(float f) { unsigned u; std::memcpy(&u, &f, 4); return u; }
 inline int __builtin_amdgcn_readlane(int v, int src) { return ::q35emu::readlane(v, src); }
+// value of `v` in lane `src` (per lane) of the wavefront; every lane calls it
+template <typename T>
+inline T __shfl(T v, int src, int width = 64) {
+  (void)width;
+  static_assert(sizeof(T) <= 8, "shuffle of at most 8 bytes");
+  auto &slots = ::q35emu::t_ctx.launch->slots_a[::q35emu::t_ctx.wave];
+  uint64_t bits = 0;
+  std::memcpy(&bits, &v, sizeof(T));
+  slots[::q35emu::t_ctx.lane] = bits;
+  ::q35emu::wave_sync();
+  const uint64_t got = slots[src & 63];
+  ::q35emu::wave_sync();
+  T r;
+  std::memcpy(&r, &got, sizeof(T));
+  return r;
+}
 inline int __float_as_int(float f) { int u; std::memcpy(&u, &f, 4); return u; }
 inline float __int_as_float(int u) { float f; std::memcpy(&f, &u, 4); return f; }
 inline float __uint_as_float(unsigned u) { float f; std::memcpy(&f, &u, 4); return f; }

@@ -9,22 +9,28 @@ the prefix ending inside a page (the shared tail page is copied on the first
 write, kv_pages.h:52-60) or on a page boundary, with two requests sharing one
 prefix in the same decode batch, and for a complete hit (prompt == prefix)
 whose first token comes from its own greedy head on the stored hidden row
-(cpu_engine.inl:711-726), with and without a repetition penalty."""
+(cpu_engine.inl:711-726), with and without a repetition penalty. The
+from-scratch tokens are themselves checked against the CPU oracle, so a
+prefix hit is tied to the restated reference step, not only to this engine.""" 
 import numpy as np
 import pytest
 
-from tests.model_util import build_small_model, small_dims, upload_model
+from tests.model_util import build_small_model, oracle_greedy, small_dims, upload_model
 
 pytestmark = pytest.mark.gpu
 
 NEW = 6
 
 
-@pytest.fixture(scope="module")
-def small(q, ctx):
+@pytest.fixture(scope="module", params=["q4", "g16q8"])
+def small(q, ctx, request):
+    """The small hybrid model, with the default encodings and with the G16
+    tied head plus Q8 gate rows (a complete hit runs the head itself)."""
     d, sched = small_dims()
-    tensors = build_small_model(d, sched, seed=13)
+    alt = request.param == "g16q8"
+    tensors = build_small_model(d, sched, seed=13, head_g16=alt, q8_gates=alt)
     model = upload_model(q, ctx, d, sched, tensors)
+    model.oracle = (d, sched, tensors)
     yield d, model
     model.close()
 
@@ -48,10 +54,16 @@ def drain(q, eng, ids):
 
 
 def reference_tokens(q, model, prompts, penalty=1.0):
+    """The tokens of the same requests prefilled from scratch on the HIP
+    engine, each checked against the CPU oracle's greedy decode
+    (oracle/q35_oracle.c, the restated reference step)."""
     eng = engine(q, model)
     ids = [eng.submit(p, NEW, penalty) for p in prompts]
     out = [toks for _, toks in drain(q, eng, ids)]
     eng.close()
+    d, sched, tensors = model.oracle
+    for p, toks in zip(prompts, out):
+        np.testing.assert_array_equal(toks, oracle_greedy(d, sched, tensors, p[None, :], NEW, penalty)[0])
     return out
 
 

@@ -21,13 +21,42 @@ from tests.model_util import build_small_model, small_dims, upload_model
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(scope="module")
-def small(q, ctx):
+@pytest.fixture(scope="module", params=["q4", "g16q8"])
+def small(q, ctx, request):
+    """The small hybrid model with the default encodings, and with the G16
+    tied head plus Q8 gate rows (the head_candidates path must use the
+    head's own tile format)."""
     d, sched = small_dims()
-    tensors = build_small_model(d, sched, seed=17)
+    alt = request.param == "g16q8"
+    tensors = build_small_model(d, sched, seed=17, head_g16=alt, q8_gates=alt)
     model = upload_model(q, ctx, d, sched, tensors)
     yield d, model
     model.close()
+
+
+def test_head_candidates_equal_step_logits(q, small):
+    """q35_runtime_head_candidates (the first token after a prefill or on a
+    complete prefix hit) runs the head on a stored final hidden row: its raw
+    logits and candidates must equal the logits path of the step that
+    produced the row, bit for bit, and q35_runtime_head its argmax."""
+    d, model = small
+    rt = q.Runtime(model, max_slots=1, max_batch=1, max_context=32, page_tokens=16, use_graphs=False)
+    prompt = np.random.default_rng(21).integers(0, d["vocab"], size=6).astype(np.int32)
+    slot = rt.slot_alloc(prompt)
+    table = np.array([[rt.page_alloc()]], np.int32)
+    print("head_candidates vs step logits", flush=True)
+    for t in range(prompt.size):
+        last = t == prompt.size - 1
+        res = rt.step([slot], [t], [prompt[t]], table, logits=last)
+    want = res[1][0]
+    hidden = rt.last_hidden(1)[0]
+    cand, raw = rt.head_candidates(slot, hidden, 64, 1.0, raw_logits=True)
+    np.testing.assert_array_equal(raw.view(np.uint32), want.view(np.uint32))
+    order = np.lexsort((np.arange(want.size), -want.astype(np.float64)))[:64]
+    np.testing.assert_array_equal(cand["token"], order)
+    np.testing.assert_array_equal(cand["value"].view(np.uint32), want[order].view(np.uint32))
+    assert rt.head(slot, hidden) == int(order[0])
+    rt.close()
 
 
 def engine(q, model, **kw):
