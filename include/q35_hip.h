@@ -160,10 +160,15 @@ int q35_rms_norm_f32(q35_context *ctx, const float *input, const float *weight, 
 /* l2_normalize_f32, activation.h:57-63 (in place) */
 int q35_l2_normalize_f32(q35_context *ctx, float *values, size_t rows, size_t width, float eps,
                          float output_scale);
-/* causal_conv1d_silu_f32 with batch_size 1, activation.h:29-43 (kernel-major weights) */
-int q35_causal_conv1d_silu_f32(q35_context *ctx, float *state, size_t ring_index,
-                               const float *input, const float *kernel_major_weights,
-                               float *output, size_t channel_count, size_t kernel_size);
+/* causal_conv1d_silu_f32, activation.h:29-43: batch_size tokens in order
+ * (input row t at input + t * input_stride, output [batch][channel_count]),
+ * each advancing the ring of kernel_size - 1 channel-major slots whose oldest
+ * slot is ring_index; kernel-major weights; channels [channel_begin,
+ * channel_end) only. */
+int q35_causal_conv1d_silu_f32(q35_context *ctx, float *state, size_t ring_index, const float *input,
+                               size_t input_stride, const float *kernel_major_weights, float *output,
+                               size_t batch_size, size_t channel_count, size_t kernel_size,
+                               size_t channel_begin, size_t channel_end);
 /* silu_mul_f32, activation.h:71-77 */
 int q35_silu_mul_f32(q35_context *ctx, const float *gate, const float *up, float *output,
                      size_t count);

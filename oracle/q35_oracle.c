@@ -98,6 +98,12 @@ uint16_t q35o_attention_float_to_half(float value) {
   return (uint16_t)(sign | ((rounded - 0x38000000u) >> 13));
 }
 
+/* attention_cache_store_f16 (full_attention.cpp:201-217), scalar branch: the
+ * conversion above over n values */
+void q35o_attention_store_f16(const float *x, uint16_t *out, size_t n) {
+  for (size_t i = 0; i < n; ++i) out[i] = q35o_attention_float_to_half(x[i]);
+}
+
 /* One 32-value block: src/cpu/q4_0.cpp:212-235 (scalar quantizer). The code
  * uses the unrounded 1/scale; the stored scale is the binary16-rounded one;
  * std::round rounds half away from zero (C roundf). */

@@ -27,6 +27,7 @@ typedef struct { uint16_t d; int8_t qs[32]; } q35o_q8_0;                /* 34 B 
 uint16_t q35o_float_to_half(float value);
 float q35o_half_to_float(uint16_t value);
 uint16_t q35o_attention_float_to_half(float value);
+void q35o_attention_store_f16(const float *x, uint16_t *out, size_t n);
 
 void q35o_q8_quantize_vector_1(const float *x, q35o_q8x1 *out, size_t blocks);
 void q35o_q8_quantize_vectors_4(const float *x, q35o_q8x4 *out, size_t vectors, size_t blocks);

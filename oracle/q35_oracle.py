@@ -42,6 +42,7 @@ for name, res, args in [
     ("q35o_float_to_half", c_uint16, [c_float]),
     ("q35o_half_to_float", c_float, [c_uint16]),
     ("q35o_attention_float_to_half", c_uint16, [c_float]),
+    ("q35o_attention_store_f16", None, [P, P, c_size_t]),
     ("q35o_q8_quantize_vector_1", None, [P, P, c_size_t]),
     ("q35o_q8_quantize_vectors_4", None, [P, P, c_size_t, c_size_t]),
     ("q35o_h128_sign_word", c_uint64, [c_size_t, c_size_t, c_uint64]),
@@ -306,8 +307,20 @@ def attention_decode(q, gates, keys, values, heads, kv_heads, head_dim, scale=No
 
 
 def f16_bits(x):
+    """attention_cache_store_f16's binary16 bits of every value."""
     x = np.ascontiguousarray(x, np.float32)
-    return np.array([lib.q35o_attention_float_to_half(float(v)) for v in x.ravel()], np.uint16).reshape(x.shape)
+    out = np.zeros(x.shape, np.uint16)
+    lib.q35o_attention_store_f16(ptr(x), ptr(out), x.size)
+    return out
+
+
+def rope_tables(theta, rope_dim, positions):
+    """CpuEngine's RoPE tables (cpu_engine.inl:339-352): cosine, sine [positions][rope_dim / 2]."""
+    half = rope_dim // 2
+    cs = np.zeros((positions, half), np.float32)
+    sn = np.zeros((positions, half), np.float32)
+    lib.q35o_rope_tables(c_float(theta), rope_dim, positions, ptr(cs), ptr(sn))
+    return cs, sn
 
 
 # ------------------------------------------------------------- whole model

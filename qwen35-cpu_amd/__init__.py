@@ -152,7 +152,8 @@ _SIGS = {
     "q35_attention_cache_store_f16": (c_int, [P, P, P, c_size_t]),
     "q35_rms_norm_f32": (c_int, [P, P, P, P, c_size_t, c_size_t, c_float, c_float]),
     "q35_l2_normalize_f32": (c_int, [P, P, c_size_t, c_size_t, c_float, c_float]),
-    "q35_causal_conv1d_silu_f32": (c_int, [P, P, c_size_t, P, P, P, c_size_t, c_size_t]),
+    "q35_causal_conv1d_silu_f32": (c_int, [P, P, c_size_t, P, c_size_t, P, P, c_size_t, c_size_t, c_size_t,
+                                           c_size_t, c_size_t]),
     "q35_silu_mul_f32": (c_int, [P, P, P, P, c_size_t]),
     "q35_rope_f32": (c_int, [P, P, c_size_t, c_size_t, c_size_t, P, P]),
     "q35_model_create": (c_int, [P, POINTER(ModelDims), P, POINTER(P)]),
@@ -390,8 +391,12 @@ def l2_normalize_f32(ctx, x, rows, width, eps, scale=1.0):
     ctx.check(lib.q35_l2_normalize_f32(ctx.handle, x.ptr, rows, width, eps, scale), "l2_normalize_f32")
 
 
-def causal_conv1d_silu_f32(ctx, state, ring, x, w, out, channels, kernel):
-    ctx.check(lib.q35_causal_conv1d_silu_f32(ctx.handle, state.ptr, ring, x.ptr, w.ptr, out.ptr, channels, kernel),
+def causal_conv1d_silu_f32(ctx, state, ring, x, w, out, channels, kernel, batch=1, input_stride=None,
+                           channel_begin=0, channel_end=None):
+    ctx.check(lib.q35_causal_conv1d_silu_f32(ctx.handle, state.ptr, ring, x.ptr,
+                                             channels if input_stride is None else input_stride, w.ptr, out.ptr,
+                                             batch, channels, kernel, channel_begin,
+                                             channels if channel_end is None else channel_end),
               "causal_conv1d_silu_f32")
 
 

@@ -56,17 +56,23 @@ __global__ void l2_normalize_kernel(float *x, int width, float eps, float scale)
   for (int i = threadIdx.x; i < width; i += 256) xr[i] *= m;
 }
 
-__global__ void conv1d_silu_kernel(float *state, int ring, const float *input, const float *w,
-                                   float *out, int channels, int kernel) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= channels) return;
+// causal_conv1d_silu_f32 (activation.cpp:164-222): one thread per channel of
+// [begin, end) walks the batch's tokens in order, each token advancing the
+// ring (the oldest slot is `ring`); kernel-major weights [kernel][channels].
+__global__ void conv1d_silu_kernel(float *state, int ring, const float *input, long long stride, const float *w,
+                                   float *out, int batch, int channels, int kernel, int begin, int end) {
+  const int c = begin + static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x);
+  if (c >= end) return;
   const int hist = kernel - 1;
-  const float x = input[c];
-  float sum = x * w[static_cast<size_t>(hist) * channels + c];
-  for (int k = 0; k < hist; ++k)
-    sum += state[static_cast<size_t>((ring + k) % hist) * channels + c] * w[static_cast<size_t>(k) * channels + c];
-  if (hist) state[static_cast<size_t>(ring) * channels + c] = x;
-  out[c] = silu_times(sum, 1.0F);
+  for (int t = 0; t < batch; ++t) {
+    const float x = input[t * stride + c];
+    float sum = x * w[static_cast<size_t>(hist) * channels + c];
+    for (int k = 0; k < hist; ++k)
+      sum += state[static_cast<size_t>((ring + k) % hist) * channels + c] * w[static_cast<size_t>(k) * channels + c];
+    if (hist) state[static_cast<size_t>(ring) * channels + c] = x;
+    out[static_cast<size_t>(t) * channels + c] = silu_times(sum, 1.0F);
+    if (hist) ring = (ring + 1) % hist;
+  }
 }
 
 __global__ void silu_mul_kernel(const float *g, const float *u, float *out, long long n) {
@@ -117,10 +123,11 @@ hipError_t launch_l2_normalize(float *x, int rows, int width, float eps, float s
   return hipGetLastError();
 }
 
-hipError_t launch_conv1d_silu(float *state, int ring, const float *input, const float *w,
-                              float *out, int channels, int kernel, hipStream_t stream) {
-  Q35_LAUNCH((conv1d_silu_kernel), (channels + 255) / 256, 256, 0, stream, state, ring, input, w, out,
-                                                                 channels, kernel);
+hipError_t launch_conv1d_silu(float *state, int ring, const float *input, long long stride, const float *w,
+                              float *out, int batch, int channels, int kernel, int begin, int end, hipStream_t stream) {
+  if (batch <= 0 || begin >= end) return hipSuccess;
+  Q35_LAUNCH((conv1d_silu_kernel), (end - begin + 255) / 256, 256, 0, stream, state, ring, input, stride, w, out,
+                                                                 batch, channels, kernel, begin, end);
   return hipGetLastError();
 }
 

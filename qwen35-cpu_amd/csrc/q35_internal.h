@@ -336,8 +336,8 @@ hipError_t launch_rms_norm(const float *x, const float *w, float *y, int rows, i
                            float eps, float offset, hipStream_t stream);
 hipError_t launch_l2_normalize(float *x, int rows, int width, float eps, float scale,
                                hipStream_t stream);
-hipError_t launch_conv1d_silu(float *state, int ring, const float *input, const float *w,
-                              float *out, int channels, int kernel, hipStream_t stream);
+hipError_t launch_conv1d_silu(float *state, int ring, const float *input, long long stride, const float *w,
+                              float *out, int batch, int channels, int kernel, int begin, int end, hipStream_t stream);
 hipError_t launch_silu_mul(const float *g, const float *u, float *out, long long n,
                            hipStream_t stream);
 hipError_t launch_rope(float *x, int heads, int head_dim, int rope_dim, const float *c,

@@ -503,13 +503,21 @@ extern "C" int q35_l2_normalize_f32(q35_context *ctx, float *values, size_t rows
                                                 eps, scale, ctx->stream),
                        "l2 normalize");
 }
-extern "C" int q35_causal_conv1d_silu_f32(q35_context *ctx, float *state, size_t ring,
-                                          const float *input, const float *w, float *output,
-                                          size_t channels, size_t kernel) {
-  if (ctx == nullptr || kernel < 2) return Q35_ERR_INVALID;
-  return launch_status(ctx, launch_conv1d_silu(state, static_cast<int>(ring), input, w, output,
-                                               static_cast<int>(channels), static_cast<int>(kernel),
-                                               ctx->stream),
+extern "C" int q35_causal_conv1d_silu_f32(q35_context *ctx, float *state, size_t ring_index, const float *input,
+                                          size_t input_stride, const float *kernel_major_weights, float *output,
+                                          size_t batch_size, size_t channel_count, size_t kernel_size,
+                                          size_t channel_begin, size_t channel_end) {
+  if (ctx == nullptr) return Q35_ERR_INVALID;
+  // activation.cpp:177-179: an empty kernel or channel range is a no-op
+  if (kernel_size == 0 || channel_begin >= channel_end || batch_size == 0) return Q35_OK;
+  if (channel_end > channel_count || (kernel_size > 1 && ring_index >= kernel_size - 1) ||
+      (batch_size > 1 && input_stride < channel_end))
+    return set_error(ctx, Q35_ERR_INVALID, "conv1d: channel range, ring index or input stride out of range");
+  return launch_status(ctx, launch_conv1d_silu(state, static_cast<int>(ring_index), input,
+                                               static_cast<long long>(input_stride), kernel_major_weights, output,
+                                               static_cast<int>(batch_size), static_cast<int>(channel_count),
+                                               static_cast<int>(kernel_size), static_cast<int>(channel_begin),
+                                               static_cast<int>(channel_end), ctx->stream),
                        "conv1d");
 }
 extern "C" int q35_silu_mul_f32(q35_context *ctx, const float *gate, const float *up, float *output,
