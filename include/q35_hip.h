@@ -103,6 +103,17 @@ int q35_q4_dot4_matmul(q35_context *ctx, const q35_q4_0_block_x8 *matrix,
 int q35_q4_dot4_matmul_exact(q35_context *ctx, const q35_q4_0_block_x8 *matrix,
                              const q35_q8_0_block_x4 *vectors, float *output, size_t rows,
                              size_t vectors_count, size_t blocks, size_t stride);
+/* No reference counterpart: for callers that cannot allocate device memory
+ * (code under stream capture, serving loops or harnesses that forbid
+ * hipMalloc). Same arguments, contraction and output bits as
+ * q35_q4_dot4_matmul, but the activation layout and split partials live in a
+ * 16 MiB file-scope device array per GPU (held until the process ends) instead
+ * of context scratch; calls no allocating routine. Returns
+ * Q35_ERR_UNSUPPORTED when a 16-token chunk of the shape does not fit the
+ * array. Calls that overlap on one GPU race on the array. */
+int q35_q4_dot4_matmul_noalloc(q35_context *ctx, const q35_q4_0_block_x8 *matrix,
+                               const q35_q8_0_block_x4 *vectors, float *output, size_t rows,
+                               size_t vectors_count, size_t blocks, size_t stride);
 /* Integer parity hook (no reference counterpart): the exact int32 per-block dot
  * sum_k (u-8)*a that the matmul kernel forms before its FP32 scaling, written
  * as [vectors][rows][blocks]. Runs the same device code as q35_q4_dot4_matmul. */

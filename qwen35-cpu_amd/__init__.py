@@ -141,6 +141,7 @@ _SIGS = {
     "q35_q4_dot4_matvec": (c_int, [P, P, P, P, c_size_t, c_size_t]),
     "q35_q4_dot4_matmul": (c_int, [P, P, P, P, c_size_t, c_size_t, c_size_t, c_size_t]),
     "q35_q4_dot4_matmul_exact": (c_int, [P, P, P, P, c_size_t, c_size_t, c_size_t, c_size_t]),
+    "q35_q4_dot4_matmul_noalloc": (c_int, [P, P, P, P, c_size_t, c_size_t, c_size_t, c_size_t]),
     "q35_q4_dot4_block_dots": (c_int, [P, P, P, P, c_size_t, c_size_t, c_size_t]),
     "q35_q4_dot4_argmax_batch": (c_int, [P, P, P, P, P, c_size_t, c_size_t, c_size_t, P, P]),
     "q35_gated_delta_net_update_rows": (c_int, [P, P, P, P, P, P, P, P, c_size_t, c_size_t, c_size_t,
@@ -346,6 +347,13 @@ def q4_dot4_matvec(ctx, m, v, out, rows, blocks):
 def q4_dot4_matmul(ctx, m, v, out, rows, count, blocks, stride, exact=False):
     f = lib.q35_q4_dot4_matmul_exact if exact else lib.q35_q4_dot4_matmul
     ctx.check(f(ctx.handle, m.ptr, v.ptr, out.ptr, rows, count, blocks, stride), "q4_dot4_matmul")
+
+
+def q4_dot4_matmul_noalloc(ctx, m, v, out, rows, count, blocks, stride):
+    """q4_dot4_matmul through the entry point that allocates nothing (its
+    scratch is a fixed 16 MiB device array shared by every call on the GPU)."""
+    ctx.check(lib.q35_q4_dot4_matmul_noalloc(ctx.handle, m.ptr, v.ptr, out.ptr, rows, count, blocks, stride),
+              "q4_dot4_matmul_noalloc")
 
 
 def q4_dot4_block_dots(ctx, m, v, out, rows, count, blocks):

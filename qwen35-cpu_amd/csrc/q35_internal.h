@@ -227,6 +227,21 @@ int gemm_argmax_cand_capacity(int rows, int cu_count);
 // Floats of partial sums a split launch writes (0 when it does not split).
 size_t gemm_partial_floats(int rows, int nb, int tokens, int cu_count);
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t stream);
+
+// The kernel-level DOT4 GEMM (runtime.cpp): argument checks, the scratch
+// bytes of `chunk` tokens per launch, and the run itself over caller scratch.
+int dot4_matmul_check(Context *ctx, const q35_q4_0_block_x8 *m, const q35_q8_0_block_x4 *x4,
+                      const q35_q8_0_block_x1 *x1, const void *out, const int32_t *dots, const int32_t *index,
+                      size_t rows, size_t vectors, size_t blocks, size_t stride);
+size_t dot4_matmul_scratch_bytes(int rows, int nb, int chunk, bool argmax, int cu_count);
+int dot4_matmul_run(Context *ctx, const q35_q4_0_block_x8 *m, const q35_q8_0_block_x4 *x4,
+                    const q35_q8_0_block_x1 *x1, float *out, int32_t *dots, size_t rows, size_t vectors,
+                    size_t blocks, size_t stride, bool exact, int32_t *index, float *value, const int32_t *counts,
+                    const float *penalties, void *scratch, size_t chunk);
+// Resolves, once per device, the address of the file-scope scratch array of
+// the allocation-free entry point (noalloc.hip); called by context creation
+// with the context's device current.
+int static_scratch_init(Context *ctx);
 hipError_t launch_split_reduce(const SplitRows &src, int tokens, float *out, int stride, const float *residual,
                                hipStream_t stream);
 hipError_t launch_argmax_finalize(const unsigned long long *cand, int ncand, int cand_stride, int tokens,

@@ -90,6 +90,13 @@ extern "C" int q35_context_create(int device, void *stream, q35_context **out) {
     delete ctx;
     return Q35_ERR_HIP;
   }
+  if (const int st = static_scratch_init(ctx); st != Q35_OK) {
+    (void)hipEventDestroy(ctx->t0);
+    (void)hipEventDestroy(ctx->t1);
+    if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return st;
+  }
   *out = ctx;
   return Q35_OK;
 }
@@ -239,33 +246,48 @@ extern "C" int q35_q4_h128_prepare_activations_4(q35_context *ctx, const float *
 }
 
 // ================================================================ DOT4 GEMM
-namespace {
-// Runs the GEMM over `vectors` tokens (chunks of kMaxTokens) from X4 or X1
-// activations. `exact` forces the single-wave fma chain per row. With `index`
-// set it runs the greedy head instead (penalty + argmax per vector).
-int matmul_entry(q35_context *ctx, const q35_q4_0_block_x8 *m, const q35_q8_0_block_x4 *x4,
-                 const q35_q8_0_block_x1 *x1, float *out, int32_t *dots, size_t rows,
-                 size_t vectors, size_t blocks, size_t stride, bool exact, int32_t *index,
-                 float *value, const int32_t *counts, const float *penalties) {
+namespace q35 {
+int dot4_matmul_check(Context *ctx, const q35_q4_0_block_x8 *m, const q35_q8_0_block_x4 *x4,
+                      const q35_q8_0_block_x1 *x1, const void *out, const int32_t *dots, const int32_t *index,
+                      size_t rows, size_t vectors, size_t blocks, size_t stride) {
   if (ctx == nullptr || m == nullptr || (x4 == nullptr && x1 == nullptr) ||
       (out == nullptr && dots == nullptr && index == nullptr))
     return Q35_ERR_INVALID;
   if (rows == 0 || rows % 8 != 0 || blocks == 0 || vectors == 0 || rows > (1u << 28) ||
       blocks > (1u << 16) || (out != nullptr && stride < rows))
     return set_error(ctx, Q35_ERR_INVALID, "invalid DOT4 geometry");
+  return Q35_OK;
+}
+
+size_t dot4_matmul_scratch_bytes(int rows, int nb, int chunk, bool argmax, int cu_count) {
+  const size_t tiles = static_cast<size_t>(chunk + 15) / 16;
+  const size_t code_bytes = align256(tiles * 64 * static_cast<size_t>(nb) * sizeof(uint64_t));
+  const size_t scale_bytes = align256(tiles * 16 * static_cast<size_t>(nb) * sizeof(float));
+  const size_t cand_bytes =
+      argmax ? align256(static_cast<size_t>(gemm_argmax_cand_capacity(rows, cu_count)) * kMaxTokens * 8) : 0;
+  const size_t part_bytes = align256(gemm_partial_floats(rows, nb, chunk, cu_count) * 4);
+  return code_bytes + scale_bytes + cand_bytes + part_bytes;
+}
+
+// Runs the GEMM over `vectors` tokens, `chunk` (a multiple of 16, at most
+// kMaxTokens) at a time, from X4 or X1 activations, with the activation
+// layout, candidates and split partials in `scratch` (at least
+// dot4_matmul_scratch_bytes). `exact` forces the single-wave fma chain per
+// row. With `index` set it runs the greedy head instead (penalty + argmax per
+// vector). The K split depends on rows and blocks only, so every chunk size
+// gives the same bits.
+int dot4_matmul_run(Context *ctx, const q35_q4_0_block_x8 *m, const q35_q8_0_block_x4 *x4,
+                    const q35_q8_0_block_x1 *x1, float *out, int32_t *dots, size_t rows, size_t vectors,
+                    size_t blocks, size_t stride, bool exact, int32_t *index, float *value, const int32_t *counts,
+                    const float *penalties, void *scratch, size_t chunk) {
   const int nb = static_cast<int>(blocks);
-  const size_t chunk = kMaxTokens;
-  const size_t code_bytes = align256(4 * 64 * static_cast<size_t>(nb) * sizeof(uint64_t));
-  const size_t scale_bytes = align256(4 * 16 * static_cast<size_t>(nb) * sizeof(float));
+  const size_t tiles = (chunk + 15) / 16;
+  const size_t code_bytes = align256(tiles * 64 * static_cast<size_t>(nb) * sizeof(uint64_t));
+  const size_t scale_bytes = align256(tiles * 16 * static_cast<size_t>(nb) * sizeof(float));
   const size_t cand_bytes =
       index != nullptr
           ? align256(static_cast<size_t>(gemm_argmax_cand_capacity(static_cast<int>(rows), ctx->cu_count)) * kMaxTokens * 8)
           : 0;
-  const size_t part_bytes =
-      align256(gemm_partial_floats(static_cast<int>(rows), nb, static_cast<int>(chunk), ctx->cu_count) * 4);
-  void *scratch = nullptr;
-  int st = scratch_get(ctx, code_bytes + scale_bytes + cand_bytes + part_bytes, &scratch);
-  if (st != Q35_OK) return st;
   char *base = static_cast<char *>(scratch);
   auto *codes = reinterpret_cast<uint64_t *>(base);
   auto *scales = reinterpret_cast<float *>(base + code_bytes);
@@ -320,6 +342,26 @@ int matmul_entry(q35_context *ctx, const q35_q4_0_block_x8 *m, const q35_q8_0_bl
     }
   }
   return Q35_OK;
+}
+}  // namespace q35
+
+namespace {
+// The kernel-level DOT4 entry points: chunks of kMaxTokens tokens through the
+// context's grow-only scratch.
+int matmul_entry(q35_context *ctx, const q35_q4_0_block_x8 *m, const q35_q8_0_block_x4 *x4,
+                 const q35_q8_0_block_x1 *x1, float *out, int32_t *dots, size_t rows,
+                 size_t vectors, size_t blocks, size_t stride, bool exact, int32_t *index,
+                 float *value, const int32_t *counts, const float *penalties) {
+  int st = dot4_matmul_check(ctx, m, x4, x1, out, dots, index, rows, vectors, blocks, stride);
+  if (st != Q35_OK) return st;
+  void *scratch = nullptr;
+  st = scratch_get(ctx,
+                   dot4_matmul_scratch_bytes(static_cast<int>(rows), static_cast<int>(blocks), kMaxTokens,
+                                             index != nullptr, ctx->cu_count),
+                   &scratch);
+  if (st != Q35_OK) return st;
+  return dot4_matmul_run(ctx, m, x4, x1, out, dots, rows, vectors, blocks, stride, exact, index, value, counts,
+                         penalties, scratch, kMaxTokens);
 }
 }  // namespace
 
