@@ -46,25 +46,6 @@ typedef Q35_V4I v4i;
 
 constexpr int kRowsPerGroup = 64;
 constexpr int kMaxWaves = 4;
-constexpr long kMinus8 = static_cast<long>(0xF8F8F8F8F8F8F8F8ull);  // int8 -8 x 8
-
-__device__ __forceinline__ long unpack_word(uint32_t w) {
-  const uint32_t lo = w & 0x0f0f0f0fu;
-  const uint32_t hi = (w >> 4) & 0x0f0f0f0fu;
-  return static_cast<long>((static_cast<uint64_t>(hi) << 32) | lo);
-}
-
-// Stores four consecutive rows of one token.
-__device__ __forceinline__ void store_row4(float *dst, bool vec, float v0, float v1, float v2, float v3) {
-  if (vec) {
-    *reinterpret_cast<q35_f32x4 *>(dst) = q35_f32x4{v0, v1, v2, v3};
-  } else {
-    dst[0] = v0;
-    dst[1] = v1;
-    dst[2] = v2;
-    dst[3] = v3;
-  }
-}
 
 template <int KS, bool ARGMAX, bool DOTS>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {

@@ -15,6 +15,28 @@ __device__ __forceinline__ uint16_t float_to_half_bits(float f) {
   return __half_as_ushort(__float2half_rn(f));
 }
 
+// Q4 DOT4 GEMMs: int8 -8 in every byte (the offset-binary correction
+// operand), and a body word of a Q4_0BlockX8 tile (eight nibbles: columns
+// j and j + 4 of one row) unpacked to eight int8 values, low nibbles first.
+constexpr long kMinus8 = static_cast<long>(0xF8F8F8F8F8F8F8F8ull);
+__device__ __forceinline__ long unpack_word(uint32_t w) {
+  const uint32_t lo = w & 0x0f0f0f0fu;
+  const uint32_t hi = (w >> 4) & 0x0f0f0f0fu;
+  return static_cast<long>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Stores four consecutive rows of one token (vectorized when `vec`).
+__device__ __forceinline__ void store_row4(float *dst, bool vec, float v0, float v1, float v2, float v3) {
+  if (vec) {
+    *reinterpret_cast<q35_f32x4 *>(dst) = q35_f32x4{v0, v1, v2, v3};
+  } else {
+    dst[0] = v0;
+    dst[1] = v1;
+    dst[2] = v2;
+    dst[3] = v3;
+  }
+}
+
 // XOR-butterfly reductions over groups of `Width` lanes (Width <= 64, power of 2).
 template <int Width>
 __device__ __forceinline__ float group_sum(float v) {

@@ -227,12 +227,22 @@ int gemm_argmax_cand_capacity(int rows, int cu_count);
 // Floats of partial sums a split launch writes (0 when it does not split).
 size_t gemm_partial_floats(int rows, int nb, int tokens, int cu_count);
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t stream);
+// Dense GEMM for many tokens (any count): writes the finished rows to
+// a.out [tokens][stride] with the bits the split launch of the same shape
+// and consumer bound (a.max_split) gives after its consumer's ordered sum;
+// no partials. K splits it reproduces:
+int gemm_dense_splits(int rows, int nb, int cu_count, int max_split);
+hipError_t launch_gemm_dense(const GemmArgs &a, hipStream_t stream);
+// Tokens per launch of the kernel-level dense path.
+constexpr int kDenseChunk = 4096;
 
 // The kernel-level DOT4 GEMM (runtime.cpp): argument checks, the scratch
 // bytes of `chunk` tokens per launch, and the run itself over caller scratch.
 int dot4_matmul_check(Context *ctx, const q35_q4_0_block_x8 *m, const q35_q8_0_block_x4 *x4,
                       const q35_q8_0_block_x1 *x1, const void *out, const int32_t *dots, const int32_t *index,
                       size_t rows, size_t vectors, size_t blocks, size_t stride);
+// `chunk` tokens per launch: above kMaxTokens the dense GEMM runs (plain
+// outputs only), which needs no partials.
 size_t dot4_matmul_scratch_bytes(int rows, int nb, int chunk, bool argmax, int cu_count);
 int dot4_matmul_run(Context *ctx, const q35_q4_0_block_x8 *m, const q35_q8_0_block_x4 *x4,
                     const q35_q8_0_block_x1 *x1, float *out, int32_t *dots, size_t rows, size_t vectors,

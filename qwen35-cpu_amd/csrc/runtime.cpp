@@ -265,12 +265,13 @@ size_t dot4_matmul_scratch_bytes(int rows, int nb, int chunk, bool argmax, int c
   const size_t scale_bytes = align256(tiles * 16 * static_cast<size_t>(nb) * sizeof(float));
   const size_t cand_bytes =
       argmax ? align256(static_cast<size_t>(gemm_argmax_cand_capacity(rows, cu_count)) * kMaxTokens * 8) : 0;
-  const size_t part_bytes = align256(gemm_partial_floats(rows, nb, chunk, cu_count) * 4);
+  // dense chunks write finished rows: no partials
+  const size_t part_bytes = chunk > kMaxTokens ? 0 : align256(gemm_partial_floats(rows, nb, chunk, cu_count) * 4);
   return code_bytes + scale_bytes + cand_bytes + part_bytes;
 }
 
-// Runs the GEMM over `vectors` tokens, `chunk` (a multiple of 16, at most
-// kMaxTokens) at a time, from X4 or X1 activations, with the activation
+// Runs the GEMM over `vectors` tokens, `chunk` (a multiple of 16; above
+// kMaxTokens only for plain outputs, which then run the dense GEMM) at a time, from X4 or X1 activations, with the activation
 // layout, candidates and split partials in `scratch` (at least
 // dot4_matmul_scratch_bytes). `exact` forces the single-wave fma chain per
 // row. With `index` set it runs the greedy head instead (penalty + argmax per
@@ -321,6 +322,12 @@ int dot4_matmul_run(Context *ctx, const q35_q4_0_block_x8 *m, const q35_q8_0_blo
       g.counts_stride = static_cast<long long>(rows);
       g.penalties = penalties ? penalties + t0 : nullptr;
     }
+    if (chunk > static_cast<size_t>(kMaxTokens)) {
+      // many tokens: the dense GEMM writes the finished rows (same bits)
+      e = launch_gemm_dense(g, ctx->stream);
+      if (e != hipSuccess) return hip_error(ctx, e, "dense DOT4 GEMM kernel");
+      continue;
+    }
     e = launch_gemm(g, ctx->stream);
     if (e != hipSuccess) return hip_error(ctx, e, "DOT4 GEMM kernel");
     const GemmPlan plan = gemm_plan(g.rows, nb, exact || dots != nullptr, index != nullptr, ctx->cu_count, 0, 0);
@@ -354,14 +361,19 @@ int matmul_entry(q35_context *ctx, const q35_q4_0_block_x8 *m, const q35_q8_0_bl
                  float *value, const int32_t *counts, const float *penalties) {
   int st = dot4_matmul_check(ctx, m, x4, x1, out, dots, index, rows, vectors, blocks, stride);
   if (st != Q35_OK) return st;
+  // plain outputs of more than kMaxTokens vectors: dense chunks (X4 input,
+  // so a chunk is a multiple of 16 and of 4)
+  const bool dense = out != nullptr && dots == nullptr && index == nullptr && !exact && x4 != nullptr &&
+                     vectors > static_cast<size_t>(kMaxTokens);
+  const size_t chunk = dense ? std::min<size_t>((vectors + 15) / 16 * 16, kDenseChunk) : kMaxTokens;
   void *scratch = nullptr;
   st = scratch_get(ctx,
-                   dot4_matmul_scratch_bytes(static_cast<int>(rows), static_cast<int>(blocks), kMaxTokens,
+                   dot4_matmul_scratch_bytes(static_cast<int>(rows), static_cast<int>(blocks), static_cast<int>(chunk),
                                              index != nullptr, ctx->cu_count),
                    &scratch);
   if (st != Q35_OK) return st;
   return dot4_matmul_run(ctx, m, x4, x1, out, dots, rows, vectors, blocks, stride, exact, index, value, counts,
-                         penalties, scratch, kMaxTokens);
+                         penalties, scratch, chunk);
 }
 }  // namespace
 

@@ -152,3 +152,29 @@ def test_argmax_head_shapes(q, ctx, orc, rows, cols, vectors):
                            cols // 32, idx, val)
     np.testing.assert_array_equal(idx.download(), want)
     np.testing.assert_array_equal(val.download(), adj[np.arange(vectors), want])
+
+
+@pytest.mark.parametrize("rows,blocks,vectors", [(2560, 288, 300), (3584, 32, 512), (200, 112, 132), (1032, 80, 68)])
+def test_dense_matches_split_launches(q, ctx, orc, rows, blocks, vectors):
+    """Above 64 vectors q4_dot4_matmul runs the dense GEMM (every K block of a
+    64-row group in one wavefront, the split structure folded in registers);
+    its rows must equal the 64-vector split launches bit for bit, here with
+    32, 4 and 14 K splits, a ragged row group and ragged token groups."""
+    rng = np.random.default_rng(rows + vectors)
+    packed, x = _problem(orc, rng, rows, blocks * 32, vectors)
+    act = orc.h128_prepare_4(x)
+    dm, da = ctx.array(packed), ctx.array(act)
+    stride = rows + 4
+    dense = ctx.array(np.full((vectors, stride), -5.0, np.float32))
+    print(f"dense rows={rows} blocks={blocks} vectors={vectors}", flush=True)
+    q.q4_dot4_matmul(ctx, dm, da, dense, rows, vectors, blocks, stride)
+    got = dense.download()
+    assert np.all(got[:, rows:] == -5.0)
+    for t0 in range(0, vectors, 64):
+        n = min(64, vectors - t0)
+        part = ctx.array(shape=(n, stride), dtype=np.float32)
+        q.q4_dot4_matmul(ctx, dm, ctx.array(act[t0 // 4:(t0 + n) // 4]), part, rows, n, blocks, stride)
+        np.testing.assert_array_equal(got[t0:t0 + n, :rows].view(np.uint32), part.download()[:, :rows].view(np.uint32),
+                                      err_msg=f"vectors {t0}..{t0 + n}")
+    want = orc.dot4_matmul(packed, act, rows, vectors, blocks)
+    assert np.max(np.abs(got[:, :rows] - want)) <= 1e-5 * np.abs(want).max()
