@@ -257,6 +257,9 @@ typedef struct {
   int32_t page_tokens;    /* tokens per KV page (a power of two)                        */
   int32_t total_pages;    /* KV pool capacity in pages; 0 = max_slots*ceil(ctx/page)    */
   int32_t use_graphs;     /* capture each step shape as a hipGraph and replay it        */
+  int32_t max_step_rows;  /* rows of a packed step: decode rows plus prefill positions  */
+                          /* (<= 8192; 0 = max_batch). Prefill chunks and packed steps  */
+                          /* above 64 rows run the dense projection GEMM.               */
 } q35_runtime_config;
 
 /* One sampling candidate: a penalized, temperature-scaled logit and its token. */
@@ -315,12 +318,14 @@ typedef struct {
 } q35_step_desc;
 int q35_runtime_step(q35_runtime *rt, const q35_step_desc *desc, int32_t *out_tokens,
                      float *out_logits);
-/* Chunked prefill of one request: prompt tokens tokens[0..count) at positions
+/* Chunked prefill of one request (a packed step of one segment): prompt
+ * tokens tokens[0..count) at positions
  * pos0 .. pos0 + count - 1 run through every layer in one pass -- the prefill
  * chunk of CpuEngine::advance (cpu_engine.inl:668-790; run_forward_cpu_q8_batch,
  * prefill.inl:599-791). The DeltaNet recurrence scans the chunk in order and
  * attention is causal over the request's KV pages plus the chunk, so the
- * resulting state equals count single-token steps. count <= max_batch;
+ * resulting state equals count single-token steps. count <= max(max_batch,
+ * max_step_rows);
  * page_table[max_pages] covers positions 0 .. pos0 + count - 1. The prompt
  * tokens must already be counted (q35_slot_alloc does). out_token (optional)
  * receives the greedy token after the chunk's last position: the first
@@ -328,6 +333,39 @@ int q35_runtime_step(q35_runtime *rt, const q35_step_desc *desc, int32_t *out_to
 int q35_runtime_prefill(q35_runtime *rt, int32_t slot, int32_t pos0, const int32_t *tokens,
                         int32_t count, const int32_t *page_table, int32_t max_pages, float penalty,
                         int32_t *out_token);
+struct q35_row_sampling_s; /* q35_row_sampling, below */
+/* One segment of a packed step: `count` consecutive positions pos0 .. of one
+ * request -- a prompt chunk (prefill.inl:683-696 packs such segments of
+ * several requests into one projection), or one decode row (count 1).
+ *   tokens       [count] input tokens
+ *   page_table   [max_pages] page ids covering positions 0 .. pos0 + count - 1
+ *   count_input  1: the tokens join the slot's penalty counts before the head
+ *                (generated tokens fed back), 0: prompt tokens (already counted)
+ *   want_token   1: run the head on the segment's last position */
+typedef struct {
+  int32_t slot;
+  int32_t pos0;
+  int32_t count;
+  const int32_t *tokens;
+  const int32_t *page_table;
+  int32_t max_pages;
+  float penalty;
+  uint8_t count_input;
+  uint8_t want_token;
+} q35_segment;
+/* One packed step over `count` segments on distinct slots (at most max_batch
+ * + 16 segments and max_step_rows rows in total): decode rows and prompt
+ * chunks of several requests in one pass through every layer, e.g. config 5's
+ * 64 decode rows plus a prefill chunk. Each segment's state, KV rows and
+ * token equal what separate q35_runtime_step / q35_runtime_prefill calls give
+ * for it, bit for bit. With `sampling` NULL, out_tokens[s] receives the greedy
+ * token of each segment with want_token (-1 for the others). With `sampling`
+ * ([count], read for want_token segments) the head writes logits and
+ * out_candidates [count][Q35_MAX_CANDIDATES] (and raw_logits
+ * [count][vocab], optional) receive them per segment; out_tokens is then -1. */
+int q35_runtime_step_segments(q35_runtime *rt, const q35_segment *segments, int32_t count,
+                              const struct q35_row_sampling_s *sampling, int32_t *out_tokens,
+                              q35_candidate *out_candidates, float *raw_logits);
 /* Sampled decoding (sample_token_from_logits, layers.inl:491-600). Per row:
  * top_k candidates (1..Q35_MAX_CANDIDATES; 1 with inv_temperature 1 is the
  * greedy argmax) of the logits after the repetition penalty
@@ -335,7 +373,7 @@ int q35_runtime_prefill(q35_runtime *rt, int32_t slot, int32_t pos0, const int32
  * v *= inv_temperature (layers.inl:546-549), in descending order, ties to the
  * lower token (layers.inl:552-568). The host finishes softmax, top_p and the
  * draw in the reference's order. */
-typedef struct {
+typedef struct q35_row_sampling_s {
   int32_t top_k;
   float inv_temperature;  /* 1 / SamplingOptions::temperature */
 } q35_row_sampling;

@@ -57,7 +57,15 @@ class ModelDims(ctypes.Structure):
 
 class RuntimeConfig(ctypes.Structure):
     _fields_ = [("max_slots", c_int32), ("max_batch", c_int32), ("max_context", c_int32),
-                ("page_tokens", c_int32), ("total_pages", c_int32), ("use_graphs", c_int32)]
+                ("page_tokens", c_int32), ("total_pages", c_int32), ("use_graphs", c_int32),
+                ("max_step_rows", c_int32)]
+
+
+class Segment(ctypes.Structure):
+    """q35_segment: consecutive positions of one request in a packed step."""
+    _fields_ = [("slot", c_int32), ("pos0", c_int32), ("count", c_int32), ("tokens", POINTER(c_int32)),
+                ("page_table", POINTER(c_int32)), ("max_pages", c_int32), ("penalty", c_float),
+                ("count_input", c_uint8), ("want_token", c_uint8)]
 
 
 class StepDesc(ctypes.Structure):
@@ -178,6 +186,7 @@ _SIGS = {
     "q35_runtime_free_pages": (c_int, [P]),
     "q35_runtime_step": (c_int, [P, POINTER(StepDesc), P, P]),
     "q35_runtime_prefill": (c_int, [P, c_int32, c_int32, P, c_int32, P, c_int32, c_float, P]),
+    "q35_runtime_step_segments": (c_int, [P, P, c_int32, P, P, P, P]),
     "q35_runtime_last_hidden": (c_int, [P, P, c_size_t]),
     "q35_runtime_set_profiling": (c_int, [P, c_int]),
     "q35_runtime_set_trace": (c_int, [P, c_int]),
@@ -492,9 +501,10 @@ class Runtime(_Profiled):
     """Device slots, KV page pool and the captured decode step."""
 
     def __init__(self, model, max_slots=16, max_batch=16, max_context=1024, page_tokens=16, total_pages=0,
-                 use_graphs=True):
+                 use_graphs=True, max_step_rows=0):
         self.model, self.ctx = model, model.ctx
-        self.cfg = RuntimeConfig(max_slots, max_batch, max_context, page_tokens, total_pages, int(use_graphs))
+        self.cfg = RuntimeConfig(max_slots, max_batch, max_context, page_tokens, total_pages, int(use_graphs),
+                                 int(max_step_rows))
         h = c_void_p()
         self.ctx.check(lib.q35_runtime_create(model.handle, ctypes.byref(self.cfg), ctypes.byref(h)), "runtime create")
         self.handle = h
@@ -573,6 +583,37 @@ class Runtime(_Profiled):
                                                _ptr(table), table.size, float(penalty), _ptr(out)),
                        "runtime prefill")
         return int(out[0])
+
+    def step_segments(self, segments, sampling=None, raw_logits=False):
+        """One packed step (q35_runtime_step_segments). `segments` is a list of
+        dicts with slot, pos0, tokens, page_table and optional penalty,
+        count_input (0), want_token (1). Greedy: returns the token per segment
+        (-1 without want_token). With `sampling` (a (top_k, inv_temperature)
+        pair per segment): returns the candidate arrays [segments][64] (and the
+        raw logits [segments][vocab] when asked)."""
+        n = len(segments)
+        keep = []
+        arr = (Segment * n)()
+        for i, g in enumerate(segments):
+            toks = np.ascontiguousarray(g["tokens"], np.int32).ravel()
+            table = np.ascontiguousarray(g["page_table"], np.int32).ravel()
+            keep += [toks, table]
+            arr[i] = Segment(int(g["slot"]), int(g["pos0"]), toks.size, toks.ctypes.data_as(POINTER(c_int32)),
+                             table.ctypes.data_as(POINTER(c_int32)), table.size, float(g.get("penalty", 1.0)),
+                             int(g.get("count_input", 0)), int(g.get("want_token", 1)))
+        out = np.empty(n, np.int32)
+        if sampling is None:
+            self.ctx.check(lib.q35_runtime_step_segments(self.handle, arr, n, None, _ptr(out), None, None),
+                           "step segments")
+            return out
+        rs = (RowSampling * n)(*[RowSampling(int(k), float(t)) for k, t in sampling])
+        cand = (Candidate * (n * MAX_CANDIDATES))()
+        lg = np.empty((n, self.model.dims.vocab), np.float32) if raw_logits else None
+        self.ctx.check(lib.q35_runtime_step_segments(self.handle, arr, n, rs, _ptr(out), cand, _ptr(lg)),
+                       "step segments")
+        c = np.frombuffer(cand, dtype=np.dtype([("value", np.float32), ("token", np.int32)])).reshape(
+            n, MAX_CANDIDATES).copy()
+        return (c, lg) if raw_logits else c
 
     def head(self, slot, hidden, penalty=1.0):
         """Greedy head of one final normalized hidden row with the slot's

@@ -5,10 +5,14 @@
 //   first rope_dim dims (activation.cpp:124-162), and the FP16 round-to-nearest
 //   KV append of normalised K and raw V (full_attention.cpp:18-46, kv_pages.h:40-69).
 // attention: split-K flash-decoding over chunks of 64 context tokens (one
-//   workgroup per chunk, KV head and request; see attention_kernel), then
+//   workgroup per chunk, KV head and request -- or, for the rows of a prefill
+//   segment, per chunk, KV head and tile of up to kAttnTileRows positions,
+//   which then share one load of the chunk's K and V; see attention_kernel), then
 //   attention_merge_kernel: log-sum-exp merge of the chunks, normalisation and
 //   sigmoid(gate), written as FP32 or prepared as the o projection's A16
 //   activations.
+#include <algorithm>
+
 #include "q35_quant.h"
 
 namespace q35 {
@@ -37,7 +41,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_prep_kernel(AttnPrepArgs a)
   const float cs = a.rope_cos[static_cast<size_t>(pos) * half + rd];
   const float sn = a.rope_sin[static_cast<size_t>(pos) * half + rd];
   const int pshift = __builtin_ctz(static_cast<unsigned>(a.page_tokens));  // a power of two
-  const int page = a.page_table[static_cast<size_t>(r) * a.max_pages + (pos >> pshift)];
+  const int prow = a.row_seg != nullptr ? a.row_seg[r] : r;
+  const int page = a.page_table[static_cast<size_t>(prow) * a.max_pages + (pos >> pshift)];
   // q head: [q | gate] of the head; k head: its K row and its V row
   const int col_x = is_q ? slot * 2 * hd + dd : a.heads * 2 * hd + g * hd + dd;
   const int col_2 = is_q ? slot * 2 * hd + hd + dd : a.heads * 2 * hd + a.kv_heads * hd + g * hd + dd;
@@ -83,44 +88,54 @@ constexpr int kScoreThreads = 512;
 constexpr int kScoreWaves = kScoreThreads / 64;
 constexpr int kQStride = 36;  // 32 dims + 4: the eight dim slices land on distinct LDS banks
 
-template <int QPK>
+template <int QPK, bool TILED>
 __global__ __launch_bounds__(kScoreThreads) __attribute__((amdgpu_waves_per_eu(4))) void attention_kernel(AttnArgs a) {
   constexpr int NQ = (QPK * kHeadDim + kScoreThreads - 1) / kScoreThreads;  // query values staged per thread
   __shared__ float qs[QPK * 8 * kQStride];
   __shared__ float probs[QPK][kChunkTokens];
   __shared__ float s_m[QPK], s_l[QPK];
   __shared__ float red[kScoreWaves][QPK][kHeadDim];
-  const int sp = blockIdx.x, g = blockIdx.y, r = blockIdx.z;
+  const int sp = blockIdx.x, g = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int kq = tid & 7, ti = tid >> 3;
   const int t0 = sp * kChunkTokens;
   const int kvw = a.kv_heads * kHeadDim;
-  const int32_t *pt = a.page_table + static_cast<size_t>(r) * a.max_pages;
+  // the rows of this workgroup: one request row, or a tile of consecutive
+  // positions of one segment (they share its page table, and the last row
+  // has the longest context)
+  const int r0 = TILED ? a.tile_row0[blockIdx.z] : static_cast<int>(blockIdx.z);
+  const int nrows = TILED ? a.tile_rows[blockIdx.z] : 1;
+  const int32_t *pt = a.page_table + static_cast<size_t>(a.row_seg != nullptr ? a.row_seg[r0] : r0) * a.max_pages;
   const int last_page = a.max_pages - 1;
   // page_tokens is a power of two: shifts and masks, not integer division
   const int pshift = __builtin_ctz(static_cast<unsigned>(a.page_tokens)), pmask = a.page_tokens - 1;
+  auto seq_of = [&](int r) { return a.seq_lens != nullptr ? a.seq_lens[r] : a.positions[r] + 1; };
+  auto load_q = [&](int r, float qv[NQ]) {
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) {
+      const int e = min(tid + k * kScoreThreads, QPK * kHeadDim - 1);
+      qv[k] = a.q[(static_cast<size_t>(r) * a.heads + g * QPK + e / kHeadDim) * kHeadDim + e % kHeadDim];
+    }
+  };
   // one round trip: the query heads, the context length and the page-table
   // entries of every token slot (clamped into the row)
   float qv[NQ];
-#pragma unroll
-  for (int k = 0; k < NQ; ++k) {
-    const int e = min(tid + k * kScoreThreads, QPK * kHeadDim - 1);
-    qv[k] = a.q[(static_cast<size_t>(r) * a.heads + g * QPK + e / kHeadDim) * kHeadDim + e % kHeadDim];
-  }
-  const int seq = a.seq_lens != nullptr ? a.seq_lens[r] : a.positions[r] + 1;
+  load_q(r0, qv);
+  const int seq_tile = seq_of(r0 + nrows - 1);
   const int pfirst = pt[min(t0 >> pshift, last_page)];
   const int pk = pt[min((t0 + ti) >> pshift, last_page)];
   int pv[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) pv[j] = pt[min((t0 + wave + 8 * j) >> pshift, last_page)];
-  if (t0 >= seq) return;  // whole workgroup
-  const int n = min(seq - t0, kChunkTokens);
+  if (t0 >= seq_tile) return;  // whole workgroup
+  const int n_tile = min(seq_tile - t0, kChunkTokens);
 
-  // K, then V (the memory counter retires loads in issue order)
-  const bool kin = ti < n;
-  const int ktok = kin ? t0 + ti : t0;
+  // K, then V (the memory counter retires loads in issue order); slots past
+  // the tile's context read the chunk's first token
+  const bool kload = ti < n_tile;
+  const int ktok = kload ? t0 + ti : t0;
   const q35_u32x4 *krow = reinterpret_cast<const q35_u32x4 *>(
-      a.k_pool + ((static_cast<size_t>(kin ? pk : pfirst) << pshift) + (ktok & pmask)) * kvw +
+      a.k_pool + ((static_cast<size_t>(kload ? pk : pfirst) << pshift) + (ktok & pmask)) * kvw +
       static_cast<size_t>(g) * kHeadDim + 32 * kq);
   q35_u32x4 kraw[4];
 #pragma unroll
@@ -128,111 +143,127 @@ __global__ __launch_bounds__(kScoreThreads) __attribute__((amdgpu_waves_per_eu(4
   q35_u32x2 vraw[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const bool vin = wave + 8 * j < n;
+    const bool vin = wave + 8 * j < n_tile;
     const int vt = vin ? t0 + wave + 8 * j : t0;
     vraw[j] = Q35_LOAD_NT(reinterpret_cast<const q35_u32x2 *>(
         a.v_pool + ((static_cast<size_t>(vin ? pv[j] : pfirst) << pshift) + (vt & pmask)) * kvw +
         static_cast<size_t>(g) * kHeadDim + 4 * lane));
   }
 
-  // the group's query heads into LDS, in eight padded 32-dim slices
-#pragma unroll
-  for (int k = 0; k < NQ; ++k) {
-    const int e = tid + k * kScoreThreads;
-    if (e < QPK * kHeadDim) {
-      const int u = e / kHeadDim, d = e % kHeadDim;
-      qs[(u * 8 + d / 32) * kQStride + d % 32] = qv[k];
+  for (int i = 0; i < nrows; ++i) {
+    const int r = r0 + i;
+    const int seq = TILED ? seq_of(r) : seq_tile;
+    if (t0 >= seq) {  // this row's context ends before the chunk (uniform)
+      if (TILED && i + 1 < nrows) load_q(r + 1, qv);
+      continue;
     }
-  }
-  lds_barrier();
+    // tokens past the row's context score -inf and get probability exactly 0
+    // (their V rows are finite), so a row's partial does not depend on the
+    // tile it runs in
+    const int n = min(seq - t0, kChunkTokens);
+    const bool kin = ti < n;
 
-  // ---- scores: 32 dims per thread, then the 8 lanes of the token
-  float part[QPK];
+    // the group's query heads into LDS, in eight padded 32-dim slices (the
+    // previous row's readers passed the barriers of its softmax and P*V)
 #pragma unroll
-  for (int u = 0; u < QPK; ++u) part[u] = 0.0F;
+    for (int k = 0; k < NQ; ++k) {
+      const int e = tid + k * kScoreThreads;
+      if (e < QPK * kHeadDim) {
+        const int u = e / kHeadDim, d = e % kHeadDim;
+        qs[(u * 8 + d / 32) * kQStride + d % 32] = qv[k];
+      }
+    }
+    if (TILED && i + 1 < nrows) load_q(r + 1, qv);  // the next row's query, in flight meanwhile
+    lds_barrier();
+
+    // ---- scores: 32 dims per thread, then the 8 lanes of the token
+    float part[QPK];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float kf[8];
+    for (int u = 0; u < QPK; ++u) part[u] = 0.0F;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      kf[2 * e] = half_bits_to_float(static_cast<uint16_t>(kraw[i][e] & 0xffffu));
-      kf[2 * e + 1] = half_bits_to_float(static_cast<uint16_t>(kraw[i][e] >> 16));
+    for (int i4 = 0; i4 < 4; ++i4) {
+      float kf[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        kf[2 * e] = half_bits_to_float(static_cast<uint16_t>(kraw[i4][e] & 0xffffu));
+        kf[2 * e + 1] = half_bits_to_float(static_cast<uint16_t>(kraw[i4][e] >> 16));
+      }
+#pragma unroll
+      for (int u = 0; u < QPK; ++u) {
+        const float *qp = qs + (u * 8 + kq) * kQStride + 8 * i4;
+        const q35_f32x4 qa = *reinterpret_cast<const q35_f32x4 *>(qp);
+        const q35_f32x4 qb = *reinterpret_cast<const q35_f32x4 *>(qp + 4);
+        part[u] += qa[0] * kf[0] + qa[1] * kf[1] + qa[2] * kf[2] + qa[3] * kf[3] + qb[0] * kf[4] +
+                   qb[1] * kf[5] + qb[2] * kf[6] + qb[3] * kf[7];
+      }
+      // one iteration at a time: no hoisted query reads, no sunk dot products
+#pragma unroll
+      for (int u = 0; u < QPK; ++u) q35_materialize(part[u]);
+      q35_compiler_fence();
     }
 #pragma unroll
     for (int u = 0; u < QPK; ++u) {
-      const float *qp = qs + (u * 8 + kq) * kQStride + 8 * i;
-      const q35_f32x4 qa = *reinterpret_cast<const q35_f32x4 *>(qp);
-      const q35_f32x4 qb = *reinterpret_cast<const q35_f32x4 *>(qp + 4);
-      part[u] += qa[0] * kf[0] + qa[1] * kf[1] + qa[2] * kf[2] + qa[3] * kf[3] + qb[0] * kf[4] +
-                 qb[1] * kf[5] + qb[2] * kf[6] + qb[3] * kf[7];
+      part[u] += q35_row_xor(part[u], 1);
+      part[u] += q35_row_xor(part[u], 2);
+      part[u] += q35_row_xor(part[u], 4);
+      if (kq == 0) probs[u][ti] = kin ? part[u] * a.scale : -INFINITY;
     }
-    // one iteration at a time: no hoisted query reads, no sunk dot products
-#pragma unroll
-    for (int u = 0; u < QPK; ++u) q35_materialize(part[u]);
-    q35_compiler_fence();
-  }
-#pragma unroll
-  for (int u = 0; u < QPK; ++u) {
-    part[u] += q35_row_xor(part[u], 1);
-    part[u] += q35_row_xor(part[u], 2);
-    part[u] += q35_row_xor(part[u], 4);
-    if (kq == 0) probs[u][ti] = kin ? part[u] * a.scale : -INFINITY;
-  }
-  lds_barrier();
+    lds_barrier();
 
-  // ---- chunk softmax statistics (wave u handles head u)
-  for (int u = wave; u < QPK; u += kScoreWaves) {
-    const float s = probs[u][lane];
-    const float m = group_max<64>(s);
-    const float p = lane < n ? expf(s - m) : 0.0F;
-    const float l = group_sum<64>(p);
-    probs[u][lane] = p;
-    if (lane == 0) {
-      s_m[u] = m;
-      s_l[u] = l;
+    // ---- chunk softmax statistics (wave u handles head u)
+    for (int u = wave; u < QPK; u += kScoreWaves) {
+      const float s = probs[u][lane];
+      const float m = group_max<64>(s);
+      const float p = lane < n ? expf(s - m) : 0.0F;
+      const float l = group_sum<64>(p);
+      probs[u][lane] = p;
+      if (lane == 0) {
+        s_m[u] = m;
+        s_l[u] = l;
+      }
     }
-  }
-  lds_barrier();
+    lds_barrier();
 
-  // ---- P*V over this wave's tokens, then the fixed-order wave sum
-  float acc[QPK][4];
+    // ---- P*V over this wave's tokens, then the fixed-order wave sum
+    float acc[QPK][4];
 #pragma unroll
-  for (int u = 0; u < QPK; ++u) acc[u][0] = acc[u][1] = acc[u][2] = acc[u][3] = 0.0F;
+    for (int u = 0; u < QPK; ++u) acc[u][0] = acc[u][1] = acc[u][2] = acc[u][3] = 0.0F;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int i = wave + 8 * j;
-    const float v0 = half_bits_to_float(static_cast<uint16_t>(vraw[j][0] & 0xffffu));
-    const float v1 = half_bits_to_float(static_cast<uint16_t>(vraw[j][0] >> 16));
-    const float v2 = half_bits_to_float(static_cast<uint16_t>(vraw[j][1] & 0xffffu));
-    const float v3 = half_bits_to_float(static_cast<uint16_t>(vraw[j][1] >> 16));
+    for (int j = 0; j < 8; ++j) {
+      const int t = wave + 8 * j;
+      const float v0 = half_bits_to_float(static_cast<uint16_t>(vraw[j][0] & 0xffffu));
+      const float v1 = half_bits_to_float(static_cast<uint16_t>(vraw[j][0] >> 16));
+      const float v2 = half_bits_to_float(static_cast<uint16_t>(vraw[j][1] & 0xffffu));
+      const float v3 = half_bits_to_float(static_cast<uint16_t>(vraw[j][1] >> 16));
 #pragma unroll
-    for (int u = 0; u < QPK; ++u) {
-      const float p = probs[u][i];  // 0 past the chunk's tokens
-      acc[u][0] += p * v0;
-      acc[u][1] += p * v1;
-      acc[u][2] += p * v2;
-      acc[u][3] += p * v3;
+      for (int u = 0; u < QPK; ++u) {
+        const float p = probs[u][t];  // 0 past the row's tokens
+        acc[u][0] += p * v0;
+        acc[u][1] += p * v1;
+        acc[u][2] += p * v2;
+        acc[u][3] += p * v3;
+      }
+#pragma unroll
+      for (int u = 0; u < QPK; ++u)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) q35_materialize(acc[u][k]);
+      q35_compiler_fence();
     }
 #pragma unroll
     for (int u = 0; u < QPK; ++u)
+      *reinterpret_cast<q35_f32x4 *>(&red[wave][u][4 * lane]) = q35_f32x4{acc[u][0], acc[u][1], acc[u][2], acc[u][3]};
+    lds_barrier();
+    for (int e = tid; e < QPK * kHeadDim; e += kScoreThreads) {
+      const int u = e / kHeadDim, d = e % kHeadDim;
+      float v = red[0][u][d];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) q35_materialize(acc[u][k]);
-    q35_compiler_fence();
-  }
-#pragma unroll
-  for (int u = 0; u < QPK; ++u)
-    *reinterpret_cast<q35_f32x4 *>(&red[wave][u][4 * lane]) = q35_f32x4{acc[u][0], acc[u][1], acc[u][2], acc[u][3]};
-  lds_barrier();
-  for (int e = tid; e < QPK * kHeadDim; e += kScoreThreads) {
-    const int u = e / kHeadDim, d = e % kHeadDim;
-    float v = red[0][u][d];
-#pragma unroll
-    for (int w = 1; w < kScoreWaves; ++w) v += red[w][u][d];
-    const size_t hs = (static_cast<size_t>(r) * a.heads + g * QPK + u) * a.max_splits + sp;
-    a.part_o[hs * kHeadDim + d] = v;
-    if (d == 0) {
-      a.part_ml[hs * 2] = s_m[u];
-      a.part_ml[hs * 2 + 1] = s_l[u];
+      for (int w = 1; w < kScoreWaves; ++w) v += red[w][u][d];
+      const size_t hs = (static_cast<size_t>(r) * a.heads + g * QPK + u) * a.max_splits + sp;
+      a.part_o[hs * kHeadDim + d] = v;
+      if (d == 0) {
+        a.part_ml[hs * 2] = s_m[u];
+        a.part_ml[hs * 2 + 1] = s_l[u];
+      }
     }
   }
 }
@@ -344,14 +375,22 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
   if (a.head_dim != kHeadDim || a.heads % a.kv_heads != 0 || a.split_tokens != kChunkTokens)
     return hipErrorInvalidValue;
   const int qpk = a.heads / a.kv_heads;
-  const dim3 grid(a.max_splits, a.kv_heads, a.batch), block(kScoreThreads);
+  const bool tiled = a.tile_row0 != nullptr;
+  const int gs = a.grid_splits > 0 ? std::min(a.grid_splits, a.max_splits) : a.max_splits;
+  const dim3 grid(gs, a.kv_heads, tiled ? a.tiles : a.batch), block(kScoreThreads);
+#define Q35_ATTN(Q)                                                             \
+  if (tiled)                                                                    \
+    Q35_LAUNCH((attention_kernel<Q, true>), grid, block, 0, stream, a);        \
+  else                                                                          \
+    Q35_LAUNCH((attention_kernel<Q, false>), grid, block, 0, stream, a);
   switch (qpk) {
-    case 1: Q35_LAUNCH((attention_kernel<1>), grid, block, 0, stream, a); break;
-    case 2: Q35_LAUNCH((attention_kernel<2>), grid, block, 0, stream, a); break;
-    case 4: Q35_LAUNCH((attention_kernel<4>), grid, block, 0, stream, a); break;
-    case 8: Q35_LAUNCH((attention_kernel<8>), grid, block, 0, stream, a); break;
+    case 1: Q35_ATTN(1) break;
+    case 2: Q35_ATTN(2) break;
+    case 4: Q35_ATTN(4) break;
+    case 8: Q35_ATTN(8) break;
     default: return hipErrorInvalidValue;
   }
+#undef Q35_ATTN
   return hipGetLastError();
 }
 

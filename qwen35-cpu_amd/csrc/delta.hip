@@ -268,9 +268,11 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
 }
 
 // Chunked prefill (prefill.inl:599-791 runs a prompt in chunks; the
-// recurrence itself is delta_net.cpp:63-98 per token). The `batch` rows are
-// consecutive positions positions[0] .. positions[0] + batch - 1 of ONE
-// request, and the in-projection rows arrive already summed (one split).
+// recurrence itself is delta_net.cpp:63-98 per token). The rows form
+// segments (row_seg, seg_row0, seg_count): each segment is consecutive
+// positions of ONE request -- a prompt chunk, or a single decode row -- and
+// the in-projection rows arrive already summed (one split). Without segment
+// arrays the `batch` rows are one segment.
 // Only the state recurrence is sequential, so a chunk runs as three kernels:
 //   1. delta_chunk_inputs_kernel, one workgroup per (value head, token):
 //      causal conv + SiLU, L2 norms, beta and alpha of every token at once
@@ -298,7 +300,9 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_chunk_inputs_kernel(Delta
   const int kh = vh / per;
   const int q_dim = a.k_heads * kDim, v_dim = a.v_heads * kDim;
   const int channels = 2 * q_dim + v_dim;
-  const int slot = a.slots[0], pos0 = a.positions[0], pos = pos0 + r;
+  // the row's segment: rows seg_row0 .. are consecutive positions of its slot
+  const int r0 = a.row_seg != nullptr ? a.seg_row0[a.row_seg[r]] : 0;
+  const int slot = a.slots[r0], pos0 = a.positions[r0], pos = pos0 + (r - r0);
   const float *conv = a.conv_base + static_cast<long long>(slot) * a.conv_slot_stride;
   const int i = tid & (kDim - 1);
   const bool is_k = tid >= kDim, has_v = tid < kDim;
@@ -319,7 +323,7 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_chunk_inputs_kernel(Delta
   for (int k = 0; k < K - 1; ++k) {
     const int p = pos - (K - 1) + k;  // oldest first
     if (p >= pos0) {
-      const float *hrow = a.proj.p + static_cast<long long>(p - pos0) * a.proj.width;
+      const float *hrow = a.proj.p + static_cast<long long>(r0 + p - pos0) * a.proj.width;
       hq[k] = hrow[chq];
       hv[k] = hrow[chv];
     } else {
@@ -370,7 +374,10 @@ __global__ __launch_bounds__(64) void delta_scan_kernel(DeltaArgs a) {
   __shared__ q35_f32x4 qk_lds[2][2 * kDim / 4];
   const int lane = threadIdx.x, vh = blockIdx.y;
   const int quad = lane & 3, row = kDeltaScanRows * blockIdx.x + (lane >> 2);
-  const int slot = a.slots[0], pos0 = a.positions[0], count = a.batch;
+  // segment blockIdx.z: rows r0 .. r0 + count - 1 of one slot, in order
+  const int r0 = a.row_seg != nullptr ? a.seg_row0[blockIdx.z] : 0;
+  const int count = a.row_seg != nullptr ? a.seg_count[blockIdx.z] : a.batch;
+  const int slot = a.slots[r0], pos0 = a.positions[r0];
   const int rpar = a.state_copy_stride > 0 ? (pos0 & 1) : 0;
   const int wpar = a.state_copy_stride > 0 ? ((pos0 + count) & 1) : 0;
   float *state_slot = a.state_base + static_cast<long long>(slot) * a.state_slot_stride;
@@ -380,9 +387,10 @@ __global__ __launch_bounds__(64) void delta_scan_kernel(DeltaArgs a) {
   q35_f32x4 st[8];
 #pragma unroll
   for (int m = 0; m < 8; ++m) st[m] = Q35_LOAD_NT(S + 4 * m);
-  const float *scan = a.scan + static_cast<size_t>(vh) * kDeltaScanStride;
   const size_t tstride = static_cast<size_t>(a.v_heads) * kDeltaScanStride;
-  float *outs = a.scan + static_cast<size_t>(count) * tstride + static_cast<size_t>(vh) * kDim + row;
+  const float *scan = a.scan + static_cast<size_t>(r0) * tstride + static_cast<size_t>(vh) * kDeltaScanStride;
+  float *outs = a.scan + static_cast<size_t>(a.batch) * tstride + static_cast<size_t>(r0) * a.v_heads * kDim +
+                static_cast<size_t>(vh) * kDim + row;
   auto load = [&](ScanToken &t, int r) {
     const float *e = scan + static_cast<size_t>(r) * tstride;
     t.qk = reinterpret_cast<const q35_f32x4 *>(e)[lane];
@@ -480,12 +488,15 @@ __global__ __launch_bounds__(64) void delta_chunk_out_kernel(DeltaArgs a) {
     qo.scales = a.scales;
     h128_quantize_row16(y, r, vh, v_dim / 32, true, a.seed, qo, writer);
   }
-  // the chunk's last K-1 raw inputs into the ring (slot = position % K); the
-  // inputs kernel read the ring before this launch
-  if (r >= a.batch - (K - 1)) {
+  // the segment's last K-1 raw inputs into the ring (slot = position % K);
+  // the inputs kernel read the ring before this launch
+  const int seg = a.row_seg != nullptr ? a.row_seg[r] : 0;
+  const int seg_end = a.row_seg != nullptr ? a.seg_row0[seg] + a.seg_count[seg] : a.batch;
+  if (r >= seg_end - (K - 1)) {
     const int per = a.v_heads / a.k_heads, kh = vh / per;
-    float *ring = a.conv_base + static_cast<long long>(a.slots[0]) * a.conv_slot_stride +
-                  static_cast<size_t>((a.positions[0] + r) & (K - 1)) * channels;
+    const int r0 = a.row_seg != nullptr ? a.seg_row0[seg] : 0;
+    float *ring = a.conv_base + static_cast<long long>(a.slots[r0]) * a.conv_slot_stride +
+                  static_cast<size_t>((a.positions[r0] + (r - r0)) & (K - 1)) * channels;
     for (int c = lane; c < kDim; c += 64) {
       if (vh % per == 0) {
         ring[kh * kDim + c] = prow[kh * kDim + c];
@@ -523,7 +534,8 @@ hipError_t launch_delta_chunk(const DeltaArgs &a, hipStream_t stream) {
       a.proj.splits != 1)
     return hipErrorInvalidValue;
   Q35_LAUNCH((delta_chunk_inputs_kernel), dim3(a.v_heads, a.batch), dim3(kDeltaThreads), 0, stream, a);
-  Q35_LAUNCH((delta_scan_kernel), dim3(kDim / kDeltaScanRows, a.v_heads), dim3(64), 0, stream, a);
+  Q35_LAUNCH((delta_scan_kernel), dim3(kDim / kDeltaScanRows, a.v_heads, a.row_seg != nullptr ? a.segments : 1),
+             dim3(64), 0, stream, a);
   Q35_LAUNCH((delta_chunk_out_kernel), dim3(a.v_heads, a.batch), dim3(64), 0, stream, a);
   return hipGetLastError();
 }

@@ -96,13 +96,15 @@ __global__ __launch_bounds__(kRmsThreads) void rms_prep_kernel(RmsPrepArgs a) {
       w1[4 + e] = hi[e] + 1.0F;
     }
   }
-  const q35_f32x4 *xin = reinterpret_cast<const q35_f32x4 *>(a.x_in + static_cast<size_t>(t) * K);
+  // the residual row of output row t (a gathered row set: the head rows)
+  const size_t xr = a.rows != nullptr ? static_cast<size_t>(a.rows[t]) : static_cast<size_t>(t);
+  const q35_f32x4 *xin = reinterpret_cast<const q35_f32x4 *>(a.x_in + xr * K);
   float ss = 0.0F;
   for (int i = tid; i < n4; i += kRmsThreads) {
     q35_f32x4 v = xin[i];
     if constexpr (MS > 0) {
       // columns 4i..4i+3 of every split, all loads in flight together
-      const float *pp = a.add.p + static_cast<size_t>(t) * a.add.width + 4 * i;
+      const float *pp = a.add.p + xr * a.add.width + 4 * i;
       q35_f32x4 x[MS];
 #pragma unroll
       for (int u = 0; u < MS; ++u)
@@ -113,7 +115,7 @@ __global__ __launch_bounds__(kRmsThreads) void rms_prep_kernel(RmsPrepArgs a) {
       for (int u = 1; u < MS; ++u)
         if (u < a.add.splits) sum += x[u];
       v += sum;
-      reinterpret_cast<q35_f32x4 *>(a.x_out + static_cast<size_t>(t) * K)[i] = v;
+      reinterpret_cast<q35_f32x4 *>(a.x_out + xr * K)[i] = v;
     }
     *reinterpret_cast<q35_f32x4 *>(&y[4 * i]) = v;
     ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];

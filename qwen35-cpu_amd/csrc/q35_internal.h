@@ -47,7 +47,8 @@ static_assert(offsetof(q35_q8_0_block_x1, qs) == 6, "Q8_0BlockX1 layout");
 // code sums the reference keeps beside each block (the offset-binary
 // correction of q4_dot4_simd.inl:89) are re-derived by the GEMM with an MFMA.
 constexpr float kH128InvSqrt = 0.08838834764831844055F;  // q4_h128.h:24
-constexpr int kMaxTokens = 64;                            // rows per GEMM launch
+constexpr int kMaxTokens = 64;                            // rows per split GEMM launch
+constexpr int kMaxStepRows = 8192;                        // rows per packed step (runtime bound)
 
 // ------------------------------------------------------------ launchers
 // All launchers enqueue on `stream` and return hipSuccess or the launch error.
@@ -159,6 +160,9 @@ struct RmsPrepArgs {
   uint64_t *codes = nullptr;
   float *scales = nullptr;
   float *normed_out = nullptr;   // optional [tokens][K]
+  // optional: residual row of each output row (x_in, add and x_out rows are
+  // rows[t]; codes, normed_out and gates stay at t)
+  const int32_t *rows = nullptr;
   // optional Q8 gate rows (run_q8_gate_tail, weights.inl:1015-1034): the
   // normalized row quantized in the identity basis, then gate_rows Q8 rows
   // (codes [gate_rows][K], F32 block scales [gate_rows][K/32]) written as
@@ -292,11 +296,16 @@ struct DeltaArgs {
   // chunked prefill: per-token scan entries, then the raw head outputs
   // (delta_chunk_scan_floats(batch, v_heads) floats)
   float *scan = nullptr;
+  // chunked prefill segments (NULL: the batch is one segment): segment of
+  // each row, first row and row count of each segment
+  const int32_t *row_seg = nullptr, *seg_row0 = nullptr, *seg_count = nullptr;
+  int segments = 0;
 };
 hipError_t launch_delta(const DeltaArgs &a, hipStream_t stream);
-// Chunked prefill: the `batch` rows are consecutive positions of ONE request
-// (slots[0], positions[0] + r) with the in-projection rows summed (one split);
-// the state recurrence is scanned in order, everything else runs per token.
+// Chunked prefill: each segment's rows are consecutive positions of ONE
+// request (without segment arrays: the whole batch, slots[0], positions[0] + r)
+// with the in-projection rows summed (one split); the state recurrence is
+// scanned in order per segment, everything else runs per token.
 constexpr int kDeltaScanStride = 3 * 128 + 4;  // q | k | v | alpha | beta | pad
 inline size_t delta_chunk_scan_floats(int batch, int v_heads) {
   return static_cast<size_t>(batch) * v_heads * (kDeltaScanStride + 128);
@@ -328,7 +337,8 @@ struct AttnPrepArgs {
   float eps = 1e-6F;
   const float *rope_cos = nullptr, *rope_sin = nullptr;  // [max_context][rope_dim/2]
   const int32_t *positions = nullptr;
-  const int32_t *page_table = nullptr;  // [batch][max_pages]
+  const int32_t *page_table = nullptr;  // [segment][max_pages]
+  const int32_t *row_seg = nullptr;     // segment (page-table row) of each row; NULL: the row itself
   int max_pages = 0, page_tokens = 0;
   uint16_t *k_pool = nullptr, *v_pool = nullptr;  // this layer's pool base
   float *q_out = nullptr, *gate_out = nullptr;    // [batch][heads][head_dim]
@@ -345,9 +355,16 @@ struct AttnArgs {
   int batch = 0, heads = 0, kv_heads = 0, head_dim = 0;
   float scale = 0.0625F;
   int split_tokens = 64, max_splits = 1;  // split_tokens must be kAttnChunkTokens
+  int grid_splits = 0;            // chunks launched per row (>= the longest context's; 0: max_splits)
   float *part_o = nullptr;        // [batch][heads][max_splits][head_dim]
   float *part_ml = nullptr;       // [batch][heads][max_splits][2]
+  const int32_t *row_seg = nullptr;  // page-table row of each row (NULL: the row itself)
+  // query tiles (NULL: one workgroup per row): tile z covers rows
+  // tile_row0[z] .. + tile_rows[z] - 1, consecutive positions of one segment
+  const int32_t *tile_row0 = nullptr, *tile_rows = nullptr;
+  int tiles = 0;
 };
+constexpr int kAttnTileRows = 16;  // query rows per tile
 hipError_t launch_attention(const AttnArgs &a, hipStream_t stream);
 // Merge of the chunk partials + sigmoid gate: FP32 rows into `out` and/or the
 // o projection's A16 activations into codes/scales (either may be null).

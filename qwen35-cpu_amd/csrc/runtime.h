@@ -2,6 +2,7 @@
 // device state, the paged KV pool and the captured decode step.
 #pragma once
 
+#include <array>
 #include <map>
 #include <set>
 #include <string>
@@ -29,6 +30,22 @@ struct LayerDev {
   const float *gate_scales = nullptr;
 };
 
+// Shape of one packed step: `rows` rows in `segments` segments (each a run
+// of consecutive positions of one request; a decode row is a segment of one),
+// `heads` rows that get a token (the last row of their segment), `tiles`
+// attention query tiles, and the chunks of the longest context (rounded up
+// to a power of two) the attention grid covers.
+struct StepShape {
+  int rows = 0, segments = 0, heads = 0, tiles = 0, grid_splits = 1;
+  bool single = true;          // every segment is one row (the decode kernels)
+  bool heads_identity = true;  // head h is row h
+  std::array<int, 7> key(bool want_logits) const {
+    return {rows, segments, heads, tiles, grid_splits, (single ? 1 : 0) | (heads_identity ? 2 : 0),
+            want_logits ? 1 : 0};
+  }
+};
+constexpr int kMaxPrefillSegments = 16;  // prefill segments per packed step
+
 }  // namespace q35
 
 struct q35_model {
@@ -53,6 +70,8 @@ struct q35_runtime {
   q35::Context *ctx = nullptr;
   q35_runtime_config cfg{};
   int max_pages_per_row = 0;
+  int max_rows = 0;      // rows per packed step (>= cfg.max_batch)
+  int max_segments = 0;  // segments (and head rows) per packed step
   int split_tokens = q35::kAttnChunkTokens, max_splits = 1;
   // slot state
   float *recurrent = nullptr;  // [slots][2 copies][n_lin][vh][vd][kd]
@@ -68,9 +87,9 @@ struct q35_runtime {
   float *rope_cos = nullptr, *rope_sin = nullptr;
   // work buffers
   float *x[2] = {nullptr, nullptr};  // residual stream, ping-pong
-  float *proj = nullptr, *core = nullptr, *q_rot = nullptr, *gates = nullptr;
-  float *q8_gates = nullptr;      // Q8 gate rows of the in projection [batch][kMaxGateRows]
-  float *rows_final = nullptr;  // prefill: summed in-projection rows [batch][proj_width]
+  float *proj = nullptr, *q_rot = nullptr, *gates = nullptr;
+  float *q8_gates = nullptr;      // Q8 gate rows of the in projection [rows][kMaxGateRows]
+  float *rows_final = nullptr;  // chunked steps of split GEMMs: summed in-projection rows [rows][proj_width]
   float *delta_scan = nullptr;  // prefill: DeltaNet chunk scan entries and raw outputs
   unsigned long long *sample_scratch = nullptr;  // sampling: the slices' surviving keys
   q35_candidate *candidates = nullptr;           // sampling: [max_batch][kMaxCandidates]
@@ -87,7 +106,8 @@ struct q35_runtime {
   unsigned char *meta_host = nullptr, *meta_dev = nullptr;
   int32_t *tokens_out_host = nullptr;
   size_t proj_width = 0, core_width = 0;
-  std::map<std::pair<int, int>, hipGraphExec_t> graphs;
+  q35::StepShape shape;  // of the step last packed
+  std::map<std::array<int, 7>, hipGraphExec_t> graphs;
   int last_batch = 0;
   std::vector<void *> allocations;
   // kernel-level timing: event pairs reused across steps, the (class, bytes)
@@ -104,9 +124,9 @@ struct q35_runtime {
 };
 
 namespace q35 {
-// `prefill`: the rows are consecutive positions of one request (a prompt
-// chunk); the DeltaNet recurrence then scans them in order.
-int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool prefill);
+// Enqueues one packed step whose metadata is in rt->meta_host (the host copy
+// is part of the enqueued work, so the step can be captured as a graph).
+int runtime_enqueue_step(q35_runtime *rt, const StepShape &shape, bool want_logits);
 // Algorithmic HBM bytes of one GEMM launch: packed weights, A16 codes and
 // scales of every token, FP32 outputs (and the residual read when fused).
 double gemm_algorithmic_bytes(int rows, int nb, int tokens, bool stores, bool residual);

@@ -342,25 +342,44 @@ extern "C" int q35_model_finalize(q35_model *m) {
 namespace {
 
 struct MetaLayout {
-  size_t slots, positions, tokens, seq_lens, penalties, count_input, inv_temperature, top_k, page_table, total;
+  // per row
+  size_t slots, positions, tokens, seq_lens, count_input, row_seg;
+  // per segment: first row, rows, page-table row
+  size_t seg_row0, seg_count, page_table;
+  // per head row (a segment that wants a token): its row, slot, penalty and
+  // sampling settings
+  size_t head_rows, head_slots, head_penalties, inv_temperature, top_k;
+  // attention query tiles
+  size_t tile_row0, tile_rows;
+  size_t total;
 };
 
-MetaLayout meta_layout(int max_batch, int max_pages) {
+MetaLayout meta_layout(int max_rows, int max_segments, int max_pages) {
   MetaLayout L{};
   size_t o = 0;
   auto take = [&](size_t bytes) { const size_t at = o; o = align256(o + bytes); return at; };
-  L.slots = take(max_batch * 4);
-  L.positions = take(max_batch * 4);
-  L.tokens = take(max_batch * 4);
-  L.seq_lens = take(max_batch * 4);
-  L.penalties = take(max_batch * 4);
-  L.count_input = take(max_batch);
-  L.inv_temperature = take(max_batch * 4);
-  L.top_k = take(max_batch * 4);
-  L.page_table = take(static_cast<size_t>(max_batch) * max_pages * 4);
+  const size_t R = static_cast<size_t>(max_rows), M = static_cast<size_t>(max_segments);
+  L.slots = take(R * 4);
+  L.positions = take(R * 4);
+  L.tokens = take(R * 4);
+  L.seq_lens = take(R * 4);
+  L.count_input = take(R);
+  L.row_seg = take(R * 4);
+  L.seg_row0 = take(M * 4);
+  L.seg_count = take(M * 4);
+  L.page_table = take(M * static_cast<size_t>(max_pages) * 4);
+  L.head_rows = take(M * 4);
+  L.head_slots = take(M * 4);
+  L.head_penalties = take(M * 4);
+  L.inv_temperature = take(M * 4);
+  L.top_k = take(M * 4);
+  L.tile_row0 = take(R * 4);
+  L.tile_rows = take(R * 4);
   L.total = o;
   return L;
 }
+
+MetaLayout meta_layout(const q35_runtime *rt) { return meta_layout(rt->max_rows, rt->max_segments, rt->max_pages_per_row); }
 
 }  // namespace
 
@@ -370,7 +389,8 @@ extern "C" int q35_runtime_create(q35_model *m, const q35_runtime_config *cfg, q
   if (!m->finalized) return set_error(m->ctx, Q35_ERR_STATE, "model not finalized");
   const q35_model_dims &d = m->d;
   if (cfg->max_slots <= 0 || cfg->max_batch <= 0 || cfg->max_batch > kMaxTokens ||
-      cfg->max_context <= 0 || cfg->page_tokens < 1 || (cfg->page_tokens & (cfg->page_tokens - 1)))
+      cfg->max_context <= 0 || cfg->page_tokens < 1 || (cfg->page_tokens & (cfg->page_tokens - 1)) ||
+      cfg->max_step_rows < 0 || cfg->max_step_rows > kMaxStepRows)
     return set_error(m->ctx, Q35_ERR_INVALID, "invalid runtime config");
   auto *rt = new (std::nothrow) q35_runtime();
   if (rt == nullptr) return Q35_ERR_OOM;
@@ -380,8 +400,12 @@ extern "C" int q35_runtime_create(q35_model *m, const q35_runtime_config *cfg, q
   rt->max_pages_per_row = (cfg->max_context + cfg->page_tokens - 1) / cfg->page_tokens;
   rt->max_splits = (cfg->max_context + rt->split_tokens - 1) / rt->split_tokens;
   if (rt->cfg.total_pages <= 0) rt->cfg.total_pages = cfg->max_slots * rt->max_pages_per_row;
+  rt->max_rows = std::max(cfg->max_batch, cfg->max_step_rows);
+  rt->max_segments = cfg->max_batch + kMaxPrefillSegments;
   Context *ctx = m->ctx;
-  const int B = cfg->max_batch;
+  // R rows of a packed step, M segments (and head rows); a split GEMM runs
+  // up to kMaxTokens rows, the dense GEMM (no partials) anything larger
+  const int R = rt->max_rows, M = rt->max_segments, Bs = std::min(R, kMaxTokens);
   const size_t H = d.hidden, I = d.intermediate;
   const size_t v_dim = static_cast<size_t>(d.lin_v_heads) * d.lin_v_dim;
   const size_t q_dim = static_cast<size_t>(d.lin_k_heads) * d.lin_k_dim;
@@ -414,45 +438,48 @@ extern "C" int q35_runtime_create(q35_model *m, const q35_runtime_config *cfg, q
   alloc(static_cast<size_t>(cfg->max_context) * half * 4, reinterpret_cast<void **>(&rt->rope_cos));
   alloc(static_cast<size_t>(cfg->max_context) * half * 4, reinterpret_cast<void **>(&rt->rope_sin));
   // work buffers
-  alloc(B * H * 4, reinterpret_cast<void **>(&rt->x[0]));
-  alloc(B * H * 4, reinterpret_cast<void **>(&rt->x[1]));
-  // GEMM outputs: [split][batch][rows] for the largest split plan of any projection
-  size_t proj_floats = static_cast<size_t>(B) * rt->proj_width;
+  alloc(static_cast<size_t>(R) * H * 4, reinterpret_cast<void **>(&rt->x[0]));
+  alloc(static_cast<size_t>(R) * H * 4, reinterpret_cast<void **>(&rt->x[1]));
+  // GEMM outputs: [split][rows][width] for the largest split plan of any
+  // projection (split launches, up to kMaxTokens rows), [rows][width] for
+  // the dense GEMM
+  size_t proj_floats = static_cast<size_t>(R) * rt->proj_width;
   for (const auto &L : m->layers) {
-    proj_floats = std::max(proj_floats, gemm_partial_floats(L.in_rows, d.hidden / 32, B, ctx->cu_count));
-    proj_floats = std::max(proj_floats, gemm_partial_floats(d.hidden, L.out_cols / 32, B, ctx->cu_count));
-    proj_floats = std::max(proj_floats, gemm_partial_floats(2 * d.intermediate, d.hidden / 32, B, ctx->cu_count));
-    proj_floats = std::max(proj_floats, gemm_partial_floats(d.hidden, d.intermediate / 32, B, ctx->cu_count));
+    proj_floats = std::max(proj_floats, gemm_partial_floats(L.in_rows, d.hidden / 32, Bs, ctx->cu_count));
+    proj_floats = std::max(proj_floats, gemm_partial_floats(d.hidden, L.out_cols / 32, Bs, ctx->cu_count));
+    proj_floats = std::max(proj_floats, gemm_partial_floats(2 * d.intermediate, d.hidden / 32, Bs, ctx->cu_count));
+    proj_floats = std::max(proj_floats, gemm_partial_floats(d.hidden, d.intermediate / 32, Bs, ctx->cu_count));
   }
   alloc(proj_floats * 4, reinterpret_cast<void **>(&rt->proj));
-  // prefill: the in projection's split partials summed once, [batch][rows]
-  alloc(static_cast<size_t>(B) * rt->proj_width * 4, reinterpret_cast<void **>(&rt->rows_final));
-  alloc(static_cast<size_t>(B) * kMaxGateRows * 4, reinterpret_cast<void **>(&rt->q8_gates));
+  // chunked steps of split GEMMs: the in projection's split partials summed
+  // once, [rows][width]
+  alloc(static_cast<size_t>(Bs) * rt->proj_width * 4, reinterpret_cast<void **>(&rt->rows_final));
+  alloc(static_cast<size_t>(R) * kMaxGateRows * 4, reinterpret_cast<void **>(&rt->q8_gates));
   if (d.lin_v_heads > 0)
-    alloc(delta_chunk_scan_floats(B, d.lin_v_heads) * 4, reinterpret_cast<void **>(&rt->delta_scan));
-  // sampling: per-row candidate lists and the slices' survivors
-  alloc(sample_scratch_bytes(B), reinterpret_cast<void **>(&rt->sample_scratch));
-  alloc(static_cast<size_t>(B) * kMaxCandidates * sizeof(q35_candidate), reinterpret_cast<void **>(&rt->candidates));
-  alloc(B * rt->core_width * 4, reinterpret_cast<void **>(&rt->core));
-  alloc(B * static_cast<size_t>(d.n_heads) * d.head_dim * 4, reinterpret_cast<void **>(&rt->q_rot));
-  alloc(B * static_cast<size_t>(d.n_heads) * d.head_dim * 4, reinterpret_cast<void **>(&rt->gates));
-  const size_t parts = static_cast<size_t>(B) * d.n_heads * rt->max_splits;
+    alloc(delta_chunk_scan_floats(R, d.lin_v_heads) * 4, reinterpret_cast<void **>(&rt->delta_scan));
+  // sampling: per-head-row candidate lists and the slices' survivors
+  alloc(sample_scratch_bytes(M), reinterpret_cast<void **>(&rt->sample_scratch));
+  alloc(static_cast<size_t>(M) * kMaxCandidates * sizeof(q35_candidate), reinterpret_cast<void **>(&rt->candidates));
+  alloc(static_cast<size_t>(R) * d.n_heads * d.head_dim * 4, reinterpret_cast<void **>(&rt->q_rot));
+  alloc(static_cast<size_t>(R) * d.n_heads * d.head_dim * 4, reinterpret_cast<void **>(&rt->gates));
+  const size_t parts = static_cast<size_t>(R) * d.n_heads * rt->max_splits;
   alloc(parts * d.head_dim * 4, reinterpret_cast<void **>(&rt->part_o));
   alloc(parts * 2 * 4, reinterpret_cast<void **>(&rt->part_ml));
-  alloc(B * H * 4, reinterpret_cast<void **>(&rt->hidden_out));
+  alloc(static_cast<size_t>(M) * H * 4, reinterpret_cast<void **>(&rt->hidden_out));
   const size_t kmax = std::max({H, I, rt->core_width});
-  alloc(4 * 64 * (kmax / 32) * 8, reinterpret_cast<void **>(&rt->codes));
-  alloc(4 * 16 * (kmax / 32) * sizeof(float), reinterpret_cast<void **>(&rt->scales));
+  const size_t tiles = (static_cast<size_t>(R) + 15) / 16;
+  alloc(tiles * 64 * (kmax / 32) * 8, reinterpret_cast<void **>(&rt->codes));
+  alloc(tiles * 16 * (kmax / 32) * sizeof(float), reinterpret_cast<void **>(&rt->scales));
   rt->cand_rows = gemm_argmax_cand_capacity(d.vocab, ctx->cu_count);
   alloc(static_cast<size_t>(rt->cand_rows) * kMaxTokens * 8, reinterpret_cast<void **>(&rt->cand));
-  const MetaLayout ml = meta_layout(B, rt->max_pages_per_row);
+  const MetaLayout ml = meta_layout(rt);
   rt->meta_bytes = ml.total;
   alloc(ml.total, reinterpret_cast<void **>(&rt->meta_dev));
   if (st == Q35_OK && hipHostMalloc(reinterpret_cast<void **>(&rt->meta_host), ml.total) != hipSuccess)
     st = set_error(ctx, Q35_ERR_OOM, "pinned metadata");
   // the greedy tokens are stored by the argmax kernel straight into pinned
   // host memory (no copy node at the end of the step)
-  if (st == Q35_OK && hipHostMalloc(reinterpret_cast<void **>(&rt->tokens_out_host), kMaxTokens * 4) != hipSuccess)
+  if (st == Q35_OK && hipHostMalloc(reinterpret_cast<void **>(&rt->tokens_out_host), static_cast<size_t>(M) * 4) != hipSuccess)
     st = set_error(ctx, Q35_ERR_OOM, "pinned output");
   if (st == Q35_OK &&
       hipHostGetDevicePointer(reinterpret_cast<void **>(&rt->tokens_out_dev), rt->tokens_out_host, 0) != hipSuccess)
@@ -667,20 +694,31 @@ static hipError_t trace_copy(q35_runtime *rt, int layer, int point, const void *
   return e;
 }
 
-int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool prefill) {
+int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits) {
   q35_model *m = rt->model;
   Context *ctx = rt->ctx;
   const q35_model_dims &d = m->d;
   hipStream_t s = ctx->stream;
-  const MetaLayout ml = meta_layout(rt->cfg.max_batch, rt->max_pages_per_row);
+  const int batch = sh.rows;
+  // segments of several positions: the DeltaNet chunk scan and the tiled
+  // attention (a decode-only step runs the per-row kernels)
+  const bool chunked = !sh.single;
+  const MetaLayout ml = meta_layout(rt);
   auto *mdev = rt->meta_dev;
   const auto *slots = reinterpret_cast<const int32_t *>(mdev + ml.slots);
   const auto *positions = reinterpret_cast<const int32_t *>(mdev + ml.positions);
   const auto *tokens = reinterpret_cast<const int32_t *>(mdev + ml.tokens);
   const auto *seq_lens = reinterpret_cast<const int32_t *>(mdev + ml.seq_lens);
-  const auto *penalties = reinterpret_cast<const float *>(mdev + ml.penalties);
   const auto *count_input = reinterpret_cast<const uint8_t *>(mdev + ml.count_input);
+  const auto *row_seg = reinterpret_cast<const int32_t *>(mdev + ml.row_seg);
+  const auto *seg_row0 = reinterpret_cast<const int32_t *>(mdev + ml.seg_row0);
+  const auto *seg_count = reinterpret_cast<const int32_t *>(mdev + ml.seg_count);
   const auto *page_table = reinterpret_cast<const int32_t *>(mdev + ml.page_table);
+  const auto *head_rows = reinterpret_cast<const int32_t *>(mdev + ml.head_rows);
+  const auto *head_slots = reinterpret_cast<const int32_t *>(mdev + ml.head_slots);
+  const auto *head_penalties = reinterpret_cast<const float *>(mdev + ml.head_penalties);
+  const auto *tile_row0 = reinterpret_cast<const int32_t *>(mdev + ml.tile_row0);
+  const auto *tile_rows = reinterpret_cast<const int32_t *>(mdev + ml.tile_rows);
   const int H = d.hidden, I = d.intermediate;
   const int v_dim = d.lin_v_heads * d.lin_v_dim;
   const int q_dim = d.lin_k_heads * d.lin_k_dim;
@@ -727,6 +765,25 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
   // attention prep, the SiLU prep) get GEMMs split at most that many ways.
   constexpr int kConsumerSplits = 8;
   auto gemm = [&](const q35_q4_0_block_x8 *w, int rows, int K, int max_split = 32) -> hipError_t {
+    if (batch > kMaxTokens) {
+      // the dense GEMM: finished rows with the split launch's bits
+      GemmArgs g;
+      g.w = w;
+      g.rows = rows;
+      g.nb = K / 32;
+      g.codes = rt->codes;
+      g.scales = rt->scales;
+      g.tokens = batch;
+      g.out = rt->proj;
+      g.stride = rows;
+      g.cu_count = ctx->cu_count;
+      g.max_split = max_split;
+      pending.p = rt->proj;
+      pending.splits = 1;
+      pending.split_stride = 0;
+      pending.width = rows;
+      return launch_gemm_dense(g, s);
+    }
     const GemmPlan p = gemm_plan(rows, K / 32, false, false, ctx->cu_count, 0, 0, max_split);
     GemmArgs g;
     g.w = w;
@@ -780,6 +837,7 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
     return B * (H * 4.0 + (add ? pending.splits * H * 4.0 + H * 4.0 : 0.0) + H + H / 32.0 * 4.0) + H * 4.0;
   };
   auto gemm_bytes = [&](int rows, int K, int max_split = 32) {
+    if (batch > kMaxTokens) return gemm_algorithmic_bytes(rows, K / 32, batch, true, false);
     const GemmPlan p = gemm_plan(rows, K / 32, false, false, ctx->cu_count, 0, 0, max_split);
     return gemm_algorithmic_bytes(rows, K / 32, batch, true, false) + (p.split - 1) * B * rows * 4.0;
   };
@@ -787,7 +845,7 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
   // Stage trace (test hook, decode steps only): copies of the stage inputs
   // and outputs; the split GEMM outputs are summed in split order into the
   // copy, exactly as their consumer sums them.
-  const bool tracing = rt->tracing && !prefill;
+  const bool tracing = rt->tracing && sh.single && sh.heads_identity;
   const auto *host_slots = reinterpret_cast<const int32_t *>(rt->meta_host + ml.slots);
   const auto *host_pos = reinterpret_cast<const int32_t *>(rt->meta_host + ml.positions);
   const size_t code_tiles = (batch + 15) / 16;
@@ -864,7 +922,7 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
       a.out = nullptr;
       a.proj = pending;
       a.gates = L.gate_rows > 0 ? rt->q8_gates : nullptr;
-      if (prefill && pending.splits > 1) {
+      if (chunked && pending.splits > 1) {
         // the chunk scan reads every token's inputs in order: sum the split
         // partials once over the whole GPU, so each token is one load per channel
         Q35_KERNEL(Q35_KERNEL_PREP, B * L.in_rows * (pending.splits + 1) * 4.0,
@@ -887,6 +945,12 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
       a.scales = rt->scales;
       a.seed = d.sign_seed;
       a.scan = rt->delta_scan;
+      if (chunked) {
+        a.row_seg = row_seg;
+        a.seg_row0 = seg_row0;
+        a.seg_count = seg_count;
+        a.segments = sh.segments;
+      }
       // recurrent state read + written, projection row in (per split), conv
       // ring (K-1 rows read, one written), prepared out-projection activations
       const double delta_bytes =
@@ -897,7 +961,7 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
         Q35_STEP(trace_conv(l, li, Q35_TRACE_CONV_BEFORE), "trace");
         a.out = trace_fp32(l, Q35_TRACE_CORE, v_dim);
       }
-      Q35_KERNEL(Q35_KERNEL_DELTA, delta_bytes, (prefill ? launch_delta_chunk(a, s) : launch_delta(a, s)), "DeltaNet");
+      Q35_KERNEL(Q35_KERNEL_DELTA, delta_bytes, (chunked ? launch_delta_chunk(a, s) : launch_delta(a, s)), "DeltaNet");
       if (tracing) {
         Q35_STEP(trace_state(l, li, Q35_TRACE_STATE_AFTER, 1), "trace");
         Q35_STEP(trace_conv(l, li, Q35_TRACE_CONV_AFTER), "trace");
@@ -919,6 +983,7 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
       p.rope_sin = rt->rope_sin;
       p.positions = positions;
       p.page_table = page_table;
+      p.row_seg = row_seg;
       p.max_pages = rt->max_pages_per_row;
       p.page_tokens = rt->cfg.page_tokens;
       p.k_pool = rt->k_pool + static_cast<size_t>(fi) * rt->layer_pool_elems;
@@ -951,8 +1016,15 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
       a.scale = 1.0F / std::sqrt(static_cast<float>(d.head_dim));
       a.split_tokens = rt->split_tokens;
       a.max_splits = rt->max_splits;
+      a.grid_splits = sh.grid_splits;
       a.part_o = rt->part_o;
       a.part_ml = rt->part_ml;
+      a.row_seg = row_seg;
+      if (chunked) {
+        a.tile_row0 = tile_row0;
+        a.tile_rows = tile_rows;
+        a.tiles = sh.tiles;
+      }
       // every cached K and V row of each request once, q in, split partials out
       const double splits_used = std::ceil(kv_tokens / rt->split_tokens);
       Q35_KERNEL(Q35_KERNEL_ATTENTION,
@@ -997,62 +1069,70 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
     if (tracing) Q35_STEP(trace_rows(l, Q35_TRACE_DOWN, H), "trace");
     add_pending = true;
   }
-  // A prefill chunk needs the head only for its last position: the final
-  // norm and the head run on that one row (row 0 of hidden_out afterwards).
-  const int head_tokens = prefill ? 1 : batch;
-  const int head_row0 = prefill ? batch - 1 : 0;
-  if (prefill) {
+  // Final norm and head on the head rows: every row of a decode step, the
+  // last position of each segment that wants a token otherwise (hidden_out
+  // and the head outputs are then indexed by head row).
+  const int heads = sh.heads;
+  {
     RmsPrepArgs a;
-    a.x_in = rt->x[cur] + static_cast<size_t>(head_row0) * H;
+    a.x_in = rt->x[cur];
     a.add = pending;
-    a.add.p = pending.p + static_cast<size_t>(head_row0) * pending.width;
-    a.x_out = rt->x[cur ^ 1] + static_cast<size_t>(head_row0) * H;
+    a.x_out = rt->x[cur ^ 1];
     a.weight = m->final_norm;
     a.eps = d.rms_eps;
-    a.tokens = 1;
+    a.tokens = heads;
     a.K = H;
     a.h128 = false;
     a.seed = d.sign_seed;
     a.codes = rt->codes;
     a.scales = rt->scales;
     a.normed_out = rt->hidden_out;
-    Q35_KERNEL(Q35_KERNEL_PREP, pending.splits * H * 4.0 + 3.0 * H * 4.0, launch_rms_prep(a, s), "final norm prep");
+    a.rows = sh.heads_identity ? nullptr : head_rows;
+    const double HR = heads;
+    Q35_KERNEL(Q35_KERNEL_PREP, HR * (H * 4.0 + pending.splits * H * 4.0 + H * 4.0 + H + H / 32.0 * 4.0) + H * 4.0 +
+                                    HR * H * 4.0,
+               launch_rms_prep(a, s), "final norm prep");
     cur ^= 1;
-  } else {
-    Q35_KERNEL(Q35_KERNEL_PREP, rms_bytes(true) + B * H * 4.0, rms_prep(m->final_norm, true, false, rt->hidden_out),
-               "final norm prep");
-    if (tracing) {
-      const int fl = d.n_layers;
-      Q35_STEP(trace_copy(rt, fl, Q35_TRACE_X_FINAL, rt->x[cur], static_cast<size_t>(batch) * H * 4, s), "trace");
-      Q35_STEP(trace_copy(rt, fl, Q35_TRACE_HIDDEN, rt->hidden_out, static_cast<size_t>(batch) * H * 4, s), "trace");
-      Q35_STEP(trace_codes(fl, Q35_TRACE_CODES_HEAD, H), "trace");
-    }
   }
-  const double HB = head_tokens;
-  if (want_logits) {
-    GemmArgs g;
-    g.w = m->embed;
-    g.g16 = m->embed_g16;
-    g.rows = d.vocab;
-    g.nb = H / 32;
-    g.codes = rt->codes;
-    g.scales = rt->scales;
-    g.tokens = head_tokens;
-    g.out = rt->logits;
-    g.stride = d.vocab;
-    g.head = true;
-    g.force_split = 1;  // rt->logits holds one [batch][vocab] copy: never split K here
-    g.cu_count = ctx->cu_count;
-    Q35_KERNEL(Q35_KERNEL_HEAD, gemm_algorithmic_bytes(d.vocab, H / 32, head_tokens, true, false) + g16_extra, launch_gemm(g, s),
-               "logits head");
-  } else {
-    const GemmArgs g = greedy_head_args(rt, head_tokens, slots + head_row0, penalties + head_row0);
-    const int ncand = gemm_argmax_cands(d.vocab, H / 32, head_tokens, ctx->cu_count, 0, m->embed_g16);
-    Q35_KERNEL(Q35_KERNEL_HEAD, gemm_algorithmic_bytes(d.vocab, H / 32, head_tokens, false, false) + g16_extra + ncand * HB * 8.0,
-               launch_gemm(g, s), "greedy head");
-    Q35_KERNEL(Q35_KERNEL_ARGMAX, ncand * HB * 8.0 + HB * 4.0,
-               launch_argmax_finalize(rt->cand, ncand, kMaxTokens, head_tokens, rt->tokens_out_dev, nullptr, s),
-               "argmax finalize");
+  if (tracing) {
+    const int fl = d.n_layers;
+    Q35_STEP(trace_copy(rt, fl, Q35_TRACE_X_FINAL, rt->x[cur], static_cast<size_t>(batch) * H * 4, s), "trace");
+    Q35_STEP(trace_copy(rt, fl, Q35_TRACE_HIDDEN, rt->hidden_out, static_cast<size_t>(batch) * H * 4, s), "trace");
+    Q35_STEP(trace_codes(fl, Q35_TRACE_CODES_HEAD, H), "trace");
+  }
+  // the head in launches of at most kMaxTokens rows
+  for (int h0 = 0; h0 < heads; h0 += kMaxTokens) {
+    const int n = std::min(kMaxTokens, heads - h0);
+    const double HB = n;
+    const size_t tile0 = static_cast<size_t>(h0 / 16);
+    if (want_logits) {
+      GemmArgs g;
+      g.w = m->embed;
+      g.g16 = m->embed_g16;
+      g.rows = d.vocab;
+      g.nb = H / 32;
+      g.codes = rt->codes + tile0 * (H / 32) * 64;
+      g.scales = rt->scales + tile0 * (H / 32) * 16;
+      g.tokens = n;
+      g.out = rt->logits + static_cast<size_t>(h0) * d.vocab;
+      g.stride = d.vocab;
+      g.head = true;
+      g.force_split = 1;  // rt->logits holds one [rows][vocab] copy: never split K here
+      g.cu_count = ctx->cu_count;
+      Q35_KERNEL(Q35_KERNEL_HEAD, gemm_algorithmic_bytes(d.vocab, H / 32, n, true, false) + g16_extra,
+                 launch_gemm(g, s), "logits head");
+    } else {
+      GemmArgs g = greedy_head_args(rt, n, head_slots + h0, head_penalties + h0);
+      g.codes = rt->codes + tile0 * (H / 32) * 64;
+      g.scales = rt->scales + tile0 * (H / 32) * 16;
+      const int ncand = gemm_argmax_cands(d.vocab, H / 32, n, ctx->cu_count, 0, m->embed_g16);
+      Q35_KERNEL(Q35_KERNEL_HEAD,
+                 gemm_algorithmic_bytes(d.vocab, H / 32, n, false, false) + g16_extra + ncand * HB * 8.0,
+                 launch_gemm(g, s), "greedy head");
+      Q35_KERNEL(Q35_KERNEL_ARGMAX, ncand * HB * 8.0 + HB * 4.0,
+                 launch_argmax_finalize(rt->cand, ncand, kMaxTokens, n, rt->tokens_out_dev + h0, nullptr, s),
+                 "argmax finalize");
+    }
   }
 #undef Q35_KERNEL
 #undef Q35_STEP
@@ -1063,73 +1143,152 @@ int runtime_enqueue_step(q35_runtime *rt, int batch, bool want_logits, bool pref
 
 namespace {
 
-// Validates a step descriptor on the host (no kernel ever sees an
-// out-of-range index) and packs it into the pinned metadata block.
-int pack_step(q35_runtime *rt, const q35_step_desc *desc) {
+// Validates the segments of a packed step on the host (no kernel ever sees
+// an out-of-range index) and packs them into the pinned metadata block:
+// rows segment by segment, a page-table row per segment, the head rows (the
+// last position of each segment that wants a token) and the attention query
+// tiles (runs of up to kAttnTileRows positions of one segment).
+int pack_segments(q35_runtime *rt, const q35_segment *segs, int n, StepShape *shape) {
   Context *ctx = rt->ctx;
   const q35_model_dims &d = rt->model->d;
-  const int B = desc->batch;
-  if (B <= 0 || B > rt->cfg.max_batch || desc->slots == nullptr || desc->positions == nullptr ||
-      desc->tokens == nullptr || desc->page_table == nullptr || desc->max_pages <= 0)
-    return set_error(ctx, Q35_ERR_INVALID, "invalid step descriptor");
-  // validate on the host so no kernel ever sees an out-of-range index
+  if (segs == nullptr || n <= 0 || n > rt->max_segments)
+    return set_error(ctx, Q35_ERR_INVALID, "segment count outside 1 .. max_batch + " +
+                                               std::to_string(kMaxPrefillSegments));
   std::vector<uint8_t> seen(rt->cfg.max_slots, 0);
-  for (int b = 0; b < B; ++b) {
-    const int slot = desc->slots[b], pos = desc->positions[b], tok = desc->tokens[b];
-    if (slot < 0 || slot >= rt->cfg.max_slots || !rt->slot_used[slot] || seen[slot])
+  long long rows = 0;
+  for (int i = 0; i < n; ++i) {
+    const q35_segment &g = segs[i];
+    if (g.slot < 0 || g.slot >= rt->cfg.max_slots || !rt->slot_used[g.slot] || seen[g.slot])
       return set_error(ctx, Q35_ERR_INVALID, "step rows need distinct allocated slots");
-    seen[slot] = 1;
-    if (pos < 0 || pos >= rt->cfg.max_context) return set_error(ctx, Q35_ERR_INVALID, "position outside max_context");
-    if (tok < 0 || tok >= d.vocab) return set_error(ctx, Q35_ERR_INVALID, "token out of range");
-    if (pos / rt->cfg.page_tokens >= desc->max_pages)
-      return set_error(ctx, Q35_ERR_INVALID, "page table does not cover the position");
-    for (int p = 0; p <= pos / rt->cfg.page_tokens; ++p) {
-      const int page = desc->page_table[static_cast<size_t>(b) * desc->max_pages + p];
-      if (page < 0 || page >= rt->cfg.total_pages || rt->page_ref[page] <= 0)
+    seen[g.slot] = 1;
+    if (g.count <= 0 || g.tokens == nullptr || g.page_table == nullptr || g.max_pages <= 0)
+      return set_error(ctx, Q35_ERR_INVALID, "invalid step segment");
+    if (g.pos0 < 0 || static_cast<long long>(g.pos0) + g.count > rt->cfg.max_context)
+      return set_error(ctx, Q35_ERR_INVALID, "position outside max_context");
+    if (!(g.penalty >= 1.0F)) return set_error(ctx, Q35_ERR_INVALID, "penalty must be >= 1");
+    for (int r = 0; r < g.count; ++r)
+      if (g.tokens[r] < 0 || g.tokens[r] >= d.vocab) return set_error(ctx, Q35_ERR_INVALID, "token out of range");
+    const int last = (g.pos0 + g.count - 1) / rt->cfg.page_tokens;
+    if (last >= g.max_pages) return set_error(ctx, Q35_ERR_INVALID, "page table does not cover the position");
+    for (int pg = 0; pg <= last; ++pg)
+      if (g.page_table[pg] < 0 || g.page_table[pg] >= rt->cfg.total_pages || rt->page_ref[g.page_table[pg]] <= 0)
         return set_error(ctx, Q35_ERR_INVALID, "page table names a free or invalid page");
-    }
+    rows += g.count;
   }
-  const MetaLayout ml = meta_layout(rt->cfg.max_batch, rt->max_pages_per_row);
+  if (rows > rt->max_rows)
+    return set_error(ctx, Q35_ERR_INVALID, "step rows exceed max_step_rows (" + std::to_string(rt->max_rows) + ")");
+  const MetaLayout ml = meta_layout(rt);
   unsigned char *h = rt->meta_host;
   std::memset(h, 0, rt->meta_bytes);
   auto *slots = reinterpret_cast<int32_t *>(h + ml.slots);
   auto *positions = reinterpret_cast<int32_t *>(h + ml.positions);
   auto *tokens = reinterpret_cast<int32_t *>(h + ml.tokens);
   auto *seq_lens = reinterpret_cast<int32_t *>(h + ml.seq_lens);
-  auto *penalties = reinterpret_cast<float *>(h + ml.penalties);
   auto *count_input = reinterpret_cast<uint8_t *>(h + ml.count_input);
+  auto *row_seg = reinterpret_cast<int32_t *>(h + ml.row_seg);
+  auto *seg_row0 = reinterpret_cast<int32_t *>(h + ml.seg_row0);
+  auto *seg_count = reinterpret_cast<int32_t *>(h + ml.seg_count);
   auto *pt = reinterpret_cast<int32_t *>(h + ml.page_table);
-  for (int b = 0; b < B; ++b) {
-    slots[b] = desc->slots[b];
-    positions[b] = desc->positions[b];
-    tokens[b] = desc->tokens[b];
-    seq_lens[b] = desc->positions[b] + 1;
-    penalties[b] = desc->penalties ? desc->penalties[b] : 1.0F;
-    count_input[b] = desc->count_input ? desc->count_input[b] : 0;
-    const int used = std::min(desc->max_pages, rt->max_pages_per_row);
-    for (int p = 0; p < used; ++p)
-      pt[static_cast<size_t>(b) * rt->max_pages_per_row + p] = desc->page_table[static_cast<size_t>(b) * desc->max_pages + p];
+  auto *head_rows = reinterpret_cast<int32_t *>(h + ml.head_rows);
+  auto *head_slots = reinterpret_cast<int32_t *>(h + ml.head_slots);
+  auto *head_pen = reinterpret_cast<float *>(h + ml.head_penalties);
+  auto *tile_row0 = reinterpret_cast<int32_t *>(h + ml.tile_row0);
+  auto *tile_rows = reinterpret_cast<int32_t *>(h + ml.tile_rows);
+  StepShape sh;
+  int r = 0, heads = 0, tiles = 0, longest = 1;
+  for (int i = 0; i < n; ++i) {
+    const q35_segment &g = segs[i];
+    seg_row0[i] = r;
+    seg_count[i] = g.count;
+    const int used = std::min(g.max_pages, rt->max_pages_per_row);
+    std::memcpy(pt + static_cast<size_t>(i) * rt->max_pages_per_row, g.page_table, static_cast<size_t>(used) * 4);
+    for (int t0 = 0; t0 < g.count; t0 += kAttnTileRows) {
+      tile_row0[tiles] = r + t0;
+      tile_rows[tiles] = std::min(kAttnTileRows, g.count - t0);
+      ++tiles;
+    }
+    for (int k = 0; k < g.count; ++k, ++r) {
+      slots[r] = g.slot;
+      positions[r] = g.pos0 + k;
+      tokens[r] = g.tokens[k];
+      seq_lens[r] = g.pos0 + k + 1;  // causal: the prefix and the segment up to this position
+      count_input[r] = g.count_input;
+      row_seg[r] = i;
+    }
+    longest = std::max(longest, g.pos0 + g.count);
+    if (g.want_token) {
+      head_rows[heads] = r - 1;
+      head_slots[heads] = g.slot;
+      head_pen[heads] = g.penalty;
+      sh.heads_identity = sh.heads_identity && heads == r - 1;
+      ++heads;
+    }
+    sh.single = sh.single && g.count == 1;
   }
+  if (heads == 0) return set_error(ctx, Q35_ERR_INVALID, "a step needs at least one segment that wants a token");
+  sh.rows = r;
+  sh.segments = n;
+  sh.heads = heads;
+  sh.tiles = tiles;
+  sh.heads_identity = sh.heads_identity && heads == r;
+  // attention chunks of the longest context, rounded up to a power of two so
+  // that few graph shapes cover a growing context
+  const int need = (longest + rt->split_tokens - 1) / rt->split_tokens;
+  int gs = 1;
+  while (gs < need) gs <<= 1;
+  sh.grid_splits = std::min(gs, rt->max_splits);
+  *shape = sh;
+  rt->shape = sh;
   return Q35_OK;
+}
+
+// A decode step descriptor as segments of one row that all want a token.
+int pack_step(q35_runtime *rt, const q35_step_desc *desc, StepShape *shape) {
+  const int B = desc->batch;
+  if (B <= 0 || B > rt->cfg.max_batch || desc->slots == nullptr || desc->positions == nullptr ||
+      desc->tokens == nullptr || desc->page_table == nullptr || desc->max_pages <= 0)
+    return set_error(rt->ctx, Q35_ERR_INVALID, "invalid step descriptor");
+  std::vector<q35_segment> segs(B);
+  for (int b = 0; b < B; ++b) {
+    q35_segment &g = segs[b];
+    g.slot = desc->slots[b];
+    g.pos0 = desc->positions[b];
+    g.count = 1;
+    g.tokens = desc->tokens + b;
+    g.page_table = desc->page_table + static_cast<size_t>(b) * desc->max_pages;
+    g.max_pages = desc->max_pages;
+    g.penalty = desc->penalties ? desc->penalties[b] : 1.0F;
+    g.count_input = desc->count_input ? desc->count_input[b] : 0;
+    g.want_token = 1;
+  }
+  return pack_segments(rt, segs.data(), B, shape);
 }
 
 int ensure_logits(q35_runtime *rt) {
   if (rt->logits != nullptr) return Q35_OK;
-  return rt_alloc(rt, static_cast<size_t>(rt->cfg.max_batch) * rt->model->d.vocab * 4,
+  return rt_alloc(rt, static_cast<size_t>(rt->max_segments) * rt->model->d.vocab * 4,
                   reinterpret_cast<void **>(&rt->logits));
 }
 
-// Runs the packed step: replays (or captures) its graph, or launches eagerly.
-int launch_step(q35_runtime *rt, int B, bool want_logits) {
+// Runs the packed step: replays (or captures) the graph of its shape, or
+// launches eagerly (profiling and the stage trace time or copy single launches).
+int launch_step(q35_runtime *rt, const StepShape &sh, bool want_logits) {
   Context *ctx = rt->ctx;
   int st = Q35_OK;
   if (rt->cfg.use_graphs && !rt->profiling && !rt->tracing) {
-    const auto key = std::make_pair(B, want_logits ? 1 : 0);
+    const auto key = sh.key(want_logits);
     auto it = rt->graphs.find(key);
     if (it == rt->graphs.end()) {
+      // a bounded cache: the decode shapes of a serving loop and a few chunk
+      // shapes recur; anything else is re-captured when it comes back
+      if (rt->graphs.size() >= 64) {
+        Q35_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+        for (auto &kv : rt->graphs) (void)hipGraphExecDestroy(kv.second);
+        rt->graphs.clear();
+      }
       Q35_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
       Q35_HIP_TRY(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
-      st = runtime_enqueue_step(rt, B, want_logits, false);
+      st = runtime_enqueue_step(rt, sh, want_logits);
       hipGraph_t graph = nullptr;
       const hipError_t ce = hipStreamEndCapture(ctx->stream, &graph);
       if (st != Q35_OK) {
@@ -1145,7 +1304,7 @@ int launch_step(q35_runtime *rt, int B, bool want_logits) {
     }
     Q35_HIP_TRY(ctx, hipGraphLaunch(it->second, ctx->stream));
   } else {
-    st = runtime_enqueue_step(rt, B, want_logits, false);
+    st = runtime_enqueue_step(rt, sh, want_logits);
     if (st != Q35_OK) return st;
   }
   return Q35_OK;
@@ -1159,11 +1318,12 @@ extern "C" int q35_runtime_step(q35_runtime *rt, const q35_step_desc *desc, int3
   Context *ctx = rt->ctx;
   const q35_model_dims &d = rt->model->d;
   const int B = desc->batch;
-  int st = pack_step(rt, desc);
+  StepShape sh;
+  int st = pack_step(rt, desc, &sh);
   if (st != Q35_OK) return st;
   const bool want_logits = out_logits != nullptr;
   if (want_logits && (st = ensure_logits(rt)) != Q35_OK) return st;
-  if ((st = launch_step(rt, B, want_logits)) != Q35_OK) return st;
+  if ((st = launch_step(rt, sh, want_logits)) != Q35_OK) return st;
   if (want_logits)
     Q35_HIP_TRY(ctx, hipMemcpyAsync(out_logits, rt->logits, static_cast<size_t>(B) * d.vocab * 4,
                                     hipMemcpyDeviceToHost, ctx->stream));
@@ -1202,10 +1362,11 @@ extern "C" int q35_runtime_step(q35_runtime *rt, const q35_step_desc *desc, int3
 
 namespace {
 
-// Per-row candidate settings into the metadata block (rows 0..B-1).
+// Per-head-row candidate settings into the metadata block (head rows
+// 0..B-1; `sampling` indexed by head row).
 int pack_sampling(q35_runtime *rt, int B, const q35_row_sampling *sampling) {
   if (sampling == nullptr) return set_error(rt->ctx, Q35_ERR_INVALID, "missing sampling rows");
-  const MetaLayout ml = meta_layout(rt->cfg.max_batch, rt->max_pages_per_row);
+  const MetaLayout ml = meta_layout(rt);
   auto *inv_t = reinterpret_cast<float *>(rt->meta_host + ml.inv_temperature);
   auto *top_k = reinterpret_cast<int32_t *>(rt->meta_host + ml.top_k);
   for (int b = 0; b < B; ++b) {
@@ -1223,15 +1384,15 @@ int pack_sampling(q35_runtime *rt, int B, const q35_row_sampling *sampling) {
 int finish_candidates(q35_runtime *rt, int rows, q35_candidate *out, float *raw_logits) {
   Context *ctx = rt->ctx;
   const q35_model_dims &d = rt->model->d;
-  const MetaLayout ml = meta_layout(rt->cfg.max_batch, rt->max_pages_per_row);
+  const MetaLayout ml = meta_layout(rt);
   SampleArgs a;
   a.logits = rt->logits;
   a.logits_stride = d.vocab;
   a.rows = rows;
   a.vocab = d.vocab;
   a.counts = rt->counts;
-  a.count_rows = reinterpret_cast<const int32_t *>(rt->meta_dev + ml.slots);
-  a.penalties = reinterpret_cast<const float *>(rt->meta_dev + ml.penalties);
+  a.count_rows = reinterpret_cast<const int32_t *>(rt->meta_dev + ml.head_slots);
+  a.penalties = reinterpret_cast<const float *>(rt->meta_dev + ml.head_penalties);
   a.inv_temperature = reinterpret_cast<const float *>(rt->meta_dev + ml.inv_temperature);
   a.top_k = reinterpret_cast<const int32_t *>(rt->meta_dev + ml.top_k);
   a.out = rt->candidates;
@@ -1252,10 +1413,11 @@ extern "C" int q35_runtime_step_candidates(q35_runtime *rt, const q35_step_desc 
                                            const q35_row_sampling *sampling, q35_candidate *out_candidates,
                                            float *raw_logits) {
   if (rt == nullptr || desc == nullptr || out_candidates == nullptr) return Q35_ERR_INVALID;
-  int st = pack_step(rt, desc);
+  StepShape sh;
+  int st = pack_step(rt, desc, &sh);
   if (st == Q35_OK) st = pack_sampling(rt, desc->batch, sampling);
   if (st == Q35_OK) st = ensure_logits(rt);
-  if (st == Q35_OK) st = launch_step(rt, desc->batch, true);
+  if (st == Q35_OK) st = launch_step(rt, sh, true);
   if (st != Q35_OK) return st;
   if (rt->profiling) {
     Q35_HIP_TRY(rt->ctx, hipStreamSynchronize(rt->ctx->stream));
@@ -1273,13 +1435,13 @@ extern "C" int q35_runtime_head_candidates(q35_runtime *rt, int32_t slot, const 
   if (!(penalty >= 1.0F)) return set_error(rt->ctx, Q35_ERR_INVALID, "penalty must be >= 1");
   Context *ctx = rt->ctx;
   const q35_model_dims &d = rt->model->d;
-  const MetaLayout ml = meta_layout(rt->cfg.max_batch, rt->max_pages_per_row);
+  const MetaLayout ml = meta_layout(rt);
   std::memset(rt->meta_host, 0, rt->meta_bytes);
   int st = pack_sampling(rt, 1, sampling);
   if (st == Q35_OK) st = ensure_logits(rt);
   if (st != Q35_OK) return st;
-  reinterpret_cast<int32_t *>(rt->meta_host + ml.slots)[0] = slot;
-  reinterpret_cast<float *>(rt->meta_host + ml.penalties)[0] = penalty;
+  reinterpret_cast<int32_t *>(rt->meta_host + ml.head_slots)[0] = slot;
+  reinterpret_cast<float *>(rt->meta_host + ml.head_penalties)[0] = penalty;
   hipStream_t s = ctx->stream;
   Q35_HIP_TRY(ctx, hipMemcpyAsync(rt->meta_dev, rt->meta_host, rt->meta_bytes, hipMemcpyHostToDevice, s));
   Q35_HIP_TRY(ctx, hipMemcpyAsync(rt->hidden_out, hidden, static_cast<size_t>(d.hidden) * 4, hipMemcpyHostToDevice, s));
@@ -1365,44 +1527,23 @@ extern "C" int q35_runtime_prefill(q35_runtime *rt, int32_t slot, int32_t pos0, 
                                    int32_t *out_token) {
   if (rt == nullptr) return Q35_ERR_INVALID;
   Context *ctx = rt->ctx;
-  const q35_model_dims &d = rt->model->d;
-  if (tokens == nullptr || page_table == nullptr || count <= 0 || count > rt->cfg.max_batch || max_pages <= 0)
+  if (tokens == nullptr || page_table == nullptr || count <= 0 || count > rt->max_rows || max_pages <= 0)
     return set_error(ctx, Q35_ERR_INVALID, "invalid prefill chunk");
-  // validate on the host so no kernel ever sees an out-of-range index
-  if (slot < 0 || slot >= rt->cfg.max_slots || !rt->slot_used[slot])
-    return set_error(ctx, Q35_ERR_INVALID, "prefill needs an allocated slot");
-  if (pos0 < 0 || static_cast<long long>(pos0) + count > rt->cfg.max_context)
-    return set_error(ctx, Q35_ERR_INVALID, "prefill chunk outside max_context");
-  const int pos_last = pos0 + count - 1;
-  if (pos_last / rt->cfg.page_tokens >= max_pages)
-    return set_error(ctx, Q35_ERR_INVALID, "page table does not cover the chunk");
-  for (int p = 0; p <= pos_last / rt->cfg.page_tokens; ++p)
-    if (page_table[p] < 0 || page_table[p] >= rt->cfg.total_pages || rt->page_ref[page_table[p]] <= 0)
-      return set_error(ctx, Q35_ERR_INVALID, "page table names a free or invalid page");
-  for (int r = 0; r < count; ++r)
-    if (tokens[r] < 0 || tokens[r] >= d.vocab) return set_error(ctx, Q35_ERR_INVALID, "token out of range");
-  // one row per position of the chunk, all on the request's slot and pages
-  const MetaLayout ml = meta_layout(rt->cfg.max_batch, rt->max_pages_per_row);
-  unsigned char *h = rt->meta_host;
-  std::memset(h, 0, rt->meta_bytes);
-  auto *slots = reinterpret_cast<int32_t *>(h + ml.slots);
-  auto *positions = reinterpret_cast<int32_t *>(h + ml.positions);
-  auto *toks = reinterpret_cast<int32_t *>(h + ml.tokens);
-  auto *seq_lens = reinterpret_cast<int32_t *>(h + ml.seq_lens);
-  auto *penalties = reinterpret_cast<float *>(h + ml.penalties);
-  auto *pt = reinterpret_cast<int32_t *>(h + ml.page_table);
-  const int used = std::min(max_pages, rt->max_pages_per_row);
-  for (int r = 0; r < count; ++r) {
-    slots[r] = slot;
-    positions[r] = pos0 + r;
-    toks[r] = tokens[r];
-    seq_lens[r] = pos0 + r + 1;  // causal: the prefix and the chunk up to this position
-    penalties[r] = penalty;
-    for (int p = 0; p < used; ++p) pt[static_cast<size_t>(r) * rt->max_pages_per_row + p] = page_table[p];
-  }
-  // chunk sizes vary (the last chunk of a prompt is ragged): eager launches
-  int st = runtime_enqueue_step(rt, count, false, true);
+  // one segment: every position of the chunk on the request's slot and pages
+  q35_segment g{};
+  g.slot = slot;
+  g.pos0 = pos0;
+  g.count = count;
+  g.tokens = tokens;
+  g.page_table = page_table;
+  g.max_pages = max_pages;
+  g.penalty = penalty;
+  g.count_input = 0;
+  g.want_token = 1;
+  StepShape sh;
+  int st = pack_segments(rt, &g, 1, &sh);
   if (st != Q35_OK) return st;
+  if ((st = launch_step(rt, sh, false)) != Q35_OK) return st;
   Q35_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
   if (rt->profiling) {
     st = profile_collect(rt);
@@ -1410,6 +1551,57 @@ extern "C" int q35_runtime_prefill(q35_runtime *rt, int32_t slot, int32_t pos0, 
   }
   rt->last_batch = 1;  // the head ran on the chunk's last position only
   if (out_token != nullptr) *out_token = rt->tokens_out_host[0];
+  return Q35_OK;
+}
+
+extern "C" int q35_runtime_step_segments(q35_runtime *rt, const q35_segment *segments, int32_t count,
+                                         const q35_row_sampling *sampling, int32_t *out_tokens,
+                                         q35_candidate *out_candidates, float *raw_logits) {
+  if (rt == nullptr || out_tokens == nullptr) return Q35_ERR_INVALID;
+  Context *ctx = rt->ctx;
+  if (sampling != nullptr && out_candidates == nullptr)
+    return set_error(ctx, Q35_ERR_INVALID, "sampling needs out_candidates");
+  StepShape sh;
+  int st = pack_segments(rt, segments, count, &sh);
+  if (st != Q35_OK) return st;
+  // head row h -> segment
+  std::vector<int> head_seg;
+  for (int i = 0; i < count; ++i)
+    if (segments[i].want_token) head_seg.push_back(i);
+  const bool want_logits = sampling != nullptr;
+  if (want_logits) {
+    std::vector<q35_row_sampling> rows(sh.heads);
+    for (int h = 0; h < sh.heads; ++h) rows[h] = sampling[head_seg[h]];
+    if ((st = pack_sampling(rt, sh.heads, rows.data())) != Q35_OK) return st;
+    if ((st = ensure_logits(rt)) != Q35_OK) return st;
+  }
+  if ((st = launch_step(rt, sh, want_logits)) != Q35_OK) return st;
+  if (rt->profiling) {
+    Q35_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    if ((st = profile_collect(rt)) != Q35_OK) return st;
+  }
+  for (int i = 0; i < count; ++i) out_tokens[i] = -1;
+  if (!want_logits) {
+    Q35_HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    rt->last_batch = sh.heads;
+    for (int h = 0; h < sh.heads; ++h) out_tokens[head_seg[h]] = rt->tokens_out_host[h];
+    return Q35_OK;
+  }
+  const int vocab = rt->model->d.vocab;
+  std::vector<q35_candidate> cands(static_cast<size_t>(sh.heads) * kMaxCandidates);
+  std::vector<float> raw(raw_logits != nullptr ? static_cast<size_t>(sh.heads) * vocab : 0);
+  if ((st = finish_candidates(rt, sh.heads, cands.data(), raw_logits != nullptr ? raw.data() : nullptr)) != Q35_OK)
+    return st;
+  for (int i = 0; i < count; ++i)
+    for (int k = 0; k < kMaxCandidates; ++k)
+      out_candidates[static_cast<size_t>(i) * kMaxCandidates + k] = q35_candidate{-INFINITY, -1};
+  for (int h = 0; h < sh.heads; ++h) {
+    std::memcpy(out_candidates + static_cast<size_t>(head_seg[h]) * kMaxCandidates,
+                cands.data() + static_cast<size_t>(h) * kMaxCandidates, kMaxCandidates * sizeof(q35_candidate));
+    if (raw_logits != nullptr)
+      std::memcpy(raw_logits + static_cast<size_t>(head_seg[h]) * vocab, raw.data() + static_cast<size_t>(h) * vocab,
+                  static_cast<size_t>(vocab) * 4);
+  }
   return Q35_OK;
 }
 
@@ -1510,10 +1702,10 @@ extern "C" int q35_runtime_head(q35_runtime *rt, int32_t slot, const float *hidd
   if (!(penalty >= 1.0F)) return set_error(rt->ctx, Q35_ERR_INVALID, "penalty must be >= 1");
   Context *ctx = rt->ctx;
   const q35_model_dims &d = rt->model->d;
-  const MetaLayout ml = meta_layout(rt->cfg.max_batch, rt->max_pages_per_row);
+  const MetaLayout ml = meta_layout(rt);
   std::memset(rt->meta_host, 0, rt->meta_bytes);
-  reinterpret_cast<int32_t *>(rt->meta_host + ml.slots)[0] = slot;
-  reinterpret_cast<float *>(rt->meta_host + ml.penalties)[0] = penalty;
+  reinterpret_cast<int32_t *>(rt->meta_host + ml.head_slots)[0] = slot;
+  reinterpret_cast<float *>(rt->meta_host + ml.head_penalties)[0] = penalty;
   hipStream_t s = ctx->stream;
   Q35_HIP_TRY(ctx, hipMemcpyAsync(rt->meta_dev, rt->meta_host, rt->meta_bytes, hipMemcpyHostToDevice, s));
   Q35_HIP_TRY(ctx, hipMemcpyAsync(rt->hidden_out, hidden, static_cast<size_t>(d.hidden) * 4, hipMemcpyHostToDevice, s));
@@ -1528,8 +1720,8 @@ extern "C" int q35_runtime_head(q35_runtime *rt, int32_t slot, const float *hidd
   p.codes = rt->codes;
   p.scales = rt->scales;
   Q35_HIP_TRY(ctx, launch_prep(p, s));
-  const GemmArgs g = greedy_head_args(rt, 1, reinterpret_cast<const int32_t *>(rt->meta_dev + ml.slots),
-                                      reinterpret_cast<const float *>(rt->meta_dev + ml.penalties));
+  const GemmArgs g = greedy_head_args(rt, 1, reinterpret_cast<const int32_t *>(rt->meta_dev + ml.head_slots),
+                                      reinterpret_cast<const float *>(rt->meta_dev + ml.head_penalties));
   Q35_HIP_TRY(ctx, launch_gemm(g, s));
   const int ncand = gemm_argmax_cands(d.vocab, d.hidden / 32, 1, ctx->cu_count, 0, rt->model->embed_g16);
   Q35_HIP_TRY(ctx, launch_argmax_finalize(rt->cand, ncand, kMaxTokens, 1, rt->tokens_out_dev, nullptr, s));
