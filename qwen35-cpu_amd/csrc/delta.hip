@@ -5,10 +5,12 @@
 // round trip; its loads are issued right after the head's few small inputs
 // (conv ring, projections, weights), so the 64 KiB are in flight while those
 // are combined.
-// Thread t owns rows t/4 and 64 + t/4 and, within each, the eight float4 at
-// columns 16m + 4(t%4) (m = 0..7): four lanes share a row, so every row dot
-// product finishes with two DPP quad exchanges instead of a shuffle chain,
-// and one load instruction covers 16 rows x 64 contiguous bytes.
+// Sixteen lanes share a value row: lane o = t % 16 owns the two float4 at
+// columns 4o + 64m (m = 0, 1), and thread t owns rows t/16 + 16j (j = 0..7).
+// A row's dot products are summed per lane in column order and then across
+// its 16 lanes with four DPP exchanges (xor 1, 2, 4, 8) -- delta_row below,
+// shared with the prefill chunk scan so both give the same bits -- and one
+// load instruction covers 4 rows x 256 contiguous bytes per wavefront.
 //
 // Per value row (src/cpu/delta_net.cpp:63-98), in the reference's order:
 //   S *= alpha;  sk = S.k;  delta = (v - sk) * beta;  S += delta * k;  o = S.q
@@ -34,6 +36,42 @@ namespace {
 constexpr int kDeltaThreads = 256;
 constexpr int kDim = 128;
 constexpr int kConvKernel = 4;  // linear_conv_kernel_dim of every Qwen3.5 size
+constexpr int kRowLanes = 16;                                    // lanes per value row
+constexpr int kRowsPerThread = kDim * kRowLanes / kDeltaThreads;  // 8
+
+// The delta rule on one value row held by 16 lanes (this lane: columns
+// 4o + 64m, m = 0, 1), in the reference's order (delta_net.cpp:63-98):
+//   S *= alpha;  sk = S.k;  delta = (v - sk) * beta;  S += delta * k;  o = S.q
+// Each dot product is summed over the lane's 8 columns in order, then over
+// the row's lanes (xor 1, 2, 4, 8). Every lane of the row returns o.
+__device__ __forceinline__ float delta_row(q35_f32x4 st[2], const q35_f32x4 kc[2], const q35_f32x4 qc[2], float v,
+                                           float alpha, float beta) {
+  float d = 0.0F;
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    st[m] *= alpha;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) d += st[m][e] * kc[m][e];
+  }
+  d += q35_row_xor(d, 1);
+  d += q35_row_xor(d, 2);
+  d += q35_row_xor(d, 4);
+  d += q35_row_xor(d, 8);
+  const float delta = (v - d) * beta;
+  float o = 0.0F;
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      st[m][e] += delta * kc[m][e];
+      o += st[m][e] * qc[m][e];
+    }
+  o += q35_row_xor(o, 1);
+  o += q35_row_xor(o, 2);
+  o += q35_row_xor(o, 4);
+  o += q35_row_xor(o, 8);
+  return o;
+}
 
 // FUSED: the linear-attention step around the update; MS: compile-time bound
 // on the in-projection's K splits (so every input load is straight-line).
@@ -46,7 +84,7 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int per = a.v_heads / a.k_heads;
   const int kh = vh / per;
-  const int quad = tid & 3, rowp = tid >> 2;
+  const int col = tid & (kRowLanes - 1), rowg = tid >> 4;  // rows rowg + 16j
 
   // state tile pointers (the loads are issued after this head's small inputs,
   // so those arrive first: on gfx9 loads retire in issue order)
@@ -63,18 +101,14 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
     state_r = a.state_base != nullptr ? a.state_base + static_cast<long long>(a.slots[r]) * a.state_slot_stride
                                       : a.states[r];
   }
-  q35_f32x4 *S = reinterpret_cast<q35_f32x4 *>(state_r + static_cast<size_t>(vh) * kDim * kDim);
-  q35_f32x4 *S0 = S + rowp * (kDim / 4) + quad;         // row rowp
-  q35_f32x4 *S1 = S + (rowp + 64) * (kDim / 4) + quad;  // row rowp + 64
-  q35_f32x4 *W0 = reinterpret_cast<q35_f32x4 *>(reinterpret_cast<float *>(S0) + write_offset);
-  q35_f32x4 *W1 = reinterpret_cast<q35_f32x4 *>(reinterpret_cast<float *>(S1) + write_offset);
-  q35_f32x4 st0[8], st1[8];
+  q35_f32x4 *S = reinterpret_cast<q35_f32x4 *>(state_r + static_cast<size_t>(vh) * kDim * kDim) + rowg * (kDim / 4) + col;
+  q35_f32x4 *W = reinterpret_cast<q35_f32x4 *>(reinterpret_cast<float *>(S) + write_offset);
+  q35_f32x4 st[kRowsPerThread][2];
   auto load_state = [&]() {
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      st0[m] = Q35_LOAD_NT(S0 + 4 * m);
-      st1[m] = Q35_LOAD_NT(S1 + 4 * m);
-    }
+    for (int j = 0; j < kRowsPerThread; ++j)
+#pragma unroll
+      for (int m = 0; m < 2; ++m) st[j][m] = Q35_LOAD_NT(S + j * 16 * (kDim / 4) + 16 * m);
   };
 
   // ---- 2. q, k, v, gates of this head: every load first (the conv ring is
@@ -174,46 +208,19 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
   }
   lds_barrier();
 
-  // ---- 3. delta rule on the two rows of this thread
+  // ---- 3. delta rule on the eight rows of this thread
   const float alpha = s_alpha, beta = s_beta;
-  q35_f32x4 kc[8];
+  q35_f32x4 kc[2], qc[2];
 #pragma unroll
-  for (int m = 0; m < 8; ++m) kc[m] = *reinterpret_cast<const q35_f32x4 *>(sk + 16 * m + 4 * quad);
-  float d0 = 0.0F, d1 = 0.0F;
-#pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    st0[m] *= alpha;
-    st1[m] *= alpha;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      d0 += st0[m][e] * kc[m][e];
-      d1 += st1[m][e] * kc[m][e];
-    }
+  for (int m = 0; m < 2; ++m) {
+    kc[m] = *reinterpret_cast<const q35_f32x4 *>(sk + 4 * col + 64 * m);
+    qc[m] = *reinterpret_cast<const q35_f32x4 *>(sq + 4 * col + 64 * m);
   }
-  d0 += q35_quad_xor1(d0);
-  d1 += q35_quad_xor1(d1);
-  d0 += q35_quad_xor2(d0);
-  d1 += q35_quad_xor2(d1);
-  const float delta0 = (sv[rowp] - d0) * beta, delta1 = (sv[rowp + 64] - d1) * beta;
-  float o0 = 0.0F, o1 = 0.0F;
 #pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    const q35_f32x4 qc = *reinterpret_cast<const q35_f32x4 *>(sq + 16 * m + 4 * quad);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      st0[m][e] += delta0 * kc[m][e];
-      st1[m][e] += delta1 * kc[m][e];
-      o0 += st0[m][e] * qc[e];
-      o1 += st1[m][e] * qc[e];
-    }
-  }
-  o0 += q35_quad_xor1(o0);
-  o1 += q35_quad_xor1(o1);
-  o0 += q35_quad_xor2(o0);
-  o1 += q35_quad_xor2(o1);
-  if (quad == 0) {
-    so[rowp] = o0;
-    so[rowp + 64] = o1;
+  for (int j = 0; j < kRowsPerThread; ++j) {
+    const int row = rowg + 16 * j;
+    const float o = delta_row(st[j], kc, qc, sv[row], alpha, beta);
+    if (col == 0) so[row] = o;
   }
   // the outputs are shared through LDS before the state goes back; waves
   // 1-3 store their rows at once, wave 0 after the epilogue (a later load
@@ -221,10 +228,9 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
   lds_barrier();
   auto store_state = [&]() {
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      Q35_STORE_NT(st0[m], W0 + 4 * m);
-      Q35_STORE_NT(st1[m], W1 + 4 * m);
-    }
+    for (int j = 0; j < kRowsPerThread; ++j)
+#pragma unroll
+      for (int m = 0; m < 2; ++m) Q35_STORE_NT(st[j][m], W + j * 16 * (kDim / 4) + 16 * m);
   };
   if (wave != 0) {
     store_state();
@@ -357,13 +363,14 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_chunk_inputs_kernel(Delta
   e[(is_k ? kDim : 0) + i] = yq * mul;
 }
 
-// One wavefront per 16 value rows (grid: row blocks x value heads); lane
-// quad q = lane % 4 of row 16 * blockIdx.x + lane / 4 owns the float4 at
-// columns 16m + 4q (m = 0..7), as in delta_kernel. A token's q and k go
-// through LDS (one float4 per lane); the next kDeltaScanAhead tokens' loads
-// are in flight while a token is computed.
+// One wavefront per 4 value rows (grid: row blocks x value heads x
+// segments): the 16 lanes of row 4 * blockIdx.x + lane / 16 hold it as
+// delta_kernel does (columns 4o + 64m) and run delta_row per token, so the
+// chain of a token is 8 columns long and the scan has a wavefront per SIMD at
+// the 4B shapes. A token's q and k go through LDS (one float4 per lane); the
+// next kDeltaScanAhead tokens' loads are in flight while a token is computed.
 constexpr int kDeltaScanAhead = 4;
-constexpr int kDeltaScanRows = 16;
+constexpr int kDeltaScanRows = 64 / kRowLanes;
 
 struct ScanToken {
   q35_f32x4 qk;  // floats 4 * lane .. +3 of [q | k]
@@ -373,7 +380,7 @@ struct ScanToken {
 __global__ __launch_bounds__(64) void delta_scan_kernel(DeltaArgs a) {
   __shared__ q35_f32x4 qk_lds[2][2 * kDim / 4];
   const int lane = threadIdx.x, vh = blockIdx.y;
-  const int quad = lane & 3, row = kDeltaScanRows * blockIdx.x + (lane >> 2);
+  const int col = lane & (kRowLanes - 1), row = kDeltaScanRows * blockIdx.x + (lane >> 4);
   // segment blockIdx.z: rows r0 .. r0 + count - 1 of one slot, in order
   const int r0 = a.row_seg != nullptr ? a.seg_row0[blockIdx.z] : 0;
   const int count = a.row_seg != nullptr ? a.seg_count[blockIdx.z] : a.batch;
@@ -381,12 +388,12 @@ __global__ __launch_bounds__(64) void delta_scan_kernel(DeltaArgs a) {
   const int rpar = a.state_copy_stride > 0 ? (pos0 & 1) : 0;
   const int wpar = a.state_copy_stride > 0 ? ((pos0 + count) & 1) : 0;
   float *state_slot = a.state_base + static_cast<long long>(slot) * a.state_slot_stride;
-  const size_t off = static_cast<size_t>(vh) * kDim * kDim + static_cast<size_t>(row) * kDim + 4 * quad;
+  const size_t off = static_cast<size_t>(vh) * kDim * kDim + static_cast<size_t>(row) * kDim + 4 * col;
   const q35_f32x4 *S = reinterpret_cast<const q35_f32x4 *>(state_slot + rpar * a.state_copy_stride + off);
   q35_f32x4 *W = reinterpret_cast<q35_f32x4 *>(state_slot + wpar * a.state_copy_stride + off);
-  q35_f32x4 st[8];
+  q35_f32x4 st[2];
 #pragma unroll
-  for (int m = 0; m < 8; ++m) st[m] = Q35_LOAD_NT(S + 4 * m);
+  for (int m = 0; m < 2; ++m) st[m] = Q35_LOAD_NT(S + 16 * m);
   const size_t tstride = static_cast<size_t>(a.v_heads) * kDeltaScanStride;
   const float *scan = a.scan + static_cast<size_t>(r0) * tstride + static_cast<size_t>(vh) * kDeltaScanStride;
   float *outs = a.scan + static_cast<size_t>(a.batch) * tstride + static_cast<size_t>(r0) * a.v_heads * kDim +
@@ -401,46 +408,28 @@ __global__ __launch_bounds__(64) void delta_scan_kernel(DeltaArgs a) {
   ScanToken buf[kDeltaScanAhead];
 #pragma unroll
   for (int d = 0; d < kDeltaScanAhead; ++d) load(buf[d], min(d, count - 1));
-  for (int r0 = 0; r0 < count; r0 += kDeltaScanAhead) {
+  for (int r0t = 0; r0t < count; r0t += kDeltaScanAhead) {
 #pragma unroll
     for (int d = 0; d < kDeltaScanAhead; ++d) {
-      const int r = r0 + d;
+      const int r = r0t + d;
       if (r >= count) break;
       q35_f32x4 *lds = qk_lds[d & 1];
       lds[lane] = buf[d].qk;
       const float v = buf[d].v, alpha = buf[d].alpha, beta = buf[d].beta;
       load(buf[d], min(r + kDeltaScanAhead, count - 1));
       lds_barrier();
-      q35_f32x4 kc[8];
+      q35_f32x4 kc[2], qc[2];
 #pragma unroll
-      for (int m = 0; m < 8; ++m) kc[m] = lds[kDim / 4 + 4 * m + quad];
-      float dot = 0.0F;
-#pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        st[m] *= alpha;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) dot += st[m][e] * kc[m][e];
+      for (int m = 0; m < 2; ++m) {
+        kc[m] = lds[kDim / 4 + col + 16 * m];
+        qc[m] = lds[col + 16 * m];
       }
-      dot += q35_quad_xor1(dot);
-      dot += q35_quad_xor2(dot);
-      const float delta = (v - dot) * beta;
-      float o = 0.0F;
-#pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        const q35_f32x4 qc = lds[4 * m + quad];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          st[m][e] += delta * kc[m][e];
-          o += st[m][e] * qc[e];
-        }
-      }
-      o += q35_quad_xor1(o);
-      o += q35_quad_xor2(o);
-      if (quad == 0) outs[static_cast<size_t>(r) * a.v_heads * kDim] = o;
+      const float o = delta_row(st, kc, qc, v, alpha, beta);
+      if (col == 0) outs[static_cast<size_t>(r) * a.v_heads * kDim] = o;
     }
   }
 #pragma unroll
-  for (int m = 0; m < 8; ++m) Q35_STORE_NT(st[m], W + 4 * m);
+  for (int m = 0; m < 2; ++m) Q35_STORE_NT(st[m], W + 16 * m);
 }
 
 // Lane j = lane % 16 holds columns 8j .. 8j+7 of the head's outputs (the four
