@@ -485,7 +485,25 @@ typedef struct {
   int32_t page_tokens;
   int32_t use_graphs;
   uint64_t max_prefix_bytes;   /* CpuEngineConfig::max_prefix_bytes; 0 = 256 MiB */
+  int32_t max_prefill_requests; /* CpuEngineConfig::max_prefill_requests: prompt chunks of up to this
+                                   many requests share one step (1..16; 0 = 1) */
+  int32_t packed_steps;         /* no reference counterpart: 1 = q35_engine_step runs the decode batch
+                                   and the prompt chunks in one packed step when both are pending,
+                                   0 = alternate them as the reference scheduler does */
 } q35_engine_config;
+/* CpuEngineStats (cpu_engine.h:151-168) for the counters this engine keeps;
+ * packed_ticks / packed_rows (steps that carried decode rows and prompt
+ * chunks together) have no reference counterpart. */
+typedef struct {
+  uint64_t batch_ticks, batch_rows;            /* advance_batch calls, their rows */
+  uint64_t projection_batches;                 /* projection GEMM launches (plus greedy heads) */
+  uint64_t lm_head_batches, greedy_lm_head_batches;
+  uint64_t state_batches;                      /* per-layer DeltaNet / attention batches */
+  uint64_t shared_prefill_ticks, shared_prefill_requests;
+  uint64_t packed_ticks, packed_rows;
+  uint64_t queued_requests, resident_requests;
+  uint64_t physical_kv_bytes;                  /* KV pages held by requests and prefixes */
+} q35_engine_stats;
 typedef struct {
   int32_t status;
   uint64_t generated_tokens, committed_tokens, prefill_tokens, decode_forwards;
@@ -536,9 +554,11 @@ int q35_engine_advance(q35_engine *engine, uint64_t id);
 int q35_engine_advance_batch(q35_engine *engine, const uint64_t *ids, size_t count);
 int q35_engine_step(q35_engine *engine, int32_t *progressed);
 /* No reference counterpart: prefill several requests, each to the end of its
- * prompt in chunks of up to max_decode_batch_size positions (the reference
+ * prompt in chunks of up to prefill_chunk_size positions (the reference
  * prefills one chunk of one request per advance(), cpu_engine.inl:668-790). */
 int q35_engine_prefill_batch(q35_engine *engine, const uint64_t *ids, size_t count);
+/* CpuEngine::stats (cpu_engine.inl:1017-1043). */
+int q35_engine_get_stats(const q35_engine *engine, q35_engine_stats *out);
 int q35_engine_result(q35_engine *engine, uint64_t id, q35_request_result *out,
                       int32_t *tokens, size_t token_capacity, size_t *token_count);
 int q35_engine_cancel(q35_engine *engine, uint64_t id);

@@ -77,7 +77,16 @@ class StepDesc(ctypes.Structure):
 class EngineConfig(ctypes.Structure):
     _fields_ = [("max_resident_requests", c_int32), ("max_context", c_int32),
                 ("max_decode_batch_size", c_int32), ("prefill_chunk_size", c_int32),
-                ("page_tokens", c_int32), ("use_graphs", c_int32), ("max_prefix_bytes", c_uint64)]
+                ("page_tokens", c_int32), ("use_graphs", c_int32), ("max_prefix_bytes", c_uint64),
+                ("max_prefill_requests", c_int32), ("packed_steps", c_int32)]
+
+
+class EngineStats(ctypes.Structure):
+    """q35_engine_stats (CpuEngineStats, cpu_engine.h:151-168)."""
+    _fields_ = [(n, c_uint64) for n in (
+        "batch_ticks", "batch_rows", "projection_batches", "lm_head_batches", "greedy_lm_head_batches",
+        "state_batches", "shared_prefill_ticks", "shared_prefill_requests", "packed_ticks", "packed_rows",
+        "queued_requests", "resident_requests", "physical_kv_bytes")]
 
 
 class RequestResult(ctypes.Structure):
@@ -211,6 +220,7 @@ _SIGS = {
     "q35_engine_submit_prefixed": (c_int, [P, P, c_size_t, c_size_t, c_float, P, c_size_t, c_uint64,
                                            POINTER(c_uint64)]),
     "q35_engine_prefix_stats": (c_int, [P, POINTER(PrefixStats)]),
+    "q35_engine_get_stats": (c_int, [P, POINTER(EngineStats)]),
     "q35_runtime_head": (c_int, [P, c_int32, P, c_float, P]),
     "q35_runtime_step_candidates": (c_int, [P, POINTER(StepDesc), P, P, P]),
     "q35_runtime_head_candidates": (c_int, [P, c_int32, P, c_float, P, P, P]),
@@ -673,10 +683,12 @@ class Engine(_Profiled):
     """CpuEngine mirror (include/qwen35x/runtime/cpu_engine.h:173-215), greedy requests."""
 
     def __init__(self, model, max_resident_requests=32, max_context=8192, max_decode_batch_size=32,
-                 prefill_chunk_size=128, page_tokens=16, use_graphs=True, max_prefix_bytes=0):
+                 prefill_chunk_size=128, page_tokens=16, use_graphs=True, max_prefix_bytes=0,
+                 max_prefill_requests=1, packed_steps=False):
         self.model, self.ctx = model, model.ctx
         cfg = EngineConfig(max_resident_requests, max_context, max_decode_batch_size, prefill_chunk_size,
-                           page_tokens, int(use_graphs), max_prefix_bytes)
+                           page_tokens, int(use_graphs), max_prefix_bytes, int(max_prefill_requests),
+                           int(packed_steps))
         h = c_void_p()
         self.ctx.check(lib.q35_engine_create(model.handle, ctypes.byref(cfg), ctypes.byref(h)), "engine create")
         self.handle = h
@@ -755,6 +767,12 @@ class Engine(_Profiled):
     def free_pages(self):
         """Free pages of the engine's KV pool (q35_runtime_free_pages)."""
         return lib.q35_runtime_free_pages(self._rt())
+
+    def stats(self):
+        """Engine counters (q35_engine_get_stats) as a dict."""
+        st = EngineStats()
+        self._check(lib.q35_engine_get_stats(self.handle, ctypes.byref(st)), "stats")
+        return {f: getattr(st, f) for f, _ in st._fields_}
 
     def prefix_stats(self):
         st = PrefixStats()

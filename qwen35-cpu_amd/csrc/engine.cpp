@@ -8,7 +8,9 @@
 //                   row and is never retried (cpu_engine.inl:939-1017)
 //   step            serving scheduler: retire, admit, alternate decode batches
 //                   with prefill chunks, rotate for fairness
-//                   (cpu_engine_scheduler.inl:2-105)
+//                   (cpu_engine_scheduler.inl:2-105) -- or, with packed_steps,
+//                   run the decode batch and the prompt chunks of up to
+//                   max_prefill_requests requests in one packed step
 //   register_prefix / find_prefix   cpu_engine_prefix.inl:11-96: a state
 //                   snapshot plus the prefix's KV pages, shared by the
 //                   requests that attach it (CpuRequestSpec::prefix)
@@ -25,6 +27,7 @@
 #include <new>
 #include <numeric>
 #include <random>
+#include <set>
 #include <string>
 #include <vector>
 
@@ -90,6 +93,7 @@ struct q35_engine {
   uint64_t next_prefix = 1;
   size_t max_prefix_bytes = 0, prefix_bytes = 0;
   q35_prefix_stats prefix_stats{};
+  q35_engine_stats stats{};
 };
 
 namespace {
@@ -347,6 +351,16 @@ void select_token(Request &r, int32_t token) {
   }
 }
 
+// The counters of one forward through every layer (cpu_engine.inl:201-325):
+// four projections and one state batch per layer, then the head.
+void count_forward(q35_engine *e, bool greedy_head) {
+  const uint64_t layers = static_cast<uint64_t>(e->model->d.n_layers);
+  e->stats.projection_batches += 4 * layers + (greedy_head ? 1 : 0);
+  e->stats.state_batches += layers;
+  e->stats.lm_head_batches += 1;
+  e->stats.greedy_lm_head_batches += greedy_head ? 1 : 0;
+}
+
 // One device step over `rows`: each row feeds `inputs[i]` at position
 // rows[i]->committed. count_input marks generated tokens. With `sample` the
 // head keeps the logits and returns each row's candidates (and the raw logits
@@ -394,6 +408,7 @@ int run_step(q35_engine *e, const std::vector<Request *> &rows, const std::vecto
   }
   if (st != Q35_OK) return fail(e, st, e->model->ctx->error.c_str());
   for (auto *r : rows) ++r->committed;
+  count_forward(e, !sample);
   return Q35_OK;
 }
 
@@ -426,6 +441,11 @@ extern "C" int q35_engine_create(q35_model *m, const q35_engine_config *cfg, q35
   e->model = m;
   e->cfg = *cfg;
   if (e->cfg.prefill_chunk_size <= 0) e->cfg.prefill_chunk_size = 128;
+  if (e->cfg.max_prefill_requests <= 0) e->cfg.max_prefill_requests = 1;
+  if (e->cfg.max_prefill_requests > q35::kMaxPrefillSegments || e->cfg.prefill_chunk_size > q35::kMaxStepRows) {
+    delete e;
+    return Q35_ERR_INVALID;
+  }
   e->max_prefix_bytes = cfg->max_prefix_bytes ? static_cast<size_t>(cfg->max_prefix_bytes) : size_t(256) << 20;
   q35_runtime_config rc{};
   rc.max_slots = cfg->max_resident_requests;
@@ -433,6 +453,11 @@ extern "C" int q35_engine_create(q35_model *m, const q35_engine_config *cfg, q35
   rc.max_context = cfg->max_context;
   rc.page_tokens = cfg->page_tokens;
   rc.use_graphs = cfg->use_graphs;
+  // rows of the largest step: the prompt chunks of a shared prefill, plus
+  // the decode batch when the two are packed together
+  const long long step_rows = static_cast<long long>(e->cfg.max_prefill_requests) * e->cfg.prefill_chunk_size +
+                              (e->cfg.packed_steps ? rc.max_batch : 0);
+  rc.max_step_rows = static_cast<int32_t>(std::min<long long>(step_rows, q35::kMaxStepRows));
   const int st = q35_runtime_create(m, &rc, &e->rt);
   if (st != Q35_OK) {
     delete e;
@@ -545,7 +570,7 @@ extern "C" int q35_engine_submit_spec(q35_engine *e, const q35_request_spec *spe
 // prompt token yields the first generated token.
 static int prefill_chunks(q35_engine *e, Request &r, size_t limit) {
   const auto t0 = std::chrono::steady_clock::now();
-  const size_t rows = static_cast<size_t>(e->cfg.max_decode_batch_size);
+  const size_t rows = static_cast<size_t>(std::max(e->rt->max_rows, 1));
   const int max_pages = (e->cfg.max_context + e->cfg.page_tokens - 1) / e->cfg.page_tokens;
   std::vector<int32_t> table(max_pages, 0);
   if (r.committed == r.prompt.size() && r.status == Q35_REQ_PREFILL) {
@@ -583,6 +608,7 @@ static int prefill_chunks(q35_engine *e, Request &r, size_t limit) {
       r.status = Q35_REQ_FAILED;
       return fail(e, st, e->model->ctx->error.c_str());
     }
+    count_forward(e, true);
     r.committed += n;
     r.result.prefill_tokens += n;
     done += n;
@@ -646,6 +672,8 @@ extern "C" int q35_engine_advance_batch(q35_engine *e, const uint64_t *ids, size
     fail_rows(rows);
     return st;
   }
+  ++e->stats.batch_ticks;
+  e->stats.batch_rows += rows.size();
   const double ms = ms_since(t0);
   const int vocab = e->model->d.vocab;
   int result = Q35_OK;
@@ -695,6 +723,113 @@ extern "C" int q35_engine_prefill_batch(q35_engine *e, const uint64_t *ids, size
   return Q35_OK;
 }
 
+// One packed step (q35_runtime_step_segments): a decode row of every request
+// in `decode` and the next prompt chunk of every request in `prefill`. Every
+// request's rows get exactly what its advance_batch / advance call would give
+// it; a failed step fails every request in it (state may have moved, so it is
+// never retried).
+static int packed_step(q35_engine *e, const std::vector<Request *> &decode, const std::vector<Request *> &prefill) {
+  const auto t0 = std::chrono::steady_clock::now();
+  const int max_pages = (e->cfg.max_context + e->cfg.page_tokens - 1) / e->cfg.page_tokens;
+  const size_t nd = decode.size(), n = nd + prefill.size();
+  std::vector<Request *> all(decode);
+  all.insert(all.end(), prefill.begin(), prefill.end());
+  std::vector<int32_t> table(n * static_cast<size_t>(max_pages), 0), inputs(nd);
+  std::vector<q35_segment> segs(n);
+  std::vector<size_t> counts(n, 1);
+  bool sample = false;
+  for (size_t i = 0; i < n; ++i) {
+    Request &r = *all[i];
+    const bool dec = i < nd;
+    if (!dec) counts[i] = std::min(static_cast<size_t>(e->cfg.prefill_chunk_size), r.prompt.size() - r.committed);
+    int st = own_page(e, r, r.committed);
+    if (st == Q35_OK) st = ensure_page(e, r, r.committed + counts[i] - 1);
+    if (st != Q35_OK) {
+      fail_rows(all);
+      return st;
+    }
+    std::copy(r.pages.begin(), r.pages.end(), table.begin() + i * max_pages);
+    q35_segment &g = segs[i];
+    g.slot = r.slot;
+    g.pos0 = static_cast<int32_t>(r.committed);
+    g.count = static_cast<int32_t>(counts[i]);
+    if (dec) inputs[i] = r.pending;
+    g.tokens = dec ? &inputs[i] : r.prompt.data() + r.committed;
+    g.page_table = table.data() + i * max_pages;
+    g.max_pages = max_pages;
+    g.penalty = r.penalty;
+    g.count_input = dec ? 1 : 0;
+    g.want_token = dec || r.committed + counts[i] == r.prompt.size();
+    if (g.want_token && !is_greedy(r)) sample = true;
+  }
+  std::vector<int32_t> out(n, -1);
+  std::vector<q35_row_sampling> rs;
+  std::vector<q35_candidate> cands;
+  std::vector<float> raw;
+  if (sample) {
+    bool need_raw = false;
+    for (auto *r : all) {
+      rs.push_back(row_sampling(*r));
+      need_raw = need_raw || needs_raw_logits(*r);
+    }
+    cands.assign(n * Q35_MAX_CANDIDATES, q35_candidate{});
+    raw.assign(need_raw ? n * static_cast<size_t>(e->model->d.vocab) : 0, 0.0F);
+  }
+  const int st = q35_runtime_step_segments(e->rt, segs.data(), static_cast<int32_t>(n), sample ? rs.data() : nullptr,
+                                           out.data(), sample ? cands.data() : nullptr,
+                                           raw.empty() ? nullptr : raw.data());
+  if (st != Q35_OK) {
+    fail_rows(all);
+    return fail(e, st, e->model->ctx->error.c_str());
+  }
+  count_forward(e, !sample);
+  if (nd > 0) {
+    ++e->stats.batch_ticks;
+    e->stats.batch_rows += nd;
+  }
+  if (prefill.size() > 1) {
+    ++e->stats.shared_prefill_ticks;
+    e->stats.shared_prefill_requests += prefill.size();
+  }
+  if (nd > 0 && !prefill.empty()) {
+    ++e->stats.packed_ticks;
+    e->stats.packed_rows += nd + std::accumulate(counts.begin() + nd, counts.end(), size_t{0});
+  }
+  const double ms = ms_since(t0) / n;
+  const int vocab = e->model->d.vocab;
+  int result = Q35_OK;
+  std::string first_error;
+  for (size_t i = 0; i < n; ++i) {
+    Request &r = *all[i];
+    const bool dec = i < nd;
+    r.committed += counts[i];
+    if (dec) {
+      ++r.result.decode_forwards;
+      r.result.decode_ms += ms;
+    } else {
+      r.result.prefill_tokens += counts[i];
+      r.result.prefill_ms += ms;
+    }
+    r.result.committed_tokens = r.committed;
+    if (!segs[i].want_token) continue;
+    int32_t token = out[i];
+    if (sample) {
+      const int cs = choose_token(e, r, cands.data() + i * Q35_MAX_CANDIDATES,
+                                  raw.empty() ? nullptr : raw.data() + i * static_cast<size_t>(vocab), token);
+      if (cs != Q35_OK) {
+        // this request fails; the others keep their tokens (cpu_engine.inl:1006-1013)
+        r.status = Q35_REQ_FAILED;
+        if (result == Q35_OK) first_error = e->error;
+        result = cs;
+        continue;
+      }
+    }
+    select_token(r, token);
+  }
+  if (result != Q35_OK) e->error = first_error;
+  return result;
+}
+
 extern "C" int q35_engine_step(q35_engine *e, int32_t *progressed) {
   if (e == nullptr || progressed == nullptr) return Q35_ERR_INVALID;
   *progressed = 0;
@@ -733,9 +868,37 @@ extern "C" int q35_engine_step(q35_engine *e, int32_t *progressed) {
   rotate(prefill, e->last_prefill);
   rotate(decode, e->last_decode);
   if (prefill.empty() && decode.empty()) return Q35_OK;
+  *progressed = 1;
+  // prompt chunks of up to max_prefill_requests requests (a complete prefix
+  // hit goes through advance(): its first token comes from the prefix)
+  auto chunkable = [&](uint64_t id) {
+    const Request &r = e->reqs.at(id);
+    return r.committed < r.prompt.size();
+  };
+  std::vector<uint64_t> shared;
+  for (auto id : prefill) {
+    if (shared.size() == static_cast<size_t>(e->cfg.max_prefill_requests)) break;
+    if (chunkable(id)) shared.push_back(id);
+  }
+  const bool pack = !shared.empty() && (shared.size() > 1 || (e->cfg.packed_steps && !decode.empty())) &&
+                    (!prefill.empty() && chunkable(prefill.front()));
+  if (pack) {
+    std::vector<Request *> drows, prows;
+    if (e->cfg.packed_steps) {
+      decode.resize(std::min(decode.size(), static_cast<size_t>(e->cfg.max_decode_batch_size)));
+      for (auto id : decode) drows.push_back(&e->reqs.at(id));
+      if (!decode.empty()) e->last_decode = decode.back();
+    }
+    for (auto id : shared) prows.push_back(&e->reqs.at(id));
+    e->last_prefill = shared.back();
+    e->prefer_decode = drows.empty();
+    const int st = packed_step(e, drows, prows);
+    for (auto *r : drows) retire(e, *r);
+    for (auto *r : prows) retire(e, *r);
+    return st;
+  }
   const bool do_decode = !decode.empty() && (prefill.empty() || e->prefer_decode);
   e->prefer_decode = !do_decode;
-  *progressed = 1;
   int st;
   std::vector<uint64_t> work;
   if (do_decode) {
@@ -769,6 +932,25 @@ extern "C" int q35_engine_result(q35_engine *e, uint64_t id, q35_request_result 
 }
 
 extern "C" q35_runtime *q35_engine_runtime(q35_engine *e) { return e ? e->rt : nullptr; }
+
+extern "C" int q35_engine_get_stats(const q35_engine *e, q35_engine_stats *out) {
+  if (e == nullptr || out == nullptr) return Q35_ERR_INVALID;
+  *out = e->stats;
+  out->queued_requests = out->resident_requests = 0;
+  std::set<int32_t> pages;
+  for (const auto &kv : e->reqs) {
+    out->queued_requests += kv.second.status == Q35_REQ_QUEUED;
+    out->resident_requests += kv.second.resident;
+    pages.insert(kv.second.pages.begin(), kv.second.pages.end());
+  }
+  for (const auto &p : e->prefixes) pages.insert(p->pages.begin(), p->pages.end());
+  const q35_model_dims &d = e->model->d;
+  // K and V rows of every full-attention layer, FP16
+  const uint64_t page_bytes = static_cast<uint64_t>(e->cfg.page_tokens) * d.n_kv_heads * d.head_dim * 2 * 2 *
+                              static_cast<uint64_t>(e->model->n_full);
+  out->physical_kv_bytes = pages.size() * page_bytes;
+  return Q35_OK;
+}
 
 extern "C" int q35_engine_cancel(q35_engine *e, uint64_t id) {
   if (e == nullptr) return Q35_ERR_INVALID;
