@@ -771,10 +771,12 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t stream) {
   if (a.g16 && (!(argmax || a.head) || exact || (!argmax && a.out == nullptr))) return hipErrorInvalidValue;
   if ((argmax || a.head) && !exact && (argmax || a.out != nullptr)) {
     const HeadPlan hp = head_plan(a.rows, a.nb, a.tokens, a.cu_count, a.force_gpw);
-    if (!hp.use && a.g16) {
-      // G16 has only the staged-activation kernel: launches over groups of
-      // token tiles that fit, all at one grid so that the candidate rows
-      // (argmax) line up with gemm_argmax_cands
+    if (!hp.use && (a.g16 || !argmax)) {
+      // G16 has only the staged-activation kernel, and a logits head must
+      // keep its single fma chain per output at every batch size (the split
+      // fallback would sum several wavefronts' chains): launches over groups
+      // of token tiles that fit, all at one grid so that the candidate rows
+      // (G16 argmax) line up with gemm_argmax_cands
       const int fit = head_fit_tiles(a.nb);
       if (fit < 1) return hipErrorInvalidValue;
       const int gpw = head_plan(a.rows, a.nb, 16 * fit, a.cu_count, a.force_gpw).gpw;
