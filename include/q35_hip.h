@@ -518,11 +518,26 @@ typedef struct {
  * zero fails the request. It must not call back into the engine. */
 typedef int (*q35_logits_callback)(void *context, size_t index, int32_t forced_token, const float *logits,
                                    size_t count);
-/* CpuRequestSpec (cpu_engine.h:105-133) without constraints, selected readout
- * and drafting. Sampling follows SamplingOptions (options.h:10-13): temperature
- * <= 1e-6 is greedy; seed < 0 seeds the request's mt19937 from random_device
- * (cpu_engine.inl:379-381). stop_sequences holds stop_sequence_count
- * sequences back to back, of the given lengths. */
+/* CpuSamplingConstraint (cpu_engine.h:84-94) in C, owned by the caller and
+ * alive until the request ends; called by the engine owner only. apply masks
+ * disallowed logits of a row in place (count = vocab; it must leave a finite
+ * candidate), accept advances after the token is chosen; each returns nonzero
+ * to go on, zero to fail the request. */
+typedef struct {
+  void *context;
+  int (*apply)(void *context, float *logits, size_t count);
+  int (*accept)(void *context, int32_t token);
+} q35_sampling_constraint;
+/* CpuRequestSpec (cpu_engine.h:105-133) without drafting. Sampling follows
+ * SamplingOptions (options.h:10-13): temperature <= 1e-6 is greedy; seed < 0
+ * seeds the request's mt19937 from random_device (cpu_engine.inl:379-381).
+ * stop_sequences holds stop_sequence_count sequences back to back, of the
+ * given lengths. select() order (cpu_engine.inl:441-465): selected readout
+ * callback, logits callback, constraint apply, forced / greedy / sampled
+ * token, constraint accept. A selected readout (values at the given token
+ * IDs, duplicates included) needs its own callback, no logits callback,
+ * max_new_tokens 1 and one forced token; a constraint cannot be combined
+ * with forced or selected readout (cpu_engine.inl:866-875). */
 typedef struct {
   const int32_t *prompt_tokens;
   size_t prompt_count;
@@ -541,6 +556,11 @@ typedef struct {
   q35_logits_callback logits_callback;
   void *logits_callback_context;
   uint64_t prefix;                     /* 0 = none (q35_engine_register_prefix) */
+  const q35_sampling_constraint *sampling_constraint; /* NULL = none */
+  const int32_t *selected_logit_tokens;
+  size_t selected_logit_count;
+  q35_logits_callback selected_logits_callback;
+  void *selected_logits_callback_context;
 } q35_request_spec;
 
 int q35_engine_create(q35_model *model, const q35_engine_config *config, q35_engine **out);

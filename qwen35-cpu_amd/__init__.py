@@ -118,7 +118,18 @@ class RequestSpec(ctypes.Structure):
                 ("stop_sequence_count", c_size_t),
                 ("forced_output_tokens", POINTER(c_int32)), ("forced_count", c_size_t),
                 ("logits_callback", LOGITS_CALLBACK), ("logits_callback_context", c_void_p),
-                ("prefix", c_uint64)]
+                ("prefix", c_uint64), ("sampling_constraint", c_void_p),
+                ("selected_logit_tokens", POINTER(c_int32)), ("selected_logit_count", c_size_t),
+                ("selected_logits_callback", LOGITS_CALLBACK), ("selected_logits_callback_context", c_void_p)]
+
+
+CONSTRAINT_APPLY = ctypes.CFUNCTYPE(c_int, c_void_p, POINTER(c_float), c_size_t)
+CONSTRAINT_ACCEPT = ctypes.CFUNCTYPE(c_int, c_void_p, c_int32)
+
+
+class SamplingConstraint(ctypes.Structure):
+    """q35_sampling_constraint (CpuSamplingConstraint, cpu_engine.h:84-94)."""
+    _fields_ = [("context", c_void_p), ("apply", CONSTRAINT_APPLY), ("accept", CONSTRAINT_ACCEPT)]
 
 
 class PrefixStats(ctypes.Structure):
@@ -712,11 +723,15 @@ class Engine(_Profiled):
 
     def submit_spec(self, prompt, max_new_tokens=128, temperature=0.7, top_p=0.8, top_k=20,
                     repetition_penalty=1.05, seed=-1, stop_token_ids=(), stop_sequences=(), forced_output_tokens=(),
-                    logits_callback=None, prefix=0):
+                    logits_callback=None, prefix=0, sampling_constraint=None, selected_logit_tokens=(),
+                    selected_logits_callback=None):
         """CpuEngine::submit with a CpuRequestSpec (q35_engine_submit_spec); the
         sampling defaults are SamplingOptions' (options.h:10-13). logits_callback,
         when given, is a Python callable (index, forced_token, logits ndarray) ->
-        bool, called with each row's raw logits."""
+        bool, called with each row's raw logits. sampling_constraint is an object
+        with apply(logits ndarray, masked in place) -> bool and accept(token) ->
+        bool (CpuSamplingConstraint). selected_logits_callback (same signature as
+        logits_callback) receives the logits at selected_logit_tokens."""
         keep = []  # arrays and the callback must outlive the call
 
         def arr(values, dtype, ctype):
@@ -739,8 +754,35 @@ class Engine(_Profiled):
                     return 0
             cb = LOGITS_CALLBACK(trampoline)
             self._callbacks = getattr(self, "_callbacks", []) + [cb]
+        def wrap(fn):
+            def trampoline(_ctx, index, forced, logits, count):
+                try:
+                    return 1 if fn(index, forced, np.ctypeslib.as_array(logits, (count,)).copy()) else 0
+                except Exception:  # a raising callback fails the request, as returning false does
+                    return 0
+            return LOGITS_CALLBACK(trampoline)
+
+        scb = wrap(selected_logits_callback) if selected_logits_callback is not None else LOGITS_CALLBACK()
+        sel_p, nsel = arr(selected_logit_tokens, np.int32, c_int32)
+        cons = None
+        if sampling_constraint is not None:
+            def apply(_ctx, logits, count):
+                try:
+                    return 1 if sampling_constraint.apply(np.ctypeslib.as_array(logits, (count,))) else 0
+                except Exception:
+                    return 0
+
+            def accept(_ctx, token):
+                try:
+                    return 1 if sampling_constraint.accept(int(token)) else 0
+                except Exception:
+                    return 0
+            cons = SamplingConstraint(None, CONSTRAINT_APPLY(apply), CONSTRAINT_ACCEPT(accept))
+        self._callbacks = getattr(self, "_callbacks", []) + [scb, cons]
         spec = RequestSpec(prompt_p, n, max_new_tokens, temperature, top_p, top_k, repetition_penalty, seed,
-                           stops_p, ns, flat_p, lens_p, nseq, forced_p, nf, cb, None, prefix)
+                           stops_p, ns, flat_p, lens_p, nseq, forced_p, nf, cb, None, prefix,
+                           ctypes.cast(ctypes.pointer(cons), c_void_p) if cons is not None else None,
+                           sel_p, nsel, scb, None)
         rid = c_uint64()
         self._check(lib.q35_engine_submit_spec(self.handle, ctypes.byref(spec), ctypes.byref(rid)), "submit")
         return rid.value

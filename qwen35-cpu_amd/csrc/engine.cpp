@@ -47,6 +47,10 @@ struct Request {
   std::vector<int32_t> forced;  // forced_output_tokens
   q35_logits_callback callback = nullptr;
   void *callback_context = nullptr;
+  const q35_sampling_constraint *constraint = nullptr;
+  std::vector<int32_t> selected;  // selected readout token IDs
+  q35_logits_callback selected_callback = nullptr;
+  void *selected_context = nullptr;
   std::vector<int32_t> stops;
   std::vector<std::vector<int32_t>> stop_sequences;
   int status = Q35_REQ_QUEUED;
@@ -223,7 +227,10 @@ int ensure_page(q35_engine *e, Request &r, size_t position) {
 }
 
 // The fused greedy head serves a request (cpu_engine.inl:307-313, 676-678).
-bool is_greedy(const Request &r) { return r.temperature <= 1e-6F && r.forced.empty() && r.callback == nullptr; }
+bool is_greedy(const Request &r) {
+  return r.temperature <= 1e-6F && r.forced.empty() && r.callback == nullptr && r.constraint == nullptr &&
+         r.selected.empty();
+}
 
 // Device candidate settings of a request: greedy argmax (k = 1, scale 1) at
 // temperature ~0, top_k candidates when 1 <= top_k <= 64, else one
@@ -237,7 +244,7 @@ q35_row_sampling row_sampling(const Request &r) {
   return s;
 }
 bool needs_raw_logits(const Request &r) {
-  return r.callback != nullptr ||
+  return r.callback != nullptr || r.constraint != nullptr || !r.selected.empty() ||
          (r.temperature > 1e-6F && (r.top_k <= 0 || r.top_k > Q35_MAX_CANDIDATES) && r.forced.empty());
 }
 
@@ -313,9 +320,47 @@ int32_t sample_full(const float *raw, int vocab, const std::vector<int32_t> &cou
 int choose_token(q35_engine *e, Request &r, const q35_candidate *cands, const float *raw, int32_t &token) {
   const int vocab = e->model->d.vocab;
   const size_t index = r.output.size();
+  if (!r.selected.empty()) {
+    // selected readout: the head rows of the given tokens, which are the
+    // same single-chain dots as the full row (layers.inl:414-455)
+    std::vector<float> values(r.selected.size());
+    for (size_t i = 0; i < values.size(); ++i) values[i] = raw[r.selected[i]];
+    if (!r.selected_callback(r.selected_context, index, r.forced[index], values.data(), values.size()))
+      return fail(e, Q35_ERR_STATE, "Selected logits callback failed.");
+  }
   if (r.callback != nullptr &&
       !r.callback(r.callback_context, index, r.forced.empty() ? -1 : r.forced[index], raw, static_cast<size_t>(vocab)))
     return fail(e, Q35_ERR_STATE, "Logits callback failed.");
+  if (r.constraint != nullptr) {
+    // the constraint masks a copy of the raw row; the token is then chosen
+    // from the whole masked row (sample_token_from_logits, layers.inl:491-600)
+    std::vector<float> masked(raw, raw + vocab);
+    if (!r.constraint->apply(r.constraint->context, masked.data(), masked.size()))
+      return fail(e, Q35_ERR_STATE, "Sampling constraint rejected the logits.");
+    std::vector<int32_t> counts(vocab);
+    const int st = q35_slot_counts(e->rt, r.slot, counts.data(), counts.size());
+    if (st != Q35_OK) return fail(e, st, e->model->ctx->error.c_str());
+    if (r.temperature <= 1e-6F) {
+      // argmax after the repetition penalty, lowest index on ties (layers.inl:519-541)
+      float best = -INFINITY;
+      token = -1;
+      for (int i = 0; i < vocab; ++i) {
+        float v = masked[i];
+        if (r.penalty > 1.0F && counts[i] > 0) v = v > 0.0F ? v / r.penalty : v * r.penalty;
+        if (token < 0 || v > best) {
+          best = v;
+          token = i;
+        }
+      }
+      if (!(best > -INFINITY)) return fail(e, Q35_ERR_STATE, "Sampling constraint left no finite candidate.");
+    } else {
+      token = sample_full(masked.data(), vocab, counts, r);
+    }
+    if (token < 0 || token >= vocab) return fail(e, Q35_ERR_STATE, "Invalid sampled token.");
+    if (!r.constraint->accept(r.constraint->context, token))
+      return fail(e, Q35_ERR_STATE, "Sampling constraint rejected the token.");
+    return Q35_OK;
+  }
   if (!r.forced.empty()) {
     token = r.forced[index];
   } else if (r.temperature <= 1e-6F) {
@@ -525,6 +570,19 @@ extern "C" int q35_engine_submit_spec(q35_engine *e, const q35_request_spec *spe
   if (!std::all_of(prompt, prompt + n, valid_token) ||
       !std::all_of(spec->forced_output_tokens, spec->forced_output_tokens + spec->forced_count, valid_token))
     return fail(e, Q35_ERR_INVALID, "Invalid request token.");
+  const bool selected = spec->selected_logit_count != 0 || spec->selected_logits_callback != nullptr;
+  if (spec->sampling_constraint != nullptr &&
+      (selected || spec->forced_count != 0 || spec->sampling_constraint->apply == nullptr ||
+       spec->sampling_constraint->accept == nullptr))
+    return fail(e, Q35_ERR_INVALID, "Sampling constraints cannot be combined with forced or selected readout.");
+  if (selected &&
+      (spec->selected_logit_count == 0 || spec->selected_logit_tokens == nullptr ||
+       spec->selected_logits_callback == nullptr || spec->logits_callback != nullptr || max_new != 1 ||
+       spec->forced_count != 1 || e->model->embed_g16 ||
+       !std::all_of(spec->selected_logit_tokens, spec->selected_logit_tokens + spec->selected_logit_count,
+                    valid_token)))
+    return fail(e, Q35_ERR_INVALID,
+                "Selected readout requires a Q4 DOT4 head, valid token IDs, its own callback and one forced token.");
   Prefix *pre = nullptr;
   if (prefix != 0) {
     // the attached prefix must be a prefix of the prompt (cpu_engine.inl:895-910)
@@ -544,6 +602,10 @@ extern "C" int q35_engine_submit_spec(q35_engine *e, const q35_request_spec *spe
   r.forced.assign(spec->forced_output_tokens, spec->forced_output_tokens + spec->forced_count);
   r.callback = spec->logits_callback;
   r.callback_context = spec->logits_callback_context;
+  r.constraint = spec->sampling_constraint;
+  if (selected) r.selected.assign(spec->selected_logit_tokens, spec->selected_logit_tokens + spec->selected_logit_count);
+  r.selected_callback = spec->selected_logits_callback;
+  r.selected_context = spec->selected_logits_callback_context;
   if (spec->stop_count) r.stops.assign(spec->stop_token_ids, spec->stop_token_ids + spec->stop_count);
   for (size_t i = 0, at = 0; i < spec->stop_sequence_count; at += spec->stop_sequence_lengths[i++])
     r.stop_sequences.emplace_back(spec->stop_sequences + at, spec->stop_sequences + at + spec->stop_sequence_lengths[i]);

@@ -206,3 +206,105 @@ def test_forced_callback_failure_and_stop_sequences(q, small):
     with pytest.raises(q.Q35Error):
         eng.submit_spec(prompt, 5, 0.7, 0.0, 20, 1.0, 1)  # top_p must be in (0, 1]
     eng.close()
+
+
+class ModuloConstraint:
+    """A stateful CpuSamplingConstraint: output token i must be congruent to
+    i (mod 3); apply masks the rest with -inf, accept records the token."""
+
+    def __init__(self):
+        self.accepted = []
+
+    def allowed(self, vocab):
+        return np.arange(vocab) % 3 == len(self.accepted) % 3
+
+    def apply(self, logits):
+        logits[~self.allowed(logits.size)] = -np.inf
+        return True
+
+    def accept(self, token):
+        if token % 3 != len(self.accepted) % 3:
+            return False
+        self.accepted.append(token)
+        return True
+
+
+@pytest.mark.parametrize("temperature,top_p,top_k,penalty,seed", [(0.0, 1.0, 0, 1.2, 1), (0.9, 0.8, 0, 1.1, 41),
+                                                                   (1.2, 1.0, 16, 1.0, 7)])
+def test_constraint_matches_restatement(q, small, temperature, top_p, top_k, penalty, seed):
+    """select() with a sampling constraint (cpu_engine.inl:441-465): the
+    logits callback sees the raw row, the constraint masks it, the token is
+    chosen from the masked row (greedy argmax after the penalty, or the full
+    row draw), and accept sees every token: equal to the restatement applied
+    to the masked raw rows, from the same seed."""
+    d, model = small
+    vocab = d["vocab"]
+    prompt = np.random.default_rng(seed + 100).integers(0, vocab, size=9).astype(np.int32)
+    new, seen = 8, {}
+    cons = ModuloConstraint()
+
+    def callback(index, forced, logits):
+        seen[index] = logits
+        return True
+
+    eng = engine(q, model)
+    print(f"constraint t={temperature} p={top_p} k={top_k}", flush=True)
+    rid = eng.submit_spec(prompt, new, temperature, top_p, top_k, penalty, seed, logits_callback=callback,
+                          sampling_constraint=cons)
+    res, toks = drain(q, eng, [rid])[0]
+    assert q.REQ_STATUS[res.status] == "complete" and toks.size == new
+    assert cons.accepted == toks.tolist()
+    counts = np.bincount(prompt, minlength=vocab)
+    mt = MT19937(seed)
+    for s in range(new):
+        masked = seen[s].copy()
+        masked[np.arange(vocab) % 3 != s % 3] = -np.inf
+        want = sample_token(masked, counts, temperature, top_p, top_k, penalty, mt)
+        assert toks[s] == want and toks[s] % 3 == s % 3, (s, toks[s], want)
+        counts[toks[s]] += 1
+    eng.close()
+
+
+def test_selected_readout_and_contract(q, small, request):
+    """A selected readout (selected_logit_tokens + selected_logits_callback,
+    one forced token) gets the head's values at the given token IDs, in
+    order and with duplicates: bit-equal to the full row a logits callback
+    sees for the same prompt. Combinations the reference rejects are
+    rejected (cpu_engine.inl:866-875)."""
+    d, model = small
+    vocab = d["vocab"]
+    prompt = np.random.default_rng(77).integers(0, vocab, size=10).astype(np.int32)
+    sel = np.array([5, 3, 5, vocab - 1, 0], np.int32)
+    eng = engine(q, model)
+    g16 = request.node.callspec.params["small"] == "g16q8"
+    full, got = {}, {}
+    rid = eng.submit_spec(prompt, 1, 0.0, 1.0, 0, 1.0, 0, forced_output_tokens=[7],
+                          logits_callback=lambda i, f, lg: full.setdefault(i, lg) is not None)
+    drain(q, eng, [rid])
+    kw = dict(forced_output_tokens=[7], selected_logit_tokens=sel,
+              selected_logits_callback=lambda i, f, v: got.setdefault(i, (f, v)) is not None)
+    if g16:  # the selected readout needs a Q4 DOT4 head (layers.inl:417-421)
+        with pytest.raises(q.Q35Error):
+            eng.submit_spec(prompt, 1, 0.0, 1.0, 0, 1.0, 0, **kw)
+        eng.close()
+        return
+    sid = eng.submit_spec(prompt, 1, 0.0, 1.0, 0, 1.0, 0, **kw)
+    res, toks = drain(q, eng, [sid])[0]
+    assert q.REQ_STATUS[res.status] == "complete" and toks.tolist() == [7]
+    forced, values = got[0]
+    assert forced == 7
+    np.testing.assert_array_equal(values.view(np.uint32), full[0][sel].view(np.uint32))
+    cons = ModuloConstraint()
+    for kw in (dict(forced_output_tokens=[7], sampling_constraint=cons),
+               dict(forced_output_tokens=[7], selected_logit_tokens=sel, sampling_constraint=cons,
+                    selected_logits_callback=lambda *a: True),
+               dict(forced_output_tokens=[7], selected_logit_tokens=sel, logits_callback=lambda *a: True,
+                    selected_logits_callback=lambda *a: True),
+               dict(forced_output_tokens=[7], selected_logit_tokens=sel),
+               dict(forced_output_tokens=[7], selected_logit_tokens=[vocab], selected_logits_callback=lambda *a: True)):
+        with pytest.raises(q.Q35Error):
+            eng.submit_spec(prompt, 1, 0.0, 1.0, 0, 1.0, 0, **kw)
+    with pytest.raises(q.Q35Error):  # a selected readout reads one token
+        eng.submit_spec(prompt, 2, 0.0, 1.0, 0, 1.0, 0, forced_output_tokens=[7, 7], selected_logit_tokens=sel,
+                        selected_logits_callback=lambda *a: True)
+    eng.close()
