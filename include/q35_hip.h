@@ -97,6 +97,14 @@ int q35_q4_dot4_matvec(q35_context *ctx, const q35_q4_0_block_x8 *matrix,
 int q35_q4_dot4_matmul(q35_context *ctx, const q35_q4_0_block_x8 *matrix,
                        const q35_q8_0_block_x4 *vectors, float *output, size_t rows,
                        size_t vectors_count, size_t blocks, size_t stride);
+/* q4_dot4_matmul_x1, q4_dot4.h:15-18: `count` independently prepared X1 rows
+ * ([count][blocks]) with matmul's output layout (row stride `stride`). */
+int q35_q4_dot4_matmul_x1(q35_context *ctx, const q35_q4_0_block_x8 *matrix,
+                          const q35_q8_0_block_x1 *vectors, float *output, size_t rows,
+                          size_t count, size_t blocks, size_t stride);
+/* q4_dot4_has_x1_tile, q4_dot4.h:14: whether matmul_x1 has a tiled path for
+ * `count` rows (every count >= 1 runs the MFMA tiles here). */
+int q35_q4_dot4_has_x1_tile(size_t count);
 /* Same contraction with one wavefront per 64-row group running the whole block
  * range, so every output is the reference's single fma chain over blocks
  * (q4_dot4.cpp:43-56): bit-exact FP32. No reference counterpart; slower. */

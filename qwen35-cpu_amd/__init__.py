@@ -170,6 +170,8 @@ _SIGS = {
     "q35_q4_dot4_matmul": (c_int, [P, P, P, P, c_size_t, c_size_t, c_size_t, c_size_t]),
     "q35_q4_dot4_matmul_exact": (c_int, [P, P, P, P, c_size_t, c_size_t, c_size_t, c_size_t]),
     "q35_q4_dot4_matmul_noalloc": (c_int, [P, P, P, P, c_size_t, c_size_t, c_size_t, c_size_t]),
+    "q35_q4_dot4_matmul_x1": (c_int, [P, P, P, P, c_size_t, c_size_t, c_size_t, c_size_t]),
+    "q35_q4_dot4_has_x1_tile": (c_int, [c_size_t]),
     "q35_q4_dot4_block_dots": (c_int, [P, P, P, P, c_size_t, c_size_t, c_size_t]),
     "q35_q4_dot4_argmax_batch": (c_int, [P, P, P, P, P, c_size_t, c_size_t, c_size_t, P, P]),
     "q35_gated_delta_net_update_rows": (c_int, [P, P, P, P, P, P, P, P, c_size_t, c_size_t, c_size_t,
@@ -384,6 +386,12 @@ def q4_dot4_matmul_noalloc(ctx, m, v, out, rows, count, blocks, stride):
     scratch is a fixed 16 MiB device array shared by every call on the GPU)."""
     ctx.check(lib.q35_q4_dot4_matmul_noalloc(ctx.handle, m.ptr, v.ptr, out.ptr, rows, count, blocks, stride),
               "q4_dot4_matmul_noalloc")
+
+
+def q4_dot4_matmul_x1(ctx, m, v, out, rows, count, blocks, stride):
+    """q4_dot4_matmul_x1: independently prepared X1 rows [count][blocks]."""
+    ctx.check(lib.q35_q4_dot4_matmul_x1(ctx.handle, m.ptr, v.ptr, out.ptr, rows, count, blocks, stride),
+              "q4_dot4_matmul_x1")
 
 
 def q4_dot4_block_dots(ctx, m, v, out, rows, count, blocks):

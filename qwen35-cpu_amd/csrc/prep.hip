@@ -204,19 +204,21 @@ __global__ void x4_to_a16_kernel(const q35_q8_0_block_x4 *x4, int tokens, int nb
   if (g == 0) scales[(static_cast<size_t>(tile) * nb + b) * 16 + (lane & 15)] = p;
 }
 
-__global__ void x1_to_a16_kernel(const q35_q8_0_block_x1 *x1, int nb, uint64_t *codes,
+// X1 rows [token][nb] (independently prepared vectors) -> A16.
+__global__ void x1_to_a16_kernel(const q35_q8_0_block_x1 *x1, int tokens, int nb, uint64_t *codes,
                                  float *scales) {
-  const int b = blockIdx.x, lane = threadIdx.x;
-  const int tok = lane & 15, g = lane >> 4;
+  const int b = blockIdx.x, tile = blockIdx.y, lane = threadIdx.x;
+  const int tok = tile * 16 + (lane & 15), g = lane >> 4;
   uint64_t word = 0;
   float p = 0.0F;
-  if (tok == 0) {
-    const uint8_t *q = reinterpret_cast<const uint8_t *>(x1[b].qs) + g * 8;
+  if (tok < tokens) {
+    const q35_q8_0_block_x1 &src = x1[static_cast<size_t>(tok) * nb + b];
+    const uint8_t *q = reinterpret_cast<const uint8_t *>(src.qs) + g * 8;
     for (int i = 0; i < 8; ++i) word |= static_cast<uint64_t>(q[i]) << (8 * i);
-    p = x1[b].scales[0];
+    p = src.scales[0];
   }
-  codes[static_cast<size_t>(b) * 64 + lane] = word;
-  if (g == 0) scales[static_cast<size_t>(b) * 16 + tok] = p;
+  codes[(static_cast<size_t>(tile) * nb + b) * 64 + lane] = word;
+  if (g == 0) scales[(static_cast<size_t>(tile) * nb + b) * 16 + (lane & 15)] = p;
 }
 
 }  // namespace
@@ -276,9 +278,9 @@ hipError_t launch_x4_to_a16(const q35_q8_0_block_x4 *x4, int tokens, int nb, uin
   return hipGetLastError();
 }
 
-hipError_t launch_x1_to_a16(const q35_q8_0_block_x1 *x1, int nb, uint64_t *codes,
+hipError_t launch_x1_to_a16(const q35_q8_0_block_x1 *x1, int tokens, int nb, uint64_t *codes,
                             float *scales, hipStream_t stream) {
-  Q35_LAUNCH((x1_to_a16_kernel), nb, 64, 0, stream, x1, nb, codes, scales);
+  Q35_LAUNCH((x1_to_a16_kernel), dim3(nb, (tokens + 15) / 16), 64, 0, stream, x1, tokens, nb, codes, scales);
   return hipGetLastError();
 }
 

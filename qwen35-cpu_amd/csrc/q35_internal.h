@@ -180,7 +180,7 @@ hipError_t launch_rms_prep(const RmsPrepArgs &a, hipStream_t stream);
 // Converts reference X4 blocks into the A16 layout (kernel-level matmul entry).
 hipError_t launch_x4_to_a16(const q35_q8_0_block_x4 *x4, int tokens, int nb, uint64_t *codes,
                             float *scales, hipStream_t stream);
-hipError_t launch_x1_to_a16(const q35_q8_0_block_x1 *x1, int nb, uint64_t *codes,
+hipError_t launch_x1_to_a16(const q35_q8_0_block_x1 *x1, int tokens, int nb, uint64_t *codes,
                             float *scales, hipStream_t stream);
 
 struct GemmArgs {

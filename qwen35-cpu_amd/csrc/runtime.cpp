@@ -300,7 +300,7 @@ int dot4_matmul_run(Context *ctx, const q35_q4_0_block_x8 *m, const q35_q8_0_blo
     if (x4 != nullptr)
       e = launch_x4_to_a16(x4 + (t0 / 4) * blocks, static_cast<int>(n), nb, codes, scales, ctx->stream);
     else
-      e = launch_x1_to_a16(x1 + t0 * blocks, nb, codes, scales, ctx->stream);
+      e = launch_x1_to_a16(x1 + t0 * blocks, static_cast<int>(n), nb, codes, scales, ctx->stream);
     if (e != hipSuccess) return hip_error(ctx, e, "activation layout kernel");
     GemmArgs g;
     g.w = m;
@@ -361,9 +361,9 @@ int matmul_entry(q35_context *ctx, const q35_q4_0_block_x8 *m, const q35_q8_0_bl
                  float *value, const int32_t *counts, const float *penalties) {
   int st = dot4_matmul_check(ctx, m, x4, x1, out, dots, index, rows, vectors, blocks, stride);
   if (st != Q35_OK) return st;
-  // plain outputs of more than kMaxTokens vectors: dense chunks (X4 input,
-  // so a chunk is a multiple of 16 and of 4)
-  const bool dense = out != nullptr && dots == nullptr && index == nullptr && !exact && x4 != nullptr &&
+  // plain outputs of more than kMaxTokens vectors: dense chunks (a chunk is
+  // a multiple of 16, so X4 groups never straddle two)
+  const bool dense = out != nullptr && dots == nullptr && index == nullptr && !exact &&
                      vectors > static_cast<size_t>(kMaxTokens);
   const size_t chunk = dense ? std::min<size_t>((vectors + 15) / 16 * 16, kDenseChunk) : kMaxTokens;
   void *scratch = nullptr;
@@ -383,6 +383,13 @@ extern "C" int q35_q4_dot4_matvec(q35_context *ctx, const q35_q4_0_block_x8 *mat
   return matmul_entry(ctx, matrix, nullptr, vector, output, nullptr, rows, 1, blocks, rows, false,
                       nullptr, nullptr, nullptr, nullptr);
 }
+extern "C" int q35_q4_dot4_matmul_x1(q35_context *ctx, const q35_q4_0_block_x8 *matrix,
+                                     const q35_q8_0_block_x1 *vectors, float *output, size_t rows, size_t count,
+                                     size_t blocks, size_t stride) {
+  return matmul_entry(ctx, matrix, nullptr, vectors, output, nullptr, rows, count, blocks, stride, false,
+                      nullptr, nullptr, nullptr, nullptr);
+}
+extern "C" int q35_q4_dot4_has_x1_tile(size_t count) { return count >= 1 ? 1 : 0; }
 extern "C" int q35_q4_dot4_matmul(q35_context *ctx, const q35_q4_0_block_x8 *matrix,
                                   const q35_q8_0_block_x4 *vectors, float *output, size_t rows,
                                   size_t count, size_t blocks, size_t stride) {

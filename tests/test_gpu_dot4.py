@@ -178,3 +178,29 @@ def test_dense_matches_split_launches(q, ctx, orc, rows, blocks, vectors):
                                       err_msg=f"vectors {t0}..{t0 + n}")
     want = orc.dot4_matmul(packed, act, rows, vectors, blocks)
     assert np.max(np.abs(got[:, :rows] - want)) <= 1e-5 * np.abs(want).max()
+
+
+@pytest.mark.parametrize("count", [5, 8, 70])
+def test_matmul_x1_rows(q, ctx, orc, count):
+    """q4_dot4_matmul_x1 (q4_dot4.h:15-18): independently prepared X1 rows
+    give the bits of the X4 path on the same vectors (every count, the dense
+    path above 64), and each row equals the oracle's matvec within 1e-5."""
+    rng = np.random.default_rng(4100 + count)
+    rows, cols = 520, 1024
+    packed, x = _problem(orc, rng, rows, cols, count)
+    x1 = np.stack([orc.h128_prepare_1(x[i]) for i in range(count)])
+    dm = ctx.array(packed)
+    stride = rows + 8
+    out = ctx.array(np.full((count, stride), 3.0, np.float32))
+    print(f"matmul_x1 count={count}", flush=True)
+    q.q4_dot4_matmul_x1(ctx, dm, ctx.array(x1), out, rows, count, cols // 32, stride)
+    got = out.download()
+    assert np.all(got[:, rows:] == 3.0)
+    assert q.lib.q35_q4_dot4_has_x1_tile(count) == 1
+    if count % 4 == 0:
+        ref = ctx.array(shape=(count, stride), dtype=np.float32)
+        q.q4_dot4_matmul(ctx, dm, ctx.array(orc.h128_prepare_4(x)), ref, rows, count, cols // 32, stride)
+        np.testing.assert_array_equal(got[:, :rows].view(np.uint32), ref.download()[:, :rows].view(np.uint32))
+    for i in (0, count - 1):
+        want = orc.dot4_matvec(packed, x1[i], rows, cols // 32)
+        assert np.max(np.abs(got[i, :rows] - want)) <= 1e-5 * np.abs(want).max()
