@@ -74,35 +74,80 @@ def prepare_model_dir(q, seed, weight_std, encodings="q4"):
     return d, sched, path, art
 
 
+def host_cpus(threads):
+    """The CPUs the baseline runs on: one logical CPU per physical core of the
+    process's allowed set where the topology is readable (so `threads`
+    workers land on distinct cores), then the CPU model and the counts."""
+    allowed = sorted(os.sched_getaffinity(0))
+    cores, seen = [], set()
+    for c in allowed:
+        try:
+            with open(f"/sys/devices/system/cpu/cpu{c}/topology/core_id") as f:
+                core = f.read().strip()
+            with open(f"/sys/devices/system/cpu/cpu{c}/topology/physical_package_id") as f:
+                pkg = f.read().strip()
+        except OSError:
+            core, pkg = str(c), "0"
+        if (pkg, core) not in seen:
+            seen.add((pkg, core))
+            cores.append(c)
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    use = (cores + [c for c in allowed if c not in cores])[:threads]
+    return use, model, len(allowed), len(cores)
+
+
 def cpu_baseline(model_dir, artifact, batch, prompt_len, new_tokens, threads):
     """The reference CpuEngine (oracle/_ref, built from the reference sources)
-    on a bounded sample: `batch` requests, `prompt_len`-token prompts,
-    `new_tokens` greedy outputs; decode forwards x rows / decode seconds."""
+    on the same workload as cpu_engine_bench_main.cpp:241-301: `batch`
+    requests, `prompt_len`-token prompts, `new_tokens` greedy outputs (127
+    decode forwards per request at the default 128), Q8_0Backend::auto_select;
+    decode forwards x rows / decode seconds. The process is pinned to
+    `threads` CPUs, one per physical core where possible."""
     from oracle import q35_oracle as orc  # the checker build, timed as the baseline only
 
     if not orc.ref_available():
         log("oracle/_ref not built: no CPU baseline")
         return None
     r = orc.ref()
+    cpus, cpu_model, allowed, physical = host_cpus(threads)
+    threads = len(cpus)
+    before = os.sched_getaffinity(0)
+    os.sched_setaffinity(0, cpus)
+    isa = r.ref_backend_name(0).decode()
     rng = np.random.default_rng(4242)
     prompts = rng.integers(0, CONFIG_08B["text_config"]["vocab_size"], size=(batch, prompt_len)).astype(np.int32)
     out = np.zeros((batch, new_tokens), np.int32)
     ms = ctypes.c_double()
     err = ctypes.create_string_buffer(512)
     t = time.time()
-    rc = r.ref_engine_greedy(os.fsencode(model_dir), os.fsencode(artifact), threads, 0, prompts.ctypes.data,
-                             prompt_len, batch, new_tokens, 1.0, None, out.ctypes.data, None, None, ctypes.byref(ms),
-                             err, 512)
+    try:
+        rc = r.ref_engine_greedy(os.fsencode(model_dir), os.fsencode(artifact), threads, 0, prompts.ctypes.data,
+                                 prompt_len, batch, new_tokens, 1.0, None, out.ctypes.data, None, None,
+                                 ctypes.byref(ms), err, 512)
+    finally:
+        os.sched_setaffinity(0, before)
     if rc != 0:
         log(f"reference engine failed: {err.value.decode(errors='replace')}")
         return None
     forwards = new_tokens - 1  # the first output token comes out of prefill
     value = batch * forwards * 1000.0 / ms.value
-    log(f"reference CPU engine: {value:.1f} tok/s decode on {threads} threads ({time.time() - t:.1f}s wall)")
+    log(f"reference CPU engine: {value:.1f} tok/s decode on {threads} threads pinned to CPUs {cpus} "
+        f"({cpu_model}, {isa}; {physical} physical cores / {allowed} CPUs allowed) ({time.time() - t:.1f}s wall)")
     return {"value": round(value, 2), "unit": "tokens/s", "cores": threads, "kind": "reference",
+            "cpu_model": cpu_model, "isa": isa, "threads": threads, "pinned_cpus": cpus,
+            "allowed_cpus": allowed, "physical_cores_allowed": physical,
             "sample": f"{batch} requests x {prompt_len}-token random prompts, {new_tokens} greedy tokens each; "
                       f"{forwards} decode forwards per request timed through CpuEngine::advance_batch on the "
-                      f"same random-init 0.8B artifact"}
+                      f"same random-init 0.8B artifact (cpu_engine_bench_main.cpp:241-301 workload), "
+                      f"Q8_0Backend::auto_select -> {isa}, one thread per physical core of the box's CPU share"}
 
 
 def run_mixed4b(args, q, ctx):
@@ -456,8 +501,9 @@ def main():
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--profile-steps", type=int, default=16, help="decode forwards in the profiled region")
     ap.add_argument("--cpu-baseline", choices=("on", "off"), default="on")
-    ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, cpus)")
-    ap.add_argument("--cpu-tokens", type=int, default=32, help="greedy tokens per request in the CPU sample")
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="0 = one per physical core of the allowed CPUs, at most 16 (the box's CPU share)")
+    ap.add_argument("--cpu-tokens", type=int, default=128, help="greedy tokens per request in the CPU sample")
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--prefill-chunk", type=int, default=2048, help="mixed4b: prompt positions per packed step")
     ap.add_argument("--calibration-copy-mb", type=int, default=0,
@@ -561,26 +607,32 @@ def main():
     head_name = ("head_kernel<4, 3, NT, true, *> (greedy head: streaming Q4 GEMV + penalty + argmax, NT token tiles)"
                  if not sfx else "head_kernel<4, 2, NT, true, *, true> (greedy G16 head: Q4G16Tile GEMV, per-half "
                  "MFMA dots + penalty + argmax)")
-    roof = roofline("head" + sfx, prof["head"], traffic, head_name) if prof else None
-    gemm_roof = roofline("gemm" + sfx, prof["gemm"], traffic, "gemm_kernel<8, false, false> (per-layer Q4 projections, split-K)") if prof else None
+    head_roof = roofline("head" + sfx, prof["head"], traffic, head_name) if prof else None
+    # the dominant kernel class: the per-layer Q4 projections (split-K
+    # single-token-tile launches at B <= 16)
+    roof = roofline("gemm" + sfx, prof["gemm"], traffic,
+                    "gemm_rows_kernel<KS, RM> (per-layer Q4 projections: in, out, gate_up, down; split-K)") \
+        if prof else None
     breakdown = ({k: {"us_per_step": round(v[0] / args.profile_steps * 1000.0, 1),
                       "launches_per_step": v[1] // args.profile_steps} for k, v in prof.items() if v[1]}
                  if prof else None)
 
     base = None
     if args.cpu_baseline == "on":
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        threads = args.cpu_threads or min(16, host_cpus(1 << 20)[3] or 1)
         base = cpu_baseline(model_dir, artifact, args.batch, args.prompt, args.cpu_tokens, threads)
 
     line = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(elapsed * 1000 / args.steps, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "q4xi8->i32 (projections), f32 (DeltaNet, attention)",
-        "data": "synthetic: random-init weights N(0,0.02) packed to Q4-G32-DOT4 H128, random-token prompts",
+        "data": "synthetic: random-init weights N(0,0.02) packed to Q4-G32-DOT4 H128, random-token prompts" +
+                ("" if args.encodings == "q4" else
+                 "; tied head/embedding as Q4G16Tile (G16), linear_attn.in_proj_ba gate rows as Q8_0"),
         "config": {"workload": "random-init Qwen3.5-0.8B-shaped hybrid, batched greedy decode",
                    "batch": args.batch, "prompt_tokens": args.prompt, "encodings": args.encodings,
                    "decode_forwards_timed": args.steps, "graphs": args.graphs == "on"},
-        "roofline": roof, "q4_projection_roofline": gemm_roof, "step_kernel_breakdown": breakdown,
+        "roofline": roof, "head_roofline": head_roof, "step_kernel_breakdown": breakdown,
         "cpu_baseline": base,
     }
     if base:

@@ -152,6 +152,11 @@ int gemm_dense_splits(int rows, int nb, int cu_count, int max_split) {
   return gemm_plan(rows, nb, false, false, cu_count, 0, 0, max_split > 0 ? max_split : 32).split;
 }
 
+bool gemm_dense_fits(int rows, int tokens, int cu_count) {
+  const long long waves = static_cast<long long>((rows / 8 + 7) / 8) * ((tokens + 31) / 32);
+  return tokens > kMaxTokens && waves >= 2LL * (cu_count > 0 ? cu_count : 256);
+}
+
 hipError_t launch_gemm_dense(const GemmArgs &a, hipStream_t stream) {
   if (a.tokens <= 0 || a.rows <= 0) return hipSuccess;
   if (a.out == nullptr || a.rows % 8 != 0 || a.stride < a.rows || a.residual != nullptr) return hipErrorInvalidValue;

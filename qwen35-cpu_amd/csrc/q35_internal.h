@@ -237,6 +237,10 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t stream);
 // no partials. K splits it reproduces:
 int gemm_dense_splits(int rows, int nb, int cu_count, int max_split);
 hipError_t launch_gemm_dense(const GemmArgs &a, hipStream_t stream);
+// Whether the dense GEMM fills the GPU for `rows` x `tokens` (at least two
+// wavefronts per CU, and more tokens than one split launch takes); the split
+// launches give the same bits, so the step picks by speed alone.
+bool gemm_dense_fits(int rows, int tokens, int cu_count);
 // Tokens per launch of the kernel-level dense path.
 constexpr int kDenseChunk = 4096;
 

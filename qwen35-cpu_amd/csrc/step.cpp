@@ -403,9 +403,8 @@ extern "C" int q35_runtime_create(q35_model *m, const q35_runtime_config *cfg, q
   rt->max_rows = std::max(cfg->max_batch, cfg->max_step_rows);
   rt->max_segments = cfg->max_batch + kMaxPrefillSegments;
   Context *ctx = m->ctx;
-  // R rows of a packed step, M segments (and head rows); a split GEMM runs
-  // up to kMaxTokens rows, the dense GEMM (no partials) anything larger
-  const int R = rt->max_rows, M = rt->max_segments, Bs = std::min(R, kMaxTokens);
+  // R rows of a packed step, M segments (and head rows)
+  const int R = rt->max_rows, M = rt->max_segments;
   const size_t H = d.hidden, I = d.intermediate;
   const size_t v_dim = static_cast<size_t>(d.lin_v_heads) * d.lin_v_dim;
   const size_t q_dim = static_cast<size_t>(d.lin_k_heads) * d.lin_k_dim;
@@ -441,19 +440,19 @@ extern "C" int q35_runtime_create(q35_model *m, const q35_runtime_config *cfg, q
   alloc(static_cast<size_t>(R) * H * 4, reinterpret_cast<void **>(&rt->x[0]));
   alloc(static_cast<size_t>(R) * H * 4, reinterpret_cast<void **>(&rt->x[1]));
   // GEMM outputs: [split][rows][width] for the largest split plan of any
-  // projection (split launches, up to kMaxTokens rows), [rows][width] for
-  // the dense GEMM
+  // projection at any row count a step can have (split launches), and
+  // [rows][width] for the dense GEMM
   size_t proj_floats = static_cast<size_t>(R) * rt->proj_width;
   for (const auto &L : m->layers) {
-    proj_floats = std::max(proj_floats, gemm_partial_floats(L.in_rows, d.hidden / 32, Bs, ctx->cu_count));
-    proj_floats = std::max(proj_floats, gemm_partial_floats(d.hidden, L.out_cols / 32, Bs, ctx->cu_count));
-    proj_floats = std::max(proj_floats, gemm_partial_floats(2 * d.intermediate, d.hidden / 32, Bs, ctx->cu_count));
-    proj_floats = std::max(proj_floats, gemm_partial_floats(d.hidden, d.intermediate / 32, Bs, ctx->cu_count));
+    proj_floats = std::max(proj_floats, gemm_partial_floats(L.in_rows, d.hidden / 32, R, ctx->cu_count));
+    proj_floats = std::max(proj_floats, gemm_partial_floats(d.hidden, L.out_cols / 32, R, ctx->cu_count));
+    proj_floats = std::max(proj_floats, gemm_partial_floats(2 * d.intermediate, d.hidden / 32, R, ctx->cu_count));
+    proj_floats = std::max(proj_floats, gemm_partial_floats(d.hidden, d.intermediate / 32, R, ctx->cu_count));
   }
   alloc(proj_floats * 4, reinterpret_cast<void **>(&rt->proj));
   // chunked steps of split GEMMs: the in projection's split partials summed
   // once, [rows][width]
-  alloc(static_cast<size_t>(Bs) * rt->proj_width * 4, reinterpret_cast<void **>(&rt->rows_final));
+  alloc(static_cast<size_t>(R) * rt->proj_width * 4, reinterpret_cast<void **>(&rt->rows_final));
   alloc(static_cast<size_t>(R) * kMaxGateRows * 4, reinterpret_cast<void **>(&rt->q8_gates));
   if (d.lin_v_heads > 0)
     alloc(delta_chunk_scan_floats(R, d.lin_v_heads) * 4, reinterpret_cast<void **>(&rt->delta_scan));
@@ -765,7 +764,7 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
   // attention prep, the SiLU prep) get GEMMs split at most that many ways.
   constexpr int kConsumerSplits = 8;
   auto gemm = [&](const q35_q4_0_block_x8 *w, int rows, int K, int max_split = 32) -> hipError_t {
-    if (batch > kMaxTokens) {
+    if (gemm_dense_fits(rows, batch, ctx->cu_count)) {
       // the dense GEMM: finished rows with the split launch's bits
       GemmArgs g;
       g.w = w;
@@ -837,7 +836,7 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
     return B * (H * 4.0 + (add ? pending.splits * H * 4.0 + H * 4.0 : 0.0) + H + H / 32.0 * 4.0) + H * 4.0;
   };
   auto gemm_bytes = [&](int rows, int K, int max_split = 32) {
-    if (batch > kMaxTokens) return gemm_algorithmic_bytes(rows, K / 32, batch, true, false);
+    if (gemm_dense_fits(rows, batch, ctx->cu_count)) return gemm_algorithmic_bytes(rows, K / 32, batch, true, false);
     const GemmPlan p = gemm_plan(rows, K / 32, false, false, ctx->cu_count, 0, 0, max_split);
     return gemm_algorithmic_bytes(rows, K / 32, batch, true, false) + (p.split - 1) * B * rows * 4.0;
   };
