@@ -153,7 +153,7 @@ int gemm_dense_splits(int rows, int nb, int cu_count, int max_split) {
 }
 
 bool gemm_dense_fits(int rows, int tokens, int cu_count) {
-  const long long waves = static_cast<long long>((rows / 8 + 7) / 8) * ((tokens + 31) / 32);
+  const long long waves = static_cast<long long>((rows / 8 + 7) / 8) * ((tokens + 31) / 32);  // two-tile units
   return tokens > kMaxTokens && waves >= 2LL * (cu_count > 0 ? cu_count : 256);
 }
 
@@ -161,15 +161,20 @@ hipError_t launch_gemm_dense(const GemmArgs &a, hipStream_t stream) {
   if (a.tokens <= 0 || a.rows <= 0) return hipSuccess;
   if (a.out == nullptr || a.rows % 8 != 0 || a.stride < a.rows || a.residual != nullptr) return hipErrorInvalidValue;
   // two token tiles per wavefront with the next block's loads in flight (145
-  // VGPRs, three wavefronts per SIMD): measured ahead of four tiles (two per
-  // SIMD) and of the unprefetched forms at the 4B projection shapes
-  constexpr int kNT = 2;
+  // VGPRs, three wavefronts per SIMD) measured ahead of the unprefetched forms
+  // at the 4B projection shapes; four tiles (two wavefronts per SIMD, half the
+  // unpacking per token) win only on tall matrices (4B gate_up: 444 against
+  // 478 us at 2048 tokens; narrow outputs lose 20%)
+  const int nt = a.rows >= 16384 ? 4 : 2;
   const int S = gemm_dense_splits(a.rows, a.nb, a.cu_count, a.max_split);
   const int groups = (a.rows / 8 + 7) / 8;
-  const int token_groups = (a.tokens + 16 * kNT - 1) / (16 * kNT);
+  const int token_groups = (a.tokens + 16 * nt - 1) / (16 * nt);
   const int units = groups * token_groups;
   const int wgs = ((units + 3) / 4 + 7) / 8 * 8;
-  Q35_LAUNCH((gemm_dense_kernel<kNT, true>), dim3(wgs), dim3(256), 0, stream, a, S, token_groups, units);
+  if (nt == 4)
+    Q35_LAUNCH((gemm_dense_kernel<4, true>), dim3(wgs), dim3(256), 0, stream, a, S, token_groups, units);
+  else
+    Q35_LAUNCH((gemm_dense_kernel<2, true>), dim3(wgs), dim3(256), 0, stream, a, S, token_groups, units);
   return hipGetLastError();
 }
 

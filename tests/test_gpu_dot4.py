@@ -154,12 +154,14 @@ def test_argmax_head_shapes(q, ctx, orc, rows, cols, vectors):
     np.testing.assert_array_equal(val.download(), adj[np.arange(vectors), want])
 
 
-@pytest.mark.parametrize("rows,blocks,vectors", [(2560, 288, 300), (3584, 32, 512), (200, 112, 132), (1032, 80, 68)])
+@pytest.mark.parametrize("rows,blocks,vectors", [(2560, 288, 300), (3584, 32, 512), (200, 112, 132), (1032, 80, 68),
+                                                  (16392, 40, 100)])
 def test_dense_matches_split_launches(q, ctx, orc, rows, blocks, vectors):
     """Above 64 vectors q4_dot4_matmul runs the dense GEMM (every K block of a
     64-row group in one wavefront, the split structure folded in registers);
     its rows must equal the 64-vector split launches bit for bit, here with
-    32, 4 and 14 K splits, a ragged row group and ragged token groups."""
+    32, 4 and 14 K splits, a ragged row group and ragged token groups; 16392
+    rows run the four-tile form of tall matrices."""
     rng = np.random.default_rng(rows + vectors)
     packed, x = _problem(orc, rng, rows, blocks * 32, vectors)
     act = orc.h128_prepare_4(x)
