@@ -69,8 +69,9 @@ extern "C" int q35_q4_dot4_matmul_noalloc(q35_context *ctx, const q35_q4_0_block
     if (ctx->device >= 0 && ctx->device < kMaxDevices) ptr = g_static_ptr[ctx->device];
   }
   if (ptr == nullptr) return set_error(ctx, Q35_ERR_HIP, "static scratch not resolved for this device");
-  size_t chunk = 0;
-  for (size_t c = kMaxTokens; c >= 16; c -= 16) {
+  // one to four vectors run the single-launch GEMV, which needs no scratch
+  size_t chunk = vectors_count <= static_cast<size_t>(kMatvecMaxVectors) ? kMaxTokens : 0;
+  for (size_t c = kMaxTokens; chunk == 0 && c >= 16; c -= 16) {
     if (dot4_matmul_scratch_bytes(static_cast<int>(rows), static_cast<int>(blocks), static_cast<int>(c), false,
                                   ctx->cu_count) <= kStaticScratchBytes) {
       chunk = c;

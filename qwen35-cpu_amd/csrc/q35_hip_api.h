@@ -7,15 +7,32 @@
 #ifdef Q35_HOST_EMULATION
 #include "q35_host_emulation.h"
 #else
+#include <hip/hip_ext.h>
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
-#define Q35_LAUNCH(kernel, grid, block, smem, stream, ...) \
-  hipLaunchKernelGGL(kernel, grid, block, smem, stream, __VA_ARGS__)
+namespace q35 {
+// Profiling hook of the launch macro: while a profiled step is enqueued it
+// returns true with a fresh event pair, which the launch records its own
+// dispatch start and end into (hipExtLaunchKernelGGL), so the pair brackets
+// the kernel's execution and nothing else. Otherwise it returns false.
+bool launch_events(hipEvent_t *start, hipEvent_t *stop);
+}  // namespace q35
+
+#define Q35_LAUNCH(kernel, grid, block, smem, stream, ...)                                        \
+  do {                                                                                            \
+    hipEvent_t q35_ev0_ = nullptr, q35_ev1_ = nullptr;                                            \
+    if (::q35::launch_events(&q35_ev0_, &q35_ev1_))                                               \
+      hipExtLaunchKernelGGL(kernel, grid, block, smem, stream, q35_ev0_, q35_ev1_, 0, __VA_ARGS__); \
+    else                                                                                          \
+      hipLaunchKernelGGL(kernel, grid, block, smem, stream, __VA_ARGS__);                         \
+  } while (0)
 #define Q35_V4I int __attribute__((ext_vector_type(4)))
 #define Q35_MFMA_I32_16X16X32_I8(a, b, c, cbsz, abid, blgp) \
   __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, cbsz, abid, blgp)
 #define Q35_DYNAMIC_SHARED(type, name) extern __shared__ type name[]
+// four int8 products of a and b (byte-wise, signed) added to c: v_dot4_i32_i8
+#define Q35_SDOT4(a, b, c) __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), (c), false)
 // Streaming loads of data read once per step (weights, recurrent state, KV):
 // marked non-temporal so they do not displace reused lines in L1/L2.
 typedef unsigned int q35_u32x4 __attribute__((ext_vector_type(4)));

@@ -237,6 +237,12 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t stream);
 // no partials. K splits it reproduces:
 int gemm_dense_splits(int rows, int nb, int cu_count, int max_split);
 hipError_t launch_gemm_dense(const GemmArgs &a, hipStream_t stream);
+// Single-launch GEMV of 1..kMatvecMaxVectors vectors in X1 blocks ([count][nb])
+// or one X4 group (count 4): each output is the block-order fma chain, so the
+// rows are bit-exact; out[v * stride + row]. rows % 8 == 0.
+constexpr int kMatvecMaxVectors = 4;
+hipError_t launch_dot4_matvec(const q35_q4_0_block_x8 *w, const void *act, bool x4, int count, int rows, int nb,
+                              float *out, long long stride, hipStream_t stream);
 // Whether the dense GEMM fills the GPU for `rows` x `tokens` (at least two
 // wavefronts per CU, and more tokens than one split launch takes); the split
 // launches give the same bits, so the step picks by speed alone.

@@ -282,6 +282,14 @@ int dot4_matmul_run(Context *ctx, const q35_q4_0_block_x8 *m, const q35_q8_0_blo
                     size_t blocks, size_t stride, bool exact, int32_t *index, float *value, const int32_t *counts,
                     const float *penalties, void *scratch, size_t chunk) {
   const int nb = static_cast<int>(blocks);
+  if (out != nullptr && dots == nullptr && index == nullptr && !exact && vectors <= kMatvecMaxVectors) {
+    // one to four vectors: the single-launch dot4 GEMV (bit-exact chains)
+    const hipError_t e = launch_dot4_matvec(m, x4 != nullptr ? static_cast<const void *>(x4) : x1, x4 != nullptr,
+                                            static_cast<int>(vectors), static_cast<int>(rows), nb, out,
+                                            static_cast<long long>(stride), ctx->stream);
+    if (e != hipSuccess) return hip_error(ctx, e, "dot4 GEMV kernel");
+    return Q35_OK;
+  }
   const size_t tiles = (chunk + 15) / 16;
   const size_t code_bytes = align256(tiles * 64 * static_cast<size_t>(nb) * sizeof(uint64_t));
   const size_t scale_bytes = align256(tiles * 16 * static_cast<size_t>(nb) * sizeof(float));
@@ -367,6 +375,10 @@ int matmul_entry(q35_context *ctx, const q35_q4_0_block_x8 *m, const q35_q8_0_bl
                      vectors > static_cast<size_t>(kMaxTokens);
   const size_t chunk = dense ? std::min<size_t>((vectors + 15) / 16 * 16, kDenseChunk) : kMaxTokens;
   void *scratch = nullptr;
+  // one to four plain outputs: the single-launch GEMV, no scratch
+  if (out != nullptr && dots == nullptr && index == nullptr && !exact && vectors <= kMatvecMaxVectors)
+    return dot4_matmul_run(ctx, m, x4, x1, out, dots, rows, vectors, blocks, stride, exact, index, value, counts,
+                           penalties, nullptr, chunk);
   st = scratch_get(ctx,
                    dot4_matmul_scratch_bytes(static_cast<int>(rows), static_cast<int>(blocks), static_cast<int>(chunk),
                                              index != nullptr, ctx->cu_count),

@@ -114,7 +114,12 @@ struct q35_runtime {
   // of each bracketed launch of the step in flight, and per-class totals
   bool profiling = false;
   std::vector<std::pair<hipEvent_t, hipEvent_t>> prof_events;
-  std::vector<std::pair<int, double>> prof_pending;
+  struct ProfLaunch {
+    int cls;       // kernel class
+    double bytes;  // algorithmic bytes (on the first kernel of a logical launch)
+    bool counted;  // first kernel of a logical launch
+  };
+  std::vector<ProfLaunch> prof_pending;
   // stage trace (test hook): (layer, point) -> device copy and its size
   bool tracing = false;
   std::map<std::pair<int, int>, std::pair<void *, size_t>> trace;

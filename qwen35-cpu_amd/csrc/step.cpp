@@ -609,43 +609,53 @@ double gemm_algorithmic_bytes(int rows, int nb, int tokens, bool stores, bool re
 
 namespace {
 
-// Starts a bracketed launch: records the start event of the next free pair on
-// `s` and remembers the launch's class and algorithmic bytes; *stop receives
-// the event to record after the launch.
-hipError_t profile_begin(q35_runtime *rt, hipStream_t s, int cls, double bytes, hipEvent_t *stop) {
-  const size_t i = rt->prof_pending.size();
-  if (i == rt->prof_events.size()) {
-    hipEvent_t a = nullptr, b = nullptr;
-    hipError_t e = hipEventCreate(&a);
-    if (e != hipSuccess) return e;
-    e = hipEventCreate(&b);
-    if (e != hipSuccess) {
-      (void)hipEventDestroy(a);
-      return e;
-    }
-    rt->prof_events.emplace_back(a, b);
-  }
-  rt->prof_pending.emplace_back(cls, bytes);
-  *stop = rt->prof_events[i].second;
-  return hipEventRecord(rt->prof_events[i].first, s);
-}
+// The logical launch being enqueued under profiling: its class and bytes go to
+// the first kernel it dispatches, every kernel gets its own event pair.
+struct ProfScope {
+  q35_runtime *rt;
+  int cls;
+  double bytes;
+  bool first;
+};
+thread_local ProfScope *t_prof = nullptr;
 
-// After the step's stream synchronisation: fold the bracketed launches into
-// the per-class totals.
+// After the step's stream synchronisation: fold the bracketed kernels into the
+// per-class totals (durations of every kernel, one launch per logical launch).
 int profile_collect(q35_runtime *rt) {
   for (size_t i = 0; i < rt->prof_pending.size(); ++i) {
     float ms = 0;
     Q35_HIP_TRY(rt->ctx, hipEventElapsedTime(&ms, rt->prof_events[i].first, rt->prof_events[i].second));
-    const int cls = rt->prof_pending[i].first;
-    rt->prof_ms[cls] += ms;
-    rt->prof_bytes[cls] += rt->prof_pending[i].second;
-    rt->prof_launches[cls] += 1;
+    const auto &p = rt->prof_pending[i];
+    rt->prof_ms[p.cls] += ms;
+    rt->prof_bytes[p.cls] += p.bytes;
+    rt->prof_launches[p.cls] += p.counted ? 1 : 0;
   }
   rt->prof_pending.clear();
   return Q35_OK;
 }
 
 }  // namespace
+
+bool launch_events(hipEvent_t *start, hipEvent_t *stop) {
+  ProfScope *p = t_prof;
+  if (p == nullptr) return false;
+  q35_runtime *rt = p->rt;
+  const size_t i = rt->prof_pending.size();
+  if (i == rt->prof_events.size()) {
+    hipEvent_t a = nullptr, b = nullptr;
+    if (hipEventCreate(&a) != hipSuccess) return false;
+    if (hipEventCreate(&b) != hipSuccess) {
+      (void)hipEventDestroy(a);
+      return false;
+    }
+    rt->prof_events.emplace_back(a, b);
+  }
+  rt->prof_pending.push_back({p->cls, p->first ? p->bytes : 0.0, p->first});
+  p->first = false;
+  *start = rt->prof_events[i].first;
+  *stop = rt->prof_events[i].second;
+  return true;
+}
 
 // Enqueues one decode step for `batch` rows whose metadata is already in
 // rt->meta_host; the host copy is part of the enqueued work so the whole
@@ -731,14 +741,16 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
     e = (expr);                                            \
     if (e != hipSuccess) return hip_error(ctx, e, what);   \
   } while (0)
-  // A kernel launch; with profiling on it is bracketed by an event pair and
-  // counted under `cls` with `bytes` algorithmic HBM bytes.
+  // A logical launch (one or more kernels); with profiling on each kernel
+  // records its own start and end events and the launch is counted under
+  // `cls` with `bytes` algorithmic HBM bytes.
 #define Q35_KERNEL(cls, bytes, expr, what)                                     \
   do {                                                                         \
-    hipEvent_t q35_stop_ = nullptr;                                            \
-    if (rt->profiling) Q35_STEP(profile_begin(rt, s, (cls), (bytes), &q35_stop_), "profile event"); \
-    Q35_STEP(expr, what);                                                      \
-    if (q35_stop_ != nullptr) Q35_STEP(hipEventRecord(q35_stop_, s), "profile event"); \
+    ProfScope q35_scope_{rt, (cls), (bytes), true};                            \
+    if (rt->profiling) t_prof = &q35_scope_;                                   \
+    e = (expr);                                                                \
+    t_prof = nullptr;                                                          \
+    if (e != hipSuccess) return hip_error(ctx, e, what);                       \
   } while (0)
   const double B = batch;
   const auto *host_seq = reinterpret_cast<const int32_t *>(rt->meta_host + ml.seq_lens);

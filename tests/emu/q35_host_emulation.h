@@ -255,6 +255,12 @@ typedef unsigned int q35_u32x2 __attribute__((vector_size(8)));
 typedef float q35_f32x4 __attribute__((vector_size(16)));
 typedef float q35_f32x2 __attribute__((vector_size(8)));
 #define Q35_LOAD_NT(ptr) (*(ptr))
+inline int q35emu_sdot4(uint32_t a, uint32_t b, int c) {
+  for (int i = 0; i < 4; ++i)
+    c += static_cast<int>(static_cast<int8_t>(a >> (8 * i))) * static_cast<int>(static_cast<int8_t>(b >> (8 * i)));
+  return c;
+}
+#define Q35_SDOT4(a, b, c) q35emu_sdot4(static_cast<uint32_t>(a), static_cast<uint32_t>(b), (c))
 inline void lds_barrier() { __syncthreads(); }
 inline void q35_compiler_fence() { asm volatile("" ::: "memory"); }
 inline void q35_materialize(float &) {}
@@ -296,6 +302,12 @@ inline hipError_t hipGetDeviceProperties(hipDeviceProp_t *p, int) {
 inline hipError_t hipStreamCreateWithFlags(hipStream_t *s, unsigned) { *s = new int(0); return hipSuccess; }
 inline hipError_t hipStreamDestroy(hipStream_t s) { delete static_cast<int *>(s); return hipSuccess; }
 inline hipError_t hipStreamSynchronize(hipStream_t) { return hipSuccess; }
+// a __device__ array is a host array here: its symbol address is the array
+#define HIP_SYMBOL(x) (&(x))
+inline hipError_t hipGetSymbolAddress(void **p, const void *symbol) {
+  *p = const_cast<void *>(symbol);
+  return hipSuccess;
+}
 inline hipError_t hipEventCreate(hipEvent_t *e) { *e = new q35emu_event(); return hipSuccess; }
 inline hipError_t hipEventDestroy(hipEvent_t e) { delete e; return hipSuccess; }
 inline hipError_t hipEventRecord(hipEvent_t e, hipStream_t) { e->t = std::chrono::steady_clock::now(); return hipSuccess; }

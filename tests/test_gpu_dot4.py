@@ -53,7 +53,40 @@ def test_config1_matvec_b1(q, ctx, orc):
     print("config1 matvec B=1", flush=True)
     q.q4_dot4_matvec(ctx, dm, da, out, rows, cols // 32)
     got = out.download()
-    assert np.max(np.abs(got - want)) <= 1e-5 * np.abs(want).max()
+    # the single-launch dot4 GEMV runs the reference's chain: bit-exact
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,blocks,count", [(8, 1, 1), (200, 112, 2), (3584, 32, 3), (1032, 288, 4),
+                                               (64, 129, 1), (2560, 80, 4)])
+def test_small_count_gemv_exact(q, ctx, orc, rows, blocks, count):
+    """One to four vectors run the single-launch dot4 GEMV: X1 rows
+    (matvec, matmul_x1) and an X4 group (matmul, 4 vectors) give the oracle's
+    block-order chain (q4_dot4.cpp:43-56) bit for bit, over one and several
+    128-block passes and a ragged last pass; outputs beyond `rows` in the
+    strided layout stay untouched."""
+    rng = np.random.default_rng(rows * 7 + blocks + count)
+    packed, x = _problem(orc, rng, rows, blocks * 32, count)
+    x1 = np.stack([orc.q8_quantize_1(x[i]) for i in range(count)])
+    want = np.stack([orc.dot4_matvec(packed, x1[i], rows, blocks) for i in range(count)])
+    dm = ctx.array(packed)
+    stride = rows + 3
+    out = ctx.array(np.full((count, stride), 7.0, np.float32))
+    print(f"small-count GEMV rows={rows} blocks={blocks} count={count}", flush=True)
+    q.q4_dot4_matmul_x1(ctx, dm, ctx.array(x1), out, rows, count, blocks, stride)
+    got = out.download()
+    assert np.all(got[:, rows:] == 7.0)
+    np.testing.assert_array_equal(got[:, :rows].view(np.uint32), want.view(np.uint32))
+    if count == 1:
+        one = ctx.array(shape=(rows,), dtype=np.float32)
+        q.q4_dot4_matvec(ctx, dm, ctx.array(x1[0]), one, rows, blocks)
+        np.testing.assert_array_equal(one.download().view(np.uint32), want[0].view(np.uint32))
+    if count == 4:
+        act = orc.h128_prepare_4(x)
+        want4 = orc.dot4_matmul(packed, act, rows, 4, blocks)
+        out4 = ctx.array(shape=(4, stride), dtype=np.float32)
+        q.q4_dot4_matmul(ctx, dm, ctx.array(act), out4, rows, 4, blocks, stride)
+        np.testing.assert_array_equal(out4.download()[:, :rows].view(np.uint32), want4.view(np.uint32))
 
 
 @pytest.mark.parametrize("rows,blocks,vectors,stride", [(8, 1, 4, 8), (24, 3, 8, 31), (200, 112, 12, 207),
@@ -174,9 +207,14 @@ def test_dense_matches_split_launches(q, ctx, orc, rows, blocks, vectors):
     assert np.all(got[:, rows:] == -5.0)
     for t0 in range(0, vectors, 64):
         n = min(64, vectors - t0)
-        part = ctx.array(shape=(n, stride), dtype=np.float32)
-        q.q4_dot4_matmul(ctx, dm, ctx.array(act[t0 // 4:(t0 + n) // 4]), part, rows, n, blocks, stride)
-        np.testing.assert_array_equal(got[t0:t0 + n, :rows].view(np.uint32), part.download()[:, :rows].view(np.uint32),
+        # up to four vectors would run the GEMV's single chains: launch eight
+        # (the group twice) and keep the first rows, which are batch-invariant
+        sub = act[t0 // 4:(t0 + n) // 4]
+        n_run = 8 if n <= 4 else n
+        part = ctx.array(shape=(n_run, stride), dtype=np.float32)
+        q.q4_dot4_matmul(ctx, dm, ctx.array(np.concatenate([sub, sub]) if n <= 4 else sub), part, rows, n_run,
+                         blocks, stride)
+        np.testing.assert_array_equal(got[t0:t0 + n, :rows].view(np.uint32), part.download()[:n, :rows].view(np.uint32),
                                       err_msg=f"vectors {t0}..{t0 + n}")
     want = orc.dot4_matmul(packed, act, rows, vectors, blocks)
     assert np.max(np.abs(got[:, :rows] - want)) <= 1e-5 * np.abs(want).max()

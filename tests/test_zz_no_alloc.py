@@ -23,8 +23,9 @@ def _call(q, ctx, fn, dm, da, out, rows, vectors, blocks, stride):
 
 
 # (rows, blocks, vectors, stride): a 4B down projection shape (K split 32 ways,
-# 48-token chunks), then a smaller one with a ragged token count and padding
-SHAPES = [(2560, 288, 132, 2560), (1032, 40, 20, 1039)]
+# 48-token chunks), then a smaller one with a ragged token count and padding,
+# then four vectors (the GEMV, no scratch)
+SHAPES = [(2560, 288, 132, 2560), (1032, 40, 20, 1039), (520, 36, 4, 523)]
 
 
 def test_two_calls_match_allocating_entry_point(q, ctx, orc):
@@ -53,9 +54,10 @@ def test_limits_and_errors(q, ctx, orc):
     out = ctx.array(np.full((4, 64), 5.0, np.float32))
     fn = q.lib.q35_q4_dot4_matmul_noalloc
     print("noalloc: rejected shapes", flush=True)
-    # 16384 rows x 288 blocks: 32 K splits x 16 tokens x 16384 rows of FP32
-    # partials (32 MiB) exceed the array; rejected before any launch
-    assert _call(q, ctx, fn, dm, da, out, 16384, 4, 288, 16384) == 5  # Q35_ERR_UNSUPPORTED
+    # 16384 rows x 288 blocks at 8 vectors: 32 K splits x 16 tokens x 16384
+    # rows of FP32 partials (32 MiB) exceed the array; rejected before any
+    # launch (up to 4 vectors run the GEMV, which uses no scratch)
+    assert _call(q, ctx, fn, dm, da, out, 16384, 8, 288, 16384) == 5  # Q35_ERR_UNSUPPORTED
     assert b"static scratch" in q.lib.q35_context_last_error(ctx.handle)
     assert _call(q, ctx, fn, dm, da, out, 64, 6, 4, 64) == 1  # vector count % 4
     assert _call(q, ctx, fn, dm, da, out, 60, 4, 4, 64) == 1  # rows % 8
