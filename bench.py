@@ -121,7 +121,7 @@ def cpu_baseline(model_dir, artifact, batch, prompt_len, new_tokens, threads):
     threads = len(cpus)
     before = os.sched_getaffinity(0)
     os.sched_setaffinity(0, cpus)
-    isa = r.ref_backend_name(0).decode()
+    isa = r.ref_backend_name(r.ref_backend_resolve(0)).decode()  # auto_select resolved on this host
     rng = np.random.default_rng(4242)
     prompts = rng.integers(0, CONFIG_08B["text_config"]["vocab_size"], size=(batch, prompt_len)).astype(np.int32)
     out = np.zeros((batch, new_tokens), np.int32)

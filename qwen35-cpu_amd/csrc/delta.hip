@@ -369,7 +369,7 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_chunk_inputs_kernel(Delta
 // chain of a token is 8 columns long and the scan has a wavefront per SIMD at
 // the 4B shapes. A token's q and k go through LDS (one float4 per lane); the
 // next kDeltaScanAhead tokens' loads are in flight while a token is computed.
-constexpr int kDeltaScanAhead = 4;
+constexpr int kDeltaScanAhead = 16;
 constexpr int kDeltaScanRows = 64 / kRowLanes;
 
 struct ScanToken {
@@ -379,8 +379,17 @@ struct ScanToken {
 
 __global__ __launch_bounds__(64) void delta_scan_kernel(DeltaArgs a) {
   __shared__ q35_f32x4 qk_lds[2][2 * kDim / 4];
-  const int lane = threadIdx.x, vh = blockIdx.y;
-  const int col = lane & (kRowLanes - 1), row = kDeltaScanRows * blockIdx.x + (lane >> 4);
+  const int lane = threadIdx.x;
+  // workgroup i runs on XCD i % 8: with v_heads % 8 == 0 the row blocks of a
+  // head share one XCD, whose L2 then serves the head's q and k to all of
+  // them (spread over the XCDs, each XCD would fetch the token stream again)
+  int vh = blockIdx.y, rb = blockIdx.x;
+  if ((a.v_heads & 7) == 0) {
+    const int p = static_cast<int>(blockIdx.x + gridDim.x * blockIdx.y), k = p >> 3;
+    vh = (k / static_cast<int>(gridDim.x)) * 8 + (p & 7);
+    rb = k % static_cast<int>(gridDim.x);
+  }
+  const int col = lane & (kRowLanes - 1), row = kDeltaScanRows * rb + (lane >> 4);
   // segment blockIdx.z: rows r0 .. r0 + count - 1 of one slot, in order
   const int r0 = a.row_seg != nullptr ? a.seg_row0[blockIdx.z] : 0;
   const int count = a.row_seg != nullptr ? a.seg_count[blockIdx.z] : a.batch;
