@@ -227,7 +227,9 @@ int q35_model_upload_tensor(q35_model *model, const char *name, int encoding,
                             size_t byte_count);
 int q35_model_finalize(q35_model *model); /* checks every required tensor is present */
 void q35_model_destroy(q35_model *model);
-/* Reads a Q35H128 v1 artifact (src/weights/q4_h128_artifact.cpp) and uploads it. */
+/* Reads a Q35H128 v1 artifact (src/weights/q4_h128_artifact.cpp) and uploads it.
+ * The header's layers, hidden, intermediate and vocab must match dims;
+ * dims->sign_seed must equal the header's H128 sign seed, or be 0 to take it. */
 int q35_model_load_artifact(q35_context *ctx, const char *artifact_path,
                             const q35_model_dims *dims, const uint8_t *layer_is_linear,
                             q35_model **out);

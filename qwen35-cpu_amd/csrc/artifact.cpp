@@ -475,15 +475,17 @@ extern "C" int q35_model_load_artifact(q35_context *ctx, const char *path, const
   const uint64_t count = u64(hdr + 24), dir_bytes = u64(hdr + 40), seed = u64(hdr + 56);
   if (u32(hdr + 64) != static_cast<uint32_t>(dims->n_layers) || u32(hdr + 68) != static_cast<uint32_t>(dims->hidden) ||
       u32(hdr + 72) != static_cast<uint32_t>(dims->intermediate) || u32(hdr + 76) != static_cast<uint32_t>(dims->vocab) ||
-      seed == 0 || seed != dims->sign_seed)
+      seed == 0 || (dims->sign_seed != 0 && seed != dims->sign_seed))
     return q35::set_error(ctx, Q35_ERR_IO, "artifact fingerprint does not match the model dims");
   if (count == 0 || count > 100000 || kHeaderSize + dir_bytes > file_size)
     return q35::set_error(ctx, Q35_ERR_IO, "bad artifact directory");
   std::vector<uint8_t> dir(dir_bytes);
   if (!f.read(reinterpret_cast<char *>(dir.data()), static_cast<std::streamsize>(dir_bytes)))
     return q35::set_error(ctx, Q35_ERR_IO, "truncated directory");
+  q35_model_dims md = *dims;
+  md.sign_seed = seed;  // 0 in dims: the artifact's own H128 sign seed
   q35_model *m = nullptr;
-  int st = q35_model_create(ctx, dims, is_linear, &m);
+  int st = q35_model_create(ctx, &md, is_linear, &m);
   if (st != Q35_OK) return st;
   size_t o = 0;
   std::vector<uint8_t> payload;
