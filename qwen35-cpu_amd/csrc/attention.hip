@@ -74,197 +74,337 @@ __global__ __launch_bounds__(kAttnThreads) void attn_prep_kernel(AttnPrepArgs a)
 }
 
 // ---------------------------------------------------------------- attention
-// One workgroup of 512 threads per (chunk of kChunkTokens context tokens, KV
-// head, request) serves the QPK query heads of the GQA group, so every K/V
-// byte is read once. Thread t scores token t/8 over dims 32*(t%8)..+31 (four
-// 16-byte K loads) and accumulates P*V for dims 4*(t%64)..+3 over tokens
-// t/64 + 8j (eight 8-byte V loads). The page-table entries are loaded together
-// with the context length (a slot past the context reads the chunk's first
-// page and gets probability zero), so K and V are issued after one round
-// trip. Scores are FP32 dot products over FP16 keys (full_attention.cpp:82-93);
-// the chunk leaves its partial (max, sum, sum p*V) for the merge.
+// Scores and P*V run on v_mfma_f32_16x16x32_f16 over 64-token chunks of the
+// paged FP16 cache (full_attention.cpp:82-127 computes them as FP32 dot
+// products over FP16 keys and values). An M tile holds 16 query vectors:
+//   S[m][t] = sum_d q[m][d] k[t][d]: A = the queries, B = the keys (lane l
+//     holds dims 32kk + 8(l/16) .. +7 of token l%16 -- 16 contiguous bytes of
+//     its cache row), the eight 32-dim steps accumulated in order;
+//   O[m][d] = sum_t p[m][t] v[t][d]: A = the probabilities, B = V^T staged
+//     in LDS, the two 32-token steps accumulated in order.
+// The FP32 queries and probabilities enter as two FP16 operands each,
+// hi = binary16(x) and lo = binary16(x - hi), so every product with an FP16
+// key or value is exact in FP32 and x is carried to 22 significant bits
+// (|q| below 65504; probabilities are in [0, 1]). Each output element of an
+// MFMA depends only on its own A row, B column and C element, so a query's
+// scores, statistics and partial do not depend on which M row it occupies or
+// what else shares the tile: the decode kernel (one request row, its QPK
+// heads in an M tile) and the tiled prefill kernel (16 positions of a head
+// in an M tile) give every row the same bits.
+// Per chunk and query the softmax takes the maximum over the chunk's tokens,
+// p = exp(s - max) (0 past the row's context), and the sum of p as a tree
+// over each 16-token tile (the xor-1/2/4/8 exchange) added tile by tile;
+// the partial (max, sum, sum p*V) goes to attention_merge_kernel.
 constexpr int kChunkTokens = 64;
-constexpr int kScoreThreads = 512;
-constexpr int kScoreWaves = kScoreThreads / 64;
-constexpr int kQStride = 36;  // 32 dims + 4: the eight dim slices land on distinct LDS banks
+constexpr int kKStride = kHeadDim + 8;  // halfs per staged K row: the lanes' 16-byte key reads spread over the banks
+constexpr int kVStride = kKStride;      // halfs per staged V row (16-byte aligned rows for the 16-byte stores)
+constexpr int kPStride = kChunkTokens + 4;  // floats per probability row in LDS
 
-template <int QPK, bool TILED>
-__global__ __launch_bounds__(kScoreThreads) __attribute__((amdgpu_waves_per_eu(4))) void attention_kernel(AttnArgs a) {
-  constexpr int NQ = (QPK * kHeadDim + kScoreThreads - 1) / kScoreThreads;  // query values staged per thread
-  __shared__ float qs[QPK * 8 * kQStride];
-  __shared__ float probs[QPK][kChunkTokens];
-  __shared__ float s_m[QPK], s_l[QPK];
-  __shared__ float red[kScoreWaves][QPK][kHeadDim];
-  const int sp = blockIdx.x, g = blockIdx.y;
+// The query operands of one lane (query l % 16): dims 32kk + 8(l/16) .. +7
+// of the query for kk = 0..7, as hi and lo parts (zeros when !live).
+struct QOps {
+  q35_f16x8 hi[8], lo[8];
+};
+__device__ __forceinline__ void load_q_ops(const float *q, bool live, int lane, QOps &o) {
+  const int kg = lane >> 4;
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) {
+    float x[8];
+    if (live) {
+      const q35_f32x4 a = *reinterpret_cast<const q35_f32x4 *>(q + 32 * kk + 8 * kg);
+      const q35_f32x4 b = *reinterpret_cast<const q35_f32x4 *>(q + 32 * kk + 8 * kg + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[i] = a[i];
+        x[4 + i] = b[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = 0.0F;
+    }
+    q35_split_f16(x, o.hi[kk], o.lo[kk]);
+  }
+}
+
+// Scores of a 16-token tile; key(kk) is the lane's key operand of step kk.
+// Lane l receives S[4(l/16) + j][l % 16], j = 0..3.
+template <typename Key>
+__device__ __forceinline__ q35_f32x4 qk_tile(const QOps &q, Key key) {
+  q35_f32x4 c = {0.0F, 0.0F, 0.0F, 0.0F};
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) {
+    const q35_f16x8 k = key(kk);
+    c = Q35_MFMA_F32_16X16X32_F16(q.hi[kk], k, c);
+    c = Q35_MFMA_F32_16X16X32_F16(q.lo[kk], k, c);
+  }
+  return c;
+}
+
+__device__ __forceinline__ float tile_max(float v) {
+  v = fmaxf(v, q35_row_xor(v, 1));
+  v = fmaxf(v, q35_row_xor(v, 2));
+  v = fmaxf(v, q35_row_xor(v, 4));
+  return fmaxf(v, q35_row_xor(v, 8));
+}
+__device__ __forceinline__ float tile_sum(float v) {
+  v += q35_row_xor(v, 1);
+  v += q35_row_xor(v, 2);
+  v += q35_row_xor(v, 4);
+  return v + q35_row_xor(v, 8);
+}
+
+// The probability operands of one lane (query l % 16): tokens
+// 32ks + 8(l/16) .. +7 of the row in `pl` for ks = 0, 1.
+__device__ __forceinline__ void load_p_ops(const float *pl, int lane, q35_f16x8 hi[2], q35_f16x8 lo[2]) {
+  const float *row = pl + (lane & 15) * kPStride + 8 * (lane >> 4);
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const q35_f32x4 a = *reinterpret_cast<const q35_f32x4 *>(row + 32 * ks);
+    const q35_f32x4 b = *reinterpret_cast<const q35_f32x4 *>(row + 32 * ks + 4);
+    float x[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[i] = a[i];
+      x[4 + i] = b[i];
+    }
+    q35_split_f16(x, hi[ks], lo[ks]);
+  }
+}
+
+// P*V of dims 16dt .. 16dt+15 from V rows staged in LDS (row stride
+// kVStride): the value operand of lane l gathers dim 16dt + l%16 of tokens
+// 32ks + 8(l/16) .. +7. Lane l receives O[4(l/16) + j][16dt + l % 16].
+__device__ __forceinline__ q35_f32x4 pv_tile(const q35_f16x8 phi[2], const q35_f16x8 plo[2], const uint16_t *vs,
+                                             int dt, int lane) {
+  const uint16_t *col = vs + (8 * (lane >> 4)) * kVStride + 16 * dt + (lane & 15);
+  q35_f32x4 c = {0.0F, 0.0F, 0.0F, 0.0F};
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    q35_u32x4 raw;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t lo = col[(32 * ks + 2 * e) * kVStride], hi = col[(32 * ks + 2 * e + 1) * kVStride];
+      raw[e] = lo | (hi << 16);
+    }
+    const q35_f16x8 v = q35_f16x8_bits(raw);
+    c = Q35_MFMA_F32_16X16X32_F16(phi[ks], v, c);
+    c = Q35_MFMA_F32_16X16X32_F16(plo[ks], v, c);
+  }
+  return c;
+}
+
+// Decode: one workgroup of 4 wavefronts per (chunk, KV head, request row);
+// the row's QPK heads are the live rows of one M tile. Wavefront w scores
+// token tile w (its keys loaded straight into operands); the chunk's V rows
+// are staged in LDS with coalesced loads (32 lanes per row); the tile maxima
+// and sums meet in LDS; wavefront w then forms P*V for dims 64w .. 64w+63.
+template <int QPK>
+__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
+  __shared__ __align__(16) uint16_t vs[kChunkTokens * kVStride];
+  __shared__ __align__(16) float pl[16 * kPStride];
+  __shared__ float tmax[4][16], tsum[4][16];
+  const int sp = blockIdx.x, g = blockIdx.y, r = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int kq = tid & 7, ti = tid >> 3;
   const int t0 = sp * kChunkTokens;
   const int kvw = a.kv_heads * kHeadDim;
-  // the rows of this workgroup: one request row, or a tile of consecutive
-  // positions of one segment (they share its page table, and the last row
-  // has the longest context)
-  const int r0 = TILED ? a.tile_row0[blockIdx.z] : static_cast<int>(blockIdx.z);
-  const int nrows = TILED ? a.tile_rows[blockIdx.z] : 1;
-  const int32_t *pt = a.page_table + static_cast<size_t>(a.row_seg != nullptr ? a.row_seg[r0] : r0) * a.max_pages;
+  const int32_t *pt = a.page_table + static_cast<size_t>(a.row_seg != nullptr ? a.row_seg[r] : r) * a.max_pages;
   const int last_page = a.max_pages - 1;
   // page_tokens is a power of two: shifts and masks, not integer division
   const int pshift = __builtin_ctz(static_cast<unsigned>(a.page_tokens)), pmask = a.page_tokens - 1;
-  auto seq_of = [&](int r) { return a.seq_lens != nullptr ? a.seq_lens[r] : a.positions[r] + 1; };
-  auto load_q = [&](int r, float qv[NQ]) {
-#pragma unroll
-    for (int k = 0; k < NQ; ++k) {
-      const int e = min(tid + k * kScoreThreads, QPK * kHeadDim - 1);
-      qv[k] = a.q[(static_cast<size_t>(r) * a.heads + g * QPK + e / kHeadDim) * kHeadDim + e % kHeadDim];
-    }
-  };
-  // one round trip: the query heads, the context length and the page-table
-  // entries of every token slot (clamped into the row)
-  float qv[NQ];
-  load_q(r0, qv);
-  const int seq_tile = seq_of(r0 + nrows - 1);
+  const int kt = 16 * wave + (lane & 15);  // this lane's key token within the chunk
+  // one round trip: the context length and the page-table entries of the
+  // lane's key token and of its 8 value rows (2w + 8i + l/32)
+  const int seq = a.seq_lens != nullptr ? a.seq_lens[r] : a.positions[r] + 1;
   const int pfirst = pt[min(t0 >> pshift, last_page)];
-  const int pk = pt[min((t0 + ti) >> pshift, last_page)];
+  const int pk = pt[min((t0 + kt) >> pshift, last_page)];
   int pv[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) pv[j] = pt[min((t0 + wave + 8 * j) >> pshift, last_page)];
+  for (int i = 0; i < 8; ++i) pv[i] = pt[min((t0 + 2 * wave + 8 * i + (lane >> 5)) >> pshift, last_page)];
+  if (t0 >= seq) return;  // whole workgroup
+  const int n = min(seq - t0, kChunkTokens);
+  // keys of tile `wave` (slots past the context read the chunk's first token)
+  const bool kin = kt < n;
+  const uint16_t *krow = a.k_pool + ((static_cast<size_t>(kin ? pk : pfirst) << pshift) + ((kin ? t0 + kt : t0) & pmask)) * kvw +
+                         static_cast<size_t>(g) * kHeadDim + 8 * (lane >> 4);
+  q35_u32x4 kraw[8];
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) kraw[kk] = Q35_LOAD_NT(reinterpret_cast<const q35_u32x4 *>(krow + 32 * kk));
+  // value rows 2w + 8i + l/32, 16 bytes each at dims 8(l%32)
+  q35_u32x4 vraw[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int vt = 2 * wave + 8 * i + (lane >> 5);
+    const bool vin = vt < n;
+    vraw[i] = Q35_LOAD_NT(reinterpret_cast<const q35_u32x4 *>(
+        a.v_pool + ((static_cast<size_t>(vin ? pv[i] : pfirst) << pshift) + ((vin ? t0 + vt : t0) & pmask)) * kvw +
+        static_cast<size_t>(g) * kHeadDim + 8 * (lane & 31)));
+  }
+  // query m = lane % 16 is head g*QPK + m
+  const int m = lane & 15;
+  QOps q;
+  load_q_ops(a.q + (static_cast<size_t>(r) * a.heads + g * QPK + min(m, QPK - 1)) * kHeadDim, m < QPK, lane, q);
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    *reinterpret_cast<q35_u32x4 *>(vs + (2 * wave + 8 * i + (lane >> 5)) * kVStride + 8 * (lane & 31)) = vraw[i];
+
+  const q35_f32x4 s = qk_tile(q, [&](int kk) { return q35_f16x8_bits(kraw[kk]); });
+  float sc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    sc[j] = kin ? s[j] * a.scale : -INFINITY;
+    const float mx = tile_max(sc[j]);
+    if ((lane & 15) == 0) tmax[wave][4 * (lane >> 4) + j] = mx;
+  }
+  lds_barrier();
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int mm = 4 * (lane >> 4) + j;
+    const float mx = fmaxf(fmaxf(fmaxf(tmax[0][mm], tmax[1][mm]), tmax[2][mm]), tmax[3][mm]);
+    const float p = kin ? expf(sc[j] - mx) : 0.0F;
+    pl[mm * kPStride + kt] = p;
+    const float ps = tile_sum(p);
+    if ((lane & 15) == 0) tsum[wave][mm] = ps;
+  }
+  lds_barrier();
+
+  q35_f16x8 phi[2], plo[2];
+  load_p_ops(pl, lane, phi, plo);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int dt = 4 * wave + i;
+    const q35_f32x4 o = pv_tile(phi, plo, vs, dt, lane);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int mm = 4 * (lane >> 4) + j;
+      if (mm < QPK) {
+        const size_t hs = (static_cast<size_t>(r) * a.heads + g * QPK + mm) * a.max_splits + sp;
+        a.part_o[hs * kHeadDim + 16 * dt + (lane & 15)] = o[j];
+      }
+    }
+  }
+  if (wave == 0 && lane < QPK) {
+    const float mx = fmaxf(fmaxf(fmaxf(tmax[0][lane], tmax[1][lane]), tmax[2][lane]), tmax[3][lane]);
+    const size_t hs = (static_cast<size_t>(r) * a.heads + g * QPK + lane) * a.max_splits + sp;
+    a.part_ml[hs * 2] = mx;
+    a.part_ml[hs * 2 + 1] = ((tsum[0][lane] + tsum[1][lane]) + tsum[2][lane]) + tsum[3][lane];
+  }
+}
+
+// Prefill: one workgroup per (chunk, KV head, tile of up to kAttnTileRows
+// consecutive positions of one segment; the tile's rows share its page table
+// and its last row has the longest context), one wavefront per query head:
+// wavefront u's M tile is head g*QPK + u of the tile's rows. The chunk's K
+// and V rows are loaded up front with coalesced loads (32 lanes per row);
+// K goes to LDS for the scores, then V takes its place for P*V, so three
+// workgroups fit a CU. Each wavefront runs the decode kernel's sequence for
+// its 16 queries.
+template <int QPK>
+__global__ __launch_bounds__(64 * QPK) Q35_WAVES_PER_EU(QPK == 4 ? 3 : 1) void attention_tile_kernel(AttnArgs a) {
+  constexpr int kThreads = 64 * QPK;
+  constexpr int NP = kChunkTokens * 32 / kThreads;  // 16-byte pieces of K (and of V) per thread
+  __shared__ __align__(16) uint16_t kv[kChunkTokens * kKStride];
+  __shared__ __align__(16) float pls[QPK][16 * kPStride];
+  const int sp = blockIdx.x, g = blockIdx.y;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int t0 = sp * kChunkTokens;
+  const int kvw = a.kv_heads * kHeadDim;
+  const int r0 = a.tile_row0[blockIdx.z], nrows = a.tile_rows[blockIdx.z];
+  const int32_t *pt = a.page_table + static_cast<size_t>(a.row_seg != nullptr ? a.row_seg[r0] : r0) * a.max_pages;
+  const int last_page = a.max_pages - 1;
+  const int pshift = __builtin_ctz(static_cast<unsigned>(a.page_tokens)), pmask = a.page_tokens - 1;
+  auto seq_of = [&](int r) { return a.seq_lens != nullptr ? a.seq_lens[r] : a.positions[r] + 1; };
+  const int seq_tile = seq_of(r0 + nrows - 1);
   if (t0 >= seq_tile) return;  // whole workgroup
   const int n_tile = min(seq_tile - t0, kChunkTokens);
-
-  // K, then V (the memory counter retires loads in issue order); slots past
-  // the tile's context read the chunk's first token
-  const bool kload = ti < n_tile;
-  const int ktok = kload ? t0 + ti : t0;
-  const q35_u32x4 *krow = reinterpret_cast<const q35_u32x4 *>(
-      a.k_pool + ((static_cast<size_t>(kload ? pk : pfirst) << pshift) + (ktok & pmask)) * kvw +
-      static_cast<size_t>(g) * kHeadDim + 32 * kq);
-  q35_u32x4 kraw[4];
+  const int pfirst = pt[min(t0 >> pshift, last_page)];
+  // piece e = tid + kThreads*i: token e/32, dims 8(e%32) (slots past the
+  // tile's context hold the chunk's first token)
+  size_t rows[NP];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) kraw[i] = Q35_LOAD_NT(krow + i);
-  q35_u32x2 vraw[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const bool vin = wave + 8 * j < n_tile;
-    const int vt = vin ? t0 + wave + 8 * j : t0;
-    vraw[j] = Q35_LOAD_NT(reinterpret_cast<const q35_u32x2 *>(
-        a.v_pool + ((static_cast<size_t>(vin ? pv[j] : pfirst) << pshift) + (vt & pmask)) * kvw +
-        static_cast<size_t>(g) * kHeadDim + 4 * lane));
+  for (int i = 0; i < NP; ++i) {
+    const int t = (tid + kThreads * i) >> 5;
+    const bool in = t < n_tile;
+    const int page = in ? pt[min((t0 + t) >> pshift, last_page)] : pfirst;
+    rows[i] = ((static_cast<size_t>(page) << pshift) + ((in ? t0 + t : t0) & pmask)) * kvw +
+              static_cast<size_t>(g) * kHeadDim + 8 * (tid & 31);
   }
+  q35_u32x4 kraw[NP], vraw[NP];
+#pragma unroll
+  for (int i = 0; i < NP; ++i) kraw[i] = Q35_LOAD_NT(reinterpret_cast<const q35_u32x4 *>(a.k_pool + rows[i]));
+#pragma unroll
+  for (int i = 0; i < NP; ++i) vraw[i] = Q35_LOAD_NT(reinterpret_cast<const q35_u32x4 *>(a.v_pool + rows[i]));
+  // this wavefront's queries: rows r0 + m of head g*QPK + wave
+  const int m = lane & 15;
+  QOps q;
+  load_q_ops(a.q + (static_cast<size_t>(r0 + min(m, nrows - 1)) * a.heads + g * QPK + wave) * kHeadDim, m < nrows,
+             lane, q);
+#pragma unroll
+  for (int i = 0; i < NP; ++i)
+    *reinterpret_cast<q35_u32x4 *>(kv + ((tid + kThreads * i) >> 5) * kKStride + 8 * (tid & 31)) = kraw[i];
+  lds_barrier();
 
-  for (int i = 0; i < nrows; ++i) {
-    const int r = r0 + i;
-    const int seq = TILED ? seq_of(r) : seq_tile;
-    if (t0 >= seq) {  // this row's context ends before the chunk (uniform)
-      if (TILED && i + 1 < nrows) load_q(r + 1, qv);
-      continue;
+  q35_f32x4 s[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    const uint16_t *krow = kv + (16 * tt + (lane & 15)) * kKStride + 8 * (lane >> 4);
+    s[tt] = qk_tile(q, [&](int kk) { return q35_f16x8_bits(*reinterpret_cast<const q35_u32x4 *>(krow + 32 * kk)); });
+  }
+  // rows 4(l/16) + j: context lengths, masked scores, maxima over the tiles
+  int nm[4];
+  float mx[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int mm = 4 * (lane >> 4) + j;
+    nm[j] = mm < nrows ? min(seq_of(r0 + mm) - t0, kChunkTokens) : 0;
+  }
+  float sc[4][4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      sc[tt][j] = 16 * tt + (lane & 15) < nm[j] ? s[tt][j] * a.scale : -INFINITY;
+      const float t = tile_max(sc[tt][j]);
+      mx[j] = tt == 0 ? t : fmaxf(mx[j], t);
     }
-    // tokens past the row's context score -inf and get probability exactly 0
-    // (their V rows are finite), so a row's partial does not depend on the
-    // tile it runs in
-    const int n = min(seq - t0, kChunkTokens);
-    const bool kin = ti < n;
+  float *pl = pls[wave];
+  float lsum[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = 16 * tt + (lane & 15);
+      const float p = t < nm[j] ? expf(sc[tt][j] - mx[j]) : 0.0F;
+      pl[(4 * (lane >> 4) + j) * kPStride + t] = p;
+      const float ps = tile_sum(p);
+      lsum[j] = tt == 0 ? ps : lsum[j] + ps;
+    }
+  lds_barrier();  // every wavefront is done with K
+#pragma unroll
+  for (int i = 0; i < NP; ++i)
+    *reinterpret_cast<q35_u32x4 *>(kv + ((tid + kThreads * i) >> 5) * kVStride + 8 * (tid & 31)) = vraw[i];
+  lds_barrier();
 
-    // the group's query heads into LDS, in eight padded 32-dim slices (the
-    // previous row's readers passed the barriers of its softmax and P*V)
+  q35_f16x8 phi[2], plo[2];
+  load_p_ops(pl, lane, phi, plo);
+  // a row gets a partial when its context reaches into the chunk
+  size_t hs[4];
 #pragma unroll
-    for (int k = 0; k < NQ; ++k) {
-      const int e = tid + k * kScoreThreads;
-      if (e < QPK * kHeadDim) {
-        const int u = e / kHeadDim, d = e % kHeadDim;
-        qs[(u * 8 + d / 32) * kQStride + d % 32] = qv[k];
+  for (int j = 0; j < 4; ++j)
+    hs[j] = (static_cast<size_t>(r0 + 4 * (lane >> 4) + j) * a.heads + g * QPK + wave) * a.max_splits + sp;
+#pragma unroll 4
+  for (int dt = 0; dt < kHeadDim / 16; ++dt) {
+    const q35_f32x4 o = pv_tile(phi, plo, kv, dt, lane);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (nm[j] > 0) a.part_o[hs[j] * kHeadDim + 16 * dt + (lane & 15)] = o[j];
+  }
+  if ((lane & 15) == 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (nm[j] > 0) {
+        a.part_ml[hs[j] * 2] = mx[j];
+        a.part_ml[hs[j] * 2 + 1] = lsum[j];
       }
-    }
-    if (TILED && i + 1 < nrows) load_q(r + 1, qv);  // the next row's query, in flight meanwhile
-    lds_barrier();
-
-    // ---- scores: 32 dims per thread, then the 8 lanes of the token
-    float part[QPK];
-#pragma unroll
-    for (int u = 0; u < QPK; ++u) part[u] = 0.0F;
-#pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) {
-      float kf[8];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        kf[2 * e] = half_bits_to_float(static_cast<uint16_t>(kraw[i4][e] & 0xffffu));
-        kf[2 * e + 1] = half_bits_to_float(static_cast<uint16_t>(kraw[i4][e] >> 16));
-      }
-#pragma unroll
-      for (int u = 0; u < QPK; ++u) {
-        const float *qp = qs + (u * 8 + kq) * kQStride + 8 * i4;
-        const q35_f32x4 qa = *reinterpret_cast<const q35_f32x4 *>(qp);
-        const q35_f32x4 qb = *reinterpret_cast<const q35_f32x4 *>(qp + 4);
-        part[u] += qa[0] * kf[0] + qa[1] * kf[1] + qa[2] * kf[2] + qa[3] * kf[3] + qb[0] * kf[4] +
-                   qb[1] * kf[5] + qb[2] * kf[6] + qb[3] * kf[7];
-      }
-      // one iteration at a time: no hoisted query reads, no sunk dot products
-#pragma unroll
-      for (int u = 0; u < QPK; ++u) q35_materialize(part[u]);
-      q35_compiler_fence();
-    }
-#pragma unroll
-    for (int u = 0; u < QPK; ++u) {
-      part[u] += q35_row_xor(part[u], 1);
-      part[u] += q35_row_xor(part[u], 2);
-      part[u] += q35_row_xor(part[u], 4);
-      if (kq == 0) probs[u][ti] = kin ? part[u] * a.scale : -INFINITY;
-    }
-    lds_barrier();
-
-    // ---- chunk softmax statistics (wave u handles head u)
-    for (int u = wave; u < QPK; u += kScoreWaves) {
-      const float s = probs[u][lane];
-      const float m = group_max<64>(s);
-      const float p = lane < n ? expf(s - m) : 0.0F;
-      const float l = group_sum<64>(p);
-      probs[u][lane] = p;
-      if (lane == 0) {
-        s_m[u] = m;
-        s_l[u] = l;
-      }
-    }
-    lds_barrier();
-
-    // ---- P*V over this wave's tokens, then the fixed-order wave sum
-    float acc[QPK][4];
-#pragma unroll
-    for (int u = 0; u < QPK; ++u) acc[u][0] = acc[u][1] = acc[u][2] = acc[u][3] = 0.0F;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int t = wave + 8 * j;
-      const float v0 = half_bits_to_float(static_cast<uint16_t>(vraw[j][0] & 0xffffu));
-      const float v1 = half_bits_to_float(static_cast<uint16_t>(vraw[j][0] >> 16));
-      const float v2 = half_bits_to_float(static_cast<uint16_t>(vraw[j][1] & 0xffffu));
-      const float v3 = half_bits_to_float(static_cast<uint16_t>(vraw[j][1] >> 16));
-#pragma unroll
-      for (int u = 0; u < QPK; ++u) {
-        const float p = probs[u][t];  // 0 past the row's tokens
-        acc[u][0] += p * v0;
-        acc[u][1] += p * v1;
-        acc[u][2] += p * v2;
-        acc[u][3] += p * v3;
-      }
-#pragma unroll
-      for (int u = 0; u < QPK; ++u)
-#pragma unroll
-        for (int k = 0; k < 4; ++k) q35_materialize(acc[u][k]);
-      q35_compiler_fence();
-    }
-#pragma unroll
-    for (int u = 0; u < QPK; ++u)
-      *reinterpret_cast<q35_f32x4 *>(&red[wave][u][4 * lane]) = q35_f32x4{acc[u][0], acc[u][1], acc[u][2], acc[u][3]};
-    lds_barrier();
-    for (int e = tid; e < QPK * kHeadDim; e += kScoreThreads) {
-      const int u = e / kHeadDim, d = e % kHeadDim;
-      float v = red[0][u][d];
-#pragma unroll
-      for (int w = 1; w < kScoreWaves; ++w) v += red[w][u][d];
-      const size_t hs = (static_cast<size_t>(r) * a.heads + g * QPK + u) * a.max_splits + sp;
-      a.part_o[hs * kHeadDim + d] = v;
-      if (d == 0) {
-        a.part_ml[hs * 2] = s_m[u];
-        a.part_ml[hs * 2 + 1] = s_l[u];
-      }
-    }
   }
 }
 
@@ -377,12 +517,12 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
   const int qpk = a.heads / a.kv_heads;
   const bool tiled = a.tile_row0 != nullptr;
   const int gs = a.grid_splits > 0 ? std::min(a.grid_splits, a.max_splits) : a.max_splits;
-  const dim3 grid(gs, a.kv_heads, tiled ? a.tiles : a.batch), block(kScoreThreads);
+  const dim3 grid(gs, a.kv_heads, tiled ? a.tiles : a.batch);
 #define Q35_ATTN(Q)                                                             \
   if (tiled)                                                                    \
-    Q35_LAUNCH((attention_kernel<Q, true>), grid, block, 0, stream, a);        \
+    Q35_LAUNCH((attention_tile_kernel<Q>), grid, dim3(64 * (Q)), 0, stream, a); \
   else                                                                          \
-    Q35_LAUNCH((attention_kernel<Q, false>), grid, block, 0, stream, a);
+    Q35_LAUNCH((attention_kernel<Q>), grid, dim3(256), 0, stream, a);
   switch (qpk) {
     case 1: Q35_ATTN(1) break;
     case 2: Q35_ATTN(2) break;

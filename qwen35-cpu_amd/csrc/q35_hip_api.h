@@ -31,6 +31,11 @@ bool launch_events(hipEvent_t *start, hipEvent_t *stop);
 #define Q35_MFMA_I32_16X16X32_I8(a, b, c, cbsz, abid, blgp) \
   __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, cbsz, abid, blgp)
 #define Q35_DYNAMIC_SHARED(type, name) extern __shared__ type name[]
+// occupancy target of a kernel: at least n wavefronts per SIMD (caps its VGPRs)
+#define Q35_WAVES_PER_EU(n) __attribute__((amdgpu_waves_per_eu(n)))
+// fp16 MFMA operands: eight binary16 values per lane
+typedef _Float16 q35_f16x8 __attribute__((ext_vector_type(8)));
+#define Q35_MFMA_F32_16X16X32_F16(a, b, c) __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0)
 // four int8 products of a and b (byte-wise, signed) added to c: v_dot4_i32_i8
 #define Q35_SDOT4(a, b, c) __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), (c), false)
 // Streaming loads of data read once per step (weights, recurrent state, KV):
@@ -77,10 +82,31 @@ __device__ __forceinline__ void q35_compiler_fence() { asm volatile("" ::: "memo
 // loads and keep their results live meanwhile.
 __device__ __forceinline__ void q35_materialize(float &x) { asm volatile("" : "+v"(x)); }
 
+// Orders a wavefront's LDS writes before its later LDS reads by other lanes of
+// the same wavefront. The LDS executes one wavefront's instructions in order,
+// so this only stops the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+// Sixteen bytes of binary16 bits as an fp16 MFMA operand.
+__device__ __forceinline__ q35_f16x8 q35_f16x8_bits(q35_u32x4 raw) { return __builtin_bit_cast(q35_f16x8, raw); }
+// x = hi + lo with hi = binary16(x) and lo = binary16(x - hi) (round to
+// nearest even): 22 significant bits in two fp16 operands, whose products with
+// an fp16 value are exact in fp32.
+__device__ __forceinline__ void q35_split_f16(const float x[8], q35_f16x8 &hi, q35_f16x8 &lo) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const _Float16 h = static_cast<_Float16>(x[i]);
+    hi[i] = h;
+    lo[i] = static_cast<_Float16>(x[i] - static_cast<float>(h));
+  }
 }
 __device__ __forceinline__ float q35_quad_xor1(float v) { return q35_row_xor(v, 1); }
 __device__ __forceinline__ float q35_quad_xor2(float v) { return q35_row_xor(v, 2); }

@@ -34,6 +34,7 @@ using std::isnan;
 #define __host__
 #define __forceinline__ inline
 #define __launch_bounds__(...)
+#define Q35_WAVES_PER_EU(n)
 #define __align__(n) alignas(n)
 // Blocks of one launch run one after another, so a function-local static is a
 // faithful per-block shared array.
@@ -54,7 +55,7 @@ namespace q35emu {
 struct Launch {
   std::barrier<> *block = nullptr;
   std::vector<std::unique_ptr<std::barrier<>>> waves;
-  std::vector<std::vector<uint64_t>> slots_a, slots_b;  // per wave, 64 lanes
+  std::vector<std::vector<uint64_t>> slots_a, slots_b, slots_c, slots_d;  // per wave, 64 lanes
   std::vector<float> dynamic_smem;
 };
 
@@ -106,6 +107,8 @@ void run_launch(K kernel, dim3 grid, dim3 block, size_t smem, Args... args) {
     L.waves.emplace_back(new std::barrier<>(static_cast<std::ptrdiff_t>(std::min(64u, n - 64 * w))));
   L.slots_a.assign(nw, std::vector<uint64_t>(64));
   L.slots_b.assign(nw, std::vector<uint64_t>(64));
+  L.slots_c.assign(nw, std::vector<uint64_t>(64));
+  L.slots_d.assign(nw, std::vector<uint64_t>(64));
   L.dynamic_smem.assign(smem / sizeof(float) + 1, 0.0F);
   std::vector<std::thread> pool;
   pool.reserve(n);
@@ -254,6 +257,51 @@ typedef unsigned int q35_u32x4 __attribute__((vector_size(16)));
 typedef unsigned int q35_u32x2 __attribute__((vector_size(8)));
 typedef float q35_f32x4 __attribute__((vector_size(16)));
 typedef float q35_f32x2 __attribute__((vector_size(8)));
+// fp16 MFMA (v_mfma_f32_16x16x32_f16): the i8 operand layout with eight
+// binary16 values per lane; each output is C plus the 32 products summed in
+// k order in fp32 (the hardware's internal order differs; every use here is
+// compared across paths of this same emulation or against a tolerance)
+typedef uint16_t q35_f16x8 __attribute__((vector_size(16)));
+inline q35_f16x8 q35_f16x8_bits(q35_u32x4 raw) {
+  q35_f16x8 r;
+  std::memcpy(&r, &raw, 16);
+  return r;
+}
+inline void q35_split_f16(const float x[8], q35_f16x8 &hi, q35_f16x8 &lo) {
+  for (int i = 0; i < 8; ++i) {
+    hi[i] = ::q35emu::f2h(x[i]);
+    lo[i] = ::q35emu::f2h(x[i] - ::q35emu::h2f(hi[i]));
+  }
+}
+inline q35_f32x4 q35emu_mfma_f16(q35_f16x8 a, q35_f16x8 b, q35_f32x4 c) {
+  auto &ctx = ::q35emu::t_ctx;
+  auto &a0 = ctx.launch->slots_a[ctx.wave], &a1 = ctx.launch->slots_b[ctx.wave];
+  auto &b0 = ctx.launch->slots_c[ctx.wave], &b1 = ctx.launch->slots_d[ctx.wave];
+  uint64_t w[4];
+  std::memcpy(w, &a, 16);
+  a0[ctx.lane] = w[0];
+  a1[ctx.lane] = w[1];
+  std::memcpy(w, &b, 16);
+  b0[ctx.lane] = w[0];
+  b1[ctx.lane] = w[1];
+  ::q35emu::wave_sync();
+  auto elem = [](const std::vector<uint64_t> &lo, const std::vector<uint64_t> &hi, int lane, int k) {
+    const uint64_t word = k < 4 ? lo[lane] : hi[lane];
+    return ::q35emu::h2f(static_cast<uint16_t>(word >> (16 * (k % 4))));
+  };
+  q35_f32x4 d;
+  const int col = ctx.lane % 16;
+  for (int v = 0; v < 4; ++v) {
+    const int row = 4 * (ctx.lane / 16) + v;
+    float sum = c[v];
+    for (int k = 0; k < 32; ++k)
+      sum += elem(a0, a1, row + 16 * (k / 8), k % 8) * elem(b0, b1, col + 16 * (k / 8), k % 8);
+    d[v] = sum;
+  }
+  ::q35emu::wave_sync();
+  return d;
+}
+#define Q35_MFMA_F32_16X16X32_F16(a, b, c) q35emu_mfma_f16(a, b, c)
 #define Q35_LOAD_NT(ptr) (*(ptr))
 inline int q35emu_sdot4(uint32_t a, uint32_t b, int c) {
   for (int i = 0; i < 4; ++i)
@@ -262,6 +310,7 @@ inline int q35emu_sdot4(uint32_t a, uint32_t b, int c) {
 }
 #define Q35_SDOT4(a, b, c) q35emu_sdot4(static_cast<uint32_t>(a), static_cast<uint32_t>(b), (c))
 inline void lds_barrier() { __syncthreads(); }
+inline void wave_lds_sync() { ::q35emu::wave_sync(); }
 inline void q35_compiler_fence() { asm volatile("" ::: "memory"); }
 inline void q35_materialize(float &) {}
 inline int __lane_id() { return ::q35emu::t_ctx.lane; }
