@@ -367,18 +367,17 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_chunk_inputs_kernel(Delta
 // segments): the 16 lanes of row 4 * blockIdx.x + lane / 16 hold it as
 // delta_kernel does (columns 4o + 64m) and run delta_row per token, so the
 // chain of a token is 8 columns long and the scan has a wavefront per SIMD at
-// the 4B shapes. A token's q and k go through LDS (one float4 per lane); the
-// next kDeltaScanAhead tokens' loads are in flight while a token is computed.
-constexpr int kDeltaScanAhead = 16;
+// the 4B shapes. Tokens go in blocks of kScanBlock: the block's inputs (q and
+// k, the 4 rows' values, alpha and beta) sit in LDS, and the next block's are
+// loaded into registers meanwhile and stored after the block, so a token's
+// step waits on LDS only, never on memory.
 constexpr int kDeltaScanRows = 64 / kRowLanes;
-
-struct ScanToken {
-  q35_f32x4 qk;  // floats 4 * lane .. +3 of [q | k]
-  float v, alpha, beta;
-};
+constexpr int kScanBlock = 16;
 
 __global__ __launch_bounds__(64) void delta_scan_kernel(DeltaArgs a) {
-  __shared__ q35_f32x4 qk_lds[2][2 * kDim / 4];
+  __shared__ q35_f32x4 qk_lds[2][kScanBlock][2 * kDim / 4];
+  __shared__ float v_lds[2][kScanBlock][kDeltaScanRows];
+  __shared__ float ab_lds[2][kScanBlock][2];
   const int lane = threadIdx.x;
   // workgroup i runs on XCD i % 8: with v_heads % 8 == 0 the row blocks of a
   // head share one XCD, whose L2 then serves the head's q and k to all of
@@ -407,35 +406,50 @@ __global__ __launch_bounds__(64) void delta_scan_kernel(DeltaArgs a) {
   const float *scan = a.scan + static_cast<size_t>(r0) * tstride + static_cast<size_t>(vh) * kDeltaScanStride;
   float *outs = a.scan + static_cast<size_t>(a.batch) * tstride + static_cast<size_t>(r0) * a.v_heads * kDim +
                 static_cast<size_t>(vh) * kDim + row;
-  auto load = [&](ScanToken &t, int r) {
-    const float *e = scan + static_cast<size_t>(r) * tstride;
-    t.qk = reinterpret_cast<const q35_f32x4 *>(e)[lane];
-    t.v = e[2 * kDim + row];
-    t.alpha = e[3 * kDim];
-    t.beta = e[3 * kDim + 1];
+  // the inputs of tokens t0 .. t0 + kScanBlock - 1 (clamped into the
+  // segment): lane l holds q|k floats 4l..4l+3 of every token, the value of
+  // row l % 4 of token l / 4, and alpha (l even) or beta (l odd) of token l / 2
+  struct Block {
+    q35_f32x4 qk[kScanBlock];
+    float v, ab;
   };
-  ScanToken buf[kDeltaScanAhead];
+  const int rbase = kDeltaScanRows * rb;
+  auto load = [&](Block &k, int t0) {
 #pragma unroll
-  for (int d = 0; d < kDeltaScanAhead; ++d) load(buf[d], min(d, count - 1));
-  for (int r0t = 0; r0t < count; r0t += kDeltaScanAhead) {
+    for (int i = 0; i < kScanBlock; ++i)
+      k.qk[i] = reinterpret_cast<const q35_f32x4 *>(scan + static_cast<size_t>(min(t0 + i, count - 1)) * tstride)[lane];
+    k.v = scan[static_cast<size_t>(min(t0 + (lane >> 2), count - 1)) * tstride + 2 * kDim + rbase + (lane & 3)];
+    k.ab = scan[static_cast<size_t>(min(t0 + ((lane >> 1) & (kScanBlock - 1)), count - 1)) * tstride + 3 * kDim + (lane & 1)];
+  };
+  auto store = [&](const Block &k, int buf) {
 #pragma unroll
-    for (int d = 0; d < kDeltaScanAhead; ++d) {
-      const int r = r0t + d;
-      if (r >= count) break;
-      q35_f32x4 *lds = qk_lds[d & 1];
-      lds[lane] = buf[d].qk;
-      const float v = buf[d].v, alpha = buf[d].alpha, beta = buf[d].beta;
-      load(buf[d], min(r + kDeltaScanAhead, count - 1));
-      lds_barrier();
+    for (int i = 0; i < kScanBlock; ++i) qk_lds[buf][i][lane] = k.qk[i];
+    v_lds[buf][lane >> 2][lane & 3] = k.v;
+    if (lane < 2 * kScanBlock) ab_lds[buf][lane >> 1][lane & 1] = k.ab;
+  };
+  Block blk;
+  load(blk, 0);
+  store(blk, 0);
+  lds_barrier();
+  for (int t0 = 0, cur = 0; t0 < count; t0 += kScanBlock, cur ^= 1) {
+    const bool more = t0 + kScanBlock < count;
+    if (more) load(blk, t0 + kScanBlock);
+    // the next block's loads stay issued here, a block ahead of their use
+    // (left alone, the compiler sinks them next to the store)
+    q35_compiler_fence();
+    const int n = min(kScanBlock, count - t0);
+    for (int i = 0; i < n; ++i) {
       q35_f32x4 kc[2], qc[2];
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
-        kc[m] = lds[kDim / 4 + col + 16 * m];
-        qc[m] = lds[col + 16 * m];
+        kc[m] = qk_lds[cur][i][kDim / 4 + col + 16 * m];
+        qc[m] = qk_lds[cur][i][col + 16 * m];
       }
-      const float o = delta_row(st, kc, qc, v, alpha, beta);
-      if (col == 0) outs[static_cast<size_t>(r) * a.v_heads * kDim] = o;
+      const float o = delta_row(st, kc, qc, v_lds[cur][i][lane >> 4], ab_lds[cur][i][0], ab_lds[cur][i][1]);
+      if (col == 0) outs[static_cast<size_t>(t0 + i) * a.v_heads * kDim] = o;
     }
+    if (more) store(blk, cur ^ 1);
+    lds_barrier();
   }
 #pragma unroll
   for (int m = 0; m < 2; ++m) Q35_STORE_NT(st[m], W + 16 * m);
