@@ -475,6 +475,14 @@ enum {
   Q35_TRACE_CODES_HEAD, Q35_TRACE_SCALES_HEAD, Q35_TRACE_POINTS
 };
 int q35_runtime_set_trace(q35_runtime *rt, int enable);
+
+/* Fused decode projections (no reference counterpart: a test and measurement
+ * switch, on by default). Steps of at most 16 rows fold each residual +
+ * RMSNorm + H128 preparation into the prologue of the projection that
+ * consumes it, and finish the out / o and down projections with the residual
+ * added (6 kernels per linear layer instead of 8). Disabled, the same steps
+ * run the general split path; both give identical bits. */
+int q35_runtime_set_fused(q35_runtime *rt, int enable);
 /* Copies the traced bytes of (layer, point) of the last step into `out`
  * (at most `capacity` bytes); *bytes receives the traced size (0: none). */
 int q35_runtime_trace_read(q35_runtime *rt, int layer, int point, void *out, size_t capacity, size_t *bytes);

@@ -212,6 +212,7 @@ _SIGS = {
     "q35_runtime_last_hidden": (c_int, [P, P, c_size_t]),
     "q35_runtime_set_profiling": (c_int, [P, c_int]),
     "q35_runtime_set_trace": (c_int, [P, c_int]),
+    "q35_runtime_set_fused": (c_int, [P, c_int]),
     "q35_runtime_trace_read": (c_int, [P, c_int, c_int, P, c_size_t, POINTER(c_size_t)]),
     "q35_runtime_profile_reset": (c_int, [P]),
     "q35_runtime_profile_read": (c_int, [P, c_int, POINTER(c_double), POINTER(c_uint64), POINTER(c_double)]),
@@ -666,6 +667,10 @@ class Runtime(_Profiled):
                        "head candidates")
         arr = np.frombuffer(cand, dtype=np.dtype([("value", np.float32), ("token", np.int32)])).copy()
         return (arr, lg) if raw_logits else arr
+
+    def set_fused(self, enable=True):
+        """Fused decode projections on or off (q35_runtime_set_fused; both give identical bits)."""
+        self.ctx.check(lib.q35_runtime_set_fused(self.handle, int(enable)), "set fused")
 
     def set_trace(self, enable=True):
         """Stage trace of the next steps (q35_runtime_set_trace, a test hook)."""

@@ -271,22 +271,6 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 // (k-group G) and those rows' FP16 scales; word i is the B operand of MFMA #i
 // for column c, i.e. output row RM·c + i of the group. The int32 block dot
 // and the fp32 chain per block are gemm_kernel's.
-template <int RM>
-struct RowWords;
-template <>
-struct RowWords<1> {
-  typedef uint32_t Q;
-  typedef uint16_t D;
-  static __device__ __forceinline__ uint32_t word(const Q &q, int) { return q; }
-  static __device__ __forceinline__ uint16_t scale(const D &d, int) { return d; }
-};
-template <>
-struct RowWords<2> {
-  typedef q35_u32x2 Q;
-  typedef uint32_t D;
-  static __device__ __forceinline__ uint32_t word(const Q &q, int i) { return q[i]; }
-  static __device__ __forceinline__ uint16_t scale(const D &d, int i) { return static_cast<uint16_t>(d >> (16 * i)); }
-};
 template <int KS, int RM>
 __global__ __launch_bounds__(64) void gemm_rows_kernel(GemmArgs a) {
   typedef RowWords<RM> RW;

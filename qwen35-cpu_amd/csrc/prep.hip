@@ -75,7 +75,8 @@ constexpr int kRmsMaxK = 4096;
 template <int MS, bool GATES>  // MS: bound on the added rows' K splits (0: nothing to add)
 __global__ __launch_bounds__(kRmsThreads) void rms_prep_kernel(RmsPrepArgs a) {
   __shared__ float y[kRmsMaxK];
-  __shared__ float red[kRmsThreads / 64];
+  __shared__ float gsq[kRmsMaxK / 16];  // sums of squares per 16-column group
+  __shared__ float total_sq;
   __shared__ __align__(16) int8_t gq[GATES ? kRmsMaxK : 8];
   __shared__ float gsc[GATES ? kRmsMaxK / 32 : 1];
   __shared__ float gdot[GATES ? kMaxGateItems : 1];
@@ -99,7 +100,6 @@ __global__ __launch_bounds__(kRmsThreads) void rms_prep_kernel(RmsPrepArgs a) {
   // the residual row of output row t (a gathered row set: the head rows)
   const size_t xr = a.rows != nullptr ? static_cast<size_t>(a.rows[t]) : static_cast<size_t>(t);
   const q35_f32x4 *xin = reinterpret_cast<const q35_f32x4 *>(a.x_in + xr * K);
-  float ss = 0.0F;
   for (int i = tid; i < n4; i += kRmsThreads) {
     q35_f32x4 v = xin[i];
     if constexpr (MS > 0) {
@@ -118,13 +118,18 @@ __global__ __launch_bounds__(kRmsThreads) void rms_prep_kernel(RmsPrepArgs a) {
       reinterpret_cast<q35_f32x4 *>(a.x_out + xr * K)[i] = v;
     }
     *reinterpret_cast<q35_f32x4 *>(&y[4 * i]) = v;
-    ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+    // K % 128 == 0: the four lanes of a group run the same iterations
+    const float gs = sq_group16_quad(v);
+    if ((tid & 3) == 0) gsq[i >> 2] = gs;
   }
-  ss = group_sum<64>(ss);
-  if (lane == 0) red[wave] = ss;
   // only LDS is shared: the x_out stores stay in flight
   lds_barrier();
-  const float total = (red[0] + red[1]) + (red[2] + red[3]);
+  if (wave == 0) {
+    const float t = norm_total_groups(gsq, K >> 4);
+    if (lane == 0) total_sq = t;
+  }
+  lds_barrier();
+  const float total = total_sq;
   const float rms_inv = 1.0F / sqrtf(total / static_cast<float>(K) + a.eps);
   QuantOut o;
   o.codes = a.codes;

@@ -37,6 +37,24 @@ __device__ __forceinline__ void store_row4(float *dst, bool vec, float v0, float
   }
 }
 
+// Row words of a DOT4 tile for a lane covering RM consecutive rows
+// (RM = 1 or 2): the lane's body word(s) and binary16 row scale(s).
+template <int RM>
+struct RowWords;
+template <>
+struct RowWords<1> {
+  typedef uint32_t Q;
+  typedef uint16_t D;
+  static __device__ __forceinline__ uint32_t word(const Q &q, int) { return q; }
+  static __device__ __forceinline__ uint16_t scale(const D &d, int) { return d; }
+};
+template <>
+struct RowWords<2> {
+  typedef q35_u32x2 Q;
+  typedef uint32_t D;
+  static __device__ __forceinline__ uint32_t word(const Q &q, int i) { return q[i]; }
+  static __device__ __forceinline__ uint16_t scale(const D &d, int i) { return static_cast<uint16_t>(d >> (16 * i)); }
+};
 // XOR-butterfly reductions over groups of `Width` lanes (Width <= 64, power of 2).
 template <int Width>
 __device__ __forceinline__ float group_sum(float v) {
@@ -81,6 +99,40 @@ __device__ __forceinline__ float block_sum(float v, float *scratch) {
 #pragma unroll
   for (int w = 0; w < Waves; ++w) total += scratch[w];
   return total;
+}
+
+// The RMSNorm's sum of squares, one tree shared by every kernel that
+// normalizes a residual row (so their norms round identically): the squares
+// x*x are summed per 16-column group as a butterfly over the columns in lane
+// order (exchanges xor 1, 2, 4, 8), then lane l of one wavefront takes the
+// group sums l, l + 64, l + 128, ... in order and wave_sum adds the lanes.
+//
+// A group held by four consecutive lanes, lane k with columns 4k..4k+3 (the
+// xor 1, 2 steps in registers, xor 4, 8 as lane exchanges 1, 2):
+__device__ __forceinline__ float sq_group16_quad(q35_f32x4 v) {
+#pragma clang fp contract(off)
+  const float s0 = v[0] * v[0], s1 = v[1] * v[1], s2 = v[2] * v[2], s3 = v[3] * v[3];
+  float s = (s0 + s1) + (s2 + s3);
+  s += q35_row_xor(s, 1);
+  s += q35_row_xor(s, 2);
+  return s;
+}
+// A group held by sixteen consecutive lanes (one DPP row), one column each:
+__device__ __forceinline__ float sq_group16_lanes(float x) {
+#pragma clang fp contract(off)
+  float s = x * x;
+  s += q35_row_xor(s, 1);
+  s += q35_row_xor(s, 2);
+  s += q35_row_xor(s, 4);
+  s += q35_row_xor(s, 8);
+  return s;
+}
+// The row total from its n group sums (every lane of one wavefront calls it).
+__device__ __forceinline__ float norm_total_groups(const float *gp, int n) {
+  const int l = threadIdx.x & 63;
+  float v = l < n ? gp[l] : 0.0F;
+  for (int g = l + 64; g < n; g += 64) v += gp[g];
+  return wave_sum(v);
 }
 
 // splitmix64 sign words of the randomized-sign H128 basis (src/cpu/q4_h128.cpp:16-33).

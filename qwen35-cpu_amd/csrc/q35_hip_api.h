@@ -51,7 +51,8 @@ typedef float q35_f32x2 __attribute__((ext_vector_type(2)));
 #ifndef Q35_HOST_EMULATION
 // Exchange with lane l^m inside each 16-lane row, as register-to-register DPP
 // moves (no LDS crossbar): m = 1, 2 are quad_perm [1,0,3,2] / [2,3,0,1];
-// m = 4, 8 combine row_shl:m (lanes with bit m clear) and row_shr:m (set).
+// m = 4 combines row_shl:4 (lanes with bit 2 clear) and row_shr:4 (set);
+// m = 8 is row_ror:8 (a rotation by half the row is the exchange l <-> l^8).
 __device__ __forceinline__ int q35_row_xor_i(int v, int m) {
   switch (m) {
     case 1: return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, true);
@@ -61,11 +62,7 @@ __device__ __forceinline__ int q35_row_xor_i(int v, int m) {
       const int dn = __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);
       return (__lane_id() & 4) ? dn : up;
     }
-    default: {
-      const int up = __builtin_amdgcn_update_dpp(0, v, 0x108, 0xF, 0xF, true);
-      const int dn = __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);
-      return (__lane_id() & 8) ? dn : up;
-    }
+    default: return __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, true);
   }
 }
 __device__ __forceinline__ float q35_row_xor(float v, int m) {

@@ -231,6 +231,42 @@ int gemm_argmax_cand_capacity(int rows, int cu_count);
 // Floats of partial sums a split launch writes (0 when it does not split).
 size_t gemm_partial_floats(int rows, int nb, int tokens, int cu_count);
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t stream);
+// Decode projections of one token tile (at most 16 rows) with a neighbour
+// folded in (fused.hip); both give the bits of the split launch + consumer.
+// gemm_norm: the RMSNorm(1 + w) + H128 preparation of complete residual rows
+// as the prologue of the split projection (plan as launch_gemm with
+// max_split); outputs as launch_gemm's (partials, or out for one split),
+// described for the consumer in *out_rows.
+struct NormGemmArgs {
+  GemmArgs g;                     // w, rows, nb, tokens, partials or out/stride, cu_count
+  int max_split = 32;
+  const float *x = nullptr;       // [tokens][nb * 32] complete residual rows
+  const float *weight = nullptr;  // RMSNorm weight, applied as (1 + w)
+  float eps = 1e-6F;
+  uint64_t seed = 0;
+  const float *sq_groups = nullptr;  // [tokens][nb * 2] group sums of squares (gemm_resid)
+  uint64_t *codes_out = nullptr;  // optional copy of the prepared A16 activations (token tile 0)
+  float *scales_out = nullptr;
+  float *normed_out = nullptr;    // optional normalized rows [tokens][nb * 32]
+};
+bool gemm_norm_fits(int rows, int nb, int tokens, int cu_count, int max_split);
+hipError_t launch_gemm_norm(const NormGemmArgs &a, SplitRows *out_rows, hipStream_t stream);
+// gemm_resid: x_out = residual + the projection of the A16 activations in
+// g.codes/g.scales (every K split of the default plan, summed in split
+// order); proj_out optionally keeps the projection rows. Rows are
+// [tokens][rows]. It also leaves each token's sums of squares of x_out per
+// 16-column group, which the next gemm_norm reads (the norm tree of
+// norm_total_groups).
+struct ResidGemmArgs {
+  GemmArgs g;                     // w, rows, nb, codes, scales, tokens, cu_count
+  const float *residual = nullptr;
+  float *x_out = nullptr;
+  float *proj_out = nullptr;
+  float *sq_groups = nullptr;     // [tokens][rows / 16] sums of squares of x_out per 16-column group
+  int splits = 0;                 // set by the launcher
+};
+bool gemm_resid_fits(int rows, int nb, int tokens, int cu_count);
+hipError_t launch_gemm_resid(const ResidGemmArgs &a, hipStream_t stream);
 // Dense GEMM for many tokens (any count): writes the finished rows to
 // a.out [tokens][stride] with the bits the split launch of the same shape
 // and consumer bound (a.max_split) gives after its consumer's ordered sum;

@@ -85,14 +85,13 @@ __device__ __forceinline__ void h128_quantize_core(float v[8], int blk, bool h12
           v[e] = a + b;
           v[e + s] = a - b;
         }
+    // the partner's value p: a lower lane keeps v + p, an upper lane p - v,
+    // both as one exact fma(v, +-1, p)
 #pragma unroll
     for (int m = 1; m < 16; m <<= 1) {
-      const bool upper = (j & m) != 0;
+      const float sgn = (j & m) != 0 ? -1.0F : 1.0F;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float p = q35_row_xor(v[e], m);
-        v[e] = upper ? p - v[e] : v[e] + p;
-      }
+      for (int e = 0; e < 8; ++e) v[e] = fmaf(v[e], sgn, q35_row_xor(v[e], m));
     }
   }
   float amax = 0.0F;

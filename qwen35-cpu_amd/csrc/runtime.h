@@ -87,6 +87,7 @@ struct q35_runtime {
   float *rope_cos = nullptr, *rope_sin = nullptr;
   // work buffers
   float *x[2] = {nullptr, nullptr};  // residual stream, ping-pong
+  float *sq_groups = nullptr;         // [16][hidden / 16] group sums of squares of the residual rows
   float *proj = nullptr, *q_rot = nullptr, *gates = nullptr;
   float *q8_gates = nullptr;      // Q8 gate rows of the in projection [rows][kMaxGateRows]
   float *rows_final = nullptr;  // chunked steps of split GEMMs: summed in-projection rows [rows][proj_width]
@@ -120,6 +121,8 @@ struct q35_runtime {
     bool counted;  // first kernel of a logical launch
   };
   std::vector<ProfLaunch> prof_pending;
+  // decode steps of one token tile run the fused projections (fused.hip)
+  bool fuse_decode = true;
   // stage trace (test hook): (layer, point) -> device copy and its size
   bool tracing = false;
   std::map<std::pair<int, int>, std::pair<void *, size_t>> trace;

@@ -439,6 +439,8 @@ extern "C" int q35_runtime_create(q35_model *m, const q35_runtime_config *cfg, q
   // work buffers
   alloc(static_cast<size_t>(R) * H * 4, reinterpret_cast<void **>(&rt->x[0]));
   alloc(static_cast<size_t>(R) * H * 4, reinterpret_cast<void **>(&rt->x[1]));
+  // group sums of squares of the residual rows (fused decode projections: 16 rows)
+  alloc(static_cast<size_t>(16) * (H / 16) * 4, reinterpret_cast<void **>(&rt->sq_groups));
   // GEMM outputs: [split][rows][width] for the largest split plan of any
   // projection at any row count a step can have (split launches), and
   // [rows][width] for the dense GEMM
@@ -815,6 +817,7 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
     return launch_gemm(g, s);
   };
   // Residual update with the pending split rows (if `add`) + RMSNorm + prep.
+  bool groups_ready = false;  // rt->sq_groups holds the sums of squares of x[cur] (set by gemm_resid)
   auto rms_prep = [&](const float *w, bool add, bool h128, float *normed,
                       const LayerDev *gate_layer = nullptr) -> hipError_t {
     RmsPrepArgs a;
@@ -839,13 +842,70 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
     a.scales = rt->scales;
     a.normed_out = normed;
     const hipError_t e = launch_rms_prep(a, s);
-    if (add) cur ^= 1;
+    if (add) {
+      cur ^= 1;
+      groups_ready = false;
+    }
     return e;
   };
   // bytes: residual row in (+ split partial rows and the new residual out),
   // codes and scales out
   auto rms_bytes = [&](bool add) {
     return B * (H * 4.0 + (add ? pending.splits * H * 4.0 + H * 4.0 : 0.0) + H + H / 32.0 * 4.0) + H * 4.0;
+  };
+  // Steps of one token tile fold the residual + RMSNorm preparations into
+  // the projections (fused.hip): the in / qkv and gate_up projections
+  // normalize and prepare complete residual rows in their prologue, and the
+  // out / o and down projections finish their rows with the residual added.
+  // Same bits as the split launches and rms_prep (q35_runtime_set_fused).
+  const bool fuse = rt->fuse_decode && batch <= 16;
+  constexpr bool fuse_down = false;
+  auto gemm_norm = [&](const q35_q4_0_block_x8 *w, int rows, const float *norm_w, int max_split,
+                       float *normed) -> hipError_t {
+    NormGemmArgs a;
+    a.g.w = w;
+    a.g.rows = rows;
+    a.g.nb = H / 32;
+    a.g.tokens = batch;
+    a.g.out = rt->proj;
+    a.g.stride = rows;
+    a.g.partials = rt->proj;
+    a.g.cu_count = ctx->cu_count;
+    a.max_split = max_split;
+    a.x = rt->x[cur];
+    a.sq_groups = rt->sq_groups;
+    a.weight = norm_w;
+    a.eps = d.rms_eps;
+    a.seed = d.sign_seed;
+    a.normed_out = normed;
+    if (normed != nullptr) {  // the stage trace copies the prepared activations
+      a.codes_out = rt->codes;
+      a.scales_out = rt->scales;
+    }
+    return launch_gemm_norm(a, &pending, s);
+  };
+  auto gemm_resid = [&](const q35_q4_0_block_x8 *w, int K, float *proj_out) -> hipError_t {
+    ResidGemmArgs a;
+    a.g.w = w;
+    a.g.rows = H;
+    a.g.nb = K / 32;
+    a.g.codes = rt->codes;
+    a.g.scales = rt->scales;
+    a.g.tokens = batch;
+    a.g.cu_count = ctx->cu_count;
+    a.residual = rt->x[cur];
+    a.x_out = rt->x[cur ^ 1];
+    a.proj_out = proj_out;
+    a.sq_groups = rt->sq_groups;
+    const hipError_t e = launch_gemm_resid(a, s);
+    cur ^= 1;
+    groups_ready = true;
+    return e;
+  };
+  auto norm_bytes = [&](int rows, int max_split) {
+    const GemmPlan p = gemm_plan(rows, H / 32, false, false, ctx->cu_count, 0, 0, max_split);
+    return gemm_algorithmic_bytes(rows, H / 32, batch, true, false) + (p.split - 1) * B * rows * 4.0 + B * H * 4.0 +
+           H * 4.0 - B * (H + 4.0);  // residual rows and the norm weight in; no A16 activations read
   };
   auto gemm_bytes = [&](int rows, int K, int max_split = 32) {
     if (gemm_dense_fits(rows, batch, ctx->cu_count)) return gemm_algorithmic_bytes(rows, K / 32, batch, true, false);
@@ -905,8 +965,15 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
   for (int l = 0; l < d.n_layers; ++l) {
     const LayerDev &L = m->layers[l];
     float *normed_in = tracing ? trace_fp32(l, Q35_TRACE_NORMED_IN, H) : nullptr;
-    Q35_KERNEL(Q35_KERNEL_PREP, rms_bytes(add_pending), rms_prep(L.input_norm, add_pending, true, normed_in, L.linear ? &L : nullptr),
-               "input norm prep");
+    const bool fuse_in = fuse && groups_ready && !add_pending && L.gate_rows == 0 &&
+                         gemm_norm_fits(L.in_rows, H / 32, batch, ctx->cu_count, kConsumerSplits);
+    if (fuse_in) {
+      Q35_KERNEL(Q35_KERNEL_GEMM, norm_bytes(L.in_rows, kConsumerSplits),
+                 gemm_norm(L.in_proj, L.in_rows, L.input_norm, kConsumerSplits, normed_in), "norm + in projection");
+    } else {
+      Q35_KERNEL(Q35_KERNEL_PREP, rms_bytes(add_pending),
+                 rms_prep(L.input_norm, add_pending, true, normed_in, L.linear ? &L : nullptr), "input norm prep");
+    }
     if (tracing) {
       Q35_STEP(trace_copy(rt, l, Q35_TRACE_X_IN, rt->x[cur], static_cast<size_t>(batch) * H * 4, s), "trace");
       Q35_STEP(trace_codes(l, Q35_TRACE_CODES_IN, H), "trace");
@@ -914,8 +981,9 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
         Q35_STEP(trace_copy(rt, l, Q35_TRACE_GATES, rt->q8_gates, static_cast<size_t>(batch) * L.gate_rows * 4, s),
                  "trace");
     }
-    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(L.in_rows, H, kConsumerSplits),
-               gemm(L.in_proj, L.in_rows, H, kConsumerSplits), "in projection");
+    if (!fuse_in)
+      Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(L.in_rows, H, kConsumerSplits),
+                 gemm(L.in_proj, L.in_rows, H, kConsumerSplits), "in projection");
     if (tracing) Q35_STEP(trace_rows(l, Q35_TRACE_PROJ_IN, L.in_rows), "trace");
     if (L.linear) {
       const int li = m->linear_index[l];
@@ -1052,16 +1120,31 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
                  "attention merge");
       if (tracing) Q35_STEP(trace_codes(l, Q35_TRACE_CODES_CORE, d.n_heads * d.head_dim), "trace");
     }
-    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(H, L.out_cols), gemm(L.out_proj, H, L.out_cols), "out projection");
-    if (tracing) Q35_STEP(trace_rows(l, Q35_TRACE_PROJ_OUT, H), "trace");
+    const bool fuse_out = fuse && gemm_resid_fits(H, L.out_cols / 32, batch, ctx->cu_count);
+    if (fuse_out) {
+      Q35_KERNEL(Q35_KERNEL_GEMM, gemm_algorithmic_bytes(H, L.out_cols / 32, batch, true, true),
+                 gemm_resid(L.out_proj, L.out_cols, tracing ? trace_fp32(l, Q35_TRACE_PROJ_OUT, H) : nullptr),
+                 "out projection + residual");
+    } else {
+      Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(H, L.out_cols), gemm(L.out_proj, H, L.out_cols), "out projection");
+      if (tracing) Q35_STEP(trace_rows(l, Q35_TRACE_PROJ_OUT, H), "trace");
+    }
     float *normed_post = tracing ? trace_fp32(l, Q35_TRACE_NORMED_POST, H) : nullptr;
-    Q35_KERNEL(Q35_KERNEL_PREP, rms_bytes(true), rms_prep(L.post_norm, true, true, normed_post), "post norm prep");
+    const bool fuse_post = fuse_out && gemm_norm_fits(2 * I, H / 32, batch, ctx->cu_count, kConsumerSplits);
+    if (fuse_post) {
+      Q35_KERNEL(Q35_KERNEL_GEMM, norm_bytes(2 * I, kConsumerSplits),
+                 gemm_norm(L.gate_up, 2 * I, L.post_norm, kConsumerSplits, normed_post), "post norm + gate_up projection");
+    } else {
+      Q35_KERNEL(Q35_KERNEL_PREP, rms_bytes(!fuse_out), rms_prep(L.post_norm, !fuse_out, true, normed_post),
+                 "post norm prep");
+    }
     if (tracing) {
       Q35_STEP(trace_copy(rt, l, Q35_TRACE_X_MID, rt->x[cur], static_cast<size_t>(batch) * H * 4, s), "trace");
       Q35_STEP(trace_codes(l, Q35_TRACE_CODES_POST, H), "trace");
     }
-    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(2 * I, H, kConsumerSplits), gemm(L.gate_up, 2 * I, H, kConsumerSplits),
-               "gate_up projection");
+    if (!fuse_post)
+      Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(2 * I, H, kConsumerSplits), gemm(L.gate_up, 2 * I, H, kConsumerSplits),
+                 "gate_up projection");
     if (tracing) Q35_STEP(trace_rows(l, Q35_TRACE_GATE_UP, 2 * I), "trace");
     PrepArgs sp;
     sp.source = kPrepSiluMul;
@@ -1076,9 +1159,19 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
     Q35_KERNEL(Q35_KERNEL_PREP, B * (pending.splits * 2.0 * I * 4.0 + I + I / 32.0 * 4.0), launch_prep(sp, s),
                "silu prep");
     if (tracing) Q35_STEP(trace_codes(l, Q35_TRACE_CODES_DOWN, I), "trace");
-    Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(H, I), gemm(L.down, H, I), "down projection");
-    if (tracing) Q35_STEP(trace_rows(l, Q35_TRACE_DOWN, H), "trace");
-    add_pending = true;
+    // the down projection stays split: owning all of its K splits, a
+    // 16-row workgroup re-reads every activation code (K x 16 bytes), and the
+    // next input norm then runs as rms_prep + the split in projection
+    if (fuse && fuse_down && gemm_resid_fits(H, I / 32, batch, ctx->cu_count)) {
+      Q35_KERNEL(Q35_KERNEL_GEMM, gemm_algorithmic_bytes(H, I / 32, batch, true, true),
+                 gemm_resid(L.down, I, tracing ? trace_fp32(l, Q35_TRACE_DOWN, H) : nullptr),
+                 "down projection + residual");
+      add_pending = false;
+    } else {
+      Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(H, I), gemm(L.down, H, I), "down projection");
+      if (tracing) Q35_STEP(trace_rows(l, Q35_TRACE_DOWN, H), "trace");
+      add_pending = true;
+    }
   }
   // Final norm and head on the head rows: every row of a decode step, the
   // last position of each segment that wants a token otherwise (hidden_out
@@ -1087,8 +1180,10 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
   {
     RmsPrepArgs a;
     a.x_in = rt->x[cur];
-    a.add = pending;
-    a.x_out = rt->x[cur ^ 1];
+    if (add_pending) {
+      a.add = pending;
+      a.x_out = rt->x[cur ^ 1];
+    }
     a.weight = m->final_norm;
     a.eps = d.rms_eps;
     a.tokens = heads;
@@ -1100,10 +1195,10 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
     a.normed_out = rt->hidden_out;
     a.rows = sh.heads_identity ? nullptr : head_rows;
     const double HR = heads;
-    Q35_KERNEL(Q35_KERNEL_PREP, HR * (H * 4.0 + pending.splits * H * 4.0 + H * 4.0 + H + H / 32.0 * 4.0) + H * 4.0 +
-                                    HR * H * 4.0,
+    const double add_rows = add_pending ? pending.splits * H * 4.0 + H * 4.0 : 0.0;
+    Q35_KERNEL(Q35_KERNEL_PREP, HR * (H * 4.0 + add_rows + H + H / 32.0 * 4.0) + H * 4.0 + HR * H * 4.0,
                launch_rms_prep(a, s), "final norm prep");
-    cur ^= 1;
+    if (add_pending) cur ^= 1;
   }
   if (tracing) {
     const int fl = d.n_layers;
@@ -1512,6 +1607,16 @@ extern "C" int q35_runtime_profile_read(q35_runtime *rt, int cls, double *total_
   if (total_ms) *total_ms = rt->prof_ms[cls];
   if (launches) *launches = rt->prof_launches[cls];
   if (bytes) *bytes = rt->prof_bytes[cls];
+  return Q35_OK;
+}
+
+extern "C" int q35_runtime_set_fused(q35_runtime *rt, int enable) {
+  if (rt == nullptr) return Q35_ERR_INVALID;
+  if (rt->fuse_decode != (enable != 0)) {
+    for (auto &kv : rt->graphs) (void)hipGraphExecDestroy(kv.second);
+    rt->graphs.clear();
+  }
+  rt->fuse_decode = enable != 0;
   return Q35_OK;
 }
 

@@ -114,14 +114,17 @@ def upload_model(q, ctx, d, sched, tensors):
 
 
 def hip_greedy(q, ctx, d, sched, tensors, prompts, new_tokens, penalty=1.0, want_logits=False,
-               use_graphs=True, page_tokens=16, model=None):
-    """Same schedule as oracle_greedy on the HIP runtime."""
+               use_graphs=True, page_tokens=16, model=None, fused=None):
+    """Same schedule as oracle_greedy on the HIP runtime (fused: the fused
+    decode projections on or off; None keeps the runtime's default)."""
     model = model or upload_model(q, ctx, d, sched, tensors)
     prompts = np.asarray(prompts, np.int32)
     b, plen = prompts.shape
     ctx_len = plen + new_tokens + 8
     rt = q.Runtime(model, max_slots=b, max_batch=b, max_context=ctx_len, page_tokens=page_tokens,
                    use_graphs=use_graphs)
+    if fused is not None:
+        rt.set_fused(fused)
     slots = np.array([rt.slot_alloc(prompts[r]) for r in range(b)], np.int32)
     table = np.zeros((b, rt.max_pages), np.int32)
     npages = 0

@@ -71,6 +71,23 @@ def test_graph_replay_equals_eager(q, ctx, small):
     assert np.array_equal(a, b) and np.array_equal(la, lb)
 
 
+def test_fused_projections_equal_general_path(q, ctx, small):
+    """Steps of at most 16 rows fold the residual + RMSNorm + H128 preparation
+    into the projections that consume it and finish the out / down
+    projections with the residual added; that path must give the bits of the
+    general split launches + preparation kernels (which chunked prefill and
+    larger batches run), in graph replay and eagerly."""
+    d, sched, tensors, model = small
+    prompts = np.random.default_rng(4).integers(0, d["vocab"], size=(5, 14)).astype(np.int32)
+    for graphs in (True, False):
+        a, la = hip_greedy(q, ctx, d, sched, tensors, prompts, 6, want_logits=True, use_graphs=graphs, model=model,
+                           fused=True)
+        b, lb = hip_greedy(q, ctx, d, sched, tensors, prompts, 6, want_logits=True, use_graphs=graphs, model=model,
+                           fused=False)
+        assert np.array_equal(a, b)
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+
+
 def test_penalty_and_page_sizes(q, ctx, orc, small):
     d, sched, tensors, model = small
     prompts = np.random.default_rng(4).integers(0, 64, size=(2, 20)).astype(np.int32)
