@@ -1,12 +1,12 @@
 // GatedDeltaNet decode update on CDNA4.
 //
-// One workgroup (256 threads) per (value head, request). The head's fp32
+// One workgroup (512 threads) per (value head, request). The head's fp32
 // state tile [value_row][key_col] = 128 x 128 (64 KiB) makes exactly one HBM
 // round trip; its loads are issued right after the head's few small inputs
 // (conv ring, projections, weights), so the 64 KiB are in flight while those
 // are combined.
 // Sixteen lanes share a value row: lane o = t % 16 owns the two float4 at
-// columns 4o + 64m (m = 0, 1), and thread t owns rows t/16 + 16j (j = 0..7).
+// columns 4o + 64m (m = 0, 1), and thread t owns rows t/16 + 32j (j = 0..3).
 // A row's dot products are summed per lane in column order and then across
 // its 16 lanes with four DPP exchanges (xor 1, 2, 4, 8) -- delta_row below,
 // shared with the prefill chunk scan so both give the same bits -- and one
@@ -38,6 +38,11 @@ constexpr int kDim = 128;
 constexpr int kConvKernel = 4;  // linear_conv_kernel_dim of every Qwen3.5 size
 constexpr int kRowLanes = 16;                                    // lanes per value row
 constexpr int kRowsPerThread = kDim * kRowLanes / kDeltaThreads;  // 8
+// decode: 512 threads per (value head, request), four value rows per thread
+// (rows rowg + 32j), so two wavefronts per SIMD overlap the row updates
+constexpr int kDecodeThreads = 512;
+constexpr int kDecodeRowStride = kDecodeThreads / kRowLanes;  // 32
+constexpr int kDecodeRows = kDim / kDecodeRowStride;           // 4
 
 // The delta rule on one value row held by 16 lanes (this lane: columns
 // 4o + 64m, m = 0, 1), in the reference's order (delta_net.cpp:63-98):
@@ -76,7 +81,7 @@ __device__ __forceinline__ float delta_row(q35_f32x4 st[2], const q35_f32x4 kc[2
 // FUSED: the linear-attention step around the update; MS: compile-time bound
 // on the in-projection's K splits (so every input load is straight-line).
 template <bool FUSED, int MS>
-__global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
+__global__ __launch_bounds__(kDecodeThreads) void delta_kernel(DeltaArgs a) {
   __shared__ float sq[kDim], sk[kDim], sv[kDim], so[kDim];
   __shared__ float red[8];
   __shared__ float s_alpha, s_beta;
@@ -84,7 +89,10 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int per = a.v_heads / a.k_heads;
   const int kh = vh / per;
-  const int col = tid & (kRowLanes - 1), rowg = tid >> 4;  // rows rowg + 16j
+  const int col = tid & (kRowLanes - 1), rowg = tid >> 4;  // rows rowg + 32j
+  // the input phase runs on 256 threads' worth of channels; threads 256..511
+  // repeat threads 0..255 (the same loads and the same values stored)
+  const int itid = tid & (kDeltaThreads - 1);
 
   // state tile pointers (the loads are issued after this head's small inputs,
   // so those arrive first: on gfx9 loads retire in issue order)
@@ -103,12 +111,12 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
   }
   q35_f32x4 *S = reinterpret_cast<q35_f32x4 *>(state_r + static_cast<size_t>(vh) * kDim * kDim) + rowg * (kDim / 4) + col;
   q35_f32x4 *W = reinterpret_cast<q35_f32x4 *>(reinterpret_cast<float *>(S) + write_offset);
-  q35_f32x4 st[kRowsPerThread][2];
+  q35_f32x4 st[kDecodeRows][2];
   auto load_state = [&]() {
 #pragma unroll
-    for (int j = 0; j < kRowsPerThread; ++j)
+    for (int j = 0; j < kDecodeRows; ++j)
 #pragma unroll
-      for (int m = 0; m < 2; ++m) st[j][m] = Q35_LOAD_NT(S + j * 16 * (kDim / 4) + 16 * m);
+      for (int m = 0; m < 2; ++m) st[j][m] = Q35_LOAD_NT(S + j * kDecodeRowStride * (kDim / 4) + 16 * m);
   };
 
   // ---- 2. q, k, v, gates of this head: every load first (the conv ring is
@@ -124,10 +132,10 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
     const int pos = a.positions[r];
     // threads 0..127: q channel, 128..255: k channel of key head kh; threads
     // 0..127 also own the v channel of value head vh
-    const int i = tid & (kDim - 1);
-    const bool is_k = tid >= kDim, has_v = tid < kDim;
+    const int i = itid & (kDim - 1);
+    const bool is_k = itid >= kDim, has_v = itid < kDim;
     const int chq = (is_k ? q_dim : 0) + kh * kDim + i;
-    const int chv = has_v ? 2 * q_dim + vh * kDim + tid : chq;
+    const int chv = has_v ? 2 * q_dim + vh * kDim + itid : chq;
     // raw (split) loads of every small input first, then the state tile,
     // then the reductions
     float xq_s[MS], xv_s[MS], b_s[MS], a_s[MS];
@@ -184,7 +192,7 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
     // L2 norms of q (waves 0-1) and k (waves 2-3) over 128 values
     const float ss = wave_sum(yq * yq);
     if (lane == 0) red[wave] = ss;
-    if (has_v) sv[tid] = yv;
+    if (has_v) sv[itid] = yv;
     lds_barrier();
     const float tot = is_k ? red[2] + red[3] : red[0] + red[1];
     const float scale = is_k ? 1.0F : 1.0F / sqrtf(static_cast<float>(kDim));
@@ -217,8 +225,8 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
     qc[m] = *reinterpret_cast<const q35_f32x4 *>(sq + 4 * col + 64 * m);
   }
 #pragma unroll
-  for (int j = 0; j < kRowsPerThread; ++j) {
-    const int row = rowg + 16 * j;
+  for (int j = 0; j < kDecodeRows; ++j) {
+    const int row = rowg + kDecodeRowStride * j;
     const float o = delta_row(st[j], kc, qc, sv[row], alpha, beta);
     if (col == 0) so[row] = o;
   }
@@ -228,9 +236,9 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_kernel(DeltaArgs a) {
   lds_barrier();
   auto store_state = [&]() {
 #pragma unroll
-    for (int j = 0; j < kRowsPerThread; ++j)
+    for (int j = 0; j < kDecodeRows; ++j)
 #pragma unroll
-      for (int m = 0; m < 2; ++m) Q35_STORE_NT(st[j][m], W + j * 16 * (kDim / 4) + 16 * m);
+      for (int m = 0; m < 2; ++m) Q35_STORE_NT(st[j][m], W + j * kDecodeRowStride * (kDim / 4) + 16 * m);
   };
   if (wave != 0) {
     store_state();
@@ -524,7 +532,7 @@ __global__ __launch_bounds__(64) void delta_chunk_out_kernel(DeltaArgs a) {
 hipError_t launch_delta(const DeltaArgs &a, hipStream_t stream) {
   if (a.batch <= 0) return hipSuccess;
   if (a.kd != kDim || a.vd != kDim || a.v_heads % a.k_heads != 0) return hipErrorInvalidValue;
-  const dim3 grid(a.v_heads, a.batch), block(kDeltaThreads);
+  const dim3 grid(a.v_heads, a.batch), block(kDecodeThreads);
   if (!a.fused) {
     Q35_LAUNCH((delta_kernel<false, 1>), grid, block, 0, stream, a);
     return hipGetLastError();
