@@ -608,10 +608,13 @@ def main():
                  if not sfx else "head_kernel<4, 2, NT, true, *, true> (greedy G16 head: Q4G16Tile GEMV, per-half "
                  "MFMA dots + penalty + argmax)")
     head_roof = roofline("head" + sfx, prof["head"], traffic, head_name) if prof else None
-    # the dominant kernel class: the per-layer Q4 projections (split-K
-    # single-token-tile launches at B <= 16)
+    # the dominant kernel class: the per-layer Q4 projections (at B <= 16:
+    # split-K launches, the out / o projection with its residual, and the
+    # gate_up projection with the post-attention norm in its prologue)
     roof = roofline("gemm" + sfx, prof["gemm"], traffic,
-                    "gemm_rows_kernel<KS, RM> (per-layer Q4 projections: in, out, gate_up, down; split-K)") \
+                    "per-layer Q4 projections: gemm_rows_kernel<KS, RM> (in / qkv, down; split-K), "
+                    "gemm_resid_kernel<BPS, W> (out / o, all K splits + residual in one workgroup), "
+                    "gemm_norm_kernel<RM, NQ, BPS> (post-attention RMSNorm + H128 prologue, gate_up; split-K)") \
         if prof else None
     breakdown = ({k: {"us_per_step": round(v[0] / args.profile_steps * 1000.0, 1),
                       "launches_per_step": v[1] // args.profile_steps} for k, v in prof.items() if v[1]}

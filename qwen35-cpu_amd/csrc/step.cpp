@@ -905,7 +905,8 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
   auto norm_bytes = [&](int rows, int max_split) {
     const GemmPlan p = gemm_plan(rows, H / 32, false, false, ctx->cu_count, 0, 0, max_split);
     return gemm_algorithmic_bytes(rows, H / 32, batch, true, false) + (p.split - 1) * B * rows * 4.0 + B * H * 4.0 +
-           H * 4.0 - B * (H + 4.0);  // residual rows and the norm weight in; no A16 activations read
+           H * 4.0 + B * (H / 16) * 4.0 - B * (H + 4.0);  // residual rows, group sums and the norm weight in;
+                                                            // no A16 activations read
   };
   auto gemm_bytes = [&](int rows, int K, int max_split = 32) {
     if (gemm_dense_fits(rows, batch, ctx->cu_count)) return gemm_algorithmic_bytes(rows, K / 32, batch, true, false);
