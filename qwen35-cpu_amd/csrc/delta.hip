@@ -1,12 +1,12 @@
 // GatedDeltaNet decode update on CDNA4.
 //
-// One workgroup (512 threads) per (value head, request). The head's fp32
+// One workgroup (256 or 512 threads) per (value head, request). The head's fp32
 // state tile [value_row][key_col] = 128 x 128 (64 KiB) makes exactly one HBM
 // round trip; its loads are issued right after the head's few small inputs
 // (conv ring, projections, weights), so the 64 KiB are in flight while those
 // are combined.
 // Sixteen lanes share a value row: lane o = t % 16 owns the two float4 at
-// columns 4o + 64m (m = 0, 1), and thread t owns rows t/16 + 32j (j = 0..3).
+// columns 4o + 64m (m = 0, 1), and thread t owns rows t/16 + (threads/16) j.
 // A row's dot products are summed per lane in column order and then across
 // its 16 lanes with four DPP exchanges (xor 1, 2, 4, 8) -- delta_row below,
 // shared with the prefill chunk scan so both give the same bits -- and one
@@ -38,11 +38,12 @@ constexpr int kDim = 128;
 constexpr int kConvKernel = 4;  // linear_conv_kernel_dim of every Qwen3.5 size
 constexpr int kRowLanes = 16;                                    // lanes per value row
 constexpr int kRowsPerThread = kDim * kRowLanes / kDeltaThreads;  // 8
-// decode: 512 threads per (value head, request), four value rows per thread
-// (rows rowg + 32j), so two wavefronts per SIMD overlap the row updates
-constexpr int kDecodeThreads = 512;
-constexpr int kDecodeRowStride = kDecodeThreads / kRowLanes;  // 32
-constexpr int kDecodeRows = kDim / kDecodeRowStride;           // 4
+// decode: THREADS (256 or 512) per (value head, request), kDim * 16 /
+// THREADS value rows per thread (rows rowg + THREADS/16 * j). 512 threads
+// let two wavefronts per SIMD overlap the row updates when the grid leaves
+// most of the GPU idle (256 workgroups at 16 requests); with many
+// workgroups (64 requests of the 4B shape: 2048) 256 threads keep more
+// (head, request) tiles resident per compute unit and measure faster.
 
 // The delta rule on one value row held by 16 lanes (this lane: columns
 // 4o + 64m, m = 0, 1), in the reference's order (delta_net.cpp:63-98):
@@ -80,8 +81,10 @@ __device__ __forceinline__ float delta_row(q35_f32x4 st[2], const q35_f32x4 kc[2
 
 // FUSED: the linear-attention step around the update; MS: compile-time bound
 // on the in-projection's K splits (so every input load is straight-line).
-template <bool FUSED, int MS>
-__global__ __launch_bounds__(kDecodeThreads) void delta_kernel(DeltaArgs a) {
+template <bool FUSED, int MS, int THREADS>
+__global__ __launch_bounds__(THREADS) void delta_kernel(DeltaArgs a) {
+  constexpr int kDecodeRowStride = THREADS / kRowLanes;
+  constexpr int kDecodeRows = kDim / kDecodeRowStride;
   __shared__ float sq[kDim], sk[kDim], sv[kDim], so[kDim];
   __shared__ float red[8];
   __shared__ float s_alpha, s_beta;
@@ -89,9 +92,10 @@ __global__ __launch_bounds__(kDecodeThreads) void delta_kernel(DeltaArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int per = a.v_heads / a.k_heads;
   const int kh = vh / per;
-  const int col = tid & (kRowLanes - 1), rowg = tid >> 4;  // rows rowg + 32j
-  // the input phase runs on 256 threads' worth of channels; threads 256..511
-  // repeat threads 0..255 (the same loads and the same values stored)
+  const int col = tid & (kRowLanes - 1), rowg = tid >> 4;  // rows rowg + (THREADS / 16) j
+  // the input phase runs on 256 threads' worth of channels; with 512
+  // threads, threads 256..511 repeat threads 0..255 (the same loads and the
+  // same values stored)
   const int itid = tid & (kDeltaThreads - 1);
 
   // state tile pointers (the loads are issued after this head's small inputs,
@@ -532,18 +536,26 @@ __global__ __launch_bounds__(64) void delta_chunk_out_kernel(DeltaArgs a) {
 hipError_t launch_delta(const DeltaArgs &a, hipStream_t stream) {
   if (a.batch <= 0) return hipSuccess;
   if (a.kd != kDim || a.vd != kDim || a.v_heads % a.k_heads != 0) return hipErrorInvalidValue;
-  const dim3 grid(a.v_heads, a.batch), block(kDecodeThreads);
+  const dim3 grid(a.v_heads, a.batch);
+  // 512 threads while the grid is at most two workgroups per compute unit
+  const bool wide = a.v_heads * a.batch <= 512;
+#define Q35_DELTA(F, MS)                                                                   \
+  if (wide)                                                                                \
+    Q35_LAUNCH((delta_kernel<F, MS, 512>), grid, dim3(512), 0, stream, a);                 \
+  else                                                                                     \
+    Q35_LAUNCH((delta_kernel<F, MS, 256>), grid, dim3(256), 0, stream, a);
   if (!a.fused) {
-    Q35_LAUNCH((delta_kernel<false, 1>), grid, block, 0, stream, a);
+    Q35_DELTA(false, 1)
     return hipGetLastError();
   }
   if (a.kernel != kConvKernel) return hipErrorInvalidValue;
   switch (split_bound(a.proj.splits)) {
-    case 1: Q35_LAUNCH((delta_kernel<true, 1>), grid, block, 0, stream, a); break;
-    case 4: Q35_LAUNCH((delta_kernel<true, 4>), grid, block, 0, stream, a); break;
-    case 8: Q35_LAUNCH((delta_kernel<true, 8>), grid, block, 0, stream, a); break;
+    case 1: Q35_DELTA(true, 1) break;
+    case 4: Q35_DELTA(true, 4) break;
+    case 8: Q35_DELTA(true, 8) break;
     default: return hipErrorInvalidValue;
   }
+#undef Q35_DELTA
   return hipGetLastError();
 }
 
