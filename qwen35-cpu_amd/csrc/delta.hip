@@ -148,9 +148,22 @@ __global__ __launch_bounds__(THREADS) void delta_kernel(DeltaArgs a) {
     a.proj.template load<MS>(r, chv, xv_s);
     a.proj.template load8<MS>(r, channels + vh * kDim + 8 * (lane & 15), z_s);
     // with separate gate rows the projection row is [qkv | z] only
-    const bool sep = a.gates != nullptr;
-    a.proj.template load<MS>(r, sep ? chq : channels + v_dim + vh, b_s);
-    a.proj.template load<MS>(r, sep ? chq : channels + v_dim + a.v_heads + vh, a_s);
+    // b and a of this head: projection columns, or (Q8 gate tail) the
+    // separate gate rows [batch][2 v_heads] read as one split -- one view, so
+    // the loads are issued here, before the state, under no branch (a load
+    // under a branch holds its join until every load in flight returns)
+    SplitRows ba = a.proj;
+    int cb = channels + v_dim + vh, ca = channels + v_dim + a.v_heads + vh;
+    if (a.gates != nullptr) {
+      ba.p = a.gates;
+      ba.splits = 1;
+      ba.split_stride = 0;
+      ba.width = 2 * a.v_heads;
+      cb = vh;
+      ca = a.v_heads + vh;
+    }
+    ba.template load<MS>(r, cb, b_s);
+    ba.template load<MS>(r, ca, a_s);
     float hq[K - 1], hv[K - 1], wq[K], wv[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -172,9 +185,8 @@ __global__ __launch_bounds__(THREADS) void delta_kernel(DeltaArgs a) {
     const float xq = a.proj.template reduce<MS>(xq_s);
     const float xv = a.proj.template reduce<MS>(xv_s);
     a.proj.template reduce8<MS>(z_s, z);
-    const float bval = sep ? a.gates[static_cast<size_t>(r) * 2 * a.v_heads + vh] : a.proj.template reduce<MS>(b_s);
-    const float aval =
-        sep ? a.gates[static_cast<size_t>(r) * 2 * a.v_heads + a.v_heads + vh] : a.proj.template reduce<MS>(a_s);
+    const float bval = ba.template reduce<MS>(b_s);
+    const float aval = ba.template reduce<MS>(a_s);
     // causal conv1d + SiLU (activation.cpp:164-222: x * w[K-1] first, then
     // the history oldest first)
     float yq = xq * wq[K - 1], yv = xv * wv[K - 1];
