@@ -430,12 +430,14 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(AttnArgs a, const f
   const q35_f32x4 gate_lo = *reinterpret_cast<const q35_f32x4 *>(gates + o);
   const q35_f32x4 gate_hi = *reinterpret_cast<const q35_f32x4 *>(gates + o + 4);
   const int seq = a.seq_lens != nullptr ? a.seq_lens[r] : a.positions[r] + 1;
-  const int splits = (seq + kChunkTokens - 1) / kChunkTokens;
+  // the first statistics and partial rows are read at indices bounded by the
+  // buffer (max_splits), not by the chunk count, so they do not wait for the
+  // context length; chunks past the context are masked below and never used
   q35_f32x4 rows[kMergeBatch][2];
-  auto load_rows = [&](int s0) {
+  auto load_rows = [&](int s0, int bound) {
 #pragma unroll
     for (int u = 0; u < kMergeBatch; ++u) {
-      const q35_f32x4 *src = reinterpret_cast<const q35_f32x4 *>(a.part_o + (hs + min(s0 + u, splits - 1)) * kHeadDim + d0);
+      const q35_f32x4 *src = reinterpret_cast<const q35_f32x4 *>(a.part_o + (hs + min(s0 + u, bound - 1)) * kHeadDim + d0);
       rows[u][0] = src[0];
       rows[u][1] = src[1];
     }
@@ -444,12 +446,13 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(AttnArgs a, const f
   // stays in registers
   float m0 = -INFINITY, l0 = 0.0F;
   {
-    const int s = min(lane, splits - 1);
+    const int s = min(lane, a.max_splits - 1);
     m0 = a.part_ml[(hs + s) * 2];
     l0 = a.part_ml[(hs + s) * 2 + 1];
-    if (lane >= splits) m0 = -INFINITY;
   }
-  load_rows(0);
+  load_rows(0, a.max_splits);
+  const int splits = (seq + kChunkTokens - 1) / kChunkTokens;
+  if (lane >= splits) m0 = -INFINITY;
   float M = m0;
   for (int s = lane + 64; s < splits; s += 64) M = fmaxf(M, a.part_ml[(hs + s) * 2]);
   M = group_max<64>(M);
@@ -469,7 +472,7 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(AttnArgs a, const f
     }
     L += group_sum<64>(lw);
     for (int s = 0; s < cnt; s += kMergeBatch) {
-      if (s0 + s > 0) load_rows(s0 + s);
+      if (s0 + s > 0) load_rows(s0 + s, splits);
 #pragma unroll
       for (int u = 0; u < kMergeBatch; ++u) {
         if (s + u >= cnt) break;

@@ -34,6 +34,9 @@ constexpr int kNormWaves = 8;      // wavefronts per gemm_norm workgroup (512 th
 constexpr int kNormMaxGroups = 5;  // H128 groups one K split touches (staged in LDS)
 constexpr int kResidMaxSplits = 32;
 constexpr int kResidMaxBlocks = 512;  // K / 32 of a residual projection (activation scales in LDS)
+// staged scale slots: every block's 16, plus room for the clamped copies a
+// staging batch of 4 x 1024 threads writes past them
+constexpr int kResidScaleSlots = kResidMaxBlocks * 16 + 4 * 1024;
 
 // The int32 block dots of one block for RM rows and 4 tokens (the -8
 // correction MFMA seeds C, so D is the reference's exact dot).
@@ -213,7 +216,7 @@ template <int BPS, int MAXW>
 __global__ __launch_bounds__(64 * MAXW) void gemm_resid_kernel(ResidGemmArgs a) {
   typedef RowWords<1> RW;
   __shared__ float part[kResidMaxSplits * 256];  // [split][token slot][row]
-  __shared__ __align__(16) float lsc[kResidMaxBlocks * 16];
+  __shared__ __align__(16) float lsc[kResidScaleSlots];
   const GemmArgs &g = a.g;
   const int W = static_cast<int>(blockDim.x) >> 6;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -246,15 +249,15 @@ __global__ __launch_bounds__(64 * MAXW) void gemm_resid_kernel(ResidGemmArgs a) 
   };
   int s = wave;
   if (s < S) load(s);
+  // the staged copies past nsc land in LDS padding (no store under a branch,
+  // which would wait for every load in flight, the split's weights included)
 #pragma unroll
-  for (int k = 0; k < 4; ++k)
-    if (k * bd + tid < nsc) lsc[k * bd + tid] = sc[k];
+  for (int k = 0; k < 4; ++k) lsc[min(k * bd + tid, kResidScaleSlots - 1)] = sc[k];
   for (int base = 4 * bd; base < nsc; base += 4 * bd) {  // wider K: more batches
 #pragma unroll
     for (int k = 0; k < 4; ++k) sc[k] = g.scales[min(base + k * bd + tid, nsc - 1)];
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-      if (base + k * bd + tid < nsc) lsc[base + k * bd + tid] = sc[k];
+    for (int k = 0; k < 4; ++k) lsc[min(base + k * bd + tid, kResidScaleSlots - 1)] = sc[k];
   }
   lds_barrier();
   while (s < S) {
