@@ -146,12 +146,7 @@ __device__ __forceinline__ float tile_max(float v) {
   v = fmaxf(v, q35_row_xor(v, 4));
   return fmaxf(v, q35_row_xor(v, 8));
 }
-__device__ __forceinline__ float tile_sum(float v) {
-  v += q35_row_xor(v, 1);
-  v += q35_row_xor(v, 2);
-  v += q35_row_xor(v, 4);
-  return v + q35_row_xor(v, 8);
-}
+__device__ __forceinline__ float tile_sum(float v) { return row_sum16(v); }
 
 // The probability operands of one lane (query l % 16): tokens
 // 32ks + 8(l/16) .. +7 of the row in `pl` for ks = 0, 1.

@@ -59,10 +59,7 @@ __device__ __forceinline__ float delta_row(q35_f32x4 st[2], const q35_f32x4 kc[2
 #pragma unroll
     for (int e = 0; e < 4; ++e) d += st[m][e] * kc[m][e];
   }
-  d += q35_row_xor(d, 1);
-  d += q35_row_xor(d, 2);
-  d += q35_row_xor(d, 4);
-  d += q35_row_xor(d, 8);
+  d = row_sum16(d);
   const float delta = (v - d) * beta;
   float o = 0.0F;
 #pragma unroll
@@ -72,10 +69,7 @@ __device__ __forceinline__ float delta_row(q35_f32x4 st[2], const q35_f32x4 kc[2
       st[m][e] += delta * kc[m][e];
       o += st[m][e] * qc[m][e];
     }
-  o += q35_row_xor(o, 1);
-  o += q35_row_xor(o, 2);
-  o += q35_row_xor(o, 4);
-  o += q35_row_xor(o, 8);
+  o = row_sum16(o);
   return o;
 }
 
@@ -273,10 +267,7 @@ __global__ __launch_bounds__(THREADS) void delta_kernel(DeltaArgs a) {
     float ss = 0.0F;
 #pragma unroll
     for (int e = 0; e < 8; ++e) ss += y[e] * y[e];
-    ss += q35_row_xor(ss, 1);
-    ss += q35_row_xor(ss, 2);
-    ss += q35_row_xor(ss, 4);
-    ss += q35_row_xor(ss, 8);
+    ss = row_sum16(ss);
     const float inv = 1.0F / sqrtf(ss / static_cast<float>(kDim) + a.eps);
 #pragma unroll
     for (int e = 0; e < 8; ++e) y[e] = silu_times(z[e], y[e] * inv * (nw[e] + 0.0F));
@@ -462,16 +453,40 @@ __global__ __launch_bounds__(64) void delta_scan_kernel(DeltaArgs a) {
     // (left alone, the compiler sinks them next to the store)
     q35_compiler_fence();
     const int n = min(kScanBlock, count - t0);
-    for (int i = 0; i < n; ++i) {
+    // token i's inputs are read from LDS while token i-1's row update runs
+    // (two register sets, alternating), so a step never waits for its own
+    // reads; lane `col` keeps the output of token t0 + col of its row and
+    // stores it after the block
+    struct Tok {
       q35_f32x4 kc[2], qc[2];
+      float v, alpha, beta;
+    };
+    auto read = [&](Tok &x, int i) {
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
-        kc[m] = qk_lds[cur][i][kDim / 4 + col + 16 * m];
-        qc[m] = qk_lds[cur][i][col + 16 * m];
+        x.kc[m] = qk_lds[cur][i][kDim / 4 + col + 16 * m];
+        x.qc[m] = qk_lds[cur][i][col + 16 * m];
       }
-      const float o = delta_row(st, kc, qc, v_lds[cur][i][lane >> 4], ab_lds[cur][i][0], ab_lds[cur][i][1]);
-      if (col == 0) outs[static_cast<size_t>(t0 + i) * a.v_heads * kDim] = o;
+      x.v = v_lds[cur][i][lane >> 4];
+      x.alpha = ab_lds[cur][i][0];
+      x.beta = ab_lds[cur][i][1];
+    };
+    float kept = 0.0F;
+    auto step = [&](const Tok &x, int i) {
+      const float o = delta_row(st, x.kc, x.qc, x.v, x.alpha, x.beta);
+      kept = col == i ? o : kept;
+    };
+    Tok A, B;
+    read(A, 0);
+    int i = 0;
+    for (; i + 1 < n; i += 2) {
+      read(B, i + 1);
+      step(A, i);
+      read(A, min(i + 2, n - 1));  // past the block's last token: re-read, unused
+      step(B, i + 1);
     }
+    if (i < n) step(A, i);
+    if (col < n) outs[static_cast<size_t>(t0 + col) * a.v_heads * kDim] = kept;
     if (more) store(blk, cur ^ 1);
     lds_barrier();
   }
@@ -508,10 +523,7 @@ __global__ __launch_bounds__(64) void delta_chunk_out_kernel(DeltaArgs a) {
   float yss = 0.0F;
 #pragma unroll
   for (int e = 0; e < 8; ++e) yss += y[e] * y[e];
-  yss += q35_row_xor(yss, 1);
-  yss += q35_row_xor(yss, 2);
-  yss += q35_row_xor(yss, 4);
-  yss += q35_row_xor(yss, 8);
+  yss = row_sum16(yss);
   const float inv = 1.0F / sqrtf(yss / static_cast<float>(kDim) + a.eps);
 #pragma unroll
   for (int e = 0; e < 8; ++e) y[e] = silu_times(z[e], y[e] * inv * (nw[e] + 0.0F));

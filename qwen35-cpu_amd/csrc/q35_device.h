@@ -75,13 +75,23 @@ __device__ __forceinline__ int group_sum_int(int v) {
   return v;
 }
 
-// Wavefront-wide sum: DPP exchanges inside each 16-lane row, then the two
-// cross-row steps; every lane gets the total.
-__device__ __forceinline__ float wave_sum(float v) {
+// Sum over each 16-lane DPP row, every lane of the row getting the total:
+// the butterfly xor 1, 2, 4, 8. After the xor 1 and xor 2 steps all four
+// lanes of a quad hold the same partial, so the xor-4 step takes the other
+// quad's partial from the mirror lane (7 - i inside each half row): the value
+// the xor-4 exchange brings, added in the same operand order, through one DPP
+// add instead of two DPP moves and a select.
+__device__ __forceinline__ float row_sum16(float v) {
   v += q35_row_xor(v, 1);
   v += q35_row_xor(v, 2);
-  v += q35_row_xor(v, 4);
-  v += q35_row_xor(v, 8);
+  v += q35_row_half_mirror(v);
+  return v + q35_row_xor(v, 8);
+}
+
+// Wavefront-wide sum: the 16-lane row sums, then the two cross-row steps;
+// every lane gets the total.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row_sum16(v);
   v += __shfl_xor(v, 16, 64);
   v += __shfl_xor(v, 32, 64);
   return v;
@@ -120,12 +130,7 @@ __device__ __forceinline__ float sq_group16_quad(q35_f32x4 v) {
 // A group held by sixteen consecutive lanes (one DPP row), one column each:
 __device__ __forceinline__ float sq_group16_lanes(float x) {
 #pragma clang fp contract(off)
-  float s = x * x;
-  s += q35_row_xor(s, 1);
-  s += q35_row_xor(s, 2);
-  s += q35_row_xor(s, 4);
-  s += q35_row_xor(s, 8);
-  return s;
+  return row_sum16(x * x);
 }
 // The row total from its n group sums (every lane of one wavefront calls it).
 __device__ __forceinline__ float norm_total_groups(const float *gp, int n) {

@@ -68,6 +68,11 @@ __device__ __forceinline__ int q35_row_xor_i(int v, int m) {
 __device__ __forceinline__ float q35_row_xor(float v, int m) {
   return __int_as_float(q35_row_xor_i(__float_as_int(v), m));
 }
+// The value of lane 7 - i of this lane's 8-lane half row (row_half_mirror):
+// one DPP move to a lane of the other quad of the half.
+__device__ __forceinline__ float q35_row_half_mirror(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, true));
+}
 // Workgroup barrier that orders LDS only: outstanding global loads and
 // stores keep flying (__syncthreads is a release fence at workgroup scope and
 // waits for them -- on gfx9 the vmcnt counter covers loads and stores).

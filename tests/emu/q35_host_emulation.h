@@ -93,6 +93,22 @@ inline T shfl_xor(T v, int mask) {
   return r;
 }
 
+// value of `v` in lane `src` of the wavefront (every lane must call it)
+template <typename T>
+inline T shfl_src(T v, int src) {
+  static_assert(sizeof(T) <= 8, "shuffle of at most 8 bytes");
+  auto &slots = t_ctx.launch->slots_a[t_ctx.wave];
+  uint64_t bits = 0;
+  std::memcpy(&bits, &v, sizeof(T));
+  slots[t_ctx.lane] = bits;
+  wave_sync();
+  const uint64_t got = slots[src & 63];
+  wave_sync();
+  T r;
+  std::memcpy(&r, &got, sizeof(T));
+  return r;
+}
+
 inline std::atomic<bool> g_capturing{false};
 inline std::vector<std::function<void()>> *g_capture = nullptr;
 
@@ -318,6 +334,10 @@ inline float q35_quad_xor1(float v) { return ::q35emu::shfl_xor(v, 1); }
 inline float q35_quad_xor2(float v) { return ::q35emu::shfl_xor(v, 2); }
 inline float q35_row_xor(float v, int m) { return ::q35emu::shfl_xor(v, m); }
 inline int q35_row_xor_i(int v, int m) { return ::q35emu::shfl_xor(v, m); }
+inline float q35_row_half_mirror(float v) {
+  const int l = ::q35emu::t_ctx.lane;
+  return ::q35emu::shfl_src(v, (l & ~7) | (7 - (l & 7)));
+}
 #define Q35_STORE_NT(value, ptr) (*(ptr) = (value))
 #define Q35_DYNAMIC_SHARED(type, name) \
   type *name = reinterpret_cast<type *>(::q35emu::t_ctx.launch->dynamic_smem.data())
