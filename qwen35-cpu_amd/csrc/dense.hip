@@ -23,7 +23,7 @@ namespace {
 typedef Q35_V4I v4i;
 constexpr int kRowsPerGroup = 64;
 
-template <int NT, bool PREFETCH>
+template <int NT>
 __global__ __launch_bounds__(256) void gemm_dense_kernel(GemmArgs a, int S, int token_groups, int units) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int G = lane >> 4, c = lane & 15, h = c & 1, T = c >> 1;
@@ -95,41 +95,33 @@ __global__ __launch_bounds__(256) void gemm_dense_kernel(GemmArgs a, int S, int 
   };
   // splits s = 0..S-1 over blocks [s·nb/S, (s+1)·nb/S); a finished chain is
   // added to the running sum (which starts at +0, and no chain is -0, so the
-  // first addition is exact: tot = p_0)
-  Block A, B;
-  load(A, 0);
-  int b = 0;
-  for (int s = 0; s < S; ++s) {
-    const int be = ((s + 1) * nb) / S;
-    if constexpr (PREFETCH) {
-      // A holds block b: two blocks per iteration with ping-pong buffers
-      for (; b + 1 < be; b += 2) {
-        load(B, b + 1);
-        compute(A);
-        load(A, b + 2);
-        compute(B);
-      }
-      if (b < be) {
-        load(B, b + 1);
-        compute(A);
-        A = B;
-        ++b;
-      }
-    } else {
-      for (; b < be; ++b) {
-        load(A, b);
-        compute(A);
+  // first addition is exact: tot = p_0). The loads run two blocks ahead of
+  // the compute across split boundaries (ping-pong buffers, the loop unrolled
+  // by two), and a boundary only folds the chain: a uniform branch.
+  Block buf[2];
+  load(buf[0], 0);
+  int s = 0, be = nb / S;  // the end of split s: ((s + 1) * nb) / S
+  for (int b = 0; b < nb; b += 2) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      load(buf[k ^ 1], b + k + 1);  // past the last block: re-reads it, unused
+      if (b + k < nb) {
+        compute(buf[k]);
+        if (b + k + 1 == be) {
+#pragma unroll
+          for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                tot[t][r][j] += acc[t][r][j];
+                acc[t][r][j] = 0.0F;
+              }
+          ++s;
+          be = ((s + 1) * nb) / S;
+        }
       }
     }
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          tot[t][r][j] += acc[t][r][j];
-          acc[t][r][j] = 0.0F;
-        }
   }
   // rows 4c..4c+3 of the group (one per MFMA) for tokens 4G..4G+3 of each tile
   const int row = g * kRowsPerGroup + 4 * c;
@@ -160,21 +152,23 @@ bool gemm_dense_fits(int rows, int tokens, int cu_count) {
 hipError_t launch_gemm_dense(const GemmArgs &a, hipStream_t stream) {
   if (a.tokens <= 0 || a.rows <= 0) return hipSuccess;
   if (a.out == nullptr || a.rows % 8 != 0 || a.stride < a.rows || a.residual != nullptr) return hipErrorInvalidValue;
-  // two token tiles per wavefront with the next block's loads in flight (145
-  // VGPRs, three wavefronts per SIMD) measured ahead of the unprefetched forms
-  // at the 4B projection shapes; four tiles (two wavefronts per SIMD, half the
-  // unpacking per token) win only on tall matrices (4B gate_up: 444 against
-  // 478 us at 2048 tokens; narrow outputs lose 20%)
-  const int nt = a.rows >= 16384 ? 4 : 2;
-  const int S = gemm_dense_splits(a.rows, a.nb, a.cu_count, a.max_split);
+  // four token tiles per wavefront (239 VGPRs, two wavefronts per SIMD: half
+  // the weight unpacking per token) on matrices of 8192 rows or more while
+  // the grid keeps a wavefront per SIMD; two tiles (145 VGPRs, three per
+  // SIMD) on narrower ones, whose grids four tiles would leave too thin (4B at
+  // 2048 tokens: in_proj 310 against 347 us, gate_up 424 against 491; the
+  // 2560-row projections 115 and 259 us with two tiles against 125 and 272)
   const int groups = (a.rows / 8 + 7) / 8;
+  const int cus = a.cu_count > 0 ? a.cu_count : 256;
+  const int nt = a.rows >= 8192 && static_cast<long long>(groups) * ((a.tokens + 63) / 64) >= 4LL * cus ? 4 : 2;
+  const int S = gemm_dense_splits(a.rows, a.nb, a.cu_count, a.max_split);
   const int token_groups = (a.tokens + 16 * nt - 1) / (16 * nt);
   const int units = groups * token_groups;
   const int wgs = ((units + 3) / 4 + 7) / 8 * 8;
   if (nt == 4)
-    Q35_LAUNCH((gemm_dense_kernel<4, true>), dim3(wgs), dim3(256), 0, stream, a, S, token_groups, units);
+    Q35_LAUNCH((gemm_dense_kernel<4>), dim3(wgs), dim3(256), 0, stream, a, S, token_groups, units);
   else
-    Q35_LAUNCH((gemm_dense_kernel<2, true>), dim3(wgs), dim3(256), 0, stream, a, S, token_groups, units);
+    Q35_LAUNCH((gemm_dense_kernel<2>), dim3(wgs), dim3(256), 0, stream, a, S, token_groups, units);
   return hipGetLastError();
 }
 
