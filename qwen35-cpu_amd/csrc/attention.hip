@@ -4,13 +4,13 @@
 //   per-head RMSNorm with (1 + w) (weights.inl:1517-1527), split-half RoPE on the
 //   first rope_dim dims (activation.cpp:124-162), and the FP16 round-to-nearest
 //   KV append of normalised K and raw V (full_attention.cpp:18-46, kv_pages.h:40-69).
-// attention: split-K flash-decoding over chunks of 64 context tokens (one
-//   workgroup per chunk, KV head and request -- or, for the rows of a prefill
-//   segment, per chunk, KV head and tile of up to kAttnTileRows positions,
-//   which then share one load of the chunk's K and V; see attention_kernel), then
-//   attention_merge_kernel: log-sum-exp merge of the chunks, normalisation and
-//   sigmoid(gate), written as FP32 or prepared as the o projection's A16
-//   activations.
+// attention: split-K flash-decoding over chunks of 64 context tokens, one
+//   workgroup per chunk, KV head and request (attention_kernel); the rows of
+//   prompt segments run as tiles of up to kAttnTileRows positions, one
+//   workgroup per tile and KV head walking the chunks and merging them itself
+//   (attention_flash_kernel). Then attention_merge_kernel: log-sum-exp merge
+//   of the chunks, normalisation and sigmoid(gate), written as FP32 or
+//   prepared as the o projection's A16 activations.
 #include <algorithm>
 
 #include "q35_quant.h"
@@ -198,7 +198,8 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
   __shared__ __align__(16) uint16_t vs[kChunkTokens * kVStride];
   __shared__ __align__(16) float pl[16 * kPStride];
   __shared__ float tmax[4][16], tsum[4][16];
-  const int sp = blockIdx.x, g = blockIdx.y, r = blockIdx.z;
+  const int sp = blockIdx.x, g = blockIdx.y;
+  const int r = a.row_list != nullptr ? a.row_list[blockIdx.z] : static_cast<int>(blockIdx.z);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int t0 = sp * kChunkTokens;
   const int kvw = a.kv_heads * kHeadDim;
@@ -285,121 +286,211 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
   }
 }
 
-// Prefill: one workgroup per (chunk, KV head, tile of up to kAttnTileRows
-// consecutive positions of one segment; the tile's rows share its page table
-// and its last row has the longest context), one wavefront per query head:
-// wavefront u's M tile is head g*QPK + u of the tile's rows. The chunk's K
-// and V rows are loaded up front with coalesced loads (32 lanes per row);
-// K goes to LDS for the scores, then V takes its place for P*V, so three
-// workgroups fit a CU. Each wavefront runs the decode kernel's sequence for
-// its 16 queries.
+// Prefill and packed steps: one workgroup per (tile of up to kAttnTileRows
+// consecutive positions of one segment, KV head), one wavefront per query
+// head of the group (wavefront u's M tile is head g*QPK + u of the tile's
+// rows; the rows share the segment's page table). The workgroup walks the
+// tile's 64-token chunks in order, twice:
+//   pass 1 scores every chunk and keeps each row's largest chunk maximum, M
+//     (the merge's maximum over the row's chunks);
+//   pass 2 runs each chunk as the decode kernel does (scores, the chunk
+//     maximum m_s, p = exp(s - m_s) with 0 past the row's context, l_s, the
+//     P*V partial o_s) and folds it at once as attention_merge_kernel folds
+//     the decode kernel's partials: acc = fma(exp(m_s - M), o_s, acc) in chunk
+//     order, and per batch of 64 chunks L += the merge's 64-lane tree over
+//     exp(m_s - M) * l_s.
+// The row's one partial (M, L, acc) then goes through attention_merge_kernel,
+// whose weight for it is exp(0) = 1, so every row gets the bits of the decode
+// kernel's chunk partials merged, while no chunk partial leaves the
+// workgroup. A chunk's K rows are staged in LDS for the scores, then its V
+// rows take their place for P*V.
+constexpr int kFlashBatch = 64;  // chunks per merge tree (the merge's 64 lanes)
+
 template <int QPK>
-__global__ __launch_bounds__(64 * QPK) Q35_WAVES_PER_EU(QPK == 4 ? 3 : 1) void attention_tile_kernel(AttnArgs a) {
+__global__ __launch_bounds__(64 * QPK) Q35_WAVES_PER_EU(QPK == 4 ? 2 : 1) void attention_flash_kernel(AttnArgs a) {
   constexpr int kThreads = 64 * QPK;
-  constexpr int NP = kChunkTokens * 32 / kThreads;  // 16-byte pieces of K (and of V) per thread
+  constexpr int NP = kChunkTokens * 32 / kThreads;  // 16-byte pieces of a K (or V) chunk per thread
   __shared__ __align__(16) uint16_t kv[kChunkTokens * kKStride];
   __shared__ __align__(16) float pls[QPK][16 * kPStride];
-  const int sp = blockIdx.x, g = blockIdx.y;
+  __shared__ float lwb[QPK][16][kFlashBatch];
+  __shared__ float lsum_rows[QPK][16];
+  const int z = blockIdx.x, g = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int t0 = sp * kChunkTokens;
   const int kvw = a.kv_heads * kHeadDim;
-  const int r0 = a.tile_row0[blockIdx.z], nrows = a.tile_rows[blockIdx.z];
+  const int r0 = a.tile_row0[z], nrows = a.tile_rows[z];
   const int32_t *pt = a.page_table + static_cast<size_t>(a.row_seg != nullptr ? a.row_seg[r0] : r0) * a.max_pages;
   const int last_page = a.max_pages - 1;
   const int pshift = __builtin_ctz(static_cast<unsigned>(a.page_tokens)), pmask = a.page_tokens - 1;
   auto seq_of = [&](int r) { return a.seq_lens != nullptr ? a.seq_lens[r] : a.positions[r] + 1; };
-  const int seq_tile = seq_of(r0 + nrows - 1);
-  if (t0 >= seq_tile) return;  // whole workgroup
-  const int n_tile = min(seq_tile - t0, kChunkTokens);
-  const int pfirst = pt[min(t0 >> pshift, last_page)];
-  // piece e = tid + kThreads*i: token e/32, dims 8(e%32) (slots past the
-  // tile's context hold the chunk's first token)
-  size_t rows[NP];
+  const int seq_tile = seq_of(r0 + nrows - 1);  // the tile's last row has the longest context
+  const int nch = (seq_tile + kChunkTokens - 1) / kChunkTokens;
+  // rows 4(l/16) + j of this lane: their context lengths (0 past the tile)
+  int seq_r[4];
 #pragma unroll
-  for (int i = 0; i < NP; ++i) {
-    const int t = (tid + kThreads * i) >> 5;
-    const bool in = t < n_tile;
-    const int page = in ? pt[min((t0 + t) >> pshift, last_page)] : pfirst;
-    rows[i] = ((static_cast<size_t>(page) << pshift) + ((in ? t0 + t : t0) & pmask)) * kvw +
-              static_cast<size_t>(g) * kHeadDim + 8 * (tid & 31);
+  for (int j = 0; j < 4; ++j) {
+    const int mm = 4 * (lane >> 4) + j;
+    seq_r[j] = mm < nrows ? seq_of(r0 + mm) : 0;
   }
-  q35_u32x4 kraw[NP], vraw[NP];
-#pragma unroll
-  for (int i = 0; i < NP; ++i) kraw[i] = Q35_LOAD_NT(reinterpret_cast<const q35_u32x4 *>(a.k_pool + rows[i]));
-#pragma unroll
-  for (int i = 0; i < NP; ++i) vraw[i] = Q35_LOAD_NT(reinterpret_cast<const q35_u32x4 *>(a.v_pool + rows[i]));
-  // this wavefront's queries: rows r0 + m of head g*QPK + wave
   const int m = lane & 15;
   QOps q;
   load_q_ops(a.q + (static_cast<size_t>(r0 + min(m, nrows - 1)) * a.heads + g * QPK + wave) * kHeadDim, m < nrows,
              lane, q);
-#pragma unroll
-  for (int i = 0; i < NP; ++i)
-    *reinterpret_cast<q35_u32x4 *>(kv + ((tid + kThreads * i) >> 5) * kKStride + 8 * (tid & 31)) = kraw[i];
-  lds_barrier();
+  if (lane < 16) lsum_rows[wave][lane] = 0.0F;
 
-  q35_f32x4 s[4];
+  // Piece i of a thread is token tid/32 + i*kThreads/32 of a chunk, dims
+  // 8(tid%32) .. +7 (one base address plus a constant in LDS); pieces past
+  // the tile's context read the chunk's first token. Each load is issued one
+  // compute phase ahead of its use: a chunk's page ids during the previous
+  // chunk, its K during the previous chunk's P*V (pass 2) or scores (pass 1),
+  // its V during its own scores.
+  const uint16_t *k_col = a.k_pool + static_cast<size_t>(g) * kHeadDim + 8 * (tid & 31);
+  const uint16_t *v_col = a.v_pool + static_cast<size_t>(g) * kHeadDim + 8 * (tid & 31);
+  uint16_t *kv_piece = kv + (tid >> 5) * kKStride + 8 * (tid & 31);
+  auto piece_token = [&](int i) { return (tid >> 5) + (kThreads >> 5) * i; };
+  // cache row (token index into the pool, page resolved) of each piece of chunk sp
+  auto chunk_rows = [&](int sp, int rows[NP]) {
+    const int t0 = min(sp, nch - 1) * kChunkTokens;
+    const int n_tile = min(seq_tile - t0, kChunkTokens);
+    const int pfirst = pt[min(t0 >> pshift, last_page)];
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
-    const uint16_t *krow = kv + (16 * tt + (lane & 15)) * kKStride + 8 * (lane >> 4);
-    s[tt] = qk_tile(q, [&](int kk) { return q35_f16x8_bits(*reinterpret_cast<const q35_u32x4 *>(krow + 32 * kk)); });
+    for (int i = 0; i < NP; ++i) {
+      const int t = piece_token(i);
+      const bool in = t < n_tile;
+      const int page = in ? pt[min((t0 + t) >> pshift, last_page)] : pfirst;
+      rows[i] = (page << pshift) + ((in ? t0 + t : t0) & pmask);
+    }
+  };
+  auto load = [&](const uint16_t *col, const int rows[NP], q35_u32x4 raw[NP]) {
+#pragma unroll
+    for (int i = 0; i < NP; ++i) raw[i] = *reinterpret_cast<const q35_u32x4 *>(col + static_cast<size_t>(rows[i]) * kvw);
+  };
+  auto store = [&](const q35_u32x4 raw[NP]) {
+#pragma unroll
+    for (int i = 0; i < NP; ++i) *reinterpret_cast<q35_u32x4 *>(kv_piece + (kThreads >> 5) * i * kKStride) = raw[i];
+  };
+  // the masked, scaled scores of chunk sp (K staged) and their per-row
+  // maxima over the chunk, as the decode kernel forms them
+  auto scores = [&](int sp, float sc[4][4], float mx[4]) {
+    const int t0 = sp * kChunkTokens;
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const uint16_t *krow = kv + (16 * tt + (lane & 15)) * kKStride + 8 * (lane >> 4);
+      const q35_f32x4 s =
+          qk_tile(q, [&](int kk) { return q35_f16x8_bits(*reinterpret_cast<const q35_u32x4 *>(krow + 32 * kk)); });
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        sc[tt][j] = t0 + 16 * tt + (lane & 15) < seq_r[j] ? s[j] * a.scale : -INFINITY;
+        const float t = tile_max(sc[tt][j]);
+        mx[j] = tt == 0 ? t : fmaxf(mx[j], t);
+      }
+    }
+  };
+
+  int rows_cur[NP], rows_next[NP];
+  q35_u32x4 raw[NP];  // one chunk's K or V pieces in flight
+  // pass 1: M
+  float M[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  chunk_rows(0, rows_cur);
+  load(k_col, rows_cur, raw);
+  for (int sp = 0; sp < nch; ++sp) {
+    chunk_rows(sp + 1, rows_next);  // past the last chunk: re-reads it, unused
+    store(raw);
+    lds_barrier();
+    load(k_col, rows_next, raw);
+    float sc[4][4], mx[4];
+    scores(sp, sc, mx);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) M[j] = fmaxf(M[j], mx[j]);
+#pragma unroll
+    for (int i = 0; i < NP; ++i) rows_cur[i] = rows_next[i];
+    lds_barrier();  // every wavefront is done with K
   }
-  // rows 4(l/16) + j: context lengths, masked scores, maxima over the tiles
-  int nm[4];
-  float mx[4];
+
+  // pass 2: the chunks folded in order
+  float acc[kHeadDim / 16][4];
+#pragma unroll
+  for (int dt = 0; dt < kHeadDim / 16; ++dt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[dt][j] = 0.0F;
+  float *pl = pls[wave];
+  chunk_rows(0, rows_cur);
+  load(k_col, rows_cur, raw);
+  for (int sp = 0; sp < nch; ++sp) {
+    const int t0 = sp * kChunkTokens;
+    store(raw);
+    load(v_col, rows_cur, raw);  // this chunk's V, behind its scores
+    chunk_rows(sp + 1, rows_next);
+    lds_barrier();
+    float sc[4][4], mx[4], lsum[4];
+    scores(sp, sc, mx);
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int t = 16 * tt + (lane & 15);
+        const float p = t0 + t < seq_r[j] ? expf(sc[tt][j] - mx[j]) : 0.0F;
+        pl[(4 * (lane >> 4) + j) * kPStride + t] = p;
+        const float ps = tile_sum(p);
+        lsum[j] = tt == 0 ? ps : lsum[j] + ps;
+      }
+    // the sums are formed here, not sunk next to their use after P*V (which
+    // would keep the sixteen tile sums live through it)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) q35_materialize(lsum[j]);
+    lds_barrier();  // every wavefront is done with K
+    store(raw);
+    lds_barrier();
+    load(k_col, rows_next, raw);  // the next chunk's K, behind this chunk's P*V
+    // the chunk's weight in the merge; rows whose context ends before the
+    // chunk have no partial for it
+    float w[4];
+    bool live[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      live[j] = t0 < seq_r[j];
+      w[j] = live[j] ? expf(mx[j] - M[j]) : 0.0F;
+    }
+    q35_f16x8 phi[2], plo[2];
+    load_p_ops(pl, lane, phi, plo);
+#pragma unroll
+    for (int dt = 0; dt < kHeadDim / 16; ++dt) {
+      const q35_f32x4 o = pv_tile(phi, plo, kv, dt, lane);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (live[j]) acc[dt][j] = fmaf(w[j], o[j], acc[dt][j]);
+    }
+    if ((lane & 15) == 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        lwb[wave][4 * (lane >> 4) + j][sp % kFlashBatch] = live[j] ? __fmul_rn(w[j], lsum[j]) : 0.0F;
+    }
+    if (sp % kFlashBatch == kFlashBatch - 1 || sp == nch - 1) {
+      // the merge's tree over the batch's chunks (lane = chunk), row by row
+      wave_lds_sync();
+      const int cnt = sp % kFlashBatch + 1;
+      for (int rr = 0; rr < 16; ++rr) {
+        const float v = group_sum<kFlashBatch>(lane < cnt ? lwb[wave][rr][lane] : 0.0F);
+        if (lane == 0) lsum_rows[wave][rr] += v;
+      }
+      wave_lds_sync();
+    }
+#pragma unroll
+    for (int i = 0; i < NP; ++i) rows_cur[i] = rows_next[i];
+    lds_barrier();  // every wavefront is done with V
+  }
+
+  // the row's merged partial, at chunk slot 0
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int mm = 4 * (lane >> 4) + j;
-    nm[j] = mm < nrows ? min(seq_of(r0 + mm) - t0, kChunkTokens) : 0;
-  }
-  float sc[4][4];
+    if (mm >= nrows) continue;
+    const size_t hs = (static_cast<size_t>(r0 + mm) * a.heads + g * QPK + wave) * a.max_splits;
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      sc[tt][j] = 16 * tt + (lane & 15) < nm[j] ? s[tt][j] * a.scale : -INFINITY;
-      const float t = tile_max(sc[tt][j]);
-      mx[j] = tt == 0 ? t : fmaxf(mx[j], t);
+    for (int dt = 0; dt < kHeadDim / 16; ++dt) a.part_o[hs * kHeadDim + 16 * dt + (lane & 15)] = acc[dt][j];
+    if ((lane & 15) == 0) {
+      a.part_ml[hs * 2] = M[j];
+      a.part_ml[hs * 2 + 1] = lsum_rows[wave][mm];
     }
-  float *pl = pls[wave];
-  float lsum[4];
-#pragma unroll
-  for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int t = 16 * tt + (lane & 15);
-      const float p = t < nm[j] ? expf(sc[tt][j] - mx[j]) : 0.0F;
-      pl[(4 * (lane >> 4) + j) * kPStride + t] = p;
-      const float ps = tile_sum(p);
-      lsum[j] = tt == 0 ? ps : lsum[j] + ps;
-    }
-  lds_barrier();  // every wavefront is done with K
-#pragma unroll
-  for (int i = 0; i < NP; ++i)
-    *reinterpret_cast<q35_u32x4 *>(kv + ((tid + kThreads * i) >> 5) * kVStride + 8 * (tid & 31)) = vraw[i];
-  lds_barrier();
-
-  q35_f16x8 phi[2], plo[2];
-  load_p_ops(pl, lane, phi, plo);
-  // a row gets a partial when its context reaches into the chunk
-  size_t hs[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    hs[j] = (static_cast<size_t>(r0 + 4 * (lane >> 4) + j) * a.heads + g * QPK + wave) * a.max_splits + sp;
-#pragma unroll 4
-  for (int dt = 0; dt < kHeadDim / 16; ++dt) {
-    const q35_f32x4 o = pv_tile(phi, plo, kv, dt, lane);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (nm[j] > 0) a.part_o[hs[j] * kHeadDim + 16 * dt + (lane & 15)] = o[j];
-  }
-  if ((lane & 15) == 0) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (nm[j] > 0) {
-        a.part_ml[hs[j] * 2] = mx[j];
-        a.part_ml[hs[j] * 2 + 1] = lsum[j];
-      }
   }
 }
 
@@ -446,7 +537,10 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(AttnArgs a, const f
     l0 = a.part_ml[(hs + s) * 2 + 1];
   }
   load_rows(0, a.max_splits);
-  const int splits = (seq + kChunkTokens - 1) / kChunkTokens;
+  // in a tiled launch the rows of segments of two or more rows hold one
+  // partial, already merged by attention_flash_kernel
+  const bool merged = a.tile_row0 != nullptr && a.seg_count[a.row_seg[r]] > 1;
+  const int splits = merged ? 1 : (seq + kChunkTokens - 1) / kChunkTokens;
   if (lane >= splits) m0 = -INFINITY;
   float M = m0;
   for (int s = lane + 64; s < splits; s += 64) M = fmaxf(M, a.part_ml[(hs + s) * 2]);
@@ -463,7 +557,7 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(AttnArgs a, const f
     float w = 0.0F, lw = 0.0F;
     if (lane < cnt) {
       w = expf(m - M);
-      lw = w * l;
+      lw = __fmul_rn(w, l);
     }
     L += group_sum<64>(lw);
     for (int s = 0; s < cnt; s += kMergeBatch) {
@@ -474,8 +568,8 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(AttnArgs a, const f
         const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), s + u));
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          acc[e] += ws * rows[u][0][e];
-          acc[4 + e] += ws * rows[u][1][e];
+          acc[e] = fmaf(ws, rows[u][0][e], acc[e]);
+          acc[4 + e] = fmaf(ws, rows[u][1][e], acc[4 + e]);
         }
       }
     }
@@ -515,12 +609,12 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
   const int qpk = a.heads / a.kv_heads;
   const bool tiled = a.tile_row0 != nullptr;
   const int gs = a.grid_splits > 0 ? std::min(a.grid_splits, a.max_splits) : a.max_splits;
-  const dim3 grid(gs, a.kv_heads, tiled ? a.tiles : a.batch);
-#define Q35_ATTN(Q)                                                             \
-  if (tiled)                                                                    \
-    Q35_LAUNCH((attention_tile_kernel<Q>), grid, dim3(64 * (Q)), 0, stream, a); \
-  else                                                                          \
-    Q35_LAUNCH((attention_kernel<Q>), grid, dim3(256), 0, stream, a);
+  // tiled: the prompt tiles, then the one-row segments' rows as decode rows
+  const int decode_rows = tiled ? a.row_count : a.batch;
+#define Q35_ATTN(Q)                                                                                    \
+  if (tiled && a.tiles > 0)                                                                            \
+    Q35_LAUNCH((attention_flash_kernel<Q>), dim3(a.tiles, a.kv_heads), dim3(64 * (Q)), 0, stream, a); \
+  if (decode_rows > 0) Q35_LAUNCH((attention_kernel<Q>), dim3(gs, a.kv_heads, decode_rows), dim3(256), 0, stream, a);
   switch (qpk) {
     case 1: Q35_ATTN(1) break;
     case 2: Q35_ATTN(2) break;

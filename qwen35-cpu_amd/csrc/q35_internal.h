@@ -405,10 +405,16 @@ struct AttnArgs {
   float *part_o = nullptr;        // [batch][heads][max_splits][head_dim]
   float *part_ml = nullptr;       // [batch][heads][max_splits][2]
   const int32_t *row_seg = nullptr;  // page-table row of each row (NULL: the row itself)
-  // query tiles (NULL: one workgroup per row): tile z covers rows
-  // tile_row0[z] .. + tile_rows[z] - 1, consecutive positions of one segment
+  // query tiles of a packed step or prompt chunk (NULL: one workgroup per
+  // row and chunk): tile z covers rows tile_row0[z] .. + tile_rows[z] - 1,
+  // consecutive positions of one segment of two or more rows, whose chunks
+  // one workgroup merges itself (one partial per row); the rows of one-row
+  // segments are listed in row_list and run as decode rows
   const int32_t *tile_row0 = nullptr, *tile_rows = nullptr;
   int tiles = 0;
+  const int32_t *row_list = nullptr;  // rows of the decode kernel (NULL: rows 0 .. batch-1)
+  int row_count = 0;
+  const int32_t *seg_count = nullptr;  // rows per segment (tiled launches: which rows hold one partial)
 };
 constexpr int kAttnTileRows = 16;  // query rows per tile
 hipError_t launch_attention(const AttnArgs &a, hipStream_t stream);

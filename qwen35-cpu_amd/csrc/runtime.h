@@ -37,11 +37,12 @@ struct LayerDev {
 // to a power of two) the attention grid covers.
 struct StepShape {
   int rows = 0, segments = 0, heads = 0, tiles = 0, grid_splits = 1;
+  int attn_rows = 0;           // rows of one-row segments (the decode attention kernel in a packed step)
   bool single = true;          // every segment is one row (the decode kernels)
   bool heads_identity = true;  // head h is row h
-  std::array<int, 7> key(bool want_logits) const {
+  std::array<int, 8> key(bool want_logits) const {
     return {rows, segments, heads, tiles, grid_splits, (single ? 1 : 0) | (heads_identity ? 2 : 0),
-            want_logits ? 1 : 0};
+            want_logits ? 1 : 0, attn_rows};
   }
 };
 constexpr int kMaxPrefillSegments = 16;  // prefill segments per packed step
@@ -108,7 +109,7 @@ struct q35_runtime {
   int32_t *tokens_out_host = nullptr;
   size_t proj_width = 0, core_width = 0;
   q35::StepShape shape;  // of the step last packed
-  std::map<std::array<int, 7>, hipGraphExec_t> graphs;
+  std::map<std::array<int, 8>, hipGraphExec_t> graphs;
   int last_batch = 0;
   std::vector<void *> allocations;
   // kernel-level timing: event pairs reused across steps, the (class, bytes)

@@ -349,8 +349,8 @@ struct MetaLayout {
   // per head row (a segment that wants a token): its row, slot, penalty and
   // sampling settings
   size_t head_rows, head_slots, head_penalties, inv_temperature, top_k;
-  // attention query tiles
-  size_t tile_row0, tile_rows;
+  // attention query tiles, and the rows of one-row segments
+  size_t tile_row0, tile_rows, attn_rows;
   size_t total;
 };
 
@@ -375,6 +375,7 @@ MetaLayout meta_layout(int max_rows, int max_segments, int max_pages) {
   L.top_k = take(M * 4);
   L.tile_row0 = take(R * 4);
   L.tile_rows = take(R * 4);
+  L.attn_rows = take(R * 4);
   L.total = o;
   return L;
 }
@@ -729,6 +730,7 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
   const auto *head_slots = reinterpret_cast<const int32_t *>(mdev + ml.head_slots);
   const auto *head_penalties = reinterpret_cast<const float *>(mdev + ml.head_penalties);
   const auto *tile_row0 = reinterpret_cast<const int32_t *>(mdev + ml.tile_row0);
+  const auto *attn_rows = reinterpret_cast<const int32_t *>(mdev + ml.attn_rows);
   const auto *tile_rows = reinterpret_cast<const int32_t *>(mdev + ml.tile_rows);
   const int H = d.hidden, I = d.intermediate;
   const int v_dim = d.lin_v_heads * d.lin_v_dim;
@@ -1104,6 +1106,9 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
         a.tile_row0 = tile_row0;
         a.tile_rows = tile_rows;
         a.tiles = sh.tiles;
+        a.row_list = attn_rows;
+        a.row_count = sh.attn_rows;
+        a.seg_count = seg_count;
       }
       // every cached K and V row of each request once, q in, split partials out
       const double splits_used = std::ceil(kv_tokens / rt->split_tokens);
@@ -1301,18 +1306,23 @@ int pack_segments(q35_runtime *rt, const q35_segment *segs, int n, StepShape *sh
   auto *head_pen = reinterpret_cast<float *>(h + ml.head_penalties);
   auto *tile_row0 = reinterpret_cast<int32_t *>(h + ml.tile_row0);
   auto *tile_rows = reinterpret_cast<int32_t *>(h + ml.tile_rows);
+  auto *attn_rows = reinterpret_cast<int32_t *>(h + ml.attn_rows);
   StepShape sh;
-  int r = 0, heads = 0, tiles = 0, longest = 1;
+  int r = 0, heads = 0, tiles = 0, singles = 0, longest = 1;
   for (int i = 0; i < n; ++i) {
     const q35_segment &g = segs[i];
     seg_row0[i] = r;
     seg_count[i] = g.count;
     const int used = std::min(g.max_pages, rt->max_pages_per_row);
     std::memcpy(pt + static_cast<size_t>(i) * rt->max_pages_per_row, g.page_table, static_cast<size_t>(used) * 4);
-    for (int t0 = 0; t0 < g.count; t0 += kAttnTileRows) {
-      tile_row0[tiles] = r + t0;
-      tile_rows[tiles] = std::min(kAttnTileRows, g.count - t0);
-      ++tiles;
+    if (g.count == 1) {
+      attn_rows[singles++] = r;
+    } else {
+      for (int t0 = 0; t0 < g.count; t0 += kAttnTileRows) {
+        tile_row0[tiles] = r + t0;
+        tile_rows[tiles] = std::min(kAttnTileRows, g.count - t0);
+        ++tiles;
+      }
     }
     for (int k = 0; k < g.count; ++k, ++r) {
       slots[r] = g.slot;
@@ -1337,6 +1347,7 @@ int pack_segments(q35_runtime *rt, const q35_segment *segs, int n, StepShape *sh
   sh.segments = n;
   sh.heads = heads;
   sh.tiles = tiles;
+  sh.attn_rows = singles;
   sh.heads_identity = sh.heads_identity && heads == r;
   // attention chunks of the longest context, rounded up to a power of two so
   // that few graph shapes cover a growing context

@@ -330,6 +330,11 @@ inline void wave_lds_sync() { ::q35emu::wave_sync(); }
 inline void q35_compiler_fence() { asm volatile("" ::: "memory"); }
 inline void q35_materialize(float &) {}
 inline int __lane_id() { return ::q35emu::t_ctx.lane; }
+// a product rounded on its own (never contracted into an fma)
+inline float __fmul_rn(float a, float b) {
+  volatile float p = a * b;
+  return p;
+}
 inline float q35_quad_xor1(float v) { return ::q35emu::shfl_xor(v, 1); }
 inline float q35_quad_xor2(float v) { return ::q35emu::shfl_xor(v, 2); }
 inline float q35_row_xor(float v, int m) { return ::q35emu::shfl_xor(v, m); }
