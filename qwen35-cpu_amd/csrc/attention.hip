@@ -287,10 +287,13 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
 }
 
 // Prefill and packed steps: one workgroup per (tile of up to kAttnTileRows
-// consecutive positions of one segment, KV head), one wavefront per query
-// head of the group (wavefront u's M tile is head g*QPK + u of the tile's
-// rows; the rows share the segment's page table). The workgroup walks the
-// tile's 64-token chunks in order, twice:
+// consecutive positions of one segment of two or more rows, KV head), two
+// wavefronts per query head of the group: wavefront w serves head
+// g*QPK + w/2 of the tile's rows (its M tile), scores the chunk's token tiles
+// 2(w%2) and 2(w%2)+1, and forms P*V for dims 128(w%2) .. +127, as the decode
+// kernel splits a chunk over its wavefronts (the tile maxima and sums meet in
+// LDS and combine in the same order). The rows share the segment's page
+// table. The workgroup walks the tile's 64-token chunks in order, twice:
 //   pass 1 scores every chunk and keeps each row's largest chunk maximum, M
 //     (the merge's maximum over the row's chunks);
 //   pass 2 runs each chunk as the decode kernel does (scores, the chunk
@@ -303,19 +306,24 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
 // whose weight for it is exp(0) = 1, so every row gets the bits of the decode
 // kernel's chunk partials merged, while no chunk partial leaves the
 // workgroup. A chunk's K rows are staged in LDS for the scores, then its V
-// rows take their place for P*V.
+// rows take their place for P*V. Workgroups start longest tile first (the
+// last tiles of a segment have the longest contexts).
 constexpr int kFlashBatch = 64;  // chunks per merge tree (the merge's 64 lanes)
 
 template <int QPK>
-__global__ __launch_bounds__(64 * QPK) Q35_WAVES_PER_EU(QPK == 4 ? 2 : 1) void attention_flash_kernel(AttnArgs a) {
-  constexpr int kThreads = 64 * QPK;
+__global__ __launch_bounds__(128 * QPK) Q35_WAVES_PER_EU(2) void attention_flash_kernel(AttnArgs a) {
+  constexpr int kThreads = 128 * QPK;
   constexpr int NP = kChunkTokens * 32 / kThreads;  // 16-byte pieces of a K (or V) chunk per thread
+  constexpr int kDimTiles = kHeadDim / 32;          // 16-dim P*V tiles per wavefront
   __shared__ __align__(16) uint16_t kv[kChunkTokens * kKStride];
   __shared__ __align__(16) float pls[QPK][16 * kPStride];
+  __shared__ float tmax[QPK][4][16], tsum[QPK][4][16];
   __shared__ float lwb[QPK][16][kFlashBatch];
   __shared__ float lsum_rows[QPK][16];
-  const int z = blockIdx.x, g = blockIdx.y;
+  __shared__ int rows_lds[2][kChunkTokens];
+  const int z = static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x), g = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int u = wave >> 1, hf = wave & 1;  // query head in the group, half of the chunk
   const int kvw = a.kv_heads * kHeadDim;
   const int r0 = a.tile_row0[z], nrows = a.tile_rows[z];
   const int32_t *pt = a.page_table + static_cast<size_t>(a.row_seg != nullptr ? a.row_seg[r0] : r0) * a.max_pages;
@@ -333,150 +341,159 @@ __global__ __launch_bounds__(64 * QPK) Q35_WAVES_PER_EU(QPK == 4 ? 2 : 1) void a
   }
   const int m = lane & 15;
   QOps q;
-  load_q_ops(a.q + (static_cast<size_t>(r0 + min(m, nrows - 1)) * a.heads + g * QPK + wave) * kHeadDim, m < nrows,
-             lane, q);
-  if (lane < 16) lsum_rows[wave][lane] = 0.0F;
+  load_q_ops(a.q + (static_cast<size_t>(r0 + min(m, nrows - 1)) * a.heads + g * QPK + u) * kHeadDim, m < nrows, lane,
+             q);
+  if (hf == 0 && lane < 16) lsum_rows[u][lane] = 0.0F;
 
   // Piece i of a thread is token tid/32 + i*kThreads/32 of a chunk, dims
-  // 8(tid%32) .. +7 (one base address plus a constant in LDS); pieces past
-  // the tile's context read the chunk's first token. Each load is issued one
-  // compute phase ahead of its use: a chunk's page ids during the previous
-  // chunk, its K during the previous chunk's P*V (pass 2) or scores (pass 1),
-  // its V during its own scores.
+  // 8(tid%32) .. +7 (one base address plus a constant in LDS). The cache rows
+  // of a chunk's tokens (page resolved; tokens past the tile's context read
+  // the chunk's first token) are resolved one chunk ahead by the first 64
+  // threads into rows_lds[chunk % 2]. Each load is issued one compute phase
+  // ahead of its use: a chunk's K during the previous chunk's P*V (pass 2)
+  // or scores (pass 1), its V during its own scores.
   const uint16_t *k_col = a.k_pool + static_cast<size_t>(g) * kHeadDim + 8 * (tid & 31);
   const uint16_t *v_col = a.v_pool + static_cast<size_t>(g) * kHeadDim + 8 * (tid & 31);
   uint16_t *kv_piece = kv + (tid >> 5) * kKStride + 8 * (tid & 31);
   auto piece_token = [&](int i) { return (tid >> 5) + (kThreads >> 5) * i; };
-  // cache row (token index into the pool, page resolved) of each piece of chunk sp
-  auto chunk_rows = [&](int sp, int rows[NP]) {
-    const int t0 = min(sp, nch - 1) * kChunkTokens;
-    const int n_tile = min(seq_tile - t0, kChunkTokens);
-    const int pfirst = pt[min(t0 >> pshift, last_page)];
-#pragma unroll
-    for (int i = 0; i < NP; ++i) {
-      const int t = piece_token(i);
-      const bool in = t < n_tile;
-      const int page = in ? pt[min((t0 + t) >> pshift, last_page)] : pfirst;
-      rows[i] = (page << pshift) + ((in ? t0 + t : t0) & pmask);
+  auto fill_rows = [&](int sp) {  // past the last chunk: its last chunk again
+    if (tid < kChunkTokens) {
+      const int t0 = min(sp, nch - 1) * kChunkTokens;
+      const bool in = t0 + tid < seq_tile;
+      const int page = pt[min((in ? t0 + tid : t0) >> pshift, last_page)];
+      rows_lds[sp & 1][tid] = (page << pshift) + ((in ? t0 + tid : t0) & pmask);
     }
   };
-  auto load = [&](const uint16_t *col, const int rows[NP], q35_u32x4 raw[NP]) {
+  auto load = [&](const uint16_t *col, int sp, q35_u32x4 raw[NP]) {
 #pragma unroll
-    for (int i = 0; i < NP; ++i) raw[i] = *reinterpret_cast<const q35_u32x4 *>(col + static_cast<size_t>(rows[i]) * kvw);
+    for (int i = 0; i < NP; ++i)
+      raw[i] = *reinterpret_cast<const q35_u32x4 *>(col + static_cast<size_t>(rows_lds[sp & 1][piece_token(i)]) * kvw);
   };
   auto store = [&](const q35_u32x4 raw[NP]) {
 #pragma unroll
     for (int i = 0; i < NP; ++i) *reinterpret_cast<q35_u32x4 *>(kv_piece + (kThreads >> 5) * i * kKStride) = raw[i];
   };
-  // the masked, scaled scores of chunk sp (K staged) and their per-row
-  // maxima over the chunk, as the decode kernel forms them
-  auto scores = [&](int sp, float sc[4][4], float mx[4]) {
+  // this wavefront's two token tiles of chunk sp (K staged): masked, scaled
+  // scores, and each tile's per-row maximum into tmax
+  auto scores = [&](int sp, float sc[2][4]) {
     const int t0 = sp * kChunkTokens;
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
+    for (int k = 0; k < 2; ++k) {
+      const int tt = 2 * hf + k;
       const uint16_t *krow = kv + (16 * tt + (lane & 15)) * kKStride + 8 * (lane >> 4);
       const q35_f32x4 s =
           qk_tile(q, [&](int kk) { return q35_f16x8_bits(*reinterpret_cast<const q35_u32x4 *>(krow + 32 * kk)); });
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        sc[tt][j] = t0 + 16 * tt + (lane & 15) < seq_r[j] ? s[j] * a.scale : -INFINITY;
-        const float t = tile_max(sc[tt][j]);
-        mx[j] = tt == 0 ? t : fmaxf(mx[j], t);
+        sc[k][j] = t0 + 16 * tt + (lane & 15) < seq_r[j] ? s[j] * a.scale : -INFINITY;
+        const float t = tile_max(sc[k][j]);
+        if ((lane & 15) == 0) tmax[u][tt][4 * (lane >> 4) + j] = t;
       }
     }
   };
+  // the chunk's per-row maximum over its four tiles, in tile order
+  auto chunk_max = [&](float mx[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int mm = 4 * (lane >> 4) + j;
+      mx[j] = fmaxf(fmaxf(fmaxf(tmax[u][0][mm], tmax[u][1][mm]), tmax[u][2][mm]), tmax[u][3][mm]);
+    }
+  };
 
-  int rows_cur[NP], rows_next[NP];
   q35_u32x4 raw[NP];  // one chunk's K or V pieces in flight
   // pass 1: M
   float M[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-  chunk_rows(0, rows_cur);
-  load(k_col, rows_cur, raw);
+  fill_rows(0);
+  lds_barrier();
+  load(k_col, 0, raw);
   for (int sp = 0; sp < nch; ++sp) {
-    chunk_rows(sp + 1, rows_next);  // past the last chunk: re-reads it, unused
+    fill_rows(sp + 1);
     store(raw);
     lds_barrier();
-    load(k_col, rows_next, raw);
-    float sc[4][4], mx[4];
-    scores(sp, sc, mx);
+    load(k_col, sp + 1, raw);  // past the last chunk: re-reads it, unused
+    float sc[2][4], mx[4];
+    scores(sp, sc);
+    lds_barrier();  // the tile maxima are in; every wavefront is done with K
+    chunk_max(mx);
 #pragma unroll
     for (int j = 0; j < 4; ++j) M[j] = fmaxf(M[j], mx[j]);
-#pragma unroll
-    for (int i = 0; i < NP; ++i) rows_cur[i] = rows_next[i];
-    lds_barrier();  // every wavefront is done with K
   }
 
   // pass 2: the chunks folded in order
-  float acc[kHeadDim / 16][4];
+  float acc[kDimTiles][4];
 #pragma unroll
-  for (int dt = 0; dt < kHeadDim / 16; ++dt)
+  for (int dt = 0; dt < kDimTiles; ++dt)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[dt][j] = 0.0F;
-  float *pl = pls[wave];
-  chunk_rows(0, rows_cur);
-  load(k_col, rows_cur, raw);
+  float *pl = pls[u];
+  lds_barrier();  // pass 1's last reads of tmax and rows_lds are done
+  fill_rows(0);
+  lds_barrier();
+  load(k_col, 0, raw);
   for (int sp = 0; sp < nch; ++sp) {
     const int t0 = sp * kChunkTokens;
     store(raw);
-    load(v_col, rows_cur, raw);  // this chunk's V, behind its scores
-    chunk_rows(sp + 1, rows_next);
+    load(v_col, sp, raw);  // this chunk's V, behind its scores
+    fill_rows(sp + 1);
     lds_barrier();
-    float sc[4][4], mx[4], lsum[4];
-    scores(sp, sc, mx);
+    float sc[2][4], mx[4];
+    scores(sp, sc);
+    lds_barrier();  // the tile maxima are in
+    chunk_max(mx);
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
+    for (int k = 0; k < 2; ++k) {
+      const int tt = 2 * hf + k;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int t = 16 * tt + (lane & 15);
-        const float p = t0 + t < seq_r[j] ? expf(sc[tt][j] - mx[j]) : 0.0F;
+        const float p = t0 + t < seq_r[j] ? expf(sc[k][j] - mx[j]) : 0.0F;
         pl[(4 * (lane >> 4) + j) * kPStride + t] = p;
         const float ps = tile_sum(p);
-        lsum[j] = tt == 0 ? ps : lsum[j] + ps;
+        if ((lane & 15) == 0) tsum[u][tt][4 * (lane >> 4) + j] = ps;
       }
-    // the sums are formed here, not sunk next to their use after P*V (which
-    // would keep the sixteen tile sums live through it)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) q35_materialize(lsum[j]);
-    lds_barrier();  // every wavefront is done with K
+    }
+    lds_barrier();  // every wavefront is done with K; p and the tile sums are in
     store(raw);
     lds_barrier();
-    load(k_col, rows_next, raw);  // the next chunk's K, behind this chunk's P*V
+    load(k_col, sp + 1, raw);  // the next chunk's K, behind this chunk's P*V
     // the chunk's weight in the merge; rows whose context ends before the
     // chunk have no partial for it
-    float w[4];
+    float w[4], lsum[4];
     bool live[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      const int mm = 4 * (lane >> 4) + j;
+      lsum[j] = ((tsum[u][0][mm] + tsum[u][1][mm]) + tsum[u][2][mm]) + tsum[u][3][mm];
       live[j] = t0 < seq_r[j];
       w[j] = live[j] ? expf(mx[j] - M[j]) : 0.0F;
     }
     q35_f16x8 phi[2], plo[2];
     load_p_ops(pl, lane, phi, plo);
 #pragma unroll
-    for (int dt = 0; dt < kHeadDim / 16; ++dt) {
-      const q35_f32x4 o = pv_tile(phi, plo, kv, dt, lane);
+    for (int dt = 0; dt < kDimTiles; ++dt) {
+      const q35_f32x4 o = pv_tile(phi, plo, kv, kDimTiles * hf + dt, lane);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         if (live[j]) acc[dt][j] = fmaf(w[j], o[j], acc[dt][j]);
     }
-    if ((lane & 15) == 0) {
+    if (hf == 0) {
+      if ((lane & 15) == 0) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        lwb[wave][4 * (lane >> 4) + j][sp % kFlashBatch] = live[j] ? __fmul_rn(w[j], lsum[j]) : 0.0F;
-    }
-    if (sp % kFlashBatch == kFlashBatch - 1 || sp == nch - 1) {
-      // the merge's tree over the batch's chunks (lane = chunk), row by row
-      wave_lds_sync();
-      const int cnt = sp % kFlashBatch + 1;
-      for (int rr = 0; rr < 16; ++rr) {
-        const float v = group_sum<kFlashBatch>(lane < cnt ? lwb[wave][rr][lane] : 0.0F);
-        if (lane == 0) lsum_rows[wave][rr] += v;
+        for (int j = 0; j < 4; ++j)
+          lwb[u][4 * (lane >> 4) + j][sp % kFlashBatch] = live[j] ? __fmul_rn(w[j], lsum[j]) : 0.0F;
       }
-      wave_lds_sync();
+      if (sp % kFlashBatch == kFlashBatch - 1 || sp == nch - 1) {
+        // the merge's tree over the batch's chunks (lane = chunk), row by row
+        wave_lds_sync();
+        const int cnt = sp % kFlashBatch + 1;
+        for (int rr = 0; rr < 16; ++rr) {
+          const float v = group_sum<kFlashBatch>(lane < cnt ? lwb[u][rr][lane] : 0.0F);
+          if (lane == 0) lsum_rows[u][rr] += v;
+        }
+        wave_lds_sync();
+      }
     }
-#pragma unroll
-    for (int i = 0; i < NP; ++i) rows_cur[i] = rows_next[i];
-    lds_barrier();  // every wavefront is done with V
+    lds_barrier();  // every wavefront is done with V, p and the tile sums
   }
 
   // the row's merged partial, at chunk slot 0
@@ -484,12 +501,13 @@ __global__ __launch_bounds__(64 * QPK) Q35_WAVES_PER_EU(QPK == 4 ? 2 : 1) void a
   for (int j = 0; j < 4; ++j) {
     const int mm = 4 * (lane >> 4) + j;
     if (mm >= nrows) continue;
-    const size_t hs = (static_cast<size_t>(r0 + mm) * a.heads + g * QPK + wave) * a.max_splits;
+    const size_t hs = (static_cast<size_t>(r0 + mm) * a.heads + g * QPK + u) * a.max_splits;
 #pragma unroll
-    for (int dt = 0; dt < kHeadDim / 16; ++dt) a.part_o[hs * kHeadDim + 16 * dt + (lane & 15)] = acc[dt][j];
-    if ((lane & 15) == 0) {
+    for (int dt = 0; dt < kDimTiles; ++dt)
+      a.part_o[hs * kHeadDim + 16 * (kDimTiles * hf + dt) + (lane & 15)] = acc[dt][j];
+    if (hf == 0 && (lane & 15) == 0) {
       a.part_ml[hs * 2] = M[j];
-      a.part_ml[hs * 2 + 1] = lsum_rows[wave][mm];
+      a.part_ml[hs * 2 + 1] = lsum_rows[u][mm];
     }
   }
 }
@@ -613,7 +631,7 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
   const int decode_rows = tiled ? a.row_count : a.batch;
 #define Q35_ATTN(Q)                                                                                    \
   if (tiled && a.tiles > 0)                                                                            \
-    Q35_LAUNCH((attention_flash_kernel<Q>), dim3(a.tiles, a.kv_heads), dim3(64 * (Q)), 0, stream, a); \
+    Q35_LAUNCH((attention_flash_kernel<Q>), dim3(a.tiles, a.kv_heads), dim3(128 * (Q)), 0, stream, a); \
   if (decode_rows > 0) Q35_LAUNCH((attention_kernel<Q>), dim3(gs, a.kv_heads, decode_rows), dim3(256), 0, stream, a);
   switch (qpk) {
     case 1: Q35_ATTN(1) break;
