@@ -8,7 +8,7 @@
 // Sixteen lanes share a value row: lane o = t % 16 owns the two float4 at
 // columns 4o + 64m (m = 0, 1), and thread t owns rows t/16 + (threads/16) j.
 // A row's dot products are summed per lane in column order and then across
-// its 16 lanes with four DPP exchanges (xor 1, 2, 4, 8) -- delta_row below,
+// its 16 lanes with a four-step DPP butterfly (row_sum16) -- delta_row below,
 // shared with the prefill chunk scan so both give the same bits -- and one
 // load instruction covers 4 rows x 256 contiguous bytes per wavefront.
 //
@@ -37,7 +37,6 @@ constexpr int kDeltaThreads = 256;
 constexpr int kDim = 128;
 constexpr int kConvKernel = 4;  // linear_conv_kernel_dim of every Qwen3.5 size
 constexpr int kRowLanes = 16;                                    // lanes per value row
-constexpr int kRowsPerThread = kDim * kRowLanes / kDeltaThreads;  // 8
 // decode: THREADS (256 or 512) per (value head, request), kDim * 16 /
 // THREADS value rows per thread (rows rowg + THREADS/16 * j). 512 threads
 // let two wavefronts per SIMD overlap the row updates when the grid leaves
@@ -49,7 +48,7 @@ constexpr int kRowsPerThread = kDim * kRowLanes / kDeltaThreads;  // 8
 // 4o + 64m, m = 0, 1), in the reference's order (delta_net.cpp:63-98):
 //   S *= alpha;  sk = S.k;  delta = (v - sk) * beta;  S += delta * k;  o = S.q
 // Each dot product is summed over the lane's 8 columns in order, then over
-// the row's lanes (xor 1, 2, 4, 8). Every lane of the row returns o.
+// the row's 16 lanes (row_sum16). Every lane of the row returns o.
 __device__ __forceinline__ float delta_row(q35_f32x4 st[2], const q35_f32x4 kc[2], const q35_f32x4 qc[2], float v,
                                            float alpha, float beta) {
   float d = 0.0F;
@@ -82,7 +81,8 @@ __global__ __launch_bounds__(THREADS) void delta_kernel(DeltaArgs a) {
   __shared__ float sq[kDim], sk[kDim], sv[kDim], so[kDim];
   __shared__ float red[8];
   __shared__ float s_alpha, s_beta;
-  const int vh = blockIdx.x, r = blockIdx.y;
+  const int vh = blockIdx.x;
+  const int r = a.row_list != nullptr ? a.row_list[blockIdx.y] : static_cast<int>(blockIdx.y);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int per = a.v_heads / a.k_heads;
   const int kh = vh / per;
@@ -315,7 +315,8 @@ __global__ __launch_bounds__(THREADS) void delta_kernel(DeltaArgs a) {
 __global__ __launch_bounds__(kDeltaThreads) void delta_chunk_inputs_kernel(DeltaArgs a) {
   __shared__ float red[4];
   constexpr int K = kConvKernel;
-  const int vh = blockIdx.x, r = blockIdx.y;
+  const int vh = blockIdx.x;
+  const int r = a.chunk_rows != nullptr ? a.chunk_rows[blockIdx.y] : static_cast<int>(blockIdx.y);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int per = a.v_heads / a.k_heads;
   const int kh = vh / per;
@@ -404,9 +405,12 @@ __global__ __launch_bounds__(64) void delta_scan_kernel(DeltaArgs a) {
     rb = k % static_cast<int>(gridDim.x);
   }
   const int col = lane & (kRowLanes - 1), row = kDeltaScanRows * rb + (lane >> 4);
-  // segment blockIdx.z: rows r0 .. r0 + count - 1 of one slot, in order
-  const int r0 = a.row_seg != nullptr ? a.seg_row0[blockIdx.z] : 0;
-  const int count = a.row_seg != nullptr ? a.seg_count[blockIdx.z] : a.batch;
+  // segment seg: rows r0 .. r0 + count - 1 of one slot, in order; the
+  // longest segments are dispatched first, so a prompt chunk's row groups
+  // start ahead of a packed step's one-token segments
+  const int seg = a.seg_order != nullptr ? a.seg_order[blockIdx.z] : static_cast<int>(blockIdx.z);
+  const int r0 = a.row_seg != nullptr ? a.seg_row0[seg] : 0;
+  const int count = a.row_seg != nullptr ? a.seg_count[seg] : a.batch;
   const int slot = a.slots[r0], pos0 = a.positions[r0];
   const int rpar = a.state_copy_stride > 0 ? (pos0 & 1) : 0;
   const int wpar = a.state_copy_stride > 0 ? ((pos0 + count) & 1) : 0;
@@ -499,7 +503,8 @@ __global__ __launch_bounds__(64) void delta_scan_kernel(DeltaArgs a) {
 // epilogue.
 __global__ __launch_bounds__(64) void delta_chunk_out_kernel(DeltaArgs a) {
   constexpr int K = kConvKernel;
-  const int vh = blockIdx.x, r = blockIdx.y, lane = threadIdx.x;
+  const int vh = blockIdx.x, lane = threadIdx.x;
+  const int r = a.chunk_rows != nullptr ? a.chunk_rows[blockIdx.y] : static_cast<int>(blockIdx.y);
   const int q_dim = a.k_heads * kDim, v_dim = a.v_heads * kDim;
   const int channels = 2 * q_dim + v_dim;
   const int j = lane & 15;
@@ -558,11 +563,12 @@ __global__ __launch_bounds__(64) void delta_chunk_out_kernel(DeltaArgs a) {
 }  // namespace
 
 hipError_t launch_delta(const DeltaArgs &a, hipStream_t stream) {
-  if (a.batch <= 0) return hipSuccess;
+  const int rows = a.row_list != nullptr ? a.row_count : a.batch;
+  if (rows <= 0) return hipSuccess;
   if (a.kd != kDim || a.vd != kDim || a.v_heads % a.k_heads != 0) return hipErrorInvalidValue;
-  const dim3 grid(a.v_heads, a.batch);
+  const dim3 grid(a.v_heads, rows);
   // 512 threads while the grid is at most two workgroups per compute unit
-  const bool wide = a.v_heads * a.batch <= 512;
+  const bool wide = a.v_heads * rows <= 512;
 #define Q35_DELTA(F, MS)                                                                   \
   if (wide)                                                                                \
     Q35_LAUNCH((delta_kernel<F, MS, 512>), grid, dim3(512), 0, stream, a);                 \
@@ -589,11 +595,18 @@ hipError_t launch_delta_chunk(const DeltaArgs &a, hipStream_t stream) {
       a.state_base == nullptr || a.slots == nullptr || a.positions == nullptr || a.scan == nullptr ||
       a.proj.splits != 1)
     return hipErrorInvalidValue;
-  Q35_LAUNCH((delta_chunk_inputs_kernel), dim3(a.v_heads, a.batch), dim3(kDeltaThreads), 0, stream, a);
-  Q35_LAUNCH((delta_scan_kernel), dim3(kDim / kDeltaScanRows, a.v_heads, a.row_seg != nullptr ? a.segments : 1),
-             dim3(64), 0, stream, a);
-  Q35_LAUNCH((delta_chunk_out_kernel), dim3(a.v_heads, a.batch), dim3(64), 0, stream, a);
-  return hipGetLastError();
+  // a packed step's one-row segments run the decode kernel (the same
+  // arithmetic), the other segments the three chunk kernels
+  const int rows = a.chunk_rows != nullptr ? a.chunk_row_count : a.batch;
+  const int scans = a.chunk_rows != nullptr ? a.scan_segments : (a.row_seg != nullptr ? a.segments : 1);
+  if (rows > 0) {
+    Q35_LAUNCH((delta_chunk_inputs_kernel), dim3(a.v_heads, rows), dim3(kDeltaThreads), 0, stream, a);
+    Q35_LAUNCH((delta_scan_kernel), dim3(kDim / kDeltaScanRows, a.v_heads, scans), dim3(64), 0, stream, a);
+    Q35_LAUNCH((delta_chunk_out_kernel), dim3(a.v_heads, rows), dim3(64), 0, stream, a);
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return a.row_list != nullptr ? launch_delta(a, stream) : hipSuccess;
 }
 
 }  // namespace q35

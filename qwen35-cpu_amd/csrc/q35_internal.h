@@ -346,6 +346,14 @@ struct DeltaArgs {
   // each row, first row and row count of each segment
   const int32_t *row_seg = nullptr, *seg_row0 = nullptr, *seg_count = nullptr;
   int segments = 0;
+  const int32_t *seg_order = nullptr;  // segments longest first (the scan's dispatch order; NULL: in order)
+  // packed steps: the rows of segments of two or more rows (the chunk
+  // kernels; NULL: every row) and how many leading seg_order entries such
+  // segments are; the rows of one-row segments, which run delta_kernel
+  const int32_t *chunk_rows = nullptr;
+  int chunk_row_count = 0, scan_segments = 0;
+  const int32_t *row_list = nullptr;  // delta_kernel's rows (NULL: rows 0 .. batch-1)
+  int row_count = 0;
 };
 hipError_t launch_delta(const DeltaArgs &a, hipStream_t stream);
 // Chunked prefill: each segment's rows are consecutive positions of ONE

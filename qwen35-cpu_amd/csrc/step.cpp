@@ -344,13 +344,14 @@ namespace {
 struct MetaLayout {
   // per row
   size_t slots, positions, tokens, seq_lens, count_input, row_seg;
-  // per segment: first row, rows, page-table row
-  size_t seg_row0, seg_count, page_table;
+  // per segment: first row, rows, page-table row; segments longest first
+  size_t seg_row0, seg_count, page_table, seg_order;
   // per head row (a segment that wants a token): its row, slot, penalty and
   // sampling settings
   size_t head_rows, head_slots, head_penalties, inv_temperature, top_k;
-  // attention query tiles, and the rows of one-row segments
-  size_t tile_row0, tile_rows, attn_rows;
+  // attention query tiles, the rows of one-row segments and those of the
+  // other segments
+  size_t tile_row0, tile_rows, attn_rows, chunk_rows;
   size_t total;
 };
 
@@ -368,6 +369,7 @@ MetaLayout meta_layout(int max_rows, int max_segments, int max_pages) {
   L.seg_row0 = take(M * 4);
   L.seg_count = take(M * 4);
   L.page_table = take(M * static_cast<size_t>(max_pages) * 4);
+  L.seg_order = take(M * 4);
   L.head_rows = take(M * 4);
   L.head_slots = take(M * 4);
   L.head_penalties = take(M * 4);
@@ -376,6 +378,7 @@ MetaLayout meta_layout(int max_rows, int max_segments, int max_pages) {
   L.tile_row0 = take(R * 4);
   L.tile_rows = take(R * 4);
   L.attn_rows = take(R * 4);
+  L.chunk_rows = take(R * 4);
   L.total = o;
   return L;
 }
@@ -725,12 +728,14 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
   const auto *row_seg = reinterpret_cast<const int32_t *>(mdev + ml.row_seg);
   const auto *seg_row0 = reinterpret_cast<const int32_t *>(mdev + ml.seg_row0);
   const auto *seg_count = reinterpret_cast<const int32_t *>(mdev + ml.seg_count);
+  const auto *seg_order = reinterpret_cast<const int32_t *>(mdev + ml.seg_order);
   const auto *page_table = reinterpret_cast<const int32_t *>(mdev + ml.page_table);
   const auto *head_rows = reinterpret_cast<const int32_t *>(mdev + ml.head_rows);
   const auto *head_slots = reinterpret_cast<const int32_t *>(mdev + ml.head_slots);
   const auto *head_penalties = reinterpret_cast<const float *>(mdev + ml.head_penalties);
   const auto *tile_row0 = reinterpret_cast<const int32_t *>(mdev + ml.tile_row0);
   const auto *attn_rows = reinterpret_cast<const int32_t *>(mdev + ml.attn_rows);
+  const auto *chunk_rows = reinterpret_cast<const int32_t *>(mdev + ml.chunk_rows);
   const auto *tile_rows = reinterpret_cast<const int32_t *>(mdev + ml.tile_rows);
   const int H = d.hidden, I = d.intermediate;
   const int v_dim = d.lin_v_heads * d.lin_v_dim;
@@ -1032,6 +1037,12 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
         a.seg_row0 = seg_row0;
         a.seg_count = seg_count;
         a.segments = sh.segments;
+        a.seg_order = seg_order;
+        a.chunk_rows = chunk_rows;
+        a.chunk_row_count = sh.rows - sh.attn_rows;
+        a.scan_segments = sh.segments - sh.attn_rows;  // seg_order puts them first
+        a.row_list = attn_rows;
+        a.row_count = sh.attn_rows;
       }
       // recurrent state read + written, projection row in (per split), conv
       // ring (K-1 rows read, one written), prepared out-projection activations
@@ -1307,8 +1318,9 @@ int pack_segments(q35_runtime *rt, const q35_segment *segs, int n, StepShape *sh
   auto *tile_row0 = reinterpret_cast<int32_t *>(h + ml.tile_row0);
   auto *tile_rows = reinterpret_cast<int32_t *>(h + ml.tile_rows);
   auto *attn_rows = reinterpret_cast<int32_t *>(h + ml.attn_rows);
+  auto *chunk_rows = reinterpret_cast<int32_t *>(h + ml.chunk_rows);
   StepShape sh;
-  int r = 0, heads = 0, tiles = 0, singles = 0, longest = 1;
+  int r = 0, heads = 0, tiles = 0, singles = 0, multis = 0, longest = 1;
   for (int i = 0; i < n; ++i) {
     const q35_segment &g = segs[i];
     seg_row0[i] = r;
@@ -1318,6 +1330,7 @@ int pack_segments(q35_runtime *rt, const q35_segment *segs, int n, StepShape *sh
     if (g.count == 1) {
       attn_rows[singles++] = r;
     } else {
+      for (int k = 0; k < g.count; ++k) chunk_rows[multis++] = r + k;
       for (int t0 = 0; t0 < g.count; t0 += kAttnTileRows) {
         tile_row0[tiles] = r + t0;
         tile_rows[tiles] = std::min(kAttnTileRows, g.count - t0);
@@ -1343,6 +1356,11 @@ int pack_segments(q35_runtime *rt, const q35_segment *segs, int n, StepShape *sh
     sh.single = sh.single && g.count == 1;
   }
   if (heads == 0) return set_error(ctx, Q35_ERR_INVALID, "a step needs at least one segment that wants a token");
+  // the scan's dispatch order: segments by row count, longest first (ties in
+  // segment order)
+  auto *seg_order = reinterpret_cast<int32_t *>(h + ml.seg_order);
+  for (int i = 0; i < n; ++i) seg_order[i] = i;
+  std::stable_sort(seg_order, seg_order + n, [&](int x, int y) { return seg_count[x] > seg_count[y]; });
   sh.rows = r;
   sh.segments = n;
   sh.heads = heads;
