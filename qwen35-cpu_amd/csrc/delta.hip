@@ -295,7 +295,8 @@ __global__ __launch_bounds__(THREADS) void delta_kernel(DeltaArgs a) {
 // the in-projection rows arrive already summed (one split). Without segment
 // arrays the `batch` rows are one segment.
 // Only the state recurrence is sequential, so a chunk runs as three kernels:
-//   1. delta_chunk_inputs_kernel, one workgroup per (value head, token):
+//   1. delta_chunk_inputs_kernel, one workgroup per (value head, kInTokens
+//      tokens):
 //      causal conv + SiLU, L2 norms, beta and alpha of every token at once
 //      (the conv history of a token is the ring for positions before the
 //      chunk and the chunk's own rows after it);
@@ -303,7 +304,7 @@ __global__ __launch_bounds__(THREADS) void delta_kernel(DeltaArgs a) {
 //      are independent recurrences, so each wavefront walks the chunk's tokens
 //      with its rows' state in registers (one load, one store per chunk) and
 //      no workgroup barrier;
-//   3. delta_chunk_out_kernel, one wavefront per (value head, token): gated
+//   3. delta_chunk_out_kernel, one 16-lane row per (value head, token): gated
 //      RMSNorm * SiLU(z) and the A16 preparation of the out projection's
 //      input, plus the ring update with the chunk's last K-1 inputs.
 // Each step is delta_kernel<true>'s arithmetic in the same order (the same
@@ -312,71 +313,82 @@ __global__ __launch_bounds__(THREADS) void delta_kernel(DeltaArgs a) {
 // for bit. Scan entries are [token][value head][kDeltaScanStride] floats:
 // q (normalised, x 1/sqrt(d_k)) | k (normalised) | v | alpha | beta; the raw
 // head outputs follow at scan + batch * v_heads * kDeltaScanStride.
-__global__ __launch_bounds__(kDeltaThreads) void delta_chunk_inputs_kernel(DeltaArgs a) {
-  __shared__ float red[4];
+constexpr int kInTokens = 8;  // tokens per workgroup of delta_chunk_inputs_kernel
+
+__global__ __launch_bounds__(kDeltaThreads) void delta_chunk_inputs_kernel(DeltaArgs a, int rows) {
+  __shared__ float red[2][4];
   constexpr int K = kConvKernel;
   const int vh = blockIdx.x;
-  const int r = a.chunk_rows != nullptr ? a.chunk_rows[blockIdx.y] : static_cast<int>(blockIdx.y);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int per = a.v_heads / a.k_heads;
   const int kh = vh / per;
   const int q_dim = a.k_heads * kDim, v_dim = a.v_heads * kDim;
   const int channels = 2 * q_dim + v_dim;
-  // the row's segment: rows seg_row0 .. are consecutive positions of its slot
-  const int r0 = a.row_seg != nullptr ? a.seg_row0[a.row_seg[r]] : 0;
-  const int slot = a.slots[r0], pos0 = a.positions[r0], pos = pos0 + (r - r0);
-  const float *conv = a.conv_base + static_cast<long long>(slot) * a.conv_slot_stride;
   const int i = tid & (kDim - 1);
   const bool is_k = tid >= kDim, has_v = tid < kDim;
   const int chq = (is_k ? q_dim : 0) + kh * kDim + i;
   const int chv = has_v ? 2 * q_dim + vh * kDim + tid : chq;
-  const float *row = a.proj.p + static_cast<long long>(r) * a.proj.width;
-  const float xq = row[chq], xv = row[chv];
-  const float bval = a.gates != nullptr ? a.gates[static_cast<size_t>(r) * 2 * a.v_heads + vh] : row[channels + v_dim + vh];
-  const float aval = a.gates != nullptr ? a.gates[static_cast<size_t>(r) * 2 * a.v_heads + a.v_heads + vh]
-                                        : row[channels + v_dim + a.v_heads + vh];
-  float hq[K - 1], hv[K - 1], wq[K], wv[K];
+  // the head's conv weights and gate constants, once for the workgroup's tokens
+  float wq[K], wv[K];
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     wq[k] = a.conv_w[static_cast<size_t>(k) * channels + chq];
     wv[k] = a.conv_w[static_cast<size_t>(k) * channels + chv];
   }
-#pragma unroll
-  for (int k = 0; k < K - 1; ++k) {
-    const int p = pos - (K - 1) + k;  // oldest first
-    if (p >= pos0) {
-      const float *hrow = a.proj.p + static_cast<long long>(r0 + p - pos0) * a.proj.width;
-      hq[k] = hrow[chq];
-      hv[k] = hrow[chv];
-    } else {
-      hq[k] = conv[static_cast<size_t>(p & (K - 1)) * channels + chq];
-      hv[k] = conv[static_cast<size_t>(p & (K - 1)) * channels + chv];
-    }
-  }
   const float dtb = a.dt_bias[vh];
   const float sa_ = a.ssm_a[vh];
-  float yq = xq * wq[K - 1], yv = xv * wv[K - 1];
+  for (int t = 0; t < kInTokens; ++t) {
+    const int y = blockIdx.y * kInTokens + t;
+    if (y >= rows) break;  // uniform
+    const int r = a.chunk_rows != nullptr ? a.chunk_rows[y] : y;
+    // the row's segment: rows seg_row0 .. are consecutive positions of its slot
+    const int r0 = a.row_seg != nullptr ? a.seg_row0[a.row_seg[r]] : 0;
+    const int slot = a.slots[r0], pos0 = a.positions[r0], pos = pos0 + (r - r0);
+    const float *conv = a.conv_base + static_cast<long long>(slot) * a.conv_slot_stride;
+    const float *row = a.proj.p + static_cast<long long>(r) * a.proj.width;
+    const float xq = row[chq], xv = row[chv];
+    const float bval =
+        a.gates != nullptr ? a.gates[static_cast<size_t>(r) * 2 * a.v_heads + vh] : row[channels + v_dim + vh];
+    const float aval = a.gates != nullptr ? a.gates[static_cast<size_t>(r) * 2 * a.v_heads + a.v_heads + vh]
+                                          : row[channels + v_dim + a.v_heads + vh];
+    float hq[K - 1], hv[K - 1];
 #pragma unroll
-  for (int k = 0; k < K - 1; ++k) {
-    yq += hq[k] * wq[k];
-    yv += hv[k] * wv[k];
+    for (int k = 0; k < K - 1; ++k) {
+      const int p = pos - (K - 1) + k;  // oldest first
+      if (p >= pos0) {
+        const float *hrow = a.proj.p + static_cast<long long>(r0 + p - pos0) * a.proj.width;
+        hq[k] = hrow[chq];
+        hv[k] = hrow[chv];
+      } else {
+        hq[k] = conv[static_cast<size_t>(p & (K - 1)) * channels + chq];
+        hv[k] = conv[static_cast<size_t>(p & (K - 1)) * channels + chv];
+      }
+    }
+    float yq = xq * wq[K - 1], yv = xv * wv[K - 1];
+#pragma unroll
+    for (int k = 0; k < K - 1; ++k) {
+      yq += hq[k] * wq[k];
+      yv += hv[k] * wv[k];
+    }
+    yq = silu_times(yq, 1.0F);
+    yv = silu_times(yv, 1.0F);
+    float *e = a.scan + (static_cast<size_t>(r) * a.v_heads + vh) * kDeltaScanStride;
+    if (tid == 0) {
+      e[3 * kDim + 1] = sigmoid_stable(bval);
+      const float pre = softplus_stable(aval + dtb);
+      e[3 * kDim] = expf(pre * sa_);
+    }
+    const float ss = wave_sum(yq * yq);
+    // two slots: a token's partial sums are written while the previous
+    // token's may still be read
+    if (lane == 0) red[t & 1][wave] = ss;
+    if (has_v) e[2 * kDim + tid] = yv;
+    lds_barrier();
+    const float tot = is_k ? red[t & 1][2] + red[t & 1][3] : red[t & 1][0] + red[t & 1][1];
+    const float scale = is_k ? 1.0F : 1.0F / sqrtf(static_cast<float>(kDim));
+    const float mul = scale / sqrtf(tot + 1.0e-6F);
+    e[(is_k ? kDim : 0) + i] = yq * mul;
   }
-  yq = silu_times(yq, 1.0F);
-  yv = silu_times(yv, 1.0F);
-  float *e = a.scan + (static_cast<size_t>(r) * a.v_heads + vh) * kDeltaScanStride;
-  if (tid == 0) {
-    e[3 * kDim + 1] = sigmoid_stable(bval);
-    const float pre = softplus_stable(aval + dtb);
-    e[3 * kDim] = expf(pre * sa_);
-  }
-  const float ss = wave_sum(yq * yq);
-  if (lane == 0) red[wave] = ss;
-  if (has_v) e[2 * kDim + tid] = yv;
-  lds_barrier();
-  const float tot = is_k ? red[2] + red[3] : red[0] + red[1];
-  const float scale = is_k ? 1.0F : 1.0F / sqrtf(static_cast<float>(kDim));
-  const float mul = scale / sqrtf(tot + 1.0e-6F);
-  e[(is_k ? kDim : 0) + i] = yq * mul;
 }
 
 // One wavefront per 4 value rows (grid: row blocks x value heads x
@@ -498,28 +510,33 @@ __global__ __launch_bounds__(64) void delta_scan_kernel(DeltaArgs a) {
   for (int m = 0; m < 2; ++m) Q35_STORE_NT(st[m], W + 16 * m);
 }
 
-// Lane j = lane % 16 holds columns 8j .. 8j+7 of the head's outputs (the four
-// 16-lane rows compute the same values; row 0 stores), as delta_kernel's
-// epilogue.
-__global__ __launch_bounds__(64) void delta_chunk_out_kernel(DeltaArgs a) {
+// One 16-lane row per (value head, token), kOutTokens tokens of one head per
+// workgroup: lane j = lane % 16 holds columns 8j .. 8j+7 of the head's
+// outputs, as delta_kernel's epilogue (whose four rows compute the same
+// token).
+constexpr int kOutTokens = 16;  // tokens per workgroup of delta_chunk_out_kernel
+
+__global__ __launch_bounds__(16 * kOutTokens) void delta_chunk_out_kernel(DeltaArgs a, int rows) {
   constexpr int K = kConvKernel;
-  const int vh = blockIdx.x, lane = threadIdx.x;
-  const int r = a.chunk_rows != nullptr ? a.chunk_rows[blockIdx.y] : static_cast<int>(blockIdx.y);
+  const int vh = blockIdx.x, lane = threadIdx.x & 63;
+  const int y = blockIdx.y * kOutTokens + (threadIdx.x >> 4);
+  const bool active = y < rows;  // rows past the list compute the last one and store nothing
+  const int yy = min(y, rows - 1);
+  const int r = a.chunk_rows != nullptr ? a.chunk_rows[yy] : yy;
   const int q_dim = a.k_heads * kDim, v_dim = a.v_heads * kDim;
   const int channels = 2 * q_dim + v_dim;
   const int j = lane & 15;
-  const bool writer = lane < 16;
   const float *prow = a.proj.p + static_cast<long long>(r) * a.proj.width;
   const q35_f32x4 *zp = reinterpret_cast<const q35_f32x4 *>(prow + channels + vh * kDim + 8 * j);
   const q35_f32x4 *op = reinterpret_cast<const q35_f32x4 *>(
       a.scan + static_cast<size_t>(a.batch) * a.v_heads * kDeltaScanStride + (static_cast<size_t>(r) * a.v_heads + vh) * kDim + 8 * j);
   const q35_f32x4 *wp = reinterpret_cast<const q35_f32x4 *>(a.norm_w + 8 * j);
   const q35_f32x4 z0 = zp[0], z1 = zp[1], o0 = op[0], o1 = op[1], w0 = wp[0], w1 = wp[1];
-  float y[8], z[8], nw[8];
+  float yv[8], z[8], nw[8];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    y[e] = o0[e];
-    y[4 + e] = o1[e];
+    yv[e] = o0[e];
+    yv[4 + e] = o1[e];
     z[e] = z0[e];
     z[4 + e] = z1[e];
     nw[e] = w0[e];
@@ -527,30 +544,30 @@ __global__ __launch_bounds__(64) void delta_chunk_out_kernel(DeltaArgs a) {
   }
   float yss = 0.0F;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) yss += y[e] * y[e];
+  for (int e = 0; e < 8; ++e) yss += yv[e] * yv[e];
   yss = row_sum16(yss);
   const float inv = 1.0F / sqrtf(yss / static_cast<float>(kDim) + a.eps);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) y[e] = silu_times(z[e], y[e] * inv * (nw[e] + 0.0F));
-  if (a.out != nullptr && writer)
+  for (int e = 0; e < 8; ++e) yv[e] = silu_times(z[e], yv[e] * inv * (nw[e] + 0.0F));
+  if (a.out != nullptr && active)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) a.out[static_cast<size_t>(r) * v_dim + vh * kDim + 8 * j + e] = y[e];
+    for (int e = 0; e < 8; ++e) a.out[static_cast<size_t>(r) * v_dim + vh * kDim + 8 * j + e] = yv[e];
   if (a.codes != nullptr) {
     QuantOut qo;
     qo.codes = a.codes;
     qo.scales = a.scales;
-    h128_quantize_row16(y, r, vh, v_dim / 32, true, a.seed, qo, writer);
+    h128_quantize_row16(yv, r, vh, v_dim / 32, true, a.seed, qo, active);
   }
   // the segment's last K-1 raw inputs into the ring (slot = position % K);
   // the inputs kernel read the ring before this launch
   const int seg = a.row_seg != nullptr ? a.row_seg[r] : 0;
   const int seg_end = a.row_seg != nullptr ? a.seg_row0[seg] + a.seg_count[seg] : a.batch;
-  if (r >= seg_end - (K - 1)) {
+  if (active && r >= seg_end - (K - 1)) {
     const int per = a.v_heads / a.k_heads, kh = vh / per;
     const int r0 = a.row_seg != nullptr ? a.seg_row0[seg] : 0;
     float *ring = a.conv_base + static_cast<long long>(a.slots[r0]) * a.conv_slot_stride +
                   static_cast<size_t>((a.positions[r0] + (r - r0)) & (K - 1)) * channels;
-    for (int c = lane; c < kDim; c += 64) {
+    for (int c = j; c < kDim; c += 16) {
       if (vh % per == 0) {
         ring[kh * kDim + c] = prow[kh * kDim + c];
         ring[q_dim + kh * kDim + c] = prow[q_dim + kh * kDim + c];
@@ -600,9 +617,11 @@ hipError_t launch_delta_chunk(const DeltaArgs &a, hipStream_t stream) {
   const int rows = a.chunk_rows != nullptr ? a.chunk_row_count : a.batch;
   const int scans = a.chunk_rows != nullptr ? a.scan_segments : (a.row_seg != nullptr ? a.segments : 1);
   if (rows > 0) {
-    Q35_LAUNCH((delta_chunk_inputs_kernel), dim3(a.v_heads, rows), dim3(kDeltaThreads), 0, stream, a);
+    Q35_LAUNCH((delta_chunk_inputs_kernel), dim3(a.v_heads, (rows + kInTokens - 1) / kInTokens), dim3(kDeltaThreads), 0,
+               stream, a, rows);
     Q35_LAUNCH((delta_scan_kernel), dim3(kDim / kDeltaScanRows, a.v_heads, scans), dim3(64), 0, stream, a);
-    Q35_LAUNCH((delta_chunk_out_kernel), dim3(a.v_heads, rows), dim3(64), 0, stream, a);
+    Q35_LAUNCH((delta_chunk_out_kernel), dim3(a.v_heads, (rows + kOutTokens - 1) / kOutTokens), dim3(16 * kOutTokens),
+               0, stream, a, rows);
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
