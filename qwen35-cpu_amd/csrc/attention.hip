@@ -534,9 +534,14 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(AttnArgs a, const f
   const q35_f32x4 gate_lo = *reinterpret_cast<const q35_f32x4 *>(gates + o);
   const q35_f32x4 gate_hi = *reinterpret_cast<const q35_f32x4 *>(gates + o + 4);
   const int seq = a.seq_lens != nullptr ? a.seq_lens[r] : a.positions[r] + 1;
+  // in a tiled launch the rows of segments of two or more rows hold one
+  // partial, already merged by attention_flash_kernel
+  const bool merged = a.tile_row0 != nullptr && a.seg_count[a.row_seg[r]] > 1;
   // the first statistics and partial rows are read at indices bounded by the
-  // buffer (max_splits), not by the chunk count, so they do not wait for the
-  // context length; chunks past the context are masked below and never used
+  // row's partial slots (max_splits, or the one merged partial), not by the
+  // chunk count, so they do not wait for the context length; chunks past the
+  // context are masked below and never used
+  const int bound = merged ? 1 : a.max_splits;
   q35_f32x4 rows[kMergeBatch][2];
   auto load_rows = [&](int s0, int bound) {
 #pragma unroll
@@ -550,14 +555,11 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(AttnArgs a, const f
   // stays in registers
   float m0 = -INFINITY, l0 = 0.0F;
   {
-    const int s = min(lane, a.max_splits - 1);
+    const int s = min(lane, bound - 1);
     m0 = a.part_ml[(hs + s) * 2];
     l0 = a.part_ml[(hs + s) * 2 + 1];
   }
-  load_rows(0, a.max_splits);
-  // in a tiled launch the rows of segments of two or more rows hold one
-  // partial, already merged by attention_flash_kernel
-  const bool merged = a.tile_row0 != nullptr && a.seg_count[a.row_seg[r]] > 1;
+  load_rows(0, bound);
   const int splits = merged ? 1 : (seq + kChunkTokens - 1) / kChunkTokens;
   if (lane >= splits) m0 = -INFINITY;
   float M = m0;

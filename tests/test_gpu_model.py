@@ -108,11 +108,24 @@ def test_chunked_prefill_equals_single_steps(q, ctx, small, chunks):
     single-token step per position leaves: the greedy token after the prompt
     agrees, and the logits of the decode steps that follow are bit-identical
     (both requests decode in the same batch)."""
+    _chunked_equals_single_steps(q, small, chunks, max_step_rows=0)
+
+
+def test_chunked_prefill_past_64_context_chunks(q, ctx, small):
+    """As above with a second chunk whose rows see more than 64 context chunks
+    of 64 tokens: the prompt attention workgroups, like the merge of the
+    decode path, sum the chunks' exp(m - M) * l in trees of 64 chunks, so this
+    prompt takes the second tree on both paths."""
+    _chunked_equals_single_steps(q, small, [2048, 2100], max_step_rows=2112)
+
+
+def _chunked_equals_single_steps(q, small, chunks, max_step_rows):
     d, sched, tensors, model = small
     plen, new, page_tokens = sum(chunks), 5, 16
     prompt = np.random.default_rng(6).integers(0, d["vocab"], size=plen).astype(np.int32)
     ctx_len = plen + new + 8
-    rt = q.Runtime(model, max_slots=2, max_batch=32, max_context=ctx_len, page_tokens=page_tokens, use_graphs=False)
+    rt = q.Runtime(model, max_slots=2, max_batch=32, max_context=ctx_len, page_tokens=page_tokens, use_graphs=False,
+                   max_step_rows=max_step_rows)
     sa, sb = rt.slot_alloc(prompt), rt.slot_alloc(prompt)
     npages = (ctx_len + page_tokens - 1) // page_tokens
     table = np.zeros((2, rt.max_pages), np.int32)
