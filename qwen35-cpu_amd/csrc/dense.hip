@@ -15,12 +15,20 @@ namespace q35 {
 // is kept as the summation structure: the fma chain restarts from 0 at each
 // split boundary (b0 = s·nb/S) and the finished split sums are added in split
 // order, out = ((p_0 + p_1) + p_2) + ..., which is what a consumer of the
-// split partials computes (SplitRows::reduce). Per block the MFMAs and the
-// fp32 epilogue are gemm_kernel's, so every output carries the split
-// launch's bits. Workgroup i runs on XCD i % 8; the logical order puts the
-// token groups of one row group on one XCD, where they share its L2.
+// split partials computes (SplitRows::reduce). Per block the int8 MFMAs and
+// the fp32 chain acc = fma(float(dot), d·s, acc) are gemm_kernel's. The
+// multipliers d·s of a token tile (4 rows x 4 tokens per lane) come from one
+// v_mfma_f32_16x16x1_4b outer product (block b: the tile's 16 token scales
+// times the scales of rows 4n + b) instead of 16 VALU products per lane: an
+// fp32 product with one live term, bit-identical to the VALU product
+// whenever it is zero or in the normal range, so every output carries the
+// split launch's bits unless some weight-scale x activation-scale product is
+// subnormal (below 2^-126: scales of order 1e-19 each). Workgroup i runs on
+// XCD i % 8; the logical order puts the token groups of one row group on one
+// XCD, where they share its L2.
 namespace {
 typedef Q35_V4I v4i;
+typedef q35_f32x16 v16f;
 constexpr int kRowsPerGroup = 64;
 
 template <int NT>
@@ -40,18 +48,18 @@ __global__ __launch_bounds__(256) void gemm_dense_kernel(GemmArgs a, int S, int 
   const q35_u32x4 *qp = reinterpret_cast<const q35_u32x4 *>(wt + 16 + 16 * (2 * G + h));
   const q35_u32x2 *dp = reinterpret_cast<const q35_u32x2 *>(wt + 8 * h);
   const uint64_t *ap[NT];
-  const q35_f32x4 *sp[NT];
+  const float *sp[NT];  // the scale of token lane%16 of each tile
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const int tile = min(tg * NT + t, tiles - 1);
     ap[t] = a.codes + static_cast<size_t>(tile) * nb * 64 + lane;
-    sp[t] = reinterpret_cast<const q35_f32x4 *>(a.scales + static_cast<size_t>(tile) * nb * 16 + 4 * G);
+    sp[t] = a.scales + static_cast<size_t>(tile) * nb * 16 + c;
   }
   struct Block {
     q35_u32x4 q;
     q35_u32x2 d;
     long act[NT];
-    q35_f32x4 sa[NT];
+    float sa[NT];
   };
   // block b (clamped into the matrix: a load past the end re-reads the last
   // block, an L2 hit, instead of branching)
@@ -62,7 +70,7 @@ __global__ __launch_bounds__(256) void gemm_dense_kernel(GemmArgs a, int S, int 
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       k.act[t] = static_cast<long>(ap[t][static_cast<size_t>(b) * 64]);
-      k.sa[t] = sp[t][static_cast<size_t>(b) * 4];
+      k.sa[t] = sp[t][static_cast<size_t>(b) * 16];
     }
   };
   float acc[NT][4][4], tot[NT][4][4];
@@ -79,6 +87,12 @@ __global__ __launch_bounds__(256) void gemm_dense_kernel(GemmArgs a, int S, int 
                          half_bits_to_float(static_cast<uint16_t>(k.d[1] & 0xffffu)),
                          half_bits_to_float(static_cast<uint16_t>(k.d[1] >> 16))};
     const long w0 = unpack_word(k.q[0]), w1 = unpack_word(k.q[1]), w2 = unpack_word(k.q[2]), w3 = unpack_word(k.q[3]);
+    // the B operand of the multiplier outer product: lane 16b + n holds the
+    // scale of row 4n + b (this lane's row 4c + G)
+    const float dsel = G == 0 ? dw[0] : G == 1 ? dw[1] : G == 2 ? dw[2] : dw[3];
+    v16f zero16;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) zero16[e] = 0.0F;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const v4i corr = Q35_MFMA_I32_16X16X32_I8(k.act[t], kMinus8, zero, 0, 0, 0);
@@ -87,10 +101,13 @@ __global__ __launch_bounds__(256) void gemm_dense_kernel(GemmArgs a, int S, int 
       D[1] = Q35_MFMA_I32_16X16X32_I8(k.act[t], w1, corr, 0, 0, 0);
       D[2] = Q35_MFMA_I32_16X16X32_I8(k.act[t], w2, corr, 0, 0, 0);
       D[3] = Q35_MFMA_I32_16X16X32_I8(k.act[t], w3, corr, 0, 0, 0);
+      // element 4r + j: token 4G + j's scale times row 4c + r's (the layout
+      // of D[r][j])
+      const v16f m = Q35_MFMA_F32_16X16X1_4B(k.sa[t], dsel, zero16);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[t][r][j] = fmaf(static_cast<float>(D[r][j]), dw[r] * k.sa[t][j], acc[t][r][j]);
+        for (int j = 0; j < 4; ++j) acc[t][r][j] = fmaf(static_cast<float>(D[r][j]), m[4 * r + j], acc[t][r][j]);
     }
   };
   // splits s = 0..S-1 over blocks [s·nb/S, (s+1)·nb/S); a finished chain is
@@ -152,15 +169,15 @@ bool gemm_dense_fits(int rows, int tokens, int cu_count) {
 hipError_t launch_gemm_dense(const GemmArgs &a, hipStream_t stream) {
   if (a.tokens <= 0 || a.rows <= 0) return hipSuccess;
   if (a.out == nullptr || a.rows % 8 != 0 || a.stride < a.rows || a.residual != nullptr) return hipErrorInvalidValue;
-  // four token tiles per wavefront (239 VGPRs, two wavefronts per SIMD: half
-  // the weight unpacking per token) on matrices of 8192 rows or more while
-  // the grid keeps a wavefront per SIMD; two tiles (145 VGPRs, three per
-  // SIMD) on narrower ones, whose grids four tiles would leave too thin (4B at
-  // 2048 tokens: in_proj 310 against 347 us, gate_up 424 against 491; the
-  // 2560-row projections 115 and 259 us with two tiles against 125 and 272)
+  // four token tiles per wavefront (228 VGPRs, two wavefronts per SIMD: half
+  // the weight unpacking per token) on matrices of 16384 rows or more while
+  // the grid keeps a wavefront per SIMD; two tiles (144 VGPRs, three per
+  // SIMD) below (4B at 2048 tokens: gate_up 411 against 434 us with two
+  // tiles; in_proj 295, qkv 230, out/o 103 and down 237 us with two tiles
+  // against 304, 231, 128 and 276 with four)
   const int groups = (a.rows / 8 + 7) / 8;
   const int cus = a.cu_count > 0 ? a.cu_count : 256;
-  const int nt = a.rows >= 8192 && static_cast<long long>(groups) * ((a.tokens + 63) / 64) >= 4LL * cus ? 4 : 2;
+  const int nt = a.rows >= 16384 && static_cast<long long>(groups) * ((a.tokens + 63) / 64) >= 4LL * cus ? 4 : 2;
   const int S = gemm_dense_splits(a.rows, a.nb, a.cu_count, a.max_split);
   const int token_groups = (a.tokens + 16 * nt - 1) / (16 * nt);
   const int units = groups * token_groups;

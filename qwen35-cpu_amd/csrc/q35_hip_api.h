@@ -36,6 +36,11 @@ bool launch_events(hipEvent_t *start, hipEvent_t *stop);
 // fp16 MFMA operands: eight binary16 values per lane
 typedef _Float16 q35_f16x8 __attribute__((ext_vector_type(8)));
 #define Q35_MFMA_F32_16X16X32_F16(a, b, c) __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0)
+// four 16x16 fp32 outer products (K = 1): lane 16b + m supplies A_b[m], lane
+// 16b + n supplies B_b[n]; element 4b + k of lane l is A_b[4(l/16) + k] x
+// B_b[l % 16] (+ c)
+typedef float q35_f32x16 __attribute__((ext_vector_type(16)));
+#define Q35_MFMA_F32_16X16X1_4B(a, b, c) __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, c, 0, 0, 0)
 // four int8 products of a and b (byte-wise, signed) added to c: v_dot4_i32_i8
 #define Q35_SDOT4(a, b, c) __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), (c), false)
 // Streaming loads of data read once per step (weights, recurrent state, KV):

@@ -318,6 +318,30 @@ inline q35_f32x4 q35emu_mfma_f16(q35_f16x8 a, q35_f16x8 b, q35_f32x4 c) {
   return d;
 }
 #define Q35_MFMA_F32_16X16X32_F16(a, b, c) q35emu_mfma_f16(a, b, c)
+typedef float q35_f32x16 __attribute__((vector_size(64)));
+inline q35_f32x16 q35emu_mfma_outer4(float a, float b, q35_f32x16 c) {
+  auto &ctx = ::q35emu::t_ctx;
+  auto &as = ctx.launch->slots_a[ctx.wave], &bs = ctx.launch->slots_b[ctx.wave];
+  uint32_t ab, bb;
+  std::memcpy(&ab, &a, 4);
+  std::memcpy(&bb, &b, 4);
+  as[ctx.lane] = ab;
+  bs[ctx.lane] = bb;
+  ::q35emu::wave_sync();
+  q35_f32x16 d;
+  const int l = ctx.lane;
+  for (int blk = 0; blk < 4; ++blk)
+    for (int k = 0; k < 4; ++k) {
+      float x, y;
+      const uint32_t xa = static_cast<uint32_t>(as[16 * blk + 4 * (l / 16) + k]), yb = static_cast<uint32_t>(bs[16 * blk + l % 16]);
+      std::memcpy(&x, &xa, 4);
+      std::memcpy(&y, &yb, 4);
+      d[4 * blk + k] = x * y + c[4 * blk + k];
+    }
+  ::q35emu::wave_sync();
+  return d;
+}
+#define Q35_MFMA_F32_16X16X1_4B(a, b, c) q35emu_mfma_outer4(a, b, c)
 #define Q35_LOAD_NT(ptr) (*(ptr))
 inline int q35emu_sdot4(uint32_t a, uint32_t b, int c) {
   for (int i = 0; i < 4; ++i)
