@@ -55,6 +55,15 @@ struct RowWords<2> {
   static __device__ __forceinline__ uint32_t word(const Q &q, int i) { return q[i]; }
   static __device__ __forceinline__ uint16_t scale(const D &d, int i) { return static_cast<uint16_t>(d >> (16 * i)); }
 };
+template <>
+struct RowWords<4> {
+  typedef q35_u32x4 Q;
+  typedef q35_u32x2 D;
+  static __device__ __forceinline__ uint32_t word(const Q &q, int i) { return q[i]; }
+  static __device__ __forceinline__ uint16_t scale(const D &d, int i) {
+    return static_cast<uint16_t>(d[i >> 1] >> (16 * (i & 1)));
+  }
+};
 // XOR-butterfly reductions over groups of `Width` lanes (Width <= 64, power of 2).
 template <int Width>
 __device__ __forceinline__ float group_sum(float v) {
