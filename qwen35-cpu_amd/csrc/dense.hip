@@ -99,7 +99,10 @@ __global__ __launch_bounds__(256) void gemm_dense_kernel(GemmArgs a, int S, int 
         // the multipliers as one outer-product MFMA: element 4r + j is token
         // 4G + j's scale times row 4c + r's (the layout of D[r][j]); lane
         // 16b + n supplies row 4n + b's scale, every lane token lane%16's
-        const float dsel = G == 0 ? dw[0] : G == 1 ? dw[1] : G == 2 ? dw[2] : dw[3];
+        // (formed branch-free from the packed fp16 pair: a select chain on
+        // G compiles to divergent branches)
+        const uint32_t dpair = (G & 2) != 0 ? k.d[1] : k.d[0];
+        const float dsel = half_bits_to_float(static_cast<uint16_t>(dpair >> (16 * (G & 1))));
         q35_f32x16 zero16;
 #pragma unroll
         for (int e = 0; e < 16; ++e) zero16[e] = 0.0F;
