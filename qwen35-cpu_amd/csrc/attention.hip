@@ -10,7 +10,8 @@
 //   workgroup per tile and KV head walking the chunks and merging them itself
 //   (attention_flash_kernel). Then attention_merge_kernel: log-sum-exp merge
 //   of the chunks, normalisation and sigmoid(gate), written as FP32 or
-//   prepared as the o projection's A16 activations.
+//   prepared as the o projection's A16 activations (attention_finish_kernel
+//   for the prompt rows, whose chunks are merged already).
 #include <algorithm>
 
 #include "q35_quant.h"
@@ -302,9 +303,10 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
 //     the decode kernel's partials: acc = fma(exp(m_s - M), o_s, acc) in chunk
 //     order, and per batch of 64 chunks L += the merge's 64-lane tree over
 //     exp(m_s - M) * l_s.
-// The row's one partial (M, L, acc) then goes through attention_merge_kernel,
-// whose weight for it is exp(0) = 1, so every row gets the bits of the decode
-// kernel's chunk partials merged, while no chunk partial leaves the
+// The row's one partial (M, L, acc) then goes through the merge's
+// one-partial case (attention_finish_kernel), whose weight for it is
+// exp(0) = 1, so every row gets the bits of the decode kernel's chunk
+// partials merged, while no chunk partial leaves the
 // workgroup. A chunk's K rows are staged in LDS for the scores, then its V
 // rows take their place for P*V. Workgroups start longest tile first (the
 // last tiles of a segment have the longest contexts).
@@ -526,7 +528,8 @@ constexpr int kMergeBatch = 16;
 
 __global__ __launch_bounds__(64) void attention_merge_kernel(AttnArgs a, const float *gates, float *out,
                                                             QuantOut qo, uint64_t seed) {
-  const int b = blockIdx.x & 1, h = blockIdx.x >> 1, r = blockIdx.y;
+  const int b = blockIdx.x & 1, h = blockIdx.x >> 1;
+  const int r = a.row_list != nullptr ? a.row_list[blockIdx.y] : blockIdx.y;
   const int lane = threadIdx.x, j = lane & 15;
   const size_t hs = (static_cast<size_t>(r) * a.heads + h) * a.max_splits;
   const int d0 = 128 * b + 8 * j;
@@ -534,14 +537,10 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(AttnArgs a, const f
   const q35_f32x4 gate_lo = *reinterpret_cast<const q35_f32x4 *>(gates + o);
   const q35_f32x4 gate_hi = *reinterpret_cast<const q35_f32x4 *>(gates + o + 4);
   const int seq = a.seq_lens != nullptr ? a.seq_lens[r] : a.positions[r] + 1;
-  // in a tiled launch the rows of segments of two or more rows hold one
-  // partial, already merged by attention_flash_kernel
-  const bool merged = a.tile_row0 != nullptr && a.seg_count[a.row_seg[r]] > 1;
   // the first statistics and partial rows are read at indices bounded by the
-  // row's partial slots (max_splits, or the one merged partial), not by the
-  // chunk count, so they do not wait for the context length; chunks past the
-  // context are masked below and never used
-  const int bound = merged ? 1 : a.max_splits;
+  // row's partial slots, not by the chunk count, so they do not wait for the
+  // context length; chunks past the context are masked below and never used
+  const int bound = a.max_splits;
   q35_f32x4 rows[kMergeBatch][2];
   auto load_rows = [&](int s0, int bound) {
 #pragma unroll
@@ -560,7 +559,7 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(AttnArgs a, const f
     l0 = a.part_ml[(hs + s) * 2 + 1];
   }
   load_rows(0, bound);
-  const int splits = merged ? 1 : (seq + kChunkTokens - 1) / kChunkTokens;
+  const int splits = (seq + kChunkTokens - 1) / kChunkTokens;
   if (lane >= splits) m0 = -INFINITY;
   float M = m0;
   for (int s = lane + 64; s < splits; s += 64) M = fmaxf(M, a.part_ml[(hs + s) * 2]);
@@ -605,6 +604,48 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(AttnArgs a, const f
 #pragma unroll
     for (int e = 0; e < 8; ++e) out[o + e] = y[e];
   if (qo.codes != nullptr) h128_quantize_row16(y, r, 2 * h + b, a.heads * kHeadDim / 32, true, seed, qo, lane < 16);
+}
+
+// The rows of the segments of two or more rows in a tiled launch (prompt
+// rows): attention_flash_kernel has merged all their chunks into one partial
+// at slot 0, so their merge is attention_merge_kernel's one-partial case --
+// weight w = expf(m - M) with M = m, L = w * l, acc = fma(w, o, 0) -- done
+// here with the same operations (the same bits as that kernel on such a row),
+// then the normalisation, gate and quantisation. Each 16-lane row serves its
+// own (row, 128-dim block, head) item, kFinishItems per workgroup, so the
+// loads of an item do not wait on the row's context length.
+constexpr int kFinishItems = 16;
+
+__global__ __launch_bounds__(16 * kFinishItems) void attention_finish_kernel(AttnArgs a, const float *gates,
+                                                                            float *out, QuantOut qo, uint64_t seed) {
+  const int pairs = 2 * a.heads, total = a.prompt_row_count * pairs;
+  const int want = blockIdx.x * kFinishItems + (threadIdx.x >> 4);
+  const bool active = want < total;
+  const int item = active ? want : total - 1;  // spare rows redo the last item and store nothing
+  const int i = item / pairs, p = item - i * pairs;
+  const int b = p & 1, h = p >> 1, r = a.prompt_rows[i], j = threadIdx.x & 15;
+  const size_t hs = (static_cast<size_t>(r) * a.heads + h) * a.max_splits;
+  const int d0 = 128 * b + 8 * j;
+  const size_t o = (static_cast<size_t>(r) * a.heads + h) * kHeadDim + d0;
+  const q35_f32x4 gate_lo = *reinterpret_cast<const q35_f32x4 *>(gates + o);
+  const q35_f32x4 gate_hi = *reinterpret_cast<const q35_f32x4 *>(gates + o + 4);
+  const q35_f32x4 *src = reinterpret_cast<const q35_f32x4 *>(a.part_o + hs * kHeadDim + d0);
+  const q35_f32x4 o_lo = src[0], o_hi = src[1];
+  const float m = a.part_ml[hs * 2], l = a.part_ml[hs * 2 + 1];
+  const float M = m;
+  const float w = expf(m - M);
+  const float L = __fmul_rn(w, l);
+  const float inv = 1.0F / (L > 0.0F ? L : 1.0F);
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    y[e] = (fmaf(w, o_lo[e], 0.0F) * inv) * sigmoid_stable(gate_lo[e]);
+    y[4 + e] = (fmaf(w, o_hi[e], 0.0F) * inv) * sigmoid_stable(gate_hi[e]);
+  }
+  if (out != nullptr && active)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[o + e] = y[e];
+  if (qo.codes != nullptr) h128_quantize_row16(y, r, 2 * h + b, a.heads * kHeadDim / 32, true, seed, qo, active);
 }
 
 }  // namespace
@@ -653,7 +694,15 @@ hipError_t launch_attention_merge(const AttnArgs &a, const float *gates, float *
   QuantOut qo;
   qo.codes = codes;
   qo.scales = scales;
-  Q35_LAUNCH((attention_merge_kernel), dim3(2 * a.heads, a.batch), 64, 0, stream, a, gates, out, qo, seed);
+  // tiled: the one-row segments' rows (decode rows) here, the prompt rows below
+  const bool tiled = a.tile_row0 != nullptr;
+  const int rows = tiled ? a.row_count : a.batch;
+  if (rows > 0) Q35_LAUNCH((attention_merge_kernel), dim3(2 * a.heads, rows), 64, 0, stream, a, gates, out, qo, seed);
+  if (tiled && a.prompt_row_count > 0) {
+    const int items = a.prompt_row_count * 2 * a.heads;
+    Q35_LAUNCH((attention_finish_kernel), dim3((items + kFinishItems - 1) / kFinishItems), 16 * kFinishItems, 0, stream,
+               a, gates, out, qo, seed);
+  }
   return hipGetLastError();
 }
 

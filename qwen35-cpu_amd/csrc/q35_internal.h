@@ -422,7 +422,10 @@ struct AttnArgs {
   int tiles = 0;
   const int32_t *row_list = nullptr;  // rows of the decode kernel (NULL: rows 0 .. batch-1)
   int row_count = 0;
-  const int32_t *seg_count = nullptr;  // rows per segment (tiled launches: which rows hold one partial)
+  // tiled launches: the rows of the segments of two or more rows, whose one
+  // merged partial attention_finish_kernel completes
+  const int32_t *prompt_rows = nullptr;
+  int prompt_row_count = 0;
 };
 constexpr int kAttnTileRows = 16;  // query rows per tile
 hipError_t launch_attention(const AttnArgs &a, hipStream_t stream);

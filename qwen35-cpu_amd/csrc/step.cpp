@@ -1119,7 +1119,8 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
         a.tiles = sh.tiles;
         a.row_list = attn_rows;
         a.row_count = sh.attn_rows;
-        a.seg_count = seg_count;
+        a.prompt_rows = chunk_rows;
+        a.prompt_row_count = sh.rows - sh.attn_rows;
       }
       // every cached K and V row of each request once, q in, split partials out
       const double splits_used = std::ceil(kv_tokens / rt->split_tokens);
