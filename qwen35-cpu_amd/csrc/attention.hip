@@ -194,8 +194,9 @@ __device__ __forceinline__ q35_f32x4 pv_tile(const q35_f16x8 phi[2], const q35_f
 // token tile w (its keys loaded straight into operands); the chunk's V rows
 // are staged in LDS with coalesced loads (32 lanes per row); the tile maxima
 // and sums meet in LDS; wavefront w then forms P*V for dims 64w .. 64w+63.
+// Occupancy floor 2 keeps the MFMA results in VGPRs (no AGPR copies).
 template <int QPK>
-__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) Q35_WAVES_PER_EU(2) void attention_kernel(AttnArgs a) {
   __shared__ __align__(16) uint16_t vs[kChunkTokens * kVStride];
   __shared__ __align__(16) float pl[16 * kPStride];
   __shared__ float tmax[4][16], tsum[4][16];

@@ -316,7 +316,7 @@ __global__ __launch_bounds__(THREADS) void delta_kernel(DeltaArgs a) {
 constexpr int kInTokens = 8;  // tokens per workgroup of delta_chunk_inputs_kernel
 
 __global__ __launch_bounds__(kDeltaThreads) void delta_chunk_inputs_kernel(DeltaArgs a, int rows) {
-  __shared__ float red[2][4];
+  __shared__ float red[kInTokens][4];
   constexpr int K = kConvKernel;
   const int vh = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -328,6 +328,8 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_chunk_inputs_kernel(Delta
   const bool is_k = tid >= kDim, has_v = tid < kDim;
   const int chq = (is_k ? q_dim : 0) + kh * kDim + i;
   const int chv = has_v ? 2 * q_dim + vh * kDim + tid : chq;
+  const int y0 = blockIdx.y * kInTokens;
+  const int nt = min(kInTokens, rows - y0);  // tokens of this workgroup (uniform, >= 1)
   // the head's conv weights and gate constants, once for the workgroup's tokens
   float wq[K], wv[K];
 #pragma unroll
@@ -337,57 +339,72 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_chunk_inputs_kernel(Delta
   }
   const float dtb = a.dt_bias[vh];
   const float sa_ = a.ssm_a[vh];
+  // every token's loads first (their index chains and inputs do not depend on
+  // one another, so they are in flight together), then the arithmetic
+  int rr[kInTokens];
+  float xq[kInTokens], xv[kInTokens], bval[kInTokens], aval[kInTokens];
+  float hq[kInTokens][K - 1], hv[kInTokens][K - 1];
+#pragma unroll
   for (int t = 0; t < kInTokens; ++t) {
-    const int y = blockIdx.y * kInTokens + t;
-    if (y >= rows) break;  // uniform
+    if (t >= nt) break;  // uniform
+    const int y = y0 + t;
     const int r = a.chunk_rows != nullptr ? a.chunk_rows[y] : y;
+    rr[t] = r;
     // the row's segment: rows seg_row0 .. are consecutive positions of its slot
     const int r0 = a.row_seg != nullptr ? a.seg_row0[a.row_seg[r]] : 0;
     const int slot = a.slots[r0], pos0 = a.positions[r0], pos = pos0 + (r - r0);
     const float *conv = a.conv_base + static_cast<long long>(slot) * a.conv_slot_stride;
     const float *row = a.proj.p + static_cast<long long>(r) * a.proj.width;
-    const float xq = row[chq], xv = row[chv];
-    const float bval =
-        a.gates != nullptr ? a.gates[static_cast<size_t>(r) * 2 * a.v_heads + vh] : row[channels + v_dim + vh];
-    const float aval = a.gates != nullptr ? a.gates[static_cast<size_t>(r) * 2 * a.v_heads + a.v_heads + vh]
-                                          : row[channels + v_dim + a.v_heads + vh];
-    float hq[K - 1], hv[K - 1];
+    xq[t] = row[chq];
+    xv[t] = row[chv];
+    bval[t] = a.gates != nullptr ? a.gates[static_cast<size_t>(r) * 2 * a.v_heads + vh] : row[channels + v_dim + vh];
+    aval[t] = a.gates != nullptr ? a.gates[static_cast<size_t>(r) * 2 * a.v_heads + a.v_heads + vh]
+                                 : row[channels + v_dim + a.v_heads + vh];
 #pragma unroll
     for (int k = 0; k < K - 1; ++k) {
       const int p = pos - (K - 1) + k;  // oldest first
       if (p >= pos0) {
         const float *hrow = a.proj.p + static_cast<long long>(r0 + p - pos0) * a.proj.width;
-        hq[k] = hrow[chq];
-        hv[k] = hrow[chv];
+        hq[t][k] = hrow[chq];
+        hv[t][k] = hrow[chv];
       } else {
-        hq[k] = conv[static_cast<size_t>(p & (K - 1)) * channels + chq];
-        hv[k] = conv[static_cast<size_t>(p & (K - 1)) * channels + chv];
+        hq[t][k] = conv[static_cast<size_t>(p & (K - 1)) * channels + chq];
+        hv[t][k] = conv[static_cast<size_t>(p & (K - 1)) * channels + chv];
       }
     }
-    float yq = xq * wq[K - 1], yv = xv * wv[K - 1];
+  }
+  float yq[kInTokens];
+#pragma unroll
+  for (int t = 0; t < kInTokens; ++t) {
+    if (t >= nt) break;
+    float q = xq[t] * wq[K - 1], v = xv[t] * wv[K - 1];
 #pragma unroll
     for (int k = 0; k < K - 1; ++k) {
-      yq += hq[k] * wq[k];
-      yv += hv[k] * wv[k];
+      q += hq[t][k] * wq[k];
+      v += hv[t][k] * wv[k];
     }
-    yq = silu_times(yq, 1.0F);
-    yv = silu_times(yv, 1.0F);
-    float *e = a.scan + (static_cast<size_t>(r) * a.v_heads + vh) * kDeltaScanStride;
+    q = silu_times(q, 1.0F);
+    v = silu_times(v, 1.0F);
+    yq[t] = q;
+    float *e = a.scan + (static_cast<size_t>(rr[t]) * a.v_heads + vh) * kDeltaScanStride;
     if (tid == 0) {
-      e[3 * kDim + 1] = sigmoid_stable(bval);
-      const float pre = softplus_stable(aval + dtb);
+      e[3 * kDim + 1] = sigmoid_stable(bval[t]);
+      const float pre = softplus_stable(aval[t] + dtb);
       e[3 * kDim] = expf(pre * sa_);
     }
-    const float ss = wave_sum(yq * yq);
-    // two slots: a token's partial sums are written while the previous
-    // token's may still be read
-    if (lane == 0) red[t & 1][wave] = ss;
-    if (has_v) e[2 * kDim + tid] = yv;
-    lds_barrier();
-    const float tot = is_k ? red[t & 1][2] + red[t & 1][3] : red[t & 1][0] + red[t & 1][1];
-    const float scale = is_k ? 1.0F : 1.0F / sqrtf(static_cast<float>(kDim));
+    const float ss = wave_sum(q * q);
+    if (lane == 0) red[t][wave] = ss;
+    if (has_v) e[2 * kDim + tid] = v;
+  }
+  lds_barrier();
+  const float scale = is_k ? 1.0F : 1.0F / sqrtf(static_cast<float>(kDim));
+#pragma unroll
+  for (int t = 0; t < kInTokens; ++t) {
+    if (t >= nt) break;
+    const float tot = is_k ? red[t][2] + red[t][3] : red[t][0] + red[t][1];
     const float mul = scale / sqrtf(tot + 1.0e-6F);
-    e[(is_k ? kDim : 0) + i] = yq * mul;
+    float *e = a.scan + (static_cast<size_t>(rr[t]) * a.v_heads + vh) * kDeltaScanStride;
+    e[(is_k ? kDim : 0) + i] = yq[t] * mul;
   }
 }
 

@@ -29,8 +29,12 @@ namespace q35 {
 namespace {
 typedef Q35_V4I v4i;
 
+// Occupancy floor 2 (at most 256 VGPRs): the MFMA results then land in VGPRs;
+// above 256 the compiler places them in AGPRs and copies each element out
+// with a VALU move (64 per K block here), in a kernel whose VALU issue --
+// the int32-to-fp32 conversion and fma of every block dot -- is its limit.
 template <int NT, int R>
-__global__ __launch_bounds__(256) void gemm_dense_kernel(GemmArgs a, int S, int token_groups, int units) {
+__global__ __launch_bounds__(256) Q35_WAVES_PER_EU(2) void gemm_dense_kernel(GemmArgs a, int S, int token_groups, int units) {
   constexpr int RM = 4;  // rows (MFMAs) per lane: 64-row groups
   typedef RowWords<4> RWv;
   constexpr int kLanesPerTile = 8 / RM, kGroupRows = 16 * RM;

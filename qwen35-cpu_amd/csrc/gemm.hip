@@ -47,8 +47,11 @@ typedef Q35_V4I v4i;
 constexpr int kRowsPerGroup = 64;
 constexpr int kMaxWaves = 4;
 
+// Occupancy floor 2 (at most 256 VGPRs) keeps the MFMA results in VGPRs
+// (above 256 the compiler places them in AGPRs and copies every element
+// out); the DOTS form needs more registers and keeps floor 1.
 template <int KS, bool ARGMAX, bool DOTS>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
+__global__ __launch_bounds__(256) Q35_WAVES_PER_EU(DOTS ? 1 : 2) void gemm_kernel(GemmArgs a) {
   Q35_DYNAMIC_SHARED(float, red);  // [W][16][64] wave partials, then [16] argmax keys
   const int W = static_cast<int>(blockDim.x) >> 6;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -271,8 +274,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 // (k-group G) and those rows' FP16 scales; word i is the B operand of MFMA #i
 // for column c, i.e. output row RM·c + i of the group. The int32 block dot
 // and the fp32 chain per block are gemm_kernel's.
+// Occupancy floor 2 keeps the MFMA results in VGPRs (no AGPR copies).
 template <int KS, int RM>
-__global__ __launch_bounds__(64) void gemm_rows_kernel(GemmArgs a) {
+__global__ __launch_bounds__(64) Q35_WAVES_PER_EU(2) void gemm_rows_kernel(GemmArgs a) {
   typedef RowWords<RM> RW;
   constexpr int kLanesPerTile = 8 / RM, kGroupRows = 16 * RM;
   const int lane = threadIdx.x;
