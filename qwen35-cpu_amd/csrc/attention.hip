@@ -201,7 +201,8 @@ __global__ __launch_bounds__(256) Q35_WAVES_PER_EU(2) void attention_kernel(Attn
   __shared__ __align__(16) float pl[16 * kPStride];
   __shared__ float tmax[4][16], tsum[4][16];
   const int sp = blockIdx.x, g = blockIdx.y;
-  const int r = a.row_list != nullptr ? a.row_list[blockIdx.z] : static_cast<int>(blockIdx.z);
+  const int ord = static_cast<int>(blockIdx.z);  // partial rows are indexed by the ordinal
+  const int r = a.row_list != nullptr ? a.row_list[ord] : ord;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int t0 = sp * kChunkTokens;
   const int kvw = a.kv_heads * kHeadDim;
@@ -275,14 +276,14 @@ __global__ __launch_bounds__(256) Q35_WAVES_PER_EU(2) void attention_kernel(Attn
     for (int j = 0; j < 4; ++j) {
       const int mm = 4 * (lane >> 4) + j;
       if (mm < QPK) {
-        const size_t hs = (static_cast<size_t>(r) * a.heads + g * QPK + mm) * a.max_splits + sp;
+        const size_t hs = (static_cast<size_t>(ord) * a.heads + g * QPK + mm) * a.max_splits + sp;
         a.part_o[hs * kHeadDim + 16 * dt + (lane & 15)] = o[j];
       }
     }
   }
   if (wave == 0 && lane < QPK) {
     const float mx = fmaxf(fmaxf(fmaxf(tmax[0][lane], tmax[1][lane]), tmax[2][lane]), tmax[3][lane]);
-    const size_t hs = (static_cast<size_t>(r) * a.heads + g * QPK + lane) * a.max_splits + sp;
+    const size_t hs = (static_cast<size_t>(ord) * a.heads + g * QPK + lane) * a.max_splits + sp;
     a.part_ml[hs * 2] = mx;
     a.part_ml[hs * 2 + 1] = ((tsum[0][lane] + tsum[1][lane]) + tsum[2][lane]) + tsum[3][lane];
   }
@@ -499,18 +500,18 @@ __global__ __launch_bounds__(128 * QPK) Q35_WAVES_PER_EU(2) void attention_flash
     lds_barrier();  // every wavefront is done with V, p and the tile sums
   }
 
-  // the row's merged partial, at chunk slot 0
+  // the row's merged partial
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int mm = 4 * (lane >> 4) + j;
     if (mm >= nrows) continue;
-    const size_t hs = (static_cast<size_t>(r0 + mm) * a.heads + g * QPK + u) * a.max_splits;
+    const size_t hs = static_cast<size_t>(r0 + mm) * a.heads + g * QPK + u;
 #pragma unroll
     for (int dt = 0; dt < kDimTiles; ++dt)
-      a.part_o[hs * kHeadDim + 16 * (kDimTiles * hf + dt) + (lane & 15)] = acc[dt][j];
+      a.prompt_o[hs * kHeadDim + 16 * (kDimTiles * hf + dt) + (lane & 15)] = acc[dt][j];
     if (hf == 0 && (lane & 15) == 0) {
-      a.part_ml[hs * 2] = M[j];
-      a.part_ml[hs * 2 + 1] = lsum_rows[u][mm];
+      a.prompt_ml[hs * 2] = M[j];
+      a.prompt_ml[hs * 2 + 1] = lsum_rows[u][mm];
     }
   }
 }
@@ -530,9 +531,10 @@ constexpr int kMergeBatch = 16;
 __global__ __launch_bounds__(64) void attention_merge_kernel(AttnArgs a, const float *gates, float *out,
                                                             QuantOut qo, uint64_t seed) {
   const int b = blockIdx.x & 1, h = blockIdx.x >> 1;
-  const int r = a.row_list != nullptr ? a.row_list[blockIdx.y] : blockIdx.y;
+  const int ord = static_cast<int>(blockIdx.y);  // the decode kernel's ordinal of the row
+  const int r = a.row_list != nullptr ? a.row_list[ord] : ord;
   const int lane = threadIdx.x, j = lane & 15;
-  const size_t hs = (static_cast<size_t>(r) * a.heads + h) * a.max_splits;
+  const size_t hs = (static_cast<size_t>(ord) * a.heads + h) * a.max_splits;
   const int d0 = 128 * b + 8 * j;
   const size_t o = (static_cast<size_t>(r) * a.heads + h) * kHeadDim + d0;
   const q35_f32x4 gate_lo = *reinterpret_cast<const q35_f32x4 *>(gates + o);
@@ -609,7 +611,8 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(AttnArgs a, const f
 
 // The rows of the segments of two or more rows in a tiled launch (prompt
 // rows): attention_flash_kernel has merged all their chunks into one partial
-// at slot 0, so their merge is attention_merge_kernel's one-partial case --
+// per (row, head) in prompt_o / prompt_ml, so their merge is
+// attention_merge_kernel's one-partial case --
 // weight w = expf(m - M) with M = m, L = w * l, acc = fma(w, o, 0) -- done
 // here with the same operations (the same bits as that kernel on such a row),
 // then the normalisation, gate and quantisation. Each 16-lane row serves its
@@ -625,14 +628,14 @@ __global__ __launch_bounds__(16 * kFinishItems) void attention_finish_kernel(Att
   const int item = active ? want : total - 1;  // spare rows redo the last item and store nothing
   const int i = item / pairs, p = item - i * pairs;
   const int b = p & 1, h = p >> 1, r = a.prompt_rows[i], j = threadIdx.x & 15;
-  const size_t hs = (static_cast<size_t>(r) * a.heads + h) * a.max_splits;
+  const size_t hs = static_cast<size_t>(r) * a.heads + h;
   const int d0 = 128 * b + 8 * j;
-  const size_t o = (static_cast<size_t>(r) * a.heads + h) * kHeadDim + d0;
+  const size_t o = hs * kHeadDim + d0;
   const q35_f32x4 gate_lo = *reinterpret_cast<const q35_f32x4 *>(gates + o);
   const q35_f32x4 gate_hi = *reinterpret_cast<const q35_f32x4 *>(gates + o + 4);
-  const q35_f32x4 *src = reinterpret_cast<const q35_f32x4 *>(a.part_o + hs * kHeadDim + d0);
+  const q35_f32x4 *src = reinterpret_cast<const q35_f32x4 *>(a.prompt_o + o);
   const q35_f32x4 o_lo = src[0], o_hi = src[1];
-  const float m = a.part_ml[hs * 2], l = a.part_ml[hs * 2 + 1];
+  const float m = a.prompt_ml[hs * 2], l = a.prompt_ml[hs * 2 + 1];
   const float M = m;
   const float w = expf(m - M);
   const float L = __fmul_rn(w, l);
@@ -673,6 +676,7 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
   const int gs = a.grid_splits > 0 ? std::min(a.grid_splits, a.max_splits) : a.max_splits;
   // tiled: the prompt tiles, then the one-row segments' rows as decode rows
   const int decode_rows = tiled ? a.row_count : a.batch;
+  if (tiled && a.tiles > 0 && (a.prompt_o == nullptr || a.prompt_ml == nullptr)) return hipErrorInvalidValue;
 #define Q35_ATTN(Q)                                                                                    \
   if (tiled && a.tiles > 0)                                                                            \
     Q35_LAUNCH((attention_flash_kernel<Q>), dim3(a.tiles, a.kv_heads), dim3(128 * (Q)), 0, stream, a); \
@@ -700,6 +704,7 @@ hipError_t launch_attention_merge(const AttnArgs &a, const float *gates, float *
   const int rows = tiled ? a.row_count : a.batch;
   if (rows > 0) Q35_LAUNCH((attention_merge_kernel), dim3(2 * a.heads, rows), 64, 0, stream, a, gates, out, qo, seed);
   if (tiled && a.prompt_row_count > 0) {
+    if (a.prompt_o == nullptr || a.prompt_ml == nullptr) return hipErrorInvalidValue;
     const int items = a.prompt_row_count * 2 * a.heads;
     Q35_LAUNCH((attention_finish_kernel), dim3((items + kFinishItems - 1) / kFinishItems), 16 * kFinishItems, 0, stream,
                a, gates, out, qo, seed);

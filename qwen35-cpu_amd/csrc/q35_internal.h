@@ -410,8 +410,13 @@ struct AttnArgs {
   float scale = 0.0625F;
   int split_tokens = 64, max_splits = 1;  // split_tokens must be kAttnChunkTokens
   int grid_splits = 0;            // chunks launched per row (>= the longest context's; 0: max_splits)
-  float *part_o = nullptr;        // [batch][heads][max_splits][head_dim]
-  float *part_ml = nullptr;       // [batch][heads][max_splits][2]
+  // chunk partials of the decode kernel's rows, by the row's ordinal in the
+  // launch (its index in row_list, or the row itself): [ordinal][heads][max_splits][..]
+  float *part_o = nullptr;        // [decode rows][heads][max_splits][head_dim]
+  float *part_ml = nullptr;       // [decode rows][heads][max_splits][2] (max, sum)
+  // the one merged partial of each prompt row of a tiled launch, by row
+  float *prompt_o = nullptr;      // [rows][heads][head_dim]
+  float *prompt_ml = nullptr;     // [rows][heads][2]
   const int32_t *row_seg = nullptr;  // page-table row of each row (NULL: the row itself)
   // query tiles of a packed step or prompt chunk (NULL: one workgroup per
   // row and chunk): tile z covers rows tile_row0[z] .. + tile_rows[z] - 1,

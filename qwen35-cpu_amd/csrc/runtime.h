@@ -96,6 +96,7 @@ struct q35_runtime {
   unsigned long long *sample_scratch = nullptr;  // sampling: the slices' surviving keys
   q35_candidate *candidates = nullptr;           // sampling: [max_batch][kMaxCandidates]
   float *part_o = nullptr, *part_ml = nullptr, *logits = nullptr;
+  float *prompt_o = nullptr, *prompt_ml = nullptr;  // prompt rows' merged attention partials
   float *hidden_out = nullptr;
   uint64_t *codes = nullptr;
   float *scales = nullptr;

@@ -467,9 +467,14 @@ extern "C" int q35_runtime_create(q35_model *m, const q35_runtime_config *cfg, q
   alloc(static_cast<size_t>(M) * kMaxCandidates * sizeof(q35_candidate), reinterpret_cast<void **>(&rt->candidates));
   alloc(static_cast<size_t>(R) * d.n_heads * d.head_dim * 4, reinterpret_cast<void **>(&rt->q_rot));
   alloc(static_cast<size_t>(R) * d.n_heads * d.head_dim * 4, reinterpret_cast<void **>(&rt->gates));
-  const size_t parts = static_cast<size_t>(R) * d.n_heads * rt->max_splits;
+  // attention partials: every chunk of the decode kernel's rows (one-row
+  // segments, at most M per step), and one merged partial per prompt row
+  const size_t parts = static_cast<size_t>(M) * d.n_heads * rt->max_splits;
   alloc(parts * d.head_dim * 4, reinterpret_cast<void **>(&rt->part_o));
   alloc(parts * 2 * 4, reinterpret_cast<void **>(&rt->part_ml));
+  const size_t prompt_parts = static_cast<size_t>(R) * d.n_heads;
+  alloc(prompt_parts * d.head_dim * 4, reinterpret_cast<void **>(&rt->prompt_o));
+  alloc(prompt_parts * 2 * 4, reinterpret_cast<void **>(&rt->prompt_ml));
   alloc(static_cast<size_t>(M) * H * 4, reinterpret_cast<void **>(&rt->hidden_out));
   const size_t kmax = std::max({H, I, rt->core_width});
   const size_t tiles = (static_cast<size_t>(R) + 15) / 16;
@@ -1112,6 +1117,8 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
       a.grid_splits = sh.grid_splits;
       a.part_o = rt->part_o;
       a.part_ml = rt->part_ml;
+      a.prompt_o = rt->prompt_o;
+      a.prompt_ml = rt->prompt_ml;
       a.row_seg = row_seg;
       if (chunked) {
         a.tile_row0 = tile_row0;
