@@ -506,8 +506,21 @@ typedef struct {
   int32_t max_prefill_requests; /* CpuEngineConfig::max_prefill_requests: prompt chunks of up to this
                                    many requests share one step (1..16; 0 = 1) */
   int32_t packed_steps;         /* no reference counterpart: 1 = q35_engine_step runs the decode batch
-                                   and the prompt chunks in one packed step when both are pending,
-                                   0 = alternate them as the reference scheduler does */
+                                   and the prompt chunks of up to max_prefill_requests requests in one
+                                   packed step, 0 = the reference scheduler (cpu_engine_scheduler.inl) */
+  /* CpuEngineConfig::max_queued_requests (cpu_engine.h:76-79): nonzero
+   * enables bounded serving mode, driven through q35_engine_step and
+   * q35_engine_read_output; submit then queues without device state, and
+   * advance / advance_batch are refused outside step. The record limit is
+   * max_resident_requests + max_queued_requests, terminal results included
+   * until release. 0 = direct mode (submit activates at once; step and
+   * read_output are refused). */
+  int32_t max_queued_requests;
+  /* CpuEngineConfig::max_buffered_tokens: in serving mode a request whose
+   * unread output reaches this many tokens is not scheduled until
+   * read_output drains it (cpu_engine.inl:429-431). Must be > 0 in serving
+   * mode. */
+  int32_t max_buffered_tokens;
 } q35_engine_config;
 /* CpuEngineStats (cpu_engine.h:151-168) for the counters this engine keeps;
  * packed_ticks / packed_rows (steps that carried decode rows and prompt
@@ -528,6 +541,8 @@ typedef struct {
   double prefill_ms, decode_ms;
   uint64_t cached_prefix_tokens;  /* prompt tokens restored from a prefix snapshot */
   double prefix_restore_ms;
+  double queue_ms;                /* submit to admission (serving mode) */
+  uint64_t prefix_written_tokens; /* newly computed tokens published in an automatic prefix */
 } q35_request_result;
 
 /* ReferenceLogitsCallback (options.h:20) in C: called synchronously with a
@@ -579,6 +594,15 @@ typedef struct {
   size_t selected_logit_count;
   q35_logits_callback selected_logits_callback;
   void *selected_logits_callback_context;
+  /* CpuRequestSpec::register_prefix_tokens / trust_namespace
+   * (cpu_engine.h:126-129, cpu_engine_singleflight.inl): serving mode only;
+   * the first register_prefix_tokens prompt tokens are built once and
+   * published as a prefix of trust_namespace when the request's prefill
+   * reaches them; a queued request of the same build waits for it and then
+   * attaches it. 0 = none. trust_namespace (NUL-terminated, may be NULL =
+   * unnamed) must equal the namespace of an attached prefix when given. */
+  uint64_t register_prefix_tokens;
+  const char *trust_namespace;
 } q35_request_spec;
 
 int q35_engine_create(q35_model *model, const q35_engine_config *config, q35_engine **out);
@@ -590,7 +614,24 @@ int q35_engine_submit(q35_engine *engine, const int32_t *prompt_tokens, size_t p
 int q35_engine_submit_spec(q35_engine *engine, const q35_request_spec *spec, uint64_t *out_id);
 int q35_engine_advance(q35_engine *engine, uint64_t id);
 int q35_engine_advance_batch(q35_engine *engine, const uint64_t *ids, size_t count);
+/* CpuEngine::step (cpu_engine_scheduler.inl:2-105): serving mode only.
+ * Retires terminal requests, admits up to max_prefill_requests queued
+ * requests (in ID order, skipping those whose automatic prefix another
+ * request is still building), then runs one decode batch or prompt chunk,
+ * alternating between the two and rotating requests for fairness. Rows whose
+ * unread output holds max_buffered_tokens are skipped. *progressed = 1 when
+ * any work was admitted or run. */
 int q35_engine_step(q35_engine *engine, int32_t *progressed);
+/* CpuEngine::read_output (cpu_engine_scheduler.inl:107-127): serving mode
+ * only. Copies up to max_tokens confirmed, unread output tokens of a request
+ * into out (capacity >= max_tokens) and *count; tokens that may still be the
+ * start of a stop sequence are held back until resolved. */
+int q35_engine_read_output(q35_engine *engine, uint64_t id, size_t max_tokens, int32_t *out, size_t *count);
+/* detail::prefill_chunk_token_count (src/runtime/prefill_chunk.h:10-17): the
+ * prompt tokens one advance() prefills from `position` with `remaining` left,
+ * for a canonical chunk of `chunk`: up to the chunk boundary, and not past the
+ * first 128 positions. Host-only; no device. */
+size_t q35_prefill_chunk_token_count(size_t position, size_t remaining, size_t chunk);
 /* No reference counterpart: prefill several requests, each to the end of its
  * prompt in chunks of up to prefill_chunk_size positions (the reference
  * prefills one chunk of one request per advance(), cpu_engine.inl:668-790). */

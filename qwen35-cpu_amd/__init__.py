@@ -78,7 +78,8 @@ class EngineConfig(ctypes.Structure):
     _fields_ = [("max_resident_requests", c_int32), ("max_context", c_int32),
                 ("max_decode_batch_size", c_int32), ("prefill_chunk_size", c_int32),
                 ("page_tokens", c_int32), ("use_graphs", c_int32), ("max_prefix_bytes", c_uint64),
-                ("max_prefill_requests", c_int32), ("packed_steps", c_int32)]
+                ("max_prefill_requests", c_int32), ("packed_steps", c_int32),
+                ("max_queued_requests", c_int32), ("max_buffered_tokens", c_int32)]
 
 
 class EngineStats(ctypes.Structure):
@@ -93,7 +94,8 @@ class RequestResult(ctypes.Structure):
     _fields_ = [("status", c_int32), ("generated_tokens", c_uint64), ("committed_tokens", c_uint64),
                 ("prefill_tokens", c_uint64), ("decode_forwards", c_uint64),
                 ("prefill_ms", c_double), ("decode_ms", c_double),
-                ("cached_prefix_tokens", c_uint64), ("prefix_restore_ms", c_double)]
+                ("cached_prefix_tokens", c_uint64), ("prefix_restore_ms", c_double),
+                ("queue_ms", c_double), ("prefix_written_tokens", c_uint64)]
 
 
 class Candidate(ctypes.Structure):
@@ -120,7 +122,8 @@ class RequestSpec(ctypes.Structure):
                 ("logits_callback", LOGITS_CALLBACK), ("logits_callback_context", c_void_p),
                 ("prefix", c_uint64), ("sampling_constraint", c_void_p),
                 ("selected_logit_tokens", POINTER(c_int32)), ("selected_logit_count", c_size_t),
-                ("selected_logits_callback", LOGITS_CALLBACK), ("selected_logits_callback_context", c_void_p)]
+                ("selected_logits_callback", LOGITS_CALLBACK), ("selected_logits_callback_context", c_void_p),
+                ("register_prefix_tokens", c_uint64), ("trust_namespace", c_char_p)]
 
 
 CONSTRAINT_APPLY = ctypes.CFUNCTYPE(c_int, c_void_p, POINTER(c_float), c_size_t)
@@ -222,6 +225,8 @@ _SIGS = {
     "q35_engine_advance": (c_int, [P, c_uint64]),
     "q35_engine_advance_batch": (c_int, [P, P, c_size_t]),
     "q35_engine_step": (c_int, [P, POINTER(c_int32)]),
+    "q35_engine_read_output": (c_int, [P, c_uint64, c_size_t, P, POINTER(c_size_t)]),
+    "q35_prefill_chunk_token_count": (c_size_t, [c_size_t, c_size_t, c_size_t]),
     "q35_engine_prefill_batch": (c_int, [P, P, c_size_t]),
     "q35_engine_result": (c_int, [P, c_uint64, POINTER(RequestResult), P, c_size_t, POINTER(c_size_t)]),
     "q35_engine_cancel": (c_int, [P, c_uint64]),
@@ -708,11 +713,13 @@ class Engine(_Profiled):
 
     def __init__(self, model, max_resident_requests=32, max_context=8192, max_decode_batch_size=32,
                  prefill_chunk_size=128, page_tokens=16, use_graphs=True, max_prefix_bytes=0,
-                 max_prefill_requests=1, packed_steps=False):
+                 max_prefill_requests=1, packed_steps=False, max_queued_requests=0, max_buffered_tokens=256):
+        """max_queued_requests > 0 selects serving mode (step / read_output);
+        0 the direct mode (advance / advance_batch), as CpuEngineConfig."""
         self.model, self.ctx = model, model.ctx
         cfg = EngineConfig(max_resident_requests, max_context, max_decode_batch_size, prefill_chunk_size,
                            page_tokens, int(use_graphs), max_prefix_bytes, int(max_prefill_requests),
-                           int(packed_steps))
+                           int(packed_steps), int(max_queued_requests), int(max_buffered_tokens))
         h = c_void_p()
         self.ctx.check(lib.q35_engine_create(model.handle, ctypes.byref(cfg), ctypes.byref(h)), "engine create")
         self.handle = h
@@ -737,7 +744,7 @@ class Engine(_Profiled):
     def submit_spec(self, prompt, max_new_tokens=128, temperature=0.7, top_p=0.8, top_k=20,
                     repetition_penalty=1.05, seed=-1, stop_token_ids=(), stop_sequences=(), forced_output_tokens=(),
                     logits_callback=None, prefix=0, sampling_constraint=None, selected_logit_tokens=(),
-                    selected_logits_callback=None):
+                    selected_logits_callback=None, register_prefix_tokens=0, trust_namespace=None):
         """CpuEngine::submit with a CpuRequestSpec (q35_engine_submit_spec); the
         sampling defaults are SamplingOptions' (options.h:10-13). logits_callback,
         when given, is a Python callable (index, forced_token, logits ndarray) ->
@@ -795,7 +802,8 @@ class Engine(_Profiled):
         spec = RequestSpec(prompt_p, n, max_new_tokens, temperature, top_p, top_k, repetition_penalty, seed,
                            stops_p, ns, flat_p, lens_p, nseq, forced_p, nf, cb, None, prefix,
                            ctypes.cast(ctypes.pointer(cons), c_void_p) if cons is not None else None,
-                           sel_p, nsel, scb, None)
+                           sel_p, nsel, scb, None, int(register_prefix_tokens),
+                           trust_namespace.encode() if trust_namespace is not None else None)
         rid = c_uint64()
         self._check(lib.q35_engine_submit_spec(self.handle, ctypes.byref(spec), ctypes.byref(rid)), "submit")
         return rid.value
@@ -850,6 +858,15 @@ class Engine(_Profiled):
         self._check(lib.q35_engine_step(self.handle, ctypes.byref(p)), "step")
         return bool(p.value)
 
+    def read_output(self, rid, max_tokens=1 << 20):
+        """CpuEngine::read_output: up to max_tokens confirmed, unread output
+        tokens (serving mode)."""
+        out = np.empty(max(int(max_tokens), 1), np.int32)
+        n = c_size_t()
+        self._check(lib.q35_engine_read_output(self.handle, rid, int(max_tokens), _ptr(out), ctypes.byref(n)),
+                    "read_output")
+        return out[:n.value].copy()
+
     def result(self, rid):
         r = RequestResult()
         n = c_size_t()
@@ -858,6 +875,10 @@ class Engine(_Profiled):
         if n.value:
             self._check(lib.q35_engine_result(self.handle, rid, None, _ptr(toks), n.value, None), "result")
         return r, toks
+
+    def terminal(self, rid):
+        """Whether the request is complete, cancelled or failed."""
+        return REQ_STATUS[self.result(rid)[0].status] in ("complete", "cancelled", "failed")
 
     def cancel(self, rid):
         self._check(lib.q35_engine_cancel(self.handle, rid), "cancel")

@@ -6,18 +6,23 @@
 // reference's own, so a caller swaps qwen35x::CpuModel / CpuEngine for
 // qwen35x::hip::HipModel / HipEngine and keeps the rest of its code.
 //
+// Both engine modes are the reference's: direct mode (advance /
+// advance_batch) and, with CpuEngineConfig::max_queued_requests > 0, serving
+// mode (step / read_output, max_buffered_tokens, automatic prefixes through
+// CpuRequestSpec::register_prefix_tokens and trust_namespace).
+//
 // Differences, each reported as an error rather than ignored:
 // - CpuPrefix has a private constructor, so prefixes are HipPrefix handles
 //   (register_prefix / find_prefix return them; submit takes one beside the
 //   spec) instead of CpuRequestSpec::prefix;
-// - drafting (draft_mode, mtp_max_tokens > 1), serving mode
-//   (max_queued_requests, register_prefix_tokens, read_output) and the CPU
-//   executor knobs (threads, spin counts, KV bit widths) have no counterpart.
+// - drafting (draft_mode, mtp_max_tokens > 1) and the CPU executor knobs
+//   (threads, spin counts, KV bit widths) have no counterpart.
 #pragma once
 
 #include "q35_hip.h"
 #include "qwen35x/runtime/cpu_engine.h"
 
+#include <algorithm>
 #include <cstdint>
 #include <map>
 #include <memory>
@@ -83,6 +88,7 @@ class HipModel final {
   HipModel(const HipModel &) = delete;
   HipModel &operator=(const HipModel &) = delete;
   q35_model *handle() const noexcept { return model_; }
+  const char *last_error() const noexcept { return q35_context_last_error(ctx_); }
 
  private:
   HipModel() = default;
@@ -174,8 +180,13 @@ class HipEngine final {
       error = "HIP backend: no model.";
       return nullptr;
     }
-    if (config.max_queued_requests != 0 || config.mtp_max_tokens > 1) {
-      error = "HIP backend: serving mode and MTP drafting are not supported.";
+    if (config.mtp_max_tokens > 1) {
+      error = "HIP backend: MTP drafting is not supported.";
+      return nullptr;
+    }
+    if (config.max_queued_requests > static_cast<std::size_t>(INT32_MAX) ||
+        config.max_buffered_tokens > static_cast<std::size_t>(INT32_MAX)) {
+      error = "Invalid CPU engine configuration.";
       return nullptr;
     }
     q35_engine_config c{};
@@ -188,10 +199,12 @@ class HipEngine final {
     c.max_prefix_bytes = config.max_prefix_bytes;
     c.max_prefill_requests = static_cast<int32_t>(config.max_prefill_requests);
     c.packed_steps = packed_steps ? 1 : 0;
+    c.max_queued_requests = static_cast<int32_t>(config.max_queued_requests);
+    c.max_buffered_tokens = static_cast<int32_t>(config.max_buffered_tokens);
     auto owner = std::make_shared<detail::EngineHandle>();
     owner->model = std::move(model);
     if (q35_engine_create(owner->model->handle(), &c, &owner->engine) != Q35_OK) {
-      error = "HIP backend: engine creation failed (check max_decode_batch_size <= 64 and the context limits).";
+      error = std::string("HIP backend: ") + owner->model->last_error();
       return nullptr;
     }
     return std::unique_ptr<HipEngine>(new HipEngine(std::move(owner)));
@@ -202,8 +215,8 @@ class HipEngine final {
 
   // CpuEngine::submit; `prefix` takes the place of CpuRequestSpec::prefix.
   CpuRequestId submit(CpuRequestSpec spec, std::string &error, std::shared_ptr<const HipPrefix> prefix = nullptr) {
-    if (spec.prefix != nullptr || spec.register_prefix_tokens != 0 || spec.draft_mode != CpuDraftMode::off) {
-      error = "HIP backend: use a HipPrefix handle; drafting and automatic prefix registration are not supported.";
+    if (spec.prefix != nullptr || spec.draft_mode != CpuDraftMode::off) {
+      error = "HIP backend: use a HipPrefix handle; drafting is not supported.";
       return 0;
     }
     auto glue = std::make_unique<detail::RequestGlue>();
@@ -250,6 +263,8 @@ class HipEngine final {
       r.sampling_constraint = &glue->c_constraint;
     }
     r.prefix = prefix != nullptr ? prefix->id() : 0;
+    r.register_prefix_tokens = spec.register_prefix_tokens;
+    r.trust_namespace = spec.trust_namespace.c_str();
     uint64_t id = 0;
     if (q35_engine_submit_spec(owner_->engine, &r, &id) != Q35_OK) {
       error = q35_engine_last_error(owner_->engine);
@@ -290,6 +305,19 @@ class HipEngine final {
     int32_t p = 0;
     const bool ok = check(q35_engine_step(owner_->engine, &p), error);
     progressed = p != 0;
+    return ok;
+  }
+  // CpuEngine::read_output (cpu_engine.h:197-201): appends to `output`.
+  bool read_output(CpuRequestId id, std::size_t max_tokens, std::vector<std::int32_t> &output, std::string &error) {
+    // at most every output token of the request is unread
+    std::size_t total = 0;
+    if (q35_engine_result(owner_->engine, id, nullptr, nullptr, 0, &total) == Q35_OK)
+      max_tokens = std::min(max_tokens, total);
+    const std::size_t at = output.size();
+    std::size_t n = 0;
+    output.resize(at + max_tokens);
+    const bool ok = check(q35_engine_read_output(owner_->engine, id, max_tokens, output.data() + at, &n), error);
+    output.resize(at + (ok ? n : 0));
     return ok;
   }
 
@@ -345,6 +373,8 @@ class HipEngine final {
     out.prefix_restore_ms = r.prefix_restore_ms;
     out.prefill_ms = r.prefill_ms;
     out.decode_ms = r.decode_ms;
+    out.queue_ms = r.queue_ms;
+    out.prefix_written_tokens = r.prefix_written_tokens;
     if (out.status == CpuRequestStatus::failed) {
       const auto g = glue_.find(id);
       out.error = g != glue_.end() && !g->second->error.empty() ? g->second->error : last_error_;

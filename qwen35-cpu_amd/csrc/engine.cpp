@@ -6,11 +6,19 @@
 //   advance_batch   one decode row per distinct active request; validation
 //                   leaves requests untouched; a failed forward fails every
 //                   row and is never retried (cpu_engine.inl:939-1017)
-//   step            serving scheduler: retire, admit, alternate decode batches
-//                   with prefill chunks, rotate for fairness
+//   step            serving scheduler (serving mode, max_queued_requests > 0):
+//                   retire, admit up to max_prefill_requests, alternate decode
+//                   batches with prefill chunks, rotate for fairness, skip
+//                   rows whose unread output is full
 //                   (cpu_engine_scheduler.inl:2-105) -- or, with packed_steps,
 //                   run the decode batch and the prompt chunks of up to
 //                   max_prefill_requests requests in one packed step
+//   read_output     confirmed tokens, stop-sequence prefixes held back
+//                   (cpu_engine_scheduler.inl:107-127)
+//   automatic prefixes  register_prefix_tokens in serving mode: built once by
+//                   the first request, published when its prefill reaches
+//                   the boundary, attached by the requests that waited for it
+//                   (cpu_engine_singleflight.inl)
 //   register_prefix / find_prefix   cpu_engine_prefix.inl:11-96: a state
 //                   snapshot plus the prefix's KV pages, shared by the
 //                   requests that attach it (CpuRequestSpec::prefix)
@@ -59,9 +67,14 @@ struct Request {
   size_t committed = 0;  // tokens whose state is in the slot / KV
   int32_t pending = -1;  // next decode input (last generated token)
   std::vector<int32_t> output;
+  size_t consumed = 0;  // output tokens handed out by read_output
   q35_request_result result{};
   bool resident = false;
   uint64_t prefix = 0;  // attached prefix, pinned until the request retires
+  size_t register_prefix = 0;  // automatic prefix boundary (0 = none)
+  std::string ns;              // trust namespace
+  bool has_ns = false;
+  std::chrono::steady_clock::time_point arrival;
 };
 
 // A cached prefix (CpuPrefix): snapshot, the pages of its tokens (one
@@ -98,6 +111,7 @@ struct q35_engine {
   size_t max_prefix_bytes = 0, prefix_bytes = 0;
   q35_prefix_stats prefix_stats{};
   q35_engine_stats stats{};
+  bool serving() const { return cfg.max_queued_requests > 0; }
 };
 
 namespace {
@@ -152,8 +166,9 @@ void unpin_prefix(q35_engine *e, uint64_t id) {
   if (p != nullptr && p->pins > 0) --p->pins;
 }
 
-void retire(q35_engine *e, Request &r) {
-  if (!r.resident || !terminal(r)) return;
+// Frees a request's device state: KV pages, slot, the attached prefix pin.
+void free_resident(q35_engine *e, Request &r) {
+  if (!r.resident) return;
   for (int32_t p : r.pages) (void)q35_page_release(e->rt, p);
   r.pages.clear();
   if (r.slot >= 0) (void)q35_slot_free(e->rt, r.slot);
@@ -161,6 +176,13 @@ void retire(q35_engine *e, Request &r) {
   r.resident = false;
   if (r.prefix != 0) unpin_prefix(e, r.prefix);
   r.prefix = 0;
+}
+
+// retire (cpu_engine.inl:432-440): in serving mode a terminal request gives
+// its device state back at once; in direct mode it keeps it until release.
+void retire(q35_engine *e, Request &r) {
+  if (!e->serving() || !r.resident || !terminal(r)) return;
+  free_resident(e, r);
 }
 
 int activate(q35_engine *e, Request &r) {
@@ -473,36 +495,182 @@ void fail_rows(const std::vector<Request *> &rows) {
   for (auto *r : rows) r->status = Q35_REQ_FAILED;
 }
 
+// Impl::confirmed (cpu_engine.inl:419-428): output tokens that can no longer
+// turn into a stop sequence (all of them once the request is terminal).
+size_t confirmed(const Request &r) {
+  if (terminal(r)) return r.output.size();
+  size_t held = 0;
+  for (const auto &stop : r.stop_sequences)
+    for (size_t n = 1; n < stop.size() && n <= r.output.size(); ++n)
+      if (std::equal(stop.begin(), stop.begin() + static_cast<std::ptrdiff_t>(n),
+                     r.output.end() - static_cast<std::ptrdiff_t>(n)))
+        held = std::max(held, n);
+  return r.output.size() - held;
+}
+
+// Impl::output_ready (cpu_engine.inl:429-431)
+bool output_ready(const q35_engine *e, const Request &r) {
+  return r.output.size() - r.consumed < static_cast<size_t>(e->cfg.max_buffered_tokens);
+}
+
+// Impl::short_readout (cpu_engine.inl:628-631): a selected readout with at
+// most 128 prompt tokens left; the reference shares prefill steps only
+// between these.
+bool short_readout(const Request &r) {
+  const size_t remaining = r.prompt.size() - r.committed;
+  return !r.selected.empty() && remaining > 0 && remaining <= 128;
+}
+
+// The prompt tokens one advance() or prompt segment prefills
+// (cpu_engine.inl:728-741): the canonical chunk (prefill_chunk_size, or 64
+// for prompts of at most 128 tokens and 128 otherwise), capped at an
+// automatic prefix boundary still ahead.
+size_t advance_chunk(const q35_engine *e, const Request &r) {
+  const size_t chunk = e->cfg.prefill_chunk_size > 0 ? static_cast<size_t>(e->cfg.prefill_chunk_size)
+                                                      : (r.prompt.size() <= 128 ? 64 : 128);
+  size_t count = q35_prefill_chunk_token_count(r.committed, r.prompt.size() - r.committed, chunk);
+  if (r.register_prefix > r.committed) count = std::min(count, r.register_prefix - r.committed);
+  return count;
+}
+
+// Device bytes of a prefix of n tokens: one recurrent state copy, the conv
+// ring and the final hidden row, plus the K and V rows of its pages.
+size_t prefix_size(const q35_engine *e, size_t n) {
+  const q35_model_dims &d = e->model->d;
+  const size_t pages = (n + e->cfg.page_tokens - 1) / e->cfg.page_tokens;
+  return (static_cast<size_t>(e->rt->rec_copy_stride) + e->rt->conv_slot_stride + d.hidden) * 4 +
+         pages * e->cfg.page_tokens * static_cast<size_t>(d.n_kv_heads) * d.head_dim * 2 * 2 * e->model->n_full;
+}
+
+// A prefix of the first n tokens of slot `slot` (state after n positions,
+// `hidden` the final normalized row of position n - 1): the snapshot plus a
+// reference to each page holding those positions. Pinned once for the
+// caller. Returns nullptr when the snapshot cannot be made.
+Prefix *capture_prefix(q35_engine *e, int32_t slot, const std::vector<int32_t> &tokens, const std::string &ns,
+                       const std::vector<int32_t> &pages, const float *hidden, size_t bytes) {
+  q35_state_snapshot *snap = nullptr;
+  if (q35_state_snapshot_create(e->rt, slot, static_cast<int32_t>(tokens.size()), hidden, &snap) != Q35_OK)
+    return nullptr;
+  auto p = std::make_unique<Prefix>();
+  p->id = e->next_prefix++;
+  p->tokens = tokens;
+  p->ns = ns;
+  p->snap = snap;
+  const size_t used = (tokens.size() + e->cfg.page_tokens - 1) / e->cfg.page_tokens;
+  p->pages.assign(pages.begin(), pages.begin() + static_cast<std::ptrdiff_t>(std::min(used, pages.size())));
+  for (int32_t page : p->pages) (void)q35_page_retain(e->rt, page);
+  p->bytes = bytes;
+  p->pins = 1;
+  e->prefix_bytes += bytes;
+  e->prefixes.push_back(std::move(p));
+  return e->prefixes.back().get();
+}
+
+// same_build (cpu_engine_singleflight.inl:2-10): two requests that would
+// build the same automatic prefix.
+bool same_build(const Request &a, const Request &b) {
+  return a.register_prefix != 0 && a.register_prefix == b.register_prefix && a.ns == b.ns &&
+         std::equal(a.prompt.begin(), a.prompt.begin() + static_cast<std::ptrdiff_t>(a.register_prefix),
+                    b.prompt.begin());
+}
+
+// prefix_admissible (cpu_engine_singleflight.inl:11-30): a request with an
+// automatic prefix attaches a published prefix of exactly that boundary, or
+// waits while another resident request is still building it.
+bool prefix_admissible(q35_engine *e, Request &r) {
+  const size_t count = r.register_prefix;
+  if (count == 0) return true;
+  for (auto &p : e->prefixes)
+    if (p->tokens.size() == count && p->ns == r.ns && std::equal(p->tokens.begin(), p->tokens.end(), r.prompt.begin())) {
+      if (r.prefix != p->id) {
+        if (r.prefix != 0) unpin_prefix(e, r.prefix);
+        r.prefix = p->id;
+        ++p->pins;
+      }
+      touch_prefix(e, p.get());
+      return true;
+    }
+  for (auto &kv : e->reqs) {
+    const Request &o = kv.second;
+    if (&o != &r && o.resident && !terminal(o) && o.committed < count && same_build(r, o)) return false;
+  }
+  return true;
+}
+
+// publish_prefix (cpu_engine_singleflight.inl:85-110): after the request's
+// prefill reached its boundary, its state and pages become a prefix the
+// request itself holds; when it cannot be stored, the request and those of
+// the same build go on as ordinary cold requests.
+void publish_prefix(q35_engine *e, Request &r, const float *hidden) {
+  const size_t count = r.register_prefix;
+  // the restored state is already private: the attached prefix may go
+  if (r.prefix != 0) unpin_prefix(e, r.prefix);
+  r.prefix = 0;
+  const size_t bytes = prefix_size(e, count);
+  Prefix *p = nullptr;
+  if (hidden != nullptr && prefix_room(e, bytes)) {
+    const std::vector<int32_t> tokens(r.prompt.begin(), r.prompt.begin() + static_cast<std::ptrdiff_t>(count));
+    p = capture_prefix(e, r.slot, tokens, r.ns, r.pages, hidden, bytes);
+  }
+  if (p != nullptr) {
+    r.prefix = p->id;
+    ++e->prefix_stats.prefix_builds;
+    r.result.prefix_written_tokens = count - r.result.cached_prefix_tokens;
+    return;
+  }
+  ++e->prefix_stats.prefix_build_fallbacks;
+  for (auto &kv : e->reqs)
+    if (&kv.second != &r && same_build(r, kv.second)) kv.second.register_prefix = 0;
+  r.register_prefix = 0;
+}
+
 }  // namespace
+
+// detail::prefill_chunk_token_count (src/runtime/prefill_chunk.h:10-17)
+extern "C" size_t q35_prefill_chunk_token_count(size_t position, size_t remaining, size_t chunk) {
+  constexpr size_t kRowAttentionLimit = 128;  // prefill_attention_row_limit
+  if (remaining == 0 || chunk == 0) return 0;
+  size_t count = std::min(chunk - position % chunk, remaining);
+  if (position < kRowAttentionLimit) count = std::min(count, kRowAttentionLimit - position);
+  return count;
+}
 
 extern "C" int q35_engine_create(q35_model *m, const q35_engine_config *cfg, q35_engine **out) {
   if (m == nullptr || cfg == nullptr || out == nullptr) return Q35_ERR_INVALID;
   *out = nullptr;
+  // CpuEngine::create validation (cpu_engine.inl:795-806)
   if (cfg->max_resident_requests <= 0 || cfg->max_context <= 0 || cfg->max_decode_batch_size <= 0 ||
-      cfg->max_decode_batch_size > q35::kMaxTokens || cfg->page_tokens <= 0)
-    return Q35_ERR_INVALID;
+      cfg->max_decode_batch_size > q35::kMaxTokens || cfg->page_tokens <= 0 || cfg->prefill_chunk_size < 0 ||
+      cfg->prefill_chunk_size > q35::kMaxStepRows || cfg->max_prefill_requests < 0 ||
+      cfg->max_prefill_requests > q35::kMaxPrefillSegments || cfg->max_queued_requests < 0 ||
+      (cfg->max_queued_requests > 0 && cfg->max_buffered_tokens <= 0))
+    return set_error(m->ctx, Q35_ERR_INVALID, "Invalid CPU engine configuration.");
   auto *e = new (std::nothrow) q35_engine();
   if (e == nullptr) return Q35_ERR_OOM;
   e->model = m;
   e->cfg = *cfg;
-  if (e->cfg.prefill_chunk_size <= 0) e->cfg.prefill_chunk_size = 128;
-  if (e->cfg.max_prefill_requests <= 0) e->cfg.max_prefill_requests = 1;
-  if (e->cfg.max_prefill_requests > q35::kMaxPrefillSegments || e->cfg.prefill_chunk_size > q35::kMaxStepRows) {
-    delete e;
-    return Q35_ERR_INVALID;
-  }
+  if (e->cfg.max_prefill_requests == 0) e->cfg.max_prefill_requests = 1;
   e->max_prefix_bytes = cfg->max_prefix_bytes ? static_cast<size_t>(cfg->max_prefix_bytes) : size_t(256) << 20;
   q35_runtime_config rc{};
-  rc.max_slots = cfg->max_resident_requests;
+  // one slot beyond the resident requests for register_prefix builds
+  rc.max_slots = cfg->max_resident_requests + 1;
   rc.max_batch = std::max(cfg->max_decode_batch_size, 1);
   rc.max_context = cfg->max_context;
   rc.page_tokens = cfg->page_tokens;
   rc.use_graphs = cfg->use_graphs;
   // rows of the largest step: the prompt chunks of a shared prefill, plus
   // the decode batch when the two are packed together
-  const long long step_rows = static_cast<long long>(e->cfg.max_prefill_requests) * e->cfg.prefill_chunk_size +
+  // (prefill_chunk_size 0: chunks of at most 128 prompt tokens)
+  const long long chunk = e->cfg.prefill_chunk_size > 0 ? e->cfg.prefill_chunk_size : 128;
+  const long long step_rows = static_cast<long long>(e->cfg.max_prefill_requests) * chunk +
                               (e->cfg.packed_steps ? rc.max_batch : 0);
-  rc.max_step_rows = static_cast<int32_t>(std::min<long long>(step_rows, q35::kMaxStepRows));
+  if (step_rows > q35::kMaxStepRows) {
+    delete e;
+    return set_error(m->ctx, Q35_ERR_INVALID,
+                     "max_prefill_requests * prefill_chunk_size (+ max_decode_batch_size with packed_steps) exceeds " +
+                         std::to_string(q35::kMaxStepRows) + " rows per step");
+  }
+  rc.max_step_rows = static_cast<int32_t>(step_rows);
   const int st = q35_runtime_create(m, &rc, &e->rt);
   if (st != Q35_OK) {
     delete e;
@@ -556,11 +724,11 @@ extern "C" int q35_engine_submit_spec(q35_engine *e, const q35_request_spec *spe
   const size_t n = spec->prompt_count, max_new = spec->max_new_tokens;
   const float penalty = spec->repetition_penalty;
   const uint64_t prefix = spec->prefix;
-  size_t resident = 0;
-  for (auto &kv : e->reqs) resident += kv.second.resident;
   auto valid_token = [&](int32_t t) { return t >= 0 && t < vocab; };
-  if (prompt == nullptr || n == 0 || max_new == 0 || n > ctx || max_new - 1 > ctx - n ||
-      e->reqs.size() >= static_cast<size_t>(e->cfg.max_resident_requests) + 64 ||
+  // record limit: resident plus queued requests, terminal results included
+  // until release (cpu_engine.inl:836)
+  const size_t records = static_cast<size_t>(e->cfg.max_resident_requests) + e->cfg.max_queued_requests;
+  if (prompt == nullptr || n == 0 || max_new == 0 || n > ctx || max_new - 1 > ctx - n || e->reqs.size() >= records ||
       (spec->forced_count != 0 && (spec->forced_output_tokens == nullptr || spec->forced_count != max_new)) ||
       !std::isfinite(spec->temperature) || spec->temperature < 0 || !std::isfinite(spec->top_p) ||
       spec->top_p <= 0 || spec->top_p > 1 || spec->top_k < 0 || !std::isfinite(penalty) || penalty < 1 ||
@@ -583,15 +751,32 @@ extern "C" int q35_engine_submit_spec(q35_engine *e, const q35_request_spec *spe
                     valid_token)))
     return fail(e, Q35_ERR_INVALID,
                 "Selected readout requires a Q4 DOT4 head, valid token IDs, its own callback and one forced token.");
+  if (e->serving()) {
+    // bounded queue; a stop sequence must fit the output buffer (cpu_engine.inl:877-886)
+    size_t queued = 0;
+    for (auto &kv : e->reqs) queued += kv.second.status == Q35_REQ_QUEUED;
+    bool long_stop = false;
+    for (size_t i = 0; i < spec->stop_sequence_count; ++i)
+      long_stop = long_stop || spec->stop_sequence_lengths[i] > static_cast<size_t>(e->cfg.max_buffered_tokens);
+    if (queued >= static_cast<size_t>(e->cfg.max_queued_requests) || long_stop)
+      return fail(e, Q35_ERR_INVALID, "Queue full or stop sequence exceeds output buffer capacity.");
+  }
+  const bool has_ns = spec->trust_namespace != nullptr;
+  const std::string ns = has_ns ? spec->trust_namespace : "";
   Prefix *pre = nullptr;
   if (prefix != 0) {
-    // the attached prefix must be a prefix of the prompt (cpu_engine.inl:895-910)
+    // the attached prefix must be a prefix of the prompt, of the request's
+    // namespace when it names one (cpu_engine.inl:895-910)
     pre = find_prefix_id(e, prefix);
-    if (pre == nullptr || pre->tokens.size() > n || !std::equal(pre->tokens.begin(), pre->tokens.end(), prompt))
-      return fail(e, Q35_ERR_INVALID, "Prefix does not match the request.");
+    if (pre == nullptr || pre->tokens.size() > n || !std::equal(pre->tokens.begin(), pre->tokens.end(), prompt) ||
+        (has_ns && pre->ns != ns))
+      return fail(e, Q35_ERR_INVALID, "Prefix model, configuration, draft kind, namespace or token identity mismatch.");
   }
+  // automatic prefix builds (cpu_engine.inl:887-892)
+  const size_t reg = spec->register_prefix_tokens;
+  if (reg != 0 && (!e->serving() || (pre != nullptr && pre->tokens.size() >= reg) || ns.empty() || reg > n))
+    return fail(e, Q35_ERR_INVALID, "Automatic prefix builds require serving mode, a namespace and a valid prefix length.");
   Request r;
-  r.id = e->next_id++;
   r.prompt.assign(prompt, prompt + n);
   r.max_new = max_new;
   r.penalty = penalty;
@@ -610,17 +795,25 @@ extern "C" int q35_engine_submit_spec(q35_engine *e, const q35_request_spec *spe
   for (size_t i = 0, at = 0; i < spec->stop_sequence_count; at += spec->stop_sequence_lengths[i++])
     r.stop_sequences.emplace_back(spec->stop_sequences + at, spec->stop_sequences + at + spec->stop_sequence_lengths[i]);
   r.status = Q35_REQ_QUEUED;
+  r.register_prefix = reg;
+  r.ns = pre != nullptr && !has_ns ? pre->ns : ns;
+  r.has_ns = has_ns;
+  r.arrival = std::chrono::steady_clock::now();
   if (pre != nullptr) {
     r.prefix = prefix;
     ++pre->pins;
   }
-  if (resident < static_cast<size_t>(e->cfg.max_resident_requests)) {
+  // direct mode activates at once; serving mode queues without device state
+  // until step admits it (cpu_engine.inl:918-921)
+  if (!e->serving()) {
     const int st = activate(e, r);
     if (st != Q35_OK) {
       if (r.prefix != 0) unpin_prefix(e, r.prefix);
       return st;
     }
   }
+  // IDs are monotonic and never reused; a rejected submit takes none
+  r.id = e->next_id++;
   *out_id = r.id;
   e->reqs.emplace(r.id, std::move(r));
   return Q35_OK;
@@ -655,7 +848,11 @@ static int prefill_chunks(q35_engine *e, Request &r, size_t limit) {
   }
   size_t done = 0;
   while (done < limit && r.committed < r.prompt.size()) {
-    const size_t n = std::min({rows, limit - done, r.prompt.size() - r.committed});
+    size_t n = std::min({rows, limit - done, r.prompt.size() - r.committed});
+    // an automatic prefix boundary ends a device chunk, so its state can be
+    // captured (cpu_engine.inl:737-741)
+    const bool building = r.register_prefix > r.committed;
+    if (building) n = std::min(n, r.register_prefix - r.committed);
     int st = own_page(e, r, r.committed);
     if (st == Q35_OK) st = ensure_page(e, r, r.committed + n - 1);
     if (st != Q35_OK) {
@@ -674,6 +871,11 @@ static int prefill_chunks(q35_engine *e, Request &r, size_t limit) {
     r.committed += n;
     r.result.prefill_tokens += n;
     done += n;
+    if (building && r.committed == r.register_prefix) {
+      std::vector<float> hidden(e->model->d.hidden);
+      const bool have = q35_runtime_last_hidden(e->rt, hidden.data(), hidden.size()) == Q35_OK;
+      publish_prefix(e, r, have ? hidden.data() : nullptr);
+    }
     if (r.committed == r.prompt.size()) {
       if (!is_greedy(r)) {
         std::vector<float> hidden(e->model->d.hidden);
@@ -695,10 +897,11 @@ static int prefill_chunks(q35_engine *e, Request &r, size_t limit) {
 extern "C" int q35_engine_advance(q35_engine *e, uint64_t id) {
   if (e == nullptr) return Q35_ERR_INVALID;
   e->error.clear();
+  if (e->serving() && !e->scheduling) return fail(e, Q35_ERR_STATE, "Serving mode must be driven through step.");
   auto it = e->reqs.find(id);
   if (it == e->reqs.end()) return fail(e, Q35_ERR_STATE, "Unknown request ID.");
   Request &r = it->second;
-  if (r.status == Q35_REQ_PREFILL) return prefill_chunks(e, r, static_cast<size_t>(e->cfg.prefill_chunk_size));
+  if (r.status == Q35_REQ_PREFILL) return prefill_chunks(e, r, advance_chunk(e, r));
   if (r.status != Q35_REQ_DECODE) return fail(e, Q35_ERR_STATE, "Request is not active.");
   return q35_engine_advance_batch(e, &id, 1);
 }
@@ -706,6 +909,7 @@ extern "C" int q35_engine_advance(q35_engine *e, uint64_t id) {
 extern "C" int q35_engine_advance_batch(q35_engine *e, const uint64_t *ids, size_t count) {
   if (e == nullptr) return Q35_ERR_INVALID;
   e->error.clear();
+  if (e->serving() && !e->scheduling) return fail(e, Q35_ERR_STATE, "Serving mode must be driven through step.");
   if (count == 0) return Q35_OK;
   if (ids == nullptr || count > static_cast<size_t>(e->cfg.max_decode_batch_size))
     return fail(e, Q35_ERR_INVALID, "Decode batch exceeds max_decode_batch_size.");
@@ -768,6 +972,7 @@ extern "C" int q35_engine_advance_batch(q35_engine *e, const uint64_t *ids, size
 extern "C" int q35_engine_prefill_batch(q35_engine *e, const uint64_t *ids, size_t count) {
   if (e == nullptr || (count && ids == nullptr)) return Q35_ERR_INVALID;
   e->error.clear();
+  if (e->serving()) return fail(e, Q35_ERR_STATE, "Serving mode must be driven through step.");
   if (count > static_cast<size_t>(e->cfg.max_decode_batch_size))
     return fail(e, Q35_ERR_INVALID, "Prefill batch exceeds max_decode_batch_size.");
   std::vector<Request *> rows;
@@ -799,11 +1004,19 @@ static int packed_step(q35_engine *e, const std::vector<Request *> &decode, cons
   std::vector<int32_t> table(n * static_cast<size_t>(max_pages), 0), inputs(nd);
   std::vector<q35_segment> segs(n);
   std::vector<size_t> counts(n, 1);
+  // segments that end at an automatic prefix boundary: their head row
+  // carries the final hidden row the prefix keeps (its token is not used
+  // unless the prompt ends there too)
+  std::vector<uint8_t> publish(n, 0), ends(n, 0);
   bool sample = false;
   for (size_t i = 0; i < n; ++i) {
     Request &r = *all[i];
     const bool dec = i < nd;
-    if (!dec) counts[i] = std::min(static_cast<size_t>(e->cfg.prefill_chunk_size), r.prompt.size() - r.committed);
+    if (!dec) {
+      counts[i] = advance_chunk(e, r);
+      publish[i] = r.register_prefix > r.committed && r.committed + counts[i] == r.register_prefix;
+      ends[i] = r.committed + counts[i] == r.prompt.size();
+    }
     int st = own_page(e, r, r.committed);
     if (st == Q35_OK) st = ensure_page(e, r, r.committed + counts[i] - 1);
     if (st != Q35_OK) {
@@ -821,8 +1034,8 @@ static int packed_step(q35_engine *e, const std::vector<Request *> &decode, cons
     g.max_pages = max_pages;
     g.penalty = r.penalty;
     g.count_input = dec ? 1 : 0;
-    g.want_token = dec || r.committed + counts[i] == r.prompt.size();
-    if (g.want_token && !is_greedy(r)) sample = true;
+    g.want_token = dec || ends[i] || publish[i];
+    if ((dec || ends[i]) && !is_greedy(r)) sample = true;
   }
   std::vector<int32_t> out(n, -1);
   std::vector<q35_row_sampling> rs;
@@ -843,6 +1056,18 @@ static int packed_step(q35_engine *e, const std::vector<Request *> &decode, cons
   if (st != Q35_OK) {
     fail_rows(all);
     return fail(e, st, e->model->ctx->error.c_str());
+  }
+  // hidden rows of the head rows (want_token segments in order), for the
+  // prefixes published by this step
+  const size_t H = static_cast<size_t>(e->model->d.hidden);
+  std::vector<float> hidden;
+  std::vector<size_t> head_of(n, 0);
+  if (std::find(publish.begin(), publish.end(), 1) != publish.end()) {
+    size_t heads = 0;
+    for (size_t i = 0; i < n; ++i)
+      if (segs[i].want_token) head_of[i] = heads++;
+    hidden.assign(heads * H, 0.0F);
+    if (q35_runtime_last_hidden(e->rt, hidden.data(), hidden.size()) != Q35_OK) hidden.clear();
   }
   count_forward(e, !sample);
   if (nd > 0) {
@@ -873,7 +1098,8 @@ static int packed_step(q35_engine *e, const std::vector<Request *> &decode, cons
       r.result.prefill_ms += ms;
     }
     r.result.committed_tokens = r.committed;
-    if (!segs[i].want_token) continue;
+    if (publish[i]) publish_prefix(e, r, hidden.empty() ? nullptr : hidden.data() + head_of[i] * H);
+    if (!segs[i].want_token || (!dec && !ends[i])) continue;
     int32_t token = out[i];
     if (sample) {
       const int cs = choose_token(e, r, cands.data() + i * Q35_MAX_CANDIDATES,
@@ -896,31 +1122,44 @@ extern "C" int q35_engine_step(q35_engine *e, int32_t *progressed) {
   if (e == nullptr || progressed == nullptr) return Q35_ERR_INVALID;
   *progressed = 0;
   e->error.clear();
-  if (e->scheduling) return fail(e, Q35_ERR_STATE, "step is not reentrant.");
+  if (!e->serving() || e->scheduling)
+    return fail(e, Q35_ERR_STATE, "step requires serving mode and a non-reentrant owner.");
   e->scheduling = true;
   struct Guard {
     bool &v;
     ~Guard() { v = false; }
   } guard{e->scheduling};
   size_t resident = 0;
-  std::vector<uint64_t> queued;
+  std::vector<uint64_t> queued;  // in ID order (the map is ordered)
   for (auto &kv : e->reqs) {
     retire(e, kv.second);
     resident += kv.second.resident;
     if (kv.second.status == Q35_REQ_QUEUED) queued.push_back(kv.first);
   }
-  // admit at most one queued request per step (max_prefill_requests = 1)
-  if (!queued.empty() && resident < static_cast<size_t>(e->cfg.max_resident_requests)) {
-    Request &r = e->reqs.at(queued.front());
+  // admission: up to max_prefill_requests queued requests while resident
+  // room lasts, skipping those waiting on another request's prefix build
+  size_t admitted = 0;
+  for (uint64_t id : queued) {
+    if (resident >= static_cast<size_t>(e->cfg.max_resident_requests) ||
+        admitted >= static_cast<size_t>(e->cfg.max_prefill_requests))
+      break;
+    Request &r = e->reqs.at(id);
+    if (!prefix_admissible(e, r)) continue;
+    ++admitted;
+    ++resident;
+    r.result.queue_ms = ms_since(r.arrival);
     *progressed = 1;
     const int st = activate(e, r);
     if (st != Q35_OK) {
       r.status = Q35_REQ_FAILED;
+      retire(e, r);
       return st;
     }
   }
+  // rows whose unread output is below max_buffered_tokens
   std::vector<uint64_t> prefill, decode;
   for (auto &kv : e->reqs) {
+    if (!output_ready(e, kv.second)) continue;
     if (kv.second.status == Q35_REQ_PREFILL) prefill.push_back(kv.first);
     if (kv.second.status == Q35_REQ_DECODE) decode.push_back(kv.first);
   }
@@ -931,50 +1170,81 @@ extern "C" int q35_engine_step(q35_engine *e, int32_t *progressed) {
   rotate(decode, e->last_decode);
   if (prefill.empty() && decode.empty()) return Q35_OK;
   *progressed = 1;
-  // prompt chunks of up to max_prefill_requests requests (a complete prefix
-  // hit goes through advance(): its first token comes from the prefix)
-  auto chunkable = [&](uint64_t id) {
-    const Request &r = e->reqs.at(id);
-    return r.committed < r.prompt.size();
-  };
-  std::vector<uint64_t> shared;
-  for (auto id : prefill) {
-    if (shared.size() == static_cast<size_t>(e->cfg.max_prefill_requests)) break;
-    if (chunkable(id)) shared.push_back(id);
-  }
-  const bool pack = !shared.empty() && (shared.size() > 1 || (e->cfg.packed_steps && !decode.empty())) &&
-                    (!prefill.empty() && chunkable(prefill.front()));
-  if (pack) {
-    std::vector<Request *> drows, prows;
-    if (e->cfg.packed_steps) {
+  if (e->cfg.packed_steps) {
+    // packed steps (no reference counterpart): the decode batch and the
+    // prompt chunks of up to max_prefill_requests requests in one step (a
+    // complete prefix hit goes through advance(): its first token comes
+    // from the prefix)
+    auto chunkable = [&](uint64_t id) {
+      const Request &r = e->reqs.at(id);
+      return r.committed < r.prompt.size();
+    };
+    std::vector<uint64_t> shared;
+    for (auto id : prefill) {
+      if (shared.size() == static_cast<size_t>(e->cfg.max_prefill_requests)) break;
+      if (chunkable(id)) shared.push_back(id);
+    }
+    if (!shared.empty() && (shared.size() > 1 || !decode.empty()) && chunkable(prefill.front())) {
+      std::vector<Request *> drows, prows;
       decode.resize(std::min(decode.size(), static_cast<size_t>(e->cfg.max_decode_batch_size)));
       for (auto id : decode) drows.push_back(&e->reqs.at(id));
       if (!decode.empty()) e->last_decode = decode.back();
+      for (auto id : shared) prows.push_back(&e->reqs.at(id));
+      e->last_prefill = shared.back();
+      e->prefer_decode = drows.empty();
+      const int st = packed_step(e, drows, prows);
+      for (auto *r : drows) retire(e, *r);
+      for (auto *r : prows) retire(e, *r);
+      return st;
     }
-    for (auto id : shared) prows.push_back(&e->reqs.at(id));
-    e->last_prefill = shared.back();
-    e->prefer_decode = drows.empty();
-    const int st = packed_step(e, drows, prows);
-    for (auto *r : drows) retire(e, *r);
-    for (auto *r : prows) retire(e, *r);
-    return st;
   }
+  // the reference's alternation (cpu_engine_scheduler.inl:64-104)
   const bool do_decode = !decode.empty() && (prefill.empty() || e->prefer_decode);
-  e->prefer_decode = !do_decode;
-  int st;
   std::vector<uint64_t> work;
   if (do_decode) {
     decode.resize(std::min(decode.size(), static_cast<size_t>(e->cfg.max_decode_batch_size)));
     work = decode;
     e->last_decode = work.back();
-    st = q35_engine_advance_batch(e, work.data(), work.size());
   } else {
     work.push_back(prefill.front());
+    // several requests share a prefill step only as short selected readouts
+    if (e->cfg.max_prefill_requests > 1 && short_readout(e->reqs.at(work.front())))
+      for (size_t i = 1; i < prefill.size(); ++i) {
+        if (work.size() == static_cast<size_t>(e->cfg.max_prefill_requests)) break;
+        if (short_readout(e->reqs.at(prefill[i]))) work.push_back(prefill[i]);
+      }
     e->last_prefill = work.back();
+  }
+  e->prefer_decode = !do_decode;
+  int st;
+  if (do_decode) {
+    st = q35_engine_advance_batch(e, work.data(), work.size());
+  } else if (work.size() == 1) {
     st = q35_engine_advance(e, work.front());
+  } else {
+    // shared prefill: a failed step fails every request in it
+    std::vector<Request *> prows;
+    for (auto id : work) prows.push_back(&e->reqs.at(id));
+    st = packed_step(e, {}, prows);
   }
   for (auto id : work) retire(e, e->reqs.at(id));
   return st;
+}
+
+extern "C" int q35_engine_read_output(q35_engine *e, uint64_t id, size_t max_tokens, int32_t *out, size_t *count) {
+  if (e == nullptr || count == nullptr || (max_tokens != 0 && out == nullptr)) return Q35_ERR_INVALID;
+  *count = 0;
+  e->error.clear();
+  if (!e->serving()) return fail(e, Q35_ERR_STATE, "read_output requires serving mode.");
+  auto it = e->reqs.find(id);
+  if (it == e->reqs.end()) return fail(e, Q35_ERR_STATE, "Unknown request ID.");
+  Request &r = it->second;
+  const size_t n = std::min(max_tokens, confirmed(r) - r.consumed);
+  std::copy(r.output.begin() + static_cast<std::ptrdiff_t>(r.consumed),
+            r.output.begin() + static_cast<std::ptrdiff_t>(r.consumed + n), out);
+  r.consumed += n;
+  *count = n;
+  return Q35_OK;
 }
 
 extern "C" int q35_engine_result(q35_engine *e, uint64_t id, q35_request_result *out, int32_t *tokens,
@@ -1029,8 +1299,7 @@ extern "C" int q35_engine_release(q35_engine *e, uint64_t id) {
   auto it = e->reqs.find(id);
   if (it == e->reqs.end()) return Q35_ERR_STATE;
   Request &r = it->second;
-  if (!terminal(r)) r.status = Q35_REQ_CANCELLED;
-  retire(e, r);
+  free_resident(e, r);
   if (r.prefix != 0) unpin_prefix(e, r.prefix);  // a queued request never became resident
   e->reqs.erase(it);
   return Q35_OK;

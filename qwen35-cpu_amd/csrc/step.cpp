@@ -1746,6 +1746,7 @@ extern "C" int q35_runtime_step_segments(q35_runtime *rt, const q35_segment *seg
   std::vector<float> raw(raw_logits != nullptr ? static_cast<size_t>(sh.heads) * vocab : 0);
   if ((st = finish_candidates(rt, sh.heads, cands.data(), raw_logits != nullptr ? raw.data() : nullptr)) != Q35_OK)
     return st;
+  rt->last_batch = sh.heads;
   for (int i = 0; i < count; ++i)
     for (int k = 0; k < kMaxCandidates; ++k)
       out_candidates[static_cast<size_t>(i) * kMaxCandidates + k] = q35_candidate{-INFINITY, -1};

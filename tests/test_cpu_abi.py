@@ -131,3 +131,27 @@ def test_generator_rows_are_deterministic_and_seeded(q):
     assert np.array_equal(a, b) and not np.array_equal(a, c)
     big = q.random_weight_rows("v", 1, 0, 256, 1024, 1.0)
     assert abs(big.mean()) < 0.01 and abs(big.std() - 1) < 0.01
+
+
+def test_prefill_chunk_token_count_matches_reference_vectors(q):
+    """q35_prefill_chunk_token_count against the schedules and single values of
+    the reference's tests/prefill_chunk_test.cpp:20-30 (host-only, no GPU)."""
+    f = q.lib.q35_prefill_chunk_token_count
+
+    def schedule(total, chunk, expected):
+        pos = 0
+        for count in expected:
+            if f(pos, total - pos, chunk) != count:
+                return False
+            pos += count
+        return pos == total
+
+    assert schedule(579, 512, [128, 384, 67])
+    assert schedule(579, 128, [128, 128, 128, 128, 67])
+    assert schedule(129, 64, [64, 64, 1])
+    assert schedule(221, 96, [96, 32, 64, 29])
+    assert schedule(127, 512, [127])
+    assert schedule(128, 512, [128])
+    assert schedule(129, 512, [128, 1])
+    assert f(74, 505, 512) == 54 and f(221, 358, 512) == 291 and f(512, 67, 512) == 67
+    assert f(0, 0, 512) == 0 and f(0, 10, 0) == 0

@@ -67,19 +67,111 @@ def test_chunked_advance_matches(q, small):
     eng.close()
 
 
+def serve(eng, ids, steps=500, read=1 << 20):
+    """Drives a serving-mode engine through step(), reading every request's
+    output after each step as server.cpp:275-300 does: the tokens read."""
+    got = {i: [] for i in ids}
+    for _ in range(steps):
+        eng.step()
+        for i in ids:
+            got[i] += eng.read_output(i, read).tolist()
+        if all(eng.terminal(i) and len(got[i]) == eng.result(i)[1].size for i in ids):
+            break
+    return got
+
+
 def test_scheduler_step_drains(q, small):
     d, sched, tensors, model, prompts, refs = small
-    # two resident slots for four requests: admission must wait for retirement
+    # serving mode, two resident slots for four queued requests: admission
+    # waits for retirement
     eng = q.Engine(model, max_resident_requests=2, max_context=64, max_decode_batch_size=2,
-                   prefill_chunk_size=5, page_tokens=16)
+                   prefill_chunk_size=5, page_tokens=16, max_queued_requests=4)
     ids = [eng.submit(p, max_new_tokens=NEW) for p in prompts]
-    for _ in range(500):
-        if not eng.step():
-            break
+    st = eng.stats()
+    assert st["queued_requests"] == 4 and st["resident_requests"] == 0  # queued requests hold no device state
+    got = serve(eng, ids, read=2)
     for rid, ref in zip(ids, refs):
         res, toks = eng.result(rid)
         assert res.status == q.REQ_STATUS_INV["complete"], res.status
         check_tokens(toks, ref)
+        assert got[rid] == toks.tolist()
+        assert res.queue_ms >= 0.0
+    assert eng.stats()["resident_requests"] == 0  # terminal requests retire at once in serving mode
+    eng.close()
+
+
+def test_serving_mode_contract(q, small):
+    """CpuEngine's two modes (cpu_engine.inl:832-948,
+    cpu_engine_scheduler.inl:2-127): step and read_output only in serving
+    mode, advance and advance_batch only outside it; the record limit and
+    the bounded queue; stop sequences longer than the output buffer are
+    rejected; a request whose unread output reaches max_buffered_tokens is
+    not scheduled until read_output drains it; a token that may start a stop
+    sequence is held back by read_output until the next token resolves it."""
+    d, sched, tensors, model, prompts, refs = small
+    E = q.Q35Error
+    direct = q.Engine(model, max_resident_requests=2, max_context=64, max_decode_batch_size=2, page_tokens=16)
+    a = direct.submit(prompts[1], max_new_tokens=NEW)
+    with pytest.raises(E, match="step requires serving mode"):
+        direct.step()
+    with pytest.raises(E, match="read_output requires serving mode"):
+        direct.read_output(a)
+    direct.submit(prompts[0], max_new_tokens=NEW)
+    with pytest.raises(E):
+        direct.submit(prompts[2], max_new_tokens=NEW)  # direct mode: at most max_resident_requests records
+    direct.close()
+    with pytest.raises(E):
+        q.Engine(model, max_resident_requests=1, max_context=64, max_decode_batch_size=2, page_tokens=16,
+                 max_queued_requests=2, max_buffered_tokens=0)
+
+    eng = q.Engine(model, max_resident_requests=1, max_context=64, max_decode_batch_size=2, page_tokens=16,
+                   max_queued_requests=2, max_buffered_tokens=2)
+    with pytest.raises(E, match="Queue full or stop sequence"):
+        eng.submit_spec(prompts[0], NEW, temperature=0.0, stop_sequences=[[1, 2, 3]])
+    a = eng.submit(prompts[1], max_new_tokens=NEW)
+    b = eng.submit(prompts[3], max_new_tokens=NEW)
+    with pytest.raises(E, match="Queue full"):
+        eng.submit(prompts[0], max_new_tokens=NEW)
+    with pytest.raises(E, match="Serving mode must be driven through step"):
+        eng.advance(a)
+    with pytest.raises(E, match="Serving mode must be driven through step"):
+        eng.advance_batch([a])
+    for _ in range(20):
+        eng.step()
+    res, toks = eng.result(a)
+    assert toks.size == 2 and res.status == q.REQ_STATUS_INV["decode"]  # two unread tokens: a waits
+    assert eng.result(b)[0].status == q.REQ_STATUS_INV["queued"]  # one resident slot
+    assert eng.read_output(a, 1).tolist() == toks[:1].tolist()
+    for _ in range(20):
+        eng.step()
+    assert eng.result(a)[1].size == 3  # one token of room, one more token
+    got = serve(eng, [a, b])
+    for rid, k in ((a, 1), (b, 3)):
+        res, toks = eng.result(rid)
+        assert res.status == q.REQ_STATUS_INV["complete"]
+        check_tokens(toks, refs[k])
+    assert [int(t) for t in eng.result(a)[1][:1]] + got[a] == eng.result(a)[1].tolist()
+    assert got[b] == eng.result(b)[1].tolist()
+    eng.close()
+
+    # a stop sequence [t2, x] with x never generated after t2: read_output
+    # holds t2 back until the next token shows the sequence does not match
+    eng = q.Engine(model, max_resident_requests=2, max_context=64, max_decode_batch_size=2, page_tokens=16,
+                   max_queued_requests=2)
+    free = serve(eng, [eng.submit(prompts[1], max_new_tokens=NEW)])
+    toks = list(free.values())[0]
+    stop = [toks[2], (toks[3] + 1) % d["vocab"]]
+    c = eng.submit_spec(prompts[1], NEW, temperature=0.0, repetition_penalty=1.0, stop_sequences=[stop])
+    seen = []
+    for _ in range(50):
+        eng.step()
+        n = eng.result(c)[1].size
+        if n == 3:
+            seen.append(eng.read_output(c).tolist())
+        if n == 4:
+            seen.append(eng.read_output(c).tolist())
+            break
+    assert seen == [toks[:2], toks[2:4]], (seen, toks)
     eng.close()
 
 

@@ -11,7 +11,9 @@ prefix in the same decode batch, and for a complete hit (prompt == prefix)
 whose first token comes from its own greedy head on the stored hidden row
 (cpu_engine.inl:711-726), with and without a repetition penalty. The
 from-scratch tokens are themselves checked against the CPU oracle, so a
-prefix hit is tied to the restated reference step, not only to this engine.""" 
+prefix hit is tied to the restated reference step, not only to this engine.
+In serving mode the same holds for automatic prefixes (register_prefix_tokens):
+built once by the first request, attached by the requests that waited.""" 
 import numpy as np
 import pytest
 
@@ -149,3 +151,75 @@ def test_find_dedup_evict_and_errors(q, small):
     assert eng.find_prefix(t, "a") == (b, 12)
     assert eng.free_pages() == free0 - 1
     eng.close()
+
+
+def serve(eng, ids):
+    """Drives a serving-mode engine through step() and read_output."""
+    got = {i: [] for i in ids}
+    for _ in range(500):
+        eng.step()
+        for i in ids:
+            got[i] += eng.read_output(i).tolist()
+        if all(eng.terminal(i) and len(got[i]) == eng.result(i)[1].size for i in ids):
+            break
+    return got
+
+
+@pytest.mark.parametrize("plen", [40, 48])
+def test_automatic_prefix_single_flight(q, small, plen):
+    """register_prefix_tokens in serving mode (cpu_engine_singleflight.inl:
+    same_build, prefix_admissible, publish_prefix; cpu_engine.inl:737-760): of
+    three queued requests sharing a plen-token prefix, the first is admitted
+    and builds it, the other two wait while it is building (not admitted
+    although slots are free), then attach the published prefix. Every
+    request's tokens equal the cold run's bit for bit; the builder reports
+    plen newly written tokens, the others plen cached ones. A prefix ending
+    inside a page (40) leaves a shared tail page that the builder itself
+    copies on its next write."""
+    d, model = small
+    rng = np.random.default_rng(17 + plen)
+    shared = rng.integers(0, d["vocab"], size=plen).astype(np.int32)
+    prompts = [np.concatenate([shared, rng.integers(0, d["vocab"], size=n).astype(np.int32)]) for n in (9, 14, 5)]
+    # the cold run on the same engine in direct mode, tied to the oracle up to
+    # the first near-tie (greedy top-2 margin below 0.1: the kernels and the
+    # oracle round differently inside the 1e-3 stage tolerance)
+    cold = engine(q, model)
+    want = [toks for _, toks in drain(q, cold, [cold.submit(p, NEW) for p in prompts])]
+    cold.close()
+    dd, sched, tensors = model.oracle
+    for p, toks in zip(prompts, want):
+        ref, lg = oracle_greedy(dd, sched, tensors, p[None, :], NEW, 1.0, want_logits=True)
+        for n in range(NEW):
+            if toks[n] != ref[0, n]:
+                top2 = np.sort(lg[0, n])[-2:]
+                assert top2[1] - top2[0] < 0.1, (n, toks, ref[0])
+                break
+    eng = engine(q, model, max_queued_requests=8, max_prefill_requests=3)
+    print(f"automatic prefix plen={plen}", flush=True)
+    ids = [eng.submit_spec(p, NEW, temperature=0.0, repetition_penalty=1.0, register_prefix_tokens=plen,
+                           trust_namespace="tenant-s") for p in prompts]
+    eng.step()  # admits only the builder: the others share its build
+    st = eng.stats()
+    assert st["resident_requests"] == 1 and st["queued_requests"] == 2
+    got = serve(eng, ids)
+    for k, (rid, ref) in enumerate(zip(ids, want)):
+        res, toks = eng.result(rid)
+        assert res.status == q.REQ_STATUS_INV["complete"]
+        np.testing.assert_array_equal(toks, ref)
+        assert got[rid] == toks.tolist()
+        if k == 0:
+            assert res.prefix_written_tokens == plen and res.cached_prefix_tokens == 0
+        else:
+            assert res.cached_prefix_tokens == plen and res.prefill_tokens == prompts[k].size - plen
+    ps = eng.prefix_stats()
+    assert ps["prefix_builds"] == 1 and ps["prefix_hits"] == 2 and ps["prefix_entries"] == 1
+    h, n = eng.find_prefix(prompts[1], "tenant-s")
+    assert n == plen
+    eng.release_prefix(h)
+    with pytest.raises(q.Q35Error):  # automatic builds need a namespace
+        eng.submit_spec(prompts[0], NEW, register_prefix_tokens=plen)
+    eng.close()
+    direct = engine(q, model)
+    with pytest.raises(q.Q35Error):  # and serving mode
+        direct.submit_spec(prompts[0], NEW, register_prefix_tokens=plen, trust_namespace="t")
+    direct.close()

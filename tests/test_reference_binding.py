@@ -3,7 +3,8 @@ compiles against the reference's own public headers
 (include/qwen35x/runtime/cpu_engine.h, options.h) and links against
 libq35hip.so: every CpuEngine method it mirrors is called with the
 reference's request, result, config and stats types. Compile and link only
-(no GPU); skipped where the reference tree or the library is absent."""
+(no GPU); skipped where the reference tree or the library is absent. The
+binding runs in tests/test_gpu_reference_binding.py."""
 import os
 import shutil
 import subprocess
@@ -48,6 +49,7 @@ int run(const char *artifact) {
   spec.sampling.temperature = 0.0f;
   spec.logits_callback = on_logits;
   spec.sampling_constraint = std::make_shared<Mask>();
+  spec.trust_namespace = "ns";
   auto prefix = engine->register_prefix(std::span<const std::int32_t>(spec.prompt_tokens), "ns", error);
   const CpuRequestId id = engine->submit(spec, error, prefix);
   bool progressed = false;
@@ -57,6 +59,8 @@ int run(const char *artifact) {
   engine->advance_batch(std::span<const CpuRequestId>(ids), error);
   CpuRequestResult result;
   engine->result(id, result);
+  std::vector<std::int32_t> read;
+  engine->read_output(id, 4, read, error);
   const CpuEngineStats stats = engine->stats();
   auto found = engine->find_prefix(std::span<const std::int32_t>(spec.prompt_tokens), "ns");
   engine->cancel(id);
