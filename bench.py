@@ -34,6 +34,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POP/s
 METRIC = "decode tokens/s at B=16 (0.8B random-init, 1 GPU); Q4 GEMV % peak HBM BW"
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
@@ -46,6 +47,19 @@ CONFIG_08B = {
         "vocab_size": 248320, "max_position_embeddings": 32768, "rms_norm_eps": 1e-06,
         "tie_word_embeddings": True, "full_attention_interval": 4, "linear_conv_kernel_dim": 4,
         "linear_num_key_heads": 16, "linear_num_value_heads": 16, "linear_key_head_dim": 128,
+        "linear_value_head_dim": 128,
+        "rope_parameters": {"rope_theta": 10000000.0, "partial_rotary_factor": 0.25}}}
+
+
+# the 4B text config (text_architecture qwen35_4b, profile_loader.cpp:439-462)
+CONFIG_4B = {
+    "_name_or_path": "Qwen/Qwen3.5-4B", "model_type": "qwen3_5",
+    "text_config": {
+        "model_type": "qwen3_5_text", "num_hidden_layers": 32, "hidden_size": 2560,
+        "intermediate_size": 9216, "num_attention_heads": 16, "num_key_value_heads": 4, "head_dim": 256,
+        "vocab_size": 248320, "max_position_embeddings": 32768, "rms_norm_eps": 1e-06,
+        "tie_word_embeddings": True, "full_attention_interval": 4, "linear_conv_kernel_dim": 4,
+        "linear_num_key_heads": 16, "linear_num_value_heads": 32, "linear_key_head_dim": 128,
         "linear_value_head_dim": 128,
         "rope_parameters": {"rope_theta": 10000000.0, "partial_rotary_factor": 0.25}}}
 
@@ -150,6 +164,118 @@ def cpu_baseline(model_dir, artifact, batch, prompt_len, new_tokens, threads):
                       f"Q8_0Backend::auto_select -> {isa}, one thread per physical core of the box's CPU share"}
 
 
+def projection_weights(d, sched):
+    """Q4 weights of every layer's projections (not the head)."""
+    H, I, hd = d.hidden, d.intermediate, d.head_dim
+    q_dim, v_dim = d.lin_k_heads * d.lin_k_dim, d.lin_v_heads * d.lin_v_dim
+    total = 0
+    for linear in sched:
+        if linear:
+            total += (2 * q_dim + 2 * v_dim + 2 * d.lin_v_heads) * H + H * v_dim
+        else:
+            total += (2 * d.n_heads * hd + 2 * d.n_kv_heads * hd) * H + H * d.n_heads * hd
+        total += 2 * I * H + H * I
+    return total
+
+
+def mfma_roofline(name, stats, ops, kernel):
+    """Achieved int8 MFMA rate of one kernel class: algorithmic ops (2 per
+    weight per token) over the class's event-timed duration."""
+    ms, launches, _ = stats
+    if launches == 0 or ms <= 0:
+        return None
+    achieved = ops / (ms / 1000.0) / 1e12
+    return {"bound": "mfma", "achieved": round(achieved, 1), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
+            "frac": round(achieved / INT8_PEAK_TOPS, 4), "traffic": None, "kernel_class": name,
+            "launches": launches, "avg_us": round(ms / launches * 1000.0, 2),
+            "algorithmic_ops_per_step": int(ops), "kernel": kernel}
+
+
+def cpu_baseline_mixed(d, sched, model_dir, artifact, rows, ctx_lens, prefill_len, chunk, threads):
+    """Config 5 on the reference (oracle/_ref, built from its sources), which
+    cannot mix decode rows and a prompt chunk (cpu_engine_scheduler.inl:64-80):
+    its packed-step equivalent is one 64-row advance_batch plus the prefill of
+    one chunk. Measured pieces, summed:
+    - the 64-row advance_batch of the reference engine, timed at 16-token
+      contexts (prefilling 64 prompts of ~4k tokens on the CPU takes far
+      longer than the bench allows);
+    - the reference attention kernel (causal_attention_decode_gqa_pairs under
+      CpuExecutor, requests x query-head pairs) over the config's own 64
+      contexts, once per full-attention layer: the part the short contexts
+      leave out;
+    - the reference engine's advance() prefill of the 4096-token prompt with
+      prefill_chunk_size = chunk, per `chunk` tokens.
+    All on `threads` pinned cores."""
+    from oracle import q35_oracle as orc  # the checker build, timed as the baseline only
+
+    if not orc.ref_available():
+        log("oracle/_ref not built: no config-5 CPU baseline")
+        return None
+    r = orc.ref()
+    with open(os.path.join(model_dir, "config.json"), "w") as f:
+        json.dump(CONFIG_4B, f)
+    cpus, cpu_model, allowed, physical = host_cpus(threads)
+    threads = len(cpus)
+    before = os.sched_getaffinity(0)
+    os.sched_setaffinity(0, cpus)
+    isa = r.ref_backend_name(r.ref_backend_resolve(0)).decode()
+    rng = np.random.default_rng(4243)
+    short = 16
+    dprompts = rng.integers(0, d.vocab, size=(rows, short)).astype(np.int32)
+    prompt = rng.integers(0, d.vocab, size=prefill_len).astype(np.int32)
+    dms, pms, calls = ctypes.c_double(), ctypes.c_double(), ctypes.c_size_t()
+    err = ctypes.create_string_buffer(512)
+    t = time.time()
+    try:
+        rc = r.ref_engine_mixed(os.fsencode(model_dir), os.fsencode(artifact), threads, dprompts.ctypes.data, short,
+                                rows, prompt.ctypes.data, prefill_len, chunk, ctypes.byref(dms), ctypes.byref(pms),
+                                ctypes.byref(calls), err, 512)
+        if rc != 0:
+            log(f"reference engine failed: {err.value.decode(errors='replace')}")
+            return None
+        # the attention over the config's contexts, every full layer
+        heads, kvh, hd = d.n_heads, d.n_kv_heads, d.head_dim
+        lens = ctx_lens.astype(np.int32)
+        total = int(lens.sum())
+        kv = rng.standard_normal((2, total, kvh * hd)).astype(np.float16).view(np.uint16)
+        kptr = (ctypes.c_void_p * total)(*[kv[0, i].ctypes.data for i in range(total)])
+        vptr = (ctypes.c_void_p * total)(*[kv[1, i].ctypes.data for i in range(total)])
+        offs = np.concatenate([[0], np.cumsum(lens)[:-1]])
+        krow = (ctypes.c_void_p * rows)(*[ctypes.addressof(kptr) + int(o) * 8 for o in offs])
+        vrow = (ctypes.c_void_p * rows)(*[ctypes.addressof(vptr) + int(o) * 8 for o in offs])
+        qv = rng.standard_normal((rows, heads * hd)).astype(np.float32)
+        gates = rng.standard_normal((rows, heads * hd)).astype(np.float32)
+        out = np.empty((rows, heads * hd), np.float32)
+        stride = int(lens.max())
+        scores = np.empty(rows * (heads // 2) * stride * heads, np.float32)
+        ex = r.ref_executor_create(threads)
+        full_layers = int(sum(1 for x in sched if not x))
+        t0 = time.perf_counter()
+        for _ in range(full_layers):
+            r.ref_par_attention(ex, qv.ctypes.data, gates.ctypes.data, ctypes.addressof(krow), ctypes.addressof(vrow),
+                                lens.ctypes.data, scores.ctypes.data, out.ctypes.data, rows, stride, heads, kvh, hd,
+                                1.0 / np.sqrt(hd), 0)
+        attn_ms = (time.perf_counter() - t0) * 1000
+        r.ref_executor_destroy(ex)
+    finally:
+        os.sched_setaffinity(0, before)
+    step_ms = dms.value + attn_ms + pms.value * chunk / prefill_len
+    value = (rows + chunk) / step_ms * 1000.0
+    log(f"reference CPU config 5: {rows}-row advance_batch {dms.value:.1f} ms (16-token contexts) + attention over "
+        f"the config's contexts {attn_ms:.1f} ms ({full_layers} layers) + {prefill_len}-token prefill "
+        f"{pms.value:.0f} ms in {calls.value} advance() calls -> {step_ms:.1f} ms per {rows} + {chunk} tokens, "
+        f"{value:.1f} tok/s on {threads} threads ({cpu_model}, {isa}) ({time.time() - t:.1f}s wall)")
+    return {"value": round(value, 2), "unit": "tokens/s", "cores": threads, "kind": "reference",
+            "cpu_model": cpu_model, "isa": isa, "threads": threads, "pinned_cpus": cpus,
+            "decode_step_ms": round(dms.value, 2), "attention_ms": round(attn_ms, 2),
+            "prefill_ms": round(pms.value, 1), "prefill_advance_calls": int(calls.value),
+            "sample": f"reference engine: one {rows}-row advance_batch (max_decode_batch_size {rows}) at 16-token "
+                      f"contexts, plus the reference attention kernel over the config's {rows} contexts (sum "
+                      f"{total}) for each of {full_layers} full layers, plus the advance() prefill of a "
+                      f"{prefill_len}-token prompt with prefill_chunk_size {chunk}, counted per {chunk} tokens; "
+                      f"value = ({rows} + {chunk}) tokens / that sum"}
+
+
 def run_mixed4b(args, q, ctx):
     """Config 5: the 4B-shaped model (hidden 2560, 32 layers 3:1, MLP 9216,
     random-init Q4) with 64 decode requests at contexts ~U[128, 8192] and one
@@ -158,9 +284,10 @@ def run_mixed4b(args, q, ctx):
     prompt positions per step). Measured beside it, the reference's
     alternating schedule (cpu_engine_scheduler.inl:64-80: a 64-row decode step,
     captured graph, then the prompt chunk on its own) and the prompt's chunked
-    prefill alone. Decode cost does not depend on KV values, so the 64 rows'
-    pages are allocated to their context lengths without running their
-    prompts."""
+    prefill alone. Every shape the timed region uses runs once untimed first
+    (graph capture and instantiation stay out of the timings). Decode cost does
+    not depend on KV values, so the 64 rows' pages are allocated to their
+    context lengths without running their prompts."""
     d, sched = q.model_dims(2)
     path = os.path.join(tempfile.gettempdir(), f"q35_bench_4b_s{args.seed}")
     os.makedirs(path, exist_ok=True)
@@ -179,9 +306,11 @@ def run_mixed4b(args, q, ctx):
     rng = np.random.default_rng(20261205)
     ctx_lens = rng.integers(128, 8193, size=rows)
     steps = max(1, min(args.steps, 40))
-    advance = args.warmup + steps + n_chunks  # decode positions written per row
+    # decode positions written per row: warm-up and timed decode steps, two
+    # rounds of packed steps (untimed, timed), the profiled steps
+    advance = args.warmup + steps + 2 * n_chunks + 3
     max_ctx = 8192 + advance + 8
-    rt = q.Runtime(model, max_slots=rows + 2, max_batch=rows, max_context=max_ctx, page_tokens=page_tokens,
+    rt = q.Runtime(model, max_slots=rows + 4, max_batch=rows, max_context=max_ctx, page_tokens=page_tokens,
                    use_graphs=args.graphs == "on", max_step_rows=rows + chunk)
     slots = np.array([rt.slot_alloc(np.array([1], np.int32)) for _ in range(rows)], np.int32)
     table = np.zeros((rows, rt.max_pages), np.int32)
@@ -206,51 +335,98 @@ def run_mixed4b(args, q, ctx):
     log(f"4B decode: {rows} rows, contexts {int(ctx_lens.min())}..{int(ctx_lens.max())} "
         f"(sum {int(ctx_lens.sum())}): {decode_ms:.3f} ms/step")
 
-    def new_prompt():
-        prompt = rng.integers(0, d.vocab, size=prefill_len).astype(np.int32)
+    prompt = rng.integers(0, d.vocab, size=prefill_len).astype(np.int32)
+
+    def prompt_slot():
         pslot = rt.slot_alloc(prompt)
         ptable = np.zeros(rt.max_pages, np.int32)
         for p in range(prefill_len // page_tokens + 1):
             ptable[p] = rt.page_alloc()
-        return prompt, pslot, ptable
+        return pslot, ptable
 
-    # the prompt alone, in chunks (the alternating schedule's prefill steps)
-    prompt, pslot, ptable = new_prompt()
-    ctx.synchronize()
-    t0 = time.perf_counter()
-    first_alone = None
-    for c0 in range(0, prefill_len, chunk):
-        first_alone = rt.prefill(pslot, c0, prompt[c0:c0 + chunk], ptable)
-    prefill_ms = (time.perf_counter() - t0) * 1000
+    def release(pslot, ptable):
+        rt.slot_free(pslot)
+        for p in range(prefill_len // page_tokens + 1):
+            rt.page_release(int(ptable[p]))
+
+    def prefill_alone():
+        """The prompt alone, in chunks (the alternating schedule's prefill steps)."""
+        pslot, ptable = prompt_slot()
+        ctx.synchronize()
+        t0 = time.perf_counter()
+        first = None
+        for c0 in range(0, prefill_len, chunk):
+            first = rt.prefill(pslot, c0, prompt[c0:c0 + chunk], ptable)
+        ms = (time.perf_counter() - t0) * 1000
+        release(pslot, ptable)
+        return ms, first
+
+    def packed(n=n_chunks):
+        """The prompt packed with the 64 decode rows, one step per chunk."""
+        nonlocal tokens
+        pslot, ptable = prompt_slot()
+        ctx.synchronize()
+        t0 = time.perf_counter()
+        first = None
+        for c0 in range(0, n * chunk, chunk):
+            last = c0 + chunk >= prefill_len
+            segs = [dict(slot=int(slots[r]), pos0=int(pos[r]), tokens=tokens[r:r + 1], page_table=table[r],
+                         count_input=1) for r in range(rows)]
+            segs.append(dict(slot=pslot, pos0=c0, tokens=prompt[c0:c0 + chunk], page_table=ptable,
+                             want_token=int(last)))
+            out = rt.step_segments(segs)
+            tokens = out[:rows].astype(np.int32)
+            pos[:] += 1
+            if last:
+                first = int(out[rows])
+        ms = (time.perf_counter() - t0) * 1000 / n
+        release(pslot, ptable)
+        return ms, first
+
+    prefill_alone()  # untimed: every prefill chunk shape
+    packed()         # untimed: every packed step shape
+    prefill_ms, first_alone = prefill_alone()
     log(f"4B chunked prefill: {prefill_len} tokens in {n_chunks} chunks of {chunk}: {prefill_ms:.1f} ms "
         f"({prefill_len / prefill_ms * 1000:.0f} tok/s), first token {first_alone}")
-    rt.slot_free(pslot)
-    # the same prompt packed with the 64 decode rows, one step per chunk
-    pslot = rt.slot_alloc(prompt)
-    ctx.synchronize()
-    t0 = time.perf_counter()
-    first_packed = None
-    for c0 in range(0, prefill_len, chunk):
-        last = c0 + chunk >= prefill_len
-        segs = [dict(slot=int(slots[r]), pos0=int(pos[r]), tokens=tokens[r:r + 1], page_table=table[r], count_input=1)
-                for r in range(rows)]
-        segs.append(dict(slot=pslot, pos0=c0, tokens=prompt[c0:c0 + chunk], page_table=ptable, want_token=int(last)))
-        out = rt.step_segments(segs)
-        tokens = out[:rows].astype(np.int32)
-        pos += 1
-        if last:
-            first_packed = int(out[rows])
-    packed_ms = (time.perf_counter() - t0) * 1000 / n_chunks
+    packed_ms, first_packed = packed()
     assert first_packed == first_alone, (first_packed, first_alone)
     alternating_ms = decode_ms + prefill_ms / n_chunks
     log(f"4B packed step: {rows} decode rows + {chunk} prompt positions: {packed_ms:.2f} ms/step; alternating "
         f"(decode step + prompt chunk): {alternating_ms:.2f} ms; same first token {first_packed}")
+    # rooflines: the decode attention (HBM) in a 64-row decode step, the dense
+    # GEMM (int8 MFMA) in a packed step; eager launches with HIP events
+    rt.set_profiling(True)
+    rt.profile_reset()
+    for _ in range(2):
+        tokens = rt.step(slots, pos, tokens, table, count_input=ones)
+        pos += 1
+    prof_dec = rt.profile()
+    rt.profile_reset()
+    packed(1)
+    prof_pack = rt.profile()
+    rt.set_profiling(False)
+    attn_roof = roofline("attention", prof_dec["attention"], None,
+                         "attention_kernel<4> (decode rows: one workgroup per (64-token chunk, KV head, row), fp16 "
+                         "MFMA scores and P*V over paged K/V)")
+    ops = 2.0 * (rows + chunk) * projection_weights(d, sched)
+    gemm_roof = mfma_roofline("gemm", prof_pack["gemm"], ops,
+                              "gemm_dense_kernel<NT, true> (every projection of a packed step of "
+                              f"{rows} + {chunk} rows: int8 MFMA over Q4 DOT4 tiles, fp32 block chain)")
+    for name, roof in (("decode attention", attn_roof), ("packed dense GEMM", gemm_roof)):
+        if roof:
+            log(f"4B {name}: {roof['achieved']} {roof['unit']} = {roof['frac']:.3f} of peak "
+                f"({roof['launches']} launches, {roof['avg_us']} us avg)")
     rt.close()
     model.close()
-    return {
+    base = None
+    if args.cpu_baseline == "on":
+        threads = args.cpu_threads or min(16, host_cpus(1 << 20)[3] or 1)
+        base = cpu_baseline_mixed(d, sched, path, art, rows, ctx_lens, prefill_len, chunk, threads)
+    value = (rows + chunk) / packed_ms * 1000
+    line = {
         "metric": "config 5 packed step: 4B-shaped, 64 decode rows (ctx ~U[128,8192]) + a chunk of a 4096-token "
                   "prompt per step",
-        "value": round((rows + chunk) / packed_ms * 1000, 1), "unit": "tokens/s", "n_gpus": 1,
+        "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": steps, "warmup": args.warmup, "ms_per_step": round(packed_ms, 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "q4xi8->i32 (projections), f32 (DeltaNet, attention)",
         "data": "synthetic: random-init 4B-shaped weights N(0,0.02) packed to Q4-G32-DOT4 H128, random tokens",
@@ -259,8 +435,11 @@ def run_mixed4b(args, q, ctx):
                    "prefill_chunk": chunk, "packed_ms_per_step": round(packed_ms, 3),
                    "alternating_ms_per_step": round(alternating_ms, 3), "decode_ms": round(decode_ms, 3),
                    "prefill_alone_ms": round(prefill_ms, 2)},
-        "roofline": None, "cpu_baseline": None,
+        "roofline": gemm_roof, "decode_attention_roofline": attn_roof, "cpu_baseline": base,
     }
+    if base:
+        line["speedup_vs_cpu_baseline"] = round(value / base["value"], 1)
+    return line
 
 
 def run_prefix0p8b(args, q, ctx):
@@ -325,7 +504,9 @@ def run_kernels(args, q, ctx):
     (median of HIP-event brackets around single calls, so a figure is the
     call's kernels plus their launch gaps; pure kernel durations come from
     rocprofv3). Beside each, the reference's own kernel (oracle/_ref, one host
-    thread) on the same inputs. Algorithmic bytes as in the reference's
+    thread, and on all physical cores under the reference's CpuExecutor, the
+    way its engine partitions the work) on the same inputs. Algorithmic bytes
+    as in the reference's
     q4_dot4 / delta_net / full_attention tests' shapes:
       config 1: W 3584 x 1024 DOT4 (2,064,384 B), 512 distinct copies rotated,
                 X1 (B=1) and X4 (B=16) activations, fp32 outputs;
@@ -353,6 +534,21 @@ def run_kernels(args, q, ctx):
         return (time.perf_counter() - t) / reps * 1e6
 
     ref = orc.ref() if orc.ref_available() else None
+    threads = args.cpu_threads or min(16, host_cpus(1 << 20)[3] or 1)
+    cpus, cpu_model, _, _ = host_cpus(threads)
+    exe = ref.ref_executor_create(len(cpus)) if ref is not None else None
+    before = os.sched_getaffinity(0)
+
+    def cpu_all_us(call, reps):
+        """`call` on the pinned cores (the executor's workers inherit the
+        process's affinity); one untimed call first."""
+        os.sched_setaffinity(0, cpus)
+        try:
+            call(0)
+            return cpu_us(call, reps)
+        finally:
+            os.sched_setaffinity(0, before)
+
     # ---- config 1
     rows, cols, copies = 3584, 1024, 512
     nb = cols // 32
@@ -387,6 +583,10 @@ def run_kernels(args, q, ctx):
                 c_us = cpu_us(lambda i: ref.ref_q4_dot4_matmul(packed.ctypes.data, act.ctypes.data, ho.ctypes.data,
                                                                rows, B, nb, rows, 0), 100)
             entry["cpu_us_per_call_1thread"] = round(c_us, 1)
+            # all cores: 8-row DOT4 tiles under CpuExecutor
+            entry["cpu_us_per_call_all_cores"] = round(cpu_all_us(
+                lambda i: ref.ref_par_q4_dot4(exe, packed.ctypes.data, act.ctypes.data, ho.ctypes.data, rows, B, nb,
+                                              0), 400), 1)
         res[f"config1_B{B}"] = entry
         log(f"config 1 B={B}: {entry}")
     dw.free()
@@ -418,6 +618,10 @@ def run_kernels(args, q, ctx):
                                                     vv[b].ctypes.data, al[b].ctypes.data, be[b].ctypes.data,
                                                     ho[b].ctypes.data, H, D, D, 0, H * D, 0)
         entry["cpu_us_per_step_1thread"] = round(cpu_us(one, 5), 1)
+        sp = (ctypes.c_void_p * B)(*[hs[b].ctypes.data for b in range(B)])
+        entry["cpu_us_per_step_all_cores"] = round(cpu_all_us(
+            lambda i: ref.ref_par_delta(exe, ctypes.addressof(sp), qq.ctypes.data, kk.ctypes.data, vv.ctypes.data,
+                                        al.ctypes.data, be.ctypes.data, ho.ctypes.data, B, H, D, D, 0), 20), 1)
     res["config2_B16"] = entry
     log(f"config 2: {entry}")
     # ---- config 3
@@ -459,7 +663,19 @@ def run_kernels(args, q, ctx):
                                                           heads * hd, kvh * hd, int(lens[b]), heads, kvh, hd,
                                                           1.0 / 16.0, 0, heads // 2, 0)
         entry["cpu_us_per_call_1thread"] = round(cpu_us(one, 3), 1)
+        krow = (ctypes.c_void_p * 16)(*[ctypes.addressof(k) for k in krows])
+        vrow = (ctypes.c_void_p * 16)(*[ctypes.addressof(v) for v in vrows])
+        pscores = np.empty(16 * (heads // 2) * int(lens.max()) * heads, np.float32)
+        entry["cpu_us_per_call_all_cores"] = round(cpu_all_us(
+            lambda i: ref.ref_par_attention(exe, qv.ctypes.data, gates.ctypes.data, ctypes.addressof(krow),
+                                            ctypes.addressof(vrow), lens.ctypes.data, pscores.ctypes.data,
+                                            ho.ctypes.data, 16, int(lens.max()), heads, kvh, hd, 1.0 / 16.0, 0),
+            10), 1)
     res["config3_B16"] = entry
+    if exe is not None:
+        ref.ref_executor_destroy(exe)
+        res["cpu"] = {"threads_all_cores": len(cpus), "pinned_cpus": cpus, "cpu_model": cpu_model,
+                      "isa": ref.ref_backend_name(ref.ref_backend_resolve(0)).decode()}
     log(f"config 3: {entry}")
     return {
         "metric": "kernel-level configs 1-3: per-call GPU latency and algorithmic HBM GB/s (1 GPU)",
@@ -482,11 +698,17 @@ def roofline(name, stats, traffic, kernel=None):
     per_launch_s = ms / launches / 1000.0
     achieved = per_launch_bytes / per_launch_s / 1e9
     t = traffic.get(name) if traffic else None
+    measured = t.get("bytes_per_launch") if isinstance(t, dict) else None
     out = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-           "frac": round(achieved / HBM_PEAK_GBS, 4),
-           "traffic": t.get("bytes_per_launch") if isinstance(t, dict) else None,
+           "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured,
            "kernel_class": name, "launches": launches, "avg_us": round(ms / launches * 1000.0, 2),
            "algorithmic_bytes_per_launch": round(per_launch_bytes)}
+    if measured:
+        # HBM bytes the rocprofv3 PMC passes measured per launch of this class
+        # (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel of known size)
+        # over the algorithmic bytes: above 1 is split partials and re-reads
+        out["traffic_vs_algorithmic"] = round(measured / per_launch_bytes, 3)
+        out["traffic_source"] = "profiles/traffic.json (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of this build)"
     if kernel:
         out["kernel"] = kernel
     return out

@@ -531,6 +531,15 @@ def ref():
                                           c_size_t]),
             "ref_engine_greedy": (c_int, [ctypes.c_char_p, ctypes.c_char_p, c_int, c_int, P, c_size_t, c_size_t, c_size_t,
                                           c_float, P, P, P, P, P, ctypes.c_char_p, c_size_t]),
+            "ref_executor_create": (P, [c_size_t]),
+            "ref_executor_destroy": (None, [P]),
+            "ref_executor_threads": (c_size_t, [P]),
+            "ref_par_q4_dot4": (c_int, [P, P, P, P, c_size_t, c_size_t, c_size_t, c_int]),
+            "ref_par_delta": (c_int, [P, P, P, P, P, P, P, P, c_size_t, c_size_t, c_size_t, c_size_t, c_int]),
+            "ref_par_attention": (c_int, [P, P, P, P, P, P, P, P, c_size_t, c_size_t, c_int, c_int, c_int, c_float,
+                                          c_int]),
+            "ref_engine_mixed": (c_int, [ctypes.c_char_p, ctypes.c_char_p, c_int, P, c_size_t, c_size_t, P, c_size_t,
+                                         c_size_t, P, P, P, ctypes.c_char_p, c_size_t]),
         }
         for name, (res, args) in sigs.items():
             f = getattr(r, name)

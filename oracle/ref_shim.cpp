@@ -9,6 +9,7 @@
 // (include/qwen35x/cpu/q8_0.h:23-31), 0 = auto_select.
 #include "qwen35x/cpu/activation.h"
 #include "qwen35x/cpu/delta_net.h"
+#include "qwen35x/cpu/executor.h"
 #include "qwen35x/cpu/full_attention.h"
 #include "qwen35x/cpu/q4_0.h"
 #include "qwen35x/cpu/q4_dot4.h"
@@ -21,6 +22,7 @@
 
 #include <chrono>
 #include <cstdint>
+#include <system_error>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -375,6 +377,171 @@ int ref_engine_sample(const char *model_dir, const char *artifact, int threads, 
   if (state.status != CpuRequestStatus::complete || state.output_tokens.size() != new_tokens)
     return fail("incomplete sampled output: " + state.error);
   std::memcpy(out_tokens, state.output_tokens.data(), new_tokens * sizeof(std::int32_t));
+  return 0;
+}
+
+// ---- configs 1-3 on all cores: the reference's kernels under its own
+// CpuExecutor (executor.h:40-77), partitioned as the engine partitions them:
+// 8-row DOT4 tiles for the projections (matmul_2d_quantized_batch,
+// weights.inl:1297-1502), requests for the DeltaNet update (state_batch,
+// cpu_engine_state_batch.inl), requests x query-head pairs for attention.
+void *ref_executor_create(std::size_t threads) {
+  CpuExecutorConfig c;
+  c.thread_count = threads;
+  c.min_parallel_rows = 1;
+  std::error_code ec;
+  auto e = CpuExecutor::create(c, ec);
+  return ec ? nullptr : e.release();
+}
+void ref_executor_destroy(void *e) { delete static_cast<CpuExecutor *>(e); }
+std::size_t ref_executor_threads(void *e) { return static_cast<CpuExecutor *>(e)->thread_count(); }
+
+// q4_dot4_matvec (count 1, X1 vector) or q4_dot4_matmul (X4 vectors,
+// token-major output of stride `rows`) over the tiles of `rows` rows.
+int ref_par_q4_dot4(void *exec, const void *m, const void *v, float *out, std::size_t rows, std::size_t count,
+                    std::size_t blocks, int b) {
+  struct Job {
+    const Q4_0BlockX8 *m;
+    const void *v;
+    float *out;
+    std::size_t rows, count, blocks;
+    Q8_0Backend b;
+  } job{static_cast<const Q4_0BlockX8 *>(m), v, out, rows, count, blocks, be(b)};
+  auto task = [](void *ctx, std::size_t t0, std::size_t t1) noexcept {
+    const auto &j = *static_cast<const Job *>(ctx);
+    const Q4_0BlockX8 *tile = j.m + t0 * j.blocks;
+    if (j.count == 1)
+      q4_dot4_matvec(tile, static_cast<const Q8_0BlockX1 *>(j.v), j.out + 8 * t0, 8 * (t1 - t0), j.blocks, j.b);
+    else
+      q4_dot4_matmul(tile, static_cast<const Q8_0BlockX4 *>(j.v), j.out + 8 * t0, 8 * (t1 - t0), j.count, j.blocks,
+                     j.rows, j.b);
+  };
+  return static_cast<CpuExecutor *>(exec)->parallel_for_rows(rows / 8, task, &job) == CpuExecutorStatus::ok ? 0 : 1;
+}
+
+// gated_delta_net_update_rows over every value row of each request; the
+// request's state is states[r], its q/k [heads][kdim], v/out [heads][vdim],
+// alpha/beta [heads] at offset r.
+int ref_par_delta(void *exec, float *const *states, const float *q, const float *k, const float *v,
+                  const float *alpha, const float *beta, float *out, std::size_t batch, std::size_t heads,
+                  std::size_t kdim, std::size_t vdim, int b) {
+  struct Job {
+    float *const *states;
+    const float *q, *k, *v, *alpha, *beta;
+    float *out;
+    std::size_t heads, kdim, vdim;
+    Q8_0Backend b;
+  } job{states, q, k, v, alpha, beta, out, heads, kdim, vdim, be(b)};
+  auto task = [](void *ctx, std::size_t r0, std::size_t r1) noexcept {
+    const auto &j = *static_cast<const Job *>(ctx);
+    for (std::size_t r = r0; r < r1; ++r)
+      gated_delta_net_update_rows(j.states[r], j.q + r * j.heads * j.kdim, j.k + r * j.heads * j.kdim,
+                                  j.v + r * j.heads * j.vdim, j.alpha + r * j.heads, j.beta + r * j.heads,
+                                  j.out + r * j.heads * j.vdim, j.heads, j.kdim, j.vdim, 0, j.heads * j.vdim, j.b);
+  };
+  return static_cast<CpuExecutor *>(exec)->parallel_for_rows(batch, task, &job) == CpuExecutorStatus::ok ? 0 : 1;
+}
+
+// causal_attention_decode_gqa_pairs per (request, query-head pair): request
+// r's q/gates/out rows at r * heads * head_dim, its K/V row pointers
+// key_rows[r] / value_rows[r], context lens[r]; scores is
+// [batch * pairs][context_stride * heads] (one private buffer per item).
+int ref_par_attention(void *exec, const float *q, const float *gates, const std::uint16_t *const *const *key_rows,
+                      const std::uint16_t *const *const *value_rows, const int *lens, float *scores, float *out,
+                      std::size_t batch, std::size_t context_stride, int heads, int kv_heads, int head_dim,
+                      float scale, int b) {
+  struct Job {
+    const float *q, *gates;
+    const std::uint16_t *const *const *keys, *const *const *values;
+    const int *lens;
+    float *scores, *out;
+    std::size_t stride, pairs;
+    int heads, kv_heads, head_dim;
+    float scale;
+    Q8_0Backend b;
+  } job{q, gates, key_rows, value_rows, lens, scores, out, context_stride, static_cast<std::size_t>(heads) / 2,
+        heads, kv_heads, head_dim, scale, be(b)};
+  auto task = [](void *ctx, std::size_t i0, std::size_t i1) noexcept {
+    const auto &j = *static_cast<const Job *>(ctx);
+    const std::size_t width = static_cast<std::size_t>(j.heads) * j.head_dim;
+    for (std::size_t i = i0; i < i1; ++i) {
+      const std::size_t r = i / j.pairs, p = i % j.pairs;
+      const AttentionKvRows pages{j.keys[r], j.values[r]};
+      causal_attention_decode_gqa_pairs(j.q + r * width, j.gates + r * width, nullptr, nullptr, nullptr, nullptr,
+                                        j.scores + i * j.stride * j.heads, j.out + r * width, j.stride, width,
+                                        static_cast<std::size_t>(j.kv_heads) * j.head_dim, j.lens[r], j.heads,
+                                        j.kv_heads, j.head_dim, j.scale, p, p + 1, j.b, &pages);
+    }
+  };
+  return static_cast<CpuExecutor *>(exec)->parallel_for_rows(batch * job.pairs, task, &job) == CpuExecutorStatus::ok
+             ? 0 : 1;
+}
+
+// Config 5 on the reference engine, which cannot put decode rows and a
+// prompt chunk in one step (cpu_engine_scheduler.inl:64-80): `rows` requests
+// with decode_len-token prompts are prefilled (untimed); one advance_batch of
+// all of them is timed (max_decode_batch_size = rows); then a
+// prefill_len-token prompt is prefilled through advance() with
+// prefill_chunk_size = chunk, timed, calls counted. Greedy, no penalty.
+int ref_engine_mixed(const char *model_dir, const char *artifact, int threads, const std::int32_t *decode_prompts,
+                     std::size_t decode_len, std::size_t rows, const std::int32_t *prompt, std::size_t prefill_len,
+                     std::size_t chunk, double *decode_ms, double *prefill_ms, std::size_t *prefill_calls,
+                     char *error, std::size_t error_size) {
+  std::string err;
+  auto fail = [&](const std::string &message) {
+    if (error && error_size) {
+      std::strncpy(error, message.c_str(), error_size - 1);
+      error[error_size - 1] = 0;
+    }
+    return 1;
+  };
+  auto profile = ProfileLoader::load_from_hf_directory(model_dir, err);
+  if (!profile) return fail(err);
+  CpuLoadOptions options;
+  options.model_dir = model_dir;
+  options.cpu_q4_h128_path = artifact;
+  auto model = CpuModel::load(*profile, options, err);
+  if (!model) return fail(err);
+  CpuEngineConfig config;
+  config.threads = threads;
+  config.max_resident_requests = rows + 1;
+  config.max_decode_batch_size = rows;
+  config.prefill_chunk_size = chunk;
+  config.max_context = std::max(decode_len, prefill_len) + 8;
+  auto engine = CpuEngine::create(model, config, err);
+  if (!engine) return fail(err);
+  auto submit = [&](const std::int32_t *tokens, std::size_t n, std::size_t new_tokens) -> CpuRequestId {
+    CpuRequestSpec spec;
+    spec.prompt_tokens.assign(tokens, tokens + n);
+    spec.max_new_tokens = new_tokens;
+    spec.sampling.temperature = 0.0F;
+    spec.sampling.repetition_penalty = 1.0F;
+    return engine->submit(std::move(spec), err);
+  };
+  std::vector<CpuRequestId> ids;
+  for (std::size_t r = 0; r < rows; ++r) {
+    const auto id = submit(decode_prompts + r * decode_len, decode_len, 2);
+    if (!id) return fail(err);
+    CpuRequestResult state;
+    do {
+      if (!engine->advance(id, err) || !engine->result(id, state)) return fail(err);
+    } while (state.status == CpuRequestStatus::prefill);
+    ids.push_back(id);
+  }
+  auto t0 = std::chrono::steady_clock::now();
+  if (!engine->advance_batch(ids, err)) return fail(err);
+  *decode_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+  const auto id = submit(prompt, prefill_len, 1);
+  if (!id) return fail(err);
+  std::size_t calls = 0;
+  CpuRequestResult state;
+  t0 = std::chrono::steady_clock::now();
+  do {
+    if (!engine->advance(id, err) || !engine->result(id, state)) return fail(err);
+    ++calls;
+  } while (state.status == CpuRequestStatus::prefill);
+  *prefill_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+  *prefill_calls = calls;
   return 0;
 }
 

@@ -860,10 +860,12 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
     }
     return e;
   };
-  // bytes: residual row in (+ split partial rows and the new residual out),
-  // codes and scales out
+  // Algorithmic bytes count each projection output row once (a split
+  // GEMM's partial rows are traffic, not algorithm: the measured HBM bytes
+  // show them). rms_prep: residual row in (+ the projection row and the new
+  // residual out), codes and scales out.
   auto rms_bytes = [&](bool add) {
-    return B * (H * 4.0 + (add ? pending.splits * H * 4.0 + H * 4.0 : 0.0) + H + H / 32.0 * 4.0) + H * 4.0;
+    return B * (H * 4.0 + (add ? H * 4.0 + H * 4.0 : 0.0) + H + H / 32.0 * 4.0) + H * 4.0;
   };
   // Steps of one token tile fold the residual + RMSNorm preparations into
   // the projections (fused.hip): the in / qkv and gate_up projections
@@ -914,17 +916,14 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
     groups_ready = true;
     return e;
   };
-  auto norm_bytes = [&](int rows, int max_split) {
-    const GemmPlan p = gemm_plan(rows, H / 32, false, false, ctx->cu_count, 0, 0, max_split);
-    return gemm_algorithmic_bytes(rows, H / 32, batch, true, false) + (p.split - 1) * B * rows * 4.0 + B * H * 4.0 +
-           H * 4.0 + B * (H / 16) * 4.0 - B * (H + 4.0);  // residual rows, group sums and the norm weight in;
-                                                            // no A16 activations read
+  // weights, residual rows, group sums and the norm weight in (no A16
+  // activations read), one output row out
+  auto norm_bytes = [&](int rows) {
+    return gemm_algorithmic_bytes(rows, H / 32, batch, true, false) + B * H * 4.0 + H * 4.0 + B * (H / 16) * 4.0 -
+           B * (H + 4.0);
   };
-  auto gemm_bytes = [&](int rows, int K, int max_split = 32) {
-    if (gemm_dense_fits(rows, batch, ctx->cu_count)) return gemm_algorithmic_bytes(rows, K / 32, batch, true, false);
-    const GemmPlan p = gemm_plan(rows, K / 32, false, false, ctx->cu_count, 0, 0, max_split);
-    return gemm_algorithmic_bytes(rows, K / 32, batch, true, false) + (p.split - 1) * B * rows * 4.0;
-  };
+  // weights, A16 activations in, one output row out
+  auto gemm_bytes = [&](int rows, int K) { return gemm_algorithmic_bytes(rows, K / 32, batch, true, false); };
 
   // Stage trace (test hook, decode steps only): copies of the stage inputs
   // and outputs; the split GEMM outputs are summed in split order into the
@@ -981,7 +980,7 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
     const bool fuse_in = fuse && groups_ready && !add_pending && L.gate_rows == 0 &&
                          gemm_norm_fits(L.in_rows, H / 32, batch, ctx->cu_count, kConsumerSplits);
     if (fuse_in) {
-      Q35_KERNEL(Q35_KERNEL_GEMM, norm_bytes(L.in_rows, kConsumerSplits),
+      Q35_KERNEL(Q35_KERNEL_GEMM, norm_bytes(L.in_rows),
                  gemm_norm(L.in_proj, L.in_rows, L.input_norm, kConsumerSplits, normed_in), "norm + in projection");
     } else {
       Q35_KERNEL(Q35_KERNEL_PREP, rms_bytes(add_pending),
@@ -995,7 +994,7 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
                  "trace");
     }
     if (!fuse_in)
-      Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(L.in_rows, H, kConsumerSplits),
+      Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(L.in_rows, H),
                  gemm(L.in_proj, L.in_rows, H, kConsumerSplits), "in projection");
     if (tracing) Q35_STEP(trace_rows(l, Q35_TRACE_PROJ_IN, L.in_rows), "trace");
     if (L.linear) {
@@ -1017,7 +1016,7 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
       if (chunked && pending.splits > 1) {
         // the chunk scan reads every token's inputs in order: sum the split
         // partials once over the whole GPU, so each token is one load per channel
-        Q35_KERNEL(Q35_KERNEL_PREP, B * L.in_rows * (pending.splits + 1) * 4.0,
+        Q35_KERNEL(Q35_KERNEL_PREP, B * L.in_rows * 2 * 4.0,
                    launch_split_reduce(pending, batch, rt->rows_final, L.in_rows, nullptr, s), "prefill row sum");
         a.proj.p = rt->rows_final;
         a.proj.width = L.in_rows;
@@ -1049,10 +1048,10 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
         a.row_list = attn_rows;
         a.row_count = sh.attn_rows;
       }
-      // recurrent state read + written, projection row in (per split), conv
-      // ring (K-1 rows read, one written), prepared out-projection activations
+      // recurrent state read + written, projection row in, conv ring (K-1
+      // rows read, one written), prepared out-projection activations
       const double delta_bytes =
-          B * (2.0 * d.lin_v_heads * d.lin_v_dim * d.lin_k_dim * 4.0 + pending.splits * L.in_rows * 4.0 +
+          B * (2.0 * d.lin_v_heads * d.lin_v_dim * d.lin_k_dim * 4.0 + L.in_rows * 4.0 +
                static_cast<double>(d.lin_kernel) * ch * 4.0 + v_dim + v_dim / 32.0 * 4.0);
       if (tracing) {
         Q35_STEP(trace_state(l, li, Q35_TRACE_STATE_BEFORE, 0), "trace");
@@ -1088,9 +1087,9 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
       p.v_pool = rt->v_pool + static_cast<size_t>(fi) * rt->layer_pool_elems;
       p.q_out = rt->q_rot;
       p.gate_out = rt->gates;
-      // projection row in (per split); rotated q, gate, and the new K/V rows (FP16) out
+      // projection row in; rotated q, gate, and the new K/V rows (FP16) out
       Q35_KERNEL(Q35_KERNEL_ATTN_PREP,
-                 B * (pending.splits * L.in_rows * 4.0 + 2.0 * d.n_heads * d.head_dim * 4.0 + 2.0 * kvw * 2.0),
+                 B * (L.in_rows * 4.0 + 2.0 * d.n_heads * d.head_dim * 4.0 + 2.0 * kvw * 2.0),
                  launch_attn_prep(p, s), "attention prep");
       if (tracing) {
         const size_t qb = static_cast<size_t>(batch) * d.n_heads * d.head_dim * 4;
@@ -1129,16 +1128,13 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
         a.prompt_rows = chunk_rows;
         a.prompt_row_count = sh.rows - sh.attn_rows;
       }
-      // every cached K and V row of each request once, q in, split partials out
-      const double splits_used = std::ceil(kv_tokens / rt->split_tokens);
-      Q35_KERNEL(Q35_KERNEL_ATTENTION,
-                 kv_tokens * kvw * 2.0 * 2.0 + B * d.n_heads * d.head_dim * 4.0 +
-                     splits_used * d.n_heads * (d.head_dim + 2) * 4.0,
+      // every cached K and V row of each request once, q in, one output row
+      // out (chunk partials are traffic, as the split GEMMs')
+      Q35_KERNEL(Q35_KERNEL_ATTENTION, kv_tokens * kvw * 2.0 * 2.0 + 2.0 * B * d.n_heads * d.head_dim * 4.0,
                  launch_attention(a, s), "attention");
-      // chunk partials and gates in, o projection A16 activations out
+      // the attention row and the gates in, o projection A16 activations out
       Q35_KERNEL(Q35_KERNEL_PREP,
-                 splits_used * d.n_heads * (d.head_dim + 2) * 4.0 + B * d.n_heads * d.head_dim * (4.0 + 1.0) +
-                     B * d.n_heads * d.head_dim / 32.0 * 4.0,
+                 B * d.n_heads * d.head_dim * (4.0 + 4.0 + 1.0) + B * d.n_heads * d.head_dim / 32.0 * 4.0,
                  launch_attention_merge(a, rt->gates, tracing ? trace_fp32(l, Q35_TRACE_CORE, d.n_heads * d.head_dim)
                                                               : nullptr,
                                         rt->codes, rt->scales, d.sign_seed, s),
@@ -1157,7 +1153,7 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
     float *normed_post = tracing ? trace_fp32(l, Q35_TRACE_NORMED_POST, H) : nullptr;
     const bool fuse_post = fuse_out && gemm_norm_fits(2 * I, H / 32, batch, ctx->cu_count, kConsumerSplits);
     if (fuse_post) {
-      Q35_KERNEL(Q35_KERNEL_GEMM, norm_bytes(2 * I, kConsumerSplits),
+      Q35_KERNEL(Q35_KERNEL_GEMM, norm_bytes(2 * I),
                  gemm_norm(L.gate_up, 2 * I, L.post_norm, kConsumerSplits, normed_post), "post norm + gate_up projection");
     } else {
       Q35_KERNEL(Q35_KERNEL_PREP, rms_bytes(!fuse_out), rms_prep(L.post_norm, !fuse_out, true, normed_post),
@@ -1168,7 +1164,7 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
       Q35_STEP(trace_codes(l, Q35_TRACE_CODES_POST, H), "trace");
     }
     if (!fuse_post)
-      Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(2 * I, H, kConsumerSplits), gemm(L.gate_up, 2 * I, H, kConsumerSplits),
+      Q35_KERNEL(Q35_KERNEL_GEMM, gemm_bytes(2 * I, H), gemm(L.gate_up, 2 * I, H, kConsumerSplits),
                  "gate_up projection");
     if (tracing) Q35_STEP(trace_rows(l, Q35_TRACE_GATE_UP, 2 * I), "trace");
     PrepArgs sp;
@@ -1181,7 +1177,7 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
     sp.codes = rt->codes;
     sp.scales = rt->scales;
     if (tracing) sp.y_out = trace_fp32(l, Q35_TRACE_SILU, I);
-    Q35_KERNEL(Q35_KERNEL_PREP, B * (pending.splits * 2.0 * I * 4.0 + I + I / 32.0 * 4.0), launch_prep(sp, s),
+    Q35_KERNEL(Q35_KERNEL_PREP, B * (2.0 * I * 4.0 + I + I / 32.0 * 4.0), launch_prep(sp, s),
                "silu prep");
     if (tracing) Q35_STEP(trace_codes(l, Q35_TRACE_CODES_DOWN, I), "trace");
     // the down projection stays split: owning all of its K splits, a
@@ -1220,7 +1216,7 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
     a.normed_out = rt->hidden_out;
     a.rows = sh.heads_identity ? nullptr : head_rows;
     const double HR = heads;
-    const double add_rows = add_pending ? pending.splits * H * 4.0 + H * 4.0 : 0.0;
+    const double add_rows = add_pending ? H * 4.0 + H * 4.0 : 0.0;
     Q35_KERNEL(Q35_KERNEL_PREP, HR * (H * 4.0 + add_rows + H + H / 32.0 * 4.0) + H * 4.0 + HR * H * 4.0,
                launch_rms_prep(a, s), "final norm prep");
     if (add_pending) cur ^= 1;
