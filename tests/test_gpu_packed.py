@@ -80,14 +80,17 @@ def test_long_chunks_equal_single_steps(q, ctx, small, chunks):
     rt.close()
 
 
-@pytest.mark.parametrize("layout", ["dense", "split"])
+@pytest.mark.parametrize("layout", ["wide", "narrow"])
 def test_packed_step_equals_separate_calls(q, ctx, small, layout):
     """Decode rows of two requests and prompt chunks of two others in one step
-    (242 rows: the dense GEMM; 30 rows: the split GEMMs) against the decode
-    step and the two prefill calls run one after another."""
+    (242 rows: more than 64, so prompt rows run the chunk scan and the tiled
+    attention; 30 rows: one token group) against the decode step and the two
+    prefill calls run one after another. At hidden 256 neither case fills the
+    chip with dense-GEMM waves (gemm_dense_fits), so both run the split GEMMs;
+    test_gpu_config5.py checks the dense GEMM in a packed step at 4B shapes."""
     d, model = small
     rng = np.random.default_rng(11)
-    plens = [40, 70, 150, 90] if layout == "dense" else [40, 70, 20, 8]
+    plens = [40, 70, 150, 90] if layout == "wide" else [40, 70, 20, 8]
     prompts = [rng.integers(0, d["vocab"], size=n).astype(np.int32) for n in plens]
     ctx_len = 200
     runs = []
