@@ -189,15 +189,40 @@ __device__ __forceinline__ q35_f32x4 pv_tile(const q35_f16x8 phi[2], const q35_f
   return c;
 }
 
+// The value operands of P*V taken straight from global memory: lane l
+// (column n = l % 16, token group tg = l / 16) of wavefront w loads 8 bytes,
+// dims 64w + 4n .. +3, of tokens 32ks + 8tg + i (i = 0..7) per 32-token step
+// ks -- each group of 16 lanes reads 128 contiguous bytes of a cache row --
+// and regroups them in registers: operand (ks, j) holds dim 64w + 4n + j of
+// its eight tokens, two per dword. Token 32ks + 8tg + i sits at k index
+// 8tg + i of step ks, as in the LDS-staged form (pv_tile), so every output
+// element sees the same products in the same order; only the dim a column
+// stands for changes.
+struct VOps {
+  q35_u32x2 raw[2][8];  // [ks][i]: 4 dims of one token
+};
+__device__ __forceinline__ q35_f16x8 v_operand(const VOps &v, int ks, int j) {
+  // binary16 j of each token: low half of dword j/2 for even j, high half for odd
+  const unsigned sel = (j & 1) ? 0x07060302u : 0x05040100u;
+  q35_u32x4 d;
+#pragma unroll
+  for (int p = 0; p < 4; ++p)
+    d[p] = __builtin_amdgcn_perm(v.raw[ks][2 * p + 1][j >> 1], v.raw[ks][2 * p][j >> 1], sel);
+  return q35_f16x8_bits(d);
+}
+
 // Decode: one workgroup of 4 wavefronts per (chunk, KV head, request row);
 // the row's QPK heads are the live rows of one M tile. Wavefront w scores
-// token tile w (its keys loaded straight into operands); the chunk's V rows
-// are staged in LDS with coalesced loads (32 lanes per row); the tile maxima
-// and sums meet in LDS; wavefront w then forms P*V for dims 64w .. 64w+63.
-// Occupancy floor 2 keeps the MFMA results in VGPRs (no AGPR copies).
+// token tile w (its keys loaded straight into operands); the tile maxima and
+// sums meet in LDS; wavefront w then forms P*V for dims 64w .. 64w+63 from
+// value operands loaded straight into registers (VOps). The loads are issued
+// queries (staged in LDS), keys, values, so the scores and the softmax run
+// while the values are still in flight. Occupancy floor 2 keeps the MFMA
+// results in VGPRs.
 template <int QPK>
 __global__ __launch_bounds__(256) Q35_WAVES_PER_EU(2) void attention_kernel(AttnArgs a) {
-  __shared__ __align__(16) uint16_t vs[kChunkTokens * kVStride];
+  constexpr int kQStride = kHeadDim + 4;  // floats per staged query row (rows start on different banks)
+  __shared__ __align__(16) float qs[QPK * kQStride];
   __shared__ __align__(16) float pl[16 * kPStride];
   __shared__ float tmax[4][16], tsum[4][16];
   const int sp = blockIdx.x, g = blockIdx.y;
@@ -211,14 +236,28 @@ __global__ __launch_bounds__(256) Q35_WAVES_PER_EU(2) void attention_kernel(Attn
   // page_tokens is a power of two: shifts and masks, not integer division
   const int pshift = __builtin_ctz(static_cast<unsigned>(a.page_tokens)), pmask = a.page_tokens - 1;
   const int kt = 16 * wave + (lane & 15);  // this lane's key token within the chunk
-  // one round trip: the context length and the page-table entries of the
-  // lane's key token and of its 8 value rows (2w + 8i + l/32)
+  const int tg = lane >> 4;                // this lane's value token group
+  // one round trip: the row's QPK query heads (QPK x 256 floats, one 16-byte
+  // load per thread), the context length and the page-table entries of the
+  // lane's key token and of its 16 value tokens (pages of 8 or more tokens
+  // hold whole 8-token groups: the group's first entry serves all 8)
+  constexpr int kQ4 = QPK * kHeadDim / 4, kQLoads = (kQ4 + 255) / 256;
+  const q35_f32x4 *qsrc = reinterpret_cast<const q35_f32x4 *>(a.q + (static_cast<size_t>(r) * a.heads + g * QPK) * kHeadDim);
+  q35_f32x4 qraw[kQLoads];
+#pragma unroll
+  for (int u = 0; u < kQLoads; ++u) {
+    const int e = tid + 256 * u;
+    if (e < kQ4) qraw[u] = qsrc[e];
+  }
   const int seq = a.seq_lens != nullptr ? a.seq_lens[r] : a.positions[r] + 1;
   const int pfirst = pt[min(t0 >> pshift, last_page)];
   const int pk = pt[min((t0 + kt) >> pshift, last_page)];
-  int pv[8];
+  const int istep = pshift >= 3 ? 0 : 1;
+  int pv[2][8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) pv[i] = pt[min((t0 + 2 * wave + 8 * i + (lane >> 5)) >> pshift, last_page)];
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pv[ks][i] = pt[min((t0 + 32 * ks + 8 * tg + i * istep) >> pshift, last_page)];
   if (t0 >= seq) return;  // whole workgroup
   const int n = min(seq - t0, kChunkTokens);
   // keys of tile `wave` (slots past the context read the chunk's first token)
@@ -228,23 +267,32 @@ __global__ __launch_bounds__(256) Q35_WAVES_PER_EU(2) void attention_kernel(Attn
   q35_u32x4 kraw[8];
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk) kraw[kk] = Q35_LOAD_NT(reinterpret_cast<const q35_u32x4 *>(krow + 32 * kk));
-  // value rows 2w + 8i + l/32, 16 bytes each at dims 8(l%32)
-  q35_u32x4 vraw[8];
+  q35_compiler_fence();  // the keys go out before the values
+  // values (slots past the context read the chunk's first token: p = 0 there)
+  VOps v;
+  const size_t vcol = static_cast<size_t>(g) * kHeadDim + 64 * wave + 4 * (lane & 15);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int vt = 2 * wave + 8 * i + (lane >> 5);
-    const bool vin = vt < n;
-    vraw[i] = Q35_LOAD_NT(reinterpret_cast<const q35_u32x4 *>(
-        a.v_pool + ((static_cast<size_t>(vin ? pv[i] : pfirst) << pshift) + ((vin ? t0 + vt : t0) & pmask)) * kvw +
-        static_cast<size_t>(g) * kHeadDim + 8 * (lane & 31)));
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int vt = 32 * ks + 8 * tg + i;
+      const bool vin = vt < n;
+      v.raw[ks][i] = Q35_LOAD_NT(reinterpret_cast<const q35_u32x2 *>(
+          a.v_pool + ((static_cast<size_t>(vin ? pv[ks][i] : pfirst) << pshift) + ((vin ? t0 + vt : t0) & pmask)) * kvw +
+          vcol));
+    }
+
+  q35_compiler_fence();  // every load above is in flight before the first wait
+#pragma unroll
+  for (int u = 0; u < kQLoads; ++u) {
+    const int e = tid + 256 * u;
+    if (e < kQ4) *reinterpret_cast<q35_f32x4 *>(qs + (e >> 6) * kQStride + 4 * (e & 63)) = qraw[u];
   }
+  lds_barrier();
   // query m = lane % 16 is head g*QPK + m
   const int m = lane & 15;
   QOps q;
-  load_q_ops(a.q + (static_cast<size_t>(r) * a.heads + g * QPK + min(m, QPK - 1)) * kHeadDim, m < QPK, lane, q);
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    *reinterpret_cast<q35_u32x4 *>(vs + (2 * wave + 8 * i + (lane >> 5)) * kVStride + 8 * (lane & 31)) = vraw[i];
+  load_q_ops(qs + min(m, QPK - 1) * kQStride, m < QPK, lane, q);
 
   const q35_f32x4 s = qk_tile(q, [&](int kk) { return q35_f16x8_bits(kraw[kk]); });
   float sc[4];
@@ -268,17 +316,27 @@ __global__ __launch_bounds__(256) Q35_WAVES_PER_EU(2) void attention_kernel(Attn
 
   q35_f16x8 phi[2], plo[2];
   load_p_ops(pl, lane, phi, plo);
+  // lane l receives O[4(l/16) + jj][column l % 16] of operand j: dim
+  // 64w + 4(l % 16) + j of query head g*QPK + 4(l/16) + jj
+  q35_f32x4 o[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int dt = 4 * wave + i;
-    const q35_f32x4 o = pv_tile(phi, plo, vs, dt, lane);
+  for (int j = 0; j < 4; ++j) {
+    q35_f32x4 c = {0.0F, 0.0F, 0.0F, 0.0F};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int mm = 4 * (lane >> 4) + j;
-      if (mm < QPK) {
-        const size_t hs = (static_cast<size_t>(ord) * a.heads + g * QPK + mm) * a.max_splits + sp;
-        a.part_o[hs * kHeadDim + 16 * dt + (lane & 15)] = o[j];
-      }
+    for (int ks = 0; ks < 2; ++ks) {
+      const q35_f16x8 vo = v_operand(v, ks, j);
+      c = Q35_MFMA_F32_16X16X32_F16(phi[ks], vo, c);
+      c = Q35_MFMA_F32_16X16X32_F16(plo[ks], vo, c);
+    }
+    o[j] = c;
+  }
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    const int mm = 4 * (lane >> 4) + jj;
+    if (mm < QPK) {
+      const size_t hs = (static_cast<size_t>(ord) * a.heads + g * QPK + mm) * a.max_splits + sp;
+      const q35_f32x4 out = {o[0][jj], o[1][jj], o[2][jj], o[3][jj]};
+      *reinterpret_cast<q35_f32x4 *>(a.part_o + hs * kHeadDim + 64 * wave + 4 * (lane & 15)) = out;
     }
   }
   if (wave == 0 && lane < QPK) {

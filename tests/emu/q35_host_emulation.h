@@ -218,6 +218,18 @@ inline unsigned long long atomicMax(unsigned long long *p, unsigned long long v)
 }
 inline unsigned __float_as_uint(float f) { unsigned u; std::memcpy(&u, &f, 4); return u; }
 inline int __builtin_amdgcn_readlane(int v, int src) { return ::q35emu::readlane(v, src); }
+// v_perm_b32: byte i of the result is byte sel.byte[i] of the eight bytes
+// {s1 (bytes 0-3), s0 (bytes 4-7)}; selectors 8 and up are not used here
+inline unsigned __builtin_amdgcn_perm(unsigned s0, unsigned s1, unsigned sel) {
+  const unsigned long long both = (static_cast<unsigned long long>(s0) << 32) | s1;
+  unsigned r = 0;
+  for (int i = 0; i < 4; ++i) {
+    const unsigned b = (sel >> (8 * i)) & 0xFFu;
+    if (b > 7) std::abort();
+    r |= static_cast<unsigned>((both >> (8 * b)) & 0xFFu) << (8 * i);
+  }
+  return r;
+}
 // value of `v` in lane `src` (per lane) of the wavefront; every lane calls it
 template <typename T>
 inline T __shfl(T v, int src, int width = 64) {
