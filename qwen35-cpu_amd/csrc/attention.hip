@@ -591,25 +591,22 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(AttnArgs a, const f
   const int b = blockIdx.x & 1, h = blockIdx.x >> 1;
   const int ord = static_cast<int>(blockIdx.y);  // the decode kernel's ordinal of the row
   const int r = a.row_list != nullptr ? a.row_list[ord] : ord;
-  const int lane = threadIdx.x, j = lane & 15;
+  // lane l holds dims 128b + 2l, +1 of the head (an H128 item of 64 lanes)
+  const int lane = threadIdx.x;
   const size_t hs = (static_cast<size_t>(ord) * a.heads + h) * a.max_splits;
-  const int d0 = 128 * b + 8 * j;
+  const int d0 = 128 * b + 2 * lane;
   const size_t o = (static_cast<size_t>(r) * a.heads + h) * kHeadDim + d0;
-  const q35_f32x4 gate_lo = *reinterpret_cast<const q35_f32x4 *>(gates + o);
-  const q35_f32x4 gate_hi = *reinterpret_cast<const q35_f32x4 *>(gates + o + 4);
+  const q35_f32x2 gate = *reinterpret_cast<const q35_f32x2 *>(gates + o);
   const int seq = a.seq_lens != nullptr ? a.seq_lens[r] : a.positions[r] + 1;
   // the first statistics and partial rows are read at indices bounded by the
   // row's partial slots, not by the chunk count, so they do not wait for the
   // context length; chunks past the context are masked below and never used
   const int bound = a.max_splits;
-  q35_f32x4 rows[kMergeBatch][2];
+  q35_f32x2 rows[kMergeBatch];
   auto load_rows = [&](int s0, int bound) {
 #pragma unroll
-    for (int u = 0; u < kMergeBatch; ++u) {
-      const q35_f32x4 *src = reinterpret_cast<const q35_f32x4 *>(a.part_o + (hs + min(s0 + u, bound - 1)) * kHeadDim + d0);
-      rows[u][0] = src[0];
-      rows[u][1] = src[1];
-    }
+    for (int u = 0; u < kMergeBatch; ++u)
+      rows[u] = *reinterpret_cast<const q35_f32x2 *>(a.part_o + (hs + min(s0 + u, bound - 1)) * kHeadDim + d0);
   };
   // chunk statistics of chunks lane, lane + 64, ...: the first batch of 64
   // stays in registers
@@ -625,7 +622,7 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(AttnArgs a, const f
   float M = m0;
   for (int s = lane + 64; s < splits; s += 64) M = fmaxf(M, a.part_ml[(hs + s) * 2]);
   M = group_max<64>(M);
-  float acc[8] = {0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F};
+  float acc[2] = {0.0F, 0.0F};
   float L = 0.0F;
   for (int s0 = 0; s0 < splits; s0 += 64) {
     const int cnt = min(64, splits - s0);
@@ -647,24 +644,16 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(AttnArgs a, const f
         if (s + u >= cnt) break;
         const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), s + u));
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          acc[e] = fmaf(ws, rows[u][0][e], acc[e]);
-          acc[4 + e] = fmaf(ws, rows[u][1][e], acc[4 + e]);
-        }
+        for (int e = 0; e < 2; ++e) acc[e] = fmaf(ws, rows[u][e], acc[e]);
       }
     }
   }
   const float inv = 1.0F / (L > 0.0F ? L : 1.0F);
-  float y[8];
+  float y[2];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    y[e] = (acc[e] * inv) * sigmoid_stable(gate_lo[e]);
-    y[4 + e] = (acc[4 + e] * inv) * sigmoid_stable(gate_hi[e]);
-  }
-  if (out != nullptr && lane < 16)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) out[o + e] = y[e];
-  if (qo.codes != nullptr) h128_quantize_row16(y, r, 2 * h + b, a.heads * kHeadDim / 32, true, seed, qo, lane < 16);
+  for (int e = 0; e < 2; ++e) y[e] = (acc[e] * inv) * sigmoid_stable(gate[e]);
+  if (out != nullptr) *reinterpret_cast<q35_f32x2 *>(out + o) = q35_f32x2{y[0], y[1]};
+  if (qo.codes != nullptr) h128_quantize_lanes<64>(y, r, 2 * h + b, a.heads * kHeadDim / 32, true, seed, qo, true);
 }
 
 // The rows of the segments of two or more rows in a tiled launch (prompt

@@ -121,9 +121,9 @@ __global__ __launch_bounds__(THREADS) void delta_kernel(DeltaArgs a) {
   // written only after all reads), then the math
   const int q_dim = a.k_heads * kDim, v_dim = a.v_heads * kDim;
   const int channels = 2 * q_dim + v_dim;
-  // output gate and gated-norm weights of columns 8(lane%16)..+7 (wave 0)
-  float z[8] = {0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F};
-  float nw[8] = {0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F, 0.0F};
+  // output gate and gated-norm weights of columns 2(lane), 2(lane)+1 (wave 0)
+  float z[2] = {0.0F, 0.0F};
+  float nw[2] = {0.0F, 0.0F};
   if constexpr (FUSED) {
     float *conv = a.conv_base + static_cast<long long>(a.slots[r]) * a.conv_slot_stride;
     constexpr int K = kConvKernel;
@@ -137,10 +137,16 @@ __global__ __launch_bounds__(THREADS) void delta_kernel(DeltaArgs a) {
     // raw (split) loads of every small input first, then the state tile,
     // then the reductions
     float xq_s[MS], xv_s[MS], b_s[MS], a_s[MS];
-    q35_f32x4 z_s[MS][2];
+    q35_f32x2 z_s[MS];
     a.proj.template load<MS>(r, chq, xq_s);
     a.proj.template load<MS>(r, chv, xv_s);
-    a.proj.template load8<MS>(r, channels + vh * kDim + 8 * (lane & 15), z_s);
+    {
+      const float *zq = a.proj.p + static_cast<long long>(r) * a.proj.width + channels + vh * kDim + 2 * lane;
+#pragma unroll
+      for (int u = 0; u < MS; ++u)
+        z_s[u] = *reinterpret_cast<const q35_f32x2 *>(zq + static_cast<long long>(min(u, a.proj.splits - 1)) *
+                                                               a.proj.split_stride);
+    }
     // with separate gate rows the projection row is [qkv | z] only
     // b and a of this head: projection columns, or (Q8 gate tail) the
     // separate gate rows [batch][2 v_heads] read as one split -- one view, so
@@ -172,13 +178,19 @@ __global__ __launch_bounds__(THREADS) void delta_kernel(DeltaArgs a) {
     }
     // (every thread loads these; wave 0 / thread 0 use them)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) nw[e] = a.norm_w[8 * (lane & 15) + e];
+    for (int e = 0; e < 2; ++e) nw[e] = a.norm_w[2 * lane + e];
     const float dtb = a.dt_bias[vh];
     const float sa_ = a.ssm_a[vh];
     load_state();
     const float xq = a.proj.template reduce<MS>(xq_s);
     const float xv = a.proj.template reduce<MS>(xv_s);
-    a.proj.template reduce8<MS>(z_s, z);
+    {
+      q35_f32x2 zz = z_s[0];
+#pragma unroll
+      for (int u = 1; u < MS; ++u) zz = u < a.proj.splits ? zz + z_s[u] : zz;
+      z[0] = zz[0];
+      z[1] = zz[1];
+    }
     const float bval = ba.template reduce<MS>(b_s);
     const float aval = ba.template reduce<MS>(a_s);
     // causal conv1d + SiLU (activation.cpp:164-222: x * w[K-1] first, then
@@ -255,35 +267,37 @@ __global__ __launch_bounds__(THREADS) void delta_kernel(DeltaArgs a) {
     return;
   }
 
-  // ---- 4. outputs: wave 0, lane j = lane % 16 holds columns 8j .. 8j+7
-  // (the four 16-lane rows compute the same values; row 0 stores)
+  // ---- 4. outputs: wave 0
   const int j = lane & 15;
-  const bool writer = lane < 16;
-  float y[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) y[e] = so[8 * j + e];
   if constexpr (FUSED) {
-    // gated RMSNorm (offset 0) over the head, then * SiLU(z)  (layers.inl:198-207)
+    // gated RMSNorm (offset 0) over the head, then * SiLU(z)  (layers.inl:198-207).
+    // The sum of squares in 16-lane order (lane j: columns 8j .. 8j+7 in
+    // order, then the row butterfly; the four rows compute the same), as the
+    // prefill chunk kernel forms it; then lane l finishes columns 2l, 2l+1
+    // and the 64 lanes prepare the head's H128 block.
     float ss = 0.0F;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) ss += y[e] * y[e];
+    for (int e = 0; e < 8; ++e) {
+      const float x = so[8 * j + e];
+      ss += x * x;
+    }
     ss = row_sum16(ss);
     const float inv = 1.0F / sqrtf(ss / static_cast<float>(kDim) + a.eps);
+    float y[2];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) y[e] = silu_times(z[e], y[e] * inv * (nw[e] + 0.0F));
-    if (a.out != nullptr && writer)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) a.out[static_cast<size_t>(r) * v_dim + vh * kDim + 8 * j + e] = y[e];
+    for (int e = 0; e < 2; ++e) y[e] = silu_times(z[e], so[2 * lane + e] * inv * (nw[e] + 0.0F));
+    if (a.out != nullptr)
+      *reinterpret_cast<q35_f32x2 *>(a.out + static_cast<size_t>(r) * v_dim + vh * kDim + 2 * lane) = q35_f32x2{y[0], y[1]};
     if (a.codes != nullptr) {
       QuantOut qo;
       qo.codes = a.codes;
       qo.scales = a.scales;
-      h128_quantize_row16(y, r, vh, v_dim / 32, true, a.seed, qo, writer);
+      h128_quantize_lanes<64>(y, r, vh, v_dim / 32, true, a.seed, qo, true);
     }
-  } else if (writer) {
+  } else if (lane < 16) {
     const size_t o = (static_cast<size_t>(r) * a.v_heads + vh) * kDim + 8 * j;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) a.out[o + e] = y[e];
+    for (int e = 0; e < 8; ++e) a.out[o + e] = so[8 * j + e];
   }
   store_state();
 }

@@ -1,15 +1,16 @@
 // Activation preparation for the Q4-G32-DOT4 projections: the producer
 // (plain rows, SiLU(gate) * up over split GEMM partials, or residual update +
 // RMSNorm) followed by the randomized-sign Hadamard-128 rotation and per-32
-// int8 quantization (h128_quantize_row16).
+// int8 quantization (h128_quantize_lanes).
 //
 // Reference semantics (bit-exact given the same FP32 input):
 //   signs + FWHT stage order 1,2,...,64     src/cpu/q4_h128.cpp:35-61
 //   absmax/127, unrounded 1/scale, round half away from zero, clamp +-127,
 //   stored scale = binary16(scale) * 1/sqrt(128)   q4_0.cpp:212-235, q4_h128.cpp:319-321
-// prep_kernel: 16 lanes per (token, 128-column block), four blocks per
-// one-wavefront workgroup. rms_prep_kernel: one workgroup per token (the row's sum of
-// squares is shared through LDS).
+// prep_kernel: 32 lanes per (token, 128-column block), two blocks per
+// one-wavefront workgroup. rms_prep_kernel: one workgroup per token (the row's
+// sum of squares is shared through LDS), 32 lanes per block (16 with the Q8
+// gate tail).
 #include "q35_quant.h"
 
 namespace q35 {
@@ -17,48 +18,59 @@ namespace {
 
 constexpr int kPrepThreads = 256;
 
-// Eight consecutive source values of token t from column c0 (c0 % 8 == 0).
+// Four consecutive source values of token t from column c0 (c0 % 4 == 0);
+// the split partial rows are summed per column in split order.
 template <int SRC, int MS>
-__device__ __forceinline__ void load_source8(const PrepArgs &a, int t, int c0, float v[8]) {
+__device__ __forceinline__ void load_source4(const PrepArgs &a, int t, int c0, float v[4]) {
   if constexpr (SRC == kPrepPlain) {
-    const q35_f32x4 *x = reinterpret_cast<const q35_f32x4 *>(a.x + static_cast<size_t>(t) * a.x_stride + c0);
-    const q35_f32x4 lo = x[0], hi = x[1];
+    const q35_f32x4 x = *reinterpret_cast<const q35_f32x4 *>(a.x + static_cast<size_t>(t) * a.x_stride + c0);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v[e] = lo[e];
-      v[4 + e] = hi[e];
-    }
+    for (int e = 0; e < 4; ++e) v[e] = x[e];
   } else {
-    float g[8], u[8];
-    a.gate_up.template sum8<MS>(t, c0, g);
-    a.gate_up.template sum8<MS>(t, c0 + a.K, u);
+    const SplitRows &s = a.gate_up;
+    const float *q = s.p + static_cast<long long>(t) * s.width + c0;
+    q35_f32x4 g[MS], u[MS];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = silu_times(g[e], u[e]);
+    for (int i = 0; i < MS; ++i) {
+      const long long off = static_cast<long long>(min(i, s.splits - 1)) * s.split_stride;
+      g[i] = *reinterpret_cast<const q35_f32x4 *>(q + off);
+      u[i] = *reinterpret_cast<const q35_f32x4 *>(q + off + a.K);
+    }
+    q35_f32x4 gs = g[0], us = u[0];
+#pragma unroll
+    for (int i = 1; i < MS; ++i) {
+      gs = i < s.splits ? gs + g[i] : gs;
+      us = i < s.splits ? us + u[i] : us;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = silu_times(gs[e], us[e]);
   }
 }
 
-// 16 lanes per (token, 128-column block) item, four items per wavefront; MS
-// bounds the source's K splits.
+// kPrepLanes (32) lanes per (token, 128-column block) item, two items per
+// wavefront; MS bounds the source's K splits.
+constexpr int kPrepLanes = 32;
 template <int SRC, int MS>
 __global__ __launch_bounds__(kPrepThreads) void prep_kernel(PrepArgs a) {
+  constexpr int V = 128 / kPrepLanes;
   const int K = a.K, nb = K >> 5, nblk = K >> 7;
   const int items = a.tokens * nblk;
-  const int item0 = static_cast<int>((blockIdx.x * blockDim.x + threadIdx.x) >> 4);
+  const int item0 = static_cast<int>((blockIdx.x * blockDim.x + threadIdx.x) / kPrepLanes);
   const bool active = item0 < items;
   const int item = active ? item0 : items - 1;  // idle rows redo a valid item and store nothing
   const int t = item / nblk, blk = item - t * nblk;
-  float v[8];
-  const int c0 = blk * 128 + 8 * (threadIdx.x & 15);
-  load_source8<SRC, MS>(a, t, c0, v);
+  float v[V];
+  const int c0 = blk * 128 + V * (threadIdx.x & (kPrepLanes - 1));
+  load_source4<SRC, MS>(a, t, c0, v);
   if (a.y_out != nullptr && active)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) a.y_out[static_cast<size_t>(t) * K + c0 + e] = v[e];
+    for (int e = 0; e < V; ++e) a.y_out[static_cast<size_t>(t) * K + c0 + e] = v[e];
   QuantOut o;
   o.codes = a.codes;
   o.scales = a.scales;
   o.x4 = a.x4;
   o.x1 = a.x1;
-  h128_quantize_row16(v, t, blk, nb, a.h128, a.seed, o, active);
+  h128_quantize_lanes<kPrepLanes>(v, t, blk, nb, a.h128, a.seed, o, active);
 }
 
 // Residual update + RMSNorm + preparation, one workgroup (256 threads) per
@@ -81,20 +93,23 @@ __global__ __launch_bounds__(kRmsThreads) void rms_prep_kernel(RmsPrepArgs a) {
   __shared__ float gsc[GATES ? kRmsMaxK / 32 : 1];
   __shared__ float gdot[GATES ? kMaxGateItems : 1];
   __shared__ float gmul[GATES ? kMaxGateItems : 1];
+  // L lanes per 128-column item (V columns each): 32, or 16 with the gate
+  // tail, whose identity-basis codes take eight columns per lane
+  constexpr int L = GATES ? 16 : 32, V = 128 / L, kItemsPerPass = kRmsThreads / L;
   const int t = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int K = a.K, n4 = K >> 2;
-  const int nblk = K >> 7, j = tid & 15;
+  const int nblk = K >> 7, j = tid & (L - 1);
   // (1 + w) of this thread's first quantization item, loaded together with
   // the row so that no load waits behind the barrier
-  float w1[8];
+  float w1[V];
   {
-    const int blk = min(tid >> 4, nblk - 1);
-    const q35_f32x4 *wp = reinterpret_cast<const q35_f32x4 *>(a.weight + blk * 128 + 8 * j);
-    const q35_f32x4 lo = wp[0], hi = wp[1];
+    const int blk = min(tid / L, nblk - 1);
+    const q35_f32x4 *wp = reinterpret_cast<const q35_f32x4 *>(a.weight + blk * 128 + V * j);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      w1[e] = lo[e] + 1.0F;
-      w1[4 + e] = hi[e] + 1.0F;
+    for (int h = 0; h < V / 4; ++h) {
+      const q35_f32x4 x = wp[h];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w1[4 * h + e] = x[e] + 1.0F;
     }
   }
   // the residual row of output row t (a gathered row set: the head rows)
@@ -134,22 +149,22 @@ __global__ __launch_bounds__(kRmsThreads) void rms_prep_kernel(RmsPrepArgs a) {
   QuantOut o;
   o.codes = a.codes;
   o.scales = a.scales;
-  for (int blk0 = 0; blk0 < nblk; blk0 += kRmsThreads / 16) {
-    if (blk0 + wave * 4 >= nblk) break;  // wave-uniform: all four rows idle
-    const int want = blk0 + (tid >> 4);
+  for (int blk0 = 0; blk0 < nblk; blk0 += kItemsPerPass) {
+    if (blk0 + wave * (64 / L) >= nblk) break;  // wave-uniform: all of its items idle
+    const int want = blk0 + tid / L;
     const bool active = want < nblk;
     const int blk = active ? want : nblk - 1;
-    const int c0 = blk * 128 + 8 * j;
-    if (blk0 > 0) {  // widths above 2048 columns: a second item per thread
+    const int c0 = blk * 128 + V * j;
+    if (blk0 > 0) {  // wider rows: a further item per thread
 #pragma unroll
-      for (int e = 0; e < 8; ++e) w1[e] = a.weight[c0 + e] + 1.0F;
+      for (int e = 0; e < V; ++e) w1[e] = a.weight[c0 + e] + 1.0F;
     }
-    float v[8];
+    float v[V];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = y[c0 + e] * rms_inv * w1[e];
+    for (int e = 0; e < V; ++e) v[e] = y[c0 + e] * rms_inv * w1[e];
     if (a.normed_out != nullptr && active)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) a.normed_out[static_cast<size_t>(t) * K + c0 + e] = v[e];
+      for (int e = 0; e < V; ++e) a.normed_out[static_cast<size_t>(t) * K + c0 + e] = v[e];
     if constexpr (GATES) {
       uint64_t word;
       int sum;
@@ -160,7 +175,7 @@ __global__ __launch_bounds__(kRmsThreads) void rms_prep_kernel(RmsPrepArgs a) {
         if ((j & 3) == 0) gsc[c0 >> 5] = stored;
       }
     }
-    h128_quantize_row16(v, t, blk, K >> 5, a.h128, a.seed, o, active);
+    h128_quantize_lanes<L>(v, t, blk, K >> 5, a.h128, a.seed, o, active);
   }
   if constexpr (GATES) {
     __syncthreads();
@@ -230,12 +245,12 @@ __global__ void x1_to_a16_kernel(const q35_q8_0_block_x1 *x1, int tokens, int nb
 
 hipError_t launch_prep(const PrepArgs &a, hipStream_t stream) {
   if (a.tokens <= 0) return hipSuccess;
-  // one wavefront (four items) per workgroup: the split partials a SiLU
-  // preparation reads spread over 4x more compute units than with 256-thread
-  // workgroups (one unit keeps only a few tens of KiB in flight)
-  constexpr int kThreads = 64;
+  // one wavefront (two items) per workgroup: the split partials a SiLU
+  // preparation reads spread over many compute units (one unit keeps only a
+  // few tens of KiB in flight), and each lane's rotation chain is short
+  constexpr int kThreads = 64, kItems = kThreads / kPrepLanes;
   const int items = a.tokens * (a.K >> 7);
-  const dim3 grid((items + kThreads / 16 - 1) / (kThreads / 16)), block(kThreads);
+  const dim3 grid((items + kItems - 1) / kItems), block(kThreads);
   if (a.source == kPrepSiluMul) {
     switch (split_bound(a.gate_up.splits)) {
       case 1: Q35_LAUNCH((prep_kernel<kPrepSiluMul, 1>), grid, block, 0, stream, a); break;

@@ -73,6 +73,17 @@ __device__ __forceinline__ int q35_row_xor_i(int v, int m) {
 __device__ __forceinline__ float q35_row_xor(float v, int m) {
   return __int_as_float(q35_row_xor_i(__float_as_int(v), m));
 }
+// Exchange with lane l^m for m = 1 .. 32: DPP row moves inside a 16-lane row,
+// ds_swizzle's xor mode across the two rows of a 32-lane half (m = 16), and
+// a bpermute across the halves (m = 32).
+__device__ __forceinline__ int q35_lane_xor_i(int v, int m) {
+  if (m < 16) return q35_row_xor_i(v, m);
+  if (m == 16) return __builtin_amdgcn_ds_swizzle(v, 0x401F);  // and 0x1F, or 0, xor 0x10
+  return __shfl_xor(v, 32, 64);
+}
+__device__ __forceinline__ float q35_lane_xor(float v, int m) {
+  return __int_as_float(q35_lane_xor_i(__float_as_int(v), m));
+}
 // The value of lane 7 - i of this lane's 8-lane half row (row_half_mirror):
 // one DPP move to a lane of the other quad of the half.
 __device__ __forceinline__ float q35_row_half_mirror(float v) {

@@ -375,6 +375,8 @@ inline float q35_quad_xor1(float v) { return ::q35emu::shfl_xor(v, 1); }
 inline float q35_quad_xor2(float v) { return ::q35emu::shfl_xor(v, 2); }
 inline float q35_row_xor(float v, int m) { return ::q35emu::shfl_xor(v, m); }
 inline int q35_row_xor_i(int v, int m) { return ::q35emu::shfl_xor(v, m); }
+inline float q35_lane_xor(float v, int m) { return ::q35emu::shfl_xor(v, m); }
+inline int q35_lane_xor_i(int v, int m) { return ::q35emu::shfl_xor(v, m); }
 inline float q35_row_half_mirror(float v) {
   const int l = ::q35emu::t_ctx.lane;
   return ::q35emu::shfl_src(v, (l & ~7) | (7 - (l & 7)));
