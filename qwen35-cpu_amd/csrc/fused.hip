@@ -234,6 +234,15 @@ __global__ __launch_bounds__(64 * MAXW) void gemm_resid_kernel(ResidGemmArgs a) 
   float sc[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) sc[k] = g.scales[min(k * bd + tid, nsc - 1)];
+  // the residual values of this thread's outputs (e = tid, tid + bd, ...
+  // below 256), loaded now so the epilogue waits on no memory; unconditional
+  // loads at clamped indices (a load under a branch holds every later wait)
+  float res[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int e = min(tid + k * bd, 255);
+    res[k] = a.residual[static_cast<size_t>(min(e >> 4, g.tokens - 1)) * g.rows + grp * 16 + (e & 15)];
+  }
   RW::Q q[BPS];
   RW::D d[BPS];
   long act[BPS];
@@ -278,13 +287,16 @@ __global__ __launch_bounds__(64 * MAXW) void gemm_resid_kernel(ResidGemmArgs a) 
   }
   __syncthreads();
   const int ng = g.rows >> 4;
-  for (int e = tid; e < 256; e += blockDim.x) {  // 16-lane rows: token t's 16 columns
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {  // 16-lane rows: token t's 16 columns
+    const int e = tid + k * bd;
+    if (e >= 256) break;
     const int t = e >> 4, r = e & 15;
     float sum = part[t * 16 + r];
     for (int u = 1; u < S; ++u) sum += part[(u * 16 + t) * 16 + r];
     const int row = grp * 16 + r;
     const size_t o = static_cast<size_t>(min(t, g.tokens - 1)) * g.rows + row;
-    const float x = a.residual[o] + sum;
+    const float x = res[k] + sum;
     const float gs = sq_group16_lanes(x);
     if (t < g.tokens) {
       if (a.proj_out != nullptr) a.proj_out[o] = sum;
