@@ -84,8 +84,10 @@ constexpr int kRmsMaxK = 4096;
 // identity-basis codes go to LDS, each thread takes whole (row, block) int8
 // dots, and one thread per gate row runs the block chain
 // acc = fma(float(dot), mscale * vscale, acc) in block order.
-template <int MS, bool GATES>  // MS: bound on the added rows' K splits (0: nothing to add)
+// EMBED: the rows are gathered from the embedding (MS == 0).
+template <int MS, bool GATES, bool EMBED>  // MS: bound on the added rows' K splits (0: nothing to add)
 __global__ __launch_bounds__(kRmsThreads) void rms_prep_kernel(RmsPrepArgs a) {
+  static_assert(!EMBED || MS == 0, "the embedding gather adds no rows");
   __shared__ float y[kRmsMaxK];
   __shared__ float gsq[kRmsMaxK / 16];  // sums of squares per 16-column group
   __shared__ float total_sq;
@@ -115,8 +117,35 @@ __global__ __launch_bounds__(kRmsThreads) void rms_prep_kernel(RmsPrepArgs a) {
   // the residual row of output row t (a gathered row set: the head rows)
   const size_t xr = a.rows != nullptr ? static_cast<size_t>(a.rows[t]) : static_cast<size_t>(t);
   const q35_f32x4 *xin = reinterpret_cast<const q35_f32x4 *>(a.x_in + xr * K);
+  int token = 0;
+  if constexpr (EMBED) token = a.token_ids[t];
   for (int i = tid; i < n4; i += kRmsThreads) {
-    q35_f32x4 v = xin[i];
+    q35_f32x4 v;
+    if constexpr (EMBED) {
+      // columns 4i..4i+3 of the token's row: one 4-byte run of the tile's
+      // DOT4 codes (the same nibble half) and the row's binary16 scale,
+      // x = half(d) * (u - 8) as embed_kernel forms it
+      const int k = 4 * i, b = k >> 5, kk = k & 31, rt = token >> 3, row = token & 7;
+      const uint8_t *tile;
+      uint16_t dh;
+      if (a.embed_g16) {
+        tile = reinterpret_cast<const uint8_t *>(a.embed) + (static_cast<size_t>(rt) * (K >> 5) + b) * 160;
+        dh = *reinterpret_cast<const uint16_t *>(tile + 2 * (8 * (kk >> 4) + row));
+        tile += 32;
+      } else {
+        tile = reinterpret_cast<const uint8_t *>(a.embed) + (static_cast<size_t>(rt) * (K >> 5) + b) * 144;
+        dh = *reinterpret_cast<const uint16_t *>(tile + 2 * row);
+        tile += 16;
+      }
+      const uint32_t q4 = *reinterpret_cast<const uint32_t *>(tile + 32 * (kk >> 3) + 4 * row);
+      const int sh = 4 * ((kk & 7) >> 2);
+      const float d = half_bits_to_float(dh);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = d * static_cast<float>(static_cast<int>((q4 >> (8 * e + sh)) & 15u) - 8);
+      reinterpret_cast<q35_f32x4 *>(a.x_out + xr * K)[i] = v;
+    } else {
+      v = xin[i];
+    }
     if constexpr (MS > 0) {
       // columns 4i..4i+3 of every split, all loads in flight together
       const float *pp = a.add.p + xr * a.add.width + 4 * i;
@@ -136,6 +165,10 @@ __global__ __launch_bounds__(kRmsThreads) void rms_prep_kernel(RmsPrepArgs a) {
     // K % 128 == 0: the four lanes of a group run the same iterations
     const float gs = sq_group16_quad(v);
     if ((tid & 3) == 0) gsq[i >> 2] = gs;
+  }
+  if constexpr (EMBED) {
+    if (tid == 0 && a.counts != nullptr && a.count_input != nullptr && a.count_input[t])
+      a.counts[static_cast<long long>(a.slots[t]) * a.counts_stride + token] += 1;
   }
   // only LDS is shared: the x_out stores stay in flight
   lds_barrier();
@@ -272,11 +305,19 @@ hipError_t launch_rms_prep(const RmsPrepArgs &a, hipStream_t stream) {
                 a.gate_scales == nullptr || a.gates == nullptr))
     return hipErrorInvalidValue;
   const dim3 grid(a.tokens), block(kRmsThreads);
+  if (a.embed != nullptr) {
+    if (a.add.p != nullptr || a.x_out == nullptr || a.token_ids == nullptr) return hipErrorInvalidValue;
+    if (gates)
+      Q35_LAUNCH((rms_prep_kernel<0, true, true>), grid, block, 0, stream, a);
+    else
+      Q35_LAUNCH((rms_prep_kernel<0, false, true>), grid, block, 0, stream, a);
+    return hipGetLastError();
+  }
 #define Q35_RMS(MS)                                                                     \
   if (gates) {                                                                          \
-    Q35_LAUNCH((rms_prep_kernel<MS, true>), grid, block, 0, stream, a);                 \
+    Q35_LAUNCH((rms_prep_kernel<MS, true, false>), grid, block, 0, stream, a);          \
   } else {                                                                              \
-    Q35_LAUNCH((rms_prep_kernel<MS, false>), grid, block, 0, stream, a);                \
+    Q35_LAUNCH((rms_prep_kernel<MS, false, false>), grid, block, 0, stream, a);         \
   }
   switch (a.add.p == nullptr ? 0 : split_bound(a.add.splits)) {
     case 0: Q35_RMS(0) break;

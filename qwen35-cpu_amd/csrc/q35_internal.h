@@ -171,6 +171,17 @@ struct RmsPrepArgs {
   const float *gate_scales = nullptr;
   int gate_rows = 0;
   float *gates = nullptr;
+  // optional embedding gather in place of x_in (no rows to add): row t is
+  // the dequantized embedding row of token_ids[t], written to x_out as the
+  // residual stream, and the penalty counts of rows with count_input[t] set
+  // count the token (dequantize_embedding_row, gguf_matrix.inl:21-26)
+  const q35_q4_0_block_x8 *embed = nullptr;
+  bool embed_g16 = false;  // Q4G16Tile (160-byte) tiles
+  const int32_t *token_ids = nullptr;
+  int32_t *counts = nullptr;
+  long long counts_stride = 0;
+  const int32_t *slots = nullptr;
+  const uint8_t *count_input = nullptr;
 };
 constexpr int kMaxGateRows = 64;
 constexpr int kMaxGateItems = 6144;  // gate rows x K/32 blocks staged in LDS (4B: 64 x 80)

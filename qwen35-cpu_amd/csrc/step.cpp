@@ -775,10 +775,15 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
   Q35_STEP(hipMemcpyAsync(rt->meta_dev, rt->meta_host, rt->meta_bytes, hipMemcpyHostToDevice, s), "metadata copy");
   // a G16 head tile is 160 bytes per 8 x 32 (20 per row block) against 144 (18)
   const double g16_extra = m->embed_g16 ? static_cast<double>(d.vocab / 8) * (H / 32) * 16.0 : 0.0;
-  Q35_KERNEL(Q35_KERNEL_EMBED, B * (H / 32 * (m->embed_g16 ? 20.0 : 18.0) + H * 4.0 + 8.0),
-             launch_embed(m->embed, H / 32, tokens, batch, rt->x[0], H, rt->counts, d.vocab, slots, count_input, s,
-                          m->embed_g16),
-             "embedding");
+  // the embedding gather runs inside the first layer's input norm (its rows
+  // land in x[0]); a model without layers gathers them on their own
+  const bool embed_in_norm = d.n_layers > 0;
+  const double embed_bytes = B * (H / 32 * (m->embed_g16 ? 20.0 : 18.0) + H * 4.0 + 8.0);
+  if (!embed_in_norm)
+    Q35_KERNEL(Q35_KERNEL_EMBED, embed_bytes,
+               launch_embed(m->embed, H / 32, tokens, batch, rt->x[0], H, rt->counts, d.vocab, slots, count_input, s,
+                            m->embed_g16),
+               "embedding");
 
   // Residual stream: x[cur] holds it; a residual update writes x[cur ^ 1]
   // (the prep kernels read whole rows, so the update cannot run in place).
@@ -830,9 +835,19 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
   };
   // Residual update with the pending split rows (if `add`) + RMSNorm + prep.
   bool groups_ready = false;  // rt->sq_groups holds the sums of squares of x[cur] (set by gemm_resid)
-  auto rms_prep = [&](const float *w, bool add, bool h128, float *normed,
-                      const LayerDev *gate_layer = nullptr) -> hipError_t {
+  auto rms_prep = [&](const float *w, bool add, bool h128, float *normed, const LayerDev *gate_layer = nullptr,
+                      bool embed_rows = false) -> hipError_t {
     RmsPrepArgs a;
+    if (embed_rows) {  // the rows are the tokens' embeddings, kept in x[cur]
+      a.embed = m->embed;
+      a.embed_g16 = m->embed_g16;
+      a.token_ids = tokens;
+      a.counts = rt->counts;
+      a.counts_stride = d.vocab;
+      a.slots = slots;
+      a.count_input = count_input;
+      a.x_out = rt->x[cur];
+    }
     if (gate_layer != nullptr && gate_layer->gate_rows > 0) {
       a.gate_codes = gate_layer->gate_codes;
       a.gate_scales = gate_layer->gate_scales;
@@ -983,8 +998,10 @@ int runtime_enqueue_step(q35_runtime *rt, const StepShape &sh, bool want_logits)
       Q35_KERNEL(Q35_KERNEL_GEMM, norm_bytes(L.in_rows),
                  gemm_norm(L.in_proj, L.in_rows, L.input_norm, kConsumerSplits, normed_in), "norm + in projection");
     } else {
-      Q35_KERNEL(Q35_KERNEL_PREP, rms_bytes(add_pending),
-                 rms_prep(L.input_norm, add_pending, true, normed_in, L.linear ? &L : nullptr), "input norm prep");
+      const bool embed_rows = embed_in_norm && l == 0;
+      Q35_KERNEL(Q35_KERNEL_PREP, rms_bytes(add_pending) + (embed_rows ? embed_bytes : 0.0),
+                 rms_prep(L.input_norm, add_pending, true, normed_in, L.linear ? &L : nullptr, embed_rows),
+                 "input norm prep");
     }
     if (tracing) {
       Q35_STEP(trace_copy(rt, l, Q35_TRACE_X_IN, rt->x[cur], static_cast<size_t>(batch) * H * 4, s), "trace");
