@@ -22,6 +22,28 @@ namespace {
 constexpr int kHeadDim = 256;
 constexpr int kAttnThreads = 256;
 
+// The head preparation's roundings, contraction off: the squares of the
+// per-head RMSNorm, its 1 / sqrt(mean square + eps) over 256 dims (the mean a
+// rounding of its own: a constant divisor would otherwise fold into an fma
+// with eps), and the split-half RoPE pair (d < half: x0 = y[d],
+// x1 = y[d + half]; the upper dim of the pair: x0 = y[d - half], x1 = y[d]).
+__device__ __forceinline__ float head_sq(float x) {
+#pragma clang fp contract(off)
+  return x * x;
+}
+__device__ __forceinline__ float head_rms_inv(float ss, float eps) {
+#pragma clang fp contract(off)
+  return 1.0F / sqrtf(ss / static_cast<float>(kHeadDim) + eps);
+}
+__device__ __forceinline__ float rope_lower(float x0, float x1, float cs, float sn) {
+#pragma clang fp contract(off)
+  return x0 * cs - x1 * sn;
+}
+__device__ __forceinline__ float rope_upper(float x0, float x1, float cs, float sn) {
+#pragma clang fp contract(off)
+  return x1 * cs + x0 * sn;
+}
+
 template <int MS>  // bound on the qkv projection's K splits
 __global__ __launch_bounds__(kAttnThreads) void attn_prep_kernel(AttnPrepArgs a) {
   __shared__ float scratch[8];
@@ -50,20 +72,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_prep_kernel(AttnPrepArgs a)
   const float x = d < hd ? a.proj.template sum<MS>(r, col_x) : 0.0F;
   const float second = a.proj.template sum<MS>(r, col_2);
   if (is_q && d < hd) a.gate_out[(static_cast<size_t>(r) * a.heads + slot) * hd + d] = second;
-  const float ss = block_sum<kAttnThreads / 64>(x * x, scratch);
-  const float inv = 1.0F / sqrtf(ss / static_cast<float>(hd) + a.eps);
+  const float ss = block_sum<kAttnThreads / 64>(head_sq(x), scratch);
+  const float inv = head_rms_inv(ss, a.eps);  // head_dim is 256 (launch_attn_prep)
   float y = d < hd ? x * inv * w1 : 0.0F;
   if (d < hd) ybuf[d] = y;
   lds_barrier();
-  if (d < a.rope_dim) {
-    if (d < half) {
-      const float x0 = ybuf[d], x1 = ybuf[d + half];
-      y = x0 * cs - x1 * sn;
-    } else {
-      const float x0 = ybuf[d - half], x1 = ybuf[d];
-      y = x1 * cs + x0 * sn;
-    }
-  }
+  if (d < a.rope_dim) y = d < half ? rope_lower(ybuf[d], ybuf[d + half], cs, sn) : rope_upper(ybuf[d - half], ybuf[d], cs, sn);
   if (d >= hd) return;
   if (is_q) {
     a.q_out[(static_cast<size_t>(r) * a.heads + slot) * hd + d] = y;
@@ -258,6 +272,9 @@ __global__ __launch_bounds__(256) Q35_WAVES_PER_EU(2) void attention_kernel(Attn
   for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
     for (int i = 0; i < 8; ++i) pv[ks][i] = pt[min((t0 + 32 * ks + 8 * tg + i * istep) >> pshift, last_page)];
+  // the page-table loads go out before the context length is waited for
+  // (otherwise the compiler sinks them below the early return)
+  q35_compiler_fence();
   if (t0 >= seq) return;  // whole workgroup
   const int n = min(seq - t0, kChunkTokens);
   // keys of tile `wave` (slots past the context read the chunk's first token)
@@ -703,7 +720,7 @@ __global__ __launch_bounds__(16 * kFinishItems) void attention_finish_kernel(Att
 
 hipError_t launch_attn_prep(const AttnPrepArgs &a, hipStream_t stream) {
   if (a.batch <= 0) return hipSuccess;
-  if (a.head_dim > kHeadDim || a.rope_dim > a.head_dim) return hipErrorInvalidValue;
+  if (a.head_dim != kHeadDim || a.rope_dim > a.head_dim) return hipErrorInvalidValue;
   const dim3 grid(a.batch, a.heads + a.kv_heads);
   switch (split_bound(a.proj.splits)) {
     case 1: Q35_LAUNCH((attn_prep_kernel<1>), grid, kAttnThreads, 0, stream, a); break;

@@ -11,7 +11,12 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
   return __half2float(__ushort_as_half(h));
 }
 // Round to nearest even, as float_to_half (src/cpu/q8_0.cpp:18-55) for finite values.
+// The value is pinned in an fp32 register first: otherwise the compiler may
+// fold the multiply that produced it into the conversion (v_fma_mixlo_f16,
+// which rounds the exact product to binary16 once), and the result would
+// depend on the surrounding code instead of on the fp32 value.
 __device__ __forceinline__ uint16_t float_to_half_bits(float f) {
+  q35_materialize(f);
   return __half_as_ushort(__float2half_rn(f));
 }
 
