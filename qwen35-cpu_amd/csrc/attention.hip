@@ -112,7 +112,6 @@ __global__ __launch_bounds__(kAttnThreads) void attn_prep_kernel(AttnPrepArgs a)
 // the partial (max, sum, sum p*V) goes to attention_merge_kernel.
 constexpr int kChunkTokens = 64;
 constexpr int kKStride = kHeadDim + 8;  // halfs per staged K row: the lanes' 16-byte key reads spread over the banks
-constexpr int kVStride = kKStride;      // halfs per staged V row (16-byte aligned rows for the 16-byte stores)
 constexpr int kPStride = kChunkTokens + 4;  // floats per probability row in LDS
 
 // The query operands of one lane (query l % 16): dims 32kk + 8(l/16) .. +7
@@ -181,22 +180,19 @@ __device__ __forceinline__ void load_p_ops(const float *pl, int lane, q35_f16x8 
   }
 }
 
-// P*V of dims 16dt .. 16dt+15 from V rows staged in LDS (row stride
-// kVStride): the value operand of lane l gathers dim 16dt + l%16 of tokens
-// 32ks + 8(l/16) .. +7. Lane l receives O[4(l/16) + j][16dt + l % 16].
-__device__ __forceinline__ q35_f32x4 pv_tile(const q35_f16x8 phi[2], const q35_f16x8 plo[2], const uint16_t *vs,
-                                             int dt, int lane) {
-  const uint16_t *col = vs + (8 * (lane >> 4)) * kVStride + 16 * dt + (lane & 15);
+// P*V of dims 16dt .. 16dt+15 from a V chunk staged transposed in LDS
+// (vt[dim][token], row stride kVTStride): the value operand of lane l is the
+// 16 bytes of dim 16dt + l%16, tokens 32ks + 8(l/16) .. +7 (token
+// 32ks + 8(l/16) + i at k index 8(l/16) + i, as in the decode kernel's
+// register operands), read whole by one 16-byte LDS load.
+constexpr int kVTStride = kChunkTokens + 8;  // halfs per staged dim row: 16 rows of an operand read on distinct banks
+__device__ __forceinline__ q35_f32x4 pvt_tile(const q35_f16x8 phi[2], const q35_f16x8 plo[2], const uint16_t *vt,
+                                              int dt, int lane) {
+  const uint16_t *row = vt + (16 * dt + (lane & 15)) * kVTStride + 8 * (lane >> 4);
   q35_f32x4 c = {0.0F, 0.0F, 0.0F, 0.0F};
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
-    q35_u32x4 raw;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t lo = col[(32 * ks + 2 * e) * kVStride], hi = col[(32 * ks + 2 * e + 1) * kVStride];
-      raw[e] = lo | (hi << 16);
-    }
-    const q35_f16x8 v = q35_f16x8_bits(raw);
+    const q35_f16x8 v = q35_f16x8_bits(*reinterpret_cast<const q35_u32x4 *>(row + 32 * ks));
     c = Q35_MFMA_F32_16X16X32_F16(phi[ks], v, c);
     c = Q35_MFMA_F32_16X16X32_F16(plo[ks], v, c);
   }
@@ -384,9 +380,10 @@ __global__ __launch_bounds__(256) Q35_WAVES_PER_EU(2) void attention_kernel(Attn
 // one-partial case (attention_finish_kernel), whose weight for it is
 // exp(0) = 1, so every row gets the bits of the decode kernel's chunk
 // partials merged, while no chunk partial leaves the
-// workgroup. A chunk's K rows are staged in LDS for the scores, then its V
-// rows take their place for P*V. Workgroups start longest tile first (the
-// last tiles of a segment have the longest contexts).
+// workgroup. A chunk's K rows are staged in LDS for the scores, then its V,
+// transposed to one 64-token row per dim (pvt_tile reads each value operand
+// whole), takes their place for P*V. Workgroups start longest tile first
+// (the last tiles of a segment have the longest contexts).
 constexpr int kFlashBatch = 64;  // chunks per merge tree (the merge's 64 lanes)
 
 template <int QPK>
@@ -394,7 +391,9 @@ __global__ __launch_bounds__(128 * QPK) Q35_WAVES_PER_EU(2) void attention_flash
   constexpr int kThreads = 128 * QPK;
   constexpr int NP = kChunkTokens * 32 / kThreads;  // 16-byte pieces of a K (or V) chunk per thread
   constexpr int kDimTiles = kHeadDim / 32;          // 16-dim P*V tiles per wavefront
-  __shared__ __align__(16) uint16_t kv[kChunkTokens * kKStride];
+  // a chunk's K rows [token][kKStride], then its V transposed [dim][kVTStride]
+  constexpr int kKVHalfs = kChunkTokens * kKStride > kHeadDim * kVTStride ? kChunkTokens * kKStride : kHeadDim * kVTStride;
+  __shared__ __align__(16) uint16_t kv[kKVHalfs];
   __shared__ __align__(16) float pls[QPK][16 * kPStride];
   __shared__ float tmax[QPK][4][16], tsum[QPK][4][16];
   __shared__ float lwb[QPK][16][kFlashBatch];
@@ -432,7 +431,6 @@ __global__ __launch_bounds__(128 * QPK) Q35_WAVES_PER_EU(2) void attention_flash
   // ahead of its use: a chunk's K during the previous chunk's P*V (pass 2)
   // or scores (pass 1), its V during its own scores.
   const uint16_t *k_col = a.k_pool + static_cast<size_t>(g) * kHeadDim + 8 * (tid & 31);
-  const uint16_t *v_col = a.v_pool + static_cast<size_t>(g) * kHeadDim + 8 * (tid & 31);
   uint16_t *kv_piece = kv + (tid >> 5) * kKStride + 8 * (tid & 31);
   auto piece_token = [&](int i) { return (tid >> 5) + (kThreads >> 5) * i; };
   auto fill_rows = [&](int sp) {  // past the last chunk: its last chunk again
@@ -451,6 +449,37 @@ __global__ __launch_bounds__(128 * QPK) Q35_WAVES_PER_EU(2) void attention_flash
   auto store = [&](const q35_u32x4 raw[NP]) {
 #pragma unroll
     for (int i = 0; i < NP; ++i) *reinterpret_cast<q35_u32x4 *>(kv_piece + (kThreads >> 5) * i * kKStride) = raw[i];
+  };
+  // V goes to LDS transposed: item it (of 512 per chunk) is tokens
+  // 8(it % 8) .. +7 at dims 4(it / 8) .. +3, eight 8-byte loads regrouped in
+  // registers (v_operand's regrouping) into four 16-byte dim-row pieces, so
+  // the eight items of a dim group fill one row's 128 contiguous bytes
+  constexpr int kVItems = kThreads >= 512 ? 1 : 512 / kThreads;
+  const bool v_item = tid < 512;  // 1024-thread workgroups: half the threads
+  auto load_v = [&](int sp, q35_u32x2 vr[kVItems][8]) {
+#pragma unroll
+    for (int s2 = 0; s2 < kVItems; ++s2) {
+      const int it = min(tid + kThreads * s2, 511), tgp = it & 7, dg = it >> 3;
+      const uint16_t *col = a.v_pool + static_cast<size_t>(g) * kHeadDim + 4 * dg;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        vr[s2][i] = *reinterpret_cast<const q35_u32x2 *>(col + static_cast<size_t>(rows_lds[sp & 1][8 * tgp + i]) * kvw);
+    }
+  };
+  auto store_v = [&](const q35_u32x2 vr[kVItems][8]) {
+#pragma unroll
+    for (int s2 = 0; s2 < kVItems; ++s2) {
+      const int it = min(tid + kThreads * s2, 511), tgp = it & 7, dg = it >> 3;
+      if (!v_item) break;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const unsigned sel = (j & 1) ? 0x07060302u : 0x05040100u;
+        q35_u32x4 d;
+#pragma unroll
+        for (int p2 = 0; p2 < 4; ++p2) d[p2] = __builtin_amdgcn_perm(vr[s2][2 * p2 + 1][j >> 1], vr[s2][2 * p2][j >> 1], sel);
+        *reinterpret_cast<q35_u32x4 *>(kv + (4 * dg + j) * kVTStride + 8 * tgp) = d;
+      }
+    }
   };
   // this wavefront's two token tiles of chunk sp (K staged): masked, scaled
   // scores, and each tile's per-row maximum into tmax
@@ -509,10 +538,11 @@ __global__ __launch_bounds__(128 * QPK) Q35_WAVES_PER_EU(2) void attention_flash
   fill_rows(0);
   lds_barrier();
   load(k_col, 0, raw);
+  q35_u32x2 vraw[kVItems][8];  // one chunk's V items in flight
   for (int sp = 0; sp < nch; ++sp) {
     const int t0 = sp * kChunkTokens;
     store(raw);
-    load(v_col, sp, raw);  // this chunk's V, behind its scores
+    load_v(sp, vraw);  // this chunk's V, behind its scores
     fill_rows(sp + 1);
     lds_barrier();
     float sc[2][4], mx[4];
@@ -532,7 +562,7 @@ __global__ __launch_bounds__(128 * QPK) Q35_WAVES_PER_EU(2) void attention_flash
       }
     }
     lds_barrier();  // every wavefront is done with K; p and the tile sums are in
-    store(raw);
+    store_v(vraw);
     lds_barrier();
     load(k_col, sp + 1, raw);  // the next chunk's K, behind this chunk's P*V
     // the chunk's weight in the merge; rows whose context ends before the
@@ -550,7 +580,7 @@ __global__ __launch_bounds__(128 * QPK) Q35_WAVES_PER_EU(2) void attention_flash
     load_p_ops(pl, lane, phi, plo);
 #pragma unroll
     for (int dt = 0; dt < kDimTiles; ++dt) {
-      const q35_f32x4 o = pv_tile(phi, plo, kv, kDimTiles * hf + dt, lane);
+      const q35_f32x4 o = pvt_tile(phi, plo, kv, kDimTiles * hf + dt, lane);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         if (live[j]) acc[dt][j] = fmaf(w[j], o[j], acc[dt][j]);
