@@ -38,7 +38,12 @@ __global__ __launch_bounds__(256) Q35_WAVES_PER_EU(2) void gemm_dense_kernel(Gem
   constexpr int RM = 4;  // rows (MFMAs) per lane: 64-row groups
   typedef RowWords<4> RWv;
   constexpr int kLanesPerTile = 8 / RM, kGroupRows = 16 * RM;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // the wavefront index is read into a scalar register so that every base
+  // below is wave-uniform: the loads are raw buffer loads from wave-uniform
+  // resources with a fixed per-lane voffset and the block's offset in a
+  // scalar register, so the loop holds no per-lane address arithmetic
+  const int wave = q35_uniform(static_cast<int>(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
   const int G = lane >> 4, c = lane & 15;
   const int nwg = static_cast<int>(gridDim.x);  // a multiple of 8
   const int logical = (static_cast<int>(blockIdx.x) & 7) * (nwg >> 3) + (static_cast<int>(blockIdx.x) >> 3);
@@ -49,32 +54,45 @@ __global__ __launch_bounds__(256) Q35_WAVES_PER_EU(2) void gemm_dense_kernel(Gem
   // rows past the matrix read a valid tile (the last); token tiles past the
   // chunk read the last valid tile; neither is stored. Lane c holds rows
   // r0 .. r0+3 of tile rt: per block their 16 code bytes of k-group G and
-  // their four fp16 scales.
-  const int rt = min(g * (kGroupRows / 8) + c / kLanesPerTile, ntiles - 1);
+  // their four fp16 scales, of which it supplies row r0 + G's to the
+  // multipliers' MFMA. (All four k-group lanes of a row pair read the same
+  // 8 scale bytes: loading only the 2 or 4 bytes a lane uses made the
+  // kernel 20% slower.) Every offset is below its resource's extent (the
+  // launcher bounds the extents by 2^31 bytes).
+  const int rt0 = g * (kGroupRows / 8);  // < ntiles: g < ceil(ntiles / 8)
+  const int rt = min(rt0 + c / kLanesPerTile, ntiles - 1);
   const int r0 = RM * (c % kLanesPerTile);
-  const uint8_t *wt = reinterpret_cast<const uint8_t *>(a.w) + static_cast<size_t>(rt) * nb * 144;
-  const uint8_t *qrow = wt + 16 + 32 * G + 4 * r0;
-  const uint8_t *drow = wt + 2 * r0;
-  const uint64_t *ap[NT];
+  const q35_buffer wres = q35_make_buffer(reinterpret_cast<const uint8_t *>(a.w) + static_cast<size_t>(rt0) * nb * 144,
+                                          (ntiles - rt0) * nb * 144);
+  const int woff = (rt - rt0) * nb * 144;
+  const int qoff = woff + 16 + 32 * G + 4 * r0, doff = woff + 2 * r0;
+  const int tile0 = min(tg * NT, tiles - 1);
+  const q35_buffer ares = q35_make_buffer(a.codes + static_cast<size_t>(tile0) * nb * 64, (tiles - tile0) * nb * 512);
+  const q35_buffer sres = q35_make_buffer(a.scales + static_cast<size_t>(tile0) * nb * 16, (tiles - tile0) * nb * 64);
+  int aoff[NT], soff[NT];
 #pragma unroll
-  for (int t = 0; t < NT; ++t) ap[t] = a.codes + static_cast<size_t>(min(tg * NT + t, tiles - 1)) * nb * 64 + lane;
+  for (int t = 0; t < NT; ++t) {
+    const int dt = min(tg * NT + t, tiles - 1) - tile0;
+    aoff[t] = dt * nb * 512 + 8 * lane;
+    soff[t] = dt * nb * 64 + 4 * c;
+  }
+  // v_perm_b32 selector moving the fp16 scale of row r0 + G (bytes 2G, 2G+1
+  // of the tile's four scales) to the low half, zeros above
+  const uint32_t dsel_bytes = 0x0C0C0000u | (static_cast<uint32_t>(2 * G + 1) << 8) | static_cast<uint32_t>(2 * G);
   struct Block {
     typename RWv::Q q;
     typename RWv::D d;
     long act[NT];
     float s1[NT];  // the scale of token lane%16 of each tile
   };
-  const float *s1p[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) s1p[t] = a.scales + static_cast<size_t>(min(tg * NT + t, tiles - 1)) * nb * 16 + (lane & 15);
   auto load = [&](Block &k, int b) {
     b = min(b, nb - 1);
-    k.q = *reinterpret_cast<const typename RWv::Q *>(qrow + static_cast<size_t>(b) * 144);
-    k.d = *reinterpret_cast<const typename RWv::D *>(drow + static_cast<size_t>(b) * 144);
+    k.q = q35_buffer_load16(wres, qoff, b * 144);
+    k.d = q35_buffer_load8(wres, doff, b * 144);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      k.act[t] = static_cast<long>(ap[t][static_cast<size_t>(b) * 64]);
-      k.s1[t] = s1p[t][static_cast<size_t>(b) * 16];
+      k.act[t] = __builtin_bit_cast(long, q35_buffer_load8(ares, aoff[t], b * 512));
+      k.s1[t] = __builtin_bit_cast(float, q35_buffer_load4(sres, soff[t], b * 64));
     }
   };
   float acc[NT][RM][4], tot[NT][RM][4];
@@ -86,13 +104,9 @@ __global__ __launch_bounds__(256) Q35_WAVES_PER_EU(2) void gemm_dense_kernel(Gem
       for (int j = 0; j < 4; ++j) acc[t][r][j] = tot[t][r][j] = 0.0F;
   auto compute = [&](const Block &k) {
     const v4i zero = {0, 0, 0, 0};
-    float dw[RM];
     long wq[RM];
 #pragma unroll
-    for (int r = 0; r < RM; ++r) {
-      dw[r] = half_bits_to_float(RWv::scale(k.d, r));
-      wq[r] = unpack_word(RWv::word(k.q, r));
-    }
+    for (int r = 0; r < RM; ++r) wq[r] = unpack_word(RWv::word(k.q, r));
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const v4i corr = Q35_MFMA_I32_16X16X32_I8(k.act[t], kMinus8, zero, 0, 0, 0);
@@ -103,10 +117,7 @@ __global__ __launch_bounds__(256) Q35_WAVES_PER_EU(2) void gemm_dense_kernel(Gem
         // the multipliers as one outer-product MFMA: element 4r + j is token
         // 4G + j's scale times row 4c + r's (the layout of D[r][j]); lane
         // 16b + n supplies row 4n + b's scale, every lane token lane%16's
-        // (formed branch-free from the packed fp16 pair: a select chain on
-        // G compiles to divergent branches)
-        const uint32_t dpair = (G & 2) != 0 ? k.d[1] : k.d[0];
-        const float dsel = half_bits_to_float(static_cast<uint16_t>(dpair >> (16 * (G & 1))));
+        const float dsel = half_bits_to_float(static_cast<uint16_t>(__builtin_amdgcn_perm(k.d[1], k.d[0], dsel_bytes)));
         q35_f32x16 zero16;
 #pragma unroll
         for (int e = 0; e < 16; ++e) zero16[e] = 0.0F;
@@ -177,11 +188,14 @@ bool gemm_dense_fits(int rows, int tokens, int cu_count) {
 hipError_t launch_gemm_dense(const GemmArgs &a, hipStream_t stream) {
   if (a.tokens <= 0 || a.rows <= 0) return hipSuccess;
   if (a.out == nullptr || a.rows % 8 != 0 || a.stride < a.rows || a.residual != nullptr) return hipErrorInvalidValue;
-  // two token tiles per wavefront (144 VGPRs, three wavefronts per SIMD):
-  // with the multipliers on the matrix pipe four tiles (228 VGPRs, two per
-  // SIMD) no longer measure faster on any 4B shape at 2048 tokens (medians:
-  // gate_up 342 against 344 us, in_proj 232 against 248, out/o 93 against
-  // 119, down 197 against 247), nor do rings of three or four blocks
+  // the kernel addresses the matrix and the activations through buffer
+  // resources with 32-bit extents
+  const long long tiles = (a.tokens + 15) / 16;
+  if (static_cast<long long>(a.rows / 8) * a.nb * 144 >= (1LL << 31) || tiles * a.nb * 512 >= (1LL << 31))
+    return hipErrorInvalidValue;
+  // two token tiles per wavefront (137 VGPRs, three wavefronts per SIMD):
+  // four tiles (217 VGPRs, two per SIMD) measure 5% slower on the config-5
+  // projections, and rings of three or four blocks are no faster either
   const int groups = (a.rows / 8 + 7) / 8;
   const int nt = 2;
   const int S = gemm_dense_splits(a.rows, a.nb, a.cu_count, a.max_split);

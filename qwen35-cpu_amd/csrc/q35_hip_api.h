@@ -99,6 +99,27 @@ __device__ __forceinline__ void q35_compiler_fence() { asm volatile("" ::: "memo
 // it), so the compiler cannot sink the arithmetic that produces it past later
 // loads and keep their results live meanwhile.
 __device__ __forceinline__ void q35_materialize(float &x) { asm volatile("" : "+v"(x)); }
+// A wave-uniform value moved into a scalar register (every lane holds the
+// same value; the compiler then treats what derives from it as uniform).
+__device__ __forceinline__ int q35_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+// Raw (stride 0) buffer resource over [base, base + extent) with a
+// wave-uniform base: a load takes a per-lane byte offset and a wave-uniform
+// one (a scalar register, so per-iteration offsets cost no VALU work); an
+// offset at or past the extent reads 0. Word 3 is gfx9's: 32-bit data
+// format, no swizzle.
+typedef __amdgpu_buffer_rsrc_t q35_buffer;
+__device__ __forceinline__ q35_buffer q35_make_buffer(const void *base, int extent) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, extent, 0x00020000);
+}
+__device__ __forceinline__ q35_u32x4 q35_buffer_load16(q35_buffer r, int voff, int soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+__device__ __forceinline__ q35_u32x2 q35_buffer_load8(q35_buffer r, int voff, int soff) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+}
+__device__ __forceinline__ uint32_t q35_buffer_load4(q35_buffer r, int voff, int soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
 
 // Orders a wavefront's LDS writes before its later LDS reads by other lanes of
 // the same wavefront. The LDS executes one wavefront's instructions in order,

@@ -219,14 +219,16 @@ inline unsigned long long atomicMax(unsigned long long *p, unsigned long long v)
 inline unsigned __float_as_uint(float f) { unsigned u; std::memcpy(&u, &f, 4); return u; }
 inline int __builtin_amdgcn_readlane(int v, int src) { return ::q35emu::readlane(v, src); }
 // v_perm_b32: byte i of the result is byte sel.byte[i] of the eight bytes
-// {s1 (bytes 0-3), s0 (bytes 4-7)}; selectors 8 and up are not used here
+// {s1 (bytes 0-3), s0 (bytes 4-7)}; selector 12 gives 0x00 and 13 and up
+// 0xFF; the sign-replicating selectors 8-11 are not used here
 inline unsigned __builtin_amdgcn_perm(unsigned s0, unsigned s1, unsigned sel) {
   const unsigned long long both = (static_cast<unsigned long long>(s0) << 32) | s1;
   unsigned r = 0;
   for (int i = 0; i < 4; ++i) {
     const unsigned b = (sel >> (8 * i)) & 0xFFu;
-    if (b > 7) std::abort();
-    r |= static_cast<unsigned>((both >> (8 * b)) & 0xFFu) << (8 * i);
+    if (b >= 8 && b <= 11) std::abort();
+    const unsigned byte = b < 8 ? static_cast<unsigned>((both >> (8 * b)) & 0xFFu) : (b == 12 ? 0u : 0xFFu);
+    r |= byte << (8 * i);
   }
   return r;
 }
@@ -289,6 +291,27 @@ typedef float q35_f32x2 __attribute__((vector_size(8)));
 // binary16 values per lane; each output is C plus the 32 products summed in
 // k order in fp32 (the hardware's internal order differs; every use here is
 // compared across paths of this same emulation or against a tolerance)
+// Buffer resources: the extent is checked on every load (the kernels never
+// read past it, so a load that would is a bug, not the hardware's zero read).
+inline int q35_uniform(int v) { return v; }
+struct q35_buffer {
+  const uint8_t *base;
+  int extent;
+};
+inline q35_buffer q35_make_buffer(const void *base, int extent) {
+  return q35_buffer{static_cast<const uint8_t *>(base), extent};
+}
+template <typename T>
+inline T q35emu_buffer_load(q35_buffer r, int voff, int soff) {
+  const long long off = static_cast<long long>(voff) + soff;
+  if (voff < 0 || soff < 0 || off + static_cast<long long>(sizeof(T)) > r.extent) std::abort();
+  T v;
+  std::memcpy(&v, r.base + off, sizeof(T));
+  return v;
+}
+inline q35_u32x4 q35_buffer_load16(q35_buffer r, int voff, int soff) { return q35emu_buffer_load<q35_u32x4>(r, voff, soff); }
+inline q35_u32x2 q35_buffer_load8(q35_buffer r, int voff, int soff) { return q35emu_buffer_load<q35_u32x2>(r, voff, soff); }
+inline uint32_t q35_buffer_load4(q35_buffer r, int voff, int soff) { return q35emu_buffer_load<uint32_t>(r, voff, soff); }
 typedef uint16_t q35_f16x8 __attribute__((vector_size(16)));
 inline q35_f16x8 q35_f16x8_bits(q35_u32x4 raw) {
   q35_f16x8 r;

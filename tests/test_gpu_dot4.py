@@ -194,7 +194,7 @@ def test_dense_matches_split_launches(q, ctx, orc, rows, blocks, vectors):
     64-row group in one wavefront, the split structure folded in registers);
     its rows must equal the 64-vector split launches bit for bit, here with
     32, 4 and 14 K splits, a ragged row group and ragged token groups; 16392
-    rows run the four-tile form of tall matrices."""
+    rows give a tall matrix whose last 64-row group holds one 8-row tile."""
     rng = np.random.default_rng(rows + vectors)
     packed, x = _problem(orc, rng, rows, blocks * 32, vectors)
     act = orc.h128_prepare_4(x)
