@@ -228,8 +228,10 @@ __device__ __forceinline__ q35_f16x8 v_operand(const VOps &v, int ks, int j) {
 // value operands loaded straight into registers (VOps). The loads are issued
 // queries (staged in LDS), keys, values, so the scores and the softmax run
 // while the values are still in flight. Occupancy floor 2 keeps the MFMA
-// results in VGPRs.
-template <int QPK>
+// results in VGPRs. GROUPS: pages hold whole 8-token groups (8 or more
+// tokens per page), so one page-table entry serves a lane's 8 value tokens
+// (2 entry loads per thread instead of 16).
+template <int QPK, bool GROUPS>
 __global__ __launch_bounds__(256) Q35_WAVES_PER_EU(2) void attention_kernel(AttnArgs a) {
   constexpr int kQStride = kHeadDim + 4;  // floats per staged query row (rows start on different banks)
   __shared__ __align__(16) float qs[QPK * kQStride];
@@ -262,12 +264,13 @@ __global__ __launch_bounds__(256) Q35_WAVES_PER_EU(2) void attention_kernel(Attn
   const int seq = a.seq_lens != nullptr ? a.seq_lens[r] : a.positions[r] + 1;
   const int pfirst = pt[min(t0 >> pshift, last_page)];
   const int pk = pt[min((t0 + kt) >> pshift, last_page)];
-  const int istep = pshift >= 3 ? 0 : 1;
+  constexpr int istep = GROUPS ? 0 : 1;
   int pv[2][8];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) pv[ks][i] = pt[min((t0 + 32 * ks + 8 * tg + i * istep) >> pshift, last_page)];
+    for (int i = 0; i < 8; ++i)
+      pv[ks][i] = (GROUPS && i > 0) ? pv[ks][0] : pt[min((t0 + 32 * ks + 8 * tg + i * istep) >> pshift, last_page)];
   // the page-table loads go out before the context length is waited for
   // (otherwise the compiler sinks them below the early return)
   q35_compiler_fence();
@@ -774,7 +777,10 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
 #define Q35_ATTN(Q)                                                                                    \
   if (tiled && a.tiles > 0)                                                                            \
     Q35_LAUNCH((attention_flash_kernel<Q>), dim3(a.tiles, a.kv_heads), dim3(128 * (Q)), 0, stream, a); \
-  if (decode_rows > 0) Q35_LAUNCH((attention_kernel<Q>), dim3(gs, a.kv_heads, decode_rows), dim3(256), 0, stream, a);
+  if (decode_rows > 0 && a.page_tokens >= 8)                                                          \
+    Q35_LAUNCH((attention_kernel<Q, true>), dim3(gs, a.kv_heads, decode_rows), dim3(256), 0, stream, a); \
+  else if (decode_rows > 0)                                                                            \
+    Q35_LAUNCH((attention_kernel<Q, false>), dim3(gs, a.kv_heads, decode_rows), dim3(256), 0, stream, a);
   switch (qpk) {
     case 1: Q35_ATTN(1) break;
     case 2: Q35_ATTN(2) break;
