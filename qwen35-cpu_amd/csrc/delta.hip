@@ -354,9 +354,19 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_chunk_inputs_kernel(Delta
   const float dtb = a.dt_bias[vh];
   const float sa_ = a.ssm_a[vh];
   // every token's loads first (their index chains and inputs do not depend on
-  // one another, so they are in flight together), then the arithmetic
+  // one another, so they are in flight together), then the arithmetic. Lane
+  // t < nt of wave 0 computes token t's gates (beta, alpha): every lane loads
+  // the b and a inputs of token min(lane, nt - 1), so no load sits under a
+  // branch, and the nt gate computations run side by side instead of one
+  // after another on one lane
+  const int gy = y0 + min(lane, nt - 1);
+  const int gr = a.chunk_rows != nullptr ? a.chunk_rows[gy] : gy;
+  const float *grow = a.proj.p + static_cast<long long>(gr) * a.proj.width;
+  const float gb = a.gates != nullptr ? a.gates[static_cast<size_t>(gr) * 2 * a.v_heads + vh] : grow[channels + v_dim + vh];
+  const float ga = a.gates != nullptr ? a.gates[static_cast<size_t>(gr) * 2 * a.v_heads + a.v_heads + vh]
+                                      : grow[channels + v_dim + a.v_heads + vh];
   int rr[kInTokens];
-  float xq[kInTokens], xv[kInTokens], bval[kInTokens], aval[kInTokens];
+  float xq[kInTokens], xv[kInTokens];
   float hq[kInTokens][K - 1], hv[kInTokens][K - 1];
 #pragma unroll
   for (int t = 0; t < kInTokens; ++t) {
@@ -371,9 +381,6 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_chunk_inputs_kernel(Delta
     const float *row = a.proj.p + static_cast<long long>(r) * a.proj.width;
     xq[t] = row[chq];
     xv[t] = row[chv];
-    bval[t] = a.gates != nullptr ? a.gates[static_cast<size_t>(r) * 2 * a.v_heads + vh] : row[channels + v_dim + vh];
-    aval[t] = a.gates != nullptr ? a.gates[static_cast<size_t>(r) * 2 * a.v_heads + a.v_heads + vh]
-                                 : row[channels + v_dim + a.v_heads + vh];
 #pragma unroll
     for (int k = 0; k < K - 1; ++k) {
       const int p = pos - (K - 1) + k;  // oldest first
@@ -401,14 +408,15 @@ __global__ __launch_bounds__(kDeltaThreads) void delta_chunk_inputs_kernel(Delta
     v = silu_times(v, 1.0F);
     yq[t] = q;
     float *e = a.scan + (static_cast<size_t>(rr[t]) * a.v_heads + vh) * kDeltaScanStride;
-    if (tid == 0) {
-      e[3 * kDim + 1] = sigmoid_stable(bval[t]);
-      const float pre = softplus_stable(aval[t] + dtb);
-      e[3 * kDim] = expf(pre * sa_);
-    }
     const float ss = wave_sum(q * q);
     if (lane == 0) red[t][wave] = ss;
     if (has_v) e[2 * kDim + tid] = v;
+  }
+  if (tid < nt) {
+    float *e = a.scan + (static_cast<size_t>(gr) * a.v_heads + vh) * kDeltaScanStride;
+    e[3 * kDim + 1] = sigmoid_stable(gb);
+    const float pre = softplus_stable(ga + dtb);
+    e[3 * kDim] = expf(pre * sa_);
   }
   lds_barrier();
   const float scale = is_k ? 1.0F : 1.0F / sqrtf(static_cast<float>(kDim));
