@@ -119,12 +119,12 @@ __global__ __launch_bounds__(kRmsThreads) void rms_prep_kernel(RmsPrepArgs a) {
   const q35_f32x4 *xin = reinterpret_cast<const q35_f32x4 *>(a.x_in + xr * K);
   int token = 0;
   if constexpr (EMBED) token = a.token_ids[t];
-  for (int i = tid; i < n4; i += kRmsThreads) {
-    q35_f32x4 v;
+  // columns 4i..4i+3 of the row (i = tid + kRmsThreads * it): the input
+  // (the residual row, or the token's embedding run) and the split rows to add
+  auto load = [&](int i, q35_f32x4 &v, q35_f32x4 x[MS > 0 ? MS : 1]) {
     if constexpr (EMBED) {
-      // columns 4i..4i+3 of the token's row: one 4-byte run of the tile's
-      // DOT4 codes (the same nibble half) and the row's binary16 scale,
-      // x = half(d) * (u - 8) as embed_kernel forms it
+      // one 4-byte run of the tile's DOT4 codes (the same nibble half) and
+      // the row's binary16 scale, x = half(d) * (u - 8) as embed_kernel forms it
       const int k = 4 * i, b = k >> 5, kk = k & 31, rt = token >> 3, row = token & 7;
       const uint8_t *tile;
       uint16_t dh;
@@ -142,29 +142,56 @@ __global__ __launch_bounds__(kRmsThreads) void rms_prep_kernel(RmsPrepArgs a) {
       const float d = half_bits_to_float(dh);
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = d * static_cast<float>(static_cast<int>((q4 >> (8 * e + sh)) & 15u) - 8);
-      reinterpret_cast<q35_f32x4 *>(a.x_out + xr * K)[i] = v;
     } else {
       v = xin[i];
     }
     if constexpr (MS > 0) {
-      // columns 4i..4i+3 of every split, all loads in flight together
+      // every split, all loads in flight together
       const float *pp = a.add.p + xr * a.add.width + 4 * i;
-      q35_f32x4 x[MS];
 #pragma unroll
       for (int u = 0; u < MS; ++u)
         x[u] = *reinterpret_cast<const q35_f32x4 *>(pp + static_cast<long long>(min(u, a.add.splits - 1)) *
                                                              a.add.split_stride);
+    }
+  };
+  auto use = [&](int i, q35_f32x4 v, const q35_f32x4 x[MS > 0 ? MS : 1]) {
+    if constexpr (MS > 0) {
       q35_f32x4 sum = x[0];
 #pragma unroll
       for (int u = 1; u < MS; ++u)
         if (u < a.add.splits) sum += x[u];
       v += sum;
-      reinterpret_cast<q35_f32x4 *>(a.x_out + xr * K)[i] = v;
     }
+    if constexpr (EMBED || MS > 0) reinterpret_cast<q35_f32x4 *>(a.x_out + xr * K)[i] = v;
     *reinterpret_cast<q35_f32x4 *>(&y[4 * i]) = v;
     // K % 128 == 0: the four lanes of a group run the same iterations
     const float gs = sq_group16_quad(v);
     if ((tid & 3) == 0) gsq[i >> 2] = gs;
+  };
+  if constexpr (MS <= 4) {
+    // every iteration's loads first (rows up to kRmsMaxK wide), then the sums:
+    // one round trip for the whole row
+    constexpr int kIters = kRmsMaxK / 4 / kRmsThreads;
+    q35_f32x4 v[kIters], x[kIters][MS > 0 ? MS : 1];
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {
+      if (it * kRmsThreads >= n4) break;  // uniform
+      load(min(tid + it * kRmsThreads, n4 - 1), v[it], x[it]);
+    }
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {
+      const int i = tid + it * kRmsThreads;
+      if (it * kRmsThreads >= n4) break;  // uniform
+      // past the row: whole runs of 32 threads (n4 is a multiple of 32), so
+      // the four lanes of a group agree
+      if (i < n4) use(i, v[it], x[it]);
+    }
+  } else {
+    for (int i = tid; i < n4; i += kRmsThreads) {
+      q35_f32x4 v, x[MS > 0 ? MS : 1];
+      load(i, v, x);
+      use(i, v, x);
+    }
   }
   if constexpr (EMBED) {
     if (tid == 0 && a.counts != nullptr && a.count_input != nullptr && a.count_input[t])
