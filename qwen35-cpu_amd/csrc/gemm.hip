@@ -766,7 +766,16 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t stream) {
       // of token tiles that fit, all at one grid so that the candidate rows
       // (G16 argmax) line up with gemm_argmax_cands
       const int fit = head_fit_tiles(a.nb);
-      if (fit < 1) return hipErrorInvalidValue;
+      if (fit < 1) {
+        // rows too wide for even one staged token tile (more than 113 K
+        // blocks): the logits head runs the exact-mode GEMM, one wavefront
+        // per row group over all K blocks -- the same single block-order
+        // chain per output. G16 has no other kernel.
+        if (a.g16) return hipErrorInvalidValue;
+        GemmArgs c = a;
+        c.exact = true;
+        return launch_gemm(c, stream);
+      }
       const int gpw = head_plan(a.rows, a.nb, 16 * fit, a.cu_count, a.force_gpw).gpw;
       for (int t0 = 0; t0 < a.tokens; t0 += 16 * fit) {
         GemmArgs c = a;

@@ -119,6 +119,37 @@ def test_chunked_prefill_past_64_context_chunks(q, ctx, small):
     _chunked_equals_single_steps(q, small, [2048, 2100], max_step_rows=2112)
 
 
+@pytest.fixture(scope="module")
+def wide(q, ctx):
+    """Two layers (one of each kind) at 4096 hidden columns, the widest row the
+    norm kernels take."""
+    d, _ = small_dims()
+    d = dict(d, n_layers=2, hidden=4096)
+    sched = np.array([1, 0], np.uint8)
+    tensors = build_small_model(d, sched, seed=29)
+    model = upload_model(q, ctx, d, sched, tensors)
+    yield d, sched, tensors, model
+    model.close()
+
+
+def test_wide_rows_greedy_and_chunked(q, ctx, orc, wide):
+    """At 4096 hidden columns each residual update + RMSNorm + H128 pass loads
+    its row as four column batches per thread before any sum: greedy tokens
+    and first-step logits within the oracle's own envelope (a wrong batch
+    would move whole rows), and chunked prefill equal to single steps."""
+    d, sched, tensors, model = wide
+    prompts = np.random.default_rng(3).integers(0, d["vocab"], size=(3, 12)).astype(np.int32)
+    print("wide rows: oracle", flush=True)
+    want_lg, want, env_max, env_mean = oracle_envelope(d, sched, tensors, prompts, 4)
+    print(f"wide rows: envelope max {env_max:.4f} mean {env_mean:.5f}; HIP", flush=True)
+    got, got_lg = hip_greedy(q, ctx, d, sched, tensors, prompts, 4, want_logits=True, model=model)
+    diff = np.abs(got_lg[:, 0] - want_lg[:, 0])
+    print(f"wide rows: HIP vs oracle max {diff.max():.4f} mean {diff.mean():.5f}", flush=True)
+    assert diff.max() <= 1.5 * env_max + 1e-3 and diff.mean() <= 1.5 * env_mean + 1e-4
+    tokens_agree(got, want, want_lg, env_max)
+    _chunked_equals_single_steps(q, wide, [20, 12], max_step_rows=0)
+
+
 def _chunked_equals_single_steps(q, small, chunks, max_step_rows):
     d, sched, tensors, model = small
     plen, new, page_tokens = sum(chunks), 5, 16
