@@ -120,8 +120,9 @@ __global__ __launch_bounds__(64 * kNormWaves) void gemm_norm_kernel(NormGemmArgs
 #pragma unroll
   for (int i = 0; i < BPS; ++i) {
     const size_t b = static_cast<size_t>(min(b0 + i, bl));
-    q[i] = *reinterpret_cast<const typename RW::Q *>(qrow + b * 144);
-    d[i] = *reinterpret_cast<const typename RW::D *>(drow + b * 144);
+    // streamed: read once per step (gemm_rows_kernel's reason)
+    q[i] = Q35_LOAD_NT(reinterpret_cast<const typename RW::Q *>(qrow + b * 144));
+    d[i] = Q35_LOAD_NT(reinterpret_cast<const typename RW::D *>(drow + b * 144));
   }
 
   // 2. the rows' sums of squares (norm_total_groups' tree)
@@ -251,8 +252,9 @@ __global__ __launch_bounds__(64 * MAXW) void gemm_resid_kernel(ResidGemmArgs a) 
 #pragma unroll
     for (int i = 0; i < BPS; ++i) {
       const size_t b = static_cast<size_t>(min(b0 + i, bl));
-      q[i] = *reinterpret_cast<const RW::Q *>(qrow + b * 144);
-      d[i] = *reinterpret_cast<const RW::D *>(drow + b * 144);
+      // streamed: read once per step (gemm_rows_kernel's reason)
+      q[i] = Q35_LOAD_NT(reinterpret_cast<const RW::Q *>(qrow + b * 144));
+      d[i] = Q35_LOAD_NT(reinterpret_cast<const RW::D *>(drow + b * 144));
       act[i] = static_cast<long>(acodes[b * 64]);
     }
   };

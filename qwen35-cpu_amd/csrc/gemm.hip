@@ -306,8 +306,11 @@ __global__ __launch_bounds__(64) Q35_WAVES_PER_EU(2) void gemm_rows_kernel(GemmA
 #pragma unroll
     for (int i = 0; i < KS; ++i) {
       const size_t b = static_cast<size_t>(min(cb + i, bl));
-      q[i] = *reinterpret_cast<const typename RW::Q *>(qrow + b * 144);
-      d[i] = *reinterpret_cast<const typename RW::D *>(drow + b * 144);
+      // read once per step: streamed (non-temporal), so that they do not
+      // evict the vocabulary head's weights from the Infinity Cache between
+      // steps (the head then reads much of its 143 MB from there)
+      q[i] = Q35_LOAD_NT(reinterpret_cast<const typename RW::Q *>(qrow + b * 144));
+      d[i] = Q35_LOAD_NT(reinterpret_cast<const typename RW::D *>(drow + b * 144));
       act[i] = static_cast<long>(acodes[b * 64]);
       sa[i] = *reinterpret_cast<const q35_f32x4 *>(ascale + b * 16);
     }
