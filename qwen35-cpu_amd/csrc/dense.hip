@@ -182,7 +182,7 @@ int gemm_dense_splits(int rows, int nb, int cu_count, int max_split) {
 
 bool gemm_dense_fits(int rows, int tokens, int cu_count) {
   const long long waves = static_cast<long long>((rows / 8 + 7) / 8) * ((tokens + 31) / 32);  // two-tile units
-  return tokens > kMaxTokens && waves >= 2LL * (cu_count > 0 ? cu_count : 256);
+  return tokens >= kMaxTokens && waves >= 2LL * (cu_count > 0 ? cu_count : 256);
 }
 
 hipError_t launch_gemm_dense(const GemmArgs &a, hipStream_t stream) {
@@ -195,14 +195,20 @@ hipError_t launch_gemm_dense(const GemmArgs &a, hipStream_t stream) {
     return hipErrorInvalidValue;
   // two token tiles per wavefront (137 VGPRs, three wavefronts per SIMD):
   // four tiles (217 VGPRs, two per SIMD) measure 5% slower on the config-5
-  // projections, and rings of three or four blocks are no faster either
+  // projections, and rings of three or four blocks are no faster either. At
+  // one split launch's rows (64) each wavefront takes one tile: twice the
+  // wavefronts for a grid that would leave most SIMDs with none (the 4B
+  // gate_up at 64 rows: 1152 instead of 576)
   const int groups = (a.rows / 8 + 7) / 8;
-  const int nt = 2;
+  const int nt = a.tokens <= kMaxTokens ? 1 : 2;
   const int S = gemm_dense_splits(a.rows, a.nb, a.cu_count, a.max_split);
   const int token_groups = (a.tokens + 16 * nt - 1) / (16 * nt);
   const int units = groups * token_groups;
   const int wgs = ((units + 3) / 4 + 7) / 8 * 8;
-  Q35_LAUNCH((gemm_dense_kernel<2, 2>), dim3(wgs), dim3(256), 0, stream, a, S, token_groups, units);
+  if (nt == 1)
+    Q35_LAUNCH((gemm_dense_kernel<1, 2>), dim3(wgs), dim3(256), 0, stream, a, S, token_groups, units);
+  else
+    Q35_LAUNCH((gemm_dense_kernel<2, 2>), dim3(wgs), dim3(256), 0, stream, a, S, token_groups, units);
   return hipGetLastError();
 }
 
