@@ -188,13 +188,15 @@ def test_argmax_head_shapes(q, ctx, orc, rows, cols, vectors):
 
 
 @pytest.mark.parametrize("rows,blocks,vectors", [(2560, 288, 300), (3584, 32, 512), (200, 112, 132), (1032, 80, 68),
-                                                  (16392, 40, 100)])
+                                                  (16392, 40, 100), (200, 8, 4136)])
 def test_dense_matches_split_launches(q, ctx, orc, rows, blocks, vectors):
     """Above 64 vectors q4_dot4_matmul runs the dense GEMM (every K block of a
     64-row group in one wavefront, the split structure folded in registers);
     its rows must equal the 64-vector split launches bit for bit, here with
     32, 4 and 14 K splits, a ragged row group and ragged token groups; 16392
-    rows give a tall matrix whose last 64-row group holds one 8-row tile."""
+    rows give a tall matrix whose last 64-row group holds one 8-row tile.
+    4136 vectors are a 4096-vector chunk and a 40-vector one, which the dense
+    GEMM runs with one token tile per wavefront (its form at 64 rows)."""
     rng = np.random.default_rng(rows + vectors)
     packed, x = _problem(orc, rng, rows, blocks * 32, vectors)
     act = orc.h128_prepare_4(x)
