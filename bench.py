@@ -722,6 +722,8 @@ def main():
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--profile-steps", type=int, default=16, help="decode forwards in the profiled region")
+    ap.add_argument("--timing-steps", type=int, default=16,
+                    help="decode forwards after the timed region whose graph replays are bracketed by HIP events")
     ap.add_argument("--cpu-baseline", choices=("on", "off"), default="on")
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="0 = one per physical core of the allowed CPUs, at most 16 (the box's CPU share)")
@@ -744,8 +746,8 @@ def main():
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               f"(asked for --gpus {args.gpus}, WORLD_SIZE {world})", file=sys.stderr)
         sys.exit(2)
-    if args.steps <= 0 or args.warmup < 0 or args.batch <= 0 or args.profile_steps < 0:
-        ap.error("steps must be positive and warmup/profile-steps non-negative")
+    if args.steps <= 0 or args.warmup < 0 or args.batch <= 0 or args.profile_steps < 0 or args.timing_steps < 0:
+        ap.error("steps must be positive and warmup/profile-steps/timing-steps non-negative")
 
     import __graft_entry__ as entry
 
@@ -772,7 +774,7 @@ def main():
     t = time.time()
     model = q.Model(ctx, d, sched, artifact=artifact)
     log(f"model resident in HBM in {time.time() - t:.1f}s")
-    total_new = 1 + args.warmup + args.steps + args.profile_steps
+    total_new = 1 + args.warmup + args.steps + args.timing_steps + args.profile_steps
     engine = q.Engine(model, max_resident_requests=args.batch, max_context=args.prompt + total_new + 16,
                       max_decode_batch_size=args.batch, prefill_chunk_size=128, page_tokens=16, use_graphs=args.graphs == "on")
     rng = np.random.default_rng(20261201)
@@ -793,6 +795,28 @@ def main():
     tok_s = args.batch * args.steps / elapsed
     log(f"timed {args.steps} decode forwards: {elapsed * 1000 / args.steps:.3f} ms/step, {tok_s:.0f} tok/s")
 
+    # the GPU time of the replayed step itself: each graph launch between two
+    # HIP events (outside the timed region; the wall time of the same steps
+    # beside it gives the host's share)
+    step_gpu = None
+    if args.timing_steps:
+        engine.set_step_timing(True)
+        t1 = time.perf_counter()
+        for _ in range(args.timing_steps):
+            engine.advance_batch(ids)
+        ctx.synchronize()
+        wall_ms = (time.perf_counter() - t1) * 1000.0
+        gpu_ms, n = engine.step_timing()
+        engine.set_step_timing(False)
+        if n != args.timing_steps:
+            raise SystemExit(f"step timing counted {n} of {args.timing_steps} steps")
+        step_gpu = {"gpu_us_per_step": round(gpu_ms / n * 1000.0, 1), "wall_us_per_step": round(wall_ms / n * 1000.0, 1),
+                    "host_us_per_step": round((wall_ms - gpu_ms) / n * 1000.0, 1), "steps": n,
+                    "graphs": args.graphs == "on",
+                    "source": "q35_runtime_set_step_timing: HIP events around each step's graph launch on its stream"}
+        log(f"step timing: {step_gpu['gpu_us_per_step']} us of GPU time in {step_gpu['wall_us_per_step']} us per "
+            f"step ({args.timing_steps} steps)")
+
     prof = {}
     if args.profile_steps:
         engine.profile_reset()
@@ -811,7 +835,7 @@ def main():
 
     for rid in ids:
         res, toks = engine.result(rid)
-        if toks.size != 1 + args.warmup + args.steps + args.profile_steps:
+        if toks.size != 1 + args.warmup + args.steps + args.timing_steps + args.profile_steps:
             raise SystemExit(f"request {rid} produced {toks.size} tokens")
     engine.close()
     model.close()
@@ -857,7 +881,7 @@ def main():
         "config": {"workload": "random-init Qwen3.5-0.8B-shaped hybrid, batched greedy decode",
                    "batch": args.batch, "prompt_tokens": args.prompt, "encodings": args.encodings,
                    "decode_forwards_timed": args.steps, "graphs": args.graphs == "on"},
-        "roofline": roof, "head_roofline": head_roof, "step_kernel_breakdown": breakdown,
+        "roofline": roof, "head_roofline": head_roof, "step_kernel_breakdown": breakdown, "step_gpu": step_gpu,
         "cpu_baseline": base,
     }
     if base:

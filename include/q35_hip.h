@@ -447,6 +447,18 @@ int q35_runtime_profile_reset(q35_runtime *rt);
 int q35_runtime_profile_read(q35_runtime *rt, int kernel_class, double *total_ms,
                              uint64_t *launches, double *algorithmic_bytes);
 
+/* Step timing, no reference counterpart (the reference reports request-level
+ * prefill_ms/decode_ms only, cpu_engine.h:147). While enabled, each step's
+ * launch -- the graph replay, or the eager launches when graphs are off -- is
+ * bracketed by a pair of HIP events on the runtime's stream; their elapsed
+ * time and a step count accumulate until the next q35_runtime_set_step_timing.
+ * Unlike q35_runtime_set_profiling it leaves the graphs in place, so it gives
+ * the GPU time of the path the engine runs; a caller's wall time per step
+ * minus it is the step's host share. Each timed step waits for its end event
+ * before returning (it does anyway). */
+int q35_runtime_set_step_timing(q35_runtime *rt, int enable);
+int q35_runtime_step_timing_read(q35_runtime *rt, double *gpu_ms, uint64_t *steps);
+
 /* Stage trace of the decode step (no reference counterpart: a test hook for
  * stage-wise parity). While enabled, q35_runtime_step launches eagerly and,
  * for every layer, keeps a device copy of each stage's input and output --

@@ -219,6 +219,8 @@ _SIGS = {
     "q35_runtime_trace_read": (c_int, [P, c_int, c_int, P, c_size_t, POINTER(c_size_t)]),
     "q35_runtime_profile_reset": (c_int, [P]),
     "q35_runtime_profile_read": (c_int, [P, c_int, POINTER(c_double), POINTER(c_uint64), POINTER(c_double)]),
+    "q35_runtime_set_step_timing": (c_int, [P, c_int]),
+    "q35_runtime_step_timing_read": (c_int, [P, POINTER(c_double), POINTER(c_uint64)]),
     "q35_engine_create": (c_int, [P, POINTER(EngineConfig), POINTER(P)]),
     "q35_engine_destroy": (None, [P]),
     "q35_engine_submit": (c_int, [P, P, c_size_t, c_size_t, c_float, P, c_size_t, POINTER(c_uint64)]),
@@ -510,7 +512,8 @@ class Model:
 
 class _Profiled:
     """Kernel-level timing of the decode step (q35_runtime_set_profiling):
-    eager launches, each bracketed by HIP events on the runtime's stream."""
+    eager launches, each bracketed by HIP events on the runtime's stream; and
+    step timing (q35_runtime_set_step_timing) of the replayed graphs."""
 
     def _rt(self):
         raise NotImplementedError
@@ -520,6 +523,18 @@ class _Profiled:
 
     def profile_reset(self):
         self.ctx.check(lib.q35_runtime_profile_reset(self._rt()), "profile reset")
+
+    def set_step_timing(self, enable=True):
+        """Step timing (q35_runtime_set_step_timing): each step's launch -- the
+        graph replay itself -- between two HIP events; restarts the totals."""
+        self.ctx.check(lib.q35_runtime_set_step_timing(self._rt(), int(enable)), "set step timing")
+
+    def step_timing(self):
+        """(GPU ms summed over the timed steps, step count)."""
+        ms, n = c_double(), c_uint64()
+        self.ctx.check(lib.q35_runtime_step_timing_read(self._rt(), ctypes.byref(ms), ctypes.byref(n)),
+                       "step timing read")
+        return ms.value, n.value
 
     def profile(self):
         """{class: (total_ms, launches, algorithmic_bytes)}."""

@@ -131,6 +131,12 @@ struct q35_runtime {
   double prof_ms[Q35_KERNEL_CLASSES] = {};
   double prof_bytes[Q35_KERNEL_CLASSES] = {};
   uint64_t prof_launches[Q35_KERNEL_CLASSES] = {};
+  // step timing: one event pair around each step's launch (graphs still
+  // replayed) and the accumulated GPU time
+  bool step_timing = false;
+  hipEvent_t step_events[2] = {nullptr, nullptr};
+  double step_gpu_ms = 0.0;
+  uint64_t step_count = 0;
 };
 
 namespace q35 {

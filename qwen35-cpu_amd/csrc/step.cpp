@@ -528,6 +528,8 @@ extern "C" void q35_runtime_destroy(q35_runtime *rt) {
   (void)hipStreamSynchronize(rt->ctx->stream);
   for (auto &kv : rt->graphs) (void)hipGraphExecDestroy(kv.second);
   for (auto &ev : rt->prof_events) (void)hipEventDestroy(ev.first), (void)hipEventDestroy(ev.second);
+  for (hipEvent_t ev : rt->step_events)
+    if (ev != nullptr) (void)hipEventDestroy(ev);
   for (void *p : rt->allocations) (void)hipFree(p);
   for (auto &kv : rt->trace) (void)hipFree(kv.second.first);
   if (rt->meta_host) (void)hipHostFree(rt->meta_host);
@@ -1429,7 +1431,7 @@ int ensure_logits(q35_runtime *rt) {
 
 // Runs the packed step: replays (or captures) the graph of its shape, or
 // launches eagerly (profiling and the stage trace time or copy single launches).
-int launch_step(q35_runtime *rt, const StepShape &sh, bool want_logits) {
+int launch_step_work(q35_runtime *rt, const StepShape &sh, bool want_logits) {
   Context *ctx = rt->ctx;
   int st = Q35_OK;
   if (rt->cfg.use_graphs && !rt->profiling && !rt->tracing) {
@@ -1459,11 +1461,32 @@ int launch_step(q35_runtime *rt, const StepShape &sh, bool want_logits) {
       if (ie != hipSuccess) return hip_error(ctx, ie, "graph instantiate");
       it = rt->graphs.emplace(key, exec).first;
     }
+    if (rt->step_timing) Q35_HIP_TRY(ctx, hipEventRecord(rt->step_events[0], ctx->stream));
     Q35_HIP_TRY(ctx, hipGraphLaunch(it->second, ctx->stream));
   } else {
+    if (rt->step_timing) Q35_HIP_TRY(ctx, hipEventRecord(rt->step_events[0], ctx->stream));
     st = runtime_enqueue_step(rt, sh, want_logits);
     if (st != Q35_OK) return st;
   }
+  return Q35_OK;
+}
+
+// The step's launch, with step timing: an event pair on the stream around it
+// (the graph replay, or the eager launches; a graph's capture, on the host,
+// comes before the first event), waited on and added up at once.
+int launch_step(q35_runtime *rt, const StepShape &sh, bool want_logits) {
+  if (!rt->step_timing) return launch_step_work(rt, sh, want_logits);
+  Context *ctx = rt->ctx;
+  for (hipEvent_t &ev : rt->step_events)
+    if (ev == nullptr) Q35_HIP_TRY(ctx, hipEventCreate(&ev));
+  const int st = launch_step_work(rt, sh, want_logits);
+  if (st != Q35_OK) return st;
+  Q35_HIP_TRY(ctx, hipEventRecord(rt->step_events[1], ctx->stream));
+  Q35_HIP_TRY(ctx, hipEventSynchronize(rt->step_events[1]));
+  float ms = 0.0F;
+  Q35_HIP_TRY(ctx, hipEventElapsedTime(&ms, rt->step_events[0], rt->step_events[1]));
+  rt->step_gpu_ms += ms;
+  ++rt->step_count;
   return Q35_OK;
 }
 
@@ -1658,6 +1681,21 @@ extern "C" int q35_runtime_profile_read(q35_runtime *rt, int cls, double *total_
   if (total_ms) *total_ms = rt->prof_ms[cls];
   if (launches) *launches = rt->prof_launches[cls];
   if (bytes) *bytes = rt->prof_bytes[cls];
+  return Q35_OK;
+}
+
+extern "C" int q35_runtime_set_step_timing(q35_runtime *rt, int enable) {
+  if (rt == nullptr) return Q35_ERR_INVALID;
+  rt->step_timing = enable != 0;
+  rt->step_gpu_ms = 0.0;
+  rt->step_count = 0;
+  return Q35_OK;
+}
+
+extern "C" int q35_runtime_step_timing_read(q35_runtime *rt, double *gpu_ms, uint64_t *steps) {
+  if (rt == nullptr) return Q35_ERR_INVALID;
+  if (gpu_ms) *gpu_ms = rt->step_gpu_ms;
+  if (steps) *steps = rt->step_count;
   return Q35_OK;
 }
 

@@ -50,6 +50,35 @@ def test_prefill_batch_then_advance_batch(q, small):
     eng.close()
 
 
+def test_step_timing_keeps_graph_steps(q, small):
+    """q35_runtime_set_step_timing brackets each step's graph replay with HIP
+    events: the steps keep their tokens (the graphs still run), every decode
+    step is counted once, and the GPU time it sums is positive and below the
+    wall time of the same steps."""
+    import time
+    d, sched, tensors, model, prompts, refs = small
+    eng = q.Engine(model, max_resident_requests=4, max_context=64, max_decode_batch_size=4, page_tokens=16)
+    ids = [eng.submit(p, max_new_tokens=NEW) for p in prompts]
+    eng.prefill_batch(ids)
+    eng.advance_batch(ids)  # the step's graph is captured outside the timed steps
+    eng.set_step_timing(True)
+    t = time.perf_counter()
+    for _ in range(NEW - 2):
+        eng.advance_batch(ids)
+    wall_ms = (time.perf_counter() - t) * 1000.0
+    gpu_ms, steps = eng.step_timing()
+    print(f"step timing: {gpu_ms:.3f} ms of GPU time in {wall_ms:.3f} ms over {steps} steps", flush=True)
+    assert steps == NEW - 2
+    assert 0.0 < gpu_ms < wall_ms
+    eng.set_step_timing(False)
+    assert eng.step_timing() == (0.0, 0)
+    for rid, ref in zip(ids, refs):
+        res, toks = eng.result(rid)
+        assert res.status == q.REQ_STATUS_INV["complete"] and toks.size == NEW
+        check_tokens(toks, ref)
+    eng.close()
+
+
 def test_chunked_advance_matches(q, small):
     d, sched, tensors, model, prompts, refs = small
     eng = q.Engine(model, max_resident_requests=2, max_context=64, max_decode_batch_size=2,
