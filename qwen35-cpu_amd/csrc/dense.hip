@@ -24,8 +24,9 @@ namespace q35 {
 // whenever it is zero or in the normal range, so every output carries the
 // split launch's bits unless some weight-scale x activation-scale product is
 // subnormal (below 2^-126: scales of order 1e-19 each). Workgroup i runs on
-// XCD i % 8; the logical order puts the token groups of one row group on one
-// XCD, where they share its L2.
+// XCD i % 8; the logical order gives each XCD about an eighth of the row
+// groups with every token group, walked row groups fastest, so that its L2
+// holds its row groups' weights and the few token groups in flight.
 namespace {
 typedef Q35_V4I v4i;
 
@@ -49,7 +50,14 @@ __global__ __launch_bounds__(256) Q35_WAVES_PER_EU(2) void gemm_dense_kernel(Gem
   const int logical = (static_cast<int>(blockIdx.x) & 7) * (nwg >> 3) + (static_cast<int>(blockIdx.x) >> 3);
   const int unit = logical * 4 + wave;
   if (unit >= units) return;
-  const int g = unit / token_groups, tg = unit - g * token_groups;
+  // units in blocks of gx row groups (an XCD's share of the rows) x every
+  // token group, the row groups fastest within a block: the units resident on
+  // an XCD at once span its row groups and a few token groups, whose weights
+  // and activations then stay in its L2 while the token groups advance
+  const int groups = units / token_groups, gx = (groups + 7) >> 3;
+  const int blk = unit / (gx * token_groups), k = unit - blk * gx * token_groups;
+  const int rb = min(gx, groups - blk * gx);  // row groups of this block
+  const int g = blk * gx + k % rb, tg = k / rb;
   const int nb = a.nb, ntiles = a.rows >> 3, tiles = (a.tokens + 15) >> 4;
   // rows past the matrix read a valid tile (the last); token tiles past the
   // chunk read the last valid tile; neither is stored. Lane c holds rows
