@@ -402,7 +402,23 @@ __global__ __launch_bounds__(128 * QPK) Q35_WAVES_PER_EU(2) void attention_flash
   __shared__ float lwb[QPK][16][kFlashBatch];
   __shared__ float lsum_rows[QPK][16];
   __shared__ int rows_lds[2][kChunkTokens];
-  const int z = static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x), g = blockIdx.y;
+  // workgroup p (linear) runs on XCD p % 8: where the KV heads divide the 8
+  // XCDs evenly, each head's tiles go to its own 8 / kv_heads XCDs, whose L2s
+  // then hold that head's K/V chunks for all of its tiles; the longest tiles
+  // still start first
+  int z, g;
+  {
+    const int nt = static_cast<int>(gridDim.x), nh = static_cast<int>(gridDim.y);
+    const int p = static_cast<int>(blockIdx.x) + nt * static_cast<int>(blockIdx.y);
+    if (8 % nh == 0 && (nt * nh) % 8 == 0) {
+      const int xph = 8 / nh;  // XCDs per KV head
+      g = (p & 7) / xph;
+      z = nt - 1 - ((p >> 3) * xph + (p & 7) % xph);
+    } else {
+      z = nt - 1 - static_cast<int>(blockIdx.x);
+      g = static_cast<int>(blockIdx.y);
+    }
+  }
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int u = wave >> 1, hf = wave & 1;  // query head in the group, half of the chunk
   const int kvw = a.kv_heads * kHeadDim;
